@@ -1,0 +1,88 @@
+"""Build libcqgdn.so (gfx950 HIP kernels + the C ABI of include/cqgdn.h) in-tree.
+
+Usage: python cq-pretrain_amd/build.py [--jobs N]
+
+Every csrc/*.hip is compiled to an object under _build/ (git-ignored), then linked
+into cqgdn/libcqgdn.so next to the Python host package, so the library travels
+with the source tree.  hipcc cross-compiles for gfx950 without a GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+INCLUDE = ROOT / "include"
+OUT = PKG / "cqgdn" / "libcqgdn.so"
+BUILD = PKG / "_build"
+
+ARCH = os.environ.get("CQGDN_ARCH", "gfx950")
+FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # never let the compiler emit packed-fp32 VALU ops (v_pk_*_f32)
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{INCLUDE}",
+    f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found: the ROCm toolchain is required to build libcqgdn")
+    return path
+
+
+def _compile(src: Path, extra: list[str]) -> Path:
+    obj = BUILD / (src.stem + ".o")
+    cmd = [hipcc(), *FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{err}")
+    if err.strip():
+        print(err, file=sys.stderr)
+    return obj
+
+
+def build(jobs: int | None = None, extra: list[str] | None = None, verbose: bool = True) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    extra = list(extra or [])
+    jobs = jobs or min(8, len(sources))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objects = list(pool.map(lambda s: _compile(s, extra), sources))
+    tmp = OUT.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stderr}")
+    os.replace(tmp, OUT)
+    if verbose:
+        print(f"built {OUT.relative_to(ROOT)} from {len(sources)} sources for {ARCH}")
+    return OUT
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--resource-usage", action="store_true", help="print per-kernel register/LDS usage")
+    args = ap.parse_args()
+    extra = ["-Rpass-analysis=kernel-resource-usage"] if args.resource_usage else []
+    build(args.jobs, extra)
+
+
+if __name__ == "__main__":
+    main()

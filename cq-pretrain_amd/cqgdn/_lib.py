@@ -1,0 +1,92 @@
+"""ctypes binding of libcqgdn.so (the C ABI declared in include/cqgdn.h).
+
+The library is loaded from this package directory (built in-tree by
+``cq-pretrain_amd/build.py``).  There is no fallback: a missing library, or a
+call that returns an error code, raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import hashlib
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("libcqgdn.so")
+
+OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
+NORMALIZE, TRAINING = 1, 2
+FWD_BUFFERS, BWD_BUFFERS = 14, 9
+FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "WT", "UT", "KgT", "hT", "h", "vnT", "vn")
+BWD_NAMES = ("dvlT", "XT", "dh", "dVnT", "dVn", "dKp", "dW", "dWT", "dGp")
+
+# every symbol include/cqgdn.h declares, with (restype, argtypes)
+_P, _I, _I64, _U, _F, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint, ctypes.c_float, ctypes.c_size_t
+SIGNATURES = {
+    "cqgdn_version": (ctypes.c_char_p, []),
+    "cqgdn_last_error": (ctypes.c_char_p, []),
+    "cqgdn_chunk_table": (_I64, [_P, _I, _P, _P]),
+    "cqgdn_fwd_workspace_size": (_SZ, [_I64, _I, _I64]),
+    "cqgdn_fwd_buffer_offsets": (_I, [_I64, _I, _I64, _P, _I]),
+    "cqgdn_bwd_workspace_size": (_SZ, [_I64, _I, _I64]),
+    "cqgdn_bwd_buffer_offsets": (_I, [_I64, _I, _I64, _P, _I]),
+    "cqgdn_fwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _P, _P, _P, _SZ, _P]),
+    "cqgdn_bwd": (_I, [_P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _SZ, _P, _SZ, _P, _P, _P, _P, _P,
+                       _P]),
+    "cqgdn_recurrent": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _F, _P]),
+    "cqgdn_l2norm_fwd": (_I, [_P, _P, _P, _I64, _P]),
+    "cqgdn_l2norm_bwd": (_I, [_P, _P, _P, _P, _I64, _P]),
+    "cqgdn_chunk_local_cumsum": (_I, [_P, _P, _I64, _I, _P, _I64, _I, _P]),
+}
+
+_LIB = None
+
+
+class CqgdnError(RuntimeError):
+    """A HIP runtime failure reported by libcqgdn."""
+
+
+def lib():
+    """Load libcqgdn.so once; raise if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python cq-pretrain_amd/build.py` "
+                "(the hip GDN backend has no fallback)")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype, fn.argtypes = res, args
+        _LIB = handle
+    return _LIB
+
+
+def check(rc: int, what: str) -> None:
+    if rc == OK:
+        return
+    msg = f"{what}: {lib().cqgdn_last_error().decode()}"
+    if rc == EINVAL:
+        raise ValueError(msg)
+    if rc == EUNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise CqgdnError(msg)
+
+
+def version() -> str:
+    return lib().cqgdn_version().decode()
+
+
+def sha256() -> str:
+    return hashlib.sha256(LIB_PATH.read_bytes()).hexdigest()
+
+
+def fwd_offsets(T: int, H: int, n_chunks: int) -> dict:
+    arr = (ctypes.c_size_t * FWD_BUFFERS)()
+    check(lib().cqgdn_fwd_buffer_offsets(T, H, n_chunks, arr, FWD_BUFFERS), "cqgdn_fwd_buffer_offsets")
+    return dict(zip(FWD_NAMES, arr))
+
+
+def bwd_offsets(T: int, H: int, n_chunks: int) -> dict:
+    arr = (ctypes.c_size_t * BWD_BUFFERS)()
+    check(lib().cqgdn_bwd_buffer_offsets(T, H, n_chunks, arr, BWD_BUFFERS), "cqgdn_bwd_buffer_offsets")
+    return dict(zip(BWD_NAMES, arr))

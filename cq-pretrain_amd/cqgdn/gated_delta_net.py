@@ -1,0 +1,373 @@
+"""MI355X GDN training/inference backend (``gdn_backend: hip``), no eager fallback.
+
+Host-side mirror of the reference's ``ops/gated_delta_net.py``: the same public
+functions (``initialize``, ``call``, ``CALLS``, ``host_bounds``, ``chunk_indices``,
+``device_metadata``, ``reverse_cumsum``, ``delta``, ``prefill``, ``recurrent``,
+``gated_norm``, ``conv``, ``provenance``) with the same argument meaning, layouts
+and error behaviour.  The device work runs in hand-written gfx950 HIP kernels of
+``libcqgdn.so`` (C ABI in include/cqgdn.h), enqueued on the current stream; the
+chunked forward always keeps w, h and v_new for the backward (the reference's
+``cached`` mode), so the serial state scan never runs twice.
+
+PyTorch only supplies device memory and streams.  Every contract violation raises
+``ValueError``/``NotImplementedError`` before any launch, like the reference.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from collections import Counter
+from functools import lru_cache
+
+import torch
+from torch.nn import functional as F
+
+from . import _lib
+
+CALLS = Counter()
+MODE = os.getenv("DELTA_HIP_MODE", "cached")
+CHUNK = 64
+_INITIALIZED = False
+
+
+def initialize():
+    """Load libcqgdn and check the device (ops/gated_delta_net.py:24-59)."""
+    global _INITIALIZED
+    if MODE != "cached":
+        raise ValueError(f"Unknown DELTA_HIP_MODE={MODE}: the hip backend always keeps w/h/v_new")
+    _lib.lib()
+    if torch.cuda.is_available():
+        arch = torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName
+        if not arch.startswith("gfx950"):
+            raise RuntimeError(f"libcqgdn is built for gfx950, the current device is {arch}")
+    _INITIALIZED = True
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def call(name, *args):
+    """Invoke one C-ABI entry point, counting calls per op (ops/gated_delta_net.py:62-64)."""
+    CALLS[name] += 1
+    _lib.check(getattr(_lib.lib(), name)(*args), name)
+
+
+def gated_norm(y, z, weight, eps=1e-6):
+    """RMSNorm(y) * weight * silu(z) (ops/gated_delta_net.py:67-74; unchanged semantics)."""
+    yf = y.float()
+    normed = yf * torch.rsqrt(yf.square().mean(-1, keepdim=True) + eps)
+    return (normed * weight.float() * F.silu(z.float())).to(y.dtype)
+
+
+def _require_gpu(*tensors):
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise ValueError("the hip GDN backend requires tensors on a ROCm GPU")
+
+
+def reverse_cumsum(dg, bounds):
+    """Reverse chunk-local cumsum of dg [1,T,H] fp32 (ops/gated_delta_net.py:77-87)."""
+    _require_gpu(dg)
+    b, t, h = dg.shape
+    x = dg.reshape(b * t, h).float().contiguous()
+    bounds = tuple(range(0, b * t + 1, t)) if bounds is None else bounds
+    _, table, _ = device_metadata(bounds, str(dg.device))
+    out = torch.empty_like(x)
+    call("cqgdn_chunk_local_cumsum", _ptr(x), _ptr(out), b * t, h, _ptr(table), table.shape[0], 1,
+         _stream(dg.device))
+    return out.reshape(b, t, h)
+
+
+@lru_cache(maxsize=128)
+def chunk_indices(bounds, size):
+    """Flat (document, chunk) pairs for chunk ``size`` (ops/gated_delta_net.py:90-99)."""
+    if bounds is None:
+        return None
+    return [
+        item
+        for i, (a, b) in enumerate(zip(bounds, bounds[1:]))
+        for j in range((b - a + size - 1) // size)
+        for item in (i, j)
+    ]
+
+
+def host_bounds(cu_seqlens, cu_seqlens_cpu):
+    """Host copy of packed-sequence bounds; never reads device metadata (ops/gated_delta_net.py:102-114)."""
+    if cu_seqlens is None:
+        return None
+    if cu_seqlens_cpu is None:
+        raise ValueError("Supply cu_seqlens_cpu: training must not copy metadata from the GPU in each layer")
+    if isinstance(cu_seqlens_cpu, torch.Tensor):
+        if cu_seqlens_cpu.device.type != "cpu":
+            raise ValueError("cu_seqlens_cpu must be on CPU")
+        cu_seqlens_cpu = cu_seqlens_cpu.tolist()
+    bounds = tuple(int(i) for i in cu_seqlens_cpu)
+    if not bounds or bounds[0] != 0 or any(b < a for a, b in zip(bounds, bounds[1:])):
+        raise ValueError("Invalid packed sequence boundaries")
+    return bounds
+
+
+def chunk_table(bounds):
+    """Host (CPU int32) chunk table [n_chunks, 2] = (start, len) and doc_chunk [n_docs + 1]."""
+    n_bounds = len(bounds)
+    b = (ctypes.c_int64 * n_bounds)(*bounds)
+    n = _lib.lib().cqgdn_chunk_table(b, n_bounds, None, None)
+    if n < 0:
+        raise ValueError(_lib.lib().cqgdn_last_error().decode())
+    table = torch.empty(max(n, 1), 2, dtype=torch.int32)
+    doc = torch.empty(n_bounds, dtype=torch.int32)
+    _lib.lib().cqgdn_chunk_table(b, n_bounds, ctypes.c_void_p(table.data_ptr()), ctypes.c_void_p(doc.data_ptr()))
+    return table[:n], doc
+
+
+@lru_cache(maxsize=64)
+def device_metadata(bounds, device):
+    """Device copies of the bounds and chunk tables, cached per bounds (ops/gated_delta_net.py:117-126).
+
+    Returns ``(cu int64 [n_docs+1], chunk_table int32 [n_chunks,2], doc_chunk int32 [n_docs+1])``.
+    """
+    if bounds is None:
+        return None, None, None
+    table, doc = chunk_table(bounds)
+    cu = torch.tensor(bounds, dtype=torch.long)
+    return (cu.to(device, non_blocking=True), table.to(device, non_blocking=True),
+            doc.to(device, non_blocking=True))
+
+
+def _flatten(q, k, v, g, beta, bounds):
+    """Packed [1,T,...] views; unpacked batches become one document per row."""
+    b, t = q.shape[0], q.shape[1]
+    if bounds is None:
+        bounds = tuple(range(0, b * t + 1, t)) if t > 0 else (0,) * (b + 1)
+    q, k, v = (x.reshape(1, b * t, *x.shape[2:]).contiguous() for x in (q, k, v))
+    g, beta = (x.reshape(1, b * t, x.shape[-1]).float().contiguous() for x in (g, beta))
+    return q, k, v, g, beta, bounds
+
+
+def _forward(q, k, v, g, beta, bounds, normalize, scale, training, initial_state=None, want_state=False):
+    t, h = q.shape[1], q.shape[2]
+    if q.shape[0] != 1 or bounds[0] != 0 or bounds[-1] != t:
+        raise ValueError("packed forward needs batch 1 and bounds (0, ..., T) covering every event")
+    for x in (q, k, v, g, beta):
+        if not x.is_contiguous():
+            raise ValueError("forward operands must be contiguous")
+    if initial_state is not None and initial_state.shape != (len(bounds) - 1, h, 128, 128):
+        raise ValueError("initial_state must be [n_docs, H, 128, 128] fp32")
+    cu, table, doc = device_metadata(bounds, str(q.device))
+    n_chunks, n_docs = table.shape[0], len(bounds) - 1
+    ws = torch.empty(_lib.lib().cqgdn_fwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=q.device)
+    o = torch.empty_like(v)
+    state = torch.empty(n_docs, h, 128, 128, dtype=torch.float32, device=q.device) if want_state else None
+    flags = (_lib.NORMALIZE if normalize else 0) | (_lib.TRAINING if training else 0)
+    call("cqgdn_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), t, h, _ptr(table), n_chunks, _ptr(doc),
+         n_docs, float(scale), flags, _ptr(initial_state), _ptr(state), _ptr(o), _ptr(ws), ws.numel(),
+         _stream(q.device))
+    return o, state, ws
+
+
+class _Delta(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, bounds, normalize, scale):
+        ctx.input_dtypes = [x.dtype for x in (q, k, v, g, beta)]
+        ctx.shapes = [x.shape for x in (q, k, v, g, beta)]
+        qf, kf, vf, gf, bf, bounds = _flatten(q, k, v, g, beta, bounds)
+        o, _, ws = _forward(qf, kf, vf, gf, bf, bounds, normalize, scale, training=True)
+        ctx.save_for_backward(vf, gf, bf, ws)
+        ctx.bounds, ctx.scale, ctx.normalize = bounds, scale, normalize
+        return o.reshape(v.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        v, g, beta, ws = ctx.saved_tensors
+        t, h = v.shape[1], v.shape[2]
+        cu, table, doc = device_metadata(ctx.bounds, str(v.device))
+        n_chunks, n_docs = table.shape[0], len(ctx.bounds) - 1
+        dy = dy.reshape(v.shape).to(v.dtype).contiguous()
+        bws = torch.empty(_lib.lib().cqgdn_bwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=v.device)
+        dq, dk, dv = torch.empty_like(v), torch.empty_like(v), torch.empty_like(v)
+        dg, db = torch.empty_like(g), torch.empty_like(beta)
+        flags = (_lib.NORMALIZE if ctx.normalize else 0) | _lib.TRAINING
+        call("cqgdn_bwd", _ptr(v), _ptr(g), _ptr(beta), _ptr(dy), t, h, _ptr(table), n_chunks, _ptr(doc), n_docs,
+             float(ctx.scale), flags, _ptr(ws), ws.numel(), _ptr(bws), bws.numel(), _ptr(dq), _ptr(dk), _ptr(dv),
+             _ptr(dg), _ptr(db), _stream(v.device))
+        grads = [x.reshape(shape).to(dtype)
+                 for x, shape, dtype in zip((dq, dk, dv, dg, db), ctx.shapes, ctx.input_dtypes)]
+        return *grads, None, None, None
+
+
+def delta(
+    q,
+    k,
+    v,
+    g,
+    beta,
+    *,
+    use_qk_l2norm_in_kernel=False,
+    cu_seqlens=None,
+    cu_seqlens_cpu=None,
+    initial_state=None,
+    output_final_state=False,
+    scale=None,
+):
+    """Chunked GDN for training, same contract as ops/gated_delta_net.py:217-249.
+
+    q, k, v: [B,T,H,128] bf16 time-first; g, beta: [B,T,H] (computed in fp32).
+    Packed documents: B == 1 with ``cu_seqlens`` (device) and ``cu_seqlens_cpu``
+    (host) bounds; the state resets at each document.  Returns ``(o, None)``.
+    """
+    if initial_state is not None or output_final_state:
+        raise NotImplementedError("This training adapter requires zero initial state and no state output")
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("QKV must share BF16/FP16 dtype")
+    if q.shape != k.shape or q.shape != v.shape or (q.shape[-1] != 128 or q.shape[-2] not in (4, 8, 16, 32)):
+        raise ValueError("GDN requires equal expanded QKV, head dimension 128 and supported local heads")
+    bounds = host_bounds(cu_seqlens, cu_seqlens_cpu)
+    if bounds is not None and (q.shape[0] != 1 or bounds[-1] != q.shape[1]):
+        raise ValueError("Packed inputs must have batch 1 and boundaries covering every token")
+    if q.dtype != torch.bfloat16:
+        raise NotImplementedError("the hip GDN kernels compute in bf16; fp16 inputs are not built yet")
+    if g.shape != q.shape[:3] or beta.shape != q.shape[:3]:
+        raise ValueError("g and beta must be [B,T,H]")
+    _require_gpu(q, k, v, g, beta)
+    return _Delta.apply(
+        q,
+        k,
+        v,
+        g,
+        beta,
+        bounds,
+        use_qk_l2norm_in_kernel,
+        q.shape[-1] ** -0.5 if scale is None else float(scale),
+    ), None
+
+
+@torch.no_grad()
+def prefill(q, k, v, g, beta, bounds, initial_state=None):
+    """Inference forward with per-document final states (ops/gated_delta_net.py:292-311).
+
+    q, k, v: [1,T,H,128] bf16 (l2norm applied inside, scale 128^-0.5); g, beta [1,T,H].
+    Returns ``(o [1,T,H,128] time-first, state [n_docs,H,K,V] fp32)``.
+    """
+    bounds = tuple(int(b) for b in bounds)
+    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("prefill needs bf16 q/k/v")
+    if q.shape[0] != 1 or bounds[0] != 0 or bounds[-1] != q.shape[1]:
+        raise ValueError("prefill needs batch 1 and bounds covering every token")
+    _require_gpu(q, k, v, g, beta)
+    qf, kf, vf, gf, bf, bounds = _flatten(q, k, v, g, beta, bounds)
+    if initial_state is not None:
+        initial_state = initial_state.float().contiguous()
+    o, state, _ = _forward(qf, kf, vf, gf, bf, bounds, True, q.shape[-1] ** -0.5, training=False,
+                           initial_state=initial_state, want_state=True)
+    return o, state
+
+
+@torch.no_grad()
+def recurrent(q, k, v, g, beta, state, out):
+    """One recurrent decode pass over t events, state updated in place (ops/gated_delta_net.py:314-352).
+
+    q, k (l2-normalized), v, out: [t,H,128] bf16; g: [t,H] fp32; beta: [t,H] fp32 or
+    bf16; state: [1,H,V,K] fp32 value-first.  Batched decode passes q of shape
+    [N,t,H,128], g/beta [N,t,H] and state [N,H,V,K].
+    """
+    if q.dim() == 3:
+        n, (t, h, d) = 1, q.shape
+    else:
+        n, t, h, d = q.shape
+    if d != 128 or state.shape != (n, h, 128, 128) or state.dtype != torch.float32:
+        raise ValueError("recurrent needs d=128 and a value-first fp32 state [N,H,128,128]")
+    if out.shape != q.shape or k.shape != q.shape or v.shape != q.shape or q.dtype != torch.bfloat16:
+        raise ValueError("q/k/v/out must share shape and be bf16")
+    if beta.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("beta must be fp32 or bf16")
+    for x in (q, k, v, g, beta, state, out):
+        if not x.is_contiguous():
+            raise ValueError("recurrent operands must be contiguous (the state is updated in place)")
+    _require_gpu(q, k, v, g, beta, state, out)
+    g = g.float() if g.dtype != torch.float32 else g
+    call("cqgdn_recurrent", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), int(beta.dtype == torch.bfloat16),
+         _ptr(state), _ptr(out), n, t, h, d ** -0.5, _stream(q.device))
+    return out
+
+
+def l2_fwd(x):
+    """Row l2norm over the last dim 128; returns (y, rstd) (the reference's ``l2_fwd`` op)."""
+    _require_gpu(x)
+    if x.shape[-1] != 128 or x.dtype != torch.bfloat16:
+        raise ValueError("l2_fwd needs bf16 rows of 128")
+    x = x.contiguous()
+    y = torch.empty_like(x)
+    rstd = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    call("cqgdn_l2norm_fwd", _ptr(x), _ptr(y), _ptr(rstd), x.numel() // 128, _stream(x.device))
+    return y, rstd
+
+
+def l2_bwd(y, rstd, dy):
+    """Backward of ``l2_fwd``: dx = rstd * (dy - y (y . dy))."""
+    _require_gpu(y, rstd, dy)
+    y, dy, rstd = y.contiguous(), dy.to(y.dtype).contiguous(), rstd.float().contiguous()
+    dx = torch.empty_like(y)
+    call("cqgdn_l2norm_bwd", _ptr(y), _ptr(rstd), _ptr(dy), _ptr(dx), y.numel() // 128, _stream(y.device))
+    return dx
+
+
+class _Conv(torch.autograd.Function):
+    """Packed depthwise causal conv (kept with the reference's semantics, ops/gated_delta_net.py:252-289)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, activation, bounds):
+        ctx.save_for_backward(x, weight)
+        ctx.activation, ctx.bounds = activation, bounds
+        return _conv_eval(x, weight, activation, bounds)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, weight = ctx.saved_tensors
+        with torch.enable_grad():
+            xx, ww = x.detach().requires_grad_(), weight.detach().requires_grad_()
+            y = _conv_eval(xx, ww, ctx.activation, ctx.bounds)
+            dx, dw = torch.autograd.grad(y, (xx, ww), dy)
+        return dx, dw, None, None
+
+
+def _conv_eval(x, weight, activation, bounds):
+    kernel = weight.shape[-1]
+    parts = []
+    for a, b in zip(bounds, bounds[1:]):
+        seg = x[:, a:b].transpose(1, 2)
+        y = F.conv1d(seg, weight[:, None], padding=kernel - 1, groups=x.shape[-1])[..., : b - a]
+        parts.append(y.transpose(1, 2))
+    y = torch.cat(parts, dim=1) if parts else x[:, :0]
+    return F.silu(y) if activation else y
+
+
+def conv(x, weight, *, activation=None, cu_seqlens=None, cu_seqlens_cpu=None):
+    """Causal conv1d over packed documents; weight [channels, kernel] (ops/gated_delta_net.py:280-289)."""
+    if activation not in (None, "silu", "swish"):
+        raise ValueError(f"Unsupported activation {activation}")
+    bounds = host_bounds(cu_seqlens, cu_seqlens_cpu) or (0, x.shape[1])
+    return _Conv.apply(x, weight, activation is not None, bounds), None
+
+
+def provenance():
+    """Backend record: library hash and version, device, per-op call counts (ops/gated_delta_net.py:355-376)."""
+    device = None
+    if torch.cuda.is_available():
+        props = torch.cuda.get_device_properties(torch.cuda.current_device())
+        device = dict(name=props.name, arch=props.gcnArchName)
+    return dict(
+        backend="hip",
+        mode=MODE,
+        library=str(_lib.LIB_PATH),
+        version=_lib.version(),
+        sha256={_lib.LIB_PATH.name: _lib.sha256()},
+        device=device,
+        calls=dict(CALLS),
+        fallback={},
+    )

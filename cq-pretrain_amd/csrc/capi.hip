@@ -1,0 +1,244 @@
+// extern "C" entry points of libcqgdn (declared in include/cqgdn.h).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "cqgdn.h"
+#include "gdn_kernels.hpp"
+#include "gdn_layout.hpp"
+
+using namespace cqgdn;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int ok() {
+  g_error.clear();
+  return CQGDN_OK;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(CQGDN_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_common(int64_t T, int H, int64_t n_chunks, int n_docs, const int32_t* chunk_table,
+                 const int32_t* doc_chunk) {
+  if (T < 0 || H <= 0 || n_chunks < 0 || n_docs < 0)
+    return fail(CQGDN_EINVAL, "invalid sizes T=%lld H=%d n_chunks=%lld n_docs=%d", (long long)T, H,
+                (long long)n_chunks, n_docs);
+  if (T > 0 && (n_chunks == 0 || n_docs == 0))
+    return fail(CQGDN_EINVAL, "T=%lld events need at least one chunk and one document", (long long)T);
+  if (n_chunks > 0 && (!chunk_table || !doc_chunk)) return fail(CQGDN_EINVAL, "chunk_table/doc_chunk are null");
+  if (n_chunks > INT32_MAX / 2 || (int64_t)n_chunks * H > 2147483647LL)
+    return fail(CQGDN_EUNSUPPORTED, "too many chunks (%lld)", (long long)n_chunks);
+  return CQGDN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* cqgdn_version(void) { return "cqgdn 0.1.0 gfx950"; }
+
+const char* cqgdn_last_error(void) { return g_error.c_str(); }
+
+int64_t cqgdn_chunk_table(const int64_t* bounds, int n_bounds, int32_t* table, int32_t* doc_chunk) {
+  if (!bounds || n_bounds < 1 || bounds[0] != 0) {
+    fail(CQGDN_EINVAL, "bounds must start at 0");
+    return -1;
+  }
+  int64_t n = 0;
+  for (int d = 0; d + 1 < n_bounds; ++d) {
+    const int64_t a = bounds[d], b = bounds[d + 1];
+    if (b < a) {
+      fail(CQGDN_EINVAL, "bounds must be non-decreasing");
+      return -1;
+    }
+    if (doc_chunk) doc_chunk[d] = (int32_t)n;
+    for (int64_t s = a; s < b; s += CQGDN_CHUNK) {
+      if (table) {
+        table[2 * n] = (int32_t)s;
+        table[2 * n + 1] = (int32_t)((b - s) < CQGDN_CHUNK ? (b - s) : CQGDN_CHUNK);
+      }
+      ++n;
+    }
+  }
+  if (doc_chunk) doc_chunk[n_bounds - 1] = (int32_t)n;
+  ok();
+  return n;
+}
+
+size_t cqgdn_fwd_workspace_size(int64_t T, int H, int64_t n_chunks) {
+  size_t s[F_COUNT], off[F_COUNT];
+  fwd_sizes(T, H, n_chunks, s);
+  return offsets(s, F_COUNT, off);
+}
+
+int cqgdn_fwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* out, int count) {
+  if (!out || count < F_COUNT) return fail(CQGDN_EINVAL, "need room for %d offsets", (int)F_COUNT);
+  size_t s[F_COUNT];
+  fwd_sizes(T, H, n_chunks, s);
+  offsets(s, F_COUNT, out);
+  return ok();
+}
+
+size_t cqgdn_bwd_workspace_size(int64_t T, int H, int64_t n_chunks) {
+  size_t s[B_COUNT], off[B_COUNT];
+  bwd_sizes(T, H, n_chunks, s);
+  return offsets(s, B_COUNT, off);
+}
+
+int cqgdn_bwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* out, int count) {
+  if (!out || count < B_COUNT) return fail(CQGDN_EINVAL, "need room for %d offsets", (int)B_COUNT);
+  size_t s[B_COUNT];
+  bwd_sizes(T, H, n_chunks, s);
+  offsets(s, B_COUNT, out);
+  return ok();
+}
+
+int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T, int H,
+              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
+              unsigned flags, const float* initial_state, float* final_state, void* o, void* workspace,
+              size_t workspace_bytes, void* stream) {
+  if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
+  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING)) return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
+  if (T == 0) {
+    if (final_state && n_docs > 0) {
+      // every document is empty: its final state is its initial state (or zero)
+      launch_copy_or_zero(final_state, initial_state, (size_t)n_docs * H * 128 * 128, (hipStream_t)stream);
+      return check_launch("cqgdn_fwd (empty)");
+    }
+    return ok();
+  }
+  if (!q || !k || !v || !g || !beta || !o || !workspace) return fail(CQGDN_EINVAL, "null tensor pointer");
+  const size_t need = cqgdn_fwd_workspace_size(T, H, n_chunks);
+  if (workspace_bytes < need)
+    return fail(CQGDN_EINVAL, "forward workspace too small: %zu < %zu bytes", workspace_bytes, need);
+  if (!aligned(workspace, 256)) return fail(CQGDN_EINVAL, "workspace must be 256-byte aligned");
+  for (const void* p : {q, k, v, (const void*)o})
+    if (!aligned(p, 16)) return fail(CQGDN_EINVAL, "q/k/v/o must be 16-byte aligned");
+  FwdArgs a{};
+  a.q = static_cast<const bf16*>(q);
+  a.k = static_cast<const bf16*>(k);
+  a.v = static_cast<const bf16*>(v);
+  a.g = g;
+  a.beta = beta;
+  a.chunks = chunk_table;
+  a.doc_chunk = doc_chunk;
+  a.T = (int)T;
+  a.H = H;
+  a.n_chunks = (int)n_chunks;
+  a.n_docs = n_docs;
+  a.scale = scale;
+  a.normalize = (flags & CQGDN_NORMALIZE) != 0;
+  a.training = (flags & CQGDN_TRAINING) != 0;
+  a.initial_state = initial_state;
+  a.final_state = final_state;
+  a.o = static_cast<bf16*>(o);
+  a.ws = static_cast<uint8_t*>(workspace);
+  cqgdn_fwd_buffer_offsets(T, H, n_chunks, a.off, F_COUNT);
+  launch_fwd(a, (hipStream_t)stream);
+  return check_launch("cqgdn_fwd");
+}
+
+int cqgdn_bwd(const void* v, const float* g, const float* beta, const void* dout, int64_t T, int H,
+              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
+              unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes, void* bwd_workspace,
+              size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta, void* stream) {
+  if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
+  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING)) return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
+  if (T == 0) return ok();
+  if (!v || !g || !beta || !dout || !fwd_workspace || !bwd_workspace || !dq || !dk || !dv || !dg || !dbeta)
+    return fail(CQGDN_EINVAL, "null tensor pointer");
+  const size_t fneed = cqgdn_fwd_workspace_size(T, H, n_chunks);
+  const size_t bneed = cqgdn_bwd_workspace_size(T, H, n_chunks);
+  if (fwd_workspace_bytes < fneed) return fail(CQGDN_EINVAL, "forward workspace too small: %zu < %zu", fwd_workspace_bytes, fneed);
+  if (bwd_workspace_bytes < bneed) return fail(CQGDN_EINVAL, "backward workspace too small: %zu < %zu", bwd_workspace_bytes, bneed);
+  if (!aligned(fwd_workspace, 256) || !aligned(bwd_workspace, 256)) return fail(CQGDN_EINVAL, "workspaces must be 256-byte aligned");
+  for (const void* p : {v, dout, (const void*)dq, (const void*)dk, (const void*)dv})
+    if (!aligned(p, 16)) return fail(CQGDN_EINVAL, "v/do/dq/dk/dv must be 16-byte aligned");
+  BwdArgs a{};
+  a.v = static_cast<const bf16*>(v);
+  a.dout = static_cast<const bf16*>(dout);
+  a.g = g;
+  a.beta = beta;
+  a.chunks = chunk_table;
+  a.doc_chunk = doc_chunk;
+  a.T = (int)T;
+  a.H = H;
+  a.n_chunks = (int)n_chunks;
+  a.n_docs = n_docs;
+  a.scale = scale;
+  a.normalize = (flags & CQGDN_NORMALIZE) != 0;
+  a.fws = static_cast<const uint8_t*>(fwd_workspace);
+  a.bws = static_cast<uint8_t*>(bwd_workspace);
+  cqgdn_fwd_buffer_offsets(T, H, n_chunks, a.foff, F_COUNT);
+  cqgdn_bwd_buffer_offsets(T, H, n_chunks, a.boff, B_COUNT);
+  a.dq = static_cast<bf16*>(dq);
+  a.dk = static_cast<bf16*>(dk);
+  a.dv = static_cast<bf16*>(dv);
+  a.dg = dg;
+  a.dbeta = dbeta;
+  launch_bwd(a, (hipStream_t)stream);
+  return check_launch("cqgdn_bwd");
+}
+
+int cqgdn_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta, int beta_is_bf16,
+                    float* state, void* out, int N, int E, int H, float scale, void* stream) {
+  if (N < 0 || E < 0 || H <= 0) return fail(CQGDN_EINVAL, "invalid sizes N=%d E=%d H=%d", N, E, H);
+  if (N == 0 || E == 0) return ok();
+  if (!q || !k || !v || !g || !beta || !state || !out) return fail(CQGDN_EINVAL, "null tensor pointer");
+  for (const void* p : {q, k, (const void*)state})
+    if (!aligned(p, 16)) return fail(CQGDN_EINVAL, "q/k/state must be 16-byte aligned");
+  if ((int64_t)N * H * 2 > 2147483647LL) return fail(CQGDN_EUNSUPPORTED, "too many sequences");
+  launch_recurrent(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), g, beta,
+                   beta_is_bf16 != 0, state, static_cast<bf16*>(out), N, E, H, scale, (hipStream_t)stream);
+  return check_launch("cqgdn_recurrent");
+}
+
+int cqgdn_l2norm_fwd(const void* x, void* y, float* rstd, int64_t rows, void* stream) {
+  if (rows < 0) return fail(CQGDN_EINVAL, "rows < 0");
+  if (rows == 0) return ok();
+  if (!x || !y) return fail(CQGDN_EINVAL, "null tensor pointer");
+  if (!aligned(x, 16) || !aligned(y, 16)) return fail(CQGDN_EINVAL, "x/y must be 16-byte aligned");
+  launch_l2norm_fwd(static_cast<const bf16*>(x), static_cast<bf16*>(y), rstd, rows, (hipStream_t)stream);
+  return check_launch("cqgdn_l2norm_fwd");
+}
+
+int cqgdn_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx, int64_t rows, void* stream) {
+  if (rows < 0) return fail(CQGDN_EINVAL, "rows < 0");
+  if (rows == 0) return ok();
+  if (!y || !rstd || !dy || !dx) return fail(CQGDN_EINVAL, "null tensor pointer");
+  if (!aligned(y, 16) || !aligned(dy, 16) || !aligned(dx, 16)) return fail(CQGDN_EINVAL, "y/dy/dx must be 16-byte aligned");
+  launch_l2norm_bwd(static_cast<const bf16*>(y), rstd, static_cast<const bf16*>(dy), static_cast<bf16*>(dx), rows,
+                    (hipStream_t)stream);
+  return check_launch("cqgdn_l2norm_bwd");
+}
+
+int cqgdn_chunk_local_cumsum(const float* g, float* out, int64_t T, int H, const int32_t* chunk_table,
+                             int64_t n_chunks, int reverse, void* stream) {
+  if (T < 0 || H <= 0 || n_chunks < 0) return fail(CQGDN_EINVAL, "invalid sizes");
+  if (T == 0 || n_chunks == 0) return ok();
+  if (!g || !out || !chunk_table) return fail(CQGDN_EINVAL, "null pointer");
+  launch_chunk_cumsum(g, out, chunk_table, (int)n_chunks, H, reverse != 0, (hipStream_t)stream);
+  return check_launch("cqgdn_chunk_local_cumsum");
+}
+
+}  // extern "C"

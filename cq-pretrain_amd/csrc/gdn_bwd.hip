@@ -1,0 +1,793 @@
+// GDN backward on gfx950.
+//
+// Per chunk (C events, S_c the state entering it, dS_{c+1} the gradient of the
+// state leaving it), with Gam_ij = exp(G_i - G_j) on i >= j, gam = exp(G),
+// kdec_i = exp(G_last - G_i), P = (Qn Kn^T) * Gam:
+//
+//   bwd_local  (grid NC x H)  dv_local = scale P^T dO ;  X = scale (gam Qn)^T dO
+//   bwd_state  (serial, reverse)  dVn = dv_local + kdec * (Kn dS_{c+1})
+//                                 dS_c = exp(G_last) dS_{c+1} + X - W^T dVn
+//   bwd_dqk    (grid NC x H)  dQn = scale gam (dO S_c^T) + (scale dP Gam) Kn   (dP = dO Vn^T)
+//                             dKn(part) = (scale dP Gam)^T Qn + kdec (Vn dS_{c+1}^T)
+//                             dW = -dVn S_c^T ; dG terms of the output and state update;
+//                             l2norm backward of dq
+//   bwd_wy     (grid NC x H)  dT = dW (beta gam Kn)^T + dVn (beta V)^T ; dA = -(T^T dT T^T)
+//                             dKn += beta (dA Gam) Kn + (dA Gam)^T (beta Kn) + beta gam (T^T dW)
+//                             dV = beta (T^T dVn) ; dbeta ; dG ; reverse cumsum -> dg ;
+//                             l2norm backward of dk
+//
+// This is the reference's backward op chain (ops/gated_delta_net.py:188-214:
+// chunk_bwd_dv_local, chunk_gated_delta_rule_bwd_dhu, chunk_bwd_dqkwg,
+// prepare_wy_repr_bwd_da/_full, reverse_cumsum, l2_bwd) regrouped into four
+// kernels.  All reductions run in a fixed order (no atomics), so results are
+// bitwise reproducible from run to run.
+#include "gdn_common.hpp"
+#include "gdn_layout.hpp"
+#include "gdn_kernels.hpp"
+
+namespace cqgdn {
+
+constexpr int LDK = 136;  // bf16 row stride, 64 x 128 tiles
+constexpr int LDT = 72;   // bf16 row stride, 128 x 64 and 64 x 64 tiles
+constexpr int LDQ = 132;  // fp32 row stride, 64 x 128 staging
+
+// ---------------------------------------------------------------------------
+// bwd_local
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bwd_local_kernel(
+    const bf16* __restrict__ qn, const bf16* __restrict__ kn, const bf16* __restrict__ dout,
+    const float* __restrict__ gc, const int32_t* __restrict__ chunks, int H, float scale,
+    bf16* __restrict__ dvlT, bf16* __restrict__ XT) {
+  const int c = blockIdx.x, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q4 = lane >> 4;
+  const ChunkInfo ci = chunk_info(chunks, c);
+  const size_t cb = (size_t)c * H + h;
+
+  __shared__ __attribute__((aligned(16))) bf16 Qs[64 * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 Ks[64 * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 QgT[128 * LDT];
+  __shared__ __attribute__((aligned(16))) bf16 dOT[128 * LDT];
+  __shared__ __attribute__((aligned(16))) bf16 PTs[64 * LDT];
+  __shared__ float Gs[64];
+
+  {
+    const int t = tid >> 2, p = tid & 3;
+    const bool in = t < ci.len;
+    const size_t row = ((size_t)(ci.start + t) * H + h) * D;
+    const float gt = gc[(size_t)(ci.start + (in ? t : ci.len - 1)) * H + h];
+    if (p == 0) Gs[t] = gt;
+    const float gam = __expf(gt);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = 32 * j + 8 * p;
+      const bf16x8 xq = in ? ld8(qn + row + col) : zero8();
+      st8(Qs + t * LDK + col, xq);
+      st8(Ks + t * LDK + col, in ? ld8(kn + row + col) : zero8());
+      const f32x8 xg = cvtf8(xq) * gam;
+      const bf16x8 xd = in ? ld8(dout + row + col) : zero8();
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        QgT[(col + s) * LDT + t] = (bf16)xg[s];
+        dOT[(col + s) * LDT + t] = xd[s];
+      }
+    }
+  }
+  __syncthreads();
+
+  // P (t-tile = wave, s-tiles <= wave), stored transposed: PTs[s][t]
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    f32x4 acc = zero4();
+    if (n <= wave) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+        acc = mfma(ld8(Qs + (16 * wave + r) * LDK + 32 * kb + 8 * q4), ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4),
+                   acc);
+      const int s = 16 * n + r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * wave + 4 * q4 + i;
+        acc[i] = (s <= t) ? acc[i] * __expf(Gs[t] - Gs[s]) : 0.f;
+      }
+    }
+    st4(PTs + (16 * n + r) * LDT + 16 * wave + 4 * q4, acc);
+  }
+  __syncthreads();
+
+  // dv_local^T: rows s = s-tile wave, 8 value tiles; only t >= s contributes
+  {
+    bf16* out = dvlT + cb * (D * CH);
+    const int kb0 = wave >= 2 ? 1 : 0;
+    bf16x8 a[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) a[kb] = ld8(PTs + (16 * wave + r) * LDT + 32 * kb + 8 * q4);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+        if (kb >= kb0) acc = mfma(a[kb], ld8(dOT + (16 * n + r) * LDT + 32 * kb + 8 * q4), acc);
+      st4(out + (16 * n + r) * CH + 16 * wave + 4 * q4, acc * scale);
+    }
+  }
+  // X^T: k-tiles 2w, 2w+1 x 8 value tiles
+  {
+    bf16* out = XT + cb * (D * D);
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      const int m = 2 * wave + mm;
+      bf16x8 a[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) a[kb] = ld8(QgT + (16 * m + r) * LDT + 32 * kb + 8 * q4);
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) acc = mfma(a[kb], ld8(dOT + (16 * n + r) * LDT + 32 * kb + 8 * q4), acc);
+        st4(out + (16 * n + r) * D + 16 * m + 4 * q4, acc * scale);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_state: one wave per (head, 16-wide value slice, document), chunks in reverse
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void bwd_state_kernel(
+    const bf16* __restrict__ kn, const float* __restrict__ gc, const bf16* __restrict__ dvlT,
+    const bf16* __restrict__ XT, const bf16* __restrict__ WT, const int32_t* __restrict__ chunks,
+    const int32_t* __restrict__ doc_chunk, int H, bf16* __restrict__ dh, bf16* __restrict__ dVnT,
+    bf16* __restrict__ dVn) {
+  const int h = blockIdx.x % H, slice = blockIdx.x / H, d = blockIdx.y;
+  const int lane = threadIdx.x, r = lane & 15, q4 = lane >> 4;
+  const int v0 = 16 * slice;
+
+  f32x4 dS[8];  // dS[m][i] = dState[k = 16m + 4q4 + i][v = v0 + r]
+#pragma unroll
+  for (int m = 0; m < 8; ++m) dS[m] = zero4();
+
+  const int c_begin = doc_chunk[d];
+  for (int c = doc_chunk[d + 1] - 1; c >= c_begin; --c) {
+    const ChunkInfo ci = chunk_info(chunks, c);
+    const size_t cb = (size_t)c * H + h;
+    bf16* dhc = dh + cb * (D * D);
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dhc[(16 * m + 4 * q4 + i) * D + v0 + r] = (bf16)dS[m][i];
+    bf16x8 sb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sb[j] = pack_perm(dS[2 * j], dS[2 * j + 1]);
+
+    const float g_lane = gc[(size_t)(ci.start + min(lane, ci.len - 1)) * H + h];
+    const float glast = __shfl(g_lane, ci.len - 1, 64);
+
+    const bf16* dvl = dvlT + cb * (D * CH);
+    f32x4 dv[4];
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      f32x4 acc = zero4();
+      const int t = 16 * i4 + r;
+      const bf16* krow = kn + ((size_t)(ci.start + t) * H + h) * D;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc = mfma((t < ci.len) ? ld8p(krow + 32 * j + 4 * q4) : zero8(), sb[j], acc);
+      const f32x4 local = cvtf4(ld4(dvl + (v0 + r) * CH + 16 * i4 + 4 * q4));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float gt = __shfl(g_lane, 16 * i4 + 4 * q4 + i, 64);
+        acc[i] = acc[i] * __expf(glast - gt) + local[i];
+      }
+      dv[i4] = acc;
+    }
+    bf16* dvt = dVnT + cb * (D * CH);
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      st4(dvt + (v0 + r) * CH + 16 * i4 + 4 * q4, dv[i4]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * i4 + 4 * q4 + i;
+        if (t < ci.len) dVn[((size_t)(ci.start + t) * H + h) * D + v0 + r] = (bf16)dv[i4][i];
+      }
+    }
+
+    const float gC = __expf(glast);
+    bf16x8 nb[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) nb[j] = neg8(pack_perm(dv[2 * j], dv[2 * j + 1]));
+    const bf16* xt = XT + cb * (D * D);
+    const bf16* wt = WT + cb * (D * CH);
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      dS[m] = dS[m] * gC + cvtf4(ld4(xt + (v0 + r) * D + 16 * m + 4 * q4));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) dS[m] = mfma(ld8p(wt + (16 * m + r) * CH + 32 * j + 4 * q4), nb[j], dS[m]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_dqk
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bwd_dqk_kernel(
+    const bf16* __restrict__ qn, const bf16* __restrict__ kn, const float* __restrict__ rq,
+    const float* __restrict__ gc, const bf16* __restrict__ hR, const bf16* __restrict__ vnR,
+    const bf16* __restrict__ dout, const bf16* __restrict__ dh, const bf16* __restrict__ dVn,
+    const int32_t* __restrict__ chunks, int H, float scale, int normalize, bf16* __restrict__ dq,
+    float* __restrict__ dKp, bf16* __restrict__ dW, bf16* __restrict__ dWT, float* __restrict__ dGp) {
+  const int c = blockIdx.x, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q4 = lane >> 4;
+  const ChunkInfo ci = chunk_info(chunks, c);
+  const size_t cb = (size_t)c * H + h;
+
+  __shared__ __attribute__((aligned(16))) bf16 Qs[64 * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 Ks[64 * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 QnT[128 * LDT];
+  __shared__ __attribute__((aligned(16))) bf16 KnT[128 * LDT];
+  __shared__ __attribute__((aligned(16))) bf16 dPm[64 * LDT];   // [t][s]
+  __shared__ __attribute__((aligned(16))) bf16 dPmT[64 * LDT];  // [s][t]
+  __shared__ __attribute__((aligned(16))) uint8_t un[2 * 64 * LDK * 2];  // dOs | Vns, later DQs
+  __shared__ float Gs[64];
+  __shared__ float dgw[4][64];
+  __shared__ float red[4];
+  bf16* dOs = reinterpret_cast<bf16*>(un);
+  bf16* Vns = dOs + 64 * LDK;
+  float* DQs = reinterpret_cast<float*>(un);
+
+  {
+    const int t = tid >> 2, p = tid & 3;
+    const bool in = t < ci.len;
+    const size_t row = ((size_t)(ci.start + t) * H + h) * D;
+    if (p == 0) Gs[t] = gc[(size_t)(ci.start + (in ? t : ci.len - 1)) * H + h];
+    dgw[wave][lane] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = 32 * j + 8 * p;
+      const bf16x8 xq = in ? ld8(qn + row + col) : zero8();
+      const bf16x8 xk = in ? ld8(kn + row + col) : zero8();
+      st8(Qs + t * LDK + col, xq);
+      st8(Ks + t * LDK + col, xk);
+      st8(dOs + t * LDK + col, in ? ld8(dout + row + col) : zero8());
+      st8(Vns + t * LDK + col, in ? ld8(vnR + row + col) : zero8());
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        QnT[(col + s) * LDT + t] = xq[s];
+        KnT[(col + s) * LDT + t] = xk[s];
+      }
+    }
+  }
+  __syncthreads();
+  const float glast = Gs[ci.len - 1];
+  float* dg = dgw[wave];
+
+  // ---- phase 1: P, dP for t-tile = wave, s-tiles <= wave ----
+  {
+    float rowE[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      f32x4 dpm = zero4();
+      if (n <= wave) {
+        f32x4 p = zero4(), dp = zero4();
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          p = mfma(ld8(Qs + (16 * wave + r) * LDK + 32 * kb + 8 * q4), ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4), p);
+          dp = mfma(ld8(dOs + (16 * wave + r) * LDK + 32 * kb + 8 * q4),
+                    ld8(Vns + (16 * n + r) * LDK + 32 * kb + 8 * q4), dp);
+        }
+        const int s = 16 * n + r;
+        float colE = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int t = 16 * wave + 4 * q4 + i;
+          const float gam = (s <= t) ? __expf(Gs[t] - Gs[s]) : 0.f;
+          dpm[i] = scale * dp[i] * gam;
+          const float e = dpm[i] * p[i];
+          rowE[i] += e;
+          colE += e;
+        }
+        colE += __shfl_xor(colE, 16, 64);
+        colE += __shfl_xor(colE, 32, 64);
+        if (q4 == 0) dg[s] -= colE;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dPm[(16 * wave + 4 * q4 + i) * LDT + 16 * n + r] = (bf16)dpm[i];
+      st4(dPmT + (16 * n + r) * LDT + 16 * wave + 4 * q4, dpm);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = sum16(rowE[i]);
+      if (r == 0) dg[16 * wave + 4 * q4 + i] += x;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 2: dQ (rows t, k-tiles 2w, 2w+1) ----
+  const bf16* hr = hR + cb * (D * D);
+  bf16x8 bh[2][4];  // h rows k (16m + r), value block kb
+#pragma unroll
+  for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) bh[mm][kb] = ld8(hr + (16 * (2 * wave + mm) + r) * D + 32 * kb + 8 * q4);
+  f32x4 dQ[2][4];
+  {
+    f32x4 a1[2][4];
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) a1[mm][n] = dQ[mm][n] = zero4();
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const bf16x8 a = ld8(dOs + (16 * n + r) * LDK + 32 * kb + 8 * q4);
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) a1[mm][n] = mfma(a, bh[mm][kb], a1[mm][n]);
+      }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        if (n < 2 * kb) continue;
+        const bf16x8 a = ld8(dPm + (16 * n + r) * LDT + 32 * kb + 8 * q4);
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm)
+          dQ[mm][n] = mfma(a, ld8(KnT + (16 * (2 * wave + mm) + r) * LDT + 32 * kb + 8 * q4), dQ[mm][n]);
+      }
+    // dQ += scale * gam_t * (dO h^T); dG_t += sum_k Qn * that
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * n + 4 * q4 + i;
+        const float f = scale * __expf(Gs[t]);
+        float x = 0.f;
+#pragma unroll
+        for (int mm = 0; mm < 2; ++mm) {
+          const float inter = a1[mm][n][i] * f;
+          dQ[mm][n][i] += inter;
+          x += (float)Qs[t * LDK + 16 * (2 * wave + mm) + r] * inter;
+        }
+        x = sum16(x);
+        if (r == 0) dg[t] += x;
+      }
+    }
+  }
+
+  // ---- phase 3: dK^T (k rows, t columns) ----
+  {
+    const bf16* dhc = dh + cb * (D * D);
+    float esum = 0.f;
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      const int m = 2 * wave + mm;
+      f32x4 a3[4], a4[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) a3[n] = a4[n] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const bf16x8 a = ld8(QnT + (16 * m + r) * LDT + 32 * kb + 8 * q4);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          if (n > 2 * kb + 1) continue;
+          a3[n] = mfma(a, ld8(dPmT + (16 * n + r) * LDT + 32 * kb + 8 * q4), a3[n]);
+        }
+      }
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const bf16x8 a = ld8(dhc + (16 * m + r) * D + 32 * kb + 8 * q4);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) a4[n] = mfma(a, ld8(Vns + (16 * n + r) * LDK + 32 * kb + 8 * q4), a4[n]);
+      }
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const int t = 16 * n + r;
+        const float kd = __expf(glast - Gs[t]);
+        const f32x4 st = a4[n] * kd;
+        const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
+        float e = st[0] * kk[0] + st[1] * kk[1] + st[2] * kk[2] + st[3] * kk[3];
+        e += __shfl_xor(e, 16, 64);
+        e += __shfl_xor(e, 32, 64);
+        if (q4 == 0) dg[t] -= e;
+        esum += (q4 == 0) ? e : 0.f;
+        if (t < ci.len)
+          *reinterpret_cast<f32x4*>(dKp + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4) = a3[n] + st;
+      }
+    }
+    esum = sum16(esum);
+    if (lane == 0) dg[ci.len - 1] += esum;
+  }
+
+  // ---- phase 4: dW = -dVn S^T  (both orientations) and <S, dS> ----
+  {
+    bf16x8 av[4][4];  // dVn rows t (16n + r), value block kb
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const int t = 16 * n + r;
+      const bf16* vrow = dVn + ((size_t)(ci.start + t) * H + h) * D;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) av[n][kb] = (t < ci.len) ? neg8(ld8(vrow + 32 * kb + 8 * q4)) : zero8();
+    }
+    bf16* wt = dWT + cb * (D * CH);
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      const int m = 2 * wave + mm;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        f32x4 w1 = zero4(), w2 = zero4();
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          w1 = mfma(av[n][kb], bh[mm][kb], w1);  // dW[t][k]  (rows t)
+          w2 = mfma(bh[mm][kb], av[n][kb], w2);  // dW^T[k][t] (rows k)
+        }
+        st4(wt + (16 * m + r) * CH + 16 * n + 4 * q4, w1);
+        const int t = 16 * n + r;
+        if (t < ci.len) st4(dW + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4, w2);
+      }
+    }
+    const bf16* dhc = dh + cb * (D * D);
+    float x = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int off = 8 * tid + 2048 * j;
+      const f32x8 a = cvtf8(ld8(hr + off)), b = cvtf8(ld8(dhc + off));
+#pragma unroll
+      for (int s = 0; s < 8; ++s) x += a[s] * b[s];
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
+    if (lane == 0) red[wave] = x;
+  }
+  __syncthreads();  // all reads of dOs / Vns are done: DQs may overwrite them
+
+  // ---- phase 5: l2norm backward of dq, dG partial ----
+#pragma unroll
+  for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) DQs[(16 * n + 4 * q4 + i) * LDQ + 16 * (2 * wave + mm) + r] = dQ[mm][n][i];
+  __syncthreads();
+  {
+    const int t = tid >> 2, p = tid & 3;
+    const bool in = t < ci.len;
+    f32x8 dqn[4], qv[4];
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = 32 * j + 8 * p;
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(DQs + t * LDQ + col);
+      const f32x4 hi = *reinterpret_cast<const f32x4*>(DQs + t * LDQ + col + 4);
+      dqn[j] = f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      qv[j] = cvtf8(ld8(Qs + t * LDK + col));
+#pragma unroll
+      for (int s = 0; s < 8; ++s) dot += qv[j][s] * dqn[j][s];
+    }
+    dot += __shfl_xor(dot, 1, 64);
+    dot += __shfl_xor(dot, 2, 64);
+    if (in) {
+      const float rs = normalize ? rq[(size_t)(ci.start + t) * H + h] : 1.f;
+      const size_t row = ((size_t)(ci.start + t) * H + h) * D;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x8 out = normalize ? (dqn[j] - qv[j] * dot) * rs : dqn[j];
+        st8(dq + row + 32 * j + 8 * p, cvt8(out));
+      }
+    }
+  }
+  if (tid < 64) {
+    const int t = tid;
+    float tot = dgw[0][t] + dgw[1][t] + dgw[2][t] + dgw[3][t];
+    if (t == ci.len - 1) tot += __expf(glast) * (red[0] + red[1] + red[2] + red[3]);
+    if (t < ci.len) dGp[(size_t)(ci.start + t) * H + h] = tot;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// bwd_wy
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void bwd_wy_kernel(
+    const bf16* __restrict__ kn, const bf16* __restrict__ vin, const float* __restrict__ beta,
+    const float* __restrict__ gc, const float* __restrict__ rk, const bf16* __restrict__ Tm,
+    const bf16* __restrict__ dW, const bf16* __restrict__ dWT, const bf16* __restrict__ dVn,
+    const bf16* __restrict__ dVnT, const float* __restrict__ dKp, const float* __restrict__ dGp,
+    const int32_t* __restrict__ chunks, int H, int normalize, bf16* __restrict__ dk, bf16* __restrict__ dv,
+    float* __restrict__ dg, float* __restrict__ dbeta) {
+  const int c = blockIdx.x, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q4 = lane >> 4;
+  const ChunkInfo ci = chunk_info(chunks, c);
+  const size_t cb = (size_t)c * H + h;
+
+  __shared__ __attribute__((aligned(16))) bf16 Ks[64 * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 Vs[64 * LDK];
+  __shared__ __attribute__((aligned(16))) bf16 KnT[128 * LDT];
+  __shared__ __attribute__((aligned(16))) bf16 Ts[64 * LDT];   // T[t][s]
+  __shared__ __attribute__((aligned(16))) bf16 TTs[64 * LDT];  // T^T[s][t]
+  __shared__ __attribute__((aligned(16))) bf16 S1[64 * LDT];   // dT[t][s], then beta*dM [i][j]
+  __shared__ __attribute__((aligned(16))) bf16 S2[64 * LDT];   // Y^T[j][t]
+  __shared__ __attribute__((aligned(16))) bf16 S3[64 * LDT];   // (beta*dM)^T [j][i]
+  __shared__ __attribute__((aligned(16))) float DKs[64 * LDQ];
+  __shared__ float Gs[64], Bs[64];
+  __shared__ float dgw[4][64], dbw[4][64];
+
+  {
+    const int t = tid >> 2, p = tid & 3;
+    const bool in = t < ci.len;
+    const size_t row = ((size_t)(ci.start + t) * H + h) * D;
+    if (p == 0) {
+      Gs[t] = gc[(size_t)(ci.start + (in ? t : ci.len - 1)) * H + h];
+      Bs[t] = in ? beta[(size_t)(ci.start + t) * H + h] : 0.f;
+    }
+    dgw[wave][lane] = 0.f;
+    dbw[wave][lane] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = 32 * j + 8 * p;
+      const bf16x8 xk = in ? ld8(kn + row + col) : zero8();
+      st8(Ks + t * LDK + col, xk);
+      st8(Vs + t * LDK + col, in ? ld8(vin + row + col) : zero8());
+#pragma unroll
+      for (int s = 0; s < 8; ++s) KnT[(col + s) * LDT + t] = xk[s];
+    }
+    const bf16* tm = Tm + cb * (CH * CH);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = 32 * j + 8 * p;
+      const bf16x8 x = ld8(tm + t * CH + col);
+      st8(Ts + t * LDT + col, x);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) TTs[(col + s) * LDT + t] = x[s];
+    }
+  }
+  __syncthreads();
+  float* dgl = dgw[wave];
+  float* dbl = dbw[wave];
+
+  // ---- phase 1: dT^T (rows s = s-tile wave, columns t) -> S1 = dT[t][s] ----
+  {
+    const int s = 16 * wave + r;
+    const float fk = Bs[s] * __expf(Gs[s]), fv = Bs[s];
+    f32x4 acc[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[b] = zero4();
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const bf16x8 ak = cvt8(cvtf8(ld8(Ks + s * LDK + 32 * kb + 8 * q4)) * fk);
+      const bf16x8 av = cvt8(cvtf8(ld8(Vs + s * LDK + 32 * kb + 8 * q4)) * fv);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int t = 16 * b + r;
+        const size_t row = ((size_t)(ci.start + t) * H + h) * D + 32 * kb + 8 * q4;
+        const bool in = t < ci.len;
+        acc[b] = mfma(ak, in ? ld8(dW + row) : zero8(), acc[b]);
+        acc[b] = mfma(av, in ? ld8(dVn + row) : zero8(), acc[b]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b) st4(S1 + (16 * b + r) * LDT + 16 * wave + 4 * q4, acc[b]);
+  }
+  __syncthreads();
+
+  // ---- phase 2: Y = dT T^T (rows t = t-tile wave) -> S2 = Y^T[j][t] ----
+  {
+    bf16x8 a[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) a[kb] = ld8(S1 + (16 * wave + r) * LDT + 32 * kb + 8 * q4);
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        if (n < 2 * kb) continue;  // T[j][b] = 0 for b > j
+        acc = mfma(a[kb], ld8(Ts + (16 * n + r) * LDT + 32 * kb + 8 * q4), acc);
+      }
+      st4(S2 + (16 * n + r) * LDT + 16 * wave + 4 * q4, acc);
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 3: dA = -T^T Y (rows i = i-tile wave), dM, dbeta and dG from A ----
+  {
+    const int kb0 = wave >= 2 ? 1 : 0;  // T[t][i] = 0 for t < i
+    bf16x8 at[2], ak[4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) at[kb] = ld8(TTs + (16 * wave + r) * LDT + 32 * kb + 8 * q4);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) ak[kb] = ld8(Ks + (16 * wave + r) * LDK + 32 * kb + 8 * q4);
+    float rowB[4] = {0.f, 0.f, 0.f, 0.f}, rowE[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      f32x4 dmp = zero4();
+      if (n <= wave) {
+        f32x4 da = zero4(), kk = zero4();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+          if (kb >= kb0) da = mfma(at[kb], ld8(S2 + (16 * n + r) * LDT + 32 * kb + 8 * q4), da);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) kk = mfma(ak[kb], ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4), kk);
+        const int j = 16 * n + r;
+        float colE = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 16 * wave + 4 * q4 + e;
+          const bool strict = j < i;
+          const float gam = strict ? __expf(Gs[i] - Gs[j]) : 0.f;
+          const float dA = strict ? -da[e] : 0.f;
+          const float dM = dA * gam;
+          const float Aij = Bs[i] * kk[e] * gam;
+          dmp[e] = Bs[i] * dM;
+          rowB[e] += dM * kk[e];
+          const float e2 = dA * Aij;
+          rowE[e] += e2;
+          colE += e2;
+        }
+        colE += __shfl_xor(colE, 16, 64);
+        colE += __shfl_xor(colE, 32, 64);
+        if (q4 == 0) dgl[j] -= colE;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) S1[(16 * wave + 4 * q4 + e) * LDT + 16 * n + r] = (bf16)dmp[e];
+      st4(S3 + (16 * n + r) * LDT + 16 * wave + 4 * q4, dmp);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float xb = sum16(rowB[e]);
+      const float xe = sum16(rowE[e]);
+      if (r == 0) {
+        dbl[16 * wave + 4 * q4 + e] += xb;
+        dgl[16 * wave + 4 * q4 + e] += xe;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 4a: dK^T (k rows 2w, 2w+1; t columns) -> DKs[t][k] ----
+  {
+    const bf16* dwt = dWT + cb * (D * CH);
+    float colB[4] = {0.f, 0.f, 0.f, 0.f}, colG[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      const int m = 2 * wave + mm;
+      f32x4 ak[4], aw[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) ak[n] = aw[n] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const bf16x8 a = ld8(KnT + (16 * m + r) * LDT + 32 * kb + 8 * q4);
+        const bf16x8 w = ld8(dwt + (16 * m + r) * CH + 32 * kb + 8 * q4);
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          if (n >= 2 * kb) ak[n] = mfma(a, ld8(S1 + (16 * n + r) * LDT + 32 * kb + 8 * q4), ak[n]);  // j < i
+          if (kb >= 1 || n < 2) {
+            ak[n] = mfma(a, ld8(S3 + (16 * n + r) * LDT + 32 * kb + 8 * q4), ak[n]);  // i > j
+            aw[n] = mfma(w, ld8(TTs + (16 * n + r) * LDT + 32 * kb + 8 * q4), aw[n]);  // t >= s
+          }
+        }
+      }
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const int t = 16 * n + r;
+        const float bg = Bs[t] * __expf(Gs[t]);
+        const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
+        const float x = aw[n][0] * kk[0] + aw[n][1] * kk[1] + aw[n][2] * kk[2] + aw[n][3] * kk[3];
+        colB[n] += __expf(Gs[t]) * x;
+        colG[n] += bg * x;
+        f32x4 tot = ak[n] + aw[n] * bg;
+        if (t < ci.len) tot += *reinterpret_cast<const f32x4*>(dKp + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4);
+        *reinterpret_cast<f32x4*>(DKs + t * LDQ + 16 * m + 4 * q4) = tot;
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      float xb = colB[n], xg = colG[n];
+      xb += __shfl_xor(xb, 16, 64);
+      xb += __shfl_xor(xb, 32, 64);
+      xg += __shfl_xor(xg, 16, 64);
+      xg += __shfl_xor(xg, 32, 64);
+      if (q4 == 0) {
+        dbl[16 * n + r] += xb;
+        dgl[16 * n + r] += xg;
+      }
+    }
+  }
+  // ---- phase 4b: dV^T (v rows 2w, 2w+1; s columns): dv = beta (T^T dVn) ----
+  {
+    const bf16* dvt = dVnT + cb * (D * CH);
+    float colB[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      const int m = 2 * wave + mm;
+      f32x4 acc[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) acc[n] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const bf16x8 a = ld8(dvt + (16 * m + r) * CH + 32 * kb + 8 * q4);
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+          if (kb >= 1 || n < 2) acc[n] = mfma(a, ld8(TTs + (16 * n + r) * LDT + 32 * kb + 8 * q4), acc[n]);
+      }
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const int s = 16 * n + r;
+        const f32x4 vv = cvtf4(ld4(Vs + s * LDK + 16 * m + 4 * q4));
+        colB[n] += acc[n][0] * vv[0] + acc[n][1] * vv[1] + acc[n][2] * vv[2] + acc[n][3] * vv[3];
+        if (s < ci.len) st4(dv + ((size_t)(ci.start + s) * H + h) * D + 16 * m + 4 * q4, acc[n] * Bs[s]);
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      float xb = colB[n];
+      xb += __shfl_xor(xb, 16, 64);
+      xb += __shfl_xor(xb, 32, 64);
+      if (q4 == 0) dbl[16 * n + r] += xb;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 5: l2norm backward of dk; dg (reverse cumsum), dbeta ----
+  {
+    const int t = tid >> 2, p = tid & 3;
+    const bool in = t < ci.len;
+    f32x8 dkn[4], kv[4];
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = 32 * j + 8 * p;
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(DKs + t * LDQ + col);
+      const f32x4 hi = *reinterpret_cast<const f32x4*>(DKs + t * LDQ + col + 4);
+      dkn[j] = f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      kv[j] = cvtf8(ld8(Ks + t * LDK + col));
+#pragma unroll
+      for (int s = 0; s < 8; ++s) dot += kv[j][s] * dkn[j][s];
+    }
+    dot += __shfl_xor(dot, 1, 64);
+    dot += __shfl_xor(dot, 2, 64);
+    if (in) {
+      const float rs = normalize ? rk[(size_t)(ci.start + t) * H + h] : 1.f;
+      const size_t row = ((size_t)(ci.start + t) * H + h) * D;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x8 out = normalize ? (dkn[j] - kv[j] * dot) * rs : dkn[j];
+        st8(dk + row + 32 * j + 8 * p, cvt8(out));
+      }
+    }
+  }
+  if (tid < 64) {
+    const int t = tid;
+    const bool in = t < ci.len;
+    float x = in ? dGp[(size_t)(ci.start + t) * H + h] + dgw[0][t] + dgw[1][t] + dgw[2][t] + dgw[3][t] : 0.f;
+    // reverse (suffix) cumsum within the chunk
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float o = __shfl_down(x, off, 64);
+      if (t + off < 64) x += o;
+    }
+    if (in) {
+      dg[(size_t)(ci.start + t) * H + h] = x;
+      dbeta[(size_t)(ci.start + t) * H + h] = dbw[0][t] + dbw[1][t] + dbw[2][t] + dbw[3][t];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+void launch_bwd(const BwdArgs& a, hipStream_t stream) {
+  auto F = [&](int i) { return reinterpret_cast<const bf16*>(a.fws + a.foff[i]); };
+  auto Ff = [&](int i) { return reinterpret_cast<const float*>(a.fws + a.foff[i]); };
+  auto B = [&](int i) { return reinterpret_cast<bf16*>(a.bws + a.boff[i]); };
+  auto Bf = [&](int i) { return reinterpret_cast<float*>(a.bws + a.boff[i]); };
+  const dim3 grid_c(a.n_chunks, a.H);
+  hipLaunchKernelGGL(bwd_local_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), a.dout, Ff(F_GC), a.chunks,
+                     a.H, a.scale, B(B_DVLT), B(B_XT));
+  hipLaunchKernelGGL(bwd_state_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(64), 0, stream, F(F_KN), Ff(F_GC),
+                     B(B_DVLT), B(B_XT), F(F_WT), a.chunks, a.doc_chunk, a.H, B(B_DH), B(B_DVNT), B(B_DVN));
+  hipLaunchKernelGGL(bwd_dqk_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_GC), F(F_HR),
+                     F(F_VN), a.dout, B(B_DH), B(B_DVN), a.chunks, a.H, a.scale, (int)a.normalize, a.dq, Bf(B_DKP),
+                     B(B_DW), B(B_DWT), Bf(B_DGP));
+  hipLaunchKernelGGL(bwd_wy_kernel, grid_c, dim3(256), 0, stream, F(F_KN), a.v, a.beta, Ff(F_GC), Ff(F_RK),
+                     F(F_TM), B(B_DW), B(B_DWT), B(B_DVN), B(B_DVNT), Bf(B_DKP), Bf(B_DGP), a.chunks, a.H,
+                     (int)a.normalize, a.dk, a.dv, a.dg, a.dbeta);
+}
+
+}  // namespace cqgdn

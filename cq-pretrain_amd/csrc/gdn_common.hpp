@@ -1,0 +1,110 @@
+// Shared device helpers for the gfx950 gated delta-rule (GDN) kernels.
+//
+// Every contraction runs on v_mfma_f32_16x16x32_bf16 (wave64).  Operand and
+// result layouts of that instruction, as used throughout:
+//
+//   lane = threadIdx.x % 64, r = lane % 16, q4 = lane / 16 (0..3)
+//   A operand (16 x 32, M x K):  lane holds A[m0 + r][k-slots of group q4]      (8 bf16)
+//   B operand (32 x 16, K x N):  lane holds B[k-slots of group q4][n0 + r]      (8 bf16)
+//   C/D       (16 x 16, M x N):  lane holds D[m0 + 4*q4 + i][n0 + r], i = 0..3  (4 fp32)
+//
+// The hardware pairs slot s of A with slot s of B, so which logical k a slot
+// carries is ours to choose as long as A and B agree.  Two slot maps are used:
+//   natural  : slot s of group q4 = k0 + 8*q4 + s              (one 16-byte load)
+//   permuted : slot s of group q4 = k0 + 4*q4 + (s&3) + 16*(s>>2)
+// The permuted map is what two stacked C tiles (rows k0..k0+15, k0+16..k0+31)
+// already hold per lane, so an MFMA result feeds a following contraction over
+// its M index straight from registers; the other operand is then fetched with
+// two 8-byte loads (k0+4*q4.. and k0+16+4*q4..).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cqgdn {
+
+constexpr int D = 128;   // head dimension (d_k = d_v), the only one the reference accepts
+constexpr int CH = 64;   // chunk length of the WY/UT form
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+__device__ __forceinline__ bf16x8 zero8() {
+  bf16x8 z;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) z[i] = (bf16)0.f;
+  return z;
+}
+
+__device__ __forceinline__ bf16x4 cvt4(f32x4 x) { return __builtin_convertvector(x, bf16x4); }
+__device__ __forceinline__ f32x4 cvtf4(bf16x4 x) { return __builtin_convertvector(x, f32x4); }
+__device__ __forceinline__ f32x8 cvtf8(bf16x8 x) { return __builtin_convertvector(x, f32x8); }
+__device__ __forceinline__ bf16x8 cvt8(f32x8 x) { return __builtin_convertvector(x, bf16x8); }
+
+// Two C tiles (rows m0..m0+15 and m0+16..m0+31 of one column) -> one operand
+// in the permuted slot map.
+__device__ __forceinline__ bf16x8 pack_perm(f32x4 lo, f32x4 hi) {
+  f32x8 x = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  return cvt8(x);
+}
+
+__device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+__device__ __forceinline__ bf16x8 neg8(bf16x8 x) {
+  // flip the sign bits (exact)
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 u = __builtin_bit_cast(u32x4, x);
+  u ^= 0x80008000u;
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+// ---- fragment loads -------------------------------------------------------
+// natural map, k-contiguous storage: 8 consecutive elements at p (16-byte aligned)
+__device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+__device__ __forceinline__ bf16x4 ld4(const bf16* p) { return *reinterpret_cast<const bf16x4*>(p); }
+// permuted map, k-contiguous storage: p points at element k0 + 4*q4
+__device__ __forceinline__ bf16x8 ld8p(const bf16* p) { return cat(ld4(p), ld4(p + 16)); }
+// natural map, strided storage: element s at p[s * stride]
+__device__ __forceinline__ bf16x8 ld8s(const bf16* p, int stride) {
+  bf16x8 x;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) x[s] = p[s * stride];
+  return x;
+}
+
+__device__ __forceinline__ void st4(bf16* p, f32x4 x) { *reinterpret_cast<bf16x4*>(p) = cvt4(x); }
+__device__ __forceinline__ void st8(bf16* p, bf16x8 x) { *reinterpret_cast<bf16x8*>(p) = x; }
+
+// ---- wave reductions -------------------------------------------------------
+// sum over the 16 lanes that share q4 (the 16 columns of a C tile)
+__device__ __forceinline__ float sum16(float x) {
+  x += __shfl_xor(x, 1, 64);
+  x += __shfl_xor(x, 2, 64);
+  x += __shfl_xor(x, 4, 64);
+  x += __shfl_xor(x, 8, 64);
+  return x;
+}
+
+// Per-chunk metadata: chunk_table[c] = (start event, length).  A chunk never
+// crosses a document boundary; doc_chunk[d] .. doc_chunk[d+1] are the chunks of
+// document d, in time order.
+struct ChunkInfo {
+  int start, len;
+};
+__device__ __forceinline__ ChunkInfo chunk_info(const int32_t* table, int c) {
+  return ChunkInfo{table[2 * c], table[2 * c + 1]};
+}
+
+}  // namespace cqgdn

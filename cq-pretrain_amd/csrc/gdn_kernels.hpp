@@ -1,0 +1,57 @@
+// Host-side argument blocks and launchers of the GDN kernels (internal to libcqgdn).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "gdn_layout.hpp"
+
+namespace cqgdn {
+
+typedef __bf16 bf16;
+
+struct FwdArgs {
+  const bf16 *q, *k, *v;
+  const float *g, *beta;
+  const int32_t* chunks;     // [n_chunks][2] (start, len)
+  const int32_t* doc_chunk;  // [n_docs + 1]
+  int T, H, n_chunks, n_docs;
+  float scale;
+  bool normalize, training;
+  const float* initial_state;  // [n_docs][H][K][V] or null
+  float* final_state;          // [n_docs][H][K][V] or null
+  bf16* o;                     // [T][H][D]
+  uint8_t* ws;
+  size_t off[F_COUNT];
+};
+
+struct BwdArgs {
+  const bf16 *v, *dout;
+  const float *g, *beta;
+  const int32_t* chunks;
+  const int32_t* doc_chunk;
+  int T, H, n_chunks, n_docs;
+  float scale;
+  bool normalize;
+  const uint8_t* fws;  // forward workspace
+  size_t foff[F_COUNT];
+  uint8_t* bws;        // backward workspace
+  size_t boff[B_COUNT];
+  bf16 *dq, *dk, *dv;
+  float *dg, *dbeta;
+};
+
+void launch_fwd(const FwdArgs& a, hipStream_t stream);
+void launch_bwd(const BwdArgs& a, hipStream_t stream);
+void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* g, const void* beta,
+                      bool beta_bf16, float* state, bf16* out, int N, int E, int H, float scale,
+                      hipStream_t stream);
+void launch_l2norm_fwd(const bf16* x, bf16* y, float* rstd, int64_t rows, hipStream_t stream);
+void launch_l2norm_bwd(const bf16* y, const float* rstd, const bf16* dy, bf16* dx, int64_t rows,
+                       hipStream_t stream);
+// dst[i] = src ? src[i] : 0 (a kernel, not hipMemset, so callers may capture it in a graph)
+void launch_copy_or_zero(float* dst, const float* src, size_t n, hipStream_t stream);
+void launch_chunk_cumsum(const float* g, float* out, const int32_t* chunks, int n_chunks, int H, bool reverse,
+                         hipStream_t stream);
+
+}  // namespace cqgdn

@@ -1,0 +1,91 @@
+// Workspace layout of the GDN forward/backward passes (host and device).
+//
+// The forward workspace holds everything the backward re-reads (the reference
+// saves q,k,v,gcum,beta,A in fused mode and also w,h,v_new in cached mode,
+// ops/gated_delta_net.py:184); keeping h and v_new avoids re-running the serial
+// state scan in the backward.  Buffers are addressed by event (time-first
+// [T][H][D], the caller's TND order) or by chunk ([NC][H][...], one 64-event
+// block per chunk, rows past a tail chunk's length are zero).
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+namespace cqgdn {
+
+enum FwdBuf {
+  F_QN = 0,  // bf16 [T][H][D]   l2-normalized q (unscaled)
+  F_KN,      // bf16 [T][H][D]   l2-normalized k
+  F_RQ,      // f32  [T][H]      rsqrt(sum q^2 + eps)
+  F_RK,      // f32  [T][H]      rsqrt(sum k^2 + eps)
+  F_GC,      // f32  [T][H]      chunk-local cumsum of g
+  F_TM,      // bf16 [NC][H][64][64]  T = (I + A)^-1, row-major (t, s)
+  F_W,       // bf16 [T][H][D]   W = T (beta*exp(G)*K), rows (t, k)
+  F_WT,      // bf16 [NC][H][D][64]   W transposed (k, t)
+  F_UT,      // bf16 [NC][H][D][64]   U = T (beta*V) transposed (v, t)
+  F_KGT,     // bf16 [NC][H][D][64]   (K * exp(G_last - G)) transposed (k, t)
+  F_HT,      // bf16 [NC][H][D][D]    state entering the chunk, (v, k)
+  F_HR,      // bf16 [NC][H][D][D]    same state, (k, v)           [training]
+  F_VNT,     // bf16 [NC][H][D][64]   v_new transposed (v, t)
+  F_VN,      // bf16 [T][H][D]        v_new rows (t, v)              [training]
+  F_COUNT
+};
+
+enum BwdBuf {
+  B_DVLT = 0,  // bf16 [NC][H][D][64]  local dv = scale*P^T dO, (v, t)
+  B_XT,        // bf16 [NC][H][D][D]   X = scale*(gam*Qn)^T dO, (v, k)
+  B_DH,        // bf16 [NC][H][D][D]   gradient of the state leaving the chunk, (k, v)
+  B_DVNT,      // bf16 [NC][H][D][64]  d v_new, (v, t)
+  B_DVN,       // bf16 [T][H][D]       d v_new rows (t, v)
+  B_DKP,       // f32  [T][H][D]       partial dKn (output and state terms)
+  B_DW,        // bf16 [T][H][D]       dW rows (t, k)
+  B_DWT,       // bf16 [NC][H][D][64]  dW transposed (k, t)
+  B_DGP,       // f32  [T][H]          partial dG (before the reverse cumsum)
+  B_COUNT
+};
+
+constexpr size_t kAlign = 256;
+
+inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+inline void fwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
+  const size_t ev = (size_t)T * H, chunk = (size_t)NC * H;
+  s[F_QN] = ev * 128 * 2;
+  s[F_KN] = ev * 128 * 2;
+  s[F_RQ] = ev * 4;
+  s[F_RK] = ev * 4;
+  s[F_GC] = ev * 4;
+  s[F_TM] = chunk * 64 * 64 * 2;
+  s[F_W] = ev * 128 * 2;
+  s[F_WT] = chunk * 128 * 64 * 2;
+  s[F_UT] = chunk * 128 * 64 * 2;
+  s[F_KGT] = chunk * 128 * 64 * 2;
+  s[F_HT] = chunk * 128 * 128 * 2;
+  s[F_HR] = chunk * 128 * 128 * 2;
+  s[F_VNT] = chunk * 128 * 64 * 2;
+  s[F_VN] = ev * 128 * 2;
+}
+
+inline void bwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
+  const size_t ev = (size_t)T * H, chunk = (size_t)NC * H;
+  s[B_DVLT] = chunk * 128 * 64 * 2;
+  s[B_XT] = chunk * 128 * 128 * 2;
+  s[B_DH] = chunk * 128 * 128 * 2;
+  s[B_DVNT] = chunk * 128 * 64 * 2;
+  s[B_DVN] = ev * 128 * 2;
+  s[B_DKP] = ev * 128 * 4;
+  s[B_DW] = ev * 128 * 2;
+  s[B_DWT] = chunk * 128 * 64 * 2;
+  s[B_DGP] = ev * 4;
+}
+
+// Offsets of every buffer; returns the total size in bytes.
+inline size_t offsets(const size_t* sizes, int n, size_t* off) {
+  size_t at = 0;
+  for (int i = 0; i < n; ++i) {
+    off[i] = at;
+    at += align_up(sizes[i]);
+  }
+  return at;
+}
+
+}  // namespace cqgdn

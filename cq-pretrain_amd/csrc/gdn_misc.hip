@@ -1,0 +1,170 @@
+// Memory-bound GDN kernels: the recurrent decode step, standalone l2norm
+// forward/backward and the chunk-local (reverse) cumsum.
+#include "gdn_common.hpp"
+#include "gdn_kernels.hpp"
+
+namespace cqgdn {
+
+// ---------------------------------------------------------------------------
+// recurrent: E events applied in order to each of N independent sequences.
+// state is value-first [N][H][V][K] fp32 and is updated in place
+// (ops/gated_delta_net.py:314-352, math of models/decoding.py:71-77):
+//   S <- exp(g) S ;  r = (v - S k) * beta ;  S <- S + r k^T ;  o = scale * S q
+// One thread owns a quarter of a state row (32 fp32 = 8 float4, interleaved so a
+// wave's loads are contiguous); the row is read once and written once per call
+// whatever E is, which makes the step HBM-bound at 2 * 64 KB per (sequence, head).
+// ---------------------------------------------------------------------------
+template <bool BETA_BF16>
+__global__ __launch_bounds__(256) void recurrent_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                        const bf16* __restrict__ v, const float* __restrict__ g,
+                                                        const void* __restrict__ beta, float* __restrict__ state,
+                                                        bf16* __restrict__ out, int E, int H, float scale) {
+  const int blk = blockIdx.x;              // (n, h, half)
+  const int half = blk & 1, nh = blk >> 1;  // nh = n * H + h
+  const int n = nh / H, h = nh % H;
+  const int tid = threadIdx.x;
+  const int vrow = 64 * half + (tid >> 2), p = tid & 3;
+  float* srow = state + ((size_t)nh * D + vrow) * D;
+  f32x4 s[8];
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) s[jj] = *reinterpret_cast<const f32x4*>(srow + 4 * (p + 4 * jj));
+  for (int e = 0; e < E; ++e) {
+    const size_t ev = ((size_t)n * E + e) * H + h;
+    const bf16* kr = k + ev * D;
+    const bf16* qr = q + ev * D;
+    const float ge = __expf(g[ev]);
+    const float be = BETA_BF16 ? (float)reinterpret_cast<const bf16*>(beta)[ev] : reinterpret_cast<const float*>(beta)[ev];
+    f32x4 kk[8];
+    float dot = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      kk[jj] = cvtf4(ld4(kr + 4 * (p + 4 * jj)));
+      s[jj] *= ge;
+      dot += s[jj][0] * kk[jj][0] + s[jj][1] * kk[jj][1] + s[jj][2] * kk[jj][2] + s[jj][3] * kk[jj][3];
+    }
+    dot += __shfl_xor(dot, 1, 64);
+    dot += __shfl_xor(dot, 2, 64);
+    const float rv = ((float)v[ev * D + vrow] - dot) * be;
+    float o = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      s[jj] += kk[jj] * rv;
+      const f32x4 qq = cvtf4(ld4(qr + 4 * (p + 4 * jj)));
+      o += s[jj][0] * qq[0] + s[jj][1] * qq[1] + s[jj][2] * qq[2] + s[jj][3] * qq[3];
+    }
+    o += __shfl_xor(o, 1, 64);
+    o += __shfl_xor(o, 2, 64);
+    if (p == 0) out[ev * D + vrow] = (bf16)(o * scale);
+  }
+#pragma unroll
+  for (int jj = 0; jj < 8; ++jj) *reinterpret_cast<f32x4*>(srow + 4 * (p + 4 * jj)) = s[jj];
+}
+
+void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* g, const void* beta,
+                      bool beta_bf16, float* state, bf16* out, int N, int E, int H, float scale,
+                      hipStream_t stream) {
+  const dim3 grid(2 * N * H);
+  if (beta_bf16)
+    hipLaunchKernelGGL(recurrent_kernel<true>, grid, dim3(256), 0, stream, q, k, v, g, beta, state, out, E, H, scale);
+  else
+    hipLaunchKernelGGL(recurrent_kernel<false>, grid, dim3(256), 0, stream, q, k, v, g, beta, state, out, E, H,
+                       scale);
+}
+
+// ---------------------------------------------------------------------------
+// l2norm over rows of 128: y = x * rsqrt(sum x^2 + 1e-6); rstd saved for the
+// backward dx = rstd * (dy - y (y . dy))  (K-a of the reference's op table,
+// fla l2norm_fwd/bwd as called at ops/gated_delta_net.py:136-137,207-209).
+// 16 threads per row, 8 elements each.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void l2norm_fwd_kernel(const bf16* __restrict__ x, bf16* __restrict__ y,
+                                                         float* __restrict__ rstd, int64_t rows) {
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int c = threadIdx.x & 15;
+  if (row >= rows) return;
+  const f32x8 a = cvtf8(ld8(x + row * D + 8 * c));
+  float ss = 0.f;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) ss += a[s] * a[s];
+  ss += __shfl_xor(ss, 1, 16);
+  ss += __shfl_xor(ss, 2, 16);
+  ss += __shfl_xor(ss, 4, 16);
+  ss += __shfl_xor(ss, 8, 16);
+  const float rs = rsqrtf(ss + 1e-6f);
+  st8(y + row * D + 8 * c, cvt8(a * rs));
+  if (c == 0 && rstd) rstd[row] = rs;
+}
+
+__global__ __launch_bounds__(256) void l2norm_bwd_kernel(const bf16* __restrict__ y, const float* __restrict__ rstd,
+                                                         const bf16* __restrict__ dy, bf16* __restrict__ dx,
+                                                         int64_t rows) {
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int c = threadIdx.x & 15;
+  if (row >= rows) return;
+  const f32x8 a = cvtf8(ld8(y + row * D + 8 * c));
+  const f32x8 b = cvtf8(ld8(dy + row * D + 8 * c));
+  float dot = 0.f;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) dot += a[s] * b[s];
+  dot += __shfl_xor(dot, 1, 16);
+  dot += __shfl_xor(dot, 2, 16);
+  dot += __shfl_xor(dot, 4, 16);
+  dot += __shfl_xor(dot, 8, 16);
+  st8(dx + row * D + 8 * c, cvt8((b - a * dot) * rstd[row]));
+}
+
+void launch_l2norm_fwd(const bf16* x, bf16* y, float* rstd, int64_t rows, hipStream_t stream) {
+  const int64_t blocks = (rows + 15) / 16;
+  hipLaunchKernelGGL(l2norm_fwd_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, x, y, rstd, rows);
+}
+
+void launch_l2norm_bwd(const bf16* y, const float* rstd, const bf16* dy, bf16* dx, int64_t rows,
+                       hipStream_t stream) {
+  const int64_t blocks = (rows + 15) / 16;
+  hipLaunchKernelGGL(l2norm_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, y, rstd, dy, dx, rows);
+}
+
+// ---------------------------------------------------------------------------
+// chunk-local cumsum of g [T][H] (forward or reverse) over the chunk table
+// (K-b: chunk_local_cumsum / reverse_cumsum, ops/gated_delta_net.py:77-87,158-164)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void chunk_cumsum_kernel(const float* __restrict__ g, float* __restrict__ out,
+                                                          const int32_t* __restrict__ chunks, int H, int reverse) {
+  const int c = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
+  const ChunkInfo ci = chunk_info(chunks, c);
+  const bool in = t < ci.len;
+  float x = in ? g[(size_t)(ci.start + t) * H + h] : 0.f;
+  if (reverse) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float o = __shfl_down(x, off, 64);
+      if (t + off < 64) x += o;
+    }
+  } else {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float o = __shfl_up(x, off, 64);
+      if (t >= off) x += o;
+    }
+  }
+  if (in) out[(size_t)(ci.start + t) * H + h] = x;
+}
+
+void launch_chunk_cumsum(const float* g, float* out, const int32_t* chunks, int n_chunks, int H, bool reverse,
+                         hipStream_t stream) {
+  hipLaunchKernelGGL(chunk_cumsum_kernel, dim3(n_chunks, H), dim3(64), 0, stream, g, out, chunks, H, (int)reverse);
+}
+
+__global__ __launch_bounds__(256) void copy_or_zero_kernel(float* __restrict__ dst, const float* __restrict__ src,
+                                                           size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    dst[i] = src ? src[i] : 0.f;
+}
+
+void launch_copy_or_zero(float* dst, const float* src, size_t n, hipStream_t stream) {
+  const size_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(copy_or_zero_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, stream, dst,
+                     src, n);
+}
+
+}  // namespace cqgdn

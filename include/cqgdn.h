@@ -1,0 +1,137 @@
+/*
+ * cqgdn - C ABI of the MI355X (gfx950) gated delta-rule (GDN) backend.
+ *
+ * This is the drop-in boundary of the `gdn_backend: hip` path.  It replaces the
+ * device ops that the reference binds in ops/gated_delta_net.py (AscendC
+ * `fla_npu` ops plus FLA Triton helpers, ops/gated_delta_net.py:24-57).  All
+ * pointers are device pointers unless stated; tensors are dense row-major with
+ * the layouts given per function; `stream` is a hipStream_t (NULL = default
+ * stream).  Every call only enqueues work on `stream` and never synchronizes.
+ * Functions return CQGDN_OK or an error code; cqgdn_last_error() gives the
+ * message of the last failure on the calling thread.
+ *
+ * Layouts (T = events, H = heads, D = 128 head dimension):
+ *   q, k, v, o, dq, dk, dv, do : bf16 [T][H][D]   (the reference's TND order, B = 1)
+ *   g, beta, dg, dbeta         : fp32 [T][H]
+ *   chunk_table                : int32 [n_chunks][2] = (first event, length <= 64);
+ *                                chunks never cross a document boundary
+ *   doc_chunk                  : int32 [n_docs + 1], chunks of document d are
+ *                                doc_chunk[d] .. doc_chunk[d+1]-1, in time order
+ *   states                     : fp32 [n_docs][H][K=128][V=128] (key-first), as the
+ *                                reference's prefill returns them (ops/gated_delta_net.py:297-311)
+ */
+#ifndef CQGDN_H_
+#define CQGDN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CQGDN_OK 0
+#define CQGDN_EINVAL 1       /* contract violation (shape, null pointer, size) */
+#define CQGDN_EUNSUPPORTED 2 /* valid request this build does not implement   */
+#define CQGDN_EHIP 3         /* a HIP runtime call failed                      */
+
+#define CQGDN_HEAD_DIM 128
+#define CQGDN_CHUNK 64
+
+/* flags of cqgdn_fwd / cqgdn_bwd */
+#define CQGDN_NORMALIZE 1u /* l2-normalize q and k in the kernels (use_qk_l2norm_in_kernel=True) */
+#define CQGDN_TRAINING 2u  /* keep the extra layouts the backward reads (h and v_new rows) */
+
+/* Library version string, e.g. "cqgdn 0.1.0 gfx950". */
+const char* cqgdn_version(void);
+
+/* Message of the last error returned on this thread ("" if none). */
+const char* cqgdn_last_error(void);
+
+/*
+ * Host helper: chunk table of packed documents.  bounds (host int64,
+ * n_bounds entries) are cumulative document boundaries (0, ..., T) as checked by
+ * host_bounds() (ops/gated_delta_net.py:102-114).  Replaces chunk_indices()
+ * (ops/gated_delta_net.py:90-99) for chunk size 64.  With table == NULL only the
+ * counts are returned.  Returns the number of chunks, or -1 on invalid bounds.
+ */
+int64_t cqgdn_chunk_table(const int64_t* bounds, int n_bounds, int32_t* table, int32_t* doc_chunk);
+
+/*
+ * Forward workspace: size in bytes, and the byte offset of each of its
+ * CQGDN_FWD_BUFFERS internal buffers (order documented in gdn_layout.hpp) so
+ * that tests can inspect intermediates.  The same workspace must be passed,
+ * unmodified, to cqgdn_bwd.
+ */
+#define CQGDN_FWD_BUFFERS 14
+#define CQGDN_BWD_BUFFERS 9
+size_t cqgdn_fwd_workspace_size(int64_t T, int H, int64_t n_chunks);
+int cqgdn_fwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets, int count);
+size_t cqgdn_bwd_workspace_size(int64_t T, int H, int64_t n_chunks);
+int cqgdn_bwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets, int count);
+
+/*
+ * Chunked GDN forward (fused l2norm, chunk cumsum, beta*K K^T, UT inverse, w/u,
+ * inter-chunk state scan, output).  Replaces `chunk_gated_delta_rule_fwd`
+ * (ops/gated_delta_net.py:144-156 training, :297-309 prefill) and the cached
+ * chain l2_fwd / chunk_local_cumsum / chunk_scaled_dot_kkt / solve_tril /
+ * recompute_w_u_fwd / chunk_gated_delta_rule_fwd_h / chunk_fwd_o
+ * (ops/gated_delta_net.py:136-137,158-183).
+ *   scale          : output scale (the reference uses D^-0.5, ops/gated_delta_net.py:248)
+ *   initial_state  : NULL or [n_docs][H][K][V] fp32 starting state per document
+ *   final_state    : NULL or [n_docs][H][K][V] fp32, written with each document's last state
+ *   o              : [T][H][D] bf16 output (time-first)
+ *   workspace      : >= cqgdn_fwd_workspace_size() bytes, 256-byte aligned
+ */
+int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T, int H,
+              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
+              unsigned flags, const float* initial_state, float* final_state, void* o, void* workspace,
+              size_t workspace_bytes, void* stream);
+
+/*
+ * Chunked GDN backward from the forward workspace (which must come from a
+ * cqgdn_fwd call with CQGDN_TRAINING on the same inputs).  Replaces the
+ * backward op chain of _Delta.backward (ops/gated_delta_net.py:188-214:
+ * chunk_bwd_dv_local, chunk_gated_delta_rule_bwd_dhu, chunk_bwd_dqkwg,
+ * prepare_wy_repr_bwd_da, prepare_wy_repr_bwd_full, reverse_cumsum, l2_bwd).
+ * Gradients are written in the input layouts: dq, dk, dv bf16 [T][H][D];
+ * dg, dbeta fp32 [T][H].
+ */
+int cqgdn_bwd(const void* v, const float* g, const float* beta, const void* dout, int64_t T, int H,
+              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
+              unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes, void* bwd_workspace,
+              size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta, void* stream);
+
+/*
+ * Recurrent GDN step(s): for each of N independent sequences, E events applied
+ * in order to a value-first fp32 state [N][H][V][K], updated in place, as the
+ * decode path does with the FLA kernel fused_recurrent_gated_delta_rule_fwd_kernel
+ * (ops/gated_delta_net.py:314-352; math of models/decoding.py:71-77):
+ *   S <- exp(g) S ; S <- S + beta k (v - S k)^T ; o = scale S q
+ * q, k (already l2-normalized), v, out: bf16 [N][E][H][D]; g: fp32 [N][E][H];
+ * beta: [N][E][H], fp32 or bf16 (beta_is_bf16).  The reference call is N = 1.
+ */
+int cqgdn_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta, int beta_is_bf16,
+                    float* state, void* out, int N, int E, int H, float scale, void* stream);
+
+/*
+ * Row-wise l2norm over D = 128 (the `l2_fwd` / `l2_bwd` ops bound at
+ * ops/gated_delta_net.py:52-53 and used at :136-137, :207-209 and
+ * models/decoding.py:63-64): y = x * rsqrt(sum x^2 + 1e-6), rstd optional.
+ * Backward: dx = rstd * (dy - y (y . dy)).  x, y, dy, dx: bf16 [rows][128].
+ */
+int cqgdn_l2norm_fwd(const void* x, void* y, float* rstd, int64_t rows, void* stream);
+int cqgdn_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx, int64_t rows, void* stream);
+
+/*
+ * Chunk-local cumsum of g fp32 [T][H] over the chunk table, forward or reverse
+ * (`chunk_local_cumsum` and reverse_cumsum(), ops/gated_delta_net.py:77-87,158-164).
+ */
+int cqgdn_chunk_local_cumsum(const float* g, float* out, int64_t T, int H, const int32_t* chunk_table,
+                             int64_t n_chunks, int reverse, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CQGDN_H_ */

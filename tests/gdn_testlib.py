@@ -1,0 +1,48 @@
+"""Helpers shared by the GPU parity tests: error metrics and workspace views."""
+
+from __future__ import annotations
+
+import torch
+
+# Tolerances (written here and used by every parity test):
+#  * bf16 outputs and gradients vs the float64 oracle: relative-L2 <= 2e-2 and
+#    normalized max error max|a-b| / max|b| <= 2e-2
+#  * fp32 final states: relative-L2 <= 1e-3
+#  * read-only events / other documents: bit-identical (atol = rtol = 0)
+TOL_BF16 = 2e-2
+TOL_STATE = 1e-3
+TOL_INTER = 1e-2  # bf16-rounded intermediates (T, W, U, h, v_new, ...)
+
+
+def rel_l2(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def max_rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+def assert_close_bf16(name, actual, expected, tol=TOL_BF16):
+    assert torch.isfinite(actual.float()).all(), f"{name}: non-finite values"
+    r, m = rel_l2(actual, expected), max_rel(actual, expected)
+    print(f"  {name}: rel_l2={r:.3e} max_rel={m:.3e}", flush=True)
+    assert r <= tol and m <= tol, f"{name}: rel_l2={r:.3e} max_rel={m:.3e} > {tol}"
+
+
+def view(ws, offset, dtype, shape):
+    n = 1
+    for s in shape:
+        n *= s
+    nbytes = n * torch.tensor([], dtype=dtype).element_size()
+    return ws[offset:offset + nbytes].view(dtype).view(*shape)
+
+
+def assemble(chunks, spans, T):
+    """Per-chunk oracle tensors [H, n, ...] -> time-first [T, H, ...]."""
+    first = chunks[0]
+    out = first.new_zeros(T, first.shape[0], *first.shape[2:])
+    for x, (a, b) in zip(chunks, spans):
+        out[a:b] = x.transpose(0, 1)
+    return out

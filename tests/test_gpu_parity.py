@@ -1,0 +1,299 @@
+"""GPU parity of the HIP GDN kernels against the CPU oracle (float64), through the C ABI.
+
+Cases follow the reference's NPU gates: lengths 1/63/64/65/129/257 with packed
+documents (scripts/validation/delta_ascendc_validate.py:21-27), intermediates
+gcum / T / w / u / h / v_new (scripts/validation/delta_ascendc_diagnose.py:23-42),
+read-only bit-exactness (tests/test_qwen35_cq.py:71-89) and document isolation
+(tests/test_document_packing.py:180-200).
+"""
+
+import pytest
+import torch
+
+from gdn_testlib import TOL_BF16, TOL_INTER, TOL_STATE, assemble, assert_close_bf16, rel_l2, view
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def inputs(T, H, seed, readonly=None):
+    from cqgdn import synthetic
+
+    return synthetic.make_inputs(T, H, 128, seed=seed, readonly=readonly)
+
+
+def to_dev(xs):
+    return [x.to(DEV) for x in xs]
+
+
+def run_fwd(gdn, xs, bounds, training=True, want_state=False, normalize=True, initial_state=None):
+    q, k, v, g, b = to_dev(xs)
+    o, state, ws = gdn._forward(q, k, v, g.contiguous(), b.contiguous(), bounds, normalize, 128 ** -0.5,
+                                training=training, want_state=want_state, initial_state=initial_state)
+    torch.cuda.synchronize()
+    return o, state, ws
+
+
+CASES = [
+    (1, (0, 1), 4),
+    (63, (0, 63), 4),
+    (64, (0, 64), 4),
+    (65, (0, 65), 4),
+    (129, (0, 129), 16),
+    (129, (0, 37, 129), 16),
+    (257, (0, 1, 37, 64, 200, 257), 8),
+]
+
+
+@pytest.mark.parametrize("T,bounds,H", CASES)
+def test_forward_intermediates_and_output(gdn, T, bounds, H):
+    print(f"case T={T} bounds={bounds} H={H}", flush=True)
+    xs = inputs(T, H, seed=900 + T)
+    o, _, ws = run_fwd(gdn, xs, bounds)
+    q, k, v, g, b = (x.double() for x in xs)
+    ref, inter = O.chunk_delta(q, k, v, g, b, bounds, return_intermediates=True)
+    from cqgdn import _lib
+
+    spans = inter["spans"]
+    nc = len(spans)
+    off = _lib.fwd_offsets(T, H, nc)
+    gc = view(ws, off["gcum"], torch.float32, (T, H))
+    assert rel_l2(gc, assemble(inter["gcum"], spans, T)) < 1e-6
+    Tm = view(ws, off["T"], torch.bfloat16, (nc, H, 64, 64))
+    W = view(ws, off["W"], torch.bfloat16, (T, H, 128))
+    UT = view(ws, off["UT"], torch.bfloat16, (nc, H, 128, 64))
+    hT = view(ws, off["hT"], torch.bfloat16, (nc, H, 128, 128))
+    hR = view(ws, off["h"], torch.bfloat16, (nc, H, 128, 128))
+    vnT = view(ws, off["vnT"], torch.bfloat16, (nc, H, 128, 64))
+    vn = view(ws, off["vn"], torch.bfloat16, (T, H, 128))
+    for c, (a, e) in enumerate(spans):
+        n = e - a
+        assert rel_l2(Tm[c, :, :n, :n], inter["T"][c]) < TOL_INTER
+        assert rel_l2(UT[c, :, :, :n].transpose(-1, -2), inter["U"][c]) < TOL_INTER
+        # h is exactly zero on the first chunk of every document
+        assert rel_l2(hT[c].transpose(-1, -2), inter["h"][c]) < TOL_INTER
+        assert rel_l2(hR[c], inter["h"][c]) < TOL_INTER
+        assert rel_l2(vnT[c, :, :, :n].transpose(-1, -2), inter["vn"][c]) < TOL_INTER
+        # rows past the tail are zero (the scan relies on it)
+        assert float(UT[c, :, :, n:].abs().max() if n < 64 else 0) == 0.0
+    assert rel_l2(W, assemble(inter["W"], spans, T)) < TOL_INTER
+    assert rel_l2(vn, assemble(inter["vn"], spans, T)) < TOL_INTER
+    assert_close_bf16("o", o.cpu(), ref)
+
+
+@pytest.mark.parametrize("T,bounds,H", CASES)
+def test_backward_matches_oracle(gdn, T, bounds, H):
+    print(f"case T={T} bounds={bounds} H={H}", flush=True)
+    xs = inputs(T, H, seed=1900 + T)
+    gen = torch.Generator().manual_seed(7 + T)
+    do = torch.randn(1, T, H, 128, generator=gen).bfloat16()
+    xd = [x.to(DEV).requires_grad_() for x in xs]
+    cu = torch.tensor(bounds, device=DEV)
+    y, _ = gdn.delta(*xd, use_qk_l2norm_in_kernel=True, cu_seqlens=cu, cu_seqlens_cpu=torch.tensor(bounds))
+    y.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    q, k, v, g, b = (x.double() for x in xs)
+    ref = O.chunk_delta(q, k, v, g, b, bounds)
+    grads = O.chunk_delta_backward(q, k, v, g, b, do.double(), bounds)
+    assert_close_bf16("o", y.detach().cpu(), ref)
+    for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta"), xd, grads):
+        assert x.grad.dtype == x.dtype
+        assert_close_bf16(name, x.grad.cpu(), r)
+
+
+def test_backward_intermediates(gdn):
+    T, H, bounds = 200, 4, (0, 70, 200)
+    xs = inputs(T, H, seed=5)
+    gen = torch.Generator().manual_seed(11)
+    do = torch.randn(1, T, H, 128, generator=gen).bfloat16()
+    do_dev = do.to(DEV)
+    from cqgdn import _lib
+
+    q, k, v, g, b = to_dev(xs)
+    o, _, ws = gdn._forward(q, k, v, g, b, bounds, True, 128 ** -0.5, training=True)
+    _, table, doc = gdn.device_metadata(bounds, DEV)
+    nc = table.shape[0]
+    bws = torch.empty(_lib.lib().cqgdn_bwd_workspace_size(T, H, nc), dtype=torch.uint8, device=DEV)
+    dq, dk, dv = (torch.empty_like(v) for _ in range(3))
+    dg, db = torch.empty_like(g), torch.empty_like(b)
+    P = gdn._ptr
+    gdn.call("cqgdn_bwd", P(v), P(g), P(b), P(do_dev), T, H, P(table), nc, P(doc), len(bounds) - 1,
+             128 ** -0.5, 3, P(ws), ws.numel(), P(bws), bws.numel(), P(dq), P(dk), P(dv), P(dg), P(db),
+             gdn._stream(q.device))
+    torch.cuda.synchronize()
+    qd, kd, vd, gd, bd = (x.double() for x in xs)
+    _, binter = O.chunk_delta_backward(qd, kd, vd, gd, bd, do.double(), bounds, return_intermediates=True)
+    off = _lib.bwd_offsets(T, H, nc)
+    dvlT = view(bws, off["dvlT"], torch.bfloat16, (nc, H, 128, 64))
+    XT = view(bws, off["XT"], torch.bfloat16, (nc, H, 128, 128))
+    dh = view(bws, off["dh"], torch.bfloat16, (nc, H, 128, 128))
+    dVnT = view(bws, off["dVnT"], torch.bfloat16, (nc, H, 128, 64))
+    spans = O.chunk_spans(bounds)
+    for c, (a, e) in enumerate(spans):
+        n = e - a
+        assert rel_l2(dvlT[c, :, :, :n].transpose(-1, -2), binter["dv_local"][c]) < TOL_INTER, c
+        assert rel_l2(XT[c].transpose(-1, -2), binter["X"][c]) < TOL_INTER, c
+        if binter["dh"][c].abs().max() > 0:
+            assert rel_l2(dh[c], binter["dh"][c]) < TOL_INTER, c
+        assert rel_l2(dVnT[c, :, :, :n].transpose(-1, -2), binter["dVn"][c]) < 2 * TOL_INTER, c
+
+
+def test_cq_config1_shape_fwd_bwd(gdn):
+    """Config 1 event stream (2048 content + 256 read-only after it), H=16, fwd+bwd vs the oracle."""
+    from cqgdn import synthetic
+
+    T, mask, bounds = synthetic.config_events(1, seed=1)
+    xs = inputs(T, 16, seed=1, readonly=mask)
+    gen = torch.Generator().manual_seed(101)
+    do = torch.randn(1, T, 16, 128, generator=gen).bfloat16()
+    xd = [x.to(DEV).requires_grad_() for x in xs]
+    y, _ = gdn.delta(*xd, use_qk_l2norm_in_kernel=True)
+    y.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    q, k, v, g, b = (x.double() for x in xs)
+    assert_close_bf16("o", y.detach().cpu(), O.chunk_delta(q, k, v, g, b))
+    grads = O.chunk_delta_backward(q, k, v, g, b, do.double())
+    for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta"), xd, grads):
+        assert_close_bf16(name, x.grad.cpu(), r)
+
+
+def test_readonly_events_leave_state_and_outputs_bit_identical(gdn):
+    """Perturbing read-only queries changes nothing but their own outputs (tests/test_qwen35_cq.py:71-89)."""
+    from cqgdn import synthetic
+
+    T = 640
+    mask = synthetic.cq_readonly_mask(512, 2, 64, seed=4)
+    xs = inputs(T, 8, seed=3, readonly=mask)
+    o1, s1, _ = run_fwd(gdn, xs, (0, T), training=False, want_state=True)
+    q2 = xs[0].clone()
+    q2[:, mask] = (q2[:, mask].float() * 10 + 3).bfloat16()
+    o2, s2, _ = run_fwd(gdn, [q2, *xs[1:]], (0, T), training=False, want_state=True)
+    assert torch.equal(o1[:, ~mask.to(DEV)], o2[:, ~mask.to(DEV)])
+    assert torch.equal(s1, s2)
+    # removing the read-only events entirely gives the same final state
+    keep = ~mask
+    o3, s3, _ = run_fwd(gdn, [x[:, keep] for x in xs], (0, int(keep.sum())), training=False, want_state=True)
+    assert rel_l2(s3, s1) < TOL_STATE
+
+
+def test_documents_are_isolated(gdn):
+    """Changing document A leaves document B bit-identical (tests/test_document_packing.py:180-200)."""
+    bounds = (0, 150, 301, 400)
+    xs = inputs(400, 8, seed=21)
+    o1, s1, _ = run_fwd(gdn, xs, bounds, want_state=True)
+    changed = [x.clone() for x in xs]
+    changed[0][:, :150] += 1
+    changed[2][:, :150] *= 3
+    changed[3][:, :150] -= 0.5
+    o2, s2, _ = run_fwd(gdn, changed, bounds, want_state=True)
+    assert torch.equal(o1[:, 150:], o2[:, 150:])
+    assert torch.equal(s1[1:], s2[1:])
+    assert not torch.equal(o1[:, :150], o2[:, :150])
+
+
+def test_prefill_final_state_and_initial_state(gdn):
+    T, H, bounds = 300, 16, (0, 100, 300)
+    xs = inputs(T, H, seed=31)
+    q, k, v, g, b = to_dev(xs)
+    o, state = gdn.prefill(q, k, v, g, b, bounds)
+    torch.cuda.synchronize()
+    qd, kd, vd, gd, bd = (x.double() for x in xs)
+    ref, ref_state = O.chunk_delta(qd, kd, vd, gd, bd, bounds, output_final_state=True)
+    assert_close_bf16("o", o.cpu(), ref)
+    r = rel_l2(state, ref_state)
+    print(f"  final state rel_l2={r:.3e}", flush=True)
+    assert r <= TOL_STATE
+    # continuing from a state: prefill(a ++ b) == prefill(b, initial_state=prefill(a))
+    s0 = torch.randn(1, H, 128, 128, generator=torch.Generator().manual_seed(3)) * 0.02
+    o4, st4 = gdn.prefill(q[:, 100:], k[:, 100:], v[:, 100:], g[:, 100:], b[:, 100:], (0, 200),
+                          initial_state=s0.to(DEV))
+    ref4, rst4 = O.chunk_delta(qd[:, 100:], kd[:, 100:], vd[:, 100:], gd[:, 100:], bd[:, 100:], (0, 200),
+                               initial_state=s0.double(), output_final_state=True)
+    assert_close_bf16("o(initial_state)", o4.cpu(), ref4)
+    assert rel_l2(st4, rst4) <= TOL_STATE
+
+
+@pytest.mark.parametrize("E,beta_bf16", [(1, False), (2, False), (2, True), (5, False)])
+def test_recurrent_decode_step(gdn, E, beta_bf16):
+    N, H = 6, 16
+    gen = torch.Generator().manual_seed(40 + E)
+    q = O.l2norm(torch.randn(N, E, H, 128, generator=gen)).bfloat16()
+    k = O.l2norm(torch.randn(N, E, H, 128, generator=gen)).bfloat16()
+    v = torch.randn(N, E, H, 128, generator=gen).bfloat16()
+    g = -torch.nn.functional.softplus(torch.randn(N, E, H, generator=gen))
+    b = torch.randn(N, E, H, generator=gen).sigmoid()
+    if E == 2:  # the CQ decode buffer: event 1 is a read-only query
+        k[:, 1] = 0
+        v[:, 1] = 0
+        g[:, 1] = 0
+        b[:, 1] = 0
+    if beta_bf16:
+        b = b.bfloat16()
+    state = torch.randn(N, H, 128, 128, generator=gen) * 0.02
+    ref_state = state.double().clone()
+    ref = O.decode_step(q.double(), k.double(), v.double(), g.double(), b.double(), ref_state)
+    st = state.to(DEV)
+    ptr = st.data_ptr()
+    out = torch.empty(N, E, H, 128, dtype=torch.bfloat16, device=DEV)
+    gdn.recurrent(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), b.to(DEV), st, out)
+    torch.cuda.synchronize()
+    assert st.data_ptr() == ptr
+    assert_close_bf16("o", out.cpu(), ref)
+    r = rel_l2(st, ref_state)
+    print(f"  state rel_l2={r:.3e}", flush=True)
+    assert r <= TOL_STATE
+
+
+def test_recurrent_reference_call_shape(gdn):
+    """The reference's call: q [t,H,128], state [1,H,V,K] (ops/gated_delta_net.py:321-351)."""
+    H = 8
+    gen = torch.Generator().manual_seed(9)
+    q = O.l2norm(torch.randn(2, H, 128, generator=gen)).bfloat16()
+    k = O.l2norm(torch.randn(2, H, 128, generator=gen)).bfloat16()
+    v = torch.randn(2, H, 128, generator=gen).bfloat16()
+    g = -torch.rand(2, H, generator=gen)
+    b = torch.rand(2, H, generator=gen).bfloat16()
+    state = torch.randn(1, H, 128, 128, generator=gen) * 0.1
+    ref_state = state.double().clone()
+    ref = O.decode_step(q[None].double(), k[None].double(), v[None].double(), g[None].double(), b[None].double(),
+                        ref_state)[0]
+    st, out = state.to(DEV), torch.empty(2, H, 128, dtype=torch.bfloat16, device=DEV)
+    gdn.recurrent(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), b.to(DEV), st, out)
+    torch.cuda.synchronize()
+    assert_close_bf16("o", out.cpu(), ref)
+    assert rel_l2(st, ref_state) <= TOL_STATE
+
+
+def test_l2norm_and_cumsum_kernels(gdn):
+    gen = torch.Generator().manual_seed(2)
+    x = torch.randn(37, 3, 128, generator=gen).bfloat16()
+    y, rstd = gdn.l2_fwd(x.to(DEV))
+    assert_close_bf16("l2_fwd", y.cpu(), O.l2norm(x.double()))
+    dy = torch.randn(37, 3, 128, generator=gen).bfloat16()
+    xx = x.double().requires_grad_()
+    O.l2norm(xx).backward(dy.double())
+    assert_close_bf16("l2_bwd", gdn.l2_bwd(y, rstd, dy.to(DEV)).cpu(), xx.grad)
+    g = torch.randn(1, 300, 4, generator=gen)
+    bounds = (0, 10, 200, 300)
+    out = gdn.reverse_cumsum(g.to(DEV), bounds)
+    ref = O.chunk_local_cumsum(g.double(), bounds, reverse=True)
+    assert rel_l2(out, ref) < 1e-6
+
+
+def test_forward_backward_bitwise_deterministic(gdn):
+    from cqgdn import synthetic
+
+    T, mask, bounds = synthetic.config_events(1, seed=2)
+    xs = inputs(T, 16, seed=2, readonly=mask)
+    do = torch.randn(1, T, 16, 128, generator=torch.Generator().manual_seed(3)).bfloat16().to(DEV)
+    outs = []
+    for _ in range(2):
+        xd = [x.to(DEV).requires_grad_() for x in xs]
+        y, _ = gdn.delta(*xd, use_qk_l2norm_in_kernel=True)
+        y.backward(do)
+        outs.append([y.detach()] + [x.grad for x in xd])
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
