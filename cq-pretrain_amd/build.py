@@ -32,6 +32,9 @@ FLAGS = [
     "-fPIC",
     # never let the compiler emit packed-fp32 VALU ops (v_pk_*_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep MFMA accumulators in VGPRs: the scans update their state with VALU
+    # ops every step, which would otherwise cost an AGPR round trip per value
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]

@@ -5,7 +5,7 @@
 // kdec_i = exp(G_last - G_i), P = (Qn Kn^T) * Gam:
 //
 //   bwd_local  (grid NC x H)  dv_local = scale P^T dO ;  X = scale (gam Qn)^T dO
-//   bwd_state  (serial, reverse)  dVn = dv_local + kdec * (Kn dS_{c+1})
+//   bwd_scan   (serial, reverse)  dVn = dv_local + kdec * (Kn dS_{c+1})
 //                                 dS_c = exp(G_last) dS_{c+1} + X - W^T dVn
 //   bwd_dqk    (grid NC x H)  dQn = scale gam (dO S_c^T) + (scale dP Gam) Kn   (dP = dO Vn^T)
 //                             dKn(part) = (scale dP Gam)^T Qn + kdec (Vn dS_{c+1}^T)
@@ -134,75 +134,210 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
 // ---------------------------------------------------------------------------
 // bwd_state: one wave per (head, 16-wide value slice, document), chunks in reverse
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void bwd_state_kernel(
-    const bf16* __restrict__ kn, const float* __restrict__ gc, const bf16* __restrict__ dvlT,
+// Reverse scan, organised like fwd_scan_kernel: one consumer wave per (head,
+// 16-wide value slice), two loader waves copying each chunk's operands
+// global -> LDS asynchronously into a 4-stage ring, BS_DEPTH chunks ahead; the
+// consumer's output tiles (dS^T, dVn^T) go into the stage region it has read
+// (Kn) and are stored by the loader that next refills that stage.  Tiles use
+// the same XOR swizzles as the forward scan:
+//   Kn  [64 rows t][16 cols]   col ^ (t & 15)      W^T [128 rows k][8 cols]  col ^ ((k >> 1) & 7)
+//   X^T [16 rows v][16 cols]   col ^ (v & 15)      dv_local^T [16 rows v][8 cols]  col ^ ((v >> 1) & 7)
+constexpr int BS_THREADS = 64 * 3;
+constexpr int BS_DEPTH = 3;
+constexpr int BS_STAGES = 4;
+constexpr int BS_SROW = 136;
+constexpr int BS_VROW = 72;
+
+struct __attribute__((aligned(16))) BwdStage {
+  bf16 kn[64 * 128];   // Kn rows t
+  bf16 wt[128 * 64];   // -W^T rows k
+  bf16 dvl[16 * 64];   // dv_local^T rows of the slice
+  bf16 xt[16 * 128];   // X^T rows of the slice
+  float g[64];         // G of every event (events past the tail repeat the last one)
+};
+
+struct __attribute__((aligned(16))) BwdScratch {
+  bf16 s[16 * BS_SROW];  // dS_{c+1}, [v][k]
+  bf16 v[16 * BS_VROW];  // dVn, [v][t]
+};
+static_assert(sizeof(BwdScratch) <= 64 * 128 * sizeof(bf16), "scratch must fit the Kn region");
+__device__ __forceinline__ BwdScratch& bwd_scratch(BwdStage& st) { return *reinterpret_cast<BwdScratch*>(st.kn); }
+
+// Issue the asynchronous copies of chunk c into stage S (no wait on memory here).
+__device__ __forceinline__ void bwd_issue(BwdStage& S, const int32_t* __restrict__ chunks, int c, int H, int h,
+                                          int v0, int lane, const bf16* __restrict__ knP,
+                                          const float* __restrict__ gc, const bf16* __restrict__ dvlT,
+                                          const bf16* __restrict__ XT, const bf16* __restrict__ WT) {
+  const ChunkInfo ci = chunk_info(chunks, c);
+  const size_t cb = (size_t)c * H + h;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {  // rows past the tail re-read row len-1 and are zeroed by bwd_fix_tail
+    const int t = 4 * i + (lane >> 4), col = (lane & 15) ^ (t & 15);
+    const int tt = min(t, ci.len - 1);
+    dma16(knP + ((size_t)(ci.start + tt) * H + h) * D + 8 * col, S.kn + 512 * i);
+  }
+  const bf16* wt = WT + cb * (D * CH);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int k = 8 * i + (lane >> 3), col = (lane & 7) ^ ((k >> 1) & 7);
+    dma16(wt + k * CH + 8 * col, S.wt + 512 * i);
+  }
+  const bf16* dvl = dvlT + cb * (D * CH) + v0 * CH;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int v = 8 * i + (lane >> 3), col = (lane & 7) ^ ((v >> 1) & 7);
+    dma16(dvl + v * CH + 8 * col, S.dvl + 512 * i);
+  }
+  const bf16* xt = XT + cb * (D * D) + v0 * D;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int v = 4 * i + (lane >> 4), col = (lane & 15) ^ (v & 15);
+    dma16(xt + v * D + 8 * col, S.xt + 512 * i);
+  }
+  __builtin_amdgcn_global_load_lds(gc + (size_t)(ci.start + min(lane, ci.len - 1)) * H + h, (lds_void_ptr)S.g, 4,
+                                   0, 0);
+}
+
+__device__ __forceinline__ void bwd_fix_tail(BwdStage& S, const int32_t* __restrict__ chunks, int c, int lane) {
+  const int len = chunk_info(chunks, c).len;
+  if (len < CH) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int t = 4 * i + (lane >> 4);
+      if (t >= len) st8(S.kn + t * 128 + 8 * (lane & 15), zero8());
+    }
+  }
+}
+
+// scratch of one step -> dS^T rows [v0..v0+15][k], dVn^T rows [v0..v0+15][t]
+__device__ __forceinline__ void bwd_copy_out(const BwdScratch& sc, int c, int H, int h, int v0, int lane,
+                                             bf16* __restrict__ dhT, bf16* __restrict__ dVnT) {
+  const size_t cb = (size_t)c * H + h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int seg = 64 * i + lane, v = seg >> 4, ks = seg & 15;
+    st8(dhT + cb * (D * D) + (v0 + v) * D + 8 * ks, ld8(sc.s + v * BS_SROW + 8 * ks));
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int seg = 64 * i + lane, v = seg >> 3, ts = seg & 7;
+    st8(dVnT + cb * (D * CH) + (v0 + v) * CH + 8 * ts, ld8(sc.v + v * BS_VROW + 8 * ts));
+  }
+}
+
+__global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
+    const bf16* __restrict__ knP, const float* __restrict__ gc, const bf16* __restrict__ dvlT,
     const bf16* __restrict__ XT, const bf16* __restrict__ WT, const int32_t* __restrict__ chunks,
-    const int32_t* __restrict__ doc_chunk, int H, bf16* __restrict__ dh, bf16* __restrict__ dVnT,
-    bf16* __restrict__ dVn) {
+    const int32_t* __restrict__ doc_chunk, int H, bf16* __restrict__ dhT, bf16* __restrict__ dVnT) {
   const int h = blockIdx.x % H, slice = blockIdx.x / H, d = blockIdx.y;
-  const int lane = threadIdx.x, r = lane & 15, q4 = lane >> 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q4 = lane >> 4;
   const int v0 = 16 * slice;
 
-  f32x4 dS[8];  // dS[m][i] = dState[k = 16m + 4q4 + i][v = v0 + r]
-#pragma unroll
-  for (int m = 0; m < 8; ++m) dS[m] = zero4();
+  __shared__ BwdStage stage[BS_STAGES];
 
-  const int c_begin = doc_chunk[d];
-  for (int c = doc_chunk[d + 1] - 1; c >= c_begin; --c) {
-    const ChunkInfo ci = chunk_info(chunks, c);
-    const size_t cb = (size_t)c * H + h;
-    bf16* dhc = dh + cb * (D * D);
+  const int c_end = doc_chunk[d + 1], n = c_end - doc_chunk[d];
+  // step tau handles chunk c_end - 1 - tau (chunks in reverse)
+  if (wave == 0) {
+    f32x4 dS[8];  // dS[m][i] = dState[k = 16m + 4q4 + i][v = v0 + r]
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
+    for (int m = 0; m < 8; ++m) dS[m] = zero4();
+    int kofs[4], wofs[2], dofs[4], xofs[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dhc[(16 * m + 4 * q4 + i) * D + v0 + r] = (bf16)dS[m][i];
-    bf16x8 sb[4];
+    for (int j = 0; j < 4; ++j) kofs[j] = 2 * (r * 128 + 8 * ((4 * j + q4) ^ r));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) sb[j] = pack_perm(dS[2 * j], dS[2 * j + 1]);
-
-    const float g_lane = gc[(size_t)(ci.start + min(lane, ci.len - 1)) * H + h];
-    const float glast = __shfl(g_lane, ci.len - 1, 64);
-
-    const bf16* dvl = dvlT + cb * (D * CH);
-    f32x4 dv[4];
+    for (int j = 0; j < 2; ++j) wofs[j] = 2 * (r * 64 + 8 * ((4 * j + q4) ^ ((r >> 1) & 7)));
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      f32x4 acc = zero4();
-      const int t = 16 * i4 + r;
-      const bf16* krow = kn + ((size_t)(ci.start + t) * H + h) * D;
+    for (int i4 = 0; i4 < 4; ++i4) dofs[i4] = 2 * (r * 64 + 8 * ((2 * i4 + (q4 >> 1)) ^ ((r >> 1) & 7)) + 4 * (q4 & 1));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc = mfma((t < ci.len) ? ld8p(krow + 32 * j + 4 * q4) : zero8(), sb[j], acc);
-      const f32x4 local = cvtf4(ld4(dvl + (v0 + r) * CH + 16 * i4 + 4 * q4));
+    for (int m = 0; m < 8; ++m) xofs[m] = 2 * (r * 128 + 8 * ((2 * m + (q4 >> 1)) ^ r) + 4 * (q4 & 1));
+    const int sofs = 2 * (r * BS_SROW + 4 * q4), vofs = 2 * (r * BS_VROW + 4 * q4);
+    for (int tau = -BS_DEPTH; tau < n; ++tau) {
+      if (tau >= 0) {
+        char* base = reinterpret_cast<char*>(&stage[tau & (BS_STAGES - 1)]);
+        const char* knb = base + offsetof(BwdStage, kn);
+        const char* wtb = base + offsetof(BwdStage, wt);
+        const char* dvb = base + offsetof(BwdStage, dvl);
+        const char* xtb = base + offsetof(BwdStage, xt);
+        const float* gs = reinterpret_cast<const float*>(base + offsetof(BwdStage, g));
+        bf16x8 fk[4][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float gt = __shfl(g_lane, 16 * i4 + 4 * q4 + i, 64);
-        acc[i] = acc[i] * __expf(glast - gt) + local[i];
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i4 = 0; i4 < 4; ++i4) fk[i4][j] = *reinterpret_cast<const bf16x8*>(knb + kofs[j] + 4096 * i4);
+        f32x4 local[4], gt[4];
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          local[i4] = cvtf4(*reinterpret_cast<const bf16x4*>(dvb + dofs[i4]));
+          gt[i4] = *reinterpret_cast<const f32x4*>(gs + 16 * i4 + 4 * q4);
+        }
+        const float glast = gs[63];
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x4 sh[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) sh[m] = cvt4(dS[m]);
+        f32x4 acc[4];
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) acc[i4] = zero4();
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8 sb = cat(sh[2 * j], sh[2 * j + 1]);
+#pragma unroll
+          for (int i4 = 0; i4 < 4; ++i4) acc[i4] = mfma(fk[i4][j], sb, acc[i4]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x8 fw[8][2];
+        f32x4 xv[8];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int m = 0; m < 8; ++m) fw[m][j] = *reinterpret_cast<const bf16x8*>(wtb + wofs[j] + 2048 * m);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) xv[m] = cvtf4(*reinterpret_cast<const bf16x4*>(xtb + xofs[m]));
+        // the Kn tile has been read: its region now takes this step's outputs
+        char* sb = base + offsetof(BwdStage, kn);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) *reinterpret_cast<bf16x4*>(sb + sofs + 32 * m) = sh[m];
+        __builtin_amdgcn_sched_barrier(0);
+        // dVn = dv_local + kdec * (Kn dS_{c+1})
+        f32x4 dv[4];
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dv[i4][i] = acc[i4][i] * __expf(glast - gt[i4][i]) + local[i4][i];
+        // dS_c = exp(G_last) dS_{c+1} + X + (-W^T) dVn
+        const float gC = __expf(glast);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) dS[m] = dS[m] * gC + xv[m];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const bf16x8 nb = pack_perm(dv[2 * j], dv[2 * j + 1]);
+#pragma unroll
+          for (int m = 0; m < 8; ++m) dS[m] = mfma(fw[m][j], nb, dS[m]);
+        }
+        char* vbp = sb + sizeof(BwdScratch::s);
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) *reinterpret_cast<bf16x4*>(vbp + vofs + 32 * i4) = cvt4(dv[i4]);
       }
-      dv[i4] = acc;
+      lds_barrier();
     }
-    bf16* dvt = dVnT + cb * (D * CH);
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      st4(dvt + (v0 + r) * CH + 16 * i4 + 4 * q4, dv[i4]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = 16 * i4 + 4 * q4 + i;
-        if (t < ci.len) dVn[((size_t)(ci.start + t) * H + h) * D + v0 + r] = (bf16)dv[i4][i];
+  } else {
+    const int j = wave - 1;
+    for (int tau = -BS_DEPTH; tau < n; ++tau) {
+      if (((tau + 1) & 1) == j) {
+        const int xn = tau + 1, xo = tau - 1, xi = tau + BS_DEPTH;
+        if (xn >= 0 && xn < n) {
+          wait_vmem_all();
+          bwd_fix_tail(stage[xn & (BS_STAGES - 1)], chunks, c_end - 1 - xn, lane);
+        }
+        if (xo >= 0) bwd_copy_out(bwd_scratch(stage[xo & (BS_STAGES - 1)]), c_end - 1 - xo, H, h, v0, lane, dhT, dVnT);
+        if (xi < n)
+          bwd_issue(stage[xi & (BS_STAGES - 1)], chunks, c_end - 1 - xi, H, h, v0, lane, knP, gc, dvlT, XT, WT);
       }
+      lds_barrier();
     }
-
-    const float gC = __expf(glast);
-    bf16x8 nb[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) nb[j] = neg8(pack_perm(dv[2 * j], dv[2 * j + 1]));
-    const bf16* xt = XT + cb * (D * D);
-    const bf16* wt = WT + cb * (D * CH);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      dS[m] = dS[m] * gC + cvtf4(ld4(xt + (v0 + r) * D + 16 * m + 4 * q4));
-#pragma unroll
-      for (int j = 0; j < 2; ++j) dS[m] = mfma(ld8p(wt + (16 * m + r) * CH + 32 * j + 4 * q4), nb[j], dS[m]);
-    }
+    if (n > 0 && (n & 1) == j)
+      bwd_copy_out(bwd_scratch(stage[(n - 1) & (BS_STAGES - 1)]), c_end - n, H, h, v0, lane, dhT, dVnT);
   }
 }
 
@@ -780,8 +915,9 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
   const dim3 grid_c(a.n_chunks, a.H);
   hipLaunchKernelGGL(bwd_local_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), a.dout, Ff(F_GC), a.chunks,
                      a.H, a.scale, B(B_DVLT), B(B_XT));
-  hipLaunchKernelGGL(bwd_state_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(64), 0, stream, F(F_KN), Ff(F_GC),
-                     B(B_DVLT), B(B_XT), F(F_WT), a.chunks, a.doc_chunk, a.H, B(B_DH), B(B_DVNT), B(B_DVN));
+  hipLaunchKernelGGL(bwd_scan_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, F(F_KNP),
+                     Ff(F_GC), B(B_DVLT), B(B_XT), F(F_WT), a.chunks, a.doc_chunk, a.H, B(B_DHT), B(B_DVNT));
+  launch_rows(B(B_DHT), B(B_DVNT), a.chunks, a.n_chunks, a.H, B(B_DH), B(B_DVN), stream);
   hipLaunchKernelGGL(bwd_dqk_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_GC), F(F_HR),
                      F(F_VN), a.dout, B(B_DH), B(B_DVN), a.chunks, a.H, a.scale, (int)a.normalize, a.dq, Bf(B_DKP),
                      B(B_DW), B(B_DWT), Bf(B_DGP));

@@ -70,6 +70,15 @@ __device__ __forceinline__ bf16x8 neg8(bf16x8 x) {
   return __builtin_bit_cast(bf16x8, u);
 }
 
+// Storage order that makes a permuted-map fragment one contiguous 16-byte
+// load: within every 32-element block, logical index x = 4q + s' + 16h
+// (q = 0..3, s' = 0..3, h = 0..1) is stored at 8q + 4h + s'.  Tensors that
+// are only ever read as permuted-map operands (W, KgT, W^T, the scan copy of
+// Kn) are written in this order, so their consumers use ld8 at 32j + 8*q4.
+__host__ __device__ __forceinline__ int perm32(int x) {
+  return (x & ~31) | (((x >> 2) & 3) << 3) | (((x >> 4) & 1) << 2) | (x & 3);
+}
+
 // ---- fragment loads -------------------------------------------------------
 // natural map, k-contiguous storage: 8 consecutive elements at p (16-byte aligned)
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
@@ -86,6 +95,25 @@ __device__ __forceinline__ bf16x8 ld8s(const bf16* p, int stride) {
 
 __device__ __forceinline__ void st4(bf16* p, f32x4 x) { *reinterpret_cast<bf16x4*>(p) = cvt4(x); }
 __device__ __forceinline__ void st8(bf16* p, bf16x8 x) { *reinterpret_cast<bf16x8*>(p) = x; }
+
+// ---- workgroup synchronization for loader/consumer kernels ----------------
+// Barrier that orders LDS only: waits for this wave's LDS operations, then
+// s_barrier.  __syncthreads() also waits for every outstanding vector-memory
+// operation (including asynchronous global->LDS copies still in flight for
+// later steps), which would serialize a prefetch pipeline.  The "memory"
+// clobber keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Wait until every vector-memory operation this wave issued has completed.
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// Asynchronous copy global -> LDS, 16 bytes per lane: lane l's 16 bytes land at
+// lds + 16*l (lds must be wave-uniform and 16-byte aligned).
+__device__ __forceinline__ void dma16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)lds, 16, 0, 0);
+}
 
 // ---- wave reductions -------------------------------------------------------
 // sum over the 16 lanes that share q4 (the 16 columns of a C tile)

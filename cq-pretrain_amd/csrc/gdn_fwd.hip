@@ -34,7 +34,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
     const float* __restrict__ g, const float* __restrict__ beta, const int32_t* __restrict__ chunks,
     int H, bf16* __restrict__ qn, bf16* __restrict__ kn, float* __restrict__ rq,
     float* __restrict__ rk, float* __restrict__ gc, bf16* __restrict__ Tm, bf16* __restrict__ W,
-    bf16* __restrict__ WT, bf16* __restrict__ UT, bf16* __restrict__ KgT) {
+    bf16* __restrict__ WT, bf16* __restrict__ UT, bf16* __restrict__ KgT, bf16* __restrict__ knP) {
   const int c = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
@@ -119,13 +119,20 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
         const bf16x8 xb = cvt8(xn);
         const int col = 32 * j + 8 * p;
         st8(Ks + t * LDK + col, xb);
-        if (in) st8(kn + row + col, xb);
+        if (in) {
+          st8(kn + row + col, xb);
+          // perm32 copy: logical 8p..8p+3 -> 16(p&1) + 4(p>>1), 8p+4..8p+7 -> that + 8
+          bf16* kp = knP + row + 32 * j + 16 * (p & 1) + 4 * (p >> 1);
+          *reinterpret_cast<bf16x4*>(kp) = __builtin_shufflevector(xb, xb, 0, 1, 2, 3);
+          *reinterpret_cast<bf16x4*>(kp + 8) = __builtin_shufflevector(xb, xb, 4, 5, 6, 7);
+        }
         const f32x8 xbg = xn * (b_t * gam_t);
         const f32x8 xkd = xn * kdec_t;
+        const int tp = perm32(t);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
           KbT[(col + s) * LDT + t] = (bf16)xbg[s];
-          kgt[(col + s) * CH + t] = (bf16)xkd[s];
+          kgt[(col + s) * CH + tp] = (bf16)xkd[s];
         }
       }
       if (in && p == 0) rk[(size_t)(ci.start + t) * H + h] = rs;
@@ -208,7 +215,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
         aw = mfma(at[kb], ld8(KbT + (16 * n + r) * LDT + 32 * kb + 8 * q4), aw);
         au = mfma(at[kb], ld8(VbT + (16 * n + r) * LDT + 32 * kb + 8 * q4), au);
       }
-      st4(wt + (16 * n + r) * CH + 16 * wave + 4 * q4, aw);
+      st4(wt + (16 * n + r) * CH + perm32(16 * wave + 4 * q4), -aw);
       st4(ut + (16 * n + r) * CH + 16 * wave + 4 * q4, au);
     }
 #pragma unroll
@@ -223,7 +230,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) acc = mfma(ak[kb], ld8(Ts + (16 * n + r) * LDT + 32 * kb + 8 * q4), acc);
         const int t = 16 * n + r;
-        if (t < ci.len) st4(W + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4, acc);
+        if (t < ci.len) st4(W + ((size_t)(ci.start + t) * H + h) * D + perm32(16 * m + 4 * q4), -acc);
       }
     }
   }
@@ -232,93 +239,266 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
 // ---------------------------------------------------------------------------
 // fwd_state: one wave per (head, 16-wide value slice, document)
 // ---------------------------------------------------------------------------
-template <bool TRAIN>
-__global__ __launch_bounds__(64) void fwd_state_kernel(
+// The scan is a chain of dependent chunk steps, so it runs at the speed one
+// step waits.  A workgroup serves one 16-wide value slice of one head with one
+// consumer wave (wave 0) and two loader waves.  Loaders copy each chunk's
+// operands global -> LDS asynchronously (global_load_lds) into a ring of
+// SC_STAGES stages, SC_DEPTH chunks ahead of use; loader (x & 1) issues chunk x
+// and, the step before chunk x is used, waits for that copy alone (it has
+// issued nothing since).  The consumer only reads LDS and writes its output
+// tiles to LDS; the idle loader of each step stores them.  So no wave holds
+// in-flight data in registers and the consumer never waits on memory.
+//
+// LDS tiles are stored with 16-byte columns XOR-swizzled by row (chosen on the
+// source side of each copy), so the consumer's fragment reads, 16 rows at one
+// logical column, hit distinct banks:
+//   W   [64 rows t][16 cols]  col' = col ^ (t & 15)
+//   KgT [128 rows k][8 cols]  col' = col ^ ((k >> 1) & 7)
+//   U^T [16 rows v][8 cols]   col' = col ^ ((v >> 1) & 7)
+constexpr int SC_THREADS = 64 * 3;
+constexpr int SC_DEPTH = 3;
+constexpr int SC_STAGES = 4;
+constexpr int SC_SROW = 136;  // scratch row stride (bf16), S^T [v][k]
+constexpr int SC_VROW = 72;   // scratch row stride (bf16), v_new^T [v][t]
+
+struct __attribute__((aligned(16))) FwdStage {
+  bf16 w[64 * 128];   // -W rows t
+  bf16 kg[128 * 64];  // KgT rows k
+  bf16 ut[16 * 64];   // U^T rows of the slice
+  float glast;        // G of the chunk's last event
+  float pad[3];
+};
+
+// the consumer's output tiles of a step, placed over the stage's W region
+struct __attribute__((aligned(16))) FwdScratch {
+  bf16 s[16 * SC_SROW];  // state entering the chunk, [v][k]
+  bf16 v[16 * SC_VROW];  // v_new, [v][t]
+};
+static_assert(sizeof(FwdScratch) <= 64 * 128 * sizeof(bf16), "scratch must fit the W region");
+__device__ __forceinline__ FwdScratch& fwd_scratch(FwdStage& st) { return *reinterpret_cast<FwdScratch*>(st.w); }
+
+// Issue the asynchronous copies of chunk c into stage S.  Nothing here waits
+// on memory: the chunk table is read with scalar loads and even the gate value
+// travels by copy (a vector load whose result were used here would make this
+// wave wait for every copy issued before it).
+__device__ __forceinline__ void fwd_issue(FwdStage& S, const int32_t* __restrict__ chunks, int c, int H, int h,
+                                          int v0, int lane, const bf16* __restrict__ W, const bf16* __restrict__ UT,
+                                          const bf16* __restrict__ KgT, const float* __restrict__ gc) {
+  const ChunkInfo ci = chunk_info(chunks, c);
+  const size_t cb = (size_t)c * H + h;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {  // rows past the tail re-read row len-1 and are zeroed by fwd_fix_tail
+    const int t = 4 * i + (lane >> 4), col = (lane & 15) ^ (t & 15);
+    const int tt = min(t, ci.len - 1);
+    dma16(W + ((size_t)(ci.start + tt) * H + h) * D + 8 * col, S.w + 512 * i);
+  }
+  const bf16* kg = KgT + cb * (D * CH);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int k = 8 * i + (lane >> 3), col = (lane & 7) ^ ((k >> 1) & 7);
+    dma16(kg + k * CH + 8 * col, S.kg + 512 * i);
+  }
+  const bf16* ut = UT + cb * (D * CH) + v0 * CH;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int v = 8 * i + (lane >> 3), col = (lane & 7) ^ ((v >> 1) & 7);
+    dma16(ut + v * CH + 8 * col, S.ut + 512 * i);
+  }
+  if (lane == 0)
+    __builtin_amdgcn_global_load_lds(gc + (size_t)(ci.start + ci.len - 1) * H + h, (lds_void_ptr)&S.glast, 4, 0, 0);
+}
+
+// After the copies of chunk c have landed: zero the W rows past its length.
+__device__ __forceinline__ void fwd_fix_tail(FwdStage& S, const int32_t* __restrict__ chunks, int c, int lane) {
+  const int len = chunk_info(chunks, c).len;
+  if (len < CH) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int t = 4 * i + (lane >> 4);
+      if (t >= len) st8(S.w + t * 128 + 8 * (lane & 15), zero8());
+    }
+  }
+}
+
+// scratch of one step -> hT [v0..v0+15][k], vnT [v0..v0+15][t]
+__device__ __forceinline__ void fwd_copy_out(const FwdScratch& sc, int c, int H, int h, int v0, int lane,
+                                             bf16* __restrict__ hT, bf16* __restrict__ vnT) {
+  const size_t cb = (size_t)c * H + h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int seg = 64 * i + lane, v = seg >> 4, ks = seg & 15;
+    st8(hT + cb * (D * D) + (v0 + v) * D + 8 * ks, ld8(sc.s + v * SC_SROW + 8 * ks));
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int seg = 64 * i + lane, v = seg >> 3, ts = seg & 7;
+    st8(vnT + cb * (D * CH) + (v0 + v) * CH + 8 * ts, ld8(sc.v + v * SC_VROW + 8 * ts));
+  }
+}
+
+__global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
     const bf16* __restrict__ W, const bf16* __restrict__ UT, const bf16* __restrict__ KgT,
     const float* __restrict__ gc, const int32_t* __restrict__ chunks, const int32_t* __restrict__ doc_chunk,
     int H, const float* __restrict__ init_state, float* __restrict__ final_state, bf16* __restrict__ hT,
-    bf16* __restrict__ hR, bf16* __restrict__ vnT, bf16* __restrict__ vnR) {
+    bf16* __restrict__ vnT) {
+  // blockIdx.x = slice * H + h: the slices of one head land on one XCD when H % 8 == 0
   const int h = blockIdx.x % H, slice = blockIdx.x / H, d = blockIdx.y;
-  const int lane = threadIdx.x, r = lane & 15, q4 = lane >> 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q4 = lane >> 4;
   const int v0 = 16 * slice;
 
-  f32x4 S[8];  // S[m][i] = state[k = 16m + 4q4 + i][v = v0 + r]
-  if (init_state) {
-    const float* s0 = init_state + ((size_t)d * H + h) * D * D;
-#pragma unroll
-    for (int m = 0; m < 8; ++m)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) S[m][i] = s0[(16 * m + 4 * q4 + i) * D + v0 + r];
-  } else {
+  __shared__ FwdStage stage[SC_STAGES];
+
+  const int c_begin = doc_chunk[d], n = doc_chunk[d + 1] - c_begin;
+  if (wave == 0) {
+    f32x4 S[8];  // S[m][i] = state[k = 16m + 4q4 + i][v = v0 + r]
 #pragma unroll
     for (int m = 0; m < 8; ++m) S[m] = zero4();
-  }
-
-  const int c_end = doc_chunk[d + 1];
-  for (int c = doc_chunk[d]; c < c_end; ++c) {
-    const ChunkInfo ci = chunk_info(chunks, c);
-    const size_t cb = (size_t)c * H + h;
-    // state entering the chunk
-    bf16* ht = hT + cb * (D * D);
-#pragma unroll
-    for (int m = 0; m < 8; ++m) st4(ht + (v0 + r) * D + 16 * m + 4 * q4, S[m]);
-    if (TRAIN) {
-      bf16* hr = hR + cb * (D * D);
+    if (init_state) {
+      const float* s0 = init_state + ((size_t)d * H + h) * D * D;
 #pragma unroll
       for (int m = 0; m < 8; ++m)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) hr[(16 * m + 4 * q4 + i) * D + v0 + r] = (bf16)S[m][i];
+        for (int i = 0; i < 4; ++i) S[m][i] = s0[(16 * m + 4 * q4 + i) * D + v0 + r];
     }
-    bf16x8 hb[4];
+    // per-lane parts of the swizzled LDS addresses (bytes); the row parts are
+    // compile-time offsets of each read
+    int wofs[4], kofs[2], uofs[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) hb[j] = neg8(pack_perm(S[2 * j], S[2 * j + 1]));
-
-    // v_new = U - W S   (rows t, 16 value columns)
-    const bf16* ut = UT + cb * (D * CH);
-    f32x4 vn[4];
+    for (int j = 0; j < 4; ++j) wofs[j] = 2 * (r * 128 + 8 * ((4 * j + q4) ^ r));
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      vn[i4] = cvtf4(ld4(ut + (v0 + r) * CH + 16 * i4 + 4 * q4));
-      const int t = 16 * i4 + r;
-      const bf16* wrow = W + ((size_t)(ci.start + t) * H + h) * D;
+    for (int j = 0; j < 2; ++j) kofs[j] = 2 * (r * 64 + 8 * ((4 * j + q4) ^ ((r >> 1) & 7)));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bf16x8 a = (t < ci.len) ? ld8p(wrow + 32 * j + 4 * q4) : zero8();
-        vn[i4] = mfma(a, hb[j], vn[i4]);
-      }
-    }
-    bf16* vt = vnT + cb * (D * CH);
+    for (int i4 = 0; i4 < 4; ++i4) uofs[i4] = 2 * (r * 64 + 8 * ((2 * i4 + (q4 >> 1)) ^ ((r >> 1) & 7)) + 4 * (q4 & 1));
+    const int sofs = 2 * (r * SC_SROW + 4 * q4), vofs = 2 * (r * SC_VROW + 4 * q4);
+    for (int tau = -SC_DEPTH; tau < n; ++tau) {
+      if (tau >= 0) {
+        char* base = reinterpret_cast<char*>(&stage[tau & (SC_STAGES - 1)]);
+        const char* wb = base + offsetof(FwdStage, w);
+        const char* kb = base + offsetof(FwdStage, kg);
+        const char* ub = base + offsetof(FwdStage, ut);
+        // all operand reads are issued ahead of the MFMAs that use them; the
+        // scheduling barriers keep the compiler from interleaving them one by one
+        bf16x8 fw[4][4];
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) st4(vt + (v0 + r) * CH + 16 * i4 + 4 * q4, vn[i4]);
-    if (TRAIN) {
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4)
+          for (int i4 = 0; i4 < 4; ++i4) fw[i4][j] = *reinterpret_cast<const bf16x8*>(wb + wofs[j] + 4096 * i4);
+        f32x4 vn[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = 16 * i4 + 4 * q4 + i;
-          if (t < ci.len) vnR[((size_t)(ci.start + t) * H + h) * D + v0 + r] = (bf16)vn[i4][i];
+        for (int i4 = 0; i4 < 4; ++i4) vn[i4] = cvtf4(*reinterpret_cast<const bf16x4*>(ub + uofs[i4]));
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x4 sh[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) sh[m] = cvt4(S[m]);
+        // v_new = U + (-W) S
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8 hb = cat(sh[2 * j], sh[2 * j + 1]);
+#pragma unroll
+          for (int i4 = 0; i4 < 4; ++i4) vn[i4] = mfma(fw[i4][j], hb, vn[i4]);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x8 fk[8][2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int m = 0; m < 8; ++m) fk[m][j] = *reinterpret_cast<const bf16x8*>(kb + kofs[j] + 2048 * m);
+        // the W tile has been read (a wave's LDS operations complete in order):
+        // its region now takes this step's outputs
+        char* sb = base + offsetof(FwdStage, w);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) *reinterpret_cast<bf16x4*>(sb + sofs + 32 * m) = sh[m];
+        const float gC = __expf(reinterpret_cast<const FwdStage*>(base)->glast);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) S[m] *= gC;
+        // S <- exp(G_last) S + (K exp(G_last - G))^T v_new
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const bf16x8 vb = pack_perm(vn[2 * j], vn[2 * j + 1]);
+#pragma unroll
+          for (int m = 0; m < 8; ++m) S[m] = mfma(fk[m][j], vb, S[m]);
+        }
+        char* vbp = sb + sizeof(FwdScratch::s);
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) *reinterpret_cast<bf16x4*>(vbp + vofs + 32 * i4) = cvt4(vn[i4]);
+      }
+      lds_barrier();
     }
-
-    // S <- exp(G_last) S + (K exp(G_last - G))^T v_new
-    const float gC = __expf(gc[(size_t)(ci.start + ci.len - 1) * H + h]);
-    bf16x8 vb[2];
+    if (final_state) {
+      float* sf = final_state + ((size_t)d * H + h) * D * D;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) vb[j] = pack_perm(vn[2 * j], vn[2 * j + 1]);
-    const bf16* kg = KgT + cb * (D * CH);
+      for (int m = 0; m < 8; ++m)
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
-      S[m] *= gC;
-#pragma unroll
-      for (int j = 0; j < 2; ++j) S[m] = mfma(ld8p(kg + (16 * m + r) * CH + 32 * j + 4 * q4), vb[j], S[m]);
+        for (int i = 0; i < 4; ++i) sf[(16 * m + 4 * q4 + i) * D + v0 + r] = S[m][i];
     }
+  } else {
+    // Step tau: loader (tau+1)&1 waits for chunk tau+1 (the only copy it has in
+    // flight) and fixes its tail, stores the outputs of step tau-1 from stage
+    // (tau-1)%4, then refills that same stage with chunk tau+3.  The other
+    // loader idles.
+    const int j = wave - 1;
+    for (int tau = -SC_DEPTH; tau < n; ++tau) {
+      if (((tau + 1) & 1) == j) {
+        const int xn = tau + 1, xo = tau - 1, xi = tau + SC_DEPTH;
+        if (xn >= 0 && xn < n) {
+          wait_vmem_all();
+          fwd_fix_tail(stage[xn & (SC_STAGES - 1)], chunks, c_begin + xn, lane);
+        }
+        if (xo >= 0) fwd_copy_out(fwd_scratch(stage[xo & (SC_STAGES - 1)]), c_begin + xo, H, h, v0, lane, hT, vnT);
+        if (xi < n) fwd_issue(stage[xi & (SC_STAGES - 1)], chunks, c_begin + xi, H, h, v0, lane, W, UT, KgT, gc);
+      }
+      lds_barrier();
+    }
+    if (n > 0 && (n & 1) == j)
+      fwd_copy_out(fwd_scratch(stage[(n - 1) & (SC_STAGES - 1)]), c_begin + n - 1, H, h, v0, lane, hT, vnT);
   }
-  if (final_state) {
-    float* sf = final_state + ((size_t)d * H + h) * D * D;
+}
+
+// ---------------------------------------------------------------------------
+// Transposes for the backward: rows [k][v] of a chunk state from its [v][k]
+// form, and time-first rows [t][v] from a chunk's [v][t] tile (h and v_new in
+// training forwards, dS and dVn in backwards).  Parallel over (chunk, head).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fwd_rows_kernel(const bf16* __restrict__ hT, const bf16* __restrict__ vnT,
+                                                       const int32_t* __restrict__ chunks, int H,
+                                                       bf16* __restrict__ hR, bf16* __restrict__ vnR) {
+  const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
+  const ChunkInfo ci = chunk_info(chunks, c);
+  const size_t cb = (size_t)c * H + h;
+  __shared__ __attribute__((aligned(16))) bf16 tile[128 * 136];
+  // h: 128 x 128
+  const bf16* src = hT + cb * (D * D);
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
+  for (int i = 0; i < 8; ++i) {
+    const int seg = 256 * i + tid, v = seg >> 4, ks = seg & 15;
+    const bf16x8 x = ld8(src + v * D + 8 * ks);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sf[(16 * m + 4 * q4 + i) * D + v0 + r] = S[m][i];
+    for (int e = 0; e < 8; ++e) tile[(8 * ks + e) * 136 + v] = x[e];
+  }
+  __syncthreads();
+  bf16* dst = hR + cb * (D * D);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int seg = 256 * i + tid, k = seg >> 4, vs = seg & 15;
+    st8(dst + k * D + 8 * vs, ld8(tile + k * 136 + 8 * vs));
+  }
+  __syncthreads();
+  // v_new: 128 (v) x 64 (t)
+  const bf16* vsrc = vnT + cb * (D * CH);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int seg = 256 * i + tid, v = seg >> 3, ts = seg & 7;
+    const bf16x8 x = ld8(vsrc + v * CH + 8 * ts);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) tile[(8 * ts + e) * 136 + v] = x[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int seg = 256 * i + tid, t = seg >> 4, vs = seg & 15;
+    if (t < ci.len) st8(vnR + ((size_t)(ci.start + t) * H + h) * D + 8 * vs, ld8(tile + t * 136 + 8 * vs));
   }
 }
 
@@ -426,6 +606,11 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
   }
 }
 
+void launch_rows(const bf16* sT, const bf16* vT, const int32_t* chunks, int n_chunks, int H, bf16* srow, bf16* vrow,
+                 hipStream_t stream) {
+  hipLaunchKernelGGL(fwd_rows_kernel, dim3(n_chunks, H), dim3(256), 0, stream, sT, vT, chunks, H, srow, vrow);
+}
+
 // ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
@@ -438,19 +623,16 @@ void launch_fwd(const FwdArgs& a, hipStream_t stream) {
   float* gcum = reinterpret_cast<float*>(ws[F_GC]);
   if (a.normalize)
     hipLaunchKernelGGL(fwd_prep_kernel<true>, grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta, a.chunks,
-                       a.H, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT], ws[F_UT], ws[F_KGT]);
+                       a.H, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT], ws[F_UT], ws[F_KGT],
+                       ws[F_KNP]);
   else
     hipLaunchKernelGGL(fwd_prep_kernel<false>, grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta, a.chunks,
-                       a.H, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT], ws[F_UT], ws[F_KGT]);
+                       a.H, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT], ws[F_UT], ws[F_KGT],
+                       ws[F_KNP]);
   const dim3 grid_s(a.H * (D / 16), a.n_docs);
-  if (a.training)
-    hipLaunchKernelGGL(fwd_state_kernel<true>, grid_s, dim3(64), 0, stream, ws[F_W], ws[F_UT], ws[F_KGT], gcum,
-                       a.chunks, a.doc_chunk, a.H, a.initial_state, a.final_state, ws[F_HT], ws[F_HR], ws[F_VNT],
-                       ws[F_VN]);
-  else
-    hipLaunchKernelGGL(fwd_state_kernel<false>, grid_s, dim3(64), 0, stream, ws[F_W], ws[F_UT], ws[F_KGT], gcum,
-                       a.chunks, a.doc_chunk, a.H, a.initial_state, a.final_state, ws[F_HT], ws[F_HR], ws[F_VNT],
-                       ws[F_VN]);
+  hipLaunchKernelGGL(fwd_scan_kernel, grid_s, dim3(SC_THREADS), 0, stream, ws[F_W], ws[F_UT], ws[F_KGT], gcum, a.chunks,
+                     a.doc_chunk, a.H, a.initial_state, a.final_state, ws[F_HT], ws[F_VNT]);
+  if (a.training) launch_rows(ws[F_HT], ws[F_VNT], a.chunks, a.n_chunks, a.H, ws[F_HR], ws[F_VN], stream);
   hipLaunchKernelGGL(fwd_out_kernel, grid_c, dim3(256), 0, stream, ws[F_QN], ws[F_KN], gcum, ws[F_HT], ws[F_VNT],
                      a.chunks, a.H, a.scale, a.o);
 }

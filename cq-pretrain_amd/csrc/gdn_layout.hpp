@@ -19,14 +19,15 @@ enum FwdBuf {
   F_RK,      // f32  [T][H]      rsqrt(sum k^2 + eps)
   F_GC,      // f32  [T][H]      chunk-local cumsum of g
   F_TM,      // bf16 [NC][H][64][64]  T = (I + A)^-1, row-major (t, s)
-  F_W,       // bf16 [T][H][D]   W = T (beta*exp(G)*K), rows (t, k)
-  F_WT,      // bf16 [NC][H][D][64]   W transposed (k, t)
+  F_W,       // bf16 [T][H][D]   -W, W = T (beta*exp(G)*K), rows (t, k), perm32 column order
+  F_WT,      // bf16 [NC][H][D][64]   -W transposed (k, t), perm32 column order
   F_UT,      // bf16 [NC][H][D][64]   U = T (beta*V) transposed (v, t)
-  F_KGT,     // bf16 [NC][H][D][64]   (K * exp(G_last - G)) transposed (k, t)
+  F_KGT,     // bf16 [NC][H][D][64]   (K * exp(G_last - G)) transposed (k, t), perm32 columns
   F_HT,      // bf16 [NC][H][D][D]    state entering the chunk, (v, k)
   F_HR,      // bf16 [NC][H][D][D]    same state, (k, v)           [training]
   F_VNT,     // bf16 [NC][H][D][64]   v_new transposed (v, t)
   F_VN,      // bf16 [T][H][D]        v_new rows (t, v)              [training]
+  F_KNP,     // bf16 [T][H][D]        Kn in perm32 column order (reverse scan operand)
   F_COUNT
 };
 
@@ -40,6 +41,7 @@ enum BwdBuf {
   B_DW,        // bf16 [T][H][D]       dW rows (t, k)
   B_DWT,       // bf16 [NC][H][D][64]  dW transposed (k, t)
   B_DGP,       // f32  [T][H]          partial dG (before the reverse cumsum)
+  B_DHT,       // bf16 [NC][H][D][D]   gradient of the state leaving the chunk, (v, k)
   B_COUNT
 };
 
@@ -63,6 +65,7 @@ inline void fwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[F_HR] = chunk * 128 * 128 * 2;
   s[F_VNT] = chunk * 128 * 64 * 2;
   s[F_VN] = ev * 128 * 2;
+  s[F_KNP] = ev * 128 * 2;
 }
 
 inline void bwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
@@ -76,6 +79,7 @@ inline void bwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[B_DW] = ev * 128 * 2;
   s[B_DWT] = chunk * 128 * 64 * 2;
   s[B_DGP] = ev * 4;
+  s[B_DHT] = chunk * 128 * 128 * 2;
 }
 
 // Offsets of every buffer; returns the total size in bytes.

@@ -46,3 +46,8 @@ def assemble(chunks, spans, T):
     for x, (a, b) in zip(chunks, spans):
         out[a:b] = x.transpose(0, 1)
     return out
+
+
+def perm32(x):
+    """Storage position of logical column x in the kernels' perm32 order (gdn_common.hpp)."""
+    return (x & ~31) | (((x >> 2) & 3) << 3) | (((x >> 4) & 1) << 2) | (x & 3)

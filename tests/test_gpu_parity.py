@@ -10,7 +10,7 @@ read-only bit-exactness (tests/test_qwen35_cq.py:71-89) and document isolation
 import pytest
 import torch
 
-from gdn_testlib import TOL_BF16, TOL_INTER, TOL_STATE, assemble, assert_close_bf16, rel_l2, view
+from gdn_testlib import TOL_BF16, TOL_INTER, TOL_STATE, assemble, assert_close_bf16, perm32, rel_l2, view
 from oracle import gdn_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -78,7 +78,9 @@ def test_forward_intermediates_and_output(gdn, T, bounds, H):
         assert rel_l2(vnT[c, :, :, :n].transpose(-1, -2), inter["vn"][c]) < TOL_INTER
         # rows past the tail are zero (the scan relies on it)
         assert float(UT[c, :, :, n:].abs().max() if n < 64 else 0) == 0.0
-    assert rel_l2(W, assemble(inter["W"], spans, T)) < TOL_INTER
+    # W is stored in perm32 column order (logical column x at perm32(x))
+    perm = torch.tensor([perm32(x) for x in range(128)])
+    assert rel_l2(-W[..., perm], assemble(inter["W"], spans, T)) < TOL_INTER  # stored negated
     assert rel_l2(vn, assemble(inter["vn"], spans, T)) < TOL_INTER
     assert_close_bf16("o", o.cpu(), ref)
 
