@@ -1,0 +1,286 @@
+#!/usr/bin/env python3
+"""Benchmark of the hip GDN backend on one MI355X.
+
+One step = one fwd+bwd of the gated delta rule through the drop-in API
+``cqgdn.gated_delta_net.delta`` (autograd, use_qk_l2norm_in_kernel=True) over
+one batch of synthetic inputs already resident in HBM.  The workload is
+benchmark config 2: content T=8192 plus 4 read-only CQ query blocks of 256
+events at seeded positions (9216 events), H=16, d=128, bf16 q/k/v, fp32 g/beta
+and state; timing follows the reference's GDN benchmark (warm-up, then
+synchronize around the timed loop, scripts/benchmark_gdn.py:51-56).
+
+Printed: one JSON line with the contract keys, plus
+  roofline      the dominant kernel priced against its bound (HIP events on the
+                stream it runs on, recorded inside the timed region)
+  cpu_baseline  the fp32 chunked torch oracle on this host's cores (a bounded
+                sample: one config-2 fwd+bwd)
+  extra         config-1 fwd+bwd, per-kernel table (MFMA / HBM fractions),
+                prefill, and the decode step (B=64, 256 steps, GB/s)
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "cq-pretrain_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "GDN fwd+bwd ms/layer @T=2048/8192 (H=16,d=128); MFMA util %; decode GB/s"
+H, D = 16, 128
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_config2.md"
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip config 1, prefill, decode and the kernel table")
+    ap.add_argument("--decode-steps", type=int, default=256)
+    ap.add_argument("--profile", action="store_true",
+                    help="profiler workload only: config-2 fwd+bwd steps, then a plain copy kernel of "
+                         "known size (the scale of the HBM byte counters); prints no JSON")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def training_case(gdn, synthetic, torch, config, device):
+    T, mask, bounds = synthetic.config_events(config, seed=0)
+    xs = [x.to(device) for x in synthetic.make_inputs(T, H, D, seed=config, readonly=mask)]
+    gen = torch.Generator().manual_seed(100 + config)
+    do = torch.randn(1, T, H, D, generator=gen).bfloat16().to(device)
+    leaves = [x.requires_grad_() for x in xs]
+
+    def step():
+        for x in leaves:
+            x.grad = None
+        y, _ = gdn.delta(*leaves, use_qk_l2norm_in_kernel=True)
+        y.backward(do)
+
+    return T, bounds, step, xs
+
+
+def time_steps(torch, step, steps):
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def kernel_table(torch, _lib, workmodel, step, bounds, reps=5):
+    """Average duration of every fwd/bwd kernel (one armed at a time) and its roofline."""
+    table = {}
+    for name in workmodel.FWD_KERNELS + workmodel.BWD_KERNELS:
+        with _lib.KernelTimer(name, reps) as t:
+            for _ in range(reps):
+                step()
+            torch.cuda.synchronize()
+        if not t.ms:
+            continue
+        sec = statistics.mean(t.ms) * 1e-3
+        flops, nbytes = workmodel.kernel_work(name, bounds, H)
+        table[name] = dict(us=round(sec * 1e6, 2), tflops=round(flops / sec / 1e12, 2),
+                           mfma_frac=round(flops / sec / workmodel.PEAK_BF16_FLOPS, 4),
+                           gbps=round(nbytes / sec / 1e9, 1),
+                           hbm_frac=round(nbytes / sec / workmodel.PEAK_HBM_BYTES, 4))
+    return table
+
+
+def traffic_for(kernel, sha):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter summary, if it
+    was measured on this exact library build; else None."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        m = re.match(r"^traffic kernel=(\S+) lib_sha256=(\S+) bytes_per_launch=(\d+)", line.strip())
+        if m and m.group(1) == kernel and m.group(2) == sha:
+            return int(m.group(3))
+    return None
+
+
+def cpu_baseline(torch):
+    """fp32 chunked torch oracle, fwd+bwd via autograd, on this host's cores: one config-2 step."""
+    from cqgdn import synthetic
+    from oracle import gdn_oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        T, mask, bounds = synthetic.config_events(2, seed=0)
+        xs = [x.float().requires_grad_() for x in synthetic.make_inputs(T, H, D, seed=2, readonly=mask)]
+        do = torch.randn(1, T, H, D, generator=torch.Generator().manual_seed(102))
+        t0 = time.perf_counter()
+        y = O.chunk_delta(*xs, bounds, normalize=True)
+        y.backward(do)
+        sec = time.perf_counter() - t0
+    finally:
+        torch.set_num_threads(prev)
+    return dict(value=round(sec * 1e3, 1), unit="ms/layer", cores=cores, kind="port",
+                sample="one fwd+bwd of config 2 (T=9216, H=16, d=128): oracle/gdn_oracle.chunk_delta in fp32 "
+                       "(chunk 64) with torch autograd for the backward, "
+                       f"torch.set_num_threads({cores})")
+
+
+def decode_case(gdn, _lib, workmodel, torch, device, steps):
+    """Config 4: B=64 sequences, H=16, one event per step, 256 steps over 8 rotated layer states."""
+    n, layers = 64, 8
+    gen = torch.Generator().manual_seed(4)
+    states = [(torch.randn(n, H, D, D, generator=gen) * 0.02).to(device) for _ in range(layers)]
+    q = torch.nn.functional.normalize(torch.randn(n, 1, H, D, generator=gen), dim=-1).bfloat16().to(device)
+    k = torch.nn.functional.normalize(torch.randn(n, 1, H, D, generator=gen), dim=-1).bfloat16().to(device)
+    v = torch.randn(n, 1, H, D, generator=gen).bfloat16().to(device)
+    g = (-torch.nn.functional.softplus(torch.randn(n, 1, H, generator=gen))).to(device)
+    b = torch.randn(n, 1, H, generator=gen).sigmoid().to(device)
+    out = torch.empty_like(q)
+    for st in states:
+        gdn.recurrent(q, k, v, g, b, st, out)
+    with _lib.KernelTimer("recurrent", steps) as t:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            gdn.recurrent(q, k, v, g, b, states[i % layers], out)
+        torch.cuda.synchronize()
+        sec = (time.perf_counter() - t0) / steps
+    nbytes = workmodel.decode_bytes(n, H)
+    kern = statistics.mean(t.ms) * 1e-3
+    return dict(us_per_step=round(sec * 1e6, 2), gbps=round(nbytes / sec / 1e9, 1),
+                kernel_us=round(kern * 1e6, 2), kernel_gbps=round(nbytes / kern / 1e9, 1),
+                kernel_hbm_frac=round(nbytes / kern / workmodel.PEAK_HBM_BYTES, 4),
+                bytes_per_step=nbytes, working_set_mb=round(layers * n * H * D * D * 4 / 1e6, 1))
+
+
+COPY_BYTES = 256 << 20
+
+
+def profile_workload(torch, step, steps):
+    """Workload run under rocprofv3: ``steps`` config-2 fwd+bwd steps, then 3 copies of COPY_BYTES."""
+    for i in range(steps):
+        step()
+        torch.cuda.synchronize()
+        log(f"profile step {i} done")
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy kernel: {COPY_BYTES} bytes read and written per launch; done")
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from cqgdn import _lib, gated_delta_net as gdn, synthetic, workmodel
+
+    gdn.initialize()  # raises without a gfx950 GPU or without libcqgdn.so
+    device = "cuda:0"
+    sha = _lib.sha256()
+
+    log("config 2 fwd+bwd")
+    T, bounds, step, _ = training_case(gdn, synthetic, torch, 2, device)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    if args.profile:
+        profile_workload(torch, step, args.steps)
+        return
+    kernels = {} if args.no_extra else kernel_table(torch, _lib, workmodel, step, bounds)
+    dominant = max(kernels, key=lambda k: kernels[k]["us"]) if kernels else "bwd_dqk"
+
+    # timed region: K steps, the dominant kernel's launches bracketed by HIP events on its stream
+    with _lib.KernelTimer(dominant, args.steps) as timer:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+    launch_s = statistics.mean(timer.ms) * 1e-3
+    flops, nbytes = workmodel.kernel_work(dominant, bounds, H)
+    roof = workmodel.roofline(dominant, flops, nbytes, launch_s)
+    roof = dict(kernel=dominant, bound=roof["bound"], achieved=round(roof["achieved"], 2), peak=roof["peak"],
+                unit=roof["unit"], frac=round(roof["frac"], 4), traffic=traffic_for(dominant, sha),
+                algorithmic_bytes=nbytes, algorithmic_flops=int(flops), launch_us=round(launch_s * 1e6, 2),
+                launches=len(timer.ms))
+    total_flops = sum(workmodel.kernel_work(k, bounds, H)[0]
+                      for k in workmodel.FWD_KERNELS + workmodel.BWD_KERNELS)
+
+    extra = dict(config2_fwd_bwd_ms=round(ms, 4), config2_tflops=round(total_flops / (ms * 1e-3) / 1e12, 2),
+                 config2_mfma_frac=round(total_flops / (ms * 1e-3) / workmodel.PEAK_BF16_FLOPS, 4),
+                 lib_sha256=sha)
+    if kernels:
+        par = [k for k in kernels if k not in workmodel.SCAN_KERNELS]
+        f = sum(workmodel.kernel_work(k, bounds, H)[0] for k in par)
+        t = sum(kernels[k]["us"] for k in par) * 1e-6
+        extra["chunk_kernels_mfma_frac"] = round(f / t / workmodel.PEAK_BF16_FLOPS, 4)
+        extra["kernels_config2"] = kernels
+    if not args.no_extra:
+        log("config 1 fwd+bwd")
+        T1, bounds1, step1, _ = training_case(gdn, synthetic, torch, 1, device)
+        for _ in range(args.warmup):
+            step1()
+        ms1 = time_steps(torch, step1, args.steps) * 1e3
+        f1 = sum(workmodel.kernel_work(k, bounds1, H)[0] for k in workmodel.FWD_KERNELS + workmodel.BWD_KERNELS)
+        extra["config1_fwd_bwd_ms"] = round(ms1, 4)
+        extra["config1_tflops"] = round(f1 / (ms1 * 1e-3) / 1e12, 2)
+        log("config 2 prefill")
+        T2, mask2, b2 = synthetic.config_events(2, seed=0)
+        xs = [x.to(device) for x in synthetic.make_inputs(T2, H, D, seed=2, readonly=mask2)]
+        for _ in range(args.warmup):
+            gdn.prefill(*xs, b2)
+        extra["config2_prefill_ms"] = round(time_steps(torch, lambda: gdn.prefill(*xs, b2), args.steps) * 1e3, 4)
+        del xs
+        log("config 4 decode")
+        extra["decode_config4"] = decode_case(gdn, _lib, workmodel, torch, device, args.decode_steps)
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (config 2 fwd+bwd, fp32 oracle)")
+        cpu = cpu_baseline(torch)
+
+    print(json.dumps(dict(
+        metric=METRIC,
+        value=round(ms, 4),
+        unit="ms/layer",
+        n_gpus=1,
+        steps=args.steps,
+        warmup=args.warmup,
+        ms_per_step=round(ms, 4),
+        higher_is_better=False,
+        scaling="weak",
+        vs_baseline=None,
+        dtype="bf16",
+        data="synthetic",
+        config=dict(workload="config 2: GDN fwd+bwd, content 8192 + 4x256 read-only CQ query events (T=9216), "
+                             "H=16, d=128, chunk 64, bf16 q/k/v, fp32 g/beta/state", events=T, heads=H,
+                    head_dim=D, chunk=64, documents=len(bounds) - 1),
+        roofline=roof,
+        cpu_baseline=cpu,
+        extra=extra,
+    )), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -36,7 +36,11 @@ SIGNATURES = {
     "cqgdn_l2norm_fwd": (_I, [_P, _P, _P, _I64, _P]),
     "cqgdn_l2norm_bwd": (_I, [_P, _P, _P, _P, _I64, _P]),
     "cqgdn_chunk_local_cumsum": (_I, [_P, _P, _I64, _I, _P, _I64, _I, _P]),
+    "cqgdn_timer_arm": (_I, [ctypes.c_char_p, _I]),
+    "cqgdn_timer_read": (_I, [_P, _I, _P]),
 }
+KERNELS = ("fwd_prep", "fwd_scan", "fwd_rows", "fwd_out", "bwd_local", "bwd_scan", "bwd_rows", "bwd_dqk", "bwd_wy",
+           "recurrent")
 
 _LIB = None
 
@@ -90,3 +94,31 @@ def bwd_offsets(T: int, H: int, n_chunks: int) -> dict:
     arr = (ctypes.c_size_t * BWD_BUFFERS)()
     check(lib().cqgdn_bwd_buffer_offsets(T, H, n_chunks, arr, BWD_BUFFERS), "cqgdn_bwd_buffer_offsets")
     return dict(zip(BWD_NAMES, arr))
+
+
+class KernelTimer:
+    """Time every launch of one library kernel with hipEvents on its own stream.
+
+    Usage: ``with KernelTimer("bwd_dqk", 64) as t: ...``; afterwards ``t.ms``
+    holds the per-launch durations (the exit waits for the recorded events).
+    """
+
+    def __init__(self, kernel: str, max_launches: int):
+        if kernel not in KERNELS:
+            raise ValueError(f"unknown kernel {kernel!r}; one of {KERNELS}")
+        self.kernel, self.max_launches, self.ms = kernel, max_launches, []
+
+    def __enter__(self):
+        rc = lib().cqgdn_timer_arm(self.kernel.encode(), self.max_launches)
+        if rc != OK:
+            raise CqgdnError(f"cqgdn_timer_arm({self.kernel}) failed with code {rc}")
+        return self
+
+    def __exit__(self, *exc):
+        buf = (ctypes.c_float * self.max_launches)()
+        n = ctypes.c_int(0)
+        rc = lib().cqgdn_timer_read(buf, self.max_launches, ctypes.byref(n))
+        if rc != OK and exc[0] is None:
+            raise CqgdnError(f"cqgdn_timer_read({self.kernel}) failed with code {rc}")
+        self.ms = list(buf[:n.value])
+        return False

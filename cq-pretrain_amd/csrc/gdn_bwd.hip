@@ -913,14 +913,24 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
   auto B = [&](int i) { return reinterpret_cast<bf16*>(a.bws + a.boff[i]); };
   auto Bf = [&](int i) { return reinterpret_cast<float*>(a.bws + a.boff[i]); };
   const dim3 grid_c(a.n_chunks, a.H);
-  hipLaunchKernelGGL(bwd_local_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), a.dout, Ff(F_GC), a.chunks,
-                     a.H, a.scale, B(B_DVLT), B(B_XT));
-  hipLaunchKernelGGL(bwd_scan_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, F(F_KNP),
-                     Ff(F_GC), B(B_DVLT), B(B_XT), F(F_WT), a.chunks, a.doc_chunk, a.H, B(B_DHT), B(B_DVNT));
-  launch_rows(B(B_DHT), B(B_DVNT), a.chunks, a.n_chunks, a.H, B(B_DH), B(B_DVN), stream);
-  hipLaunchKernelGGL(bwd_dqk_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_GC), F(F_HR),
-                     F(F_VN), a.dout, B(B_DH), B(B_DVN), a.chunks, a.H, a.scale, (int)a.normalize, a.dq, Bf(B_DKP),
-                     B(B_DW), B(B_DWT), Bf(B_DGP));
+  {
+    TimedLaunch tl(K_BWD_LOCAL, stream);
+    hipLaunchKernelGGL(bwd_local_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), a.dout, Ff(F_GC),
+                       a.chunks, a.H, a.scale, B(B_DVLT), B(B_XT));
+  }
+  {
+    TimedLaunch tl(K_BWD_SCAN, stream);
+    hipLaunchKernelGGL(bwd_scan_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, F(F_KNP),
+                       Ff(F_GC), B(B_DVLT), B(B_XT), F(F_WT), a.chunks, a.doc_chunk, a.H, B(B_DHT), B(B_DVNT));
+  }
+  launch_rows(B(B_DHT), B(B_DVNT), a.chunks, a.n_chunks, a.H, B(B_DH), B(B_DVN), K_BWD_ROWS, stream);
+  {
+    TimedLaunch tl(K_BWD_DQK, stream);
+    hipLaunchKernelGGL(bwd_dqk_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_GC),
+                       F(F_HR), F(F_VN), a.dout, B(B_DH), B(B_DVN), a.chunks, a.H, a.scale, (int)a.normalize, a.dq,
+                       Bf(B_DKP), B(B_DW), B(B_DWT), Bf(B_DGP));
+  }
+  TimedLaunch tl(K_BWD_WY, stream);
   hipLaunchKernelGGL(bwd_wy_kernel, grid_c, dim3(256), 0, stream, F(F_KN), a.v, a.beta, Ff(F_GC), Ff(F_RK),
                      F(F_TM), B(B_DW), B(B_DWT), B(B_DVN), B(B_DVNT), Bf(B_DKP), Bf(B_DGP), a.chunks, a.H,
                      (int)a.normalize, a.dk, a.dv, a.dg, a.dbeta);

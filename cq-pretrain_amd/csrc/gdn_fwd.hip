@@ -607,7 +607,8 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
 }
 
 void launch_rows(const bf16* sT, const bf16* vT, const int32_t* chunks, int n_chunks, int H, bf16* srow, bf16* vrow,
-                 hipStream_t stream) {
+                 int timer_id, hipStream_t stream) {
+  TimedLaunch tl(timer_id, stream);
   hipLaunchKernelGGL(fwd_rows_kernel, dim3(n_chunks, H), dim3(256), 0, stream, sT, vT, chunks, H, srow, vrow);
 }
 
@@ -621,18 +622,26 @@ void launch_fwd(const FwdArgs& a, hipStream_t stream) {
   float* rq = reinterpret_cast<float*>(ws[F_RQ]);
   float* rk = reinterpret_cast<float*>(ws[F_RK]);
   float* gcum = reinterpret_cast<float*>(ws[F_GC]);
-  if (a.normalize)
-    hipLaunchKernelGGL(fwd_prep_kernel<true>, grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta, a.chunks,
-                       a.H, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT], ws[F_UT], ws[F_KGT],
-                       ws[F_KNP]);
-  else
-    hipLaunchKernelGGL(fwd_prep_kernel<false>, grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta, a.chunks,
-                       a.H, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT], ws[F_UT], ws[F_KGT],
-                       ws[F_KNP]);
+  {
+    TimedLaunch tl(K_FWD_PREP, stream);
+    if (a.normalize)
+      hipLaunchKernelGGL(fwd_prep_kernel<true>, grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta, a.chunks,
+                         a.H, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT], ws[F_UT], ws[F_KGT],
+                         ws[F_KNP]);
+    else
+      hipLaunchKernelGGL(fwd_prep_kernel<false>, grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
+                         a.chunks, a.H, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT], ws[F_UT],
+                         ws[F_KGT], ws[F_KNP]);
+  }
   const dim3 grid_s(a.H * (D / 16), a.n_docs);
-  hipLaunchKernelGGL(fwd_scan_kernel, grid_s, dim3(SC_THREADS), 0, stream, ws[F_W], ws[F_UT], ws[F_KGT], gcum, a.chunks,
-                     a.doc_chunk, a.H, a.initial_state, a.final_state, ws[F_HT], ws[F_VNT]);
-  if (a.training) launch_rows(ws[F_HT], ws[F_VNT], a.chunks, a.n_chunks, a.H, ws[F_HR], ws[F_VN], stream);
+  {
+    TimedLaunch tl(K_FWD_SCAN, stream);
+    hipLaunchKernelGGL(fwd_scan_kernel, grid_s, dim3(SC_THREADS), 0, stream, ws[F_W], ws[F_UT], ws[F_KGT], gcum,
+                       a.chunks, a.doc_chunk, a.H, a.initial_state, a.final_state, ws[F_HT], ws[F_VNT]);
+  }
+  if (a.training)
+    launch_rows(ws[F_HT], ws[F_VNT], a.chunks, a.n_chunks, a.H, ws[F_HR], ws[F_VN], K_FWD_ROWS, stream);
+  TimedLaunch tl(K_FWD_OUT, stream);
   hipLaunchKernelGGL(fwd_out_kernel, grid_c, dim3(256), 0, stream, ws[F_QN], ws[F_KN], gcum, ws[F_HT], ws[F_VNT],
                      a.chunks, a.H, a.scale, a.o);
 }

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "gdn_layout.hpp"
+#include "gdn_timer.hpp"
 
 namespace cqgdn {
 
@@ -48,7 +49,7 @@ void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* 
                       hipStream_t stream);
 // rows [k][v] of chunk states and rows [t][v] from their [v][k] / [v][t] forms
 void launch_rows(const bf16* sT, const bf16* vT, const int32_t* chunks, int n_chunks, int H, bf16* srow, bf16* vrow,
-                 hipStream_t stream);
+                 int timer_id, hipStream_t stream);
 void launch_l2norm_fwd(const bf16* x, bf16* y, float* rstd, int64_t rows, hipStream_t stream);
 void launch_l2norm_bwd(const bf16* y, const float* rstd, const bf16* dy, bf16* dx, int64_t rows,
                        hipStream_t stream);

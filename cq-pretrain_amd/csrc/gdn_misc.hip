@@ -64,6 +64,7 @@ void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* 
                       bool beta_bf16, float* state, bf16* out, int N, int E, int H, float scale,
                       hipStream_t stream) {
   const dim3 grid(2 * N * H);
+  TimedLaunch tl(K_RECURRENT, stream);
   if (beta_bf16)
     hipLaunchKernelGGL(recurrent_kernel<true>, grid, dim3(256), 0, stream, q, k, v, g, beta, state, out, E, H, scale);
   else

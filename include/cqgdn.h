@@ -130,6 +130,21 @@ int cqgdn_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx,
 int cqgdn_chunk_local_cumsum(const float* g, float* out, int64_t T, int H, const int32_t* chunk_table,
                              int64_t n_chunks, int reverse, void* stream);
 
+/*
+ * Instrumentation (no counterpart in the reference; used by the benchmark to
+ * price one kernel against its roofline).  cqgdn_timer_arm(name, n) makes the
+ * library bracket each of the next n launches of the named kernel with
+ * hipEventRecord on the stream it is launched on; name = NULL disarms.  Names:
+ * fwd_prep, fwd_scan, fwd_rows, fwd_out, bwd_local, bwd_scan, bwd_rows,
+ * bwd_dqk, bwd_wy, recurrent.  cqgdn_timer_read waits for the recorded
+ * events, writes up to `capacity` per-launch durations in milliseconds,
+ * stores the number of launches recorded, and disarms.  One kernel is armed
+ * at a time, process-wide.  Both return CQGDN_OK, CQGDN_EINVAL (unknown name
+ * or n outside 1..65536) or CQGDN_EHIP; they do not set cqgdn_last_error().
+ */
+int cqgdn_timer_arm(const char* kernel, int max_launches);
+int cqgdn_timer_read(float* launch_ms, int capacity, int* launches);
+
 #ifdef __cplusplus
 }
 #endif
