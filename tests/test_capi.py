@@ -1,0 +1,115 @@
+"""The C ABI of libcqgdn.so without a GPU: the library loads, exports every symbol include/cqgdn.h
+declares, and its host-only functions (sizes, offsets, chunk table, argument checks) behave as
+documented.  No call here launches a kernel."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from cqgdn import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "cqgdn.h"
+
+
+def header_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(cqgdn_\w+)\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} not built: run python cq-pretrain_amd/build.py")
+    return _lib.lib()
+
+
+def test_every_declared_symbol_is_exported_and_bound(lib):
+    symbols = header_symbols()
+    assert len(symbols) >= 15
+    for name in symbols:
+        assert hasattr(lib, name), f"{name} declared in cqgdn.h but not exported"
+    assert set(symbols) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_version(lib):
+    assert _lib.version().startswith("cqgdn ") and "gfx950" in _lib.version()
+
+
+def test_header_constants_match_binding():
+    text = HEADER.read_text()
+    for name, value in (("CQGDN_FWD_BUFFERS", _lib.FWD_BUFFERS), ("CQGDN_BWD_BUFFERS", _lib.BWD_BUFFERS),
+                        ("CQGDN_NORMALIZE", _lib.NORMALIZE), ("CQGDN_TRAINING", _lib.TRAINING),
+                        ("CQGDN_EINVAL", _lib.EINVAL), ("CQGDN_EUNSUPPORTED", _lib.EUNSUPPORTED),
+                        ("CQGDN_EHIP", _lib.EHIP)):
+        m = re.search(rf"#define {name} (\d+)", text)
+        assert m and int(m.group(1)) == value, name
+
+
+@pytest.mark.parametrize("T,H,nc", [(1, 4, 1), (129, 16, 3), (9216, 16, 144), (32768, 32, 530)])
+def test_workspace_offsets_are_aligned_and_disjoint(lib, T, H, nc):
+    for size_fn, offs_fn, n in ((lib.cqgdn_fwd_workspace_size, _lib.fwd_offsets, _lib.FWD_BUFFERS),
+                                (lib.cqgdn_bwd_workspace_size, _lib.bwd_offsets, _lib.BWD_BUFFERS)):
+        total = size_fn(T, H, nc)
+        offs = list(offs_fn(T, H, nc).values())
+        assert len(offs) == n and offs[0] == 0
+        assert all(o % 256 == 0 for o in offs)
+        assert all(b > a for a, b in zip(offs, offs[1:])) and total > offs[-1]
+    # the largest per-chunk buffer is a [D][D] bf16 state per chunk and head
+    offs = _lib.fwd_offsets(T, H, nc)
+    assert offs["h"] - offs["hT"] >= nc * H * 128 * 128 * 2
+
+
+def test_chunk_table_c_abi(lib):
+    bounds = (ctypes.c_int64 * 4)(0, 10, 10, 140)
+    n = lib.cqgdn_chunk_table(bounds, 4, None, None)
+    assert n == 4
+    table = (ctypes.c_int32 * (2 * n))()
+    doc = (ctypes.c_int32 * 4)()
+    assert lib.cqgdn_chunk_table(bounds, 4, table, doc) == n
+    assert list(table) == [0, 10, 10, 64, 74, 64, 138, 2]
+    assert list(doc) == [0, 1, 1, 4]
+    bad = (ctypes.c_int64 * 3)(0, 10, 5)
+    assert lib.cqgdn_chunk_table(bad, 3, None, None) == -1
+    assert b"non-decreasing" in lib.cqgdn_last_error()
+
+
+def _fwd(lib, **kw):
+    p = ctypes.c_void_p(256)
+    args = dict(q=p, k=p, v=p, g=p, beta=p, T=64, H=4, table=p, n_chunks=1, doc=p, n_docs=1, scale=0.1,
+                flags=_lib.NORMALIZE | _lib.TRAINING, init=None, final=None, o=p, ws=p,
+                ws_bytes=lib.cqgdn_fwd_workspace_size(64, 4, 1), stream=None)
+    args.update(kw)
+    return lib.cqgdn_fwd(*args.values())
+
+
+def test_fwd_rejects_invalid_arguments_before_launch(lib):
+    assert _fwd(lib, T=-1) == _lib.EINVAL
+    assert _fwd(lib, H=0) == _lib.EINVAL
+    assert _fwd(lib, n_chunks=0) == _lib.EINVAL
+    assert _fwd(lib, q=None) == _lib.EINVAL
+    assert _fwd(lib, ws_bytes=100) == _lib.EINVAL
+    assert b"workspace" in lib.cqgdn_last_error()
+    assert _fwd(lib, q=ctypes.c_void_p(258)) == _lib.EINVAL  # misaligned
+
+
+def test_recurrent_and_helpers_reject_invalid_arguments(lib):
+    p = ctypes.c_void_p(256)
+    assert lib.cqgdn_recurrent(p, p, p, p, p, 0, p, p, -1, 1, 4, 0.1, None) == _lib.EINVAL
+    assert lib.cqgdn_recurrent(None, p, p, p, p, 0, p, p, 1, 1, 4, 0.1, None) == _lib.EINVAL
+    assert lib.cqgdn_recurrent(p, p, p, p, p, 0, p, p, 0, 1, 4, 0.1, None) == _lib.OK  # nothing to do
+    assert lib.cqgdn_l2norm_fwd(p, p, None, -1, None) == _lib.EINVAL
+    assert lib.cqgdn_l2norm_bwd(None, p, p, p, 4, None) == _lib.EINVAL
+    assert lib.cqgdn_chunk_local_cumsum(None, p, 4, 4, p, 1, 0, None) == _lib.EINVAL
+
+
+def test_timer_arguments(lib):
+    assert lib.cqgdn_timer_arm(b"no_such_kernel", 4) == _lib.EINVAL
+    assert lib.cqgdn_timer_arm(b"bwd_dqk", 0) == _lib.EINVAL
+    assert lib.cqgdn_timer_arm(None, 0) == _lib.OK
+    n = ctypes.c_int(-1)
+    assert lib.cqgdn_timer_read(None, 0, ctypes.byref(n)) == _lib.OK and n.value == 0
+    with pytest.raises(ValueError):
+        _lib.KernelTimer("nope", 1)

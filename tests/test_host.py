@@ -1,0 +1,130 @@
+"""Host-side logic of the hip backend (no GPU): metadata helpers, argument checks, work model, bench CLI.
+
+Mirrors the reference's host contract of ops/gated_delta_net.py: host_bounds
+(:102-114), chunk_indices (:90-99), the argument checks of delta() (:217-249)
+and the no-fallback rule (:1, :166-167).
+"""
+
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+import torch
+
+from cqgdn import gated_delta_net as gdn
+from cqgdn import synthetic, workmodel
+from oracle import gdn_oracle as O
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def test_host_bounds_contract():
+    assert gdn.host_bounds(None, None) is None
+    cu = torch.tensor([0, 5, 9])
+    assert gdn.host_bounds(cu, torch.tensor([0, 5, 9])) == (0, 5, 9)
+    assert gdn.host_bounds(cu, [0, 5, 9]) == (0, 5, 9)
+    with pytest.raises(ValueError, match="cu_seqlens_cpu"):
+        gdn.host_bounds(cu, None)
+    for bad in ([1, 5], [0, 5, 3], []):
+        with pytest.raises(ValueError, match="Invalid packed sequence boundaries"):
+            gdn.host_bounds(cu, bad)
+
+
+def test_chunk_indices_pairs():
+    assert gdn.chunk_indices(None, 64) is None
+    assert gdn.chunk_indices((0, 3, 200), 64) == [0, 0, 1, 0, 1, 1, 1, 2, 1, 3]  # 197 events: 4 chunks
+    assert gdn.chunk_indices((0, 0, 65), 64) == [1, 0, 1, 1]  # an empty document has no chunk
+
+
+@pytest.mark.parametrize("bounds", [(0, 1), (0, 64), (0, 65), (0, 37, 129), (0, 0, 130, 130),
+                                    synthetic.doc_bounds(32768, seed=6)])
+def test_chunk_table_matches_oracle_spans(bounds):
+    table, doc = gdn.chunk_table(bounds)
+    spans = O.chunk_spans(bounds)
+    assert [(int(a), int(a) + int(n)) for a, n in table.tolist()] == spans
+    assert doc.tolist()[-1] == len(spans)
+    for d, (a, b) in enumerate(zip(bounds, bounds[1:])):
+        first, last = doc[d].item(), doc[d + 1].item()
+        assert [s for s in spans if a <= s[0] < b] == spans[first:last]
+
+
+def test_chunk_table_rejects_invalid_bounds():
+    for bad in ((1, 5), (0, 5, 3)):
+        with pytest.raises(ValueError):
+            gdn.chunk_table(bad)
+
+
+def _bf16(T=4, H=4):
+    return [torch.zeros(1, T, H, 128, dtype=torch.bfloat16) for _ in range(3)] + \
+        [torch.zeros(1, T, H), torch.zeros(1, T, H)]
+
+
+def test_delta_argument_checks_match_reference():
+    q, k, v, g, b = _bf16()
+    with pytest.raises(NotImplementedError, match="zero initial state"):
+        gdn.delta(q, k, v, g, b, initial_state=torch.zeros(1))
+    with pytest.raises(NotImplementedError, match="zero initial state"):
+        gdn.delta(q, k, v, g, b, output_final_state=True)
+    with pytest.raises(ValueError, match="QKV must share"):
+        gdn.delta(q.float(), k, v, g, b)
+    with pytest.raises(ValueError, match="head dimension 128"):
+        gdn.delta(q[..., :64], k[..., :64], v[..., :64], g, b)
+    q5 = torch.zeros(1, 4, 5, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="supported local heads"):
+        gdn.delta(q5, q5, q5, g[..., :1].expand(1, 4, 5), b[..., :1].expand(1, 4, 5))
+    cu = torch.tensor([0, 3])
+    with pytest.raises(ValueError, match="covering every token"):
+        gdn.delta(q, k, v, g, b, cu_seqlens=cu, cu_seqlens_cpu=[0, 3])
+    with pytest.raises(NotImplementedError, match="fp16"):
+        gdn.delta(q.half(), k.half(), v.half(), g, b)
+
+
+def test_no_cpu_fallback():
+    # the hip backend never computes on the CPU: CPU tensors are rejected, not silently handled
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        gdn.delta(*_bf16())
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        gdn.prefill(*_bf16(), (0, 4))
+    q = torch.zeros(1, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        gdn.recurrent(q, q, q, torch.zeros(1, 4), torch.zeros(1, 4), torch.zeros(1, 4, 128, 128), q.clone())
+
+
+def test_product_package_never_imports_the_oracle():
+    pkg = ROOT / "cq-pretrain_amd"
+    for path in pkg.rglob("*.py"):
+        text = path.read_text()
+        assert "oracle" not in text.replace("oracle/", ""), f"{path} references the oracle"
+
+
+def test_workmodel_split_sums_to_algorithmic_totals():
+    # forward 10 C^2 d + 6 C d^2 + (2/3) C^3 and backward 20 C^2 d + 12 C d^2 + 4 C^3 per (chunk, head)
+    fwd = sum(workmodel.flops_per_chunk(k, 64) for k in workmodel.FWD_KERNELS)
+    bwd = sum(workmodel.flops_per_chunk(k, 64) for k in workmodel.BWD_KERNELS)
+    assert round(fwd) == 11_709_099
+    assert bwd == 24_117_248
+    # config 2: 2304 chunk-heads, 82.5 GFLOP fwd+bwd
+    total = sum(workmodel.kernel_work(k, (0, 9216), 16)[0] for k in workmodel.FWD_KERNELS + workmodel.BWD_KERNELS)
+    assert abs(total - 82.54e9) < 0.01e9
+    # decode: 64 * 16 * 132,104 bytes per step
+    assert workmodel.decode_bytes(64, 16) == 64 * 16 * 132_104
+
+
+def test_synthetic_configs():
+    T1, m1, b1 = synthetic.config_events(1)
+    assert T1 == 2304 and m1[2048:].all() and not m1[:2048].any() and b1 == (0, 2304)
+    T2, m2, b2 = synthetic.config_events(2)
+    assert T2 == 9216 and int(m2.sum()) == 1024 and b2 == (0, 9216)
+    T3, _, b3 = synthetic.config_events(3)
+    assert b3[-1] == 32768 and all(256 <= b - a <= 4096 for a, b in zip(b3, b3[1:-1]))
+    q, k, v, g, beta = synthetic.make_inputs(16, 2, 128, seed=0, readonly=torch.arange(16) >= 12)
+    assert (k[:, 12:] == 0).all() and (v[:, 12:] == 0).all() and (g[:, 12:] == 0).all() and (beta[:, 12:] == 0).all()
+    assert (g[:, :12] < 0).all() and ((beta[:, :12] > 0) & (beta[:, :12] < 1)).all()
+
+
+def test_bench_refuses_more_than_one_gpu():
+    proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                          timeout=120)
+    assert proc.returncode == 2
+    assert "one GPU" in proc.stderr
