@@ -14,9 +14,9 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().with_name("libcqgdn.so")
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
-NORMALIZE, TRAINING = 1, 2
-FWD_BUFFERS, BWD_BUFFERS = 15, 10
-FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "WT", "UT", "KgT", "hT", "h", "vnT", "vn", "knP")
+NORMALIZE, TRAINING, PRECISE = 1, 2, 4
+FWD_BUFFERS, BWD_BUFFERS = 16, 10
+FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "WT", "UT", "KgT", "hT", "h", "vnT", "vn", "knP", "vscale")
 BWD_NAMES = ("dvlT", "XT", "dh", "dVnT", "dVn", "dKp", "dW", "dWT", "dGp", "dhT")
 
 # every symbol include/cqgdn.h declares, with (restype, argtypes)

@@ -150,7 +150,8 @@ def _flatten(q, k, v, g, beta, bounds):
     return q, k, v, g, beta, bounds
 
 
-def _forward(q, k, v, g, beta, bounds, normalize, scale, training, initial_state=None, want_state=False):
+def _forward(q, k, v, g, beta, bounds, normalize, scale, training, initial_state=None, want_state=False,
+             precise=False):
     t, h = q.shape[1], q.shape[2]
     if q.shape[0] != 1 or bounds[0] != 0 or bounds[-1] != t:
         raise ValueError("packed forward needs batch 1 and bounds (0, ..., T) covering every event")
@@ -164,7 +165,8 @@ def _forward(q, k, v, g, beta, bounds, normalize, scale, training, initial_state
     ws = torch.empty(_lib.lib().cqgdn_fwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=q.device)
     o = torch.empty_like(v)
     state = torch.empty(n_docs, h, 128, 128, dtype=torch.float32, device=q.device) if want_state else None
-    flags = (_lib.NORMALIZE if normalize else 0) | (_lib.TRAINING if training else 0)
+    flags = (_lib.NORMALIZE if normalize else 0) | (_lib.TRAINING if training else 0) | \
+        (_lib.PRECISE if precise else 0)
     call("cqgdn_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), t, h, _ptr(table), n_chunks, _ptr(doc),
          n_docs, float(scale), flags, _ptr(initial_state), _ptr(state), _ptr(o), _ptr(ws), ws.numel(),
          _stream(q.device))
@@ -251,6 +253,8 @@ def delta(
 def prefill(q, k, v, g, beta, bounds, initial_state=None):
     """Inference forward with per-document final states (ops/gated_delta_net.py:292-311).
 
+    Runs the precise forward (fp16 MFMA operands, CQGDN_PRECISE), whose final states
+    stay within 1e-3 relative of an fp32 computation.
     q, k, v: [1,T,H,128] bf16 (l2norm applied inside, scale 128^-0.5); g, beta [1,T,H].
     Returns ``(o [1,T,H,128] time-first, state [n_docs,H,K,V] fp32)``.
     """
@@ -264,7 +268,7 @@ def prefill(q, k, v, g, beta, bounds, initial_state=None):
     if initial_state is not None:
         initial_state = initial_state.float().contiguous()
     o, state, _ = _forward(qf, kf, vf, gf, bf, bounds, True, q.shape[-1] ** -0.5, training=False,
-                           initial_state=initial_state, want_state=True)
+                           initial_state=initial_state, want_state=True, precise=True)
     return o, state
 
 

@@ -118,7 +118,10 @@ int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const
               unsigned flags, const float* initial_state, float* final_state, void* o, void* workspace,
               size_t workspace_bytes, void* stream) {
   if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
-  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING)) return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
+  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING | CQGDN_PRECISE))
+    return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
+  if ((flags & CQGDN_TRAINING) && (flags & CQGDN_PRECISE))
+    return fail(CQGDN_EINVAL, "CQGDN_PRECISE is an inference forward: it cannot be combined with CQGDN_TRAINING");
   if (T == 0) {
     if (final_state && n_docs > 0) {
       // every document is empty: its final state is its initial state (or zero)
@@ -149,6 +152,7 @@ int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const
   a.scale = scale;
   a.normalize = (flags & CQGDN_NORMALIZE) != 0;
   a.training = (flags & CQGDN_TRAINING) != 0;
+  a.precise = (flags & CQGDN_PRECISE) != 0;
   a.initial_state = initial_state;
   a.final_state = final_state;
   a.o = static_cast<bf16*>(o);

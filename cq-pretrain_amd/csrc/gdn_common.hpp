@@ -96,6 +96,59 @@ __device__ __forceinline__ bf16x8 ld8s(const bf16* p, int stride) {
 __device__ __forceinline__ void st4(bf16* p, f32x4 x) { *reinterpret_cast<bf16x4*>(p) = cvt4(x); }
 __device__ __forceinline__ void st8(bf16* p, bf16x8 x) { *reinterpret_cast<bf16x8*>(p) = x; }
 
+// ---- fp16 operands ----------------------------------------------------------
+// The precise (inference) forward keeps its MFMA operands in fp16: 11 mantissa
+// bits instead of bf16's 8, at the same MFMA rate (v_mfma_f32_16x16x32_f16).
+// The kernels are templates over the operand element type E (bf16 or f16);
+// Vec<E> names its vector types and the helpers below are overloaded on them.
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 mfma(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f16x8 ld8(const f16* p) { return *reinterpret_cast<const f16x8*>(p); }
+__device__ __forceinline__ f16x4 ld4(const f16* p) { return *reinterpret_cast<const f16x4*>(p); }
+__device__ __forceinline__ f32x4 cvtf4(f16x4 x) { return __builtin_convertvector(x, f32x4); }
+__device__ __forceinline__ f32x8 cvtf8(f16x8 x) { return __builtin_convertvector(x, f32x8); }
+__device__ __forceinline__ f16x8 cat(f16x4 a, f16x4 b) { return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7); }
+__device__ __forceinline__ void st4(f16* p, f32x4 x) {
+  *reinterpret_cast<f16x4*>(p) = __builtin_convertvector(x, f16x4);
+}
+__device__ __forceinline__ void st8(f16* p, f16x8 x) { *reinterpret_cast<f16x8*>(p) = x; }
+
+template <class E>
+struct Vec;
+template <>
+struct Vec<bf16> {
+  typedef bf16x8 x8;
+  typedef bf16x4 x4;
+};
+template <>
+struct Vec<f16> {
+  typedef f16x8 x8;
+  typedef f16x4 x4;
+};
+
+template <class E>
+__device__ __forceinline__ typename Vec<E>::x4 to4(f32x4 x) {
+  return __builtin_convertvector(x, typename Vec<E>::x4);
+}
+template <class E>
+__device__ __forceinline__ typename Vec<E>::x8 to8(f32x8 x) {
+  return __builtin_convertvector(x, typename Vec<E>::x8);
+}
+template <class E>
+__device__ __forceinline__ typename Vec<E>::x8 zero8v() {
+  return to8<E>(f32x8{});
+}
+// two C tiles -> one permuted-map operand (as pack_perm, for either element type)
+template <class E>
+__device__ __forceinline__ typename Vec<E>::x8 pack_permv(f32x4 lo, f32x4 hi) {
+  return to8<E>(f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+}
+
 // ---- workgroup synchronization for loader/consumer kernels ----------------
 // Barrier that orders LDS only: waits for this wave's LDS operations, then
 // s_barrier.  __syncthreads() also waits for every outstanding vector-memory

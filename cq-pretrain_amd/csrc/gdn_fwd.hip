@@ -21,20 +21,24 @@
 
 namespace cqgdn {
 
-constexpr int LDK = 136;  // row stride (bf16) of 64 x 128 tiles in LDS
-constexpr int LDT = 72;   // row stride (bf16) of 128 x 64 and 64 x 64 tiles in LDS
+constexpr int LDK = 136;  // row stride (elements) of 64 x 128 tiles in LDS
+constexpr int LDT = 72;   // row stride (elements) of 128 x 64 and 64 x 64 tiles in LDS
 constexpr int LDA = 65;   // row stride (fp32) of the 64 x 64 solve matrix
 
 // ---------------------------------------------------------------------------
 // fwd_prep
 // ---------------------------------------------------------------------------
-template <bool NORMALIZE>
+// E: operand element type (bf16, or f16 for the precise forward).  vscale: null,
+// or the power-of-two factor applied to V (fp16 range, see vscale_final_kernel).
+template <class E, bool NORMALIZE>
 __global__ __launch_bounds__(256) void fwd_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const int32_t* __restrict__ chunks,
-    int H, bf16* __restrict__ qn, bf16* __restrict__ kn, float* __restrict__ rq,
-    float* __restrict__ rk, float* __restrict__ gc, bf16* __restrict__ Tm, bf16* __restrict__ W,
-    bf16* __restrict__ WT, bf16* __restrict__ UT, bf16* __restrict__ KgT, bf16* __restrict__ knP) {
+    int H, const float* __restrict__ vscale, E* __restrict__ qn, E* __restrict__ kn, float* __restrict__ rq,
+    float* __restrict__ rk, float* __restrict__ gc, E* __restrict__ Tm, E* __restrict__ W,
+    E* __restrict__ WT, E* __restrict__ UT, E* __restrict__ KgT, E* __restrict__ knP) {
+  typedef typename Vec<E>::x8 X8;
+  typedef typename Vec<E>::x4 X4;
   const int c = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
@@ -42,11 +46,12 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
   const size_t cb = (size_t)c * H + h;
 
   __shared__ float Gs[64], Bs[64];
-  __shared__ __attribute__((aligned(16))) bf16 Ks[64 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 KbT[128 * LDT];
-  __shared__ __attribute__((aligned(16))) bf16 VbT[128 * LDT];
+  __shared__ __attribute__((aligned(16))) E Ks[64 * LDK];
+  __shared__ __attribute__((aligned(16))) E KbT[128 * LDT];
+  __shared__ __attribute__((aligned(16))) E VbT[128 * LDT];
   __shared__ float Af[64 * LDA];
-  __shared__ __attribute__((aligned(16))) bf16 Ts[64 * LDT];
+  __shared__ __attribute__((aligned(16))) E Ts[64 * LDT];
+  const float vs = vscale ? *vscale : 1.f;
 
   // ---- gates: chunk-local cumsum of g (wave 0, one event per lane) ----
   if (wave == 0) {
@@ -92,7 +97,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
       }
       if (in) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) st8(qn + row + 32 * j + 8 * p, cvt8(x[j] * rs));
+        for (int j = 0; j < 4; ++j) st8(qn + row + 32 * j + 8 * p, to8<E>(x[j] * rs));
         if (p == 0) rq[(size_t)(ci.start + t) * H + h] = rs;
       }
     }
@@ -112,27 +117,27 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
         ss += __shfl_xor(ss, 2, 64);
         rs = rsqrtf(ss + 1e-6f);
       }
-      bf16* kgt = KgT + cb * (D * CH);
+      E* kgt = KgT + cb * (D * CH);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const f32x8 xn = x[j] * rs;
-        const bf16x8 xb = cvt8(xn);
+        const X8 xb = to8<E>(xn);
         const int col = 32 * j + 8 * p;
         st8(Ks + t * LDK + col, xb);
         if (in) {
           st8(kn + row + col, xb);
           // perm32 copy: logical 8p..8p+3 -> 16(p&1) + 4(p>>1), 8p+4..8p+7 -> that + 8
-          bf16* kp = knP + row + 32 * j + 16 * (p & 1) + 4 * (p >> 1);
-          *reinterpret_cast<bf16x4*>(kp) = __builtin_shufflevector(xb, xb, 0, 1, 2, 3);
-          *reinterpret_cast<bf16x4*>(kp + 8) = __builtin_shufflevector(xb, xb, 4, 5, 6, 7);
+          E* kp = knP + row + 32 * j + 16 * (p & 1) + 4 * (p >> 1);
+          *reinterpret_cast<X4*>(kp) = __builtin_shufflevector(xb, xb, 0, 1, 2, 3);
+          *reinterpret_cast<X4*>(kp + 8) = __builtin_shufflevector(xb, xb, 4, 5, 6, 7);
         }
         const f32x8 xbg = xn * (b_t * gam_t);
         const f32x8 xkd = xn * kdec_t;
         const int tp = perm32(t);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-          KbT[(col + s) * LDT + t] = (bf16)xbg[s];
-          kgt[(col + s) * CH + tp] = (bf16)xkd[s];
+          KbT[(col + s) * LDT + t] = (E)xbg[s];
+          kgt[(col + s) * CH + tp] = (E)xkd[s];
         }
       }
       if (in && p == 0) rk[(size_t)(ci.start + t) * H + h] = rs;
@@ -142,9 +147,9 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int col = 32 * j + 8 * p;
-        const f32x8 x = in ? cvtf8(ld8(v + row + col)) * b_t : f32x8{};
+        const f32x8 x = in ? cvtf8(ld8(v + row + col)) * (b_t * vs) : f32x8{};
 #pragma unroll
-        for (int s = 0; s < 8; ++s) VbT[(col + s) * LDT + t] = (bf16)x[s];
+        for (int s = 0; s < 8; ++s) VbT[(col + s) * LDT + t] = (E)x[s];
       }
     }
   }
@@ -157,7 +162,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
     for (int n = 0; n < 4; ++n) acc[n] = zero4();
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      const bf16x8 a = ld8(Ks + (16 * wave + r) * LDK + 32 * kb + 8 * q4);
+      const X8 a = ld8(Ks + (16 * wave + r) * LDK + 32 * kb + 8 * q4);
 #pragma unroll
       for (int n = 0; n < 4; ++n)
         if (n <= wave) acc[n] = mfma(a, ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4), acc[n]);
@@ -190,10 +195,10 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
       const float val = (i > col) ? -part : ((i == col) ? 1.f : 0.f);
       if ((i & 3) == p) tc[i >> 2] = val;
     }
-    bf16* tm = Tm + cb * (CH * CH);
+    E* tm = Tm + cb * (CH * CH);
 #pragma unroll
     for (int jj = 0; jj < 16; ++jj) {
-      const bf16 b = (bf16)tc[jj];
+      const E b = (E)tc[jj];
       Ts[(4 * jj + p) * LDT + col] = b;
       tm[(4 * jj + p) * CH + col] = b;
     }
@@ -202,11 +207,11 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
 
   // ---- W (-> W^T storage), W^T (-> W rows), U (-> U^T storage) ----
   {
-    bf16x8 at[2];
+    X8 at[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) at[kb] = ld8(Ts + (16 * wave + r) * LDT + 32 * kb + 8 * q4);
-    bf16* wt = WT + cb * (D * CH);
-    bf16* ut = UT + cb * (D * CH);
+    E* wt = WT + cb * (D * CH);
+    E* ut = UT + cb * (D * CH);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       f32x4 aw = zero4(), au = zero4();
@@ -221,7 +226,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const int m = 2 * wave + mm;
-      bf16x8 ak[2];
+      X8 ak[2];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) ak[kb] = ld8(KbT + (16 * m + r) * LDT + 32 * kb + 8 * q4);
 #pragma unroll
@@ -258,32 +263,38 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
 constexpr int SC_THREADS = 64 * 3;
 constexpr int SC_DEPTH = 3;
 constexpr int SC_STAGES = 4;
-constexpr int SC_SROW = 136;  // scratch row stride (bf16), S^T [v][k]
-constexpr int SC_VROW = 72;   // scratch row stride (bf16), v_new^T [v][t]
+constexpr int SC_SROW = 136;  // scratch row stride (elements), S^T [v][k]
+constexpr int SC_VROW = 72;   // scratch row stride (elements), v_new^T [v][t]
 
+template <class E>
 struct __attribute__((aligned(16))) FwdStage {
-  bf16 w[64 * 128];   // -W rows t
-  bf16 kg[128 * 64];  // KgT rows k
-  bf16 ut[16 * 64];   // U^T rows of the slice
-  float glast;        // G of the chunk's last event
+  E w[64 * 128];   // -W rows t
+  E kg[128 * 64];  // KgT rows k
+  E ut[16 * 64];   // U^T rows of the slice
+  float glast;     // G of the chunk's last event
   float pad[3];
 };
 
 // the consumer's output tiles of a step, placed over the stage's W region
+template <class E>
 struct __attribute__((aligned(16))) FwdScratch {
-  bf16 s[16 * SC_SROW];  // state entering the chunk, [v][k]
-  bf16 v[16 * SC_VROW];  // v_new, [v][t]
+  E s[16 * SC_SROW];  // state entering the chunk, [v][k]
+  E v[16 * SC_VROW];  // v_new, [v][t]
 };
-static_assert(sizeof(FwdScratch) <= 64 * 128 * sizeof(bf16), "scratch must fit the W region");
-__device__ __forceinline__ FwdScratch& fwd_scratch(FwdStage& st) { return *reinterpret_cast<FwdScratch*>(st.w); }
+static_assert(sizeof(FwdScratch<bf16>) <= 64 * 128 * sizeof(bf16), "scratch must fit the W region");
+template <class E>
+__device__ __forceinline__ FwdScratch<E>& fwd_scratch(FwdStage<E>& st) {
+  return *reinterpret_cast<FwdScratch<E>*>(st.w);
+}
 
 // Issue the asynchronous copies of chunk c into stage S.  Nothing here waits
 // on memory: the chunk table is read with scalar loads and even the gate value
 // travels by copy (a vector load whose result were used here would make this
 // wave wait for every copy issued before it).
-__device__ __forceinline__ void fwd_issue(FwdStage& S, const int32_t* __restrict__ chunks, int c, int H, int h,
-                                          int v0, int lane, const bf16* __restrict__ W, const bf16* __restrict__ UT,
-                                          const bf16* __restrict__ KgT, const float* __restrict__ gc) {
+template <class E>
+__device__ __forceinline__ void fwd_issue(FwdStage<E>& S, const int32_t* __restrict__ chunks, int c, int H, int h,
+                                          int v0, int lane, const E* __restrict__ W, const E* __restrict__ UT,
+                                          const E* __restrict__ KgT, const float* __restrict__ gc) {
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
 #pragma unroll
@@ -292,13 +303,13 @@ __device__ __forceinline__ void fwd_issue(FwdStage& S, const int32_t* __restrict
     const int tt = min(t, ci.len - 1);
     dma16(W + ((size_t)(ci.start + tt) * H + h) * D + 8 * col, S.w + 512 * i);
   }
-  const bf16* kg = KgT + cb * (D * CH);
+  const E* kg = KgT + cb * (D * CH);
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int k = 8 * i + (lane >> 3), col = (lane & 7) ^ ((k >> 1) & 7);
     dma16(kg + k * CH + 8 * col, S.kg + 512 * i);
   }
-  const bf16* ut = UT + cb * (D * CH) + v0 * CH;
+  const E* ut = UT + cb * (D * CH) + v0 * CH;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int v = 8 * i + (lane >> 3), col = (lane & 7) ^ ((v >> 1) & 7);
@@ -309,20 +320,22 @@ __device__ __forceinline__ void fwd_issue(FwdStage& S, const int32_t* __restrict
 }
 
 // After the copies of chunk c have landed: zero the W rows past its length.
-__device__ __forceinline__ void fwd_fix_tail(FwdStage& S, const int32_t* __restrict__ chunks, int c, int lane) {
+template <class E>
+__device__ __forceinline__ void fwd_fix_tail(FwdStage<E>& S, const int32_t* __restrict__ chunks, int c, int lane) {
   const int len = chunk_info(chunks, c).len;
   if (len < CH) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int t = 4 * i + (lane >> 4);
-      if (t >= len) st8(S.w + t * 128 + 8 * (lane & 15), zero8());
+      if (t >= len) st8(S.w + t * 128 + 8 * (lane & 15), zero8v<E>());
     }
   }
 }
 
 // scratch of one step -> hT [v0..v0+15][k], vnT [v0..v0+15][t]
-__device__ __forceinline__ void fwd_copy_out(const FwdScratch& sc, int c, int H, int h, int v0, int lane,
-                                             bf16* __restrict__ hT, bf16* __restrict__ vnT) {
+template <class E>
+__device__ __forceinline__ void fwd_copy_out(const FwdScratch<E>& sc, int c, int H, int h, int v0, int lane,
+                                             E* __restrict__ hT, E* __restrict__ vnT) {
   const size_t cb = (size_t)c * H + h;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -336,30 +349,34 @@ __device__ __forceinline__ void fwd_copy_out(const FwdScratch& sc, int c, int H,
   }
 }
 
+template <class E>
 __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
-    const bf16* __restrict__ W, const bf16* __restrict__ UT, const bf16* __restrict__ KgT,
+    const E* __restrict__ W, const E* __restrict__ UT, const E* __restrict__ KgT,
     const float* __restrict__ gc, const int32_t* __restrict__ chunks, const int32_t* __restrict__ doc_chunk,
-    int H, const float* __restrict__ init_state, float* __restrict__ final_state, bf16* __restrict__ hT,
-    bf16* __restrict__ vnT) {
+    int H, const float* __restrict__ vscale, const float* __restrict__ init_state, float* __restrict__ final_state,
+    E* __restrict__ hT, E* __restrict__ vnT) {
+  typedef typename Vec<E>::x8 X8;
+  typedef typename Vec<E>::x4 X4;
   // blockIdx.x = slice * H + h: the slices of one head land on one XCD when H % 8 == 0
   const int h = blockIdx.x % H, slice = blockIdx.x / H, d = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const int v0 = 16 * slice;
 
-  __shared__ FwdStage stage[SC_STAGES];
+  __shared__ FwdStage<E> stage[SC_STAGES];
 
   const int c_begin = doc_chunk[d], n = doc_chunk[d + 1] - c_begin;
   if (wave == 0) {
     f32x4 S[8];  // S[m][i] = state[k = 16m + 4q4 + i][v = v0 + r]
 #pragma unroll
     for (int m = 0; m < 8; ++m) S[m] = zero4();
+    const float vs = vscale ? *vscale : 1.f;  // the state is carried in the scale of V
     if (init_state) {
       const float* s0 = init_state + ((size_t)d * H + h) * D * D;
 #pragma unroll
       for (int m = 0; m < 8; ++m)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) S[m][i] = s0[(16 * m + 4 * q4 + i) * D + v0 + r];
+        for (int i = 0; i < 4; ++i) S[m][i] = s0[(16 * m + 4 * q4 + i) * D + v0 + r] * vs;
     }
     // per-lane parts of the swizzled LDS addresses (bytes); the row parts are
     // compile-time offsets of each read
@@ -374,64 +391,65 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
     for (int tau = -SC_DEPTH; tau < n; ++tau) {
       if (tau >= 0) {
         char* base = reinterpret_cast<char*>(&stage[tau & (SC_STAGES - 1)]);
-        const char* wb = base + offsetof(FwdStage, w);
-        const char* kb = base + offsetof(FwdStage, kg);
-        const char* ub = base + offsetof(FwdStage, ut);
+        const char* wb = base + offsetof(FwdStage<E>, w);
+        const char* kb = base + offsetof(FwdStage<E>, kg);
+        const char* ub = base + offsetof(FwdStage<E>, ut);
         // all operand reads are issued ahead of the MFMAs that use them; the
         // scheduling barriers keep the compiler from interleaving them one by one
-        bf16x8 fw[4][4];
+        X8 fw[4][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) fw[i4][j] = *reinterpret_cast<const bf16x8*>(wb + wofs[j] + 4096 * i4);
+          for (int i4 = 0; i4 < 4; ++i4) fw[i4][j] = *reinterpret_cast<const X8*>(wb + wofs[j] + 4096 * i4);
         f32x4 vn[4];
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) vn[i4] = cvtf4(*reinterpret_cast<const bf16x4*>(ub + uofs[i4]));
+        for (int i4 = 0; i4 < 4; ++i4) vn[i4] = cvtf4(*reinterpret_cast<const X4*>(ub + uofs[i4]));
         __builtin_amdgcn_sched_barrier(0);
-        bf16x4 sh[8];
+        X4 sh[8];
 #pragma unroll
-        for (int m = 0; m < 8; ++m) sh[m] = cvt4(S[m]);
+        for (int m = 0; m < 8; ++m) sh[m] = to4<E>(S[m]);
         // v_new = U + (-W) S
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const bf16x8 hb = cat(sh[2 * j], sh[2 * j + 1]);
+          const X8 hb = cat(sh[2 * j], sh[2 * j + 1]);
 #pragma unroll
           for (int i4 = 0; i4 < 4; ++i4) vn[i4] = mfma(fw[i4][j], hb, vn[i4]);
         }
         __builtin_amdgcn_sched_barrier(0);
-        bf16x8 fk[8][2];
+        X8 fk[8][2];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int m = 0; m < 8; ++m) fk[m][j] = *reinterpret_cast<const bf16x8*>(kb + kofs[j] + 2048 * m);
+          for (int m = 0; m < 8; ++m) fk[m][j] = *reinterpret_cast<const X8*>(kb + kofs[j] + 2048 * m);
         // the W tile has been read (a wave's LDS operations complete in order):
         // its region now takes this step's outputs
-        char* sb = base + offsetof(FwdStage, w);
+        char* sb = base + offsetof(FwdStage<E>, w);
 #pragma unroll
-        for (int m = 0; m < 8; ++m) *reinterpret_cast<bf16x4*>(sb + sofs + 32 * m) = sh[m];
-        const float gC = __expf(reinterpret_cast<const FwdStage*>(base)->glast);
+        for (int m = 0; m < 8; ++m) *reinterpret_cast<X4*>(sb + sofs + 32 * m) = sh[m];
+        const float gC = __expf(reinterpret_cast<const FwdStage<E>*>(base)->glast);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 0; m < 8; ++m) S[m] *= gC;
         // S <- exp(G_last) S + (K exp(G_last - G))^T v_new
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const bf16x8 vb = pack_perm(vn[2 * j], vn[2 * j + 1]);
+          const X8 vb = pack_permv<E>(vn[2 * j], vn[2 * j + 1]);
 #pragma unroll
           for (int m = 0; m < 8; ++m) S[m] = mfma(fk[m][j], vb, S[m]);
         }
-        char* vbp = sb + sizeof(FwdScratch::s);
+        char* vbp = sb + sizeof(FwdScratch<E>::s);
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) *reinterpret_cast<bf16x4*>(vbp + vofs + 32 * i4) = cvt4(vn[i4]);
+        for (int i4 = 0; i4 < 4; ++i4) *reinterpret_cast<X4*>(vbp + vofs + 32 * i4) = to4<E>(vn[i4]);
       }
       lds_barrier();
     }
     if (final_state) {
       float* sf = final_state + ((size_t)d * H + h) * D * D;
+      const float inv = 1.f / vs;  // exact: vs is a power of two
 #pragma unroll
       for (int m = 0; m < 8; ++m)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sf[(16 * m + 4 * q4 + i) * D + v0 + r] = S[m][i];
+        for (int i = 0; i < 4; ++i) sf[(16 * m + 4 * q4 + i) * D + v0 + r] = S[m][i] * inv;
     }
   } else {
     // Step tau: loader (tau+1)&1 waits for chunk tau+1 (the only copy it has in
@@ -505,19 +523,21 @@ __global__ __launch_bounds__(256) void fwd_rows_kernel(const bf16* __restrict__ 
 // ---------------------------------------------------------------------------
 // fwd_out: O^T (v rows, t columns) per chunk and head
 // ---------------------------------------------------------------------------
+template <class E>
 __global__ __launch_bounds__(256) void fwd_out_kernel(
-    const bf16* __restrict__ qn, const bf16* __restrict__ kn, const float* __restrict__ gc,
-    const bf16* __restrict__ hT, const bf16* __restrict__ vnT, const int32_t* __restrict__ chunks, int H,
-    float scale, bf16* __restrict__ o) {
+    const E* __restrict__ qn, const E* __restrict__ kn, const float* __restrict__ gc,
+    const E* __restrict__ hT, const E* __restrict__ vnT, const int32_t* __restrict__ chunks, int H,
+    float scale, const float* __restrict__ vscale, bf16* __restrict__ o) {
+  typedef typename Vec<E>::x8 X8;
   const int c = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
 
-  __shared__ __attribute__((aligned(16))) bf16 Qs[64 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 Ks[64 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 Ps[64 * LDT];  // P[t][s], causal, gated
+  __shared__ __attribute__((aligned(16))) E Qs[64 * LDK];
+  __shared__ __attribute__((aligned(16))) E Ks[64 * LDK];
+  __shared__ __attribute__((aligned(16))) E Ps[64 * LDT];  // P[t][s], causal, gated
   __shared__ float Gs[64];
 
   {
@@ -527,8 +547,8 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      st8(Qs + t * LDK + col, in ? ld8(qn + row + col) : zero8());
-      st8(Ks + t * LDK + col, in ? ld8(kn + row + col) : zero8());
+      st8(Qs + t * LDK + col, in ? ld8(qn + row + col) : zero8v<E>());
+      st8(Ks + t * LDK + col, in ? ld8(kn + row + col) : zero8v<E>());
     }
     if (p == 0) Gs[t] = gc[(size_t)(ci.start + (in ? t : ci.len - 1)) * H + h];
   }
@@ -558,8 +578,8 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
   __syncthreads();
 
   // O^T = (h^T Qn^T) * gam_t + Vn^T P^T ; wave owns value tiles 2w, 2w+1
-  const bf16* ht = hT + cb * (D * D);
-  const bf16* vt = vnT + cb * (D * CH);
+  const E* ht = hT + cb * (D * D);
+  const E* vt = vnT + cb * (D * CH);
   f32x4 acc[2][4];
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm)
@@ -567,12 +587,12 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
     for (int n = 0; n < 4; ++n) acc[mm][n] = zero4();
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
-    bf16x8 bq[4];
+    X8 bq[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) bq[n] = ld8(Qs + (16 * n + r) * LDK + 32 * kb + 8 * q4);
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
-      const bf16x8 a = ld8(ht + (16 * (2 * wave + mm) + r) * D + 32 * kb + 8 * q4);
+      const X8 a = ld8(ht + (16 * (2 * wave + mm) + r) * D + 32 * kb + 8 * q4);
 #pragma unroll
       for (int n = 0; n < 4; ++n) acc[mm][n] = mfma(a, bq[n], acc[mm][n]);
     }
@@ -585,24 +605,25 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
   }
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
-    bf16x8 a[2];
+    X8 a[2];
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) a[mm] = ld8(vt + (16 * (2 * wave + mm) + r) * CH + 32 * kb + 8 * q4);
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       if (n < 2 * kb) continue;  // t-tile n holds no s in this block (s > t)
-      const bf16x8 b = ld8(Ps + (16 * n + r) * LDT + 32 * kb + 8 * q4);
+      const X8 b = ld8(Ps + (16 * n + r) * LDT + 32 * kb + 8 * q4);
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) acc[mm][n] = mfma(a[mm], b, acc[mm][n]);
     }
   }
+  const float osc = vscale ? scale / *vscale : scale;  // undo the power-of-two scale of V
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
     const int t = 16 * n + r;
     if (t >= ci.len) continue;
     bf16* orow = o + ((size_t)(ci.start + t) * H + h) * D;
 #pragma unroll
-    for (int mm = 0; mm < 2; ++mm) st4(orow + 16 * (2 * wave + mm) + 4 * q4, acc[mm][n] * scale);
+    for (int mm = 0; mm < 2; ++mm) st4(orow + 16 * (2 * wave + mm) + 4 * q4, acc[mm][n] * osc);
   }
 }
 
@@ -613,37 +634,103 @@ void launch_rows(const bf16* sT, const bf16* vT, const int32_t* chunks, int n_ch
 }
 
 // ---------------------------------------------------------------------------
+// Power-of-two scale of V for the fp16 (precise) forward.  The recurrence is
+// linear in (V, initial state): scaling both by vs scales W-free quantities
+// (U, v_new, every state, O) by vs exactly, so the kernels carry them scaled
+// and divide O and the final state by vs.  vs brings max(|V|, |S0|) into
+// [32, 64), far inside fp16's range (65504) for U, v_new and the state.
+// ---------------------------------------------------------------------------
+constexpr int VS_BLOCKS = kVscaleBlocks;
+
+__device__ __forceinline__ float block_max(float m, float* red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__global__ __launch_bounds__(256) void vscale_partial_kernel(const bf16* __restrict__ v, size_t nv8,
+                                                             const float* __restrict__ s0, size_t ns,
+                                                             float* __restrict__ part) {
+  __shared__ float red[4];
+  float m = 0.f;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv8; i += stride) {
+    const f32x8 x = cvtf8(ld8(v + 8 * i));
+#pragma unroll
+    for (int s = 0; s < 8; ++s) m = fmaxf(m, fabsf(x[s]));
+  }
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < ns; i += stride) m = fmaxf(m, fabsf(s0[i]));
+  m = block_max(m, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(256) void vscale_final_kernel(const float* __restrict__ part, int n,
+                                                           float* __restrict__ vscale) {
+  __shared__ float red[4];
+  float m = 0.f;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) m = fmaxf(m, part[i]);
+  m = block_max(m, red);
+  if (threadIdx.x == 0) {
+    float sc = 1.f;
+    if (m > 0.f && isfinite(m)) {
+      int e;
+      frexpf(m, &e);  // m < 2^e
+      sc = ldexpf(1.f, min(max(6 - e, -60), 60));
+    }
+    vscale[0] = sc;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
-void launch_fwd(const FwdArgs& a, hipStream_t stream) {
+template <class E>
+static void launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stream) {
   const dim3 grid_c(a.n_chunks, a.H);
-  bf16* ws[F_COUNT];
-  for (int i = 0; i < F_COUNT; ++i) ws[i] = reinterpret_cast<bf16*>(a.ws + a.off[i]);
+  E* ws[F_COUNT];
+  for (int i = 0; i < F_COUNT; ++i) ws[i] = reinterpret_cast<E*>(a.ws + a.off[i]);
   float* rq = reinterpret_cast<float*>(ws[F_RQ]);
   float* rk = reinterpret_cast<float*>(ws[F_RK]);
   float* gcum = reinterpret_cast<float*>(ws[F_GC]);
   {
     TimedLaunch tl(K_FWD_PREP, stream);
     if (a.normalize)
-      hipLaunchKernelGGL(fwd_prep_kernel<true>, grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta, a.chunks,
-                         a.H, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT], ws[F_UT], ws[F_KGT],
-                         ws[F_KNP]);
+      hipLaunchKernelGGL((fwd_prep_kernel<E, true>), grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
+                         a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT],
+                         ws[F_UT], ws[F_KGT], ws[F_KNP]);
     else
-      hipLaunchKernelGGL(fwd_prep_kernel<false>, grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
-                         a.chunks, a.H, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT], ws[F_UT],
-                         ws[F_KGT], ws[F_KNP]);
+      hipLaunchKernelGGL((fwd_prep_kernel<E, false>), grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
+                         a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT],
+                         ws[F_UT], ws[F_KGT], ws[F_KNP]);
   }
   const dim3 grid_s(a.H * (D / 16), a.n_docs);
   {
     TimedLaunch tl(K_FWD_SCAN, stream);
-    hipLaunchKernelGGL(fwd_scan_kernel, grid_s, dim3(SC_THREADS), 0, stream, ws[F_W], ws[F_UT], ws[F_KGT], gcum,
-                       a.chunks, a.doc_chunk, a.H, a.initial_state, a.final_state, ws[F_HT], ws[F_VNT]);
+    hipLaunchKernelGGL(fwd_scan_kernel<E>, grid_s, dim3(SC_THREADS), 0, stream, ws[F_W], ws[F_UT], ws[F_KGT], gcum,
+                       a.chunks, a.doc_chunk, a.H, vscale, a.initial_state, a.final_state, ws[F_HT], ws[F_VNT]);
   }
   if (a.training)
-    launch_rows(ws[F_HT], ws[F_VNT], a.chunks, a.n_chunks, a.H, ws[F_HR], ws[F_VN], K_FWD_ROWS, stream);
+    launch_rows(reinterpret_cast<bf16*>(ws[F_HT]), reinterpret_cast<bf16*>(ws[F_VNT]), a.chunks, a.n_chunks, a.H,
+                reinterpret_cast<bf16*>(ws[F_HR]), reinterpret_cast<bf16*>(ws[F_VN]), K_FWD_ROWS, stream);
   TimedLaunch tl(K_FWD_OUT, stream);
-  hipLaunchKernelGGL(fwd_out_kernel, grid_c, dim3(256), 0, stream, ws[F_QN], ws[F_KN], gcum, ws[F_HT], ws[F_VNT],
-                     a.chunks, a.H, a.scale, a.o);
+  hipLaunchKernelGGL(fwd_out_kernel<E>, grid_c, dim3(256), 0, stream, ws[F_QN], ws[F_KN], gcum, ws[F_HT], ws[F_VNT],
+                     a.chunks, a.H, a.scale, vscale, a.o);
+}
+
+void launch_fwd(const FwdArgs& a, hipStream_t stream) {
+  if (!a.precise) {
+    launch_fwd_t<bf16>(a, nullptr, stream);
+    return;
+  }
+  float* vsc = reinterpret_cast<float*>(a.ws + a.off[F_VSC]);
+  const size_t nv8 = (size_t)a.T * a.H * (D / 8);
+  const size_t ns = a.initial_state ? (size_t)a.n_docs * a.H * D * D : 0;
+  hipLaunchKernelGGL(vscale_partial_kernel, dim3(VS_BLOCKS), dim3(256), 0, stream, a.v, nv8, a.initial_state, ns,
+                     vsc + 1);
+  hipLaunchKernelGGL(vscale_final_kernel, dim3(1), dim3(256), 0, stream, vsc + 1, VS_BLOCKS, vsc);
+  launch_fwd_t<f16>(a, vsc, stream);
 }
 
 }  // namespace cqgdn

@@ -19,6 +19,7 @@ struct FwdArgs {
   int T, H, n_chunks, n_docs;
   float scale;
   bool normalize, training;
+  bool precise;                // fp16 operands (inference only); operands in the workspace are then fp16
   const float* initial_state;  // [n_docs][H][K][V] or null
   float* final_state;          // [n_docs][H][K][V] or null
   bf16* o;                     // [T][H][D]

@@ -1,5 +1,7 @@
 // Workspace layout of the GDN forward/backward passes (host and device).
 //
+// In the precise forward (CQGDN_PRECISE) every buffer listed as bf16 holds fp16.
+//
 // The forward workspace holds everything the backward re-reads (the reference
 // saves q,k,v,gcum,beta,A in fused mode and also w,h,v_new in cached mode,
 // ops/gated_delta_net.py:184); keeping h and v_new avoids re-running the serial
@@ -28,6 +30,7 @@ enum FwdBuf {
   F_VNT,     // bf16 [NC][H][D][64]   v_new transposed (v, t)
   F_VN,      // bf16 [T][H][D]        v_new rows (t, v)              [training]
   F_KNP,     // bf16 [T][H][D]        Kn in perm32 column order (reverse scan operand)
+  F_VSC,     // f32  [1 + 256]        power-of-two scale of V and block partials (precise forward)
   F_COUNT
 };
 
@@ -46,6 +49,7 @@ enum BwdBuf {
 };
 
 constexpr size_t kAlign = 256;
+constexpr int kVscaleBlocks = 256;  // partial maxima behind the precise forward's V scale
 
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
@@ -66,6 +70,7 @@ inline void fwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[F_VNT] = chunk * 128 * 64 * 2;
   s[F_VN] = ev * 128 * 2;
   s[F_KNP] = ev * 128 * 2;
+  s[F_VSC] = (1 + kVscaleBlocks) * 4;
 }
 
 inline void bwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {

@@ -41,6 +41,10 @@ extern "C" {
 /* flags of cqgdn_fwd / cqgdn_bwd */
 #define CQGDN_NORMALIZE 1u /* l2-normalize q and k in the kernels (use_qk_l2norm_in_kernel=True) */
 #define CQGDN_TRAINING 2u  /* keep the extra layouts the backward reads (h and v_new rows) */
+/* Inference forward with fp16 MFMA operands (11-bit mantissa instead of bf16's 8) for final
+ * states within 1e-3 of an fp32 computation; V and the initial state are scaled by a power of
+ * two inside the call so every fp16 operand stays in range.  Not combinable with CQGDN_TRAINING. */
+#define CQGDN_PRECISE 4u
 
 /* Library version string, e.g. "cqgdn 0.1.0 gfx950". */
 const char* cqgdn_version(void);
@@ -63,7 +67,7 @@ int64_t cqgdn_chunk_table(const int64_t* bounds, int n_bounds, int32_t* table, i
  * that tests can inspect intermediates.  The same workspace must be passed,
  * unmodified, to cqgdn_bwd.
  */
-#define CQGDN_FWD_BUFFERS 15
+#define CQGDN_FWD_BUFFERS 16
 #define CQGDN_BWD_BUFFERS 10
 size_t cqgdn_fwd_workspace_size(int64_t T, int H, int64_t n_chunks);
 int cqgdn_fwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets, int count);
@@ -82,6 +86,8 @@ int cqgdn_bwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets
  *   final_state    : NULL or [n_docs][H][K][V] fp32, written with each document's last state
  *   o              : [T][H][D] bf16 output (time-first)
  *   workspace      : >= cqgdn_fwd_workspace_size() bytes, 256-byte aligned
+ *   flags          : CQGDN_NORMALIZE | (CQGDN_TRAINING or CQGDN_PRECISE); the reference's
+ *                    prefill (ops/gated_delta_net.py:292-311) maps to NORMALIZE | PRECISE
  */
 int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T, int H,
               const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,

@@ -42,6 +42,7 @@ def test_header_constants_match_binding():
     text = HEADER.read_text()
     for name, value in (("CQGDN_FWD_BUFFERS", _lib.FWD_BUFFERS), ("CQGDN_BWD_BUFFERS", _lib.BWD_BUFFERS),
                         ("CQGDN_NORMALIZE", _lib.NORMALIZE), ("CQGDN_TRAINING", _lib.TRAINING),
+                        ("CQGDN_PRECISE", _lib.PRECISE),
                         ("CQGDN_EINVAL", _lib.EINVAL), ("CQGDN_EUNSUPPORTED", _lib.EUNSUPPORTED),
                         ("CQGDN_EHIP", _lib.EHIP)):
         m = re.search(rf"#define {name} (\d+)", text)
@@ -93,6 +94,9 @@ def test_fwd_rejects_invalid_arguments_before_launch(lib):
     assert _fwd(lib, ws_bytes=100) == _lib.EINVAL
     assert b"workspace" in lib.cqgdn_last_error()
     assert _fwd(lib, q=ctypes.c_void_p(258)) == _lib.EINVAL  # misaligned
+    assert _fwd(lib, flags=_lib.PRECISE | _lib.TRAINING) == _lib.EINVAL
+    assert b"PRECISE" in lib.cqgdn_last_error()
+    assert _fwd(lib, flags=8) == _lib.EINVAL
 
 
 def test_recurrent_and_helpers_reject_invalid_arguments(lib):
