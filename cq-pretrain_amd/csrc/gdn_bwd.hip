@@ -54,18 +54,19 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
   {
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
-    const size_t row = ((size_t)(ci.start + t) * H + h) * D;
-    const float gt = gc[(size_t)(ci.start + (in ? t : ci.len - 1)) * H + h];
+    const int tc = clamp_row(t, ci.len);
+    const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
+    const float gt = gc[(size_t)(ci.start + tc) * H + h];
     if (p == 0) Gs[t] = gt;
     const float gam = __expf(gt);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      const bf16x8 xq = in ? ld8(qn + row + col) : zero8();
+      const bf16x8 xq = keep_if(in, ld8(qn + row + col));
       st8(Qs + t * LDK + col, xq);
-      st8(Ks + t * LDK + col, in ? ld8(kn + row + col) : zero8());
+      st8(Ks + t * LDK + col, keep_if(in, ld8(kn + row + col)));
       const f32x8 xg = cvtf8(xq) * gam;
-      const bf16x8 xd = in ? ld8(dout + row + col) : zero8();
+      const bf16x8 xd = keep_if(in, ld8(dout + row + col));
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
         QgT[(col + s) * LDT + t] = (bf16)xg[s];
@@ -369,22 +370,25 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
   bf16* dOs = reinterpret_cast<bf16*>(un);
   bf16* Vns = dOs + 64 * LDK;
   float* DQs = reinterpret_cast<float*>(un);
+  float rs_t;  // rsqrt norm of q at event t = tid / 4, loaded with the inputs
 
   {
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
-    const size_t row = ((size_t)(ci.start + t) * H + h) * D;
-    if (p == 0) Gs[t] = gc[(size_t)(ci.start + (in ? t : ci.len - 1)) * H + h];
+    const int tc = clamp_row(t, ci.len);
+    const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
+    if (p == 0) Gs[t] = gc[(size_t)(ci.start + tc) * H + h];
+    rs_t = normalize ? rq[(size_t)(ci.start + tc) * H + h] : 1.f;
     dgw[wave][lane] = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      const bf16x8 xq = in ? ld8(qn + row + col) : zero8();
-      const bf16x8 xk = in ? ld8(kn + row + col) : zero8();
+      const bf16x8 xq = keep_if(in, ld8(qn + row + col));
+      const bf16x8 xk = keep_if(in, ld8(kn + row + col));
       st8(Qs + t * LDK + col, xq);
       st8(Ks + t * LDK + col, xk);
-      st8(dOs + t * LDK + col, in ? ld8(dout + row + col) : zero8());
-      st8(Vns + t * LDK + col, in ? ld8(vnR + row + col) : zero8());
+      st8(dOs + t * LDK + col, keep_if(in, ld8(dout + row + col)));
+      st8(Vns + t * LDK + col, keep_if(in, ld8(vnR + row + col)));
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
         QnT[(col + s) * LDT + t] = xq[s];
@@ -539,9 +543,9 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       const int t = 16 * n + r;
-      const bf16* vrow = dVn + ((size_t)(ci.start + t) * H + h) * D;
+      const bf16* vrow = dVn + ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D;
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) av[n][kb] = (t < ci.len) ? neg8(ld8(vrow + 32 * kb + 8 * q4)) : zero8();
+      for (int kb = 0; kb < 4; ++kb) av[n][kb] = keep_if(t < ci.len, neg8(ld8(vrow + 32 * kb + 8 * q4)));
     }
     bf16* wt = dWT + cb * (D * CH);
 #pragma unroll
@@ -601,11 +605,10 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
     dot += __shfl_xor(dot, 1, 64);
     dot += __shfl_xor(dot, 2, 64);
     if (in) {
-      const float rs = normalize ? rq[(size_t)(ci.start + t) * H + h] : 1.f;
       const size_t row = ((size_t)(ci.start + t) * H + h) * D;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f32x8 out = normalize ? (dqn[j] - qv[j] * dot) * rs : dqn[j];
+        const f32x8 out = normalize ? (dqn[j] - qv[j] * dot) * rs_t : dqn[j];
         st8(dq + row + 32 * j + 8 * p, cvt8(out));
       }
     }
@@ -645,23 +648,26 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   __shared__ __attribute__((aligned(16))) float DKs[64 * LDQ];
   __shared__ float Gs[64], Bs[64];
   __shared__ float dgw[4][64], dbw[4][64];
+  float rs_t;  // rsqrt norm of k at event t = tid / 4, loaded with the inputs
 
   {
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
-    const size_t row = ((size_t)(ci.start + t) * H + h) * D;
+    const int tc = clamp_row(t, ci.len);
+    const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
     if (p == 0) {
-      Gs[t] = gc[(size_t)(ci.start + (in ? t : ci.len - 1)) * H + h];
-      Bs[t] = in ? beta[(size_t)(ci.start + t) * H + h] : 0.f;
+      Gs[t] = gc[(size_t)(ci.start + tc) * H + h];
+      Bs[t] = keep_if(in, beta[(size_t)(ci.start + tc) * H + h]);
     }
+    rs_t = normalize ? rk[(size_t)(ci.start + tc) * H + h] : 1.f;
     dgw[wave][lane] = 0.f;
     dbw[wave][lane] = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      const bf16x8 xk = in ? ld8(kn + row + col) : zero8();
+      const bf16x8 xk = keep_if(in, ld8(kn + row + col));
       st8(Ks + t * LDK + col, xk);
-      st8(Vs + t * LDK + col, in ? ld8(vin + row + col) : zero8());
+      st8(Vs + t * LDK + col, keep_if(in, ld8(vin + row + col)));
 #pragma unroll
       for (int s = 0; s < 8; ++s) KnT[(col + s) * LDT + t] = xk[s];
     }
@@ -693,10 +699,10 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int t = 16 * b + r;
-        const size_t row = ((size_t)(ci.start + t) * H + h) * D + 32 * kb + 8 * q4;
+        const size_t row = ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D + 32 * kb + 8 * q4;
         const bool in = t < ci.len;
-        acc[b] = mfma(ak, in ? ld8(dW + row) : zero8(), acc[b]);
-        acc[b] = mfma(av, in ? ld8(dVn + row) : zero8(), acc[b]);
+        acc[b] = mfma(ak, keep_if(in, ld8(dW + row)), acc[b]);
+        acc[b] = mfma(av, keep_if(in, ld8(dVn + row)), acc[b]);
       }
     }
 #pragma unroll
@@ -809,7 +815,8 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
         colB[n] += __expf(Gs[t]) * x;
         colG[n] += bg * x;
         f32x4 tot = ak[n] + aw[n] * bg;
-        if (t < ci.len) tot += *reinterpret_cast<const f32x4*>(dKp + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4);
+        tot += keep_if(t < ci.len, *reinterpret_cast<const f32x4*>(
+                                       dKp + ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D + 16 * m + 4 * q4));
         *reinterpret_cast<f32x4*>(DKs + t * LDQ + 16 * m + 4 * q4) = tot;
       }
     }
@@ -880,11 +887,10 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
     dot += __shfl_xor(dot, 1, 64);
     dot += __shfl_xor(dot, 2, 64);
     if (in) {
-      const float rs = normalize ? rk[(size_t)(ci.start + t) * H + h] : 1.f;
       const size_t row = ((size_t)(ci.start + t) * H + h) * D;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const f32x8 out = normalize ? (dkn[j] - kv[j] * dot) * rs : dkn[j];
+        const f32x8 out = normalize ? (dkn[j] - kv[j] * dot) * rs_t : dkn[j];
         st8(dk + row + 32 * j + 8 * p, cvt8(out));
       }
     }
@@ -892,7 +898,8 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   if (tid < 64) {
     const int t = tid;
     const bool in = t < ci.len;
-    float x = in ? dGp[(size_t)(ci.start + t) * H + h] + dgw[0][t] + dgw[1][t] + dgw[2][t] + dgw[3][t] : 0.f;
+    float x = keep_if(in, dGp[(size_t)(ci.start + clamp_row(t, ci.len)) * H + h] + dgw[0][t] + dgw[1][t] + dgw[2][t] +
+                              dgw[3][t]);
     // reverse (suffix) cumsum within the chunk
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {

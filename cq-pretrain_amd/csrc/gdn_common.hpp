@@ -178,6 +178,16 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
+// Rows past a tail chunk's length re-read the chunk's last row (always in bounds)
+// and are zeroed after the load.  A load issued under a condition is waited for
+// on its own (the compiler branches around it); unconditional loads of a phase
+// are all issued before the first wait.
+__device__ __forceinline__ int clamp_row(int t, int len) { return t < len ? t : len - 1; }
+template <class V>
+__device__ __forceinline__ V keep_if(bool in, V x) {
+  return in ? x : V{};
+}
+
 // Per-chunk metadata: chunk_table[c] = (start event, length).  A chunk never
 // crosses a document boundary; doc_chunk[d] .. doc_chunk[d+1] are the chunks of
 // document d, in time order.

@@ -57,8 +57,9 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
   if (wave == 0) {
     const int t = lane;
     const bool in = t < ci.len;
-    float gv = in ? g[(size_t)(ci.start + t) * H + h] : 0.f;
-    const float bv = in ? beta[(size_t)(ci.start + t) * H + h] : 0.f;
+    const size_t ev = (size_t)(ci.start + clamp_row(t, ci.len)) * H + h;
+    float gv = keep_if(in, g[ev]);
+    const float bv = keep_if(in, beta[ev]);
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const float o = __shfl_up(gv, off, 64);
@@ -75,7 +76,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
   {
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
-    const size_t row = ((size_t)(ci.start + t) * H + h) * D;
+    const size_t row = ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D;
     const float gam_t = __expf(Gs[t]);
     const float kdec_t = __expf(glast - Gs[t]);
     const float b_t = Bs[t];
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
     {
       f32x8 x[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = in ? cvtf8(ld8(q + row + 32 * j + 8 * p)) : f32x8{};
+      for (int j = 0; j < 4; ++j) x[j] = keep_if(in, cvtf8(ld8(q + row + 32 * j + 8 * p)));
       float rs = 1.f;
       if (NORMALIZE) {
         float ss = 0.f;
@@ -105,7 +106,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
     {
       f32x8 x[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = in ? cvtf8(ld8(k + row + 32 * j + 8 * p)) : f32x8{};
+      for (int j = 0; j < 4; ++j) x[j] = keep_if(in, cvtf8(ld8(k + row + 32 * j + 8 * p)));
       float rs = 1.f;
       if (NORMALIZE) {
         float ss = 0.f;
@@ -147,7 +148,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int col = 32 * j + 8 * p;
-        const f32x8 x = in ? cvtf8(ld8(v + row + col)) * (b_t * vs) : f32x8{};
+        const f32x8 x = keep_if(in, cvtf8(ld8(v + row + col)) * (b_t * vs));
 #pragma unroll
         for (int s = 0; s < 8; ++s) VbT[(col + s) * LDT + t] = (E)x[s];
       }
@@ -543,12 +544,12 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
   {
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
-    const size_t row = ((size_t)(ci.start + t) * H + h) * D;
+    const size_t row = ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      st8(Qs + t * LDK + col, in ? ld8(qn + row + col) : zero8v<E>());
-      st8(Ks + t * LDK + col, in ? ld8(kn + row + col) : zero8v<E>());
+      st8(Qs + t * LDK + col, keep_if(in, ld8(qn + row + col)));
+      st8(Ks + t * LDK + col, keep_if(in, ld8(kn + row + col)));
     }
     if (p == 0) Gs[t] = gc[(size_t)(ci.start + (in ? t : ci.len - 1)) * H + h];
   }

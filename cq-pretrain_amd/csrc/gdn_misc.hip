@@ -134,7 +134,7 @@ __global__ __launch_bounds__(64) void chunk_cumsum_kernel(const float* __restric
   const int c = blockIdx.x, h = blockIdx.y, t = threadIdx.x;
   const ChunkInfo ci = chunk_info(chunks, c);
   const bool in = t < ci.len;
-  float x = in ? g[(size_t)(ci.start + t) * H + h] : 0.f;
+  float x = keep_if(in, g[(size_t)(ci.start + clamp_row(t, ci.len)) * H + h]);
   if (reverse) {
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
