@@ -345,7 +345,7 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
 // ---------------------------------------------------------------------------
 // bwd_dqk
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void bwd_dqk_kernel(
+__global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
     const bf16* __restrict__ qn, const bf16* __restrict__ kn, const float* __restrict__ rq,
     const float* __restrict__ gc, const bf16* __restrict__ hR, const bf16* __restrict__ vnR,
     const bf16* __restrict__ dout, const bf16* __restrict__ dh, const bf16* __restrict__ dVn,
@@ -357,12 +357,11 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
 
+  // Q, K and dPm are also read transposed (ld8_tr), so no transposed copies are
+  // kept and two workgroups fit a CU's LDS
   __shared__ __attribute__((aligned(16))) bf16 Qs[64 * LDK];
   __shared__ __attribute__((aligned(16))) bf16 Ks[64 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 QnT[128 * LDT];
-  __shared__ __attribute__((aligned(16))) bf16 KnT[128 * LDT];
-  __shared__ __attribute__((aligned(16))) bf16 dPm[64 * LDT];   // [t][s]
-  __shared__ __attribute__((aligned(16))) bf16 dPmT[64 * LDT];  // [s][t]
+  __shared__ __attribute__((aligned(16))) bf16 dPm[64 * LDT];  // [t][s]
   __shared__ __attribute__((aligned(16))) uint8_t un[2 * 64 * LDK * 2];  // dOs | Vns, later DQs
   __shared__ float Gs[64];
   __shared__ float dgw[4][64];
@@ -371,6 +370,19 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
   bf16* Vns = dOs + 64 * LDK;
   float* DQs = reinterpret_cast<float*>(un);
   float rs_t;  // rsqrt norm of q at event t = tid / 4, loaded with the inputs
+
+  // Global operands are requested one phase ahead of their use, so the kernel
+  // pays about one memory round trip.  This wave's state fragments: rows
+  // k = 16 (2 wave + mm) + r of h (with the phase-0 rows) and of dS_{c+1}
+  // (before phase 2), value block kb (32 kb + 8 q4 .. + 8).  Together the four
+  // waves hold all of both, so <h, dS> needs no second read.
+  const bf16* hr = hR + cb * (D * D);
+  const bf16* dhc = dh + cb * (D * D);
+  bf16x8 bh[2][4], bd[2][4];
+#pragma unroll
+  for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) bh[mm][kb] = ld8(hr + (16 * (2 * wave + mm) + r) * D + 32 * kb + 8 * q4);
 
   {
     const int t = tid >> 2, p = tid & 3;
@@ -389,11 +401,6 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
       st8(Ks + t * LDK + col, xk);
       st8(dOs + t * LDK + col, keep_if(in, ld8(dout + row + col)));
       st8(Vns + t * LDK + col, keep_if(in, ld8(vnR + row + col)));
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        QnT[(col + s) * LDT + t] = xq[s];
-        KnT[(col + s) * LDT + t] = xk[s];
-      }
     }
   }
   __syncthreads();
@@ -431,7 +438,6 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) dPm[(16 * wave + 4 * q4 + i) * LDT + 16 * n + r] = (bf16)dpm[i];
-      st4(dPmT + (16 * n + r) * LDT + 16 * wave + 4 * q4, dpm);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -441,13 +447,12 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
   }
   __syncthreads();
 
-  // ---- phase 2: dQ (rows t, k-tiles 2w, 2w+1) ----
-  const bf16* hr = hR + cb * (D * D);
-  bf16x8 bh[2][4];  // h rows k (16m + r), value block kb
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) bh[mm][kb] = ld8(hr + (16 * (2 * wave + mm) + r) * D + 32 * kb + 8 * q4);
+    for (int kb = 0; kb < 4; ++kb) bd[mm][kb] = ld8(dhc + (16 * (2 * wave + mm) + r) * D + 32 * kb + 8 * q4);
+
+  // ---- phase 2: dQ (rows t, k-tiles 2w, 2w+1) ----
   f32x4 dQ[2][4];
   {
     f32x4 a1[2][4];
@@ -471,7 +476,7 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
         const bf16x8 a = ld8(dPm + (16 * n + r) * LDT + 32 * kb + 8 * q4);
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm)
-          dQ[mm][n] = mfma(a, ld8(KnT + (16 * (2 * wave + mm) + r) * LDT + 32 * kb + 8 * q4), dQ[mm][n]);
+          dQ[mm][n] = mfma(a, ld8_tr(Ks, LDK, 32 * kb, 16 * (2 * wave + mm)), dQ[mm][n]);
       }
     // dQ += scale * gam_t * (dO h^T); dG_t += sum_k Qn * that
 #pragma unroll
@@ -493,9 +498,21 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
     }
   }
 
+  // dVn rows for phase 4: copied global -> LDS asynchronously into the dO tile
+  // (free once every wave has finished phase 2) while phase 3 runs; rows of
+  // 16 16-byte columns, column c at c ^ (t & 15) (conflict-free fragment reads).
+  // Rows past the tail re-read row len-1; phase 4 zeroes them in registers.
+  __syncthreads();
+  bf16* dVs = dOs;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = 16 * i + wave * 4 + (lane >> 4), col = (lane & 15) ^ (t & 15);
+    dma16(dVn + ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D + 8 * col,
+          dVs + 128 * (16 * i + 4 * wave));
+  }
+
   // ---- phase 3: dK^T (k rows, t columns) ----
   {
-    const bf16* dhc = dh + cb * (D * D);
     float esum = 0.f;
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
@@ -505,18 +522,18 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
       for (int n = 0; n < 4; ++n) a3[n] = a4[n] = zero4();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = ld8(QnT + (16 * m + r) * LDT + 32 * kb + 8 * q4);
+        const bf16x8 a = ld8_tr(Qs, LDK, 32 * kb, 16 * m);
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
           if (n > 2 * kb + 1) continue;
-          a3[n] = mfma(a, ld8(dPmT + (16 * n + r) * LDT + 32 * kb + 8 * q4), a3[n]);
+          a3[n] = mfma(a, ld8_tr(dPm, LDT, 32 * kb, 16 * n), a3[n]);
         }
       }
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        const bf16x8 a = ld8(dhc + (16 * m + r) * D + 32 * kb + 8 * q4);
 #pragma unroll
-        for (int n = 0; n < 4; ++n) a4[n] = mfma(a, ld8(Vns + (16 * n + r) * LDK + 32 * kb + 8 * q4), a4[n]);
+        for (int n = 0; n < 4; ++n)
+          a4[n] = mfma(bd[mm][kb], ld8(Vns + (16 * n + r) * LDK + 32 * kb + 8 * q4), a4[n]);
       }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
@@ -535,47 +552,46 @@ __global__ __launch_bounds__(256) void bwd_dqk_kernel(
     }
     esum = sum16(esum);
     if (lane == 0) dg[ci.len - 1] += esum;
-  }
-
-  // ---- phase 4: dW = -dVn S^T  (both orientations) and <S, dS> ----
-  {
-    bf16x8 av[4][4];  // dVn rows t (16n + r), value block kb
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const int t = 16 * n + r;
-      const bf16* vrow = dVn + ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) av[n][kb] = keep_if(t < ci.len, neg8(ld8(vrow + 32 * kb + 8 * q4)));
-    }
-    bf16* wt = dWT + cb * (D * CH);
-#pragma unroll
-    for (int mm = 0; mm < 2; ++mm) {
-      const int m = 2 * wave + mm;
-#pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        f32x4 w1 = zero4(), w2 = zero4();
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          w1 = mfma(av[n][kb], bh[mm][kb], w1);  // dW[t][k]  (rows t)
-          w2 = mfma(bh[mm][kb], av[n][kb], w2);  // dW^T[k][t] (rows k)
-        }
-        st4(wt + (16 * m + r) * CH + 16 * n + 4 * q4, w1);
-        const int t = 16 * n + r;
-        if (t < ci.len) st4(dW + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4, w2);
-      }
-    }
-    const bf16* dhc = dh + cb * (D * D);
+    // <h, dS_{c+1}> over this wave's quarter of both
     float x = 0.f;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int off = 8 * tid + 2048 * j;
-      const f32x8 a = cvtf8(ld8(hr + off)), b = cvtf8(ld8(dhc + off));
+    for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-      for (int s = 0; s < 8; ++s) x += a[s] * b[s];
-    }
+      for (int kb = 0; kb < 4; ++kb) {
+        const f32x8 a = cvtf8(bh[mm][kb]), b = cvtf8(bd[mm][kb]);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) x += a[s] * b[s];
+      }
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
     if (lane == 0) red[wave] = x;
+  }
+
+  __syncthreads();  // the dVn copies have landed (the barrier waits for them)
+
+  // ---- phase 4: dW = -dVn S^T  (both orientations) and <S, dS> ----
+  {
+    bf16* wt = dWT + cb * (D * CH);
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const int t = 16 * n + r;
+      bf16x8 av[4];  // -dVn row t, value block kb
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+        av[kb] = keep_if(t < ci.len, neg8(ld8(dVs + t * 128 + 8 * ((4 * kb + q4) ^ (t & 15)))));
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        const int m = 2 * wave + mm;
+        f32x4 w1 = zero4(), w2 = zero4();
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          w1 = mfma(av[kb], bh[mm][kb], w1);  // dW[t][k]  (rows t)
+          w2 = mfma(bh[mm][kb], av[kb], w2);  // dW^T[k][t] (rows k)
+        }
+        st4(wt + (16 * m + r) * CH + 16 * n + 4 * q4, w1);
+        if (t < ci.len) st4(dW + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4, w2);
+      }
+    }
   }
   __syncthreads();  // all reads of dOs / Vns are done: DQs may overwrite them
 
@@ -650,6 +666,21 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   __shared__ float dgw[4][64], dbw[4][64];
   float rs_t;  // rsqrt norm of k at event t = tid / 4, loaded with the inputs
 
+  // Global operands are requested one phase ahead of their use.  With the
+  // inputs: this wave's rows t = 16 wave + r of dW and dVn (phase 1), and the
+  // dG partial of event tid (phase 5).
+  bf16x8 fdw[4], fdv[4];
+  {
+    const int t = 16 * wave + r;
+    const size_t row = ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D + 8 * q4;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      fdw[kb] = keep_if(t < ci.len, ld8(dW + row + 32 * kb));
+      fdv[kb] = keep_if(t < ci.len, ld8(dVn + row + 32 * kb));
+    }
+  }
+  const float dgp_t = keep_if(lane < ci.len, dGp[(size_t)(ci.start + clamp_row(lane, ci.len)) * H + h]);
+
   {
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
@@ -685,30 +716,52 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   float* dgl = dgw[wave];
   float* dbl = dbw[wave];
 
-  // ---- phase 1: dT^T (rows s = s-tile wave, columns t) -> S1 = dT[t][s] ----
+  // ---- phase 1: dT = dW (beta gam K)^T + dVn (beta V)^T, rows t = t-tile wave -> S1 = dT[t][s] ----
   {
-    const int s = 16 * wave + r;
-    const float fk = Bs[s] * __expf(Gs[s]), fv = Bs[s];
-    f32x4 acc[4];
+    f32x4 ak[4], av[4];
 #pragma unroll
-    for (int b = 0; b < 4; ++b) acc[b] = zero4();
+    for (int n = 0; n < 4; ++n) ak[n] = av[n] = zero4();
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const bf16x8 ak = cvt8(cvtf8(ld8(Ks + s * LDK + 32 * kb + 8 * q4)) * fk);
-      const bf16x8 av = cvt8(cvtf8(ld8(Vs + s * LDK + 32 * kb + 8 * q4)) * fv);
+    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int t = 16 * b + r;
-        const size_t row = ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D + 32 * kb + 8 * q4;
-        const bool in = t < ci.len;
-        acc[b] = mfma(ak, keep_if(in, ld8(dW + row)), acc[b]);
-        acc[b] = mfma(av, keep_if(in, ld8(dVn + row)), acc[b]);
+      for (int n = 0; n < 4; ++n) {
+        ak[n] = mfma(fdw[kb], ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4), ak[n]);
+        av[n] = mfma(fdv[kb], ld8(Vs + (16 * n + r) * LDK + 32 * kb + 8 * q4), av[n]);
       }
-    }
 #pragma unroll
-    for (int b = 0; b < 4; ++b) st4(S1 + (16 * b + r) * LDT + 16 * wave + 4 * q4, acc[b]);
+    for (int n = 0; n < 4; ++n) {
+      const int s = 16 * n + r;
+      const float fk = Bs[s] * __expf(Gs[s]), fv = Bs[s];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S1[(16 * wave + 4 * q4 + i) * LDT + s] = (bf16)(ak[n][i] * fk + av[n][i] * fv);
+    }
   }
   __syncthreads();
+
+  // phase-4 operands, requested before phase 2: rows k (or v) = 16 (2 wave + mm) + r
+  // of dW^T and dVn^T, and the dK partial rows t = 16 n + r at those columns
+  bf16x8 fwt[2][2], fvt[2][2];
+  f32x4 fkp[2][4];
+  {
+    const bf16* dwt = dWT + cb * (D * CH);
+    const bf16* dvt = dVnT + cb * (D * CH);
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      const int m = 2 * wave + mm;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        fwt[mm][kb] = ld8(dwt + (16 * m + r) * CH + 32 * kb + 8 * q4);
+        fvt[mm][kb] = ld8(dvt + (16 * m + r) * CH + 32 * kb + 8 * q4);
+      }
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const int t = 16 * n + r;
+        fkp[mm][n] = keep_if(t < ci.len, *reinterpret_cast<const f32x4*>(
+                                             dKp + ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D + 16 * m +
+                                             4 * q4));
+      }
+    }
+  }
 
   // ---- phase 2: Y = dT T^T (rows t = t-tile wave) -> S2 = Y^T[j][t] ----
   {
@@ -785,7 +838,6 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
 
   // ---- phase 4a: dK^T (k rows 2w, 2w+1; t columns) -> DKs[t][k] ----
   {
-    const bf16* dwt = dWT + cb * (D * CH);
     float colB[4] = {0.f, 0.f, 0.f, 0.f}, colG[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
@@ -796,7 +848,7 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const bf16x8 a = ld8(KnT + (16 * m + r) * LDT + 32 * kb + 8 * q4);
-        const bf16x8 w = ld8(dwt + (16 * m + r) * CH + 32 * kb + 8 * q4);
+        const bf16x8 w = fwt[mm][kb];
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
           if (n >= 2 * kb) ak[n] = mfma(a, ld8(S1 + (16 * n + r) * LDT + 32 * kb + 8 * q4), ak[n]);  // j < i
@@ -814,9 +866,7 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
         const float x = aw[n][0] * kk[0] + aw[n][1] * kk[1] + aw[n][2] * kk[2] + aw[n][3] * kk[3];
         colB[n] += __expf(Gs[t]) * x;
         colG[n] += bg * x;
-        f32x4 tot = ak[n] + aw[n] * bg;
-        tot += keep_if(t < ci.len, *reinterpret_cast<const f32x4*>(
-                                       dKp + ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D + 16 * m + 4 * q4));
+        const f32x4 tot = ak[n] + aw[n] * bg + fkp[mm][n];
         *reinterpret_cast<f32x4*>(DKs + t * LDQ + 16 * m + 4 * q4) = tot;
       }
     }
@@ -835,7 +885,6 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   }
   // ---- phase 4b: dV^T (v rows 2w, 2w+1; s columns): dv = beta (T^T dVn) ----
   {
-    const bf16* dvt = dVnT + cb * (D * CH);
     float colB[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
@@ -845,7 +894,7 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
       for (int n = 0; n < 4; ++n) acc[n] = zero4();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = ld8(dvt + (16 * m + r) * CH + 32 * kb + 8 * q4);
+        const bf16x8 a = fvt[mm][kb];
 #pragma unroll
         for (int n = 0; n < 4; ++n)
           if (kb >= 1 || n < 2) acc[n] = mfma(a, ld8(TTs + (16 * n + r) * LDT + 32 * kb + 8 * q4), acc[n]);
@@ -898,8 +947,7 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   if (tid < 64) {
     const int t = tid;
     const bool in = t < ci.len;
-    float x = keep_if(in, dGp[(size_t)(ci.start + clamp_row(t, ci.len)) * H + h] + dgw[0][t] + dgw[1][t] + dgw[2][t] +
-                              dgw[3][t]);
+    float x = keep_if(in, dgp_t + dgw[0][t] + dgw[1][t] + dgw[2][t] + dgw[3][t]);
     // reverse (suffix) cumsum within the chunk
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {

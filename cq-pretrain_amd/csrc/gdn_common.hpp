@@ -96,6 +96,24 @@ __device__ __forceinline__ bf16x8 ld8s(const bf16* p, int stride) {
 __device__ __forceinline__ void st4(bf16* p, f32x4 x) { *reinterpret_cast<bf16x4*>(p) = cvt4(x); }
 __device__ __forceinline__ void st8(bf16* p, bf16x8 x) { *reinterpret_cast<bf16x8*>(p) = x; }
 
+// Transposed fragment from a row-major LDS tile (row stride ld elements):
+// lane (q4, r) gets tile[k0 + 8 q4 + e][n0 + r], e = 0..7 -- the natural-map
+// operand for a contraction over the tile's row index.  Built from two
+// ds_read_b64_tr_b16: within each 16-lane group, lane a addresses the 4
+// elements tile[k0 + 8 q4 + 4 h + (a >> 2)][n0 + 4 (a & 3) ..], and the
+// instruction returns to lane j element e of the group's lane (j >> 2) + 4 e,
+// column j & 3 (the gfx950 layout, checked on the device).  tile must be in
+// LDS, ld and n0 multiples of 4.
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ bf16x8 ld8_tr(const bf16* tile, int ld, int k0, int n0) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
+  const bf16* p = tile + (k0 + 8 * q4 + (r >> 2)) * ld + n0 + 4 * (r & 3);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * ld));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // ---- fp16 operands ----------------------------------------------------------
 // The precise (inference) forward keeps its MFMA operands in fp16: 11 mantissa
 // bits instead of bf16's 8, at the same MFMA rate (v_mfma_f32_16x16x32_f16).
