@@ -653,18 +653,16 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
 
+  // K, T and beta*dM are also read transposed (ld8_tr) and dK stays in
+  // registers, so two workgroups fit a CU's LDS
   __shared__ __attribute__((aligned(16))) bf16 Ks[64 * LDK];
   __shared__ __attribute__((aligned(16))) bf16 Vs[64 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 KnT[128 * LDT];
-  __shared__ __attribute__((aligned(16))) bf16 Ts[64 * LDT];   // T[t][s]
-  __shared__ __attribute__((aligned(16))) bf16 TTs[64 * LDT];  // T^T[s][t]
-  __shared__ __attribute__((aligned(16))) bf16 S1[64 * LDT];   // dT[t][s], then beta*dM [i][j]
-  __shared__ __attribute__((aligned(16))) bf16 S2[64 * LDT];   // Y^T[j][t]
-  __shared__ __attribute__((aligned(16))) bf16 S3[64 * LDT];   // (beta*dM)^T [j][i]
-  __shared__ __attribute__((aligned(16))) float DKs[64 * LDQ];
+  __shared__ __attribute__((aligned(16))) bf16 Ts[64 * LDT];  // T[t][s]
+  __shared__ __attribute__((aligned(16))) bf16 S1[64 * LDT];  // dT[t][s], then beta*dM [i][j]
+  __shared__ __attribute__((aligned(16))) bf16 S2[64 * LDT];  // Y^T[j][t]
   __shared__ float Gs[64], Bs[64];
   __shared__ float dgw[4][64], dbw[4][64];
-  float rs_t;  // rsqrt norm of k at event t = tid / 4, loaded with the inputs
+  __shared__ float dkdot[4][64];  // per-wave parts of k_t . dK_t
 
   // Global operands are requested one phase ahead of their use.  With the
   // inputs: this wave's rows t = 16 wave + r of dW and dVn (phase 1), and the
@@ -690,26 +688,19 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
       Gs[t] = gc[(size_t)(ci.start + tc) * H + h];
       Bs[t] = keep_if(in, beta[(size_t)(ci.start + tc) * H + h]);
     }
-    rs_t = normalize ? rk[(size_t)(ci.start + tc) * H + h] : 1.f;
     dgw[wave][lane] = 0.f;
     dbw[wave][lane] = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      const bf16x8 xk = keep_if(in, ld8(kn + row + col));
-      st8(Ks + t * LDK + col, xk);
+      st8(Ks + t * LDK + col, keep_if(in, ld8(kn + row + col)));
       st8(Vs + t * LDK + col, keep_if(in, ld8(vin + row + col)));
-#pragma unroll
-      for (int s = 0; s < 8; ++s) KnT[(col + s) * LDT + t] = xk[s];
     }
     const bf16* tm = Tm + cb * (CH * CH);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int col = 32 * j + 8 * p;
-      const bf16x8 x = ld8(tm + t * CH + col);
-      st8(Ts + t * LDT + col, x);
-#pragma unroll
-      for (int s = 0; s < 8; ++s) TTs[(col + s) * LDT + t] = x[s];
+      st8(Ts + t * LDT + col, ld8(tm + t * CH + col));
     }
   }
   __syncthreads();
@@ -739,10 +730,15 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   __syncthreads();
 
   // phase-4 operands, requested before phase 2: rows k (or v) = 16 (2 wave + mm) + r
-  // of dW^T and dVn^T, and the dK partial rows t = 16 n + r at those columns
+  // of dW^T and dVn^T, the dK partial rows t = 16 n + r at those columns, and
+  // the rsqrt norms of k at those rows
   bf16x8 fwt[2][2], fvt[2][2];
   f32x4 fkp[2][4];
+  float rsn[4];
   {
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+      rsn[n] = normalize ? rk[(size_t)(ci.start + clamp_row(16 * n + r, ci.len)) * H + h] : 1.f;
     const bf16* dwt = dWT + cb * (D * CH);
     const bf16* dvt = dVnT + cb * (D * CH);
 #pragma unroll
@@ -786,7 +782,7 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
     const int kb0 = wave >= 2 ? 1 : 0;  // T[t][i] = 0 for t < i
     bf16x8 at[2], ak[4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) at[kb] = ld8(TTs + (16 * wave + r) * LDT + 32 * kb + 8 * q4);
+    for (int kb = 0; kb < 2; ++kb) at[kb] = ld8_tr(Ts, LDT, 32 * kb, 16 * wave);
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) ak[kb] = ld8(Ks + (16 * wave + r) * LDK + 32 * kb + 8 * q4);
     float rowB[4] = {0.f, 0.f, 0.f, 0.f}, rowE[4] = {0.f, 0.f, 0.f, 0.f};
@@ -822,7 +818,6 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) S1[(16 * wave + 4 * q4 + e) * LDT + 16 * n + r] = (bf16)dmp[e];
-      st4(S3 + (16 * n + r) * LDT + 16 * wave + 4 * q4, dmp);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -836,53 +831,6 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   }
   __syncthreads();
 
-  // ---- phase 4a: dK^T (k rows 2w, 2w+1; t columns) -> DKs[t][k] ----
-  {
-    float colB[4] = {0.f, 0.f, 0.f, 0.f}, colG[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int mm = 0; mm < 2; ++mm) {
-      const int m = 2 * wave + mm;
-      f32x4 ak[4], aw[4];
-#pragma unroll
-      for (int n = 0; n < 4; ++n) ak[n] = aw[n] = zero4();
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = ld8(KnT + (16 * m + r) * LDT + 32 * kb + 8 * q4);
-        const bf16x8 w = fwt[mm][kb];
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          if (n >= 2 * kb) ak[n] = mfma(a, ld8(S1 + (16 * n + r) * LDT + 32 * kb + 8 * q4), ak[n]);  // j < i
-          if (kb >= 1 || n < 2) {
-            ak[n] = mfma(a, ld8(S3 + (16 * n + r) * LDT + 32 * kb + 8 * q4), ak[n]);  // i > j
-            aw[n] = mfma(w, ld8(TTs + (16 * n + r) * LDT + 32 * kb + 8 * q4), aw[n]);  // t >= s
-          }
-        }
-      }
-#pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const int t = 16 * n + r;
-        const float bg = Bs[t] * __expf(Gs[t]);
-        const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
-        const float x = aw[n][0] * kk[0] + aw[n][1] * kk[1] + aw[n][2] * kk[2] + aw[n][3] * kk[3];
-        colB[n] += __expf(Gs[t]) * x;
-        colG[n] += bg * x;
-        const f32x4 tot = ak[n] + aw[n] * bg + fkp[mm][n];
-        *reinterpret_cast<f32x4*>(DKs + t * LDQ + 16 * m + 4 * q4) = tot;
-      }
-    }
-#pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      float xb = colB[n], xg = colG[n];
-      xb += __shfl_xor(xb, 16, 64);
-      xb += __shfl_xor(xb, 32, 64);
-      xg += __shfl_xor(xg, 16, 64);
-      xg += __shfl_xor(xg, 32, 64);
-      if (q4 == 0) {
-        dbl[16 * n + r] += xb;
-        dgl[16 * n + r] += xg;
-      }
-    }
-  }
   // ---- phase 4b: dV^T (v rows 2w, 2w+1; s columns): dv = beta (T^T dVn) ----
   {
     float colB[4] = {0.f, 0.f, 0.f, 0.f};
@@ -897,7 +845,7 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
         const bf16x8 a = fvt[mm][kb];
 #pragma unroll
         for (int n = 0; n < 4; ++n)
-          if (kb >= 1 || n < 2) acc[n] = mfma(a, ld8(TTs + (16 * n + r) * LDT + 32 * kb + 8 * q4), acc[n]);
+          if (kb >= 1 || n < 2) acc[n] = mfma(a, ld8_tr(Ts, LDT, 32 * kb, 16 * n), acc[n]);
       }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
@@ -915,33 +863,81 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
       if (q4 == 0) dbl[16 * n + r] += xb;
     }
   }
+
+  // ---- phase 4a: dK (rows t = 16n + r, k columns 16 (2w + mm) + 4 q4 ..) in registers ----
+  f32x4 dkr[2][4];
+  {
+    float colB[4] = {0.f, 0.f, 0.f, 0.f}, colG[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) {
+      const int m = 2 * wave + mm;
+      f32x4 ak[4], aw[4];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) ak[n] = aw[n] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const bf16x8 a = ld8_tr(Ks, LDK, 32 * kb, 16 * m);
+        const bf16x8 w = fwt[mm][kb];
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          if (n >= 2 * kb) ak[n] = mfma(a, ld8(S1 + (16 * n + r) * LDT + 32 * kb + 8 * q4), ak[n]);  // j < i
+          if (kb >= 1 || n < 2) {
+            ak[n] = mfma(a, ld8_tr(S1, LDT, 32 * kb, 16 * n), ak[n]);  // i > j
+            aw[n] = mfma(w, ld8_tr(Ts, LDT, 32 * kb, 16 * n), aw[n]);  // t >= s
+          }
+        }
+      }
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const int t = 16 * n + r;
+        const float bg = Bs[t] * __expf(Gs[t]);
+        const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
+        const float x = aw[n][0] * kk[0] + aw[n][1] * kk[1] + aw[n][2] * kk[2] + aw[n][3] * kk[3];
+        colB[n] += __expf(Gs[t]) * x;
+        colG[n] += bg * x;
+        dkr[mm][n] = ak[n] + aw[n] * bg + fkp[mm][n];
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      float xb = colB[n], xg = colG[n];
+      xb += __shfl_xor(xb, 16, 64);
+      xb += __shfl_xor(xb, 32, 64);
+      xg += __shfl_xor(xg, 16, 64);
+      xg += __shfl_xor(xg, 32, 64);
+      if (q4 == 0) {
+        dbl[16 * n + r] += xb;
+        dgl[16 * n + r] += xg;
+      }
+    }
+    // this wave's part of the row dots k_t . dK_t (its 32 columns of each row)
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const int t = 16 * n + r;
+      float pd = 0.f;
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * (2 * wave + mm) + 4 * q4));
+        pd += kk[0] * dkr[mm][n][0] + kk[1] * dkr[mm][n][1] + kk[2] * dkr[mm][n][2] + kk[3] * dkr[mm][n][3];
+      }
+      pd += __shfl_xor(pd, 16, 64);
+      pd += __shfl_xor(pd, 32, 64);
+      if (q4 == 0) dkdot[wave][t] = pd;
+    }
+  }
   __syncthreads();
 
-  // ---- phase 5: l2norm backward of dk; dg (reverse cumsum), dbeta ----
-  {
-    const int t = tid >> 2, p = tid & 3;
-    const bool in = t < ci.len;
-    f32x8 dkn[4], kv[4];
-    float dot = 0.f;
+  // ---- phase 5: l2norm backward of dk (dk = rk (dK - k (k . dK))); dg (reverse cumsum), dbeta ----
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = 32 * j + 8 * p;
-      const f32x4 lo = *reinterpret_cast<const f32x4*>(DKs + t * LDQ + col);
-      const f32x4 hi = *reinterpret_cast<const f32x4*>(DKs + t * LDQ + col + 4);
-      dkn[j] = f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      kv[j] = cvtf8(ld8(Ks + t * LDK + col));
+  for (int n = 0; n < 4; ++n) {
+    const int t = 16 * n + r;
+    const float dot = dkdot[0][t] + dkdot[1][t] + dkdot[2][t] + dkdot[3][t];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) dot += kv[j][s] * dkn[j][s];
-    }
-    dot += __shfl_xor(dot, 1, 64);
-    dot += __shfl_xor(dot, 2, 64);
-    if (in) {
-      const size_t row = ((size_t)(ci.start + t) * H + h) * D;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x8 out = normalize ? (dkn[j] - kv[j] * dot) * rs_t : dkn[j];
-        st8(dk + row + 32 * j + 8 * p, cvt8(out));
-      }
+    for (int mm = 0; mm < 2; ++mm) {
+      const int m = 2 * wave + mm;
+      const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
+      const f32x4 out = normalize ? (dkr[mm][n] - kk * dot) * rsn[n] : dkr[mm][n];
+      if (t < ci.len) st4(dk + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4, out);
     }
   }
   if (tid < 64) {
