@@ -49,7 +49,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
   __shared__ __attribute__((aligned(16))) E Ks[64 * LDK];
   __shared__ __attribute__((aligned(16))) E KbT[128 * LDT];
   __shared__ __attribute__((aligned(16))) E VbT[128 * LDT];
-  __shared__ float Af[64 * LDA];
+  __shared__ __attribute__((aligned(16))) float Af[64 * LDA];  // the solve's matrix, then the KgT tile
   __shared__ __attribute__((aligned(16))) E Ts[64 * LDT];
   const float vs = vscale ? *vscale : 1.f;
 
@@ -73,10 +73,22 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
   const float glast = Gs[ci.len - 1];
 
   // ---- rows: thread (t, p) owns columns 8p + 32j, j = 0..3 ----
+  // Kg = K exp(G_last - G) is kept in registers and leaves through LDS after the
+  // solve (coalesced rows of KgT instead of 2-byte scattered stores).
+  X8 kg8[4];
   {
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
     const size_t row = ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D;
+    // all row loads are issued before any store (a wait for a load also waits
+    // for every store issued before it)
+    bf16x8 lq[4], lk[4], lv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lq[j] = ld8(q + row + 32 * j + 8 * p);
+      lk[j] = ld8(k + row + 32 * j + 8 * p);
+      lv[j] = ld8(v + row + 32 * j + 8 * p);
+    }
     const float gam_t = __expf(Gs[t]);
     const float kdec_t = __expf(glast - Gs[t]);
     const float b_t = Bs[t];
@@ -84,7 +96,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
     {
       f32x8 x[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = keep_if(in, cvtf8(ld8(q + row + 32 * j + 8 * p)));
+      for (int j = 0; j < 4; ++j) x[j] = keep_if(in, cvtf8(lq[j]));
       float rs = 1.f;
       if (NORMALIZE) {
         float ss = 0.f;
@@ -106,7 +118,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
     {
       f32x8 x[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = keep_if(in, cvtf8(ld8(k + row + 32 * j + 8 * p)));
+      for (int j = 0; j < 4; ++j) x[j] = keep_if(in, cvtf8(lk[j]));
       float rs = 1.f;
       if (NORMALIZE) {
         float ss = 0.f;
@@ -118,7 +130,6 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
         ss += __shfl_xor(ss, 2, 64);
         rs = rsqrtf(ss + 1e-6f);
       }
-      E* kgt = KgT + cb * (D * CH);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const f32x8 xn = x[j] * rs;
@@ -133,13 +144,9 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
           *reinterpret_cast<X4*>(kp + 8) = __builtin_shufflevector(xb, xb, 4, 5, 6, 7);
         }
         const f32x8 xbg = xn * (b_t * gam_t);
-        const f32x8 xkd = xn * kdec_t;
-        const int tp = perm32(t);
+        kg8[j] = to8<E>(xn * kdec_t);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          KbT[(col + s) * LDT + t] = (E)xbg[s];
-          kgt[(col + s) * CH + tp] = (E)xkd[s];
-        }
+        for (int s = 0; s < 8; ++s) KbT[(col + s) * LDT + t] = (E)xbg[s];
       }
       if (in && p == 0) rk[(size_t)(ci.start + t) * H + h] = rs;
     }
@@ -148,7 +155,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int col = 32 * j + 8 * p;
-        const f32x8 x = keep_if(in, cvtf8(ld8(v + row + col)) * (b_t * vs));
+        const f32x8 x = keep_if(in, cvtf8(lv[j]) * (b_t * vs));
 #pragma unroll
         for (int s = 0; s < 8; ++s) VbT[(col + s) * LDT + t] = (E)x[s];
       }
@@ -180,31 +187,100 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
   }
   __syncthreads();
 
-  // ---- T = (I + A)^-1 by forward substitution: column c = tid/4, lanes p split the sum ----
+  // ---- T = (I + A)^-1, blocked by 16, in fp32 ----
+  // The four diagonal blocks by forward substitution (column c = tid/4 of block
+  // c/16, lanes p split the sums), then the blocks below the diagonal level by
+  // level (i - j = 1, 2, 3):  X_ij = sum_{k=j}^{i-1} A_ik T_kj,  T_ij = -T_ii X_ij.
+  // Af then holds T_ii in the diagonal blocks and T_ij^T (i > j) in block
+  // (j, i) above the diagonal (A's upper triangle is zero and unused); the
+  // blocks below the diagonal still hold A.
   {
-    const int col = tid >> 2, p = tid & 3;
-    float tc[16];
+    const int col = tid >> 2, p = tid & 3, b0 = col & ~15, lc = col & 15;
+    float tc[4];  // T[b0 + 4 jj + p][col]
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) tc[jj] = (4 * jj + p == col) ? 1.f : 0.f;
+    for (int jj = 0; jj < 4; ++jj) tc[jj] = (4 * jj + p == lc) ? 1.f : 0.f;
 #pragma unroll
-    for (int i = 1; i < 64; ++i) {
+    for (int i = 1; i < 16; ++i) {
       float part = 0.f;
 #pragma unroll
-      for (int jj = 0; jj <= (i - 1) / 4; ++jj) part += Af[i * LDA + 4 * jj + p] * tc[jj];
+      for (int jj = 0; jj < 4; ++jj) part += Af[(b0 + i) * LDA + b0 + 4 * jj + p] * tc[jj];
       part += __shfl_xor(part, 1, 64);
       part += __shfl_xor(part, 2, 64);
-      const float val = (i > col) ? -part : ((i == col) ? 1.f : 0.f);
+      const float val = (i > lc) ? -part : ((i == lc) ? 1.f : 0.f);
       if ((i & 3) == p) tc[i >> 2] = val;
     }
-    E* tm = Tm + cb * (CH * CH);
+    __syncthreads();  // every read of A's diagonal blocks is done
 #pragma unroll
-    for (int jj = 0; jj < 16; ++jj) {
-      const E b = (E)tc[jj];
-      Ts[(4 * jj + p) * LDT + col] = b;
-      tm[(4 * jj + p) * CH + col] = b;
+    for (int jj = 0; jj < 4; ++jj) Af[(b0 + 4 * jj + p) * LDA + col] = tc[jj];
+  }
+  {
+    const int a = tid >> 4, bc = tid & 15;  // element (a, bc) of a 16 x 16 block
+#pragma unroll
+    for (int d = 1; d < 4; ++d) {
+      __syncthreads();
+      float xv[3];
+#pragma unroll
+      for (int jb = 0; jb < 4 - d; ++jb) {  // target block (ib, jb) = (jb + d, jb)
+        const int ib = jb + d;
+        const float* arow = Af + (16 * ib + a) * LDA;
+        float x = 0.f;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) x += arow[16 * jb + c] * Af[(16 * jb + c) * LDA + 16 * jb + bc];
+#pragma unroll
+        for (int kb = jb + 1; kb < ib; ++kb)
+#pragma unroll
+          for (int c = 0; c < 16; ++c) x += arow[16 * kb + c] * Af[(16 * jb + bc) * LDA + 16 * kb + c];
+        xv[jb] = x;
+      }
+      // X goes to block (jb, ib), which no read of this level's first step touches
+#pragma unroll
+      for (int jb = 0; jb < 4 - d; ++jb) Af[(16 * jb + bc) * LDA + 16 * (jb + d) + a] = xv[jb];
+      __syncthreads();
+#pragma unroll
+      for (int jb = 0; jb < 4 - d; ++jb) {
+        const int ib = jb + d;
+        float y = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) y += Af[(16 * ib + a) * LDA + 16 * ib + e] * Af[(16 * jb + bc) * LDA + 16 * ib + e];
+        xv[jb] = -y;
+      }
+      __syncthreads();  // every read of X is done
+#pragma unroll
+      for (int jb = 0; jb < 4 - d; ++jb) Af[(16 * jb + bc) * LDA + 16 * (jb + d) + a] = xv[jb];
     }
   }
   __syncthreads();
+  {
+    // T in the operand type: Ts rows [t][s], then the global copy from those rows
+    const int col = tid >> 2, p = tid & 3, bcb = col >> 4;
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) {
+      const int t = 4 * jj + p, bt = t >> 4;
+      const float val = (bt == bcb) ? Af[t * LDA + col]
+                                    : (bt > bcb ? Af[(16 * bcb + (col & 15)) * LDA + 16 * bt + (t & 15)] : 0.f);
+      Ts[t * LDT + col] = (E)val;
+    }
+  }
+  __syncthreads();
+  {
+    E* tm = Tm + cb * (CH * CH);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int seg = 256 * i + tid, row = seg >> 3, part = seg & 7;
+      st8(tm + row * CH + 8 * part, ld8(Ts + row * LDT + 8 * part));
+    }
+  }
+
+  // Kg^T tile [k][perm32(t)] over the solve's matrix (free now), stored below
+  E* kgs = reinterpret_cast<E*>(Af);
+  static_assert(sizeof(Af) >= D * CH * sizeof(E), "the KgT tile must fit the solve matrix");
+  {
+    const int t = tid >> 2, p = tid & 3, tp = perm32(t);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int s = 0; s < 8; ++s) kgs[(32 * j + 8 * p + s) * CH + tp] = kg8[j][s];
+  }
 
   // ---- W (-> W^T storage), W^T (-> W rows), U (-> U^T storage) ----
   {
@@ -238,6 +314,15 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
         const int t = 16 * n + r;
         if (t < ci.len) st4(W + ((size_t)(ci.start + t) * H + h) * D + perm32(16 * m + 4 * q4), -acc);
       }
+    }
+  }
+  __syncthreads();
+  {
+    E* kgt = KgT + cb * (D * CH);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int seg = 256 * i + tid, kr = seg >> 3, part = seg & 7;
+      st8(kgt + kr * CH + 8 * part, ld8(kgs + kr * CH + 8 * part));
     }
   }
 }
