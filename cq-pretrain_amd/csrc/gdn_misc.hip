@@ -10,9 +10,13 @@ namespace cqgdn {
 // state is value-first [N][H][V][K] fp32 and is updated in place
 // (ops/gated_delta_net.py:314-352, math of models/decoding.py:71-77):
 //   S <- exp(g) S ;  r = (v - S k) * beta ;  S <- S + r k^T ;  o = scale * S q
-// One thread owns a quarter of a state row (32 fp32 = 8 float4, interleaved so a
-// wave's loads are contiguous); the row is read once and written once per call
-// whatever E is, which makes the step HBM-bound at 2 * 64 KB per (sequence, head).
+// Two workgroups per (sequence, head), 64 state rows each, read once and
+// written once per call whatever E is: the step is HBM-bound at 2 * 64 KB per
+// (sequence, head).  A wave owns 16 rows; lane l holds columns 4 (l % 32) .. + 3
+// of rows 2 jj + l / 32, so each load or store instruction of a wave covers
+// 1 KB of contiguous state (two whole rows), and the row dot products are
+// reduced over the 32 lanes of a row.  The state is streamed with
+// non-temporal accesses: it is not reused before the next call.
 // ---------------------------------------------------------------------------
 template <bool BETA_BF16>
 __global__ __launch_bounds__(256) void recurrent_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
@@ -22,42 +26,44 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const bf16* __restrict__
   const int blk = blockIdx.x;              // (n, h, half)
   const int half = blk & 1, nh = blk >> 1;  // nh = n * H + h
   const int n = nh / H, h = nh % H;
-  const int tid = threadIdx.x;
-  const int vrow = 64 * half + (tid >> 2), p = tid & 3;
-  float* srow = state + ((size_t)nh * D + vrow) * D;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c4 = lane & 31;                                    // columns 4 c4 .. 4 c4 + 3
+  const int rbase = 64 * half + 16 * wave + (lane >> 5);       // rows rbase + 2 jj
+  float* sblk = state + (size_t)nh * D * D;
   f32x4 s[8];
 #pragma unroll
-  for (int jj = 0; jj < 8; ++jj) s[jj] = *reinterpret_cast<const f32x4*>(srow + 4 * (p + 4 * jj));
+  for (int jj = 0; jj < 8; ++jj)
+    s[jj] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(sblk + (rbase + 2 * jj) * D + 4 * c4));
   for (int e = 0; e < E; ++e) {
     const size_t ev = ((size_t)n * E + e) * H + h;
-    const bf16* kr = k + ev * D;
-    const bf16* qr = q + ev * D;
     const float ge = __expf(g[ev]);
-    const float be = BETA_BF16 ? (float)reinterpret_cast<const bf16*>(beta)[ev] : reinterpret_cast<const float*>(beta)[ev];
-    f32x4 kk[8];
-    float dot = 0.f;
+    const float be =
+        BETA_BF16 ? (float)reinterpret_cast<const bf16*>(beta)[ev] : reinterpret_cast<const float*>(beta)[ev];
+    const f32x4 kk = cvtf4(ld4(k + ev * D + 4 * c4));
+    const f32x4 qq = cvtf4(ld4(q + ev * D + 4 * c4));
+    float vv[8], o[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) vv[jj] = (float)v[ev * D + rbase + 2 * jj];
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) {
-      kk[jj] = cvtf4(ld4(kr + 4 * (p + 4 * jj)));
       s[jj] *= ge;
-      dot += s[jj][0] * kk[jj][0] + s[jj][1] * kk[jj][1] + s[jj][2] * kk[jj][2] + s[jj][3] * kk[jj][3];
-    }
-    dot += __shfl_xor(dot, 1, 64);
-    dot += __shfl_xor(dot, 2, 64);
-    const float rv = ((float)v[ev * D + vrow] - dot) * be;
-    float o = 0.f;
+      float dot = s[jj][0] * kk[0] + s[jj][1] * kk[1] + s[jj][2] * kk[2] + s[jj][3] * kk[3];
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      s[jj] += kk[jj] * rv;
-      const f32x4 qq = cvtf4(ld4(qr + 4 * (p + 4 * jj)));
-      o += s[jj][0] * qq[0] + s[jj][1] * qq[1] + s[jj][2] * qq[2] + s[jj][3] * qq[3];
+      for (int off = 1; off < 32; off <<= 1) dot += __shfl_xor(dot, off, 64);
+      s[jj] += kk * ((vv[jj] - dot) * be);
+      float od = s[jj][0] * qq[0] + s[jj][1] * qq[1] + s[jj][2] * qq[2] + s[jj][3] * qq[3];
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) od += __shfl_xor(od, off, 64);
+      o[jj] = od;
     }
-    o += __shfl_xor(o, 1, 64);
-    o += __shfl_xor(o, 2, 64);
-    if (p == 0) out[ev * D + vrow] = (bf16)(o * scale);
+    if (c4 == 0) {
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) out[ev * D + rbase + 2 * jj] = (bf16)(o[jj] * scale);
+    }
   }
 #pragma unroll
-  for (int jj = 0; jj < 8; ++jj) *reinterpret_cast<f32x4*>(srow + 4 * (p + 4 * jj)) = s[jj];
+  for (int jj = 0; jj < 8; ++jj)
+    __builtin_nontemporal_store(s[jj], reinterpret_cast<f32x4*>(sblk + (rbase + 2 * jj) * D + 4 * c4));
 }
 
 void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* g, const void* beta,
