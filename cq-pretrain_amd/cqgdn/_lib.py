@@ -15,8 +15,8 @@ LIB_PATH = Path(__file__).resolve().with_name("libcqgdn.so")
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 NORMALIZE, TRAINING, PRECISE = 1, 2, 4
-FWD_BUFFERS, BWD_BUFFERS = 16, 10
-FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "WT", "UT", "KgT", "hT", "h", "vnT", "vn", "knP", "vscale")
+FWD_BUFFERS, BWD_BUFFERS = 15, 10
+FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "WT", "UT", "KgT", "hT", "h", "vnT", "knP", "vscale")
 BWD_NAMES = ("dvlT", "XT", "dh", "dVnT", "dVn", "dKp", "dW", "dWT", "dGp", "dhT")
 
 # every symbol include/cqgdn.h declares, with (restype, argtypes)
@@ -39,8 +39,7 @@ SIGNATURES = {
     "cqgdn_timer_arm": (_I, [ctypes.c_char_p, _I]),
     "cqgdn_timer_read": (_I, [_P, _I, _P]),
 }
-KERNELS = ("fwd_prep", "fwd_scan", "fwd_rows", "fwd_out", "bwd_local", "bwd_scan", "bwd_rows", "bwd_dqk", "bwd_wy",
-           "recurrent")
+KERNELS = ("fwd_prep", "fwd_scan", "fwd_out", "bwd_local", "bwd_scan", "bwd_rows", "bwd_dqk", "bwd_wy", "recurrent")
 
 _LIB = None
 

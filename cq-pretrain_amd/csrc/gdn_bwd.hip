@@ -347,7 +347,7 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
     const bf16* __restrict__ qn, const bf16* __restrict__ kn, const float* __restrict__ rq,
-    const float* __restrict__ gc, const bf16* __restrict__ hR, const bf16* __restrict__ vnR,
+    const float* __restrict__ gc, const bf16* __restrict__ hR, const bf16* __restrict__ vnT,
     const bf16* __restrict__ dout, const bf16* __restrict__ dh, const bf16* __restrict__ dVn,
     const int32_t* __restrict__ chunks, int H, float scale, int normalize, bf16* __restrict__ dq,
     float* __restrict__ dKp, bf16* __restrict__ dW, bf16* __restrict__ dWT, float* __restrict__ dGp) {
@@ -362,12 +362,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
   __shared__ __attribute__((aligned(16))) bf16 Qs[64 * LDK];
   __shared__ __attribute__((aligned(16))) bf16 Ks[64 * LDK];
   __shared__ __attribute__((aligned(16))) bf16 dPm[64 * LDT];  // [t][s]
-  __shared__ __attribute__((aligned(16))) uint8_t un[2 * 64 * LDK * 2];  // dOs | Vns, later DQs
+  __shared__ __attribute__((aligned(16))) uint8_t un[(64 * LDK + 128 * LDT) * 2];  // dOs | VnT, later DQs
   __shared__ float Gs[64];
   __shared__ float dgw[4][64];
   __shared__ float red[4];
   bf16* dOs = reinterpret_cast<bf16*>(un);
-  bf16* Vns = dOs + 64 * LDK;
+  bf16* VnT = dOs + 64 * LDK;  // v_new^T [v][t], read transposed as v_new rows
   float* DQs = reinterpret_cast<float*>(un);
   float rs_t;  // rsqrt norm of q at event t = tid / 4, loaded with the inputs
 
@@ -391,6 +391,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
     const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
     if (p == 0) Gs[t] = gc[(size_t)(ci.start + tc) * H + h];
     rs_t = normalize ? rq[(size_t)(ci.start + tc) * H + h] : 1.f;
+    // v_new^T tile (columns past a tail chunk's length are zero in the forward's tile)
+    const bf16* vt = vnT + cb * (D * CH);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int seg = 256 * i + tid, v = seg >> 3, part = seg & 7;
+      st8(VnT + v * LDT + 8 * part, ld8(vt + v * CH + 8 * part));
+    }
     dgw[wave][lane] = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -400,7 +407,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
       st8(Qs + t * LDK + col, xq);
       st8(Ks + t * LDK + col, xk);
       st8(dOs + t * LDK + col, keep_if(in, ld8(dout + row + col)));
-      st8(Vns + t * LDK + col, keep_if(in, ld8(vnR + row + col)));
+
     }
   }
   __syncthreads();
@@ -419,7 +426,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
         for (int kb = 0; kb < 4; ++kb) {
           p = mfma(ld8(Qs + (16 * wave + r) * LDK + 32 * kb + 8 * q4), ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4), p);
           dp = mfma(ld8(dOs + (16 * wave + r) * LDK + 32 * kb + 8 * q4),
-                    ld8(Vns + (16 * n + r) * LDK + 32 * kb + 8 * q4), dp);
+                    ld8_tr(VnT, LDT, 32 * kb, 16 * n), dp);
         }
         const int s = 16 * n + r;
         float colE = 0.f;
@@ -533,7 +540,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
       for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
         for (int n = 0; n < 4; ++n)
-          a4[n] = mfma(bd[mm][kb], ld8(Vns + (16 * n + r) * LDK + 32 * kb + 8 * q4), a4[n]);
+          a4[n] = mfma(bd[mm][kb], ld8_tr(VnT, LDT, 32 * kb, 16 * n), a4[n]);
       }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
@@ -593,7 +600,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
       }
     }
   }
-  __syncthreads();  // all reads of dOs / Vns are done: DQs may overwrite them
+  __syncthreads();  // all reads of dOs / VnT are done: DQs may overwrite them
 
   // ---- phase 5: l2norm backward of dq, dG partial ----
 #pragma unroll
@@ -978,7 +985,7 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
   {
     TimedLaunch tl(K_BWD_DQK, stream);
     hipLaunchKernelGGL(bwd_dqk_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_GC),
-                       F(F_HR), F(F_VN), a.dout, B(B_DH), B(B_DVN), a.chunks, a.H, a.scale, (int)a.normalize, a.dq,
+                       F(F_HR), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.chunks, a.H, a.scale, (int)a.normalize, a.dq,
                        Bf(B_DKP), B(B_DW), B(B_DWT), Bf(B_DGP));
   }
   TimedLaunch tl(K_BWD_WY, stream);

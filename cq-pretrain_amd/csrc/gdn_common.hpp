@@ -167,6 +167,17 @@ __device__ __forceinline__ typename Vec<E>::x8 pack_permv(f32x4 lo, f32x4 hi) {
   return to8<E>(f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
 }
 
+// ld8_tr for either operand element type
+template <class E>
+__device__ __forceinline__ typename Vec<E>::x8 ld8_trv(const E* tile, int ld, int k0, int n0) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
+  const E* p = tile + (k0 + 8 * q4 + (r >> 2)) * ld + n0 + 4 * (r & 3);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * ld));
+  return __builtin_bit_cast(typename Vec<E>::x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // ---- workgroup synchronization for loader/consumer kernels ----------------
 // Barrier that orders LDS only: waits for this wave's LDS operations, then
 // s_barrier.  __syncthreads() also waits for every outstanding vector-memory

@@ -11,7 +11,6 @@ namespace cqgdn {
 enum KernelId {
   K_FWD_PREP,
   K_FWD_SCAN,
-  K_FWD_ROWS,
   K_FWD_OUT,
   K_BWD_LOCAL,
   K_BWD_SCAN,
