@@ -44,12 +44,17 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
 
-  __shared__ __attribute__((aligned(16))) bf16 Qs[64 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 Ks[64 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 QgT[128 * LDT];
-  __shared__ __attribute__((aligned(16))) bf16 dOT[128 * LDT];
+  // The outputs are staged in LDS (over the input tiles, once those are read)
+  // and stored as whole rows: X^T over QgT | dOT, dv_local^T over Qs | Ks.
+  __shared__ __attribute__((aligned(16))) bf16 QK[2 * 64 * LDK];        // Qs | Ks, then dv_local^T [v][s]
+  __shared__ __attribute__((aligned(16))) bf16 QgdO[2 * 128 * LDT];     // QgT | dOT, then X^T [v][k]
   __shared__ __attribute__((aligned(16))) bf16 PTs[64 * LDT];
   __shared__ float Gs[64];
+  bf16* Qs = QK;
+  bf16* Ks = QK + 64 * LDK;
+  bf16* QgT = QgdO;
+  bf16* dOT = QgdO + 128 * LDT;
+  static_assert(2 * 64 * LDK >= 128 * LDT && 2 * 128 * LDT >= 128 * LDK, "output tiles fit the input tiles");
 
   {
     const int t = tid >> 2, p = tid & 3;
@@ -97,37 +102,59 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
   __syncthreads();
 
   // dv_local^T: rows s = s-tile wave, 8 value tiles; only t >= s contributes
+  f32x4 dvl[8];
   {
-    bf16* out = dvlT + cb * (D * CH);
     const int kb0 = wave >= 2 ? 1 : 0;
     bf16x8 a[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) a[kb] = ld8(PTs + (16 * wave + r) * LDT + 32 * kb + 8 * q4);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
-      f32x4 acc = zero4();
+      dvl[n] = zero4();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
-        if (kb >= kb0) acc = mfma(a[kb], ld8(dOT + (16 * n + r) * LDT + 32 * kb + 8 * q4), acc);
-      st4(out + (16 * n + r) * CH + 16 * wave + 4 * q4, acc * scale);
+        if (kb >= kb0) dvl[n] = mfma(a[kb], ld8(dOT + (16 * n + r) * LDT + 32 * kb + 8 * q4), dvl[n]);
     }
   }
   // X^T: k-tiles 2w, 2w+1 x 8 value tiles
+  f32x4 xt[2][8];
+#pragma unroll
+  for (int mm = 0; mm < 2; ++mm) {
+    const int m = 2 * wave + mm;
+    bf16x8 a[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) a[kb] = ld8(QgT + (16 * m + r) * LDT + 32 * kb + 8 * q4);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      xt[mm][n] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) xt[mm][n] = mfma(a[kb], ld8(dOT + (16 * n + r) * LDT + 32 * kb + 8 * q4), xt[mm][n]);
+    }
+  }
+  __syncthreads();  // the input tiles are read: they take the output tiles
+  bf16* dvs = QK;     // dv_local^T [v][s], row stride LDT
+  bf16* xts = QgdO;   // X^T [v][k], row stride LDK
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    st4(dvs + (16 * n + r) * LDT + 16 * wave + 4 * q4, dvl[n] * scale);
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) st4(xts + (16 * n + r) * LDK + 16 * (2 * wave + mm) + 4 * q4, xt[mm][n] * scale);
+  }
+  __syncthreads();
+  {
+    bf16* out = dvlT + cb * (D * CH);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int seg = 256 * i + tid, v = seg >> 3, part = seg & 7;
+      st8(out + v * CH + 8 * part, ld8(dvs + v * LDT + 8 * part));
+    }
+  }
   {
     bf16* out = XT + cb * (D * D);
 #pragma unroll
-    for (int mm = 0; mm < 2; ++mm) {
-      const int m = 2 * wave + mm;
-      bf16x8 a[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) a[kb] = ld8(QgT + (16 * m + r) * LDT + 32 * kb + 8 * q4);
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) acc = mfma(a[kb], ld8(dOT + (16 * n + r) * LDT + 32 * kb + 8 * q4), acc);
-        st4(out + (16 * n + r) * D + 16 * m + 4 * q4, acc * scale);
-      }
+    for (int i = 0; i < 8; ++i) {
+      const int seg = 256 * i + tid, v = seg >> 4, part = seg & 15;
+      st8(out + v * D + 8 * part, ld8(xts + v * LDK + 8 * part));
     }
   }
 }
