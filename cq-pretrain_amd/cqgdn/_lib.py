@@ -15,9 +15,9 @@ LIB_PATH = Path(__file__).resolve().with_name("libcqgdn.so")
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 NORMALIZE, TRAINING, PRECISE = 1, 2, 4
-FWD_BUFFERS, BWD_BUFFERS = 15, 10
+FWD_BUFFERS, BWD_BUFFERS = 15, 8
 FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "WT", "UT", "KgT", "hT", "h", "vnT", "knP", "vscale")
-BWD_NAMES = ("dvlT", "XT", "dh", "dVnT", "dVn", "dKp", "dW", "dWT", "dGp", "dhT")
+BWD_NAMES = ("dvlT", "XT", "dh", "dVn", "dKp", "dW", "dWT", "dGp")
 
 # every symbol include/cqgdn.h declares, with (restype, argtypes)
 _P, _I, _I64, _U, _F, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint, ctypes.c_float, ctypes.c_size_t
@@ -39,7 +39,7 @@ SIGNATURES = {
     "cqgdn_timer_arm": (_I, [ctypes.c_char_p, _I]),
     "cqgdn_timer_read": (_I, [_P, _I, _P]),
 }
-KERNELS = ("fwd_prep", "fwd_scan", "fwd_out", "bwd_local", "bwd_scan", "bwd_rows", "bwd_dqk", "bwd_wy", "recurrent")
+KERNELS = ("fwd_prep", "fwd_scan", "fwd_out", "bwd_local", "bwd_scan", "bwd_dqk", "bwd_wy", "recurrent")
 
 _LIB = None
 

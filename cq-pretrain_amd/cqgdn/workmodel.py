@@ -16,7 +16,6 @@ split over the kernels by the contractions each one performs:
   bwd_scan   dS += W^T dv_new, dv_new += Kg dS                              4 c d^2
   bwd_dqk    dP, dQ and dK from P, dQ from S, dK from dS, dW = -dv_new S^T  6 c^2 d + 6 c d^2
   bwd_wy     dT (2), d(beta gamma K), d(beta V), dA = -T^T dT T^T, dK from dA  12 c^2 d + 4 c^3
-  bwd_rows   layout transposes of dS and dv_new, no FLOPs
 
 HBM bytes are the kernel's declared inputs and outputs, each read or written
 once, in the workspace layouts of gdn_layout.hpp: event-indexed rows scale with
@@ -36,7 +35,7 @@ PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA
 PEAK_HBM_BYTES = 8.0e12  # MI355X HBM3E
 
 FWD_KERNELS = ("fwd_prep", "fwd_scan", "fwd_out")
-BWD_KERNELS = ("bwd_local", "bwd_scan", "bwd_rows", "bwd_dqk", "bwd_wy")
+BWD_KERNELS = ("bwd_local", "bwd_scan", "bwd_dqk", "bwd_wy")
 SCAN_KERNELS = ("fwd_scan", "bwd_scan")
 
 
@@ -57,7 +56,6 @@ def flops_per_chunk(kernel, c, d=D):
         "fwd_out": 2 * cd2 + 4 * c2d,
         "bwd_local": 2 * c2d + 2 * cd2,
         "bwd_scan": 4 * cd2,
-        "bwd_rows": 0,
         "bwd_dqk": 6 * c2d + 6 * cd2,
         "bwd_wy": 12 * c2d + 4 * c3,
     }[kernel]
@@ -80,14 +78,12 @@ def bytes_per_chunk(kernel, c, d=D):
         "fwd_out": 2 * e + s + sq + tile + e + sq,
         # qn, kn, dO, gcum -> dv_local^T, X^T
         "bwd_local": 3 * e + s + tile + sq,
-        # Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh^T, dv_new^T
-        "bwd_scan": e + s + tile + sq + tile + sq + tile,
-        # dh^T, dv_new^T -> dh rows, dv_new rows
-        "bwd_rows": 2 * sq + tile + e,
+        # Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh (slice-major), dv_new^T, dv_new (slice-major)
+        "bwd_scan": e + s + tile + sq + tile + sq + tile + tile,
         # qn, kn, rq, gcum, h rows, v_new^T, dO, dh, dv_new -> dq, dK partial (fp32), dW, dW^T, dG partial
-        "bwd_dqk": 2 * e + 2 * s + sq + tile + e + sq + e + e + e32 + e + tile + s,
+        "bwd_dqk": 2 * e + 2 * s + sq + tile + e + sq + tile + e + e32 + e + tile + s,
         # kn, v, beta, gcum, rk, T, dW, dW^T, dv_new, dv_new^T, dK partial, dG partial -> dk, dv, dg, dbeta
-        "bwd_wy": e + e + 3 * s + tm + e + tile + e + tile + e32 + s + 2 * e + 2 * s,
+        "bwd_wy": e + e + 3 * s + tm + e + tile + tile + tile + e32 + s + 2 * e + 2 * s,
     }[kernel]
 
 

@@ -237,26 +237,24 @@ __device__ __forceinline__ void bwd_fix_tail(BwdStage& S, const int32_t* __restr
   }
 }
 
-// scratch of one step -> dS^T rows [v0..v0+15][k], dVn^T rows [v0..v0+15][t]
-__device__ __forceinline__ void bwd_copy_out(const BwdScratch& sc, int c, int H, int h, int v0, int lane,
-                                             bf16* __restrict__ dhT, bf16* __restrict__ dVnT) {
+// scratch of one step -> dS_{c+1} and dVn in value-slice-major blocks (the
+// slice's [k][16] and [t][16], read transposed from the [v][k] / [v][t] scratch)
+__device__ __forceinline__ void bwd_copy_out(const BwdScratch& sc, int c, int H, int h, int slice, int lane,
+                                             bf16* __restrict__ dhS, bf16* __restrict__ dVnS) {
   const size_t cb = (size_t)c * H + h;
+  const int r = lane & 15, q4 = lane >> 4, half = 8 * (q4 & 1), row = 16 * (q4 >> 1) + r;
+  bf16* ds = dhS + cb * (D * D) + slice * (D * 16);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int seg = 64 * i + lane, v = seg >> 4, ks = seg & 15;
-    st8(dhT + cb * (D * D) + (v0 + v) * D + 8 * ks, ld8(sc.s + v * BS_SROW + 8 * ks));
-  }
+  for (int i = 0; i < 4; ++i) st8(ds + (32 * i + row) * 16 + half, ld8_tr16(sc.s, BS_SROW, 32 * i));
+  bf16* vs = dVnS + cb * (CH * D) + slice * (CH * 16);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int seg = 64 * i + lane, v = seg >> 3, ts = seg & 7;
-    st8(dVnT + cb * (D * CH) + (v0 + v) * CH + 8 * ts, ld8(sc.v + v * BS_VROW + 8 * ts));
-  }
+  for (int i = 0; i < 2; ++i) st8(vs + (32 * i + row) * 16 + half, ld8_tr16(sc.v, BS_VROW, 32 * i));
 }
 
 __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
     const bf16* __restrict__ knP, const float* __restrict__ gc, const bf16* __restrict__ dvlT,
     const bf16* __restrict__ XT, const bf16* __restrict__ WT, const int32_t* __restrict__ chunks,
-    const int32_t* __restrict__ doc_chunk, int H, bf16* __restrict__ dhT, bf16* __restrict__ dVnT) {
+    const int32_t* __restrict__ doc_chunk, int H, bf16* __restrict__ dhS, bf16* __restrict__ dVnS) {
   const int h = blockIdx.x % H, slice = blockIdx.x / H, d = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q4 = lane >> 4;
@@ -358,14 +356,15 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
           wait_vmem_all();
           bwd_fix_tail(stage[xn & (BS_STAGES - 1)], chunks, c_end - 1 - xn, lane);
         }
-        if (xo >= 0) bwd_copy_out(bwd_scratch(stage[xo & (BS_STAGES - 1)]), c_end - 1 - xo, H, h, v0, lane, dhT, dVnT);
+        if (xo >= 0)
+          bwd_copy_out(bwd_scratch(stage[xo & (BS_STAGES - 1)]), c_end - 1 - xo, H, h, slice, lane, dhS, dVnS);
         if (xi < n)
           bwd_issue(stage[xi & (BS_STAGES - 1)], chunks, c_end - 1 - xi, H, h, v0, lane, knP, gc, dvlT, XT, WT);
       }
       lds_barrier();
     }
     if (n > 0 && (n & 1) == j)
-      bwd_copy_out(bwd_scratch(stage[(n - 1) & (BS_STAGES - 1)]), c_end - n, H, h, v0, lane, dhT, dVnT);
+      bwd_copy_out(bwd_scratch(stage[(n - 1) & (BS_STAGES - 1)]), c_end - n, H, h, slice, lane, dhS, dVnS);
   }
 }
 
@@ -484,7 +483,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) bd[mm][kb] = ld8(dhc + (16 * (2 * wave + mm) + r) * D + 32 * kb + 8 * q4);
+    for (int kb = 0; kb < 4; ++kb)
+      bd[mm][kb] = ld8(dhc + (2 * kb + (q4 >> 1)) * (D * 16) + (16 * (2 * wave + mm) + r) * 16 + 8 * (q4 & 1));
 
   // ---- phase 2: dQ (rows t, k-tiles 2w, 2w+1) ----
   f32x4 dQ[2][4];
@@ -532,17 +532,15 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
     }
   }
 
-  // dVn rows for phase 4: copied global -> LDS asynchronously into the dO tile
-  // (free once every wave has finished phase 2) while phase 3 runs; rows of
-  // 16 16-byte columns, column c at c ^ (t & 15) (conflict-free fragment reads).
-  // Rows past the tail re-read row len-1; phase 4 zeroes them in registers.
+  // dVn for phase 4: its value-slice-major tile is copied global -> LDS
+  // asynchronously into the dO tile (free once every wave has finished phase 2)
+  // while phase 3 runs.  Fragment reads of it are contiguous 512-byte runs.
   __syncthreads();
   bf16* dVs = dOs;
+  {
+    const bf16* dvs = dVn + cb * (CH * D);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = 16 * i + wave * 4 + (lane >> 4), col = (lane & 15) ^ (t & 15);
-    dma16(dVn + ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D + 8 * col,
-          dVs + 128 * (16 * i + 4 * wave));
+    for (int i = 0; i < 4; ++i) dma16(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
   }
 
   // ---- phase 3: dK^T (k rows, t columns) ----
@@ -612,7 +610,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
       bf16x8 av[4];  // -dVn row t, value block kb
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
-        av[kb] = keep_if(t < ci.len, neg8(ld8(dVs + t * 128 + 8 * ((4 * kb + q4) ^ (t & 15)))));
+        av[kb] = keep_if(t < ci.len, neg8(ld8(dVs + (2 * kb + (q4 >> 1)) * (CH * 16) + t * 16 + 8 * (q4 & 1))));
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
         const int m = 2 * wave + mm;
@@ -678,7 +676,7 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
     const bf16* __restrict__ kn, const bf16* __restrict__ vin, const float* __restrict__ beta,
     const float* __restrict__ gc, const float* __restrict__ rk, const bf16* __restrict__ Tm,
     const bf16* __restrict__ dW, const bf16* __restrict__ dWT, const bf16* __restrict__ dVn,
-    const bf16* __restrict__ dVnT, const float* __restrict__ dKp, const float* __restrict__ dGp,
+    const float* __restrict__ dKp, const float* __restrict__ dGp,
     const int32_t* __restrict__ chunks, int H, int normalize, bf16* __restrict__ dk, bf16* __restrict__ dv,
     float* __restrict__ dg, float* __restrict__ dbeta) {
   const int c = blockIdx.x, h = blockIdx.y;
@@ -708,7 +706,7 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       fdw[kb] = keep_if(t < ci.len, ld8(dW + row + 32 * kb));
-      fdv[kb] = keep_if(t < ci.len, ld8(dVn + row + 32 * kb));
+      fdv[kb] = keep_if(t < ci.len, ld8(dVn + cb * (CH * D) + (2 * kb + (q4 >> 1)) * (CH * 16) + t * 16 + 8 * (q4 & 1)));
     }
   }
   const float dgp_t = keep_if(lane < ci.len, dGp[(size_t)(ci.start + clamp_row(lane, ci.len)) * H + h]);
@@ -765,7 +763,9 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
 
   // phase-4 operands, requested before phase 2: rows k (or v) = 16 (2 wave + mm) + r
   // of dW^T and dVn^T, the dK partial rows t = 16 n + r at those columns, and
-  // the rsqrt norms of k at those rows
+  // the rsqrt norms of k at those rows.  dVn^T fragments (8 events of one value)
+  // are gathered from the value-slice-major dVn tile with 2-byte loads; each
+  // load instruction reads 4 runs of 32 bytes.
   bf16x8 fwt[2][2], fvt[2][2];
   f32x4 fkp[2][4];
   float rsn[4];
@@ -774,14 +774,18 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
     for (int n = 0; n < 4; ++n)
       rsn[n] = normalize ? rk[(size_t)(ci.start + clamp_row(16 * n + r, ci.len)) * H + h] : 1.f;
     const bf16* dwt = dWT + cb * (D * CH);
-    const bf16* dvt = dVnT + cb * (D * CH);
+    const unsigned short* dvs = reinterpret_cast<const unsigned short*>(dVn + cb * (CH * D));
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const int m = 2 * wave + mm;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         fwt[mm][kb] = ld8(dwt + (16 * m + r) * CH + 32 * kb + 8 * q4);
-        fvt[mm][kb] = ld8(dvt + (16 * m + r) * CH + 32 * kb + 8 * q4);
+        const unsigned short* p = dvs + m * (CH * 16) + (32 * kb + 8 * q4) * 16 + r;  // slice m, value r, event 32 kb + 8 q4
+        u16x8 x;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = p[16 * e];
+        fvt[mm][kb] = __builtin_bit_cast(bf16x8, x);
       }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
@@ -1006,9 +1010,8 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
   {
     TimedLaunch tl(K_BWD_SCAN, stream);
     hipLaunchKernelGGL(bwd_scan_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, F(F_KNP),
-                       Ff(F_GC), B(B_DVLT), B(B_XT), F(F_WT), a.chunks, a.doc_chunk, a.H, B(B_DHT), B(B_DVNT));
+                       Ff(F_GC), B(B_DVLT), B(B_XT), F(F_WT), a.chunks, a.doc_chunk, a.H, B(B_DH), B(B_DVN));
   }
-  launch_rows(B(B_DHT), B(B_DVNT), a.chunks, a.n_chunks, a.H, B(B_DH), B(B_DVN), K_BWD_ROWS, stream);
   {
     TimedLaunch tl(K_BWD_DQK, stream);
     hipLaunchKernelGGL(bwd_dqk_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_GC),
@@ -1017,7 +1020,7 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
   }
   TimedLaunch tl(K_BWD_WY, stream);
   hipLaunchKernelGGL(bwd_wy_kernel, grid_c, dim3(256), 0, stream, F(F_KN), a.v, a.beta, Ff(F_GC), Ff(F_RK),
-                     F(F_TM), B(B_DW), B(B_DWT), B(B_DVN), B(B_DVNT), Bf(B_DKP), Bf(B_DGP), a.chunks, a.H,
+                     F(F_TM), B(B_DW), B(B_DWT), B(B_DVN), Bf(B_DKP), Bf(B_DGP), a.chunks, a.H,
                      (int)a.normalize, a.dk, a.dv, a.dg, a.dbeta);
 }
 

@@ -27,6 +27,7 @@ constexpr int CH = 64;   // chunk length of the WY/UT form
 
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
@@ -176,6 +177,20 @@ __device__ __forceinline__ typename Vec<E>::x8 ld8_trv(const E* tile, int ld, in
   const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
   const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * ld));
   return __builtin_bit_cast(typename Vec<E>::x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// Transposed read of a 16-row LDS tile [v][k] (row stride ld): lane (q4, r)
+// gets tile[8 (q4 & 1) + e][k0 + 16 (q4 >> 1) + r], e = 0..7, i.e. 8
+// consecutive rows of one column, for 32 columns k0 .. k0 + 31 per call.  Each
+// 16-lane group transposes independently, so the groups take different row
+// and column bases (ld8_tr's layout with the groups re-based).
+__device__ __forceinline__ bf16x8 ld8_tr16(const bf16* tile, int ld, int k0) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
+  const bf16* p = tile + (8 * (q4 & 1) + (r >> 2)) * ld + k0 + 16 * (q4 >> 1) + 4 * (r & 3);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * ld));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 // ---- workgroup synchronization for loader/consumer kernels ----------------

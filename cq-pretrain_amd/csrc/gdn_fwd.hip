@@ -561,52 +561,6 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Transposes for the backward: rows [k][v] of a chunk state gradient dS from its
-// [v][k] form, and time-first rows [t][v] of dVn from a chunk's [v][t] tile.
-// Parallel over (chunk, head).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void fwd_rows_kernel(const bf16* __restrict__ hT, const bf16* __restrict__ vnT,
-                                                       const int32_t* __restrict__ chunks, int H,
-                                                       bf16* __restrict__ hR, bf16* __restrict__ vnR) {
-  const int c = blockIdx.x, h = blockIdx.y, tid = threadIdx.x;
-  const ChunkInfo ci = chunk_info(chunks, c);
-  const size_t cb = (size_t)c * H + h;
-  __shared__ __attribute__((aligned(16))) bf16 tile[128 * 136];
-  // h: 128 x 128
-  const bf16* src = hT + cb * (D * D);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int seg = 256 * i + tid, v = seg >> 4, ks = seg & 15;
-    const bf16x8 x = ld8(src + v * D + 8 * ks);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) tile[(8 * ks + e) * 136 + v] = x[e];
-  }
-  __syncthreads();
-  bf16* dst = hR + cb * (D * D);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int seg = 256 * i + tid, k = seg >> 4, vs = seg & 15;
-    st8(dst + k * D + 8 * vs, ld8(tile + k * 136 + 8 * vs));
-  }
-  __syncthreads();
-  // v_new: 128 (v) x 64 (t)
-  const bf16* vsrc = vnT + cb * (D * CH);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int seg = 256 * i + tid, v = seg >> 3, ts = seg & 7;
-    const bf16x8 x = ld8(vsrc + v * CH + 8 * ts);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) tile[(8 * ts + e) * 136 + v] = x[e];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int seg = 256 * i + tid, t = seg >> 4, vs = seg & 15;
-    if (t < ci.len) st8(vnR + ((size_t)(ci.start + t) * H + h) * D + 8 * vs, ld8(tile + t * 136 + 8 * vs));
-  }
-}
-
-// ---------------------------------------------------------------------------
 // fwd_out: O^T (v rows, t columns) per chunk and head.  In training forwards it
 // also writes the state rows h [k][v] the backward reads, by transposed reads
 // of the h^T tile it stages anyway.
@@ -731,12 +685,6 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
       st8(hr + (n0 + r) * D + k0 + 8 * q4, ld8_trv<E>(HTs, LDK, k0, n0));
     }
   }
-}
-
-void launch_rows(const bf16* sT, const bf16* vT, const int32_t* chunks, int n_chunks, int H, bf16* srow, bf16* vrow,
-                 int timer_id, hipStream_t stream) {
-  TimedLaunch tl(timer_id, stream);
-  hipLaunchKernelGGL(fwd_rows_kernel, dim3(n_chunks, H), dim3(256), 0, stream, sT, vT, chunks, H, srow, vrow);
 }
 
 // ---------------------------------------------------------------------------

@@ -48,9 +48,6 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream);
 void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* g, const void* beta,
                       bool beta_bf16, float* state, bf16* out, int N, int E, int H, float scale,
                       hipStream_t stream);
-// rows [k][v] of chunk states and rows [t][v] from their [v][k] / [v][t] forms
-void launch_rows(const bf16* sT, const bf16* vT, const int32_t* chunks, int n_chunks, int H, bf16* srow, bf16* vrow,
-                 int timer_id, hipStream_t stream);
 void launch_l2norm_fwd(const bf16* x, bf16* y, float* rstd, int64_t rows, hipStream_t stream);
 void launch_l2norm_bwd(const bf16* y, const float* rstd, const bf16* dy, bf16* dx, int64_t rows,
                        hipStream_t stream);

@@ -7,7 +7,11 @@
 // ops/gated_delta_net.py:184); keeping h and v_new avoids re-running the serial
 // state scan in the backward.  Buffers are addressed by event (time-first
 // [T][H][D], the caller's TND order) or by chunk ([NC][H][...], one 64-event
-// block per chunk, rows past a tail chunk's length are zero).
+// block per chunk, rows past a tail chunk's length are zero).  Value-slice-major
+// buffers ([8][rows][16]: slice s holds values 16 s .. 16 s + 15 of every row)
+// are written by the state scans, whose workgroups each own one 16-wide value
+// slice: a scan step stores one contiguous block, and a reader's MFMA fragment
+// (8 consecutive values of one row) is one contiguous 16-byte load.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -36,14 +40,12 @@ enum FwdBuf {
 enum BwdBuf {
   B_DVLT = 0,  // bf16 [NC][H][D][64]  local dv = scale*P^T dO, (v, t)
   B_XT,        // bf16 [NC][H][D][D]   X = scale*(gam*Qn)^T dO, (v, k)
-  B_DH,        // bf16 [NC][H][D][D]   gradient of the state leaving the chunk, (k, v)
-  B_DVNT,      // bf16 [NC][H][D][64]  d v_new, (v, t)
-  B_DVN,       // bf16 [T][H][D]       d v_new rows (t, v)
+  B_DH,        // bf16 [NC][H][8][D][16]  gradient of the state leaving the chunk, value-slice-major (s, k, v%16)
+  B_DVN,       // bf16 [NC][H][8][64][16] d v_new, value-slice-major (s, t, v%16)
   B_DKP,       // f32  [T][H][D]       partial dKn (output and state terms)
   B_DW,        // bf16 [T][H][D]       dW rows (t, k)
   B_DWT,       // bf16 [NC][H][D][64]  dW transposed (k, t)
   B_DGP,       // f32  [T][H]          partial dG (before the reverse cumsum)
-  B_DHT,       // bf16 [NC][H][D][D]   gradient of the state leaving the chunk, (v, k)
   B_COUNT
 };
 
@@ -76,13 +78,11 @@ inline void bwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[B_DVLT] = chunk * 128 * 64 * 2;
   s[B_XT] = chunk * 128 * 128 * 2;
   s[B_DH] = chunk * 128 * 128 * 2;
-  s[B_DVNT] = chunk * 128 * 64 * 2;
-  s[B_DVN] = ev * 128 * 2;
+  s[B_DVN] = chunk * 64 * 128 * 2;
   s[B_DKP] = ev * 128 * 4;
   s[B_DW] = ev * 128 * 2;
   s[B_DWT] = chunk * 128 * 64 * 2;
   s[B_DGP] = ev * 4;
-  s[B_DHT] = chunk * 128 * 128 * 2;
 }
 
 // Offsets of every buffer; returns the total size in bytes.

@@ -14,7 +14,6 @@ enum KernelId {
   K_FWD_OUT,
   K_BWD_LOCAL,
   K_BWD_SCAN,
-  K_BWD_ROWS,
   K_BWD_DQK,
   K_BWD_WY,
   K_RECURRENT,

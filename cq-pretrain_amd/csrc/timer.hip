@@ -11,8 +11,8 @@
 
 namespace cqgdn {
 
-const char* const kKernelNames[K_COUNT] = {"fwd_prep", "fwd_scan", "fwd_out", "bwd_local", "bwd_scan",
-                                           "bwd_rows", "bwd_dqk",  "bwd_wy",  "recurrent"};
+const char* const kKernelNames[K_COUNT] = {"fwd_prep",  "fwd_scan", "fwd_out", "bwd_local",
+                                           "bwd_scan",  "bwd_dqk",  "bwd_wy",  "recurrent"};
 
 namespace {
 

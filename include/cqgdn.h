@@ -40,7 +40,7 @@ extern "C" {
 
 /* flags of cqgdn_fwd / cqgdn_bwd */
 #define CQGDN_NORMALIZE 1u /* l2-normalize q and k in the kernels (use_qk_l2norm_in_kernel=True) */
-#define CQGDN_TRAINING 2u  /* keep the extra layouts the backward reads (h and v_new rows) */
+#define CQGDN_TRAINING 2u  /* keep the extra layout the backward reads (h rows) */
 /* Inference forward with fp16 MFMA operands (11-bit mantissa instead of bf16's 8) for final
  * states within 1e-3 of an fp32 computation; V and the initial state are scaled by a power of
  * two inside the call so every fp16 operand stays in range.  Not combinable with CQGDN_TRAINING. */
@@ -68,7 +68,7 @@ int64_t cqgdn_chunk_table(const int64_t* bounds, int n_bounds, int32_t* table, i
  * unmodified, to cqgdn_bwd.
  */
 #define CQGDN_FWD_BUFFERS 15
-#define CQGDN_BWD_BUFFERS 10
+#define CQGDN_BWD_BUFFERS 8
 size_t cqgdn_fwd_workspace_size(int64_t T, int H, int64_t n_chunks);
 int cqgdn_fwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets, int count);
 size_t cqgdn_bwd_workspace_size(int64_t T, int H, int64_t n_chunks);
@@ -141,8 +141,8 @@ int cqgdn_chunk_local_cumsum(const float* g, float* out, int64_t T, int H, const
  * price one kernel against its roofline).  cqgdn_timer_arm(name, n) makes the
  * library bracket each of the next n launches of the named kernel with
  * hipEventRecord on the stream it is launched on; name = NULL disarms.  Names:
- * fwd_prep, fwd_scan, fwd_out, bwd_local, bwd_scan, bwd_rows, bwd_dqk,
- * bwd_wy, recurrent.  cqgdn_timer_read waits for the recorded
+ * fwd_prep, fwd_scan, fwd_out, bwd_local, bwd_scan, bwd_dqk, bwd_wy,
+ * recurrent.  cqgdn_timer_read waits for the recorded
  * events, writes up to `capacity` per-launch durations in milliseconds,
  * stores the number of launches recorded, and disarms.  One kernel is armed
  * at a time, process-wide.  Both return CQGDN_OK, CQGDN_EINVAL (unknown name
