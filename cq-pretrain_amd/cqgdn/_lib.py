@@ -15,8 +15,8 @@ LIB_PATH = Path(__file__).resolve().with_name("libcqgdn.so")
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 NORMALIZE, TRAINING, PRECISE = 1, 2, 4
-FWD_BUFFERS, BWD_BUFFERS = 15, 8
-FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "WT", "UT", "KgT", "hT", "h", "vnT", "knP", "vscale")
+FWD_BUFFERS, BWD_BUFFERS = 14, 8
+FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "WT", "UT", "KgT", "hT", "vnT", "knP", "vscale")
 BWD_NAMES = ("dvlT", "XT", "dh", "dVn", "dKp", "dW", "dWT", "dGp")
 
 # every symbol include/cqgdn.h declares, with (restype, argtypes)

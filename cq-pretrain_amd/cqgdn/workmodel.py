@@ -74,13 +74,13 @@ def bytes_per_chunk(kernel, c, d=D):
         "fwd_prep": 3 * e + 2 * s + 2 * e + 3 * s + tm + e + 3 * tile + e,
         # -W rows, U^T, KgT, gcum -> h^T, v_new^T
         "fwd_scan": e + 2 * tile + s + sq + tile,
-        # qn, kn, gcum, h^T, v_new^T -> o, h rows (training forward)
-        "fwd_out": 2 * e + s + sq + tile + e + sq,
+        # qn, kn, gcum, h^T, v_new^T -> o
+        "fwd_out": 2 * e + s + sq + tile + e,
         # qn, kn, dO, gcum -> dv_local^T, X^T
         "bwd_local": 3 * e + s + tile + sq,
         # Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh (slice-major), dv_new^T, dv_new (slice-major)
         "bwd_scan": e + s + tile + sq + tile + sq + tile + tile,
-        # qn, kn, rq, gcum, h rows, v_new^T, dO, dh, dv_new -> dq, dK partial (fp32), dW, dW^T, dG partial
+        # qn, kn, rq, gcum, h^T, v_new^T, dO, dh, dv_new -> dq, dK partial (fp32), dW, dW^T, dG partial
         "bwd_dqk": 2 * e + 2 * s + sq + tile + e + sq + tile + e + e32 + e + tile + s,
         # kn, v, beta, gcum, rk, T, dW, dW^T, dv_new, dv_new^T, dK partial, dG partial -> dk, dv, dg, dbeta
         "bwd_wy": e + e + 3 * s + tm + e + tile + tile + tile + e32 + s + 2 * e + 2 * s,

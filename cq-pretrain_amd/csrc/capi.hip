@@ -151,7 +151,6 @@ int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const
   a.n_docs = n_docs;
   a.scale = scale;
   a.normalize = (flags & CQGDN_NORMALIZE) != 0;
-  a.training = (flags & CQGDN_TRAINING) != 0;
   a.precise = (flags & CQGDN_PRECISE) != 0;
   a.initial_state = initial_state;
   a.final_state = final_state;

@@ -373,7 +373,7 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
     const bf16* __restrict__ qn, const bf16* __restrict__ kn, const float* __restrict__ rq,
-    const float* __restrict__ gc, const bf16* __restrict__ hR, const bf16* __restrict__ vnT,
+    const float* __restrict__ gc, const bf16* __restrict__ hT, const bf16* __restrict__ vnT,
     const bf16* __restrict__ dout, const bf16* __restrict__ dh, const bf16* __restrict__ dVn,
     const int32_t* __restrict__ chunks, int H, float scale, int normalize, bf16* __restrict__ dq,
     float* __restrict__ dKp, bf16* __restrict__ dW, bf16* __restrict__ dWT, float* __restrict__ dGp) {
@@ -402,13 +402,15 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
   // k = 16 (2 wave + mm) + r of h (with the phase-0 rows) and of dS_{c+1}
   // (before phase 2), value block kb (32 kb + 8 q4 .. + 8).  Together the four
   // waves hold all of both, so <h, dS> needs no second read.
-  const bf16* hr = hR + cb * (D * D);
+  // The h fragments (8 values of one key row) are column gathers of the
+  // forward's h^T [v][k].
+  const bf16* ht = hT + cb * (D * D);
   const bf16* dhc = dh + cb * (D * D);
   bf16x8 bh[2][4], bd[2][4];
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) bh[mm][kb] = ld8(hr + (16 * (2 * wave + mm) + r) * D + 32 * kb + 8 * q4);
+    for (int kb = 0; kb < 4; ++kb) bh[mm][kb] = gather8_col(ht, D, 32 * kb, 16 * (2 * wave + mm));
 
   {
     const int t = tid >> 2, p = tid & 3;
@@ -764,8 +766,8 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   // phase-4 operands, requested before phase 2: rows k (or v) = 16 (2 wave + mm) + r
   // of dW^T and dVn^T, the dK partial rows t = 16 n + r at those columns, and
   // the rsqrt norms of k at those rows.  dVn^T fragments (8 events of one value)
-  // are gathered from the value-slice-major dVn tile with 2-byte loads; each
-  // load instruction reads 4 runs of 32 bytes.
+  // are column gathers of the value-slice-major dVn tile (slice m is a [64][16]
+  // matrix).
   bf16x8 fwt[2][2], fvt[2][2];
   f32x4 fkp[2][4];
   float rsn[4];
@@ -774,18 +776,14 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
     for (int n = 0; n < 4; ++n)
       rsn[n] = normalize ? rk[(size_t)(ci.start + clamp_row(16 * n + r, ci.len)) * H + h] : 1.f;
     const bf16* dwt = dWT + cb * (D * CH);
-    const unsigned short* dvs = reinterpret_cast<const unsigned short*>(dVn + cb * (CH * D));
+    const bf16* dvs = dVn + cb * (CH * D);
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const int m = 2 * wave + mm;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         fwt[mm][kb] = ld8(dwt + (16 * m + r) * CH + 32 * kb + 8 * q4);
-        const unsigned short* p = dvs + m * (CH * 16) + (32 * kb + 8 * q4) * 16 + r;  // slice m, value r, event 32 kb + 8 q4
-        u16x8 x;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = p[16 * e];
-        fvt[mm][kb] = __builtin_bit_cast(bf16x8, x);
+        fvt[mm][kb] = gather8_col(dvs + m * (CH * 16), 16, 32 * kb, 0);
       }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
@@ -1015,7 +1013,7 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
   {
     TimedLaunch tl(K_BWD_DQK, stream);
     hipLaunchKernelGGL(bwd_dqk_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_GC),
-                       F(F_HR), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.chunks, a.H, a.scale, (int)a.normalize, a.dq,
+                       F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.chunks, a.H, a.scale, (int)a.normalize, a.dq,
                        Bf(B_DKP), B(B_DW), B(B_DWT), Bf(B_DGP));
   }
   TimedLaunch tl(K_BWD_WY, stream);

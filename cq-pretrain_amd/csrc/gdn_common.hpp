@@ -27,7 +27,7 @@ constexpr int CH = 64;   // chunk length of the WY/UT form
 
 typedef __bf16 bf16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
@@ -65,7 +65,6 @@ __device__ __forceinline__ bf16x8 cat(bf16x4 a, bf16x4 b) {
 
 __device__ __forceinline__ bf16x8 neg8(bf16x8 x) {
   // flip the sign bits (exact)
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   u32x4 u = __builtin_bit_cast(u32x4, x);
   u ^= 0x80008000u;
   return __builtin_bit_cast(bf16x8, u);
@@ -184,13 +183,39 @@ __device__ __forceinline__ typename Vec<E>::x8 ld8_trv(const E* tile, int ld, in
 // consecutive rows of one column, for 32 columns k0 .. k0 + 31 per call.  Each
 // 16-lane group transposes independently, so the groups take different row
 // and column bases (ld8_tr's layout with the groups re-based).
-__device__ __forceinline__ bf16x8 ld8_tr16(const bf16* tile, int ld, int k0) {
+template <class E>
+__device__ __forceinline__ typename Vec<E>::x8 ld8_tr16(const E* tile, int ld, int k0) {
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
-  const bf16* p = tile + (8 * (q4 & 1) + (r >> 2)) * ld + k0 + 16 * (q4 >> 1) + 4 * (r & 3);
+  const E* p = tile + (8 * (q4 & 1) + (r >> 2)) * ld + k0 + 16 * (q4 >> 1) + 4 * (r & 3);
   const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
   const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * ld));
-  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  return __builtin_bit_cast(typename Vec<E>::x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// Column gather of an MFMA fragment from a row-major bf16 matrix M in global
+// memory (row stride ld, even; col0 even): lane (q4, r) gets
+// M[row0 + 8 q4 + e][col0 + r], e = 0..7, 8 rows of one column, i.e. the
+// fragment ld8 would give of M^T.  Lanes r and r ^ 1 share each dword: for rows
+// 2i and 2i + 1 the even lane loads columns (r, r + 1) of row 2i and the odd
+// lane columns (r - 1, r) of row 2i + 1; the pair swaps the loaded dwords
+// through DPP and each keeps its own column's halves (v_perm).  Every load
+// instruction reads 8 runs of 32 bytes.
+__device__ __forceinline__ bf16x8 gather8_col(const bf16* M, int ld, int row0, int col0) {
+  const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4, odd = r & 1;
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(M + (size_t)(row0 + 8 * q4 + odd) * ld + col0 + r - odd);
+  // {S0 = partner, S1 = own}: even keeps own low halves, odd keeps own high halves
+  const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
+  uint32_t x[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = p[i * ld];  // rows 2i + odd, ld / 2 dwords per row pair
+  u32x4 out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t y = (uint32_t)__builtin_amdgcn_mov_dpp((int)x[i], 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    out[i] = __builtin_amdgcn_perm(y, x[i], sel);
+  }
+  return __builtin_bit_cast(bf16x8, out);
 }
 
 // ---- workgroup synchronization for loader/consumer kernels ----------------

@@ -561,15 +561,13 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// fwd_out: O^T (v rows, t columns) per chunk and head.  In training forwards it
-// also writes the state rows h [k][v] the backward reads, by transposed reads
-// of the h^T tile it stages anyway.
+// fwd_out: O^T (v rows, t columns) per chunk and head.
 // ---------------------------------------------------------------------------
 template <class E>
 __global__ __launch_bounds__(256) void fwd_out_kernel(
     const E* __restrict__ qn, const E* __restrict__ kn, const float* __restrict__ gc,
     const E* __restrict__ hT, const E* __restrict__ vnT, const int32_t* __restrict__ chunks, int H,
-    float scale, const float* __restrict__ vscale, bf16* __restrict__ o, E* __restrict__ hR) {
+    float scale, const float* __restrict__ vscale, bf16* __restrict__ o) {
   typedef typename Vec<E>::x8 X8;
   const int c = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -579,17 +577,21 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
 
   __shared__ __attribute__((aligned(16))) E Qs[64 * LDK];
   __shared__ __attribute__((aligned(16))) E Ks[64 * LDK];
-  __shared__ __attribute__((aligned(16))) E Ps[64 * LDT];    // P[t][s], causal, gated
-  __shared__ __attribute__((aligned(16))) E HTs[128 * LDK];  // h^T [v][k]
+  __shared__ __attribute__((aligned(16))) E Ps[64 * LDT];  // P[t][s], causal, gated
   __shared__ float Gs[64];
 
   const E* ht = hT + cb * (D * D);
   const E* vt = vnT + cb * (D * CH);
-  X8 av[2][2];  // v_new^T rows v = 16 (2 wave + mm) + r, t block kb: requested with the inputs
+  // requested with the inputs: rows v = 16 (2 wave + mm) + r of v_new^T (t block
+  // kb) and of h^T (k block kb)
+  X8 av[2][2], ah[2][4];
 #pragma unroll
-  for (int mm = 0; mm < 2; ++mm)
+  for (int mm = 0; mm < 2; ++mm) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) av[mm][kb] = ld8(vt + (16 * (2 * wave + mm) + r) * CH + 32 * kb + 8 * q4);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) ah[mm][kb] = ld8(ht + (16 * (2 * wave + mm) + r) * D + 32 * kb + 8 * q4);
+  }
   {
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
@@ -601,11 +603,6 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
       st8(Ks + t * LDK + col, keep_if(in, ld8(kn + row + col)));
     }
     if (p == 0) Gs[t] = gc[(size_t)(ci.start + (in ? t : ci.len - 1)) * H + h];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int seg = 256 * i + tid, v = seg >> 4, part = seg & 15;
-      st8(HTs + v * LDK + 8 * part, ld8(ht + v * D + 8 * part));
-    }
   }
   __syncthreads();
 
@@ -644,11 +641,9 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
 #pragma unroll
     for (int n = 0; n < 4; ++n) bq[n] = ld8(Qs + (16 * n + r) * LDK + 32 * kb + 8 * q4);
 #pragma unroll
-    for (int mm = 0; mm < 2; ++mm) {
-      const X8 a = ld8(HTs + (16 * (2 * wave + mm) + r) * LDK + 32 * kb + 8 * q4);
+    for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-      for (int n = 0; n < 4; ++n) acc[mm][n] = mfma(a, bq[n], acc[mm][n]);
-    }
+      for (int n = 0; n < 4; ++n) acc[mm][n] = mfma(ah[mm][kb], bq[n], acc[mm][n]);
   }
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
@@ -674,16 +669,6 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
     bf16* orow = o + ((size_t)(ci.start + t) * H + h) * D;
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) st4(orow + 16 * (2 * wave + mm) + 4 * q4, acc[mm][n] * osc);
-  }
-  if (hR) {
-    // h rows [k][v]: lane (q4, r) of (row block n0, column block k0) gets
-    // HTs[k0 + 8 q4 + e][n0 + r] = h[n0 + r][k0 + 8 q4 + e], one 16-byte piece of row n0 + r
-    E* hr = hR + cb * (D * D);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int pair = 8 * wave + i, n0 = 16 * (pair >> 2), k0 = 32 * (pair & 3);
-      st8(hr + (n0 + r) * D + k0 + 8 * q4, ld8_trv<E>(HTs, LDK, k0, n0));
-    }
   }
 }
 
@@ -767,7 +752,7 @@ static void launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stre
   }
   TimedLaunch tl(K_FWD_OUT, stream);
   hipLaunchKernelGGL(fwd_out_kernel<E>, grid_c, dim3(256), 0, stream, ws[F_QN], ws[F_KN], gcum, ws[F_HT], ws[F_VNT],
-                     a.chunks, a.H, a.scale, vscale, a.o, a.training ? ws[F_HR] : nullptr);
+                     a.chunks, a.H, a.scale, vscale, a.o);
 }
 
 void launch_fwd(const FwdArgs& a, hipStream_t stream) {

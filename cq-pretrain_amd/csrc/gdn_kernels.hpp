@@ -18,7 +18,7 @@ struct FwdArgs {
   const int32_t* doc_chunk;  // [n_docs + 1]
   int T, H, n_chunks, n_docs;
   float scale;
-  bool normalize, training;
+  bool normalize;
   bool precise;                // fp16 operands (inference only); operands in the workspace are then fp16
   const float* initial_state;  // [n_docs][H][K][V] or null
   float* final_state;          // [n_docs][H][K][V] or null

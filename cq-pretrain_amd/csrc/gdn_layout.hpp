@@ -30,7 +30,6 @@ enum FwdBuf {
   F_UT,      // bf16 [NC][H][D][64]   U = T (beta*V) transposed (v, t)
   F_KGT,     // bf16 [NC][H][D][64]   (K * exp(G_last - G)) transposed (k, t), perm32 columns
   F_HT,      // bf16 [NC][H][D][D]    state entering the chunk, (v, k)
-  F_HR,      // bf16 [NC][H][D][D]    same state, (k, v), written by fwd_out   [training]
   F_VNT,     // bf16 [NC][H][D][64]   v_new transposed (v, t)
   F_KNP,     // bf16 [T][H][D]        Kn in perm32 column order (reverse scan operand)
   F_VSC,     // f32  [1 + 256]        power-of-two scale of V and block partials (precise forward)
@@ -67,7 +66,6 @@ inline void fwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[F_UT] = chunk * 128 * 64 * 2;
   s[F_KGT] = chunk * 128 * 64 * 2;
   s[F_HT] = chunk * 128 * 128 * 2;
-  s[F_HR] = chunk * 128 * 128 * 2;
   s[F_VNT] = chunk * 128 * 64 * 2;
   s[F_KNP] = ev * 128 * 2;
   s[F_VSC] = (1 + kVscaleBlocks) * 4;

@@ -40,7 +40,7 @@ extern "C" {
 
 /* flags of cqgdn_fwd / cqgdn_bwd */
 #define CQGDN_NORMALIZE 1u /* l2-normalize q and k in the kernels (use_qk_l2norm_in_kernel=True) */
-#define CQGDN_TRAINING 2u  /* keep the extra layout the backward reads (h rows) */
+#define CQGDN_TRAINING 2u  /* the workspace will feed cqgdn_bwd (bf16 operands; excludes CQGDN_PRECISE) */
 /* Inference forward with fp16 MFMA operands (11-bit mantissa instead of bf16's 8) for final
  * states within 1e-3 of an fp32 computation; V and the initial state are scaled by a power of
  * two inside the call so every fp16 operand stays in range.  Not combinable with CQGDN_TRAINING. */
@@ -67,7 +67,7 @@ int64_t cqgdn_chunk_table(const int64_t* bounds, int n_bounds, int32_t* table, i
  * that tests can inspect intermediates.  The same workspace must be passed,
  * unmodified, to cqgdn_bwd.
  */
-#define CQGDN_FWD_BUFFERS 15
+#define CQGDN_FWD_BUFFERS 14
 #define CQGDN_BWD_BUFFERS 8
 size_t cqgdn_fwd_workspace_size(int64_t T, int H, int64_t n_chunks);
 int cqgdn_fwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets, int count);

@@ -60,7 +60,7 @@ def test_workspace_offsets_are_aligned_and_disjoint(lib, T, H, nc):
         assert all(b > a for a, b in zip(offs, offs[1:])) and total > offs[-1]
     # the largest per-chunk buffer is a [D][D] bf16 state per chunk and head
     offs = _lib.fwd_offsets(T, H, nc)
-    assert offs["h"] - offs["hT"] >= nc * H * 128 * 128 * 2
+    assert offs["vnT"] - offs["hT"] >= nc * H * 128 * 128 * 2
 
 
 def test_chunk_table_c_abi(lib):
