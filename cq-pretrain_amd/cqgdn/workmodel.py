@@ -70,14 +70,14 @@ def bytes_per_chunk(kernel, c, d=D):
     sq = d * d * 2  # bf16 [D][D] chunk state
     tm = CHUNK * CHUNK * 2  # bf16 [64][64] T matrix
     return {
-        # q,k,v,g,beta -> qn,kn,rq,rk,gcum,T,-W rows,-W^T,U^T,KgT,Kn perm32
-        "fwd_prep": 3 * e + 2 * s + 2 * e + 3 * s + tm + e + 3 * tile + e,
+        # q,k,v,g,beta -> qn,kn,rq,rk,gcum,T,-W rows,-W^T,U^T,KgT
+        "fwd_prep": 3 * e + 2 * s + 2 * e + 3 * s + tm + e + 3 * tile,
         # -W rows, U^T, KgT, gcum -> h^T, v_new^T
         "fwd_scan": e + 2 * tile + s + sq + tile,
         # qn, kn, gcum, h^T, v_new^T -> o
         "fwd_out": 2 * e + s + sq + tile + e,
-        # qn, kn, dO, gcum -> dv_local^T, X^T
-        "bwd_local": 3 * e + s + tile + sq,
+        # qn, kn, dO, gcum -> dv_local^T, X^T, Kn perm32
+        "bwd_local": 3 * e + s + tile + sq + e,
         # Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh (slice-major), dv_new^T, dv_new (slice-major)
         "bwd_scan": e + s + tile + sq + tile + sq + tile + tile,
         # qn, kn, rq, gcum, h^T, v_new^T, dO, dh, dv_new -> dq, dK partial (fp32), dW, dW^T, dG partial

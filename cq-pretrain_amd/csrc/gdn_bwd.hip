@@ -37,8 +37,12 @@ constexpr int LDQ = 132;  // fp32 row stride, 64 x 128 staging
 __global__ __launch_bounds__(256) void bwd_local_kernel(
     const bf16* __restrict__ qn, const bf16* __restrict__ kn, const bf16* __restrict__ dout,
     const float* __restrict__ gc, const int32_t* __restrict__ chunks, int H, float scale,
-    bf16* __restrict__ dvlT, bf16* __restrict__ XT) {
-  const int c = blockIdx.x, h = blockIdx.y;
+    bf16* __restrict__ dvlT, bf16* __restrict__ XT, bf16* __restrict__ knP) {
+  // grid (H, NC), chunks dispatched first to last: the reverse state scan that
+  // follows reads the last chunks first, and they are then the most recently
+  // written (still in the memory-side cache).  The perm32 copy of Kn the scan
+  // reads is written here for the same reason.
+  const int h = blockIdx.x, c = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);
@@ -80,6 +84,18 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
     }
   }
   __syncthreads();
+
+  // perm32 copy of Kn from the tile: 16-byte piece p of column block j holds
+  // logical 32 j + 4 p .. + 3 and 32 j + 16 + 4 p .. + 3
+  {
+    const int t = tid >> 2, p = tid & 3;
+    if (t < ci.len) {
+      bf16* kp = knP + ((size_t)(ci.start + t) * H + h) * D + 8 * p;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        st8(kp + 32 * j, cat(ld4(Ks + t * LDK + 32 * j + 4 * p), ld4(Ks + t * LDK + 32 * j + 16 + 4 * p)));
+    }
+  }
 
   // P (t-tile = wave, s-tiles <= wave), stored transposed: PTs[s][t]
 #pragma unroll
@@ -1002,12 +1018,12 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
   const dim3 grid_c(a.n_chunks, a.H);
   {
     TimedLaunch tl(K_BWD_LOCAL, stream);
-    hipLaunchKernelGGL(bwd_local_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), a.dout, Ff(F_GC),
-                       a.chunks, a.H, a.scale, B(B_DVLT), B(B_XT));
+    hipLaunchKernelGGL(bwd_local_kernel, dim3(a.H, a.n_chunks), dim3(256), 0, stream, F(F_QN), F(F_KN), a.dout,
+                       Ff(F_GC), a.chunks, a.H, a.scale, B(B_DVLT), B(B_XT), B(B_KNP));
   }
   {
     TimedLaunch tl(K_BWD_SCAN, stream);
-    hipLaunchKernelGGL(bwd_scan_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, F(F_KNP),
+    hipLaunchKernelGGL(bwd_scan_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, B(B_KNP),
                        Ff(F_GC), B(B_DVLT), B(B_XT), F(F_WT), a.chunks, a.doc_chunk, a.H, B(B_DH), B(B_DVN));
   }
   {

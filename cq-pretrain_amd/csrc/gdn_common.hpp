@@ -229,6 +229,15 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // Wait until every vector-memory operation this wave issued has completed.
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
+// Wait until at most N of this wave's vector-memory operations are in flight.
+// On gfx9 loads and stores share one counter and retire in issue order, so
+// this waits for everything issued before the last N operations.
+template <int N>
+__device__ __forceinline__ void wait_vmem_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 // Asynchronous copy global -> LDS, 16 bytes per lane: lane l's 16 bytes land at

@@ -36,10 +36,13 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
     const float* __restrict__ g, const float* __restrict__ beta, const int32_t* __restrict__ chunks,
     int H, const float* __restrict__ vscale, E* __restrict__ qn, E* __restrict__ kn, float* __restrict__ rq,
     float* __restrict__ rk, float* __restrict__ gc, E* __restrict__ Tm, E* __restrict__ W,
-    E* __restrict__ WT, E* __restrict__ UT, E* __restrict__ KgT, E* __restrict__ knP) {
+    E* __restrict__ WT, E* __restrict__ UT, E* __restrict__ KgT) {
   typedef typename Vec<E>::x8 X8;
   typedef typename Vec<E>::x4 X4;
-  const int c = blockIdx.x, h = blockIdx.y;
+  // grid (H, NC), chunks dispatched last to first: the state scan reads the
+  // first chunks first, and they are then the most recently written (still in
+  // the memory-side cache)
+  const int h = blockIdx.x, c = gridDim.y - 1 - blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);
@@ -136,13 +139,7 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
         const X8 xb = to8<E>(xn);
         const int col = 32 * j + 8 * p;
         st8(Ks + t * LDK + col, xb);
-        if (in) {
-          st8(kn + row + col, xb);
-          // perm32 copy: logical 8p..8p+3 -> 16(p&1) + 4(p>>1), 8p+4..8p+7 -> that + 8
-          E* kp = knP + row + 32 * j + 16 * (p & 1) + 4 * (p >> 1);
-          *reinterpret_cast<X4*>(kp) = __builtin_shufflevector(xb, xb, 0, 1, 2, 3);
-          *reinterpret_cast<X4*>(kp + 8) = __builtin_shufflevector(xb, xb, 4, 5, 6, 7);
-        }
+        if (in) st8(kn + row + col, xb);
         const f32x8 xbg = xn * (b_t * gam_t);
         kg8[j] = to8<E>(xn * kdec_t);
 #pragma unroll
@@ -334,10 +331,12 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
 // step waits.  A workgroup serves one 16-wide value slice of one head with one
 // consumer wave (wave 0) and two loader waves.  Loaders copy each chunk's
 // operands global -> LDS asynchronously (global_load_lds) into a ring of
-// SC_STAGES stages, SC_DEPTH chunks ahead of use; loader (x & 1) issues chunk x
-// and, the step before chunk x is used, waits for that copy alone (it has
-// issued nothing since).  The consumer only reads LDS and writes its output
-// tiles to LDS; the idle loader of each step stores them.  So no wave holds
+// SC_STAGES stages, SC_DEPTH chunks ahead of use.  Each chunk's copies are
+// split between the two loaders (issuing them is what bounds a step: a CU
+// accepts about one 1 KB copy per 20-30 cycles, so one wave issuing all 35
+// takes longer than the consumer's MFMA work), and each loader waits for its
+// own part the step before the chunk is used.  The consumer only reads LDS and
+// writes its output tiles to LDS; loader 1 stores them.  So no wave holds
 // in-flight data in registers and the consumer never waits on memory.
 //
 // LDS tiles are stored with 16-byte columns XOR-swizzled by row (chosen on the
@@ -361,48 +360,58 @@ struct __attribute__((aligned(16))) FwdStage {
   float pad[3];
 };
 
-// the consumer's output tiles of a step, placed over the stage's W region
+// the consumer's output tiles of a step, placed over the stage's KgT region
+// once the consumer has read it (loader 1, which refills that region, stores
+// them first)
 template <class E>
 struct __attribute__((aligned(16))) FwdScratch {
   E s[16 * SC_SROW];  // state entering the chunk, [v][k]
   E v[16 * SC_VROW];  // v_new, [v][t]
 };
-static_assert(sizeof(FwdScratch<bf16>) <= 64 * 128 * sizeof(bf16), "scratch must fit the W region");
+static_assert(sizeof(FwdScratch<bf16>) <= 128 * 64 * sizeof(bf16), "scratch must fit the KgT region");
 template <class E>
 __device__ __forceinline__ FwdScratch<E>& fwd_scratch(FwdStage<E>& st) {
-  return *reinterpret_cast<FwdScratch<E>*>(st.w);
+  return *reinterpret_cast<FwdScratch<E>*>(st.kg);
 }
 
-// Issue the asynchronous copies of chunk c into stage S.  Nothing here waits
-// on memory: the chunk table is read with scalar loads and even the gate value
-// travels by copy (a vector load whose result were used here would make this
-// wave wait for every copy issued before it).
+// Issue the asynchronous copies of chunk c into stage S, in two parts: part 0
+// (loader 0) the -W rows and G_last, 17 copies; part 1 (loader 1) KgT and the
+// U^T slice, 18 copies.  Nothing here waits on memory: the chunk table is read
+// with scalar loads and even the gate value travels by copy (a vector load
+// whose result were used here would make this wave wait for every copy issued
+// before it).
+constexpr int FWD_PART_COPIES[2] = {17, 18};
 template <class E>
 __device__ __forceinline__ void fwd_issue(FwdStage<E>& S, const int32_t* __restrict__ chunks, int c, int H, int h,
-                                          int v0, int lane, const E* __restrict__ W, const E* __restrict__ UT,
-                                          const E* __restrict__ KgT, const float* __restrict__ gc) {
+                                          int v0, int lane, int part, const E* __restrict__ W,
+                                          const E* __restrict__ UT, const E* __restrict__ KgT,
+                                          const float* __restrict__ gc) {
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
+  if (part == 0) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {  // rows past the tail re-read row len-1 and are zeroed by fwd_fix_tail
-    const int t = 4 * i + (lane >> 4), col = (lane & 15) ^ (t & 15);
-    const int tt = min(t, ci.len - 1);
-    dma16(W + ((size_t)(ci.start + tt) * H + h) * D + 8 * col, S.w + 512 * i);
-  }
-  const E* kg = KgT + cb * (D * CH);
+    for (int i = 0; i < 16; ++i) {  // rows past the tail re-read row len-1 and are zeroed by fwd_fix_tail
+      const int t = 4 * i + (lane >> 4), col = (lane & 15) ^ (t & 15);
+      const int tt = min(t, ci.len - 1);
+      dma16(W + ((size_t)(ci.start + tt) * H + h) * D + 8 * col, S.w + 512 * i);
+    }
+    if (lane == 0)  // one lane: a dword copy writes 4 bytes per active lane
+      __builtin_amdgcn_global_load_lds(gc + (size_t)(ci.start + ci.len - 1) * H + h, (lds_void_ptr)&S.glast, 4, 0,
+                                       0);
+  } else {
+    const E* kg = KgT + cb * (D * CH);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int k = 8 * i + (lane >> 3), col = (lane & 7) ^ ((k >> 1) & 7);
-    dma16(kg + k * CH + 8 * col, S.kg + 512 * i);
-  }
-  const E* ut = UT + cb * (D * CH) + v0 * CH;
+    for (int i = 0; i < 16; ++i) {
+      const int k = 8 * i + (lane >> 3), col = (lane & 7) ^ ((k >> 1) & 7);
+      dma16(kg + k * CH + 8 * col, S.kg + 512 * i);
+    }
+    const E* ut = UT + cb * (D * CH) + v0 * CH;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int v = 8 * i + (lane >> 3), col = (lane & 7) ^ ((v >> 1) & 7);
-    dma16(ut + v * CH + 8 * col, S.ut + 512 * i);
+    for (int i = 0; i < 2; ++i) {
+      const int v = 8 * i + (lane >> 3), col = (lane & 7) ^ ((v >> 1) & 7);
+      dma16(ut + v * CH + 8 * col, S.ut + 512 * i);
+    }
   }
-  if (lane == 0)
-    __builtin_amdgcn_global_load_lds(gc + (size_t)(ci.start + ci.len - 1) * H + h, (lds_void_ptr)&S.glast, 4, 0, 0);
 }
 
 // After the copies of chunk c have landed: zero the W rows past its length.
@@ -417,6 +426,9 @@ __device__ __forceinline__ void fwd_fix_tail(FwdStage<E>& S, const int32_t* __re
     }
   }
 }
+
+// global stores of one copy-out (4 of h^T, 2 of v_new^T)
+constexpr int FWD_OUT_STORES = 6;
 
 // scratch of one step -> hT [v0..v0+15][k], vnT [v0..v0+15][t]
 template <class E>
@@ -507,9 +519,9 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int m = 0; m < 8; ++m) fk[m][j] = *reinterpret_cast<const X8*>(kb + kofs[j] + 2048 * m);
-        // the W tile has been read (a wave's LDS operations complete in order):
-        // its region now takes this step's outputs
-        char* sb = base + offsetof(FwdStage<E>, w);
+        // the KgT fragments have been read (a wave's LDS operations complete in
+        // order): the KgT region now takes this step's outputs
+        char* sb = base + offsetof(FwdStage<E>, kg);
 #pragma unroll
         for (int m = 0; m < 8; ++m) *reinterpret_cast<X4*>(sb + sofs + 32 * m) = sh[m];
         const float gC = __expf(reinterpret_cast<const FwdStage<E>*>(base)->glast);
@@ -538,24 +550,43 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
         for (int i = 0; i < 4; ++i) sf[(16 * m + 4 * q4 + i) * D + v0 + r] = S[m][i] * inv;
     }
   } else {
-    // Step tau: loader (tau+1)&1 waits for chunk tau+1 (the only copy it has in
-    // flight) and fixes its tail, stores the outputs of step tau-1 from stage
-    // (tau-1)%4, then refills that same stage with chunk tau+3.  The other
-    // loader idles.
+    // Step tau, both loaders: wait for their part of chunk tau+1, then refill
+    // stage (tau-1)%4 (the consumer's stage of the previous step) with their
+    // part of chunk tau+3.  Loader 0 zeroes the W rows past a tail; loader 1
+    // first stores the outputs of step tau-1 from that stage's KgT region.
+    // Loads and stores retire in issue order (one counter on gfx9), so a loader
+    // waits for its part of chunk tau+1 by letting exactly the operations it
+    // issued after that part stay in flight: its part of chunk tau+2 and, for
+    // loader 1, the stores of the copy-out before it.
     const int j = wave - 1;
     for (int tau = -SC_DEPTH; tau < n; ++tau) {
-      if (((tau + 1) & 1) == j) {
-        const int xn = tau + 1, xo = tau - 1, xi = tau + SC_DEPTH;
-        if (xn >= 0 && xn < n) {
-          wait_vmem_all();
+      const int xn = tau + 1, xo = tau - 1, xi = tau + SC_DEPTH;
+      if (xn >= 0 && xn < n) {
+        const bool later = xn + 1 < n;  // this loader's part of chunk tau+2 is in flight
+        if (j == 0) {
+          if (later)
+            wait_vmem_le<FWD_PART_COPIES[0]>();
+          else
+            wait_vmem_all();
           fwd_fix_tail(stage[xn & (SC_STAGES - 1)], chunks, c_begin + xn, lane);
+        } else {
+          const bool stored = tau >= 2;  // the copy-out of step tau-2 came after the part of chunk tau+1
+          if (later && stored)
+            wait_vmem_le<FWD_PART_COPIES[1] + FWD_OUT_STORES>();
+          else if (later)
+            wait_vmem_le<FWD_PART_COPIES[1]>();
+          else if (stored)
+            wait_vmem_le<FWD_OUT_STORES>();
+          else
+            wait_vmem_all();
         }
-        if (xo >= 0) fwd_copy_out(fwd_scratch(stage[xo & (SC_STAGES - 1)]), c_begin + xo, H, h, v0, lane, hT, vnT);
-        if (xi < n) fwd_issue(stage[xi & (SC_STAGES - 1)], chunks, c_begin + xi, H, h, v0, lane, W, UT, KgT, gc);
       }
+      if (j == 1 && xo >= 0)
+        fwd_copy_out(fwd_scratch(stage[xo & (SC_STAGES - 1)]), c_begin + xo, H, h, v0, lane, hT, vnT);
+      if (xi < n) fwd_issue(stage[xi & (SC_STAGES - 1)], chunks, c_begin + xi, H, h, v0, lane, j, W, UT, KgT, gc);
       lds_barrier();
     }
-    if (n > 0 && (n & 1) == j)
+    if (n > 0 && j == 1)
       fwd_copy_out(fwd_scratch(stage[(n - 1) & (SC_STAGES - 1)]), c_begin + n - 1, H, h, v0, lane, hT, vnT);
   }
 }
@@ -735,14 +766,15 @@ static void launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stre
   float* gcum = reinterpret_cast<float*>(ws[F_GC]);
   {
     TimedLaunch tl(K_FWD_PREP, stream);
+    const dim3 grid_p(a.H, a.n_chunks);
     if (a.normalize)
-      hipLaunchKernelGGL((fwd_prep_kernel<E, true>), grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
+      hipLaunchKernelGGL((fwd_prep_kernel<E, true>), grid_p, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
                          a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT],
-                         ws[F_UT], ws[F_KGT], ws[F_KNP]);
+                         ws[F_UT], ws[F_KGT]);
     else
-      hipLaunchKernelGGL((fwd_prep_kernel<E, false>), grid_c, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
+      hipLaunchKernelGGL((fwd_prep_kernel<E, false>), grid_p, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
                          a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT],
-                         ws[F_UT], ws[F_KGT], ws[F_KNP]);
+                         ws[F_UT], ws[F_KGT]);
   }
   const dim3 grid_s(a.H * (D / 16), a.n_docs);
   {

@@ -31,7 +31,6 @@ enum FwdBuf {
   F_KGT,     // bf16 [NC][H][D][64]   (K * exp(G_last - G)) transposed (k, t), perm32 columns
   F_HT,      // bf16 [NC][H][D][D]    state entering the chunk, (v, k)
   F_VNT,     // bf16 [NC][H][D][64]   v_new transposed (v, t)
-  F_KNP,     // bf16 [T][H][D]        Kn in perm32 column order (reverse scan operand)
   F_VSC,     // f32  [1 + 256]        power-of-two scale of V and block partials (precise forward)
   F_COUNT
 };
@@ -45,6 +44,7 @@ enum BwdBuf {
   B_DW,        // bf16 [T][H][D]       dW rows (t, k)
   B_DWT,       // bf16 [NC][H][D][64]  dW transposed (k, t)
   B_DGP,       // f32  [T][H]          partial dG (before the reverse cumsum)
+  B_KNP,       // bf16 [T][H][D]       Kn in perm32 column order (reverse scan operand), written by bwd_local
   B_COUNT
 };
 
@@ -67,7 +67,6 @@ inline void fwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[F_KGT] = chunk * 128 * 64 * 2;
   s[F_HT] = chunk * 128 * 128 * 2;
   s[F_VNT] = chunk * 128 * 64 * 2;
-  s[F_KNP] = ev * 128 * 2;
   s[F_VSC] = (1 + kVscaleBlocks) * 4;
 }
 
@@ -81,6 +80,7 @@ inline void bwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[B_DW] = ev * 128 * 2;
   s[B_DWT] = chunk * 128 * 64 * 2;
   s[B_DGP] = ev * 4;
+  s[B_KNP] = ev * 128 * 2;
 }
 
 // Offsets of every buffer; returns the total size in bytes.
