@@ -180,10 +180,12 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
 // ---------------------------------------------------------------------------
 // Reverse scan, organised like fwd_scan_kernel: one consumer wave per (head,
 // 16-wide value slice), two loader waves copying each chunk's operands
-// global -> LDS asynchronously into a 4-stage ring, BS_DEPTH chunks ahead; the
-// consumer's output tiles (dS^T, dVn^T) go into the stage region it has read
-// (Kn) and are stored by the loader that next refills that stage.  Tiles use
-// the same XOR swizzles as the forward scan:
+// global -> LDS asynchronously into a 4-stage ring, BS_DEPTH chunks ahead, each
+// loader issuing its own part of every chunk (part 0: Kn and G; part 1: -W^T,
+// dv_local^T, X^T).  The consumer's output tiles (dS^T, dVn^T) go into the
+// stage region it has read (-W^T) and are stored by loader 1, which refills
+// that region right after.  Tiles use the same XOR swizzles as the forward
+// scan:
 //   Kn  [64 rows t][16 cols]   col ^ (t & 15)      W^T [128 rows k][8 cols]  col ^ ((k >> 1) & 7)
 //   X^T [16 rows v][16 cols]   col ^ (v & 15)      dv_local^T [16 rows v][8 cols]  col ^ ((v >> 1) & 7)
 constexpr int BS_THREADS = 64 * 3;
@@ -204,42 +206,48 @@ struct __attribute__((aligned(16))) BwdScratch {
   bf16 s[16 * BS_SROW];  // dS_{c+1}, [v][k]
   bf16 v[16 * BS_VROW];  // dVn, [v][t]
 };
-static_assert(sizeof(BwdScratch) <= 64 * 128 * sizeof(bf16), "scratch must fit the Kn region");
-__device__ __forceinline__ BwdScratch& bwd_scratch(BwdStage& st) { return *reinterpret_cast<BwdScratch*>(st.kn); }
+static_assert(sizeof(BwdScratch) <= 128 * 64 * sizeof(bf16), "scratch must fit the -W^T region");
+__device__ __forceinline__ BwdScratch& bwd_scratch(BwdStage& st) { return *reinterpret_cast<BwdScratch*>(st.wt); }
 
-// Issue the asynchronous copies of chunk c into stage S (no wait on memory here).
+// Issue part `part` of the asynchronous copies of chunk c into stage S (no
+// wait on memory here): part 0 Kn and G (17 copies), part 1 -W^T, the
+// dv_local^T and X^T slices (22 copies).
+constexpr int BWD_PART_COPIES[2] = {17, 22};
 __device__ __forceinline__ void bwd_issue(BwdStage& S, const int32_t* __restrict__ chunks, int c, int H, int h,
-                                          int v0, int lane, const bf16* __restrict__ knP,
+                                          int v0, int lane, int part, const bf16* __restrict__ knP,
                                           const float* __restrict__ gc, const bf16* __restrict__ dvlT,
                                           const bf16* __restrict__ XT, const bf16* __restrict__ WT) {
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
+  if (part == 0) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {  // rows past the tail re-read row len-1 and are zeroed by bwd_fix_tail
-    const int t = 4 * i + (lane >> 4), col = (lane & 15) ^ (t & 15);
-    const int tt = min(t, ci.len - 1);
-    dma16(knP + ((size_t)(ci.start + tt) * H + h) * D + 8 * col, S.kn + 512 * i);
-  }
-  const bf16* wt = WT + cb * (D * CH);
+    for (int i = 0; i < 16; ++i) {  // rows past the tail re-read row len-1 and are zeroed by bwd_fix_tail
+      const int t = 4 * i + (lane >> 4), col = (lane & 15) ^ (t & 15);
+      const int tt = min(t, ci.len - 1);
+      dma16(knP + ((size_t)(ci.start + tt) * H + h) * D + 8 * col, S.kn + 512 * i);
+    }
+    __builtin_amdgcn_global_load_lds(gc + (size_t)(ci.start + min(lane, ci.len - 1)) * H + h, (lds_void_ptr)S.g, 4,
+                                     0, 0);
+  } else {
+    const bf16* wt = WT + cb * (D * CH);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int k = 8 * i + (lane >> 3), col = (lane & 7) ^ ((k >> 1) & 7);
-    dma16(wt + k * CH + 8 * col, S.wt + 512 * i);
-  }
-  const bf16* dvl = dvlT + cb * (D * CH) + v0 * CH;
+    for (int i = 0; i < 16; ++i) {
+      const int k = 8 * i + (lane >> 3), col = (lane & 7) ^ ((k >> 1) & 7);
+      dma16(wt + k * CH + 8 * col, S.wt + 512 * i);
+    }
+    const bf16* dvl = dvlT + cb * (D * CH) + v0 * CH;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int v = 8 * i + (lane >> 3), col = (lane & 7) ^ ((v >> 1) & 7);
-    dma16(dvl + v * CH + 8 * col, S.dvl + 512 * i);
-  }
-  const bf16* xt = XT + cb * (D * D) + v0 * D;
+    for (int i = 0; i < 2; ++i) {
+      const int v = 8 * i + (lane >> 3), col = (lane & 7) ^ ((v >> 1) & 7);
+      dma16(dvl + v * CH + 8 * col, S.dvl + 512 * i);
+    }
+    const bf16* xt = XT + cb * (D * D) + v0 * D;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int v = 4 * i + (lane >> 4), col = (lane & 15) ^ (v & 15);
-    dma16(xt + v * D + 8 * col, S.xt + 512 * i);
+    for (int i = 0; i < 4; ++i) {
+      const int v = 4 * i + (lane >> 4), col = (lane & 15) ^ (v & 15);
+      dma16(xt + v * D + 8 * col, S.xt + 512 * i);
+    }
   }
-  __builtin_amdgcn_global_load_lds(gc + (size_t)(ci.start + min(lane, ci.len - 1)) * H + h, (lds_void_ptr)S.g, 4,
-                                   0, 0);
 }
 
 __device__ __forceinline__ void bwd_fix_tail(BwdStage& S, const int32_t* __restrict__ chunks, int c, int lane) {
@@ -252,6 +260,9 @@ __device__ __forceinline__ void bwd_fix_tail(BwdStage& S, const int32_t* __restr
     }
   }
 }
+
+// global stores of one copy-out (4 of dS, 2 of dVn)
+constexpr int BWD_OUT_STORES = 6;
 
 // scratch of one step -> dS_{c+1} and dVn in value-slice-major blocks (the
 // slice's [k][16] and [t][16], read transposed from the [v][k] / [v][t] scratch)
@@ -336,8 +347,9 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
           for (int m = 0; m < 8; ++m) fw[m][j] = *reinterpret_cast<const bf16x8*>(wtb + wofs[j] + 2048 * m);
 #pragma unroll
         for (int m = 0; m < 8; ++m) xv[m] = cvtf4(*reinterpret_cast<const bf16x4*>(xtb + xofs[m]));
-        // the Kn tile has been read: its region now takes this step's outputs
-        char* sb = base + offsetof(BwdStage, kn);
+        // the -W^T fragments have been read (a wave's LDS operations complete in
+        // order): the -W^T region now takes this step's outputs
+        char* sb = base + offsetof(BwdStage, wt);
 #pragma unroll
         for (int m = 0; m < 8; ++m) *reinterpret_cast<bf16x4*>(sb + sofs + 32 * m) = sh[m];
         __builtin_amdgcn_sched_barrier(0);
@@ -364,22 +376,42 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
       lds_barrier();
     }
   } else {
+    // Step tau, both loaders: wait for their part of step tau+1's chunk, then
+    // refill stage (tau-1)%4 with their part of step tau+3's chunk (loader 1
+    // first stores step tau-1's outputs from that stage's -W^T region).  Loads
+    // and stores retire in issue order, so a loader waits by letting exactly
+    // the operations it issued after that part stay in flight (as in the
+    // forward scan).
     const int j = wave - 1;
     for (int tau = -BS_DEPTH; tau < n; ++tau) {
-      if (((tau + 1) & 1) == j) {
-        const int xn = tau + 1, xo = tau - 1, xi = tau + BS_DEPTH;
-        if (xn >= 0 && xn < n) {
-          wait_vmem_all();
+      const int xn = tau + 1, xo = tau - 1, xi = tau + BS_DEPTH;
+      if (xn >= 0 && xn < n) {
+        const bool later = xn + 1 < n;  // this loader's part of step tau+2's chunk is in flight
+        if (j == 0) {
+          if (later)
+            wait_vmem_le<BWD_PART_COPIES[0]>();
+          else
+            wait_vmem_all();
           bwd_fix_tail(stage[xn & (BS_STAGES - 1)], chunks, c_end - 1 - xn, lane);
+        } else {
+          const bool stored = tau >= 2;  // the copy-out of step tau-2 came after this part
+          if (later && stored)
+            wait_vmem_le<BWD_PART_COPIES[1] + BWD_OUT_STORES>();
+          else if (later)
+            wait_vmem_le<BWD_PART_COPIES[1]>();
+          else if (stored)
+            wait_vmem_le<BWD_OUT_STORES>();
+          else
+            wait_vmem_all();
         }
-        if (xo >= 0)
-          bwd_copy_out(bwd_scratch(stage[xo & (BS_STAGES - 1)]), c_end - 1 - xo, H, h, slice, lane, dhS, dVnS);
-        if (xi < n)
-          bwd_issue(stage[xi & (BS_STAGES - 1)], chunks, c_end - 1 - xi, H, h, v0, lane, knP, gc, dvlT, XT, WT);
       }
+      if (j == 1 && xo >= 0)
+        bwd_copy_out(bwd_scratch(stage[xo & (BS_STAGES - 1)]), c_end - 1 - xo, H, h, slice, lane, dhS, dVnS);
+      if (xi < n)
+        bwd_issue(stage[xi & (BS_STAGES - 1)], chunks, c_end - 1 - xi, H, h, v0, lane, j, knP, gc, dvlT, XT, WT);
       lds_barrier();
     }
-    if (n > 0 && (n & 1) == j)
+    if (n > 0 && j == 1)
       bwd_copy_out(bwd_scratch(stage[(n - 1) & (BS_STAGES - 1)]), c_end - n, H, h, slice, lane, dhS, dVnS);
   }
 }
