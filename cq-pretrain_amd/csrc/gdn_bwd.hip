@@ -425,7 +425,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
     const bf16* __restrict__ dout, const bf16* __restrict__ dh, const bf16* __restrict__ dVn,
     const int32_t* __restrict__ chunks, int H, float scale, int normalize, bf16* __restrict__ dq,
     float* __restrict__ dKp, bf16* __restrict__ dW, bf16* __restrict__ dWT, float* __restrict__ dGp) {
-  const int c = blockIdx.x, h = blockIdx.y;
+  // grid (H, NC), chunks first to last: the reverse state scan wrote the first
+  // chunks last, so they are the likeliest still in the memory-side cache
+  const int h = blockIdx.x, c = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);
@@ -729,7 +731,8 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
     const float* __restrict__ dKp, const float* __restrict__ dGp,
     const int32_t* __restrict__ chunks, int H, int normalize, bf16* __restrict__ dk, bf16* __restrict__ dv,
     float* __restrict__ dg, float* __restrict__ dbeta) {
-  const int c = blockIdx.x, h = blockIdx.y;
+  // grid (H, NC), chunks last to first: bwd_dqk wrote the last chunks last
+  const int h = blockIdx.x, c = gridDim.y - 1 - blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);
@@ -1047,7 +1050,7 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
   auto Ff = [&](int i) { return reinterpret_cast<const float*>(a.fws + a.foff[i]); };
   auto B = [&](int i) { return reinterpret_cast<bf16*>(a.bws + a.boff[i]); };
   auto Bf = [&](int i) { return reinterpret_cast<float*>(a.bws + a.boff[i]); };
-  const dim3 grid_c(a.n_chunks, a.H);
+  const dim3 grid_p(a.H, a.n_chunks);  // chunk-major dispatch (the kernels pick the chunk order)
   {
     TimedLaunch tl(K_BWD_LOCAL, stream);
     hipLaunchKernelGGL(bwd_local_kernel, dim3(a.H, a.n_chunks), dim3(256), 0, stream, F(F_QN), F(F_KN), a.dout,
@@ -1060,12 +1063,12 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
   }
   {
     TimedLaunch tl(K_BWD_DQK, stream);
-    hipLaunchKernelGGL(bwd_dqk_kernel, grid_c, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_GC),
+    hipLaunchKernelGGL(bwd_dqk_kernel, grid_p, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_GC),
                        F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.chunks, a.H, a.scale, (int)a.normalize, a.dq,
                        Bf(B_DKP), B(B_DW), B(B_DWT), Bf(B_DGP));
   }
   TimedLaunch tl(K_BWD_WY, stream);
-  hipLaunchKernelGGL(bwd_wy_kernel, grid_c, dim3(256), 0, stream, F(F_KN), a.v, a.beta, Ff(F_GC), Ff(F_RK),
+  hipLaunchKernelGGL(bwd_wy_kernel, grid_p, dim3(256), 0, stream, F(F_KN), a.v, a.beta, Ff(F_GC), Ff(F_RK),
                      F(F_TM), B(B_DW), B(B_DWT), B(B_DVN), Bf(B_DKP), Bf(B_DGP), a.chunks, a.H,
                      (int)a.normalize, a.dk, a.dv, a.dg, a.dbeta);
 }

@@ -600,7 +600,9 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
     const E* __restrict__ hT, const E* __restrict__ vnT, const int32_t* __restrict__ chunks, int H,
     float scale, const float* __restrict__ vscale, bf16* __restrict__ o) {
   typedef typename Vec<E>::x8 X8;
-  const int c = blockIdx.x, h = blockIdx.y;
+  // grid (H, NC), chunks last to first: the state scan wrote the last chunks
+  // last, so they are the likeliest still in the memory-side cache
+  const int h = blockIdx.x, c = gridDim.y - 1 - blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);
@@ -758,7 +760,6 @@ __global__ __launch_bounds__(256) void vscale_final_kernel(const float* __restri
 // ---------------------------------------------------------------------------
 template <class E>
 static void launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stream) {
-  const dim3 grid_c(a.n_chunks, a.H);
   E* ws[F_COUNT];
   for (int i = 0; i < F_COUNT; ++i) ws[i] = reinterpret_cast<E*>(a.ws + a.off[i]);
   float* rq = reinterpret_cast<float*>(ws[F_RQ]);
@@ -783,7 +784,7 @@ static void launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stre
                        a.chunks, a.doc_chunk, a.H, vscale, a.initial_state, a.final_state, ws[F_HT], ws[F_VNT]);
   }
   TimedLaunch tl(K_FWD_OUT, stream);
-  hipLaunchKernelGGL(fwd_out_kernel<E>, grid_c, dim3(256), 0, stream, ws[F_QN], ws[F_KN], gcum, ws[F_HT], ws[F_VNT],
+  hipLaunchKernelGGL(fwd_out_kernel<E>, dim3(a.H, a.n_chunks), dim3(256), 0, stream, ws[F_QN], ws[F_KN], gcum, ws[F_HT], ws[F_VNT],
                      a.chunks, a.H, a.scale, vscale, a.o);
 }
 
