@@ -218,6 +218,27 @@ __device__ __forceinline__ bf16x8 gather8_col(const bf16* M, int ld, int row0, i
   return __builtin_bit_cast(bf16x8, out);
 }
 
+// gather8_col over rows [0, nrows) of M (row stride ld): rows past nrows read
+// row nrows - 1 instead (in bounds, values unspecified: the caller zeroes them
+// or multiplies them by zero).
+__device__ __forceinline__ bf16x8 gather8_col_rows(const bf16* M, int ld, int row0, int col0, int nrows) {
+  const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4, odd = r & 1;
+  const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
+  uint32_t x[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = min(row0 + 8 * q4 + 2 * i + odd, nrows - 1);
+    x[i] = *reinterpret_cast<const uint32_t*>(M + (size_t)row * ld + col0 + r - odd);
+  }
+  u32x4 out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t y = (uint32_t)__builtin_amdgcn_mov_dpp((int)x[i], 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    out[i] = __builtin_amdgcn_perm(y, x[i], sel);
+  }
+  return __builtin_bit_cast(bf16x8, out);
+}
+
 // ---- workgroup synchronization for loader/consumer kernels ----------------
 // Barrier that orders LDS only: waits for this wave's LDS operations, then
 // s_barrier.  __syncthreads() also waits for every outstanding vector-memory

@@ -31,7 +31,7 @@ constexpr int LDA = 65;   // row stride (fp32) of the 64 x 64 solve matrix
 // E: operand element type (bf16, or f16 for the precise forward).  vscale: null,
 // or the power-of-two factor applied to V (fp16 range, see vscale_final_kernel).
 template <class E, bool NORMALIZE>
-__global__ __launch_bounds__(256) void fwd_prep_kernel(
+__global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const int32_t* __restrict__ chunks,
     int H, const float* __restrict__ vscale, E* __restrict__ qn, E* __restrict__ kn, float* __restrict__ rq,
@@ -48,50 +48,67 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
 
-  __shared__ float Gs[64], Bs[64];
-  __shared__ __attribute__((aligned(16))) E Ks[64 * LDK];
-  __shared__ __attribute__((aligned(16))) E KbT[128 * LDT];
-  __shared__ __attribute__((aligned(16))) E VbT[128 * LDT];
+  __shared__ __attribute__((aligned(16))) float Gs[64];
+  __shared__ __attribute__((aligned(16))) float Bs[64];
+  __shared__ __attribute__((aligned(16))) E Ks[64 * LDK];      // K rows, then (beta gam K) rows
   __shared__ __attribute__((aligned(16))) float Af[64 * LDA];  // the solve's matrix, then the KgT tile
   __shared__ __attribute__((aligned(16))) E Ts[64 * LDT];
   const float vs = vscale ? *vscale : 1.f;
 
+  // Every global load is issued first, before any store (a wait for a load
+  // also waits for every store issued before it), so the kernel pays one memory
+  // round trip: the gates (wave 0), this thread's pieces of its q and k rows,
+  // and this wave's operand fragments of V for U = T (beta V), column gathers
+  // for value tiles 2 wave, 2 wave + 1 (rows past the chunk re-read its last
+  // row; their beta is zero).
+  const int t_r = tid >> 2, p_r = tid & 3;  // row phase: thread (t, p) owns columns 8p + 32j, j = 0..3
+  const size_t row_r = ((size_t)(ci.start + clamp_row(t_r, ci.len)) * H + h) * D;
+  float gv = 0.f, bv = 0.f;
+  if (wave == 0) {
+    const size_t ev = (size_t)(ci.start + clamp_row(lane, ci.len)) * H + h;
+    gv = g[ev];
+    bv = beta[ev];
+  }
+  bf16x8 lq[4], lk[4], vf[2][2];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    lq[j] = ld8(q + row_r + 32 * j + 8 * p_r);
+    lk[j] = ld8(k + row_r + 32 * j + 8 * p_r);
+  }
+  {
+    const bf16* vb = v + ((size_t)ci.start * H + h) * D;
+#pragma unroll
+    for (int nn = 0; nn < 2; ++nn)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) vf[nn][kb] = gather8_col_rows(vb, H * D, 32 * kb, 16 * (2 * wave + nn), ci.len);
+  }
+
   // ---- gates: chunk-local cumsum of g (wave 0, one event per lane) ----
   if (wave == 0) {
-    const int t = lane;
-    const bool in = t < ci.len;
-    const size_t ev = (size_t)(ci.start + clamp_row(t, ci.len)) * H + h;
-    float gv = keep_if(in, g[ev]);
-    const float bv = keep_if(in, beta[ev]);
+    const bool in = lane < ci.len;
+    gv = keep_if(in, gv);
+    bv = keep_if(in, bv);
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const float o = __shfl_up(gv, off, 64);
       if (lane >= off) gv += o;
     }
-    Gs[t] = gv;
-    Bs[t] = bv;
-    if (in) gc[(size_t)(ci.start + t) * H + h] = gv;
+    Gs[lane] = gv;
+    Bs[lane] = bv;
+    if (in) gc[(size_t)(ci.start + lane) * H + h] = gv;
   }
   __syncthreads();
   const float glast = Gs[ci.len - 1];
 
-  // ---- rows: thread (t, p) owns columns 8p + 32j, j = 0..3 ----
+  // ---- rows ----
   // Kg = K exp(G_last - G) is kept in registers and leaves through LDS after the
-  // solve (coalesced rows of KgT instead of 2-byte scattered stores).
-  X8 kg8[4];
+  // solve (coalesced rows of KgT instead of 2-byte scattered stores); beta gam K
+  // (rounded once, from fp32) replaces K in LDS once A has been formed.
+  X8 kg8[4], kb8[4];
   {
-    const int t = tid >> 2, p = tid & 3;
+    const int t = t_r, p = p_r;
     const bool in = t < ci.len;
-    const size_t row = ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D;
-    // all row loads are issued before any store (a wait for a load also waits
-    // for every store issued before it)
-    bf16x8 lq[4], lk[4], lv[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      lq[j] = ld8(q + row + 32 * j + 8 * p);
-      lk[j] = ld8(k + row + 32 * j + 8 * p);
-      lv[j] = ld8(v + row + 32 * j + 8 * p);
-    }
+    const size_t row = row_r;
     const float gam_t = __expf(Gs[t]);
     const float kdec_t = __expf(glast - Gs[t]);
     const float b_t = Bs[t];
@@ -140,22 +157,10 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
         const int col = 32 * j + 8 * p;
         st8(Ks + t * LDK + col, xb);
         if (in) st8(kn + row + col, xb);
-        const f32x8 xbg = xn * (b_t * gam_t);
+        kb8[j] = to8<E>(xn * (b_t * gam_t));
         kg8[j] = to8<E>(xn * kdec_t);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) KbT[(col + s) * LDT + t] = (E)xbg[s];
       }
       if (in && p == 0) rk[(size_t)(ci.start + t) * H + h] = rs;
-    }
-    // v
-    {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int col = 32 * j + 8 * p;
-        const f32x8 x = keep_if(in, cvtf8(lv[j]) * (b_t * vs));
-#pragma unroll
-        for (int s = 0; s < 8; ++s) VbT[(col + s) * LDT + t] = (E)x[s];
-      }
     }
   }
   __syncthreads();
@@ -183,6 +188,9 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
     }
   }
   __syncthreads();
+  // every read of K is done: beta gam K takes its rows (read again only after the solve)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) st8(Ks + t_r * LDK + 32 * j + 8 * p_r, kb8[j]);
 
   // ---- T = (I + A)^-1, blocked by 16, in fp32 ----
   // The four diagonal blocks by forward substitution (column c = tid/4 of block
@@ -279,30 +287,52 @@ __global__ __launch_bounds__(256) void fwd_prep_kernel(
       for (int s = 0; s < 8; ++s) kgs[(32 * j + 8 * p + s) * CH + tp] = kg8[j][s];
   }
 
-  // ---- W (-> W^T storage), W^T (-> W rows), U (-> U^T storage) ----
+  // ---- W = T (beta gam K) -> W^T storage, its transpose -> W rows, U = T (beta V) -> U^T storage ----
+  // beta gam K is read transposed from its rows (ld8_tr); beta V comes from the
+  // V fragments gathered at the start, scaled here.
   {
     X8 at[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) at[kb] = ld8(Ts + (16 * wave + r) * LDT + 32 * kb + 8 * q4);
     E* wt = WT + cb * (D * CH);
-    E* ut = UT + cb * (D * CH);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
-      f32x4 aw = zero4(), au = zero4();
+      f32x4 aw = zero4();
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        aw = mfma(at[kb], ld8(KbT + (16 * n + r) * LDT + 32 * kb + 8 * q4), aw);
-        au = mfma(at[kb], ld8(VbT + (16 * n + r) * LDT + 32 * kb + 8 * q4), au);
-      }
+      for (int kb = 0; kb < 2; ++kb) aw = mfma(at[kb], ld8_trv<E>(Ks, LDK, 32 * kb, 16 * n), aw);
       st4(wt + (16 * n + r) * CH + perm32(16 * wave + 4 * q4), -aw);
-      st4(ut + (16 * n + r) * CH + 16 * wave + 4 * q4, au);
+    }
+    // U^T rows v = 16 (2 wave + nn) + 4 q4 .., all t tiles
+    X8 bvf[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(Bs + 32 * kb + 8 * q4);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(Bs + 32 * kb + 8 * q4 + 4);
+      const f32x8 bb = f32x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]} * vs;
+#pragma unroll
+      for (int nn = 0; nn < 2; ++nn) bvf[nn][kb] = to8<E>(cvtf8(vf[nn][kb]) * bb);
+    }
+    E* ut = UT + cb * (D * CH);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      X8 a[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) a[kb] = ld8(Ts + (16 * tt + r) * LDT + 32 * kb + 8 * q4);
+#pragma unroll
+      for (int nn = 0; nn < 2; ++nn) {
+        f32x4 au = zero4();
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+          if (kb == 0 || tt >= 2) au = mfma(a[kb], bvf[nn][kb], au);  // T[t][s] = 0 for s > t
+        st4(ut + (16 * (2 * wave + nn) + r) * CH + 16 * tt + 4 * q4, au);
+      }
     }
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const int m = 2 * wave + mm;
       X8 ak[2];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) ak[kb] = ld8(KbT + (16 * m + r) * LDT + 32 * kb + 8 * q4);
+      for (int kb = 0; kb < 2; ++kb) ak[kb] = ld8_trv<E>(Ks, LDK, 32 * kb, 16 * m);
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         f32x4 acc = zero4();
