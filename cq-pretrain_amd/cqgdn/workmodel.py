@@ -12,7 +12,7 @@ split over the kernels by the contractions each one performs:
   fwd_prep   beta K K^T, W = T (beta gamma K), U = T (beta V), UT inverse   6 c^2 d + (2/3) c^3
   fwd_scan   W S, K^T v_new                                                 4 c d^2
   fwd_out    Q S, Q K^T, P v_new                                            2 c d^2 + 4 c^2 d
-  bwd_local  dv_local = P^T dO (P recomputed, not counted), X = Q^T dO      2 c^2 d + 2 c d^2
+  bwd_local  dv_local = P^T dO, X = Q^T dO (P and -W^T recomputed, not counted)  2 c^2 d + 2 c d^2
   bwd_scan   dS += W^T dv_new, dv_new += Kg dS                              4 c d^2
   bwd_dqk    dP, dQ and dK from P, dQ from S, dK from dS, dW = -dv_new S^T  6 c^2 d + 6 c d^2
   bwd_wy     dT (2), d(beta gamma K), d(beta V), dA = -T^T dT T^T, dK from dA  12 c^2 d + 4 c^3
@@ -70,14 +70,14 @@ def bytes_per_chunk(kernel, c, d=D):
     sq = d * d * 2  # bf16 [D][D] chunk state
     tm = CHUNK * CHUNK * 2  # bf16 [64][64] T matrix
     return {
-        # q,k,v,g,beta -> qn,kn,rq,rk,gcum,T,-W rows,-W^T,U^T,KgT
-        "fwd_prep": 3 * e + 2 * s + 2 * e + 3 * s + tm + e + 3 * tile,
+        # q,k,v,g,beta -> qn,kn,rq,rk,gcum,T,-W rows,U^T,KgT
+        "fwd_prep": 3 * e + 2 * s + 2 * e + 3 * s + tm + e + 2 * tile,
         # -W rows, U^T, KgT, gcum -> h^T, v_new^T
         "fwd_scan": e + 2 * tile + s + sq + tile,
         # qn, kn, gcum, h^T, v_new^T -> o
         "fwd_out": 2 * e + s + sq + tile + e,
-        # qn, kn, dO, gcum -> dv_local^T, X^T, Kn perm32
-        "bwd_local": 3 * e + s + tile + sq + e,
+        # qn, kn, dO, gcum, beta, T -> dv_local^T, X^T, Kn perm32, -W^T
+        "bwd_local": 3 * e + 2 * s + tm + tile + sq + e + tile,
         # Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh (slice-major), dv_new^T, dv_new (slice-major)
         "bwd_scan": e + s + tile + sq + tile + sq + tile + tile,
         # qn, kn, rq, gcum, h^T, v_new^T, dO, dh, dv_new -> dq, dK partial (fp32), dW, dW^T, dG partial

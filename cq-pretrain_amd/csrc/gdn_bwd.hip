@@ -36,12 +36,13 @@ constexpr int LDQ = 132;  // fp32 row stride, 64 x 128 staging
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void bwd_local_kernel(
     const bf16* __restrict__ qn, const bf16* __restrict__ kn, const bf16* __restrict__ dout,
-    const float* __restrict__ gc, const int32_t* __restrict__ chunks, int H, float scale,
-    bf16* __restrict__ dvlT, bf16* __restrict__ XT, bf16* __restrict__ knP) {
+    const float* __restrict__ gc, const float* __restrict__ beta, const bf16* __restrict__ Tm,
+    const int32_t* __restrict__ chunks, int H, float scale, bf16* __restrict__ dvlT, bf16* __restrict__ XT,
+    bf16* __restrict__ knP, bf16* __restrict__ WT) {
   // grid (H, NC), chunks dispatched first to last: the reverse state scan that
   // follows reads the last chunks first, and they are then the most recently
-  // written (still in the memory-side cache).  The perm32 copy of Kn the scan
-  // reads is written here for the same reason.
+  // written (still in the memory-side cache).  The scan's other two operands,
+  // the perm32 copy of Kn and -W^T, are made here for the same reason.
   const int h = blockIdx.x, c = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
@@ -53,20 +54,27 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
   __shared__ __attribute__((aligned(16))) bf16 QK[2 * 64 * LDK];        // Qs | Ks, then dv_local^T [v][s]
   __shared__ __attribute__((aligned(16))) bf16 QgdO[2 * 128 * LDT];     // QgT | dOT, then X^T [v][k]
   __shared__ __attribute__((aligned(16))) bf16 PTs[64 * LDT];
-  __shared__ float Gs[64];
+  __shared__ float Gs[64], Bs[64];
   bf16* Qs = QK;
   bf16* Ks = QK + 64 * LDK;
   bf16* QgT = QgdO;
   bf16* dOT = QgdO + 128 * LDT;
   static_assert(2 * 64 * LDK >= 128 * LDT && 2 * 128 * LDT >= 128 * LDK, "output tiles fit the input tiles");
 
+  // T rows t = 16 wave + r, for -W^T below (requested with the inputs)
+  bf16x8 at[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) at[kb] = ld8(Tm + cb * (CH * CH) + (16 * wave + r) * CH + 32 * kb + 8 * q4);
   {
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
     const int tc = clamp_row(t, ci.len);
     const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
     const float gt = gc[(size_t)(ci.start + tc) * H + h];
-    if (p == 0) Gs[t] = gt;
+    if (p == 0) {
+      Gs[t] = gt;
+      Bs[t] = keep_if(in, beta[(size_t)(ci.start + tc) * H + h]);
+    }
     const float gam = __expf(gt);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -94,6 +102,29 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         st8(kp + 32 * j, cat(ld4(Ks + t * LDK + 32 * j + 4 * p), ld4(Ks + t * LDK + 32 * j + 16 + 4 * p)));
+    }
+  }
+
+  // -W^T [k][perm32(t)] with W = T (beta gam K): t-tile = wave, k-tiles n; beta gam K
+  // is read transposed from the K rows and scaled per event s on the way
+  {
+    f32x8 f[2];  // beta_s gam_s at s = 32 kb + 8 q4 + e
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int s = 32 * kb + 8 * q4 + e;
+        f[kb][e] = Bs[s] * __expf(Gs[s]);
+      }
+    bf16* wt = WT + cb * (D * CH);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      f32x4 aw = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+        if (kb == 0 || wave >= 2)  // T[t][s] = 0 for s > t
+          aw = mfma(at[kb], cvt8(cvtf8(ld8_tr(Ks, LDK, 32 * kb, 16 * n)) * f[kb]), aw);
+      st4(wt + (16 * n + r) * CH + perm32(16 * wave + 4 * q4), -aw);
     }
   }
 
@@ -1054,12 +1085,12 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
   {
     TimedLaunch tl(K_BWD_LOCAL, stream);
     hipLaunchKernelGGL(bwd_local_kernel, dim3(a.H, a.n_chunks), dim3(256), 0, stream, F(F_QN), F(F_KN), a.dout,
-                       Ff(F_GC), a.chunks, a.H, a.scale, B(B_DVLT), B(B_XT), B(B_KNP));
+                       Ff(F_GC), a.beta, F(F_TM), a.chunks, a.H, a.scale, B(B_DVLT), B(B_XT), B(B_KNP), B(B_WT));
   }
   {
     TimedLaunch tl(K_BWD_SCAN, stream);
     hipLaunchKernelGGL(bwd_scan_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, B(B_KNP),
-                       Ff(F_GC), B(B_DVLT), B(B_XT), F(F_WT), a.chunks, a.doc_chunk, a.H, B(B_DH), B(B_DVN));
+                       Ff(F_GC), B(B_DVLT), B(B_XT), B(B_WT), a.chunks, a.doc_chunk, a.H, B(B_DH), B(B_DVN));
   }
   {
     TimedLaunch tl(K_BWD_DQK, stream);

@@ -36,7 +36,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     const float* __restrict__ g, const float* __restrict__ beta, const int32_t* __restrict__ chunks,
     int H, const float* __restrict__ vscale, E* __restrict__ qn, E* __restrict__ kn, float* __restrict__ rq,
     float* __restrict__ rk, float* __restrict__ gc, E* __restrict__ Tm, E* __restrict__ W,
-    E* __restrict__ WT, E* __restrict__ UT, E* __restrict__ KgT) {
+    E* __restrict__ UT, E* __restrict__ KgT) {
   typedef typename Vec<E>::x8 X8;
   typedef typename Vec<E>::x4 X4;
   // grid (H, NC), chunks dispatched last to first: the state scan reads the
@@ -287,21 +287,11 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
       for (int s = 0; s < 8; ++s) kgs[(32 * j + 8 * p + s) * CH + tp] = kg8[j][s];
   }
 
-  // ---- W = T (beta gam K) -> W^T storage, its transpose -> W rows, U = T (beta V) -> U^T storage ----
+  // ---- W = T (beta gam K) -> W rows, U = T (beta V) -> U^T storage ----
   // beta gam K is read transposed from its rows (ld8_tr); beta V comes from the
-  // V fragments gathered at the start, scaled here.
+  // V fragments gathered at the start, scaled here.  (-W^T, the reverse scan's
+  // operand, is formed by bwd_local.)
   {
-    X8 at[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) at[kb] = ld8(Ts + (16 * wave + r) * LDT + 32 * kb + 8 * q4);
-    E* wt = WT + cb * (D * CH);
-#pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      f32x4 aw = zero4();
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) aw = mfma(at[kb], ld8_trv<E>(Ks, LDK, 32 * kb, 16 * n), aw);
-      st4(wt + (16 * n + r) * CH + perm32(16 * wave + 4 * q4), -aw);
-    }
     // U^T rows v = 16 (2 wave + nn) + 4 q4 .., all t tiles
     X8 bvf[2][2];
 #pragma unroll
@@ -800,11 +790,11 @@ static void launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stre
     const dim3 grid_p(a.H, a.n_chunks);
     if (a.normalize)
       hipLaunchKernelGGL((fwd_prep_kernel<E, true>), grid_p, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
-                         a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT],
+                         a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W],
                          ws[F_UT], ws[F_KGT]);
     else
       hipLaunchKernelGGL((fwd_prep_kernel<E, false>), grid_p, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
-                         a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_WT],
+                         a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W],
                          ws[F_UT], ws[F_KGT]);
   }
   const dim3 grid_s(a.H * (D / 16), a.n_docs);

@@ -26,7 +26,6 @@ enum FwdBuf {
   F_GC,      // f32  [T][H]      chunk-local cumsum of g
   F_TM,      // bf16 [NC][H][64][64]  T = (I + A)^-1, row-major (t, s)
   F_W,       // bf16 [T][H][D]   -W, W = T (beta*exp(G)*K), rows (t, k), perm32 column order
-  F_WT,      // bf16 [NC][H][D][64]   -W transposed (k, t), perm32 column order
   F_UT,      // bf16 [NC][H][D][64]   U = T (beta*V) transposed (v, t)
   F_KGT,     // bf16 [NC][H][D][64]   (K * exp(G_last - G)) transposed (k, t), perm32 columns
   F_HT,      // bf16 [NC][H][D][D]    state entering the chunk, (v, k)
@@ -45,6 +44,7 @@ enum BwdBuf {
   B_DWT,       // bf16 [NC][H][D][64]  dW transposed (k, t)
   B_DGP,       // f32  [T][H]          partial dG (before the reverse cumsum)
   B_KNP,       // bf16 [T][H][D]       Kn in perm32 column order (reverse scan operand), written by bwd_local
+  B_WT,        // bf16 [NC][H][D][64]  -W transposed (k, t), perm32 column order (reverse scan operand), by bwd_local
   B_COUNT
 };
 
@@ -62,7 +62,6 @@ inline void fwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[F_GC] = ev * 4;
   s[F_TM] = chunk * 64 * 64 * 2;
   s[F_W] = ev * 128 * 2;
-  s[F_WT] = chunk * 128 * 64 * 2;
   s[F_UT] = chunk * 128 * 64 * 2;
   s[F_KGT] = chunk * 128 * 64 * 2;
   s[F_HT] = chunk * 128 * 128 * 2;
@@ -81,6 +80,7 @@ inline void bwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[B_DWT] = chunk * 128 * 64 * 2;
   s[B_DGP] = ev * 4;
   s[B_KNP] = ev * 128 * 2;
+  s[B_WT] = chunk * 128 * 64 * 2;
 }
 
 // Offsets of every buffer; returns the total size in bytes.
