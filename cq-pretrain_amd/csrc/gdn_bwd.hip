@@ -34,7 +34,7 @@ constexpr int LDQ = 132;  // fp32 row stride, 64 x 128 staging
 // ---------------------------------------------------------------------------
 // bwd_local
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void bwd_local_kernel(
+__global__ __launch_bounds__(256, 3) void bwd_local_kernel(
     const bf16* __restrict__ qn, const bf16* __restrict__ kn, const bf16* __restrict__ dout,
     const float* __restrict__ gc, const float* __restrict__ beta, const bf16* __restrict__ Tm,
     const int32_t* __restrict__ chunks, int H, float scale, bf16* __restrict__ dvlT, bf16* __restrict__ XT,
@@ -49,17 +49,17 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
 
-  // The outputs are staged in LDS (over the input tiles, once those are read)
-  // and stored as whole rows: X^T over QgT | dOT, dv_local^T over Qs | Ks.
-  __shared__ __attribute__((aligned(16))) bf16 QK[2 * 64 * LDK];        // Qs | Ks, then dv_local^T [v][s]
-  __shared__ __attribute__((aligned(16))) bf16 QgdO[2 * 128 * LDT];     // QgT | dOT, then X^T [v][k]
-  __shared__ __attribute__((aligned(16))) bf16 PTs[64 * LDT];
-  __shared__ float Gs[64], Bs[64];
+  // Row tiles only (every transposed operand is read with ds_read_b64_tr_b16),
+  // 52 KB, so three workgroups share a CU.  The outputs are staged over them
+  // once they are read and stored as whole rows: X^T over Qs | Ks, dv_local^T
+  // (64-element rows, 16-byte columns XOR-swizzled by row) over dOs.
+  __shared__ __attribute__((aligned(16))) bf16 QK[2 * 64 * LDK];  // Qs | Ks, then X^T [v][k]
+  __shared__ __attribute__((aligned(16))) bf16 dOs[64 * LDK];     // dO rows, then dv_local^T [v][s]
+  __shared__ __attribute__((aligned(16))) float Gs[64];
+  __shared__ __attribute__((aligned(16))) float Bs[64];
   bf16* Qs = QK;
   bf16* Ks = QK + 64 * LDK;
-  bf16* QgT = QgdO;
-  bf16* dOT = QgdO + 128 * LDT;
-  static_assert(2 * 64 * LDK >= 128 * LDT && 2 * 128 * LDT >= 128 * LDK, "output tiles fit the input tiles");
+  static_assert(64 * LDK >= 128 * 64, "dv_local^T fits the dO tile");
 
   // T rows t = 16 wave + r, for -W^T below (requested with the inputs)
   bf16x8 at[2];
@@ -70,25 +70,24 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
     const bool in = t < ci.len;
     const int tc = clamp_row(t, ci.len);
     const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
-    const float gt = gc[(size_t)(ci.start + tc) * H + h];
-    if (p == 0) {
-      Gs[t] = gt;
-      Bs[t] = keep_if(in, beta[(size_t)(ci.start + tc) * H + h]);
-    }
-    const float gam = __expf(gt);
+    bf16x8 xq[4], xk[4], xd[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      const bf16x8 xq = keep_if(in, ld8(qn + row + col));
-      st8(Qs + t * LDK + col, xq);
-      st8(Ks + t * LDK + col, keep_if(in, ld8(kn + row + col)));
-      const f32x8 xg = cvtf8(xq) * gam;
-      const bf16x8 xd = keep_if(in, ld8(dout + row + col));
+      xq[j] = ld8(qn + row + col);
+      xk[j] = ld8(kn + row + col);
+      xd[j] = ld8(dout + row + col);
+    }
+    if (p == 0) {
+      Gs[t] = gc[(size_t)(ci.start + tc) * H + h];
+      Bs[t] = keep_if(in, beta[(size_t)(ci.start + tc) * H + h]);
+    }
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        QgT[(col + s) * LDT + t] = (bf16)xg[s];
-        dOT[(col + s) * LDT + t] = xd[s];
-      }
+    for (int j = 0; j < 4; ++j) {
+      const int col = 32 * j + 8 * p;
+      st8(Qs + t * LDK + col, keep_if(in, xq[j]));
+      st8(Ks + t * LDK + col, keep_if(in, xk[j]));
+      st8(dOs + t * LDK + col, keep_if(in, xd[j]));
     }
   }
   __syncthreads();
@@ -105,17 +104,20 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
     }
   }
 
+  // per-lane event factors at s = 32 kb + 8 q4 + e: beta_s gam_s (for W) and gam_s (for X)
+  f32x8 fbg[2], fg[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int s = 32 * kb + 8 * q4 + e;
+      fg[kb][e] = __expf(Gs[s]);
+      fbg[kb][e] = Bs[s] * fg[kb][e];
+    }
+
   // -W^T [k][perm32(t)] with W = T (beta gam K): t-tile = wave, k-tiles n; beta gam K
   // is read transposed from the K rows and scaled per event s on the way
   {
-    f32x8 f[2];  // beta_s gam_s at s = 32 kb + 8 q4 + e
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int s = 32 * kb + 8 * q4 + e;
-        f[kb][e] = Bs[s] * __expf(Gs[s]);
-      }
     bf16* wt = WT + cb * (D * CH);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
@@ -123,69 +125,72 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
         if (kb == 0 || wave >= 2)  // T[t][s] = 0 for s > t
-          aw = mfma(at[kb], cvt8(cvtf8(ld8_tr(Ks, LDK, 32 * kb, 16 * n)) * f[kb]), aw);
+          aw = mfma(at[kb], cvt8(cvtf8(ld8_tr(Ks, LDK, 32 * kb, 16 * n)) * fbg[kb]), aw);
       st4(wt + (16 * n + r) * CH + perm32(16 * wave + 4 * q4), -aw);
     }
   }
 
-  // P (t-tile = wave, s-tiles <= wave), stored transposed: PTs[s][t]
+  // P tiles (t-tile tt >= s-tile = wave), causal and gated, kept in registers:
+  // pp[tt][i] = P[t = 16 tt + 4 q4 + i][s = 16 wave + r]
+  f32x4 pp[4];
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
-    f32x4 acc = zero4();
-    if (n <= wave) {
+  for (int tt = 0; tt < 4; ++tt) {
+    pp[tt] = zero4();
+    if (tt >= wave) {
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
-        acc = mfma(ld8(Qs + (16 * wave + r) * LDK + 32 * kb + 8 * q4), ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4),
-                   acc);
-      const int s = 16 * n + r;
+        pp[tt] = mfma(ld8(Qs + (16 * tt + r) * LDK + 32 * kb + 8 * q4), ld8(Ks + (16 * wave + r) * LDK + 32 * kb + 8 * q4),
+                      pp[tt]);
+      const int s = 16 * wave + r;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = 16 * wave + 4 * q4 + i;
-        acc[i] = (s <= t) ? acc[i] * __expf(Gs[t] - Gs[s]) : 0.f;
+        const int t = 16 * tt + 4 * q4 + i;
+        pp[tt][i] = (s <= t) ? pp[tt][i] * __expf(Gs[t] - Gs[s]) : 0.f;
       }
     }
-    st4(PTs + (16 * n + r) * LDT + 16 * wave + 4 * q4, acc);
   }
-  __syncthreads();
 
-  // dv_local^T: rows s = s-tile wave, 8 value tiles; only t >= s contributes
+  // dv_local^T (s rows 16 wave + 4 q4 .., 8 value tiles) = P^T dO: P^T comes from
+  // the P tiles (pack_perm, events in perm32 order), dO is read transposed in the
+  // same order; only t >= s contributes
   f32x4 dvl[8];
   {
     const int kb0 = wave >= 2 ? 1 : 0;
     bf16x8 a[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) a[kb] = ld8(PTs + (16 * wave + r) * LDT + 32 * kb + 8 * q4);
+    for (int kb = 0; kb < 2; ++kb) a[kb] = pack_perm(pp[2 * kb], pp[2 * kb + 1]);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       dvl[n] = zero4();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
-        if (kb >= kb0) dvl[n] = mfma(a[kb], ld8(dOT + (16 * n + r) * LDT + 32 * kb + 8 * q4), dvl[n]);
+        if (kb >= kb0) dvl[n] = mfma(a[kb], ld8_trp(dOs, LDK, 32 * kb, 16 * n), dvl[n]);
     }
   }
-  // X^T: k-tiles 2w, 2w+1 x 8 value tiles
+  // X^T (k-tiles 2w, 2w+1 x 8 value tiles) = (gam Q)^T dO, both read transposed
   f32x4 xt[2][8];
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm) {
     const int m = 2 * wave + mm;
     bf16x8 a[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) a[kb] = ld8(QgT + (16 * m + r) * LDT + 32 * kb + 8 * q4);
+    for (int kb = 0; kb < 2; ++kb) a[kb] = cvt8(cvtf8(ld8_tr(Qs, LDK, 32 * kb, 16 * m)) * fg[kb]);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       xt[mm][n] = zero4();
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) xt[mm][n] = mfma(a[kb], ld8(dOT + (16 * n + r) * LDT + 32 * kb + 8 * q4), xt[mm][n]);
+      for (int kb = 0; kb < 2; ++kb) xt[mm][n] = mfma(a[kb], ld8_tr(dOs, LDK, 32 * kb, 16 * n), xt[mm][n]);
     }
   }
   __syncthreads();  // the input tiles are read: they take the output tiles
-  bf16* dvs = QK;     // dv_local^T [v][s], row stride LDT
-  bf16* xts = QgdO;   // X^T [v][k], row stride LDK
+  bf16* xts = QK;   // X^T [v][k], row stride LDK
+  bf16* dvs = dOs;  // dv_local^T [v][s], 64-element rows, 16-byte column c at c ^ (v & 7)
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
-    st4(dvs + (16 * n + r) * LDT + 16 * wave + 4 * q4, dvl[n] * scale);
+    const int v = 16 * n + r, sc = 2 * wave + (q4 >> 1);
+    st4(dvs + v * 64 + 8 * (sc ^ (v & 7)) + 4 * (q4 & 1), dvl[n] * scale);
 #pragma unroll
-    for (int mm = 0; mm < 2; ++mm) st4(xts + (16 * n + r) * LDK + 16 * (2 * wave + mm) + 4 * q4, xt[mm][n] * scale);
+    for (int mm = 0; mm < 2; ++mm) st4(xts + v * LDK + 16 * (2 * wave + mm) + 4 * q4, xt[mm][n] * scale);
   }
   __syncthreads();
   {
@@ -193,7 +198,7 @@ __global__ __launch_bounds__(256) void bwd_local_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int seg = 256 * i + tid, v = seg >> 3, part = seg & 7;
-      st8(out + v * CH + 8 * part, ld8(dvs + v * LDT + 8 * part));
+      st8(out + v * CH + 8 * part, ld8(dvs + v * 64 + 8 * (part ^ (v & 7))));
     }
   }
   {

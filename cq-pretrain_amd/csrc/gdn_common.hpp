@@ -178,6 +178,19 @@ __device__ __forceinline__ typename Vec<E>::x8 ld8_trv(const E* tile, int ld, in
   return __builtin_bit_cast(typename Vec<E>::x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// ld8_tr with the rows in perm32 order: lane (q4, r) gets
+// tile[k0 + 4 q4 + e][n0 + r] for e = 0..3 and tile[k0 + 16 + 4 q4 + e - 4][n0 + r]
+// for e = 4..7, the K order of a B (or A) operand built by pack_perm from
+// accumulator fragments.
+__device__ __forceinline__ bf16x8 ld8_trp(const bf16* tile, int ld, int k0, int n0) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
+  const bf16* p = tile + (k0 + 4 * q4 + (r >> 2)) * ld + n0 + 4 * (r & 3);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 16 * ld));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // Transposed read of a 16-row LDS tile [v][k] (row stride ld): lane (q4, r)
 // gets tile[8 (q4 & 1) + e][k0 + 16 (q4 >> 1) + r], e = 0..7, i.e. 8
 // consecutive rows of one column, for 32 columns k0 .. k0 + 31 per call.  Each
