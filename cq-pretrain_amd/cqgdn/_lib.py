@@ -15,9 +15,9 @@ LIB_PATH = Path(__file__).resolve().with_name("libcqgdn.so")
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 NORMALIZE, TRAINING, PRECISE = 1, 2, 4
-FWD_BUFFERS, BWD_BUFFERS = 12, 10
+FWD_BUFFERS, BWD_BUFFERS = 12, 9
 FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "UT", "KgT", "hT", "vnT", "vscale")
-BWD_NAMES = ("dvlT", "XT", "dh", "dVn", "dKp", "dW", "dWT", "dGp", "knP", "WT")
+BWD_NAMES = ("dvlT", "XT", "dh", "dVn", "dKp", "dW", "dGp", "knP", "WT")
 
 # every symbol include/cqgdn.h declares, with (restype, argtypes)
 _P, _I, _I64, _U, _F, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint, ctypes.c_float, ctypes.c_size_t

@@ -80,10 +80,10 @@ def bytes_per_chunk(kernel, c, d=D):
         "bwd_local": 3 * e + 2 * s + tm + tile + sq + e + tile,
         # Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh (slice-major), dv_new^T, dv_new (slice-major)
         "bwd_scan": e + s + tile + sq + tile + sq + tile + tile,
-        # qn, kn, rq, gcum, h^T, v_new^T, dO, dh, dv_new -> dq, dK partial (fp32), dW, dW^T, dG partial
-        "bwd_dqk": 2 * e + 2 * s + sq + tile + e + sq + tile + e + e32 + e + tile + s,
-        # kn, v, beta, gcum, rk, T, dW, dW^T, dv_new, dv_new^T, dK partial, dG partial -> dk, dv, dg, dbeta
-        "bwd_wy": e + e + 3 * s + tm + e + tile + tile + tile + e32 + s + 2 * e + 2 * s,
+        # qn, kn, rq, gcum, h^T, v_new^T, dO, dh, dv_new -> dq, dK partial (fp32), dW, dG partial
+        "bwd_dqk": 2 * e + 2 * s + sq + tile + e + sq + tile + e + e32 + e + s,
+        # kn, v, beta, gcum, rk, T, dW, dv_new, dK partial, dG partial -> dk, dv, dg, dbeta
+        "bwd_wy": e + e + 3 * s + tm + e + tile + e32 + s + 2 * e + 2 * s,
     }[kernel]
 
 

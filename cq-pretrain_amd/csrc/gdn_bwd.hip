@@ -460,7 +460,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
     const float* __restrict__ gc, const bf16* __restrict__ hT, const bf16* __restrict__ vnT,
     const bf16* __restrict__ dout, const bf16* __restrict__ dh, const bf16* __restrict__ dVn,
     const int32_t* __restrict__ chunks, int H, float scale, int normalize, bf16* __restrict__ dq,
-    float* __restrict__ dKp, bf16* __restrict__ dW, bf16* __restrict__ dWT, float* __restrict__ dGp) {
+    float* __restrict__ dKp, bf16* __restrict__ dW, float* __restrict__ dGp) {
   // grid (H, NC), chunks first to last: the reverse state scan wrote the first
   // chunks last, so they are the likeliest still in the memory-side cache
   const int h = blockIdx.x, c = blockIdx.y;
@@ -689,9 +689,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
 
   __syncthreads();  // the dVn copies have landed (the barrier waits for them)
 
-  // ---- phase 4: dW = -dVn S^T  (both orientations) and <S, dS> ----
+  // ---- phase 4: dW = -dVn S^T (rows t; bwd_wy gathers its transposed view) ----
   {
-    bf16* wt = dWT + cb * (D * CH);
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       const int t = 16 * n + r;
@@ -702,14 +701,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
         const int m = 2 * wave + mm;
-        f32x4 w1 = zero4(), w2 = zero4();
+        f32x4 w = zero4();  // dW^T[k = 16 m + 4 q4 + i][t]
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          w1 = mfma(av[kb], bh[mm][kb], w1);  // dW[t][k]  (rows t)
-          w2 = mfma(bh[mm][kb], av[kb], w2);  // dW^T[k][t] (rows k)
-        }
-        st4(wt + (16 * m + r) * CH + 16 * n + 4 * q4, w1);
-        if (t < ci.len) st4(dW + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4, w2);
+        for (int kb = 0; kb < 4; ++kb) w = mfma(bh[mm][kb], av[kb], w);
+        if (t < ci.len) st4(dW + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4, w);
       }
     }
   }
@@ -763,7 +758,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
 __global__ __launch_bounds__(256) void bwd_wy_kernel(
     const bf16* __restrict__ kn, const bf16* __restrict__ vin, const float* __restrict__ beta,
     const float* __restrict__ gc, const float* __restrict__ rk, const bf16* __restrict__ Tm,
-    const bf16* __restrict__ dW, const bf16* __restrict__ dWT, const bf16* __restrict__ dVn,
+    const bf16* __restrict__ dW, const bf16* __restrict__ dVn,
     const float* __restrict__ dKp, const float* __restrict__ dGp,
     const int32_t* __restrict__ chunks, int H, int normalize, bf16* __restrict__ dk, bf16* __restrict__ dv,
     float* __restrict__ dg, float* __restrict__ dbeta) {
@@ -852,9 +847,11 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
 
   // phase-4 operands, requested before phase 2: rows k (or v) = 16 (2 wave + mm) + r
   // of dW^T and dVn^T, the dK partial rows t = 16 n + r at those columns, and
-  // the rsqrt norms of k at those rows.  dVn^T fragments (8 events of one value)
-  // are column gathers of the value-slice-major dVn tile (slice m is a [64][16]
-  // matrix).
+  // the rsqrt norms of k at those rows.  Both transposed operands are column
+  // gathers: dW^T of the dW rows (events past the chunk re-read its last row;
+  // they meet T's identity rows past the chunk and zero K rows, so they add
+  // nothing to a kept result), dVn^T of the value-slice-major dVn tile (slice m
+  // is a [64][16] matrix).
   bf16x8 fwt[2][2], fvt[2][2];
   f32x4 fkp[2][4];
   float rsn[4];
@@ -862,14 +859,14 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
 #pragma unroll
     for (int n = 0; n < 4; ++n)
       rsn[n] = normalize ? rk[(size_t)(ci.start + clamp_row(16 * n + r, ci.len)) * H + h] : 1.f;
-    const bf16* dwt = dWT + cb * (D * CH);
+    const bf16* dwr = dW + ((size_t)ci.start * H + h) * D;
     const bf16* dvs = dVn + cb * (CH * D);
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const int m = 2 * wave + mm;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        fwt[mm][kb] = ld8(dwt + (16 * m + r) * CH + 32 * kb + 8 * q4);
+        fwt[mm][kb] = gather8_col_rows(dwr, H * D, 32 * kb, 16 * m, ci.len);
         fvt[mm][kb] = gather8_col(dvs + m * (CH * 16), 16, 32 * kb, 0);
       }
 #pragma unroll
@@ -1101,11 +1098,11 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
     TimedLaunch tl(K_BWD_DQK, stream);
     hipLaunchKernelGGL(bwd_dqk_kernel, grid_p, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_GC),
                        F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.chunks, a.H, a.scale, (int)a.normalize, a.dq,
-                       Bf(B_DKP), B(B_DW), B(B_DWT), Bf(B_DGP));
+                       Bf(B_DKP), B(B_DW), Bf(B_DGP));
   }
   TimedLaunch tl(K_BWD_WY, stream);
   hipLaunchKernelGGL(bwd_wy_kernel, grid_p, dim3(256), 0, stream, F(F_KN), a.v, a.beta, Ff(F_GC), Ff(F_RK),
-                     F(F_TM), B(B_DW), B(B_DWT), B(B_DVN), Bf(B_DKP), Bf(B_DGP), a.chunks, a.H,
+                     F(F_TM), B(B_DW), B(B_DVN), Bf(B_DKP), Bf(B_DGP), a.chunks, a.H,
                      (int)a.normalize, a.dk, a.dv, a.dg, a.dbeta);
 }
 
