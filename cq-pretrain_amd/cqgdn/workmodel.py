@@ -78,8 +78,8 @@ def bytes_per_chunk(kernel, c, d=D):
         "fwd_out": 2 * e + s + sq + tile + e,
         # qn, kn, dO, gcum, beta, T -> dv_local^T, X^T, Kn perm32, -W^T
         "bwd_local": 3 * e + 2 * s + tm + tile + sq + e + tile,
-        # Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh (slice-major), dv_new^T, dv_new (slice-major)
-        "bwd_scan": e + s + tile + sq + tile + sq + tile + tile,
+        # Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh, dv_new (both value-slice-major)
+        "bwd_scan": e + s + tile + sq + tile + sq + tile,
         # qn, kn, rq, gcum, h^T, v_new^T, dO, dh, dv_new -> dq, dK partial (fp32), dW, dG partial
         "bwd_dqk": 2 * e + 2 * s + sq + tile + e + sq + tile + e + e32 + e + s,
         # kn, v, beta, gcum, rk, T, dW, dv_new, dK partial, dG partial -> dk, dv, dg, dbeta
