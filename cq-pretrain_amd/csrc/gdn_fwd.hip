@@ -394,43 +394,76 @@ __device__ __forceinline__ FwdScratch<E>& fwd_scratch(FwdStage<E>& st) {
   return *reinterpret_cast<FwdScratch<E>*>(st.kg);
 }
 
+// Per-lane byte offsets of a loader's copies within a full chunk (the same for
+// every chunk of 64 events): part 0 the 16 W-row copies (from the chunk's first
+// event row), part 1 the 16 KgT copies and the 2 U^T copies (from the chunk's
+// tiles).  With them a full chunk's copy costs one address add.
+struct FwdCopyOffsets {
+  uint32_t o[18];
+};
+template <class E>
+__device__ __forceinline__ FwdCopyOffsets fwd_copy_offsets(int part, int H, int h, int lane) {
+  FwdCopyOffsets f;
+  if (part == 0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int t = 4 * i + (lane >> 4), col = (lane & 15) ^ (t & 15);
+      f.o[i] = (uint32_t)(((t * H + h) * D + 8 * col) * sizeof(E));
+    }
+    f.o[16] = f.o[17] = 0;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int k = 8 * i + (lane >> 3), col = (lane & 7) ^ ((k >> 1) & 7);
+      f.o[i] = (uint32_t)((k * CH + 8 * col) * sizeof(E));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int v = 8 * i + (lane >> 3), col = (lane & 7) ^ ((v >> 1) & 7);
+      f.o[16 + i] = (uint32_t)((v * CH + 8 * col) * sizeof(E));
+    }
+  }
+  return f;
+}
+
 // Issue the asynchronous copies of chunk c into stage S, in two parts: part 0
 // (loader 0) the -W rows and G_last, 17 copies; part 1 (loader 1) KgT and the
 // U^T slice, 18 copies.  Nothing here waits on memory: the chunk table is read
 // with scalar loads and even the gate value travels by copy (a vector load
 // whose result were used here would make this wave wait for every copy issued
-// before it).
+// before it).  A tail chunk re-reads its last W row for the rows past its
+// length (zeroed by fwd_fix_tail).
 constexpr int FWD_PART_COPIES[2] = {17, 18};
 template <class E>
 __device__ __forceinline__ void fwd_issue(FwdStage<E>& S, const int32_t* __restrict__ chunks, int c, int H, int h,
-                                          int v0, int lane, int part, const E* __restrict__ W,
-                                          const E* __restrict__ UT, const E* __restrict__ KgT,
-                                          const float* __restrict__ gc) {
+                                          int v0, int lane, int part, const FwdCopyOffsets& f,
+                                          const E* __restrict__ W, const E* __restrict__ UT,
+                                          const E* __restrict__ KgT, const float* __restrict__ gc) {
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
   if (part == 0) {
+    if (ci.len == CH) {
+      const char* base = reinterpret_cast<const char*>(W + (size_t)ci.start * H * D);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {  // rows past the tail re-read row len-1 and are zeroed by fwd_fix_tail
-      const int t = 4 * i + (lane >> 4), col = (lane & 15) ^ (t & 15);
-      const int tt = min(t, ci.len - 1);
-      dma16(W + ((size_t)(ci.start + tt) * H + h) * D + 8 * col, S.w + 512 * i);
+      for (int i = 0; i < 16; ++i) dma16(base + f.o[i], S.w + 512 * i);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int t = 4 * i + (lane >> 4), col = (lane & 15) ^ (t & 15);
+        const int tt = min(t, ci.len - 1);
+        dma16(W + ((size_t)(ci.start + tt) * H + h) * D + 8 * col, S.w + 512 * i);
+      }
     }
     if (lane == 0)  // one lane: a dword copy writes 4 bytes per active lane
       __builtin_amdgcn_global_load_lds(gc + (size_t)(ci.start + ci.len - 1) * H + h, (lds_void_ptr)&S.glast, 4, 0,
                                        0);
   } else {
-    const E* kg = KgT + cb * (D * CH);
+    const char* kg = reinterpret_cast<const char*>(KgT + cb * (D * CH));
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int k = 8 * i + (lane >> 3), col = (lane & 7) ^ ((k >> 1) & 7);
-      dma16(kg + k * CH + 8 * col, S.kg + 512 * i);
-    }
-    const E* ut = UT + cb * (D * CH) + v0 * CH;
+    for (int i = 0; i < 16; ++i) dma16(kg + f.o[i], S.kg + 512 * i);
+    const char* ut = reinterpret_cast<const char*>(UT + cb * (D * CH) + v0 * CH);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int v = 8 * i + (lane >> 3), col = (lane & 7) ^ ((v >> 1) & 7);
-      dma16(ut + v * CH + 8 * col, S.ut + 512 * i);
-    }
+    for (int i = 0; i < 2; ++i) dma16(ut + f.o[16 + i], S.ut + 512 * i);
   }
 }
 
@@ -579,6 +612,7 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
     // issued after that part stay in flight: its part of chunk tau+2 and, for
     // loader 1, the stores of the copy-out before it.
     const int j = wave - 1;
+    const FwdCopyOffsets offs = fwd_copy_offsets<E>(j, H, h, lane);
     for (int tau = -SC_DEPTH; tau < n; ++tau) {
       const int xn = tau + 1, xo = tau - 1, xi = tau + SC_DEPTH;
       if (xn >= 0 && xn < n) {
@@ -603,7 +637,7 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
       }
       if (j == 1 && xo >= 0)
         fwd_copy_out(fwd_scratch(stage[xo & (SC_STAGES - 1)]), c_begin + xo, H, h, v0, lane, hT, vnT);
-      if (xi < n) fwd_issue(stage[xi & (SC_STAGES - 1)], chunks, c_begin + xi, H, h, v0, lane, j, W, UT, KgT, gc);
+      if (xi < n) fwd_issue(stage[xi & (SC_STAGES - 1)], chunks, c_begin + xi, H, h, v0, lane, j, offs, W, UT, KgT, gc);
       lds_barrier();
     }
     if (n > 0 && j == 1)
