@@ -14,8 +14,10 @@ Printed: one JSON line with the contract keys, plus
                 stream it runs on, recorded inside the timed region)
   cpu_baseline  the fp32 chunked torch oracle on this host's cores (a bounded
                 sample: one config-2 fwd+bwd)
-  extra         config-1 fwd+bwd, per-kernel table (MFMA / HBM fractions),
-                prefill, and the decode step (B=64, 256 steps, GB/s)
+  extra         config-1 and config-3 fwd+bwd, per-kernel table (MFMA / HBM
+                fractions), the whole GatedDelta layer at width 2048 (content 2048 and
+                8192 on image-CQ plans, beside the reference's published Ascend 910B
+                medians), prefill, and the decode step (B=64, 256 steps, GB/s)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
 """
@@ -167,6 +169,39 @@ def decode_case(gdn, _lib, workmodel, torch, device, steps):
                 bytes_per_step=nbytes, working_set_mb=round(layers * n * H * D * D * 4 / 1e6, 1))
 
 
+def layer_case(torch, device, content, queries, iterations=12):
+    """Whole GatedDelta layer at width 2048 on an image-CQ plan with the event counts of the
+    reference's benchmark rows (scripts/benchmark_gdn.py:34-56): 3 warm-up steps, then the median
+    of ``iterations`` fwd+bwd steps, each bracketed by synchronize."""
+    from cqgdn import layer
+
+    torch.manual_seed(872)
+    model = layer.GatedDeltaLayer().to(device, torch.bfloat16)
+    model.A_log.data = model.A_log.data.float()
+    model.norm_weight.data = model.norm_weight.data.float()
+    plan = layer.cq_layer_plan(content, queries).to(device)
+    x = torch.randn(plan.hidden_length, 1, 2048, device=device, dtype=torch.bfloat16, requires_grad=True)
+    upstream = torch.randn_like(x) / 100
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        x.grad = None
+        y = model(x, plan)
+        (y * upstream).sum().backward()
+
+    for _ in range(3):
+        step()
+    durations = []
+    for _ in range(iterations):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        durations.append((time.perf_counter() - t0) * 1e3)
+    return dict(content_tokens=content, query_tokens=queries, events=len(plan.event_q),
+                median_ms=round(statistics.median(durations), 4))
+
+
 COPY_BYTES = 256 << 20
 
 
@@ -246,6 +281,19 @@ def main():
         f1 = sum(workmodel.kernel_work(k, bounds1, H)[0] for k in workmodel.FWD_KERNELS + workmodel.BWD_KERNELS)
         extra["config1_fwd_bwd_ms"] = round(ms1, 4)
         extra["config1_tflops"] = round(f1 / (ms1 * 1e-3) / 1e12, 2)
+        log("config 3 fwd+bwd (packed documents)")
+        T3, bounds3, step3, _ = training_case(gdn, synthetic, torch, 3, device)
+        for _ in range(args.warmup):
+            step3()
+        ms3 = time_steps(torch, step3, max(5, args.steps // 2)) * 1e3
+        f3 = sum(workmodel.kernel_work(k, bounds3, H)[0] for k in workmodel.FWD_KERNELS + workmodel.BWD_KERNELS)
+        extra["config3_fwd_bwd_ms"] = round(ms3, 4)
+        extra["config3_tflops"] = round(f3 / (ms3 * 1e-3) / 1e12, 2)
+        extra["config3_documents"] = len(bounds3) - 1
+        del step3
+        log("whole GatedDelta layer, width 2048 (content 2048 and 8192, image-CQ plans)")
+        extra["layer_w2048"] = [dict(layer_case(torch, device, c, nq), reference_ascend910b_ms=ref)
+                                for c, nq, ref in ((2048, 1675, 10.46), (8192, 7819, 38.60))]
         log("config 2 prefill")
         T2, mask2, b2 = synthetic.config_events(2, seed=0)
         xs = [x.to(device) for x in synthetic.make_inputs(T2, H, D, seed=2, readonly=mask2)]

@@ -1,0 +1,166 @@
+"""A whole GatedDelta layer around the hip recurrence, for the layer benchmark.
+
+The reference publishes GDN timings for the whole layer at width 2048
+(scripts/benchmark_gdn.py:34-56): fused input projection, causal conv over the
+content, the CQ query conv from the content history, the event gathers, the
+gates, the recurrence, the output gather, gated RMSNorm and out_proj.
+``GatedDeltaLayer`` follows that forward (models/backbone_qwen35.py:156-246,
+the training path without a state cache) with this package's ``delta`` as the
+recurrence and plain torch for everything around it: the reference keeps the
+conv, the norm and the planning unchanged when ``gdn_backend`` switches.
+
+``cq_layer_plan`` builds a synthetic single-document event plan with the
+structure of ops/gated_delta_layout.py:56-176 (content writes in sigma order,
+queries read before their group, every member of a multi-token image group
+read again after the group is written) and the event counts of the
+reference's image-CQ benchmark rows.
+"""
+
+from __future__ import annotations
+
+import random
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from . import gated_delta_net as gdn
+
+
+@dataclass
+class LayerPlan:
+    """The fields of the reference's DeltaPlan that the layer's forward reads."""
+
+    content_order: torch.Tensor  # hidden row of each content write, in write order
+    event_q: torch.Tensor  # per event: row of cat(content q, query q)
+    event_write: torch.Tensor  # per event: content row it writes, or n_content (zero row: read-only)
+    query_source: torch.Tensor  # hidden row of each query
+    query_history: torch.Tensor  # [n_queries, kernel - 1] content rows of the query conv (n_content = none)
+    content_cu: torch.Tensor
+    content_bounds: tuple
+    event_cu: torch.Tensor
+    event_bounds: tuple
+    hidden_length: int
+    hidden_event: torch.Tensor  # per hidden row: the event whose output it takes
+
+    def to(self, device):
+        return LayerPlan(**{k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in vars(self).items()})
+
+
+def cq_layer_plan(content: int, queries: int, image_groups=(249, 249), kernel: int = 4, seed: int = 0) -> LayerPlan:
+    """One document of ``content`` tokens (image groups at seeded positions, text tokens
+    as single-token groups) and ``queries`` read-only CQ queries attached to seeded
+    groups.  Events: content + queries + sum(image_groups)."""
+    rnd = random.Random(seed)
+    # image groups: disjoint runs of consecutive content positions
+    starts, free = [], content
+    for size in image_groups:
+        free -= size
+    cuts = sorted(rnd.sample(range(free + 1), len(image_groups)))
+    offset = 0
+    for cut, size in zip(cuts, image_groups):
+        starts.append(cut + offset)
+        offset += size
+    groups, pos = [], 0
+    image_at = dict(zip(starts, image_groups))
+    while pos < content:
+        size = image_at.get(pos, 1)
+        groups.append(list(range(pos, pos + size)))
+        pos += size
+    attach = {}
+    for j in range(queries):
+        attach.setdefault(rnd.randrange(len(groups)), []).append(j)
+
+    nc = content
+    event_q, event_write, out_event = [], [], {}
+    query_history, history = [None] * queries, []
+    for gi, members in enumerate(groups):
+        for j in attach.get(gi, []):
+            prev = history[-(kernel - 1):] if kernel > 1 else []
+            query_history[j] = [nc] * (kernel - 1 - len(prev)) + prev
+            out_event[content + j] = len(event_q)
+            event_q.append(nc + j)
+            event_write.append(nc)
+        for ci in members:
+            if len(members) == 1:
+                out_event[ci] = len(event_q)
+            event_q.append(ci)
+            event_write.append(ci)
+            history.append(ci)
+        if len(members) > 1:
+            for ci in members:
+                out_event[ci] = len(event_q)
+                event_q.append(ci)
+                event_write.append(nc)
+    hidden = content + queries
+    long = lambda xs: torch.tensor(xs, dtype=torch.long)
+    events = len(event_q)
+    return LayerPlan(
+        content_order=torch.arange(content),
+        event_q=long(event_q),
+        event_write=long(event_write),
+        query_source=torch.arange(content, hidden),
+        query_history=long(query_history).reshape(queries, kernel - 1),
+        content_cu=torch.tensor([0, content], dtype=torch.int32),
+        content_bounds=(0, content),
+        event_cu=torch.tensor([0, events], dtype=torch.long),
+        event_bounds=(0, events),
+        hidden_length=hidden,
+        hidden_event=long([out_event[r] for r in range(hidden)]),
+    )
+
+
+class GatedDeltaLayer(torch.nn.Module):
+    """GatedDelta with fused projections (models/backbone_qwen35.py:121-154), one TP rank."""
+
+    def __init__(self, width=2048, heads=16, head_dim=128, conv_kernel=4, eps=1e-6):
+        super().__init__()
+        self.heads, self.head_dim, self.kernel = heads, head_dim, conv_kernel
+        key = value = heads * head_dim
+        self.in_proj_all = torch.nn.Linear(width, 2 * key + 2 * value + 2 * heads, bias=False)
+        self.conv_weight = torch.nn.Parameter(torch.empty(2 * key + value, conv_kernel).uniform_(-0.5, 0.5))
+        self.A_log = torch.nn.Parameter(torch.rand(heads).mul(15.99).add(0.01).log())
+        self.dt_bias = torch.nn.Parameter(torch.ones(heads))
+        self.norm_weight = torch.nn.Parameter(torch.ones(head_dim))
+        self.out_proj = torch.nn.Linear(value, width, bias=False)
+        self.eps = eps
+        for lin in (self.in_proj_all, self.out_proj):
+            torch.nn.init.normal_(lin.weight, std=0.02)
+
+    def forward(self, x, plan: LayerPlan, recurrence=None):
+        """``recurrence(q, k, v, g, beta, plan)``, if given, replaces the hip delta (the layer parity
+        test passes a float64 CPU recurrence)."""
+        h, d = self.heads, self.head_dim
+        size = h * d
+        raw, z, a, beta = self.in_proj_all(x[:, 0]).split((2 * size + size, size, h, h), -1)
+        updates = raw.index_select(0, plan.content_order)
+        convolved = gdn.conv(updates[None], self.conv_weight, activation="silu", cu_seqlens=plan.content_cu,
+                             cu_seqlens_cpu=plan.content_bounds)[0][0]
+        q, k, v = convolved.split((size, size, size), -1)
+        q, k, v = q.reshape(-1, h, d), k.reshape(-1, h, d), v.reshape(-1, h, d)
+        # the CQ query conv reads the content history only
+        raw_q = raw[:, :size].index_select(0, plan.query_source)
+        weight = self.conv_weight[:size]
+        query = raw_q * weight[:, -1]
+        history = torch.cat((updates[:, :size], updates.new_zeros(1, size)), dim=0)
+        for j in range(self.kernel - 1):
+            query = query + history.index_select(0, plan.query_history[:, j]) * weight[:, j]
+        query = F.silu(query).reshape(-1, h, d)
+        q = torch.cat((q, query), dim=0).index_select(0, plan.event_q)[None]
+        zeros = k.new_zeros(1, h, d)
+        k = torch.cat((k, zeros), dim=0).index_select(0, plan.event_write)[None]
+        v = torch.cat((v, zeros), dim=0).index_select(0, plan.event_write)[None]
+        a = a.index_select(0, plan.content_order).float()
+        g = -self.A_log.float().exp() * F.softplus(a + self.dt_bias.float())
+        beta = beta.index_select(0, plan.content_order).sigmoid().float()
+        control_zero = g.new_zeros(1, h)
+        g = torch.cat((g, control_zero)).index_select(0, plan.event_write)[None]
+        beta = torch.cat((beta, control_zero)).index_select(0, plan.event_write)[None]
+        if recurrence is None:
+            y = gdn.delta(q, k, v, g, beta, use_qk_l2norm_in_kernel=True, cu_seqlens=plan.event_cu,
+                          cu_seqlens_cpu=plan.event_bounds)[0]
+        else:
+            y = recurrence(q, k, v, g, beta, plan)
+        selected = y[0].index_select(0, plan.hidden_event).to(x.dtype)
+        out = gdn.gated_norm(selected, z.reshape(-1, h, d), self.norm_weight, self.eps)
+        return self.out_proj(out.flatten(-2))[:, None]

@@ -365,3 +365,49 @@ def test_forward_backward_bitwise_deterministic(gdn):
     torch.cuda.synchronize()
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+def test_whole_layer_matches_oracle_recurrence(gdn):
+    """The GatedDelta layer mirror (width 2048, image-CQ plan) with the hip recurrence against the
+    same bf16 layer whose recurrence is the float64 CPU oracle, so the difference is the
+    recurrence's: output, dx and the input-projection gradient (the quantities the reference's
+    layer benchmark compares, scripts/benchmark_gdn.py:58-63)."""
+    from cqgdn import layer
+
+    print("case whole layer: content 300, 120 queries, image groups (40, 24)", flush=True)
+    torch.manual_seed(5)
+    model = layer.GatedDeltaLayer().to(DEV, torch.bfloat16)
+    model.A_log.data = model.A_log.data.float()
+    model.norm_weight.data = model.norm_weight.data.float()
+    plan = layer.cq_layer_plan(300, 120, image_groups=(40, 24), seed=3).to(DEV)
+    gen = torch.Generator().manual_seed(6)
+    x = torch.randn(plan.hidden_length, 1, 2048, generator=gen).bfloat16().to(DEV)
+    up = (torch.randn(plan.hidden_length, 1, 2048, generator=gen) / 100).bfloat16().to(DEV)
+
+    def run(recurrence):
+        model.zero_grad(set_to_none=True)
+        xx = x.clone().requires_grad_()
+        y = model(xx, plan, recurrence=recurrence)
+        (y * up).sum().backward()
+        torch.cuda.synchronize()
+        return y.detach().float().cpu(), xx.grad.float().cpu(), model.in_proj_all.weight.grad.float().cpu()
+
+    def oracle(q, k, v, g, b, p):
+        ins = [t.detach().double().cpu().requires_grad_() for t in (q, k, v, g, b)]
+        out = O.recurrent_delta(*ins, p.event_bounds, normalize=True)
+
+        class Bridge(torch.autograd.Function):  # float64 CPU recurrence inside the bf16 GPU graph
+            @staticmethod
+            def forward(ctx, *dev_ins):
+                return out.detach().to(q.device, q.dtype)
+
+            @staticmethod
+            def backward(ctx, dy):
+                grads = torch.autograd.grad(out, ins, dy.double().cpu())
+                return tuple(gr.to(t.device, t.dtype) for gr, t in zip(grads, (q, k, v, g, b)))
+
+        return Bridge.apply(q, k, v, g, b)
+
+    got, want = run(None), run(oracle)
+    for name, a, b in zip(("y", "dx", "dW_in"), got, want):
+        assert_close_bf16(name, a, b.double())

@@ -128,3 +128,40 @@ def test_bench_refuses_more_than_one_gpu():
                           timeout=120)
     assert proc.returncode == 2
     assert "one GPU" in proc.stderr
+
+
+def test_layer_plan_structure():
+    """Synthetic image-CQ plan: counts of the reference's benchmark rows, each content row written
+    once in order, read-only events write the zero row, the query conv sees earlier content only,
+    every hidden row takes one event's output."""
+    from cqgdn import layer
+
+    for content, queries, events in ((2048, 1675, 4221), (8192, 7819, 16509)):
+        p = layer.cq_layer_plan(content, queries)
+        assert len(p.event_q) == events and p.hidden_length == content + queries
+        writes = p.event_write[p.event_write < content]
+        assert torch.equal(writes, torch.arange(content))
+        assert int((p.event_write == content).sum()) == events - content
+        assert int((p.event_q >= content).sum()) == queries
+        assert p.hidden_event.shape == (content + queries,) and int(p.hidden_event.max()) < events
+        # a query event's conv history holds content written before it
+        first_write = {int(c): e for e, c in enumerate(p.event_write.tolist()) if c < content}
+        for j in range(0, queries, 97):
+            e = int(p.hidden_event[content + j])
+            for c in p.query_history[j].tolist():
+                assert c == content or first_write[c] < e
+
+
+def test_layer_forward_backward_on_cpu_with_oracle_recurrence():
+    """The whole-layer mirror runs fwd+bwd on the CPU with the oracle as its recurrence."""
+    from cqgdn import layer
+
+    torch.manual_seed(0)
+    model = layer.GatedDeltaLayer(width=64, heads=4).double()
+    plan = layer.cq_layer_plan(40, 9, image_groups=(6, 5))
+    x = torch.randn(plan.hidden_length, 1, 64, dtype=torch.float64, requires_grad=True)
+    rec = lambda q, k, v, g, b, p: O.recurrent_delta(q, k, v, g, b, p.event_bounds, normalize=True)
+    y = model(x, plan, recurrence=rec)
+    assert y.shape == x.shape
+    y.square().sum().backward()
+    assert torch.isfinite(x.grad).all() and model.in_proj_all.weight.grad.abs().sum() > 0
