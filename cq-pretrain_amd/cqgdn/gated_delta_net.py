@@ -321,41 +321,59 @@ def l2_bwd(y, rstd, dy):
     return dx
 
 
+@lru_cache(maxsize=64)
+def _conv_bounds(bounds, device):
+    """Device int32 document bounds for the conv kernels, cached per bounds."""
+    return torch.tensor(bounds, dtype=torch.int32).to(device, non_blocking=True)
+
+
 class _Conv(torch.autograd.Function):
-    """Packed depthwise causal conv (kept with the reference's semantics, ops/gated_delta_net.py:252-289)."""
+    """Packed depthwise causal conv1d on the GPU (ops/gated_delta_net.py:252-277): the forward
+    saves only x and the weight; the backward recomputes the pre-activation in the kernel."""
 
     @staticmethod
     def forward(ctx, x, weight, activation, bounds):
-        ctx.save_for_backward(x, weight)
-        ctx.activation, ctx.bounds = activation, bounds
-        return _conv_eval(x, weight, activation, bounds)
+        xf = x.contiguous().reshape(-1, x.shape[-1])
+        w = weight.contiguous()
+        cb = _conv_bounds(bounds, x.device)
+        y = torch.empty_like(xf)
+        call("cqgdn_conv1d_fwd", _ptr(xf), _ptr(w), _ptr(cb), len(bounds) - 1, xf.shape[0], xf.shape[1], w.shape[1],
+             int(activation), _ptr(y), _stream(x.device))
+        ctx.save_for_backward(xf, w)
+        ctx.shape, ctx.bounds, ctx.activation = x.shape, bounds, activation
+        return y.reshape(x.shape)
 
     @staticmethod
     def backward(ctx, dy):
-        x, weight = ctx.saved_tensors
-        with torch.enable_grad():
-            xx, ww = x.detach().requires_grad_(), weight.detach().requires_grad_()
-            y = _conv_eval(xx, ww, ctx.activation, ctx.bounds)
-            dx, dw = torch.autograd.grad(y, (xx, ww), dy)
-        return dx, dw, None, None
-
-
-def _conv_eval(x, weight, activation, bounds):
-    kernel = weight.shape[-1]
-    parts = []
-    for a, b in zip(bounds, bounds[1:]):
-        seg = x[:, a:b].transpose(1, 2)
-        y = F.conv1d(seg, weight[:, None], padding=kernel - 1, groups=x.shape[-1])[..., : b - a]
-        parts.append(y.transpose(1, 2))
-    y = torch.cat(parts, dim=1) if parts else x[:, :0]
-    return F.silu(y) if activation else y
+        xf, w = ctx.saved_tensors
+        dyf = dy.contiguous().reshape(xf.shape)
+        T, C, K = xf.shape[0], xf.shape[1], w.shape[1]
+        dx = torch.empty_like(xf)
+        dw = torch.empty(C, K, dtype=torch.float32, device=xf.device)
+        ws = torch.empty(_lib.lib().cqgdn_conv1d_bwd_workspace_size(T, C, K), dtype=torch.uint8, device=xf.device)
+        cb = _conv_bounds(ctx.bounds, xf.device)
+        call("cqgdn_conv1d_bwd", _ptr(xf), _ptr(w), _ptr(dyf), _ptr(cb), len(ctx.bounds) - 1, T, C, K,
+             int(ctx.activation), _ptr(dx), _ptr(dw), _ptr(ws), ws.numel(), _stream(xf.device))
+        return dx.reshape(ctx.shape), dw.to(w.dtype), None, None
 
 
 def conv(x, weight, *, activation=None, cu_seqlens=None, cu_seqlens_cpu=None):
-    """Causal conv1d over packed documents; weight [channels, kernel] (ops/gated_delta_net.py:280-289)."""
+    """Packed causal conv1d, x [1,T,C] (or [B,T,C] unpacked), weight [C,K] (ops/gated_delta_net.py:280-289).
+
+    Returns ``(y, None)`` like the reference; documents never see each other's rows.
+    """
     if activation not in (None, "silu", "swish"):
         raise ValueError(f"Unsupported activation {activation}")
-    bounds = host_bounds(cu_seqlens, cu_seqlens_cpu) or (0, x.shape[1])
+    if weight.dim() != 2 or weight.shape[0] != x.shape[-1]:
+        raise ValueError("weight must be [channels, kernel]")
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise NotImplementedError("the hip conv kernels compute on bf16 x and weight")
+    _require_gpu(x, weight)
+    bounds = host_bounds(cu_seqlens, cu_seqlens_cpu)
+    if bounds is None:  # unpacked: every batch row is its own document
+        bounds = tuple(i * x.shape[1] for i in range(x.shape[0] + 1))
+    elif x.shape[0] != 1 or bounds[-1] != x.shape[1]:
+        raise ValueError("Packed inputs must have batch 1 and boundaries covering every token")
     return _Conv.apply(x, weight, activation is not None, bounds), None
 
 

@@ -127,15 +127,18 @@ class GatedDeltaLayer(torch.nn.Module):
         for lin in (self.in_proj_all, self.out_proj):
             torch.nn.init.normal_(lin.weight, std=0.02)
 
-    def forward(self, x, plan: LayerPlan, recurrence=None):
-        """``recurrence(q, k, v, g, beta, plan)``, if given, replaces the hip delta (the layer parity
-        test passes a float64 CPU recurrence)."""
+    def forward(self, x, plan: LayerPlan, recurrence=None, conv=None):
+        """``recurrence(q, k, v, g, beta, plan)`` and ``conv(x, weight, bounds)``, if given, replace
+        the hip delta and the hip conv (tests pass float64 CPU restatements)."""
         h, d = self.heads, self.head_dim
         size = h * d
         raw, z, a, beta = self.in_proj_all(x[:, 0]).split((2 * size + size, size, h, h), -1)
         updates = raw.index_select(0, plan.content_order)
-        convolved = gdn.conv(updates[None], self.conv_weight, activation="silu", cu_seqlens=plan.content_cu,
-                             cu_seqlens_cpu=plan.content_bounds)[0][0]
+        if conv is None:
+            convolved = gdn.conv(updates[None], self.conv_weight, activation="silu", cu_seqlens=plan.content_cu,
+                                 cu_seqlens_cpu=plan.content_bounds)[0][0]
+        else:
+            convolved = conv(updates[None], self.conv_weight, plan.content_bounds)[0]
         q, k, v = convolved.split((size, size, size), -1)
         q, k, v = q.reshape(-1, h, d), k.reshape(-1, h, d), v.reshape(-1, h, d)
         # the CQ query conv reads the content history only

@@ -244,4 +244,46 @@ int cqgdn_chunk_local_cumsum(const float* g, float* out, int64_t T, int H, const
   return check_launch("cqgdn_chunk_local_cumsum");
 }
 
+namespace {
+int check_conv(const void* x, const void* w, const int32_t* bounds, int n_docs, int64_t T, int C, int K) {
+  if (T < 0 || n_docs < 0 || C <= 0) return fail(CQGDN_EINVAL, "invalid sizes T=%lld C=%d n_docs=%d", (long long)T, C, n_docs);
+  if (K < 2 || K > 4) return fail(CQGDN_EUNSUPPORTED, "kernel width %d (2..4 supported)", K);
+  if (C % 8) return fail(CQGDN_EUNSUPPORTED, "channels %d not a multiple of 8", C);
+  if (T > INT32_MAX / 2 || (int64_t)C * T > ((int64_t)1 << 40)) return fail(CQGDN_EUNSUPPORTED, "too many rows");
+  if (T > 0 && (!x || !w || !bounds || n_docs == 0)) return fail(CQGDN_EINVAL, "null pointer or no documents");
+  if (!aligned(x, 16)) return fail(CQGDN_EINVAL, "x must be 16-byte aligned");
+  return CQGDN_OK;
+}
+}  // namespace
+
+int cqgdn_conv1d_fwd(const void* x, const void* weight, const int32_t* bounds, int n_docs, int64_t T, int C, int K,
+                     int activation, void* y, void* stream) {
+  if (const int e = check_conv(x, weight, bounds, n_docs, T, C, K)) return e;
+  if (T == 0) return ok();
+  if (!y || !aligned(y, 16)) return fail(CQGDN_EINVAL, "y must be a 16-byte aligned buffer");
+  launch_conv_fwd(static_cast<const bf16*>(x), static_cast<const bf16*>(weight), bounds, n_docs, (int)T, C, K,
+                  activation != 0, static_cast<bf16*>(y), (hipStream_t)stream);
+  return check_launch("cqgdn_conv1d_fwd");
+}
+
+size_t cqgdn_conv1d_bwd_workspace_size(int64_t T, int C, int K) {
+  if (T <= 0 || C <= 0 || K <= 0) return 0;
+  return (size_t)conv_tiles(T) * (size_t)C * (size_t)K * sizeof(float);
+}
+
+int cqgdn_conv1d_bwd(const void* x, const void* weight, const void* dy, const int32_t* bounds, int n_docs, int64_t T,
+                     int C, int K, int activation, void* dx, float* dweight, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+  if (const int e = check_conv(x, weight, bounds, n_docs, T, C, K)) return e;
+  if (T == 0) return ok();
+  if (!dy || !dx || !dweight || !aligned(dy, 16) || !aligned(dx, 16))
+    return fail(CQGDN_EINVAL, "dy/dx/dweight must be non-null (dy, dx 16-byte aligned)");
+  if (!workspace || workspace_bytes < cqgdn_conv1d_bwd_workspace_size(T, C, K))
+    return fail(CQGDN_EINVAL, "workspace smaller than cqgdn_conv1d_bwd_workspace_size");
+  launch_conv_bwd(static_cast<const bf16*>(x), static_cast<const bf16*>(weight), static_cast<const bf16*>(dy), bounds,
+                  n_docs, (int)T, C, K, activation != 0, static_cast<bf16*>(dx), dweight,
+                  static_cast<float*>(workspace), (hipStream_t)stream);
+  return check_launch("cqgdn_conv1d_bwd");
+}
+
 }  // extern "C"

@@ -48,6 +48,12 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream);
 void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* g, const void* beta,
                       bool beta_bf16, float* state, bf16* out, int N, int E, int H, float scale,
                       hipStream_t stream);
+// packed depthwise causal conv1d (gdn_conv.hip); bounds: int32 [n_docs + 1] on the device
+int conv_tiles(int64_t T);
+void launch_conv_fwd(const bf16* x, const bf16* w, const int32_t* bounds, int n_docs, int T, int C, int K, int act,
+                     bf16* y, hipStream_t stream);
+void launch_conv_bwd(const bf16* x, const bf16* w, const bf16* dy, const int32_t* bounds, int n_docs, int T, int C,
+                     int K, int act, bf16* dx, float* dw, float* part, hipStream_t stream);
 void launch_l2norm_fwd(const bf16* x, bf16* y, float* rstd, int64_t rows, hipStream_t stream);
 void launch_l2norm_bwd(const bf16* y, const float* rstd, const bf16* dy, bf16* dx, int64_t rows,
                        hipStream_t stream);

@@ -130,6 +130,27 @@ int cqgdn_l2norm_fwd(const void* x, void* y, float* rstd, int64_t rows, void* st
 int cqgdn_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx, int64_t rows, void* stream);
 
 /*
+ * Packed depthwise causal conv1d (the GatedDelta layer's short conv over the
+ * q/k/v channels).  Replaces the causal_conv1d_fn / causal_conv1d_bwd calls of
+ * conv() (ops/gated_delta_net.py:252-289); semantics of the CPU form
+ * F.conv1d(padding = K - 1) per document (models/backbone_qwen35.py:81-98):
+ *   pre[t][c] = sum_{i<K} w[c][i] * x[t - (K-1) + i][c] over rows of t's document,
+ *   y = silu(pre) if activation != 0, else pre.
+ * x, y, dy, dx: bf16 [T][C], time-first (B = 1), C % 8 == 0, 16-byte aligned;
+ * weight: bf16 [C][K], 2 <= K <= 4; bounds: device int32 [n_docs + 1] document
+ * boundaries (0, ..., T).  The backward recomputes pre from x (nothing is saved
+ * by the forward) and writes dweight fp32 [C][K] through a deterministic
+ * reduction of per-row-tile partials held in the workspace
+ * (>= cqgdn_conv1d_bwd_workspace_size bytes).
+ */
+int cqgdn_conv1d_fwd(const void* x, const void* weight, const int32_t* bounds, int n_docs, int64_t T, int C, int K,
+                     int activation, void* y, void* stream);
+size_t cqgdn_conv1d_bwd_workspace_size(int64_t T, int C, int K);
+int cqgdn_conv1d_bwd(const void* x, const void* weight, const void* dy, const int32_t* bounds, int n_docs, int64_t T,
+                     int C, int K, int activation, void* dx, float* dweight, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/*
  * Chunk-local cumsum of g fp32 [T][H] over the chunk table, forward or reverse
  * (`chunk_local_cumsum` and reverse_cumsum(), ops/gated_delta_net.py:77-87,158-164).
  */

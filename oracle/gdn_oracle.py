@@ -23,6 +23,9 @@ reference's own algorithms:
 * ``decode_step``       - ``models/decoding.py:71-77`` with the value-first state and
                           in-place contract of ``ops/gated_delta_net.py:314-352``
 * ``error_stats``       - ``scripts/validation/delta64_probe.py:90-99``
+* ``causal_conv1d``     - the GatedDelta layer's short conv, the CPU form of
+                          ``models/backbone_qwen35.py:81-98`` (``F.conv1d`` with padding K-1 per
+                          document, optional SiLU) behind ``ops/gated_delta_net.py:252-289``
 
 How each function is pinned (tests/test_oracle.py): closed forms on tiny inputs
 (one event, orthonormal keys, pure decay), chunked == per-event recurrence to
@@ -292,6 +295,24 @@ def chunk_local_cumsum(g, bounds=None, chunk=CHUNK, reverse=False):
         seg = g[:, a:b]
         out[:, a:b] = seg.flip(1).cumsum(1).flip(1) if reverse else seg.cumsum(1)
     return out
+
+
+def causal_conv1d(x, weight, bounds=None, activation=True):
+    """Depthwise causal conv1d over packed documents (models/backbone_qwen35.py:81-98).
+
+    x: [1,T,C] (or [B,T,C] with ``bounds`` None: one document per row); weight: [C,K].
+    Row t of a document sees rows t-K+1 .. t of the same document only.
+    """
+    weight = weight.to(x.dtype)
+    bounds = _bounds(bounds, x.shape[1]) if bounds is not None else None
+    spans = list(zip(bounds, bounds[1:])) if bounds is not None else [(0, x.shape[1])]
+    parts = []
+    for a, b in spans:
+        seg = x[:, a:b].transpose(1, 2)
+        y = torch.nn.functional.conv1d(seg, weight[:, None], padding=weight.shape[1] - 1, groups=x.shape[-1])
+        parts.append(y[..., : b - a].transpose(1, 2))
+    y = torch.cat(parts, dim=1) if parts else x[:, :0]
+    return torch.nn.functional.silu(y) if activation else y
 
 
 def error_stats(actual, expected, tolerance=0.035):

@@ -161,7 +161,8 @@ def test_layer_forward_backward_on_cpu_with_oracle_recurrence():
     plan = layer.cq_layer_plan(40, 9, image_groups=(6, 5))
     x = torch.randn(plan.hidden_length, 1, 64, dtype=torch.float64, requires_grad=True)
     rec = lambda q, k, v, g, b, p: O.recurrent_delta(q, k, v, g, b, p.event_bounds, normalize=True)
-    y = model(x, plan, recurrence=rec)
+    cv = lambda u, w, bounds: O.causal_conv1d(u, w, bounds)
+    y = model(x, plan, recurrence=rec, conv=cv)
     assert y.shape == x.shape
     y.square().sum().backward()
     assert torch.isfinite(x.grad).all() and model.in_proj_all.weight.grad.abs().sum() > 0

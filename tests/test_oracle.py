@@ -283,3 +283,23 @@ def test_planted_backward_mistake_is_caught(monkeypatch):
     torch.testing.assert_close(dv, leaves[2].grad, rtol=1e-9, atol=1e-10)
     wrong_dv = dv / xs[4][..., None]  # the same dv without its beta factor
     assert (wrong_dv - leaves[2].grad).abs().max() > 1e-3
+
+
+def test_causal_conv1d_closed_form_and_documents():
+    """The conv oracle against a scalar loop (row t sees rows t-K+1..t of its own document),
+    with and without SiLU, K = 2..4; a planted off-by-one (seeing the next row) is caught."""
+    gen = torch.Generator().manual_seed(7)
+    for K in (2, 3, 4):
+        x = torch.randn(1, 11, 3, generator=gen, dtype=F64)
+        w = torch.randn(3, K, generator=gen, dtype=F64)
+        bounds = (0, 1, 3, 11)
+        want = torch.zeros_like(x)
+        for a, b in zip(bounds, bounds[1:]):
+            for t in range(a, b):
+                for c in range(3):
+                    want[0, t, c] = sum(w[c, i] * x[0, t - (K - 1) + i, c] for i in range(K) if t - (K - 1) + i >= a)
+        assert torch.allclose(O.causal_conv1d(x, w, bounds, activation=False), want, atol=1e-12)
+        assert torch.allclose(O.causal_conv1d(x, w, bounds), torch.nn.functional.silu(want), atol=1e-12)
+        shifted = torch.zeros_like(x)
+        shifted[:, :-1] = x[:, 1:]
+        assert not torch.allclose(O.causal_conv1d(shifted, w, bounds, activation=False), want, atol=1e-6)
