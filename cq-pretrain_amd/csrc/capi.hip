@@ -268,7 +268,7 @@ int cqgdn_conv1d_fwd(const void* x, const void* weight, const int32_t* bounds, i
 
 size_t cqgdn_conv1d_bwd_workspace_size(int64_t T, int C, int K) {
   if (T <= 0 || C <= 0 || K <= 0) return 0;
-  return (size_t)conv_tiles(T) * (size_t)C * (size_t)K * sizeof(float);
+  return (size_t)conv_strips(T) * (size_t)C * (size_t)K * sizeof(float);
 }
 
 int cqgdn_conv1d_bwd(const void* x, const void* weight, const void* dy, const int32_t* bounds, int n_docs, int64_t T,
@@ -278,8 +278,8 @@ int cqgdn_conv1d_bwd(const void* x, const void* weight, const void* dy, const in
   if (T == 0) return ok();
   if (!dy || !dx || !dweight || !aligned(dy, 16) || !aligned(dx, 16))
     return fail(CQGDN_EINVAL, "dy/dx/dweight must be non-null (dy, dx 16-byte aligned)");
-  if (!workspace || workspace_bytes < cqgdn_conv1d_bwd_workspace_size(T, C, K))
-    return fail(CQGDN_EINVAL, "workspace smaller than cqgdn_conv1d_bwd_workspace_size");
+  if (!workspace || !aligned(workspace, 16) || workspace_bytes < cqgdn_conv1d_bwd_workspace_size(T, C, K))
+    return fail(CQGDN_EINVAL, "workspace must be 16-byte aligned and >= cqgdn_conv1d_bwd_workspace_size bytes");
   launch_conv_bwd(static_cast<const bf16*>(x), static_cast<const bf16*>(weight), static_cast<const bf16*>(dy), bounds,
                   n_docs, (int)T, C, K, activation != 0, static_cast<bf16*>(dx), dweight,
                   static_cast<float*>(workspace), (hipStream_t)stream);

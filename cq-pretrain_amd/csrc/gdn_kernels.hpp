@@ -49,7 +49,7 @@ void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* 
                       bool beta_bf16, float* state, bf16* out, int N, int E, int H, float scale,
                       hipStream_t stream);
 // packed depthwise causal conv1d (gdn_conv.hip); bounds: int32 [n_docs + 1] on the device
-int conv_tiles(int64_t T);
+int conv_strips(int64_t T);  // row strips of the conv backward (dw partials per strip)
 void launch_conv_fwd(const bf16* x, const bf16* w, const int32_t* bounds, int n_docs, int T, int C, int K, int act,
                      bf16* y, hipStream_t stream);
 void launch_conv_bwd(const bf16* x, const bf16* w, const bf16* dy, const int32_t* bounds, int n_docs, int T, int C,

@@ -140,8 +140,8 @@ int cqgdn_l2norm_bwd(const void* y, const float* rstd, const void* dy, void* dx,
  * weight: bf16 [C][K], 2 <= K <= 4; bounds: device int32 [n_docs + 1] document
  * boundaries (0, ..., T).  The backward recomputes pre from x (nothing is saved
  * by the forward) and writes dweight fp32 [C][K] through a deterministic
- * reduction of per-row-tile partials held in the workspace
- * (>= cqgdn_conv1d_bwd_workspace_size bytes).
+ * reduction of per-row-strip partials held in the workspace
+ * (>= cqgdn_conv1d_bwd_workspace_size bytes, 16-byte aligned).
  */
 int cqgdn_conv1d_fwd(const void* x, const void* weight, const int32_t* bounds, int n_docs, int64_t T, int C, int K,
                      int activation, void* y, void* stream);

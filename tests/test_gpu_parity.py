@@ -420,6 +420,8 @@ def test_whole_layer_matches_oracle_recurrence(gdn):
     (200, 128, 2, (0, 200), False),
     (1000, 256, 4, (0, 5, 64, 65, 96, 97, 600, 1000), True),
     (300, 6144, 4, (0, 2, 130, 131, 300), True),
+    (5000, 512, 4, (0, 1234, 1235, 5000), True),  # 40-row strips of the backward
+    (3001, 256, 3, (0, 3001), True),  # strips of 24 rows, K = 3 groups
 ])
 def test_conv1d_matches_oracle(gdn, T, C, K, bounds, act):
     """Packed causal conv1d (fwd, dx, dw) against the float64 oracle: documents of 1-2 rows,
