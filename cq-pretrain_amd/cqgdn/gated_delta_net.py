@@ -21,7 +21,6 @@ from collections import Counter
 from functools import lru_cache
 
 import torch
-from torch.nn import functional as F
 
 from . import _lib
 
@@ -58,11 +57,90 @@ def call(name, *args):
     _lib.check(getattr(_lib.lib(), name)(*args), name)
 
 
-def gated_norm(y, z, weight, eps=1e-6):
-    """RMSNorm(y) * weight * silu(z) (ops/gated_delta_net.py:67-74; unchanged semantics)."""
-    yf = y.float()
-    normed = yf * torch.rsqrt(yf.square().mean(-1, keepdim=True) + eps)
-    return (normed * weight.float() * F.silu(z.float())).to(y.dtype)
+def _rows_view(t, rows, width):
+    """``t`` as [rows, width] with unit channel stride and a constant row stride, without a
+    copy when ``t`` is such a view already (a column slice of a wider projection)."""
+    try:
+        v = t.view(rows, width)
+    except RuntimeError:
+        v = t.reshape(rows, width)
+    if v.stride(1) != 1 or v.stride(0) % 8 or v.data_ptr() % 16:
+        v = v.contiguous()
+    return v
+
+
+class _GatedNorm(torch.autograd.Function):
+    """Gated RMSNorm over D = 128 with an optional fused row gather, on the GPU."""
+
+    @staticmethod
+    def forward(ctx, y, z, weight, eps, index, zero_rows):
+        H = y.shape[-2]
+        yc = y.contiguous()
+        rows = index.numel() if index is not None else yc.numel() // (H * 128)
+        zv = _rows_view(z, rows, H * 128)
+        w = weight.float().contiguous()
+        out = torch.empty(rows, H, 128, dtype=y.dtype, device=y.device)
+        rstd = torch.empty(rows, H, dtype=torch.float32, device=y.device)
+        call("cqgdn_gated_norm_fwd", _ptr(yc), _ptr(index), rows, H, _ptr(zv), zv.stride(0), _ptr(w), float(eps),
+             _ptr(out), _ptr(rstd), _stream(y.device))
+        ctx.save_for_backward(yc, zv, w, rstd, index, zero_rows)
+        ctx.shapes, ctx.wdtype = (y.shape, z.shape), weight.dtype
+        return out if index is not None else out.reshape(y.shape)
+
+    @staticmethod
+    def backward(ctx, dout):
+        yc, zv, w, rstd, index, zero_rows = ctx.saved_tensors
+        rows, H = rstd.shape
+        do = dout.contiguous()
+        dy = torch.empty_like(yc)
+        dz = torch.empty(rows, H * 128, dtype=zv.dtype, device=zv.device)
+        dw = torch.empty(128, dtype=torch.float32, device=zv.device)
+        ws = torch.empty(max(_lib.lib().cqgdn_gated_norm_bwd_workspace_size(rows, H), 16), dtype=torch.uint8,
+                         device=zv.device)
+        n_zero = zero_rows.numel() if zero_rows is not None else 0
+        call("cqgdn_gated_norm_bwd", _ptr(yc), _ptr(index), _ptr(zero_rows), n_zero, rows, H, _ptr(zv), zv.stride(0),
+             _ptr(w), _ptr(rstd), _ptr(do), _ptr(dy), _ptr(dz), dz.stride(0), _ptr(dw), _ptr(ws), ws.numel(),
+             _stream(zv.device))
+        return dy.reshape(ctx.shapes[0]), dz.reshape(ctx.shapes[1]), dw.to(ctx.wdtype), None, None, None
+
+
+def unread_rows(index, y_rows):
+    """Device int32 list of the rows of y that ``index`` never reads (the rows the fused
+    gated_norm backward writes with zeros); checks that ``index`` repeats no row."""
+    real = index[index >= 0].long()
+    counts = torch.bincount(real, minlength=y_rows)
+    if counts.numel() > y_rows or (counts.numel() and int(counts.max()) > 1):
+        raise ValueError("index must hold distinct values in [-1, len(y))")
+    return (counts == 0).nonzero().flatten().to(torch.int32)
+
+
+def gated_norm(y, z, weight, eps=1e-6, *, index=None, zero_rows=None):
+    """RMSNorm(y) * weight * silu(z) over D = 128 (ops/gated_delta_net.py:67-74; CPU form
+    models/backbone_qwen35.py:107-114), y and z bf16 [..., H, 128] on the GPU, computed in fp32.
+
+    ``index`` (device int32 [rows], values in [-1, len(y))) fuses the layer's output gather
+    (models/backbone_qwen35.py:242-246): row r normalizes y[index[r]], and a zero row for -1
+    (a padding row); z is then [rows, H, 128] and may be a column slice of the fused
+    projection.  ``zero_rows`` (from ``unread_rows``, cached per plan by callers) lists the y
+    rows no r reads; it is derived here when omitted.
+    """
+    if y.shape[-1] != 128 or y.dim() < 2:
+        raise ValueError("gated_norm expects y [..., H, 128]")
+    if y.dtype != torch.bfloat16 or z.dtype != torch.bfloat16:
+        raise NotImplementedError("the hip gated_norm kernels compute on bf16 y and z")
+    if weight.shape != (128,):
+        raise ValueError("weight must be [128]")
+    _require_gpu(y, z, weight)
+    if index is None:
+        if z.shape != y.shape:
+            raise ValueError("y and z must have the same shape")
+    else:
+        if y.dim() != 3 or index.dim() != 1 or z.shape != (index.numel(), y.shape[1], 128):
+            raise ValueError("with index, y is [y_rows, H, 128], index [rows] and z [rows, H, 128]")
+        index = index.to(torch.int32)
+        if zero_rows is None:
+            zero_rows = unread_rows(index, y.shape[0])
+    return _GatedNorm.apply(y, z, weight, eps, index, zero_rows)
 
 
 def _require_gpu(*tensors):

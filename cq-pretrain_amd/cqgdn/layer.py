@@ -127,9 +127,10 @@ class GatedDeltaLayer(torch.nn.Module):
         for lin in (self.in_proj_all, self.out_proj):
             torch.nn.init.normal_(lin.weight, std=0.02)
 
-    def forward(self, x, plan: LayerPlan, recurrence=None, conv=None):
-        """``recurrence(q, k, v, g, beta, plan)`` and ``conv(x, weight, bounds)``, if given, replace
-        the hip delta and the hip conv (tests pass float64 CPU restatements)."""
+    def forward(self, x, plan: LayerPlan, recurrence=None, conv=None, norm=None):
+        """``recurrence(q, k, v, g, beta, plan)``, ``conv(x, weight, bounds)`` and
+        ``norm(y, z, weight, eps)``, if given, replace the hip delta, conv and gated norm
+        (tests pass float64 CPU restatements)."""
         h, d = self.heads, self.head_dim
         size = h * d
         raw, z, a, beta = self.in_proj_all(x[:, 0]).split((2 * size + size, size, h, h), -1)
@@ -165,5 +166,8 @@ class GatedDeltaLayer(torch.nn.Module):
         else:
             y = recurrence(q, k, v, g, beta, plan)
         selected = y[0].index_select(0, plan.hidden_event).to(x.dtype)
-        out = gdn.gated_norm(selected, z.reshape(-1, h, d), self.norm_weight, self.eps)
+        if norm is None:
+            out = gdn.gated_norm(selected, z.reshape(-1, h, d), self.norm_weight, self.eps)
+        else:
+            out = norm(selected, z.reshape(-1, h, d), self.norm_weight, self.eps)
         return self.out_proj(out.flatten(-2))[:, None]

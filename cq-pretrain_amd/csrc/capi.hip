@@ -286,4 +286,51 @@ int cqgdn_conv1d_bwd(const void* x, const void* weight, const void* dy, const in
   return check_launch("cqgdn_conv1d_bwd");
 }
 
+size_t cqgdn_gated_norm_bwd_workspace_size(int64_t rows, int H) {
+  if (rows <= 0 || H <= 0) return 0;
+  return (size_t)gnorm_bwd_blocks(rows, H) * CQGDN_HEAD_DIM * sizeof(float);
+}
+
+namespace {
+int check_gnorm(const void* y, int64_t rows, int H, const void* z, int64_t z_stride, const float* weight) {
+  if (rows < 0 || H <= 0) return fail(CQGDN_EINVAL, "invalid sizes rows=%lld H=%d", (long long)rows, H);
+  if (rows > 0 && (!y || !z || !weight)) return fail(CQGDN_EINVAL, "y, z and weight must be non-null");
+  if (z_stride < (int64_t)H * CQGDN_HEAD_DIM || z_stride % 8)
+    return fail(CQGDN_EINVAL, "z_stride=%lld must be >= H*128 and a multiple of 8", (long long)z_stride);
+  if (!aligned(y, 16) || !aligned(z, 16) || !aligned(weight, 16))
+    return fail(CQGDN_EINVAL, "y, z and weight must be 16-byte aligned");
+  return CQGDN_OK;
+}
+}  // namespace
+
+int cqgdn_gated_norm_fwd(const void* y, const int32_t* index, int64_t rows, int H, const void* z, int64_t z_stride,
+                         const float* weight, float eps, void* out, float* rstd, void* stream) {
+  if (const int e = check_gnorm(y, rows, H, z, z_stride, weight)) return e;
+  if (rows == 0) return ok();
+  if (!out || !rstd || !aligned(out, 16)) return fail(CQGDN_EINVAL, "out (16-byte aligned) and rstd must be non-null");
+  launch_gnorm_fwd(static_cast<const bf16*>(y), index, rows, H, static_cast<const bf16*>(z), z_stride, weight, eps,
+                   static_cast<bf16*>(out), rstd, (hipStream_t)stream);
+  return check_launch("cqgdn_gated_norm_fwd");
+}
+
+int cqgdn_gated_norm_bwd(const void* y, const int32_t* index, const int32_t* zero_rows, int64_t n_zero, int64_t rows,
+                         int H, const void* z, int64_t z_stride, const float* weight, const float* rstd,
+                         const void* dout, void* dy, void* dz, int64_t dz_stride, float* dweight, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  if (const int e = check_gnorm(y, rows, H, z, z_stride, weight)) return e;
+  if (n_zero < 0 || (n_zero > 0 && !zero_rows)) return fail(CQGDN_EINVAL, "zero_rows must hold n_zero >= 0 rows");
+  if (rows == 0 && n_zero == 0) return ok();
+  if (!dy || !dz || !dweight || !rstd || !dout || !aligned(dy, 16) || !aligned(dz, 16) || !aligned(dout, 16))
+    return fail(CQGDN_EINVAL, "rstd, dout, dy, dz, dweight must be non-null (dout, dy, dz 16-byte aligned)");
+  if (dz_stride < (int64_t)H * CQGDN_HEAD_DIM || dz_stride % 8)
+    return fail(CQGDN_EINVAL, "dz_stride=%lld must be >= H*128 and a multiple of 8", (long long)dz_stride);
+  if (rows > 0 && (!workspace || !aligned(workspace, 16) ||
+                   workspace_bytes < cqgdn_gated_norm_bwd_workspace_size(rows, H)))
+    return fail(CQGDN_EINVAL, "workspace must be 16-byte aligned and >= cqgdn_gated_norm_bwd_workspace_size bytes");
+  launch_gnorm_bwd(static_cast<const bf16*>(y), index, zero_rows, n_zero, rows, H, static_cast<const bf16*>(z),
+                   z_stride, weight, rstd, static_cast<const bf16*>(dout), static_cast<bf16*>(dy),
+                   static_cast<bf16*>(dz), dz_stride, dweight, static_cast<float*>(workspace), (hipStream_t)stream);
+  return check_launch("cqgdn_gated_norm_bwd");
+}
+
 }  // extern "C"

@@ -106,7 +106,7 @@ __global__ __launch_bounds__(CONV_THREADS) void conv_fwd_kernel(const bf16* __re
 // place in its group, so the windows advance without register moves.  A strip
 // whose rows u0 .. uend-1 hold no document boundary (0 and T included) runs
 // without any per-row document test (DOCS = false).  Each strip writes its dw
-// partials [C][K]; conv_dw_reduce_kernel sums them.
+// partials [C][K]; colsum_kernel sums them.
 constexpr int CONV_STRIPS = 128;  // row strips per 64 * CONV_BWD_CH channels
 constexpr int CONV_BWD_CH = 4;    // channels per thread in the backward
 
@@ -235,12 +235,13 @@ __global__ __launch_bounds__(64) void conv_bwd_kernel(const bf16* __restrict__ x
     for (int k = 0; k < K; ++k) part[ch * K + k] = dwa[k][ch];
 }
 
-// dw[j] = sum over strips of the partials [strips][n] (n % 4 == 0): a lane owns
-// 4 consecutive j (16-byte loads), a workgroup 256 j; its 4 waves sum strips
+// dw[j] = sum over strips of the partials [strips][n] (n % 4 == 0; the conv's dw
+// and the other per-workgroup parameter-gradient partials): a lane owns 4
+// consecutive j (16-byte loads), a workgroup 256 j; its 4 waves sum strips
 // b = wave, wave + 4, ... with 8 loads in flight, and the four sums are added
 // in wave order (fixed order: deterministic).
-__global__ __launch_bounds__(256) void conv_dw_reduce_kernel(const float* __restrict__ part, int strips, int n,
-                                                            float* __restrict__ dw) {
+__global__ __launch_bounds__(256) void colsum_kernel(const float* __restrict__ part, int strips, int n,
+                                                    float* __restrict__ dw) {
   __shared__ f32x4 red[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = (blockIdx.x * 64 + lane) * 4;
@@ -293,8 +294,11 @@ void launch_conv_bwd(const bf16* x, const bf16* w, const bf16* dy, const int32_t
     case 3: hipLaunchKernelGGL(conv_bwd_kernel<3>, grid, dim3(64), 0, stream, x, w, dy, bounds, n_docs, T, C, rows, act, dx, part); break;
     default: hipLaunchKernelGGL(conv_bwd_kernel<4>, grid, dim3(64), 0, stream, x, w, dy, bounds, n_docs, T, C, rows, act, dx, part); break;
   }
-  const int n = C * K;
-  hipLaunchKernelGGL(conv_dw_reduce_kernel, dim3((n / 4 + 63) / 64), dim3(256), 0, stream, part, strips, n, dw);
+  launch_colsum(part, strips, C * K, dw, stream);
+}
+
+void launch_colsum(const float* part, int parts, int n, float* out, hipStream_t stream) {
+  hipLaunchKernelGGL(colsum_kernel, dim3((n / 4 + 63) / 64), dim3(256), 0, stream, part, parts, n, out);
 }
 
 }  // namespace cqgdn

@@ -54,6 +54,15 @@ void launch_conv_fwd(const bf16* x, const bf16* w, const int32_t* bounds, int n_
                      bf16* y, hipStream_t stream);
 void launch_conv_bwd(const bf16* x, const bf16* w, const bf16* dy, const int32_t* bounds, int n_docs, int T, int C,
                      int K, int act, bf16* dx, float* dw, float* part, hipStream_t stream);
+// out[j] = sum over p < parts of part[p][j], fixed order (gdn_conv.hip); n % 4 == 0, 16-byte aligned part
+void launch_colsum(const float* part, int parts, int n, float* out, hipStream_t stream);
+// gated RMSNorm over D = 128 with an optional row gather (gdn_glue.hip)
+int gnorm_bwd_blocks(int64_t rows, int H);  // workgroups of the backward (dw partials per workgroup)
+void launch_gnorm_fwd(const bf16* y, const int32_t* index, int64_t rows, int H, const bf16* z, int64_t z_stride,
+                      const float* w, float eps, bf16* out, float* rstd, hipStream_t stream);
+void launch_gnorm_bwd(const bf16* y, const int32_t* index, const int32_t* zero_rows, int64_t n_zero, int64_t rows,
+                      int H, const bf16* z, int64_t z_stride, const float* w, const float* rstd, const bf16* dout,
+                      bf16* dy, bf16* dz, int64_t dz_stride, float* dw, float* wpart, hipStream_t stream);
 void launch_l2norm_fwd(const bf16* x, bf16* y, float* rstd, int64_t rows, hipStream_t stream);
 void launch_l2norm_bwd(const bf16* y, const float* rstd, const bf16* dy, bf16* dx, int64_t rows,
                        hipStream_t stream);

@@ -151,6 +151,37 @@ int cqgdn_conv1d_bwd(const void* x, const void* weight, const void* dy, const in
                      void* stream);
 
 /*
+ * Gated RMSNorm over D = 128 fused with the layer's output gather.  Replaces
+ * gated_norm() (ops/gated_delta_net.py:67-74; CPU form GatedNorm.forward,
+ * models/backbone_qwen35.py:107-114) applied to y.index_select(0, hidden_event)
+ * with the padding rows zeroed (models/backbone_qwen35.py:242-246):
+ *   x = index ? (index[r] >= 0 ? y[index[r]][h] : 0) : y[r][h]
+ *   out[r][h] = x * rsqrt(mean(x^2) + eps) * weight * silu(z[r][h])
+ * y: bf16 [y_rows][H][128]; index: NULL or device int32 [rows], each value in
+ * [-1, y_rows) (-1: a padding row); z: bf16 rows of H*128 channels, z_stride
+ * elements apart (a column slice of the layer's fused projection is accepted);
+ * weight: fp32 [128]; out: bf16 [rows][H][128]; rstd: fp32 [rows][H], kept for
+ * the backward.  Computed in fp32 with one rounding of out.
+ */
+int cqgdn_gated_norm_fwd(const void* y, const int32_t* index, int64_t rows, int H, const void* z, int64_t z_stride,
+                         const float* weight, float eps, void* out, float* rstd, void* stream);
+/*
+ * Backward of cqgdn_gated_norm_fwd.  Row index[r] of dy bf16 [y_rows][H][128]
+ * receives row r's gradient (index must not repeat a value >= 0), and each of
+ * the n_zero rows listed in zero_rows (device int32: the y rows no r reads) is
+ * written with zeros, so that every dy row is written once and no atomics are
+ * needed; without index, dy row r is row r's gradient.  dz: bf16 rows at
+ * dz_stride elements; dweight: fp32 [128] through a deterministic reduction of
+ * per-workgroup partials held in the workspace (>= the size below, 16-byte
+ * aligned).
+ */
+size_t cqgdn_gated_norm_bwd_workspace_size(int64_t rows, int H);
+int cqgdn_gated_norm_bwd(const void* y, const int32_t* index, const int32_t* zero_rows, int64_t n_zero, int64_t rows,
+                         int H, const void* z, int64_t z_stride, const float* weight, const float* rstd,
+                         const void* dout, void* dy, void* dz, int64_t dz_stride, float* dweight, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/*
  * Chunk-local cumsum of g fp32 [T][H] over the chunk table, forward or reverse
  * (`chunk_local_cumsum` and reverse_cumsum(), ops/gated_delta_net.py:77-87,158-164).
  */

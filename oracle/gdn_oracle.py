@@ -26,6 +26,8 @@ reference's own algorithms:
 * ``causal_conv1d``     - the GatedDelta layer's short conv, the CPU form of
                           ``models/backbone_qwen35.py:81-98`` (``F.conv1d`` with padding K-1 per
                           document, optional SiLU) behind ``ops/gated_delta_net.py:252-289``
+* ``gated_rms_norm``    - the layer's gated norm, ``models/backbone_qwen35.py:107-114`` behind
+                          ``ops/gated_delta_net.py:67-74``
 
 How each function is pinned (tests/test_oracle.py): closed forms on tiny inputs
 (one event, orthonormal keys, pure decay), chunked == per-event recurrence to
@@ -313,6 +315,14 @@ def causal_conv1d(x, weight, bounds=None, activation=True):
         parts.append(y[..., : b - a].transpose(1, 2))
     y = torch.cat(parts, dim=1) if parts else x[:, :0]
     return torch.nn.functional.silu(y) if activation else y
+
+
+def gated_rms_norm(y, z, weight, eps=1e-6):
+    """RMSNorm over the last dimension, times weight and silu(z): the CPU form of the layer's
+    gated norm (models/backbone_qwen35.py:107-114), behind gated_norm (ops/gated_delta_net.py:67-74)."""
+    y, z = y.double(), z.double()
+    normalized = y * torch.rsqrt(y.square().mean(-1, keepdim=True) + eps)
+    return normalized * weight.double() * torch.nn.functional.silu(z)
 
 
 def error_stats(actual, expected, tolerance=0.035):

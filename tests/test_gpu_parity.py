@@ -463,3 +463,63 @@ def test_conv1d_deterministic_and_unpacked(gdn):
         assert torch.equal(a, b)
     yr = O.causal_conv1d(x.cpu().double(), w.cpu().double(), None)
     assert_close_bf16("y unpacked", outs[0][0].cpu(), yr)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_gated_norm_matches_oracle(gdn, fused):
+    """The gated RMSNorm against the float64 oracle and its autograd: plain, and fused with a
+    row gather (padding rows -1, y rows no row reads, z a column slice of a wider projection)."""
+    gen = torch.Generator().manual_seed(21 + fused)
+    H, y_rows = 4, 50
+    y = torch.randn(y_rows, H, 128, generator=gen).bfloat16()
+    w = (1 + 0.2 * torch.randn(128, generator=gen)).float()
+    if fused:
+        perm = torch.randperm(y_rows, generator=gen)[:37]
+        index = torch.cat((perm[:20], torch.tensor([-1, -1]), perm[20:])).to(torch.int32)
+        rows = index.numel()
+        proj = torch.randn(rows, 3 * H * 128 + 40, generator=gen).bfloat16()
+        z = proj[:, H * 128:2 * H * 128].reshape(rows, H, 128)  # strided rows
+    else:
+        index, rows = None, y_rows
+        z = torch.randn(y_rows, H, 128, generator=gen).bfloat16()
+    dout = torch.randn(rows, H, 128, generator=gen).bfloat16()
+    yd, wd = y.to(DEV).requires_grad_(), w.to(DEV).requires_grad_()
+    zsrc = (proj if fused else z).to(DEV).requires_grad_()
+    zd = zsrc[:, H * 128:2 * H * 128].reshape(rows, H, 128) if fused else zsrc
+    out = gdn.gated_norm(yd, zd, wd, index=index.to(DEV) if fused else None)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    yr, zr, wr = y.double().requires_grad_(), z.double().requires_grad_(), w.double().requires_grad_()
+    if fused:
+        gathered = torch.where((index >= 0)[:, None, None], yr[index.clamp(min=0).long()], torch.zeros_like(yr[:1]))
+    else:
+        gathered = yr
+    ref = O.gated_rms_norm(gathered, zr, wr)
+    ref.backward(dout.double())
+    assert_close_bf16("out", out.detach().cpu(), ref.detach())
+    assert_close_bf16("dy", yd.grad.cpu(), yr.grad)
+    dz = zsrc.grad.cpu()
+    if fused:
+        assert dz[:, :H * 128].abs().max() == 0 and dz[:, 2 * H * 128:].abs().max() == 0
+        dz = dz[:, H * 128:2 * H * 128].reshape(rows, H, 128)
+        unread = sorted(set(range(y_rows)) - set(index[index >= 0].tolist()))
+        assert yd.grad[unread].abs().max().item() == 0  # rows no one reads get zero gradients
+    assert_close_bf16("dz", dz, zr.grad)
+    assert_close_bf16("dweight", wd.grad.cpu(), wr.grad)
+
+
+def test_gated_norm_backward_deterministic(gdn):
+    """Two backward passes of the fused gated norm are bitwise equal (fixed-order dweight)."""
+    gen = torch.Generator().manual_seed(5)
+    y = torch.randn(3000, 16, 128, generator=gen).bfloat16().to(DEV)
+    z = torch.randn(3000, 16, 128, generator=gen).bfloat16().to(DEV)
+    w = torch.randn(128, generator=gen).to(DEV)
+    dout = torch.randn(3000, 16, 128, generator=gen).bfloat16().to(DEV)
+    grads = []
+    for _ in range(2):
+        yd, zd, wd = y.clone().requires_grad_(), z.clone().requires_grad_(), w.clone().requires_grad_()
+        gdn.gated_norm(yd, zd, wd).backward(dout)
+        grads.append((yd.grad, zd.grad, wd.grad))
+    torch.cuda.synchronize()
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)

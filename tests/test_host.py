@@ -162,7 +162,7 @@ def test_layer_forward_backward_on_cpu_with_oracle_recurrence():
     x = torch.randn(plan.hidden_length, 1, 64, dtype=torch.float64, requires_grad=True)
     rec = lambda q, k, v, g, b, p: O.recurrent_delta(q, k, v, g, b, p.event_bounds, normalize=True)
     cv = lambda u, w, bounds: O.causal_conv1d(u, w, bounds)
-    y = model(x, plan, recurrence=rec, conv=cv)
+    y = model(x, plan, recurrence=rec, conv=cv, norm=O.gated_rms_norm)
     assert y.shape == x.shape
     y.square().sum().backward()
     assert torch.isfinite(x.grad).all() and model.in_proj_all.weight.grad.abs().sum() > 0

@@ -303,3 +303,21 @@ def test_causal_conv1d_closed_form_and_documents():
         shifted = torch.zeros_like(x)
         shifted[:, :-1] = x[:, 1:]
         assert not torch.allclose(O.causal_conv1d(shifted, w, bounds, activation=False), want, atol=1e-6)
+
+
+def test_gated_rms_norm_against_library_and_closed_form():
+    """The gated-norm oracle against torch's own rms_norm times silu (a library routine) and the
+    closed form of a constant row (x = c: the norm is c / sqrt(c^2 + eps)); a planted mistake
+    (normalizing over the sum instead of the mean) is caught."""
+    gen = torch.Generator().manual_seed(11)
+    y = torch.randn(5, 3, 128, generator=gen, dtype=F64)
+    z = torch.randn(5, 3, 128, generator=gen, dtype=F64)
+    w = torch.randn(128, generator=gen, dtype=F64)
+    want = torch.nn.functional.rms_norm(y, (128,), w, eps=1e-6) * torch.nn.functional.silu(z)
+    assert torch.allclose(O.gated_rms_norm(y, z, w), want, atol=1e-12)
+    c = torch.full((1, 128), -0.25, dtype=F64)
+    ones = torch.ones(128, dtype=F64)
+    closed = -0.25 / (0.0625 + 1e-6) ** 0.5 * torch.nn.functional.silu(z[0, :1])
+    assert torch.allclose(O.gated_rms_norm(c, z[0, :1], ones), closed, atol=1e-12)
+    planted = y * torch.rsqrt(y.square().sum(-1, keepdim=True) + 1e-6) * w * torch.nn.functional.silu(z)
+    assert not torch.allclose(planted, want, atol=1e-3)
