@@ -183,23 +183,28 @@ def layer_case(torch, device, content, queries, iterations=12):
     x = torch.randn(plan.hidden_length, 1, 2048, device=device, dtype=torch.bfloat16, requires_grad=True)
     upstream = torch.randn_like(x) / 100
 
-    def step():
-        model.zero_grad(set_to_none=True)
-        x.grad = None
-        y = model(x, plan)
-        (y * upstream).sum().backward()
+    def timed(fused):
+        def step():
+            model.zero_grad(set_to_none=True)
+            x.grad = None
+            y = model(x, plan, fused=fused)
+            (y * upstream).sum().backward()
 
-    for _ in range(3):
-        step()
-    durations = []
-    for _ in range(iterations):
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        step()
-        torch.cuda.synchronize()
-        durations.append((time.perf_counter() - t0) * 1e3)
+        for _ in range(3):
+            step()
+        durations = []
+        for _ in range(iterations):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            step()
+            torch.cuda.synchronize()
+            durations.append((time.perf_counter() - t0) * 1e3)
+        return round(statistics.median(durations), 4)
+
+    # fused: everything between the projections in the fused kernels (events.layer_core);
+    # torch_glue: the reference's torch code around the hip delta, conv and gated norm
     return dict(content_tokens=content, query_tokens=queries, events=len(plan.event_q),
-                median_ms=round(statistics.median(durations), 4))
+                median_ms=timed(True), torch_glue_median_ms=timed(False))
 
 
 COPY_BYTES = 256 << 20

@@ -42,9 +42,25 @@ SIGNATURES = {
     "cqgdn_gated_norm_fwd": (_I, [_P, _P, _I64, _I, _P, _I64, _P, _F, _P, _P, _P]),
     "cqgdn_gated_norm_bwd_workspace_size": (_SZ, [_I64, _I]),
     "cqgdn_gated_norm_bwd": (_I, [_P, _P, _P, _I64, _I64, _I, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _SZ, _P]),
+    "cqgdn_event_inputs_fwd_workspace_size": (_SZ, [_I, _I]),
+    "cqgdn_event_inputs_fwd": (_I, [_P, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "cqgdn_event_inputs_bwd_workspace_size": (_SZ, [_I, _I, _I, _I]),
+    "cqgdn_event_inputs_bwd": (_I, [_P, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+                                    _P, _I64, _P, _I64, _P, _P, _P, _SZ, _P]),
     "cqgdn_timer_arm": (_I, [ctypes.c_char_p, _I]),
     "cqgdn_timer_read": (_I, [_P, _I, _P]),
 }
+class EventPlan(ctypes.Structure):
+    """struct cqgdn_event_plan of include/cqgdn.h."""
+
+    _fields_ = [("n_content", ctypes.c_int32), ("n_queries", ctypes.c_int32), ("n_events", ctypes.c_int32),
+                ("conv_kernel", ctypes.c_int32), ("content_order", _P), ("event_q", _P), ("event_write", _P),
+                ("query_source", _P), ("query_history", _P), ("content_bounds", _P),
+                ("n_content_docs", ctypes.c_int32), ("n_history_rows", ctypes.c_int32), ("q_ptr", _P),
+                ("q_list", _P), ("write_event", _P), ("query_event", _P), ("history_ptr", _P),
+                ("history_list", _P), ("history_rows", _P)]
+
+
 KERNELS = ("fwd_prep", "fwd_scan", "fwd_out", "bwd_local", "bwd_scan", "bwd_dqk", "bwd_wy", "recurrent")
 
 _LIB = None

@@ -265,20 +265,25 @@ class _Delta(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         v, g, beta, ws = ctx.saved_tensors
-        t, h = v.shape[1], v.shape[2]
-        cu, table, doc = device_metadata(ctx.bounds, str(v.device))
-        n_chunks, n_docs = table.shape[0], len(ctx.bounds) - 1
-        dy = dy.reshape(v.shape).to(v.dtype).contiguous()
-        bws = torch.empty(_lib.lib().cqgdn_bwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=v.device)
-        dq, dk, dv = torch.empty_like(v), torch.empty_like(v), torch.empty_like(v)
-        dg, db = torch.empty_like(g), torch.empty_like(beta)
-        flags = (_lib.NORMALIZE if ctx.normalize else 0) | _lib.TRAINING
-        call("cqgdn_bwd", _ptr(v), _ptr(g), _ptr(beta), _ptr(dy), t, h, _ptr(table), n_chunks, _ptr(doc), n_docs,
-             float(ctx.scale), flags, _ptr(ws), ws.numel(), _ptr(bws), bws.numel(), _ptr(dq), _ptr(dk), _ptr(dv),
-             _ptr(dg), _ptr(db), _stream(v.device))
-        grads = [x.reshape(shape).to(dtype)
-                 for x, shape, dtype in zip((dq, dk, dv, dg, db), ctx.shapes, ctx.input_dtypes)]
+        grads = _backward(v, g, beta, ws, dy, ctx.bounds, ctx.normalize, ctx.scale)
+        grads = [x.reshape(shape).to(dtype) for x, shape, dtype in zip(grads, ctx.shapes, ctx.input_dtypes)]
         return *grads, None, None, None
+
+
+def _backward(v, g, beta, ws, dy, bounds, normalize, scale):
+    """dq, dk, dv, dg, dbeta of the packed chunked forward whose TRAINING workspace is ``ws``."""
+    t, h = v.shape[1], v.shape[2]
+    cu, table, doc = device_metadata(bounds, str(v.device))
+    n_chunks, n_docs = table.shape[0], len(bounds) - 1
+    dy = dy.reshape(v.shape).to(v.dtype).contiguous()
+    bws = torch.empty(_lib.lib().cqgdn_bwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=v.device)
+    dq, dk, dv = torch.empty_like(v), torch.empty_like(v), torch.empty_like(v)
+    dg, db = torch.empty_like(g), torch.empty_like(beta)
+    flags = (_lib.NORMALIZE if normalize else 0) | _lib.TRAINING
+    call("cqgdn_bwd", _ptr(v), _ptr(g), _ptr(beta), _ptr(dy), t, h, _ptr(table), n_chunks, _ptr(doc), n_docs,
+         float(scale), flags, _ptr(ws), ws.numel(), _ptr(bws), bws.numel(), _ptr(dq), _ptr(dk), _ptr(dv),
+         _ptr(dg), _ptr(db), _stream(v.device))
+    return dq, dk, dv, dg, db
 
 
 def delta(

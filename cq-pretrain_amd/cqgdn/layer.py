@@ -5,9 +5,10 @@ The reference publishes GDN timings for the whole layer at width 2048
 content, the CQ query conv from the content history, the event gathers, the
 gates, the recurrence, the output gather, gated RMSNorm and out_proj.
 ``GatedDeltaLayer`` follows that forward (models/backbone_qwen35.py:156-246,
-the training path without a state cache) with this package's ``delta`` as the
-recurrence and plain torch for everything around it: the reference keeps the
-conv, the norm and the planning unchanged when ``gdn_backend`` switches.
+the training path without a state cache).  By default everything between the
+two projections runs in the fused kernels of ``events.layer_core``; with
+``fused=False`` it is the reference's torch code around this package's
+``delta``, ``conv`` and ``gated_norm``.
 
 ``cq_layer_plan`` builds a synthetic single-document event plan with the
 structure of ops/gated_delta_layout.py:56-176 (content writes in sigma order,
@@ -24,6 +25,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from . import events
 from . import gated_delta_net as gdn
 
 
@@ -110,6 +112,33 @@ def cq_layer_plan(content: int, queries: int, image_groups=(249, 249), kernel: i
     )
 
 
+def concat_plans(*plans: LayerPlan) -> LayerPlan:
+    """Pack single-document plans into one plan of several documents (the layout
+    ops/gated_delta_layout.py:105-150 produces for a packed batch): hidden rows, content
+    rows, queries and events of each plan follow those of the plans before it."""
+    n_c = sum(len(p.content_order) for p in plans)
+    n_q = sum(len(p.query_source) for p in plans)
+    fields = {k: [] for k in ("content_order", "event_q", "event_write", "query_source", "query_history",
+                              "hidden_event")}
+    cb, eb = [0], [0]
+    h0 = c0 = q0 = e0 = 0
+    for p in plans:
+        pc, pq, pe = len(p.content_order), len(p.query_source), len(p.event_q)
+        content = lambda t: torch.where(t < pc, t + c0, torch.full_like(t, n_c))
+        fields["content_order"].append(p.content_order + h0)
+        fields["event_q"].append(torch.where(p.event_q < pc, p.event_q + c0, p.event_q - pc + n_c + q0))
+        fields["event_write"].append(content(p.event_write))
+        fields["query_source"].append(p.query_source + h0)
+        fields["query_history"].append(content(p.query_history))
+        fields["hidden_event"].append(p.hidden_event + e0)
+        h0, c0, q0, e0 = h0 + p.hidden_length, c0 + pc, q0 + pq, e0 + pe
+        cb.append(c0)
+        eb.append(e0)
+    cat = {k: torch.cat(v) for k, v in fields.items()}
+    return LayerPlan(content_cu=torch.tensor(cb, dtype=torch.int32), content_bounds=tuple(cb),
+                     event_cu=torch.tensor(eb, dtype=torch.long), event_bounds=tuple(eb), hidden_length=h0, **cat)
+
+
 class GatedDeltaLayer(torch.nn.Module):
     """GatedDelta with fused projections (models/backbone_qwen35.py:121-154), one TP rank."""
 
@@ -127,13 +156,24 @@ class GatedDeltaLayer(torch.nn.Module):
         for lin in (self.in_proj_all, self.out_proj):
             torch.nn.init.normal_(lin.weight, std=0.02)
 
-    def forward(self, x, plan: LayerPlan, recurrence=None, conv=None, norm=None):
-        """``recurrence(q, k, v, g, beta, plan)``, ``conv(x, weight, bounds)`` and
-        ``norm(y, z, weight, eps)``, if given, replace the hip delta, conv and gated norm
-        (tests pass float64 CPU restatements)."""
+    def forward(self, x, plan: LayerPlan, recurrence=None, conv=None, norm=None, fused=True):
+        """x [rows, 1, width] -> [rows, 1, width].  See ``core`` for the hooks and ``fused``."""
+        proj = self.in_proj_all(x[:, 0])
+        return self.out_proj(self.core(proj, plan, recurrence, conv, norm, fused))[:, None]
+
+    def core(self, proj, plan: LayerPlan, recurrence=None, conv=None, norm=None, fused=True):
+        """Everything between the projections: proj [rows, 4S + 2H] -> gated-norm rows [rows, S].
+
+        With ``fused`` and no hooks this is ``events.layer_core`` (the fused HIP kernels).
+        Otherwise it is the reference's torch code with the hip delta, conv and gated norm, which
+        ``recurrence(q, k, v, g, beta, plan)``, ``conv(x, weight, bounds)`` and
+        ``norm(y, z, weight, eps)`` replace when given (tests pass float64 CPU restatements)."""
         h, d = self.heads, self.head_dim
         size = h * d
-        raw, z, a, beta = self.in_proj_all(x[:, 0]).split((2 * size + size, size, h, h), -1)
+        if fused and recurrence is None and conv is None and norm is None:
+            return events.layer_core(proj, self.conv_weight, self.A_log, self.dt_bias, self.norm_weight, plan,
+                                     heads=h, eps=self.eps)
+        raw, z, a, beta = proj.split((2 * size + size, size, h, h), -1)
         updates = raw.index_select(0, plan.content_order)
         if conv is None:
             convolved = gdn.conv(updates[None], self.conv_weight, activation="silu", cu_seqlens=plan.content_cu,
@@ -165,9 +205,9 @@ class GatedDeltaLayer(torch.nn.Module):
                           cu_seqlens_cpu=plan.event_bounds)[0]
         else:
             y = recurrence(q, k, v, g, beta, plan)
-        selected = y[0].index_select(0, plan.hidden_event).to(x.dtype)
+        selected = y[0].index_select(0, plan.hidden_event).to(proj.dtype)
         if norm is None:
             out = gdn.gated_norm(selected, z.reshape(-1, h, d), self.norm_weight, self.eps)
         else:
             out = norm(selected, z.reshape(-1, h, d), self.norm_weight, self.eps)
-        return self.out_proj(out.flatten(-2))[:, None]
+        return out.flatten(-2)

@@ -261,8 +261,8 @@ int cqgdn_conv1d_fwd(const void* x, const void* weight, const int32_t* bounds, i
   if (const int e = check_conv(x, weight, bounds, n_docs, T, C, K)) return e;
   if (T == 0) return ok();
   if (!y || !aligned(y, 16)) return fail(CQGDN_EINVAL, "y must be a 16-byte aligned buffer");
-  launch_conv_fwd(static_cast<const bf16*>(x), static_cast<const bf16*>(weight), bounds, n_docs, (int)T, C, K,
-                  activation != 0, static_cast<bf16*>(y), (hipStream_t)stream);
+  launch_conv_fwd(static_cast<const bf16*>(x), nullptr, C, static_cast<const bf16*>(weight), bounds, n_docs, (int)T, C,
+                  K, activation != 0, static_cast<bf16*>(y), (hipStream_t)stream);
   return check_launch("cqgdn_conv1d_fwd");
 }
 
@@ -280,9 +280,9 @@ int cqgdn_conv1d_bwd(const void* x, const void* weight, const void* dy, const in
     return fail(CQGDN_EINVAL, "dy/dx/dweight must be non-null (dy, dx 16-byte aligned)");
   if (!workspace || !aligned(workspace, 16) || workspace_bytes < cqgdn_conv1d_bwd_workspace_size(T, C, K))
     return fail(CQGDN_EINVAL, "workspace must be 16-byte aligned and >= cqgdn_conv1d_bwd_workspace_size bytes");
-  launch_conv_bwd(static_cast<const bf16*>(x), static_cast<const bf16*>(weight), static_cast<const bf16*>(dy), bounds,
-                  n_docs, (int)T, C, K, activation != 0, static_cast<bf16*>(dx), dweight,
-                  static_cast<float*>(workspace), (hipStream_t)stream);
+  launch_conv_bwd(static_cast<const bf16*>(x), nullptr, C, static_cast<const bf16*>(weight),
+                  static_cast<const bf16*>(dy), bounds, n_docs, (int)T, C, K, activation != 0, static_cast<bf16*>(dx),
+                  C, dweight, static_cast<float*>(workspace), (hipStream_t)stream);
   return check_launch("cqgdn_conv1d_bwd");
 }
 
@@ -331,6 +331,120 @@ int cqgdn_gated_norm_bwd(const void* y, const int32_t* index, const int32_t* zer
                    z_stride, weight, rstd, static_cast<const bf16*>(dout), static_cast<bf16*>(dy),
                    static_cast<bf16*>(dz), dz_stride, dweight, static_cast<float*>(workspace), (hipStream_t)stream);
   return check_launch("cqgdn_gated_norm_bwd");
+}
+
+namespace {
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+int ev_args(const cqgdn_event_plan* p, int H, const void* raw, int64_t raw_stride, const void* a, int64_t a_stride,
+            const void* b, int64_t b_stride, const void* w, const float* A_log, const float* dt_bias, EvArgs& out) {
+  if (!p) return fail(CQGDN_EINVAL, "plan is null");
+  if (H != 4 && H != 8 && H != 16 && H != 32) return fail(CQGDN_EINVAL, "H=%d: supported local heads are 4, 8, 16, 32", H);
+  if (p->n_content < 0 || p->n_queries < 0 || p->n_events < 0 || p->n_content_docs < 0 || p->n_history_rows < 0)
+    return fail(CQGDN_EINVAL, "negative plan sizes");
+  if (p->conv_kernel < 2 || p->conv_kernel > 4) return fail(CQGDN_EINVAL, "conv_kernel=%d not in 2..4", p->conv_kernel);
+  const int64_t S = (int64_t)H * CQGDN_HEAD_DIM;
+  if (raw_stride < 3 * S || raw_stride % 8) return fail(CQGDN_EINVAL, "raw_stride must be >= 3*H*128 and a multiple of 8");
+  if (a_stride < H || b_stride < H) return fail(CQGDN_EINVAL, "a_stride and b_stride must be >= H");
+  if (!raw || !a || !b || !w || !A_log || !dt_bias || !aligned(raw, 16))
+    return fail(CQGDN_EINVAL, "raw (16-byte aligned), a, b, conv_weight, A_log, dt_bias must be non-null");
+  if (p->n_events > 0 && (!p->event_q || !p->event_write))
+    return fail(CQGDN_EINVAL, "event_q and event_write are null");
+  if (p->n_content > 0 && (!p->content_order || !p->content_bounds || p->n_content_docs < 1 || !p->q_ptr ||
+                           !p->q_list || !p->write_event || !p->history_ptr || !p->history_list))
+    return fail(CQGDN_EINVAL, "content index arrays are null");
+  if (p->n_queries > 0 && (!p->query_source || !p->query_history || !p->query_event))
+    return fail(CQGDN_EINVAL, "query index arrays are null");
+  if (p->n_history_rows > 0 && !p->history_rows) return fail(CQGDN_EINVAL, "history_rows is null");
+  out = EvArgs{H, p->conv_kernel, p->n_content, p->n_queries, p->n_events, p->n_history_rows,
+               p->content_order, p->event_q, p->event_write, p->query_source, p->query_history,
+               p->q_ptr, p->q_list, p->write_event, p->query_event, p->history_ptr, p->history_list,
+               p->history_rows, static_cast<const bf16*>(raw), raw_stride, static_cast<const bf16*>(a), a_stride,
+               static_cast<const bf16*>(b), b_stride, static_cast<const bf16*>(w), A_log, dt_bias};
+  return CQGDN_OK;
+}
+}  // namespace
+
+size_t cqgdn_event_inputs_fwd_workspace_size(int n_content, int H) {
+  if (n_content < 0 || H <= 0) return 0;
+  return align256((size_t)n_content * 3 * H * CQGDN_HEAD_DIM * sizeof(bf16)) + 256;
+}
+
+int cqgdn_event_inputs_fwd(const cqgdn_event_plan* plan, int H, const void* raw, int64_t raw_stride, const void* a,
+                           int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
+                           const float* A_log, const float* dt_bias, void* q, void* k, void* v, float* g, float* beta,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  EvArgs ea;
+  if (const int e = ev_args(plan, H, raw, raw_stride, a, a_stride, b, b_stride, conv_weight, A_log, dt_bias, ea))
+    return e;
+  if (plan->n_events > 0 && (!q || !k || !v || !g || !beta || !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16)))
+    return fail(CQGDN_EINVAL, "q, k, v (16-byte aligned), g, beta must be non-null");
+  if (!workspace || !aligned(workspace, 256) ||
+      workspace_bytes < cqgdn_event_inputs_fwd_workspace_size(plan->n_content, H))
+    return fail(CQGDN_EINVAL, "workspace must be 256-byte aligned and >= cqgdn_event_inputs_fwd_workspace_size");
+  const int S = H * CQGDN_HEAD_DIM;
+  bf16* conv = static_cast<bf16*>(workspace);
+  hipStream_t st = (hipStream_t)stream;
+  if (plan->n_content > 0)
+    launch_conv_fwd(ea.raw, ea.order, raw_stride, ea.w, plan->content_bounds, plan->n_content_docs, plan->n_content,
+                    3 * S, plan->conv_kernel, 1, conv, st);
+  launch_events_fwd(ea, conv, static_cast<bf16*>(q), static_cast<bf16*>(k), static_cast<bf16*>(v), g, beta, st);
+  return check_launch("cqgdn_event_inputs_fwd");
+}
+
+namespace {
+struct EvLayout {
+  size_t dconv, dpre, gpart, qpart, cpart, qsum, total;
+};
+EvLayout ev_layout(int n_content, int n_queries, int H, int K) {
+  const size_t S = (size_t)H * CQGDN_HEAD_DIM;
+  EvLayout l{};
+  size_t o = 0;
+  l.dconv = o; o += align256((size_t)n_content * 3 * S * sizeof(bf16));
+  l.dpre = o; o += align256((size_t)n_queries * S * sizeof(float));
+  l.gpart = o; o += align256((size_t)n_content * 2 * H * sizeof(float));
+  l.qpart = o; o += align256((size_t)events_query_blocks(n_queries) * S * K * sizeof(float));
+  l.cpart = o; o += align256((size_t)(n_content > 0 ? conv_strips(n_content) : 0) * 3 * S * K * sizeof(float));
+  l.qsum = o; o += align256(S * K * sizeof(float));
+  l.total = o + 256;
+  return l;
+}
+}  // namespace
+
+size_t cqgdn_event_inputs_bwd_workspace_size(int n_content, int n_queries, int H, int conv_kernel) {
+  if (n_content < 0 || n_queries < 0 || H <= 0 || conv_kernel < 2 || conv_kernel > 4) return 0;
+  return ev_layout(n_content, n_queries, H, conv_kernel).total;
+}
+
+int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, const void* raw, int64_t raw_stride, const void* a,
+                           int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
+                           const float* A_log, const float* dt_bias, const void* dq, const void* dk, const void* dv,
+                           const float* dg, const float* dbeta, void* d_raw, int64_t d_raw_stride, void* d_a,
+                           int64_t d_a_stride, void* d_b, int64_t d_b_stride, float* dweight, float* dgate,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  EvArgs ea;
+  if (const int e = ev_args(plan, H, raw, raw_stride, a, a_stride, b, b_stride, conv_weight, A_log, dt_bias, ea))
+    return e;
+  const int64_t S = (int64_t)H * CQGDN_HEAD_DIM;
+  if (plan->n_events > 0 && (!dq || !dk || !dv || !dg || !dbeta || !aligned(dq, 16) || !aligned(dk, 16) ||
+                             !aligned(dv, 16)))
+    return fail(CQGDN_EINVAL, "dq, dk, dv (16-byte aligned), dg, dbeta must be non-null");
+  if (!d_raw || !d_a || !d_b || !dweight || !dgate || !aligned(d_raw, 16) || !aligned(dweight, 16))
+    return fail(CQGDN_EINVAL, "d_raw (16-byte aligned), d_a, d_b, dweight (16-byte aligned), dgate must be non-null");
+  if (d_raw_stride < 3 * S || d_raw_stride % 8 || d_a_stride < H || d_b_stride < H)
+    return fail(CQGDN_EINVAL, "gradient strides must match the input layouts");
+  const EvLayout l = ev_layout(plan->n_content, plan->n_queries, H, plan->conv_kernel);
+  if (!workspace || !aligned(workspace, 256) || workspace_bytes < l.total)
+    return fail(CQGDN_EINVAL, "workspace must be 256-byte aligned and >= cqgdn_event_inputs_bwd_workspace_size");
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const EvGrads d{static_cast<const bf16*>(dq), static_cast<const bf16*>(dk), static_cast<const bf16*>(dv), dg, dbeta,
+                  static_cast<bf16*>(d_raw), d_raw_stride, static_cast<bf16*>(d_a), d_a_stride,
+                  static_cast<bf16*>(d_b), d_b_stride, dweight, dgate};
+  const EvWork w{reinterpret_cast<bf16*>(ws + l.dconv), reinterpret_cast<float*>(ws + l.dpre),
+                 reinterpret_cast<float*>(ws + l.gpart), reinterpret_cast<float*>(ws + l.qpart),
+                 reinterpret_cast<float*>(ws + l.cpart), reinterpret_cast<float*>(ws + l.qsum)};
+  launch_events_bwd(ea, d, plan->content_bounds, plan->n_content_docs, w, (hipStream_t)stream);
+  return check_launch("cqgdn_event_inputs_bwd");
 }
 
 }  // extern "C"

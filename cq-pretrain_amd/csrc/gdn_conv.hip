@@ -7,7 +7,11 @@
 //   y = silu(pre) with the activation, else pre
 //
 // x, y, dy, dx: bf16 [T][C] (time-first, B = 1, packed documents); w: bf16
-// [C][K], K <= 4.  A thread owns 8 consecutive channels (16-byte accesses, a
+// [C][K], K <= 4.  Row u of x may be read through a row map (x row xrows[u],
+// xs elements apart) and row t of dx written to dx row xrows[t] (dxs apart):
+// the layer's content gather updates = raw.index_select(0, content_order)
+// (models/backbone_qwen35.py:167) and its backward, consumed in the loads and
+// stores.  A thread owns 8 consecutive channels (16-byte accesses, a
 // wave covers 512 channels of one row: 1 KB per load or store); a tap on a row
 // of another document contributes nothing.  The forward requests every row of
 // a CONV_ROWS tile (with the K - 1 row halo) before computing; the backward
@@ -56,7 +60,8 @@ __device__ __forceinline__ float dsilu_f(float x) {
 }
 
 template <int K>
-__global__ __launch_bounds__(CONV_THREADS) void conv_fwd_kernel(const bf16* __restrict__ x, const bf16* __restrict__ w,
+__global__ __launch_bounds__(CONV_THREADS) void conv_fwd_kernel(const bf16* __restrict__ x, const int32_t* __restrict__ xrows,
+                                                               int64_t xs, const bf16* __restrict__ w,
                                                                const int32_t* __restrict__ bounds, int n_docs,
                                                                int T, int C, int act, bf16* __restrict__ y) {
   const int c = (blockIdx.y * CONV_THREADS + threadIdx.x) * 8;
@@ -68,7 +73,7 @@ __global__ __launch_bounds__(CONV_THREADS) void conv_fwd_kernel(const bf16* __re
 #pragma unroll
   for (int i = 0; i < CONV_ROWS + K - 1; ++i) {
     const int u = min(max(u0 + i, 0), T - 1);  // rows outside [0, T) are never used
-    xr[i] = ld8(x + (size_t)u * C + c);
+    xr[i] = ld8(x + (xrows ? (int64_t)xrows[u] : (int64_t)u) * xs + c);
   }
   f32x8 wk[K];
   {
@@ -115,19 +120,21 @@ template <> struct ConvVec<8> { typedef bf16x8 b; typedef f32x8 f; };
 template <> struct ConvVec<4> { typedef bf16x4 b; typedef f32x4 f; };
 
 template <int K, int CH, bool DOCS>
-__device__ __forceinline__ void conv_bwd_strip(const bf16* __restrict__ x, const typename ConvVec<CH>::f (&wk)[K],
+__device__ __forceinline__ void conv_bwd_strip(const bf16* __restrict__ x, const int32_t* __restrict__ rows,
+                                               int64_t xstr, const typename ConvVec<CH>::f (&wk)[K],
                                                const bf16* __restrict__ dy, const int32_t* __restrict__ bounds,
                                                int n_docs, int T, int C, int c, int s, int e, int act,
-                                               bf16* __restrict__ dx, typename ConvVec<CH>::f (&dwa)[K]) {
+                                               bf16* __restrict__ dx, int64_t dxs,
+                                               typename ConvVec<CH>::f (&dwa)[K]) {
   typedef typename ConvVec<CH>::b bv;
   typedef typename ConvVec<CH>::f fv;
   const int u0 = s - (K - 1), uend = e + K - 1;
   bv nx[K], nd[K];  // the next group's rows (clamped into [0, T); rows outside are never used)
 #pragma unroll
   for (int j = 0; j < K; ++j) {
-    const size_t row = (size_t)min(max(u0 + j, 0), T - 1) * C + c;
-    nx[j] = *reinterpret_cast<const bv*>(x + row);
-    nd[j] = *reinterpret_cast<const bv*>(dy + row);
+    const int u = min(max(u0 + j, 0), T - 1);
+    nx[j] = *reinterpret_cast<const bv*>(x + (rows ? (int64_t)rows[u] : (int64_t)u) * xstr + c);
+    nd[j] = *reinterpret_cast<const bv*>(dy + (int64_t)u * C + c);
   }
   // ring slot j holds the row at place j of the current group (rows before u0 are never read)
   fv xs[K], dp[K];
@@ -148,9 +155,9 @@ __device__ __forceinline__ void conv_bwd_strip(const bf16* __restrict__ x, const
     if (ub + K < uend) {
 #pragma unroll
       for (int j = 0; j < K; ++j) {
-        const size_t row = (size_t)min(max(ub + K + j, 0), T - 1) * C + c;
-        nx[j] = *reinterpret_cast<const bv*>(x + row);
-        nd[j] = *reinterpret_cast<const bv*>(dy + row);
+        const int u = min(max(ub + K + j, 0), T - 1);
+        nx[j] = *reinterpret_cast<const bv*>(x + (rows ? (int64_t)rows[u] : (int64_t)u) * xstr + c);
+        nd[j] = *reinterpret_cast<const bv*>(dy + (int64_t)u * C + c);
       }
     }
 #pragma unroll
@@ -194,17 +201,19 @@ __device__ __forceinline__ void conv_bwd_strip(const bf16* __restrict__ x, const
 #pragma unroll
         for (int m = 1; m < K; ++m)
           if (!DOCS || st[(j + 1 + m) % K] == st[(j + 1) % K]) acc += wk[K - 1 - m] * dp[(j + 1 + m) % K];
-        *reinterpret_cast<bv*>(dx + (size_t)t * C + c) = __builtin_convertvector(acc, bv);
+        *reinterpret_cast<bv*>(dx + (rows ? (int64_t)rows[t] : (int64_t)t) * dxs + c) =
+            __builtin_convertvector(acc, bv);
       }
     }
   }
 }
 
 template <int K>
-__global__ __launch_bounds__(64) void conv_bwd_kernel(const bf16* __restrict__ x, const bf16* __restrict__ w,
+__global__ __launch_bounds__(64) void conv_bwd_kernel(const bf16* __restrict__ x, const int32_t* __restrict__ xrows,
+                                                     int64_t xs, const bf16* __restrict__ w,
                                                      const bf16* __restrict__ dy, const int32_t* __restrict__ bounds,
                                                      int n_docs, int T, int C, int rows, int act,
-                                                     bf16* __restrict__ dx, float* __restrict__ dw_part) {
+                                                     bf16* __restrict__ dx, int64_t dxs, float* __restrict__ dw_part) {
   constexpr int CH = CONV_BWD_CH;
   typedef typename ConvVec<CH>::f fv;
   const int c = (blockIdx.y * 64 + threadIdx.x) * CH;
@@ -225,9 +234,9 @@ __global__ __launch_bounds__(64) void conv_bwd_kernel(const bf16* __restrict__ x
   const int i = lower_bound(bounds, n_docs, u0 + 1);
   const bool docs = __builtin_amdgcn_readfirstlane(i <= n_docs && bounds[i] < uend);
   if (docs)
-    conv_bwd_strip<K, CH, true>(x, wk, dy, bounds, n_docs, T, C, c, s, e, act, dx, dwa);
+    conv_bwd_strip<K, CH, true>(x, xrows, xs, wk, dy, bounds, n_docs, T, C, c, s, e, act, dx, dxs, dwa);
   else
-    conv_bwd_strip<K, CH, false>(x, wk, dy, bounds, n_docs, T, C, c, s, e, act, dx, dwa);
+    conv_bwd_strip<K, CH, false>(x, xrows, xs, wk, dy, bounds, n_docs, T, C, c, s, e, act, dx, dxs, dwa);
   float* part = dw_part + ((size_t)blockIdx.x * C + c) * K;
 #pragma unroll
   for (int ch = 0; ch < CH; ++ch)
@@ -275,30 +284,66 @@ int conv_strips(int64_t T) {
   return (int)((T + rows - 1) / rows);
 }
 
-void launch_conv_fwd(const bf16* x, const bf16* w, const int32_t* bounds, int n_docs, int T, int C, int K, int act,
-                     bf16* y, hipStream_t stream) {
+void launch_conv_fwd(const bf16* x, const int32_t* xrows, int64_t xs, const bf16* w, const int32_t* bounds,
+                     int n_docs, int T, int C, int K, int act, bf16* y, hipStream_t stream) {
   const dim3 grid((T + CONV_ROWS - 1) / CONV_ROWS, (C / 8 + CONV_THREADS - 1) / CONV_THREADS);
   switch (K) {
-    case 2: hipLaunchKernelGGL(conv_fwd_kernel<2>, grid, dim3(CONV_THREADS), 0, stream, x, w, bounds, n_docs, T, C, act, y); break;
-    case 3: hipLaunchKernelGGL(conv_fwd_kernel<3>, grid, dim3(CONV_THREADS), 0, stream, x, w, bounds, n_docs, T, C, act, y); break;
-    default: hipLaunchKernelGGL(conv_fwd_kernel<4>, grid, dim3(CONV_THREADS), 0, stream, x, w, bounds, n_docs, T, C, act, y); break;
+    case 2: hipLaunchKernelGGL(conv_fwd_kernel<2>, grid, dim3(CONV_THREADS), 0, stream, x, xrows, xs, w, bounds, n_docs, T, C, act, y); break;
+    case 3: hipLaunchKernelGGL(conv_fwd_kernel<3>, grid, dim3(CONV_THREADS), 0, stream, x, xrows, xs, w, bounds, n_docs, T, C, act, y); break;
+    default: hipLaunchKernelGGL(conv_fwd_kernel<4>, grid, dim3(CONV_THREADS), 0, stream, x, xrows, xs, w, bounds, n_docs, T, C, act, y); break;
   }
 }
 
-void launch_conv_bwd(const bf16* x, const bf16* w, const bf16* dy, const int32_t* bounds, int n_docs, int T, int C,
-                     int K, int act, bf16* dx, float* dw, float* part, hipStream_t stream) {
+void launch_conv_bwd(const bf16* x, const int32_t* xrows, int64_t xs, const bf16* w, const bf16* dy,
+                     const int32_t* bounds, int n_docs, int T, int C, int K, int act, bf16* dx, int64_t dxs, float* dw,
+                     float* part, hipStream_t stream) {
   const int rows = conv_strip_rows(T), strips = conv_strips(T);
   const dim3 grid(strips, (C / CONV_BWD_CH + 63) / 64);
   switch (K) {
-    case 2: hipLaunchKernelGGL(conv_bwd_kernel<2>, grid, dim3(64), 0, stream, x, w, dy, bounds, n_docs, T, C, rows, act, dx, part); break;
-    case 3: hipLaunchKernelGGL(conv_bwd_kernel<3>, grid, dim3(64), 0, stream, x, w, dy, bounds, n_docs, T, C, rows, act, dx, part); break;
-    default: hipLaunchKernelGGL(conv_bwd_kernel<4>, grid, dim3(64), 0, stream, x, w, dy, bounds, n_docs, T, C, rows, act, dx, part); break;
+    case 2: hipLaunchKernelGGL(conv_bwd_kernel<2>, grid, dim3(64), 0, stream, x, xrows, xs, w, dy, bounds, n_docs, T, C, rows, act, dx, dxs, part); break;
+    case 3: hipLaunchKernelGGL(conv_bwd_kernel<3>, grid, dim3(64), 0, stream, x, xrows, xs, w, dy, bounds, n_docs, T, C, rows, act, dx, dxs, part); break;
+    default: hipLaunchKernelGGL(conv_bwd_kernel<4>, grid, dim3(64), 0, stream, x, xrows, xs, w, dy, bounds, n_docs, T, C, rows, act, dx, dxs, part); break;
   }
   launch_colsum(part, strips, C * K, dw, stream);
 }
 
+// The same sums for n <= 256 columns (n % 4 == 0) and many parts: one workgroup of
+// 1024 threads, n / 4 float4 columns x 1024 / (n / 4) part stripes; each thread sums
+// parts stripe, stripe + stripes, ... (8 loads in flight), then the stripes are
+// added in stripe order.
+__global__ __launch_bounds__(1024) void colsum_narrow_kernel(const float* __restrict__ part, int parts, int n,
+                                                            float* __restrict__ out) {
+  __shared__ f32x4 red[1024];
+  const int n4 = n / 4, stripes = 1024 / n4;
+  const int c4 = threadIdx.x % n4, stripe = threadIdx.x / n4;
+  f32x4 acc = f32x4{};
+  if (stripe < stripes) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(part) + c4;
+    int b = stripe;
+    for (; b + 7 * stripes < parts; b += 8 * stripes) {
+      f32x4 v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = p[(size_t)(b + q * stripes) * n4];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) acc += v[q];
+    }
+    for (; b < parts; b += stripes) acc += p[(size_t)b * n4];
+  }
+  red[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x < n4) {
+    f32x4 r = red[threadIdx.x];
+    for (int q = 1; q < stripes; ++q) r += red[q * n4 + threadIdx.x];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) out[threadIdx.x * 4 + k] = r[k];
+  }
+}
+
 void launch_colsum(const float* part, int parts, int n, float* out, hipStream_t stream) {
-  hipLaunchKernelGGL(colsum_kernel, dim3((n / 4 + 63) / 64), dim3(256), 0, stream, part, parts, n, out);
+  if (n <= 256 && parts > 64)
+    hipLaunchKernelGGL(colsum_narrow_kernel, dim3(1), dim3(1024), 0, stream, part, parts, n, out);
+  else
+    hipLaunchKernelGGL(colsum_kernel, dim3((n / 4 + 63) / 64), dim3(256), 0, stream, part, parts, n, out);
 }
 
 }  // namespace cqgdn

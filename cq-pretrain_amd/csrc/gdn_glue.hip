@@ -117,6 +117,252 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(bf16* __restrict__ x, co
   st8(x + (int64_t)rows[k] * row_elems + j * 8, bf16x8{});
 }
 
+// ---------------------------------------------------------------------------
+// Event inputs of the recurrence (models/backbone_qwen35.py:166-194): the content
+// conv output, the CQ query conv from the content history, the q/k/v gathers by
+// event_q / event_write and the gate math, in one pass over the events; the
+// backward walks the inverse maps, so every output row is written once and no
+// atomics are used.  A workgroup has S / 8 threads (S = H * 128 channels, 8 per
+// thread); EvArgs documents the index arrays.
+
+__device__ __forceinline__ float softplus_f(float x) {  // torch's softplus (threshold 20)
+  return x > 20.f ? x : log1pf(__expf(x));
+}
+
+// 8 channels x K taps of the conv weight [3S][K] as K fp32 vectors
+template <int K>
+__device__ __forceinline__ void ld_taps(const bf16* __restrict__ w, int c, f32x8 (&wk)[K]) {
+  const bf16* wc = w + (size_t)c * K;
+#pragma unroll
+  for (int ch = 0; ch < 8; ++ch)
+#pragma unroll
+    for (int i = 0; i < K; ++i) wk[i][ch] = (float)wc[ch * K + i];
+}
+
+// pre-activation of query j's conv at channels c..c+7: its own raw row (tap K-1) and
+// the history rows qhist[j][i] (content rows, read as raw rows order[.]; n_c = none)
+template <int K>
+__device__ __forceinline__ f32x8 query_pre(const EvArgs& a, int j, int c, const f32x8 (&wk)[K], f32x8 (&x)[K]) {
+  x[K - 1] = cvtf8(ld8(a.raw + (int64_t)a.qsource[j] * a.raw_stride + c));
+  f32x8 pre = wk[K - 1] * x[K - 1];
+#pragma unroll
+  for (int i = 0; i < K - 1; ++i) {
+    const int hr = a.qhist[j * (K - 1) + i];
+    x[i] = hr < a.n_c ? cvtf8(ld8(a.raw + (int64_t)a.order[hr] * a.raw_stride + c)) : f32x8{};
+    pre += wk[i] * x[i];
+  }
+  return pre;
+}
+
+template <int K>
+__global__ __launch_bounds__(512) void events_fwd_kernel(EvArgs a, const bf16* __restrict__ conv, bf16* __restrict__ q,
+                                                        bf16* __restrict__ k, bf16* __restrict__ v,
+                                                        float* __restrict__ g, float* __restrict__ beta) {
+  const int e = blockIdx.x, S = a.H * GN_D, c = threadIdx.x * 8;
+  const int sq = a.eq[e], sw = a.ew[e];
+  bf16x8 q8;
+  if (sq < a.n_c) {
+    q8 = ld8(conv + (int64_t)sq * 3 * S + c);
+  } else {
+    f32x8 wk[K], x[K];
+    ld_taps<K>(a.w, c, wk);
+    f32x8 pre = query_pre<K>(a, sq - a.n_c, c, wk, x);
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) pre[ch] *= sigm(pre[ch]);
+    q8 = cvt8(pre);
+  }
+  bf16x8 k8 = bf16x8{}, v8 = bf16x8{};
+  if (sw < a.n_c) {
+    k8 = ld8(conv + (int64_t)sw * 3 * S + S + c);
+    v8 = ld8(conv + (int64_t)sw * 3 * S + 2 * S + c);
+  }
+  st8(q + (int64_t)e * S + c, q8);
+  st8(k + (int64_t)e * S + c, k8);
+  st8(v + (int64_t)e * S + c, v8);
+  if (threadIdx.x < a.H) {
+    const int h = threadIdx.x;
+    float gv = 0.f, bv = 0.f;
+    if (sw < a.n_c) {
+      const int64_t row = a.order[sw];
+      const float av = (float)a.ga[row * a.ga_stride + h] + a.dt_bias[h];
+      gv = -__expf(a.A_log[h]) * softplus_f(av);
+      bv = sigm((float)a.gb[row * a.gb_stride + h]);
+    }
+    g[(int64_t)e * a.H + h] = gv;
+    beta[(int64_t)e * a.H + h] = bv;
+  }
+}
+
+// content row cr: dconv[cr] = (sum of dq over the events reading q of cr, dk and dv of
+// the event writing cr); gate gradients into the a/b columns of hidden row order[cr];
+// dA_log / dt_bias partials [cr][2H]
+__global__ __launch_bounds__(512) void events_bwd_content_kernel(EvArgs a, EvGrads d, bf16* __restrict__ dconv,
+                                                                float* __restrict__ gpart) {
+  const int cr = blockIdx.x, S = a.H * GN_D, c = threadIdx.x * 8;
+  const int we = a.winv[cr];
+  f32x8 acc = f32x8{};
+  for (int p = a.qptr[cr]; p < a.qptr[cr + 1]; ++p) acc += cvtf8(ld8(d.dq + (int64_t)a.qlist[p] * S + c));
+  bf16* out = dconv + (int64_t)cr * 3 * S;
+  st8(out + c, cvt8(acc));
+  st8(out + S + c, we >= 0 ? ld8(d.dk + (int64_t)we * S + c) : bf16x8{});
+  st8(out + 2 * S + c, we >= 0 ? ld8(d.dv + (int64_t)we * S + c) : bf16x8{});
+  if (threadIdx.x < a.H) {
+    const int h = threadIdx.x;
+    const int64_t row = a.order[cr];
+    float da = 0.f, db = 0.f, dA = 0.f;
+    if (we >= 0) {
+      const float av = (float)a.ga[row * a.ga_stride + h] + a.dt_bias[h];
+      const float ea = __expf(a.A_log[h]);
+      const float dg = d.dg[(int64_t)we * a.H + h];
+      da = -dg * ea * sigm(av);      // g = -exp(A_log) softplus(a + dt_bias)
+      dA = -dg * ea * softplus_f(av);  // dg/dA_log = g
+      const float sb = sigm((float)a.gb[row * a.gb_stride + h]);
+      db = d.dbeta[(int64_t)we * a.H + h] * sb * (1.f - sb);
+    }
+    d.da[row * d.da_stride + h] = (bf16)da;
+    d.db[row * d.db_stride + h] = (bf16)db;
+    gpart[(int64_t)cr * 2 * a.H + h] = dA;
+    gpart[(int64_t)cr * 2 * a.H + a.H + h] = da;
+  }
+}
+
+// queries j = blockIdx.x, + gridDim.x, ... for 512 channels (blockIdx.y): dpre[j] = dq of
+// the event reading j times silu'(pre); raw gradient of the query's own row (tap K-1; its
+// k/v channels and gates get zeros); query-conv weight partials [blockIdx.x][S][K].  The
+// next query's dq row and tap rows are requested before the current one computes.
+template <int K>
+__global__ __launch_bounds__(64) void events_bwd_query_kernel(EvArgs a, EvGrads d, float* __restrict__ dpre,
+                                                             float* __restrict__ wpart) {
+  const int S = a.H * GN_D, c = (blockIdx.y * 64 + threadIdx.x) * 8;
+  f32x8 wk[K], dw[K];
+  ld_taps<K>(a.w, c, wk);
+#pragma unroll
+  for (int i = 0; i < K; ++i) dw[i] = f32x8{};
+  bf16x8 nq = bf16x8{}, nx[K];
+  auto fetch = [&](int j) {
+    nq = ld8(d.dq + (int64_t)a.qev[j] * S + c);
+    nx[K - 1] = ld8(a.raw + (int64_t)a.qsource[j] * a.raw_stride + c);
+#pragma unroll
+    for (int i = 0; i < K - 1; ++i) {
+      const int hr = a.qhist[j * (K - 1) + i];
+      nx[i] = hr < a.n_c ? ld8(a.raw + (int64_t)a.order[hr] * a.raw_stride + c) : bf16x8{};
+    }
+  };
+  int j = blockIdx.x;
+  if (j < a.n_q) fetch(j);
+  for (; j < a.n_q; j += gridDim.x) {
+    bf16x8 cq = nq, cx[K];
+#pragma unroll
+    for (int i = 0; i < K; ++i) cx[i] = nx[i];
+    if (j + (int)gridDim.x < a.n_q) fetch(j + gridDim.x);
+    f32x8 x[K], pre = f32x8{};
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      x[i] = cvtf8(cx[i]);
+      pre += wk[i] * x[i];
+    }
+    f32x8 dp = cvtf8(cq);
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) {
+      const float sg = sigm(pre[ch]);
+      dp[ch] *= sg * (1.f + pre[ch] * (1.f - sg));
+    }
+    float* dpj = dpre + (int64_t)j * S + c;
+    *reinterpret_cast<f32x4*>(dpj) = f32x4{dp[0], dp[1], dp[2], dp[3]};
+    *reinterpret_cast<f32x4*>(dpj + 4) = f32x4{dp[4], dp[5], dp[6], dp[7]};
+#pragma unroll
+    for (int i = 0; i < K; ++i) dw[i] += dp * x[i];
+    const int64_t row = a.qsource[j];
+    bf16* dr = d.draw + row * d.draw_stride;
+    st8(dr + c, cvt8(dp * wk[K - 1]));
+    st8(dr + S + c, bf16x8{});
+    st8(dr + 2 * S + c, bf16x8{});
+    if (blockIdx.y == 0 && threadIdx.x < a.H) {
+      d.da[row * d.da_stride + threadIdx.x] = (bf16)0.f;
+      d.db[row * d.db_stride + threadIdx.x] = (bf16)0.f;
+    }
+  }
+  float* p = wpart + ((int64_t)blockIdx.x * S + c) * K;
+#pragma unroll
+  for (int ch = 0; ch < 8; ++ch)
+#pragma unroll
+    for (int i = 0; i < K; ++i) p[ch * K + i] = dw[i][ch];
+}
+
+// after the conv backward wrote the raw gradient of content row cr = hrows[blockIdx.x]:
+// add the query convs' history taps, sum over (j, i) with qhist[j][i] == cr of dpre[j] w[., i]
+template <int K>
+__global__ __launch_bounds__(512) void events_bwd_history_kernel(EvArgs a, EvGrads d, const float* __restrict__ dpre) {
+  const int cr = a.hrows[blockIdx.x], S = a.H * GN_D, c = threadIdx.x * 8;
+  f32x8 wk[K];
+  ld_taps<K>(a.w, c, wk);
+  f32x8 acc = f32x8{};
+  for (int p = a.hptr[cr]; p < a.hptr[cr + 1]; ++p) {
+    const int code = a.hlist[p], j = code / (K - 1), i = code - j * (K - 1);
+    const float* dpj = dpre + (int64_t)j * S + c;
+    const f32x4 lo = *reinterpret_cast<const f32x4*>(dpj), hi = *reinterpret_cast<const f32x4*>(dpj + 4);
+    f32x8 wi = wk[0];
+#pragma unroll
+    for (int t = 1; t < K - 1; ++t)
+      if (i == t) wi = wk[t];
+    acc += f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]} * wi;
+  }
+  bf16* dr = d.draw + (int64_t)a.order[cr] * d.draw_stride + c;
+  st8(dr, cvt8(cvtf8(ld8(dr)) + acc));
+}
+
+__global__ __launch_bounds__(256) void add_f32_kernel(float* __restrict__ dst, const float* __restrict__ src, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) dst[i] += src[i];
+}
+
+int events_query_blocks(int n_q) { return n_q < 128 ? n_q : 128; }
+
+void launch_events_fwd(const EvArgs& a, const bf16* conv, bf16* q, bf16* k, bf16* v, float* g, float* beta,
+                       hipStream_t stream) {
+  if (a.E == 0) return;
+  const dim3 grid(a.E), block(a.H * 16);
+  switch (a.K) {
+    case 2: hipLaunchKernelGGL(events_fwd_kernel<2>, grid, block, 0, stream, a, conv, q, k, v, g, beta); break;
+    case 3: hipLaunchKernelGGL(events_fwd_kernel<3>, grid, block, 0, stream, a, conv, q, k, v, g, beta); break;
+    default: hipLaunchKernelGGL(events_fwd_kernel<4>, grid, block, 0, stream, a, conv, q, k, v, g, beta); break;
+  }
+}
+
+void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content_bounds, int n_content_docs,
+                       const EvWork& w, hipStream_t stream) {
+  const int S = a.H * GN_D, H = a.H;
+  const dim3 block(H * 16);
+  if (a.n_c > 0) {
+    hipLaunchKernelGGL(events_bwd_content_kernel, dim3(a.n_c), block, 0, stream, a, d, w.dconv, w.gpart);
+  }
+  const int qb = events_query_blocks(a.n_q);
+  if (qb > 0) {
+    const dim3 qgrid(qb, S / 512);
+    switch (a.K) {
+      case 2: hipLaunchKernelGGL(events_bwd_query_kernel<2>, qgrid, dim3(64), 0, stream, a, d, w.dpre, w.qpart); break;
+      case 3: hipLaunchKernelGGL(events_bwd_query_kernel<3>, qgrid, dim3(64), 0, stream, a, d, w.dpre, w.qpart); break;
+      default: hipLaunchKernelGGL(events_bwd_query_kernel<4>, qgrid, dim3(64), 0, stream, a, d, w.dpre, w.qpart); break;
+    }
+  }
+  if (a.n_c > 0) {
+    launch_conv_bwd(a.raw, a.order, a.raw_stride, a.w, w.dconv, content_bounds, n_content_docs, a.n_c, 3 * S, a.K, 1,
+                    d.draw, d.draw_stride, d.dw, w.cpart, stream);
+  } else {
+    launch_colsum(w.cpart, 0, 3 * S * a.K, d.dw, stream);  // zeros
+  }
+  if (a.n_hrows > 0) {
+    switch (a.K) {
+      case 2: hipLaunchKernelGGL(events_bwd_history_kernel<2>, dim3(a.n_hrows), block, 0, stream, a, d, w.dpre); break;
+      case 3: hipLaunchKernelGGL(events_bwd_history_kernel<3>, dim3(a.n_hrows), block, 0, stream, a, d, w.dpre); break;
+      default: hipLaunchKernelGGL(events_bwd_history_kernel<4>, dim3(a.n_hrows), block, 0, stream, a, d, w.dpre); break;
+    }
+  }
+  launch_colsum(w.gpart, a.n_c, 2 * H, d.dgate, stream);
+  launch_colsum(w.qpart, qb, S * a.K, w.qsum, stream);
+  hipLaunchKernelGGL(add_f32_kernel, dim3((S * a.K + 255) / 256), dim3(256), 0, stream, d.dw, w.qsum, S * a.K);
+}
+
 int gnorm_bwd_blocks(int64_t rows, int H) {
   const int64_t blocks = (rows * H + GN_ITEMS - 1) / GN_ITEMS;
   return (int)(blocks < 1024 ? blocks : 1024);

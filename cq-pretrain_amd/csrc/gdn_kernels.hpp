@@ -50,12 +50,66 @@ void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* 
                       hipStream_t stream);
 // packed depthwise causal conv1d (gdn_conv.hip); bounds: int32 [n_docs + 1] on the device
 int conv_strips(int64_t T);  // row strips of the conv backward (dw partials per strip)
-void launch_conv_fwd(const bf16* x, const bf16* w, const int32_t* bounds, int n_docs, int T, int C, int K, int act,
-                     bf16* y, hipStream_t stream);
-void launch_conv_bwd(const bf16* x, const bf16* w, const bf16* dy, const int32_t* bounds, int n_docs, int T, int C,
-                     int K, int act, bf16* dx, float* dw, float* part, hipStream_t stream);
+// x row u is x + (xrows ? xrows[u] : u) * xs; dx row t likewise with dxs; y and dy are [T][C]
+void launch_conv_fwd(const bf16* x, const int32_t* xrows, int64_t xs, const bf16* w, const int32_t* bounds,
+                     int n_docs, int T, int C, int K, int act, bf16* y, hipStream_t stream);
+void launch_conv_bwd(const bf16* x, const int32_t* xrows, int64_t xs, const bf16* w, const bf16* dy,
+                     const int32_t* bounds, int n_docs, int T, int C, int K, int act, bf16* dx, int64_t dxs, float* dw,
+                     float* part, hipStream_t stream);
 // out[j] = sum over p < parts of part[p][j], fixed order (gdn_conv.hip); n % 4 == 0, 16-byte aligned part
 void launch_colsum(const float* part, int parts, int n, float* out, hipStream_t stream);
+// Event inputs of one GatedDelta layer (gdn_glue.hip).  S = H * 128 channels per
+// q/k/v part; index arrays are device int32 (content rows are 0 .. n_c-1, n_c is
+// the zero row / "none").
+struct EvArgs {
+  int H, K, n_c, n_q, E, n_hrows;
+  const int32_t* order;    // [n_c] hidden row of content row c
+  const int32_t* eq;       // [E] q source: content row, or n_c + query
+  const int32_t* ew;       // [E] content row written, n_c for read-only events
+  const int32_t* qsource;  // [n_q] hidden row of query j
+  const int32_t* qhist;    // [n_q][K-1] content rows of query j's conv history
+  const int32_t* qptr;     // [n_c + 1] CSR: events whose q is content row c ...
+  const int32_t* qlist;    //   ... in event order
+  const int32_t* winv;     // [n_c] event writing content row c, -1 if none
+  const int32_t* qev;      // [n_q] event reading query j
+  const int32_t* hptr;     // [n_c + 1] CSR: entries j * (K-1) + i with qhist[j][i] == c ...
+  const int32_t* hlist;    //   ... ascending
+  const int32_t* hrows;    // [n_hrows] content rows with history entries
+  const bf16* raw;         // projection rows, channels [0, 3S) = q | k | v
+  int64_t raw_stride;
+  const bf16* ga;          // a (H per row)
+  int64_t ga_stride;
+  const bf16* gb;          // b (H per row)
+  int64_t gb_stride;
+  const bf16* w;           // conv weight [3S][K]
+  const float* A_log;      // [H]
+  const float* dt_bias;    // [H]
+};
+struct EvGrads {
+  const bf16 *dq, *dk, *dv;  // [E][S]
+  const float *dg, *dbeta;   // [E][H]
+  bf16* draw;                // gradient rows of raw (every hidden row of order / qsource is written)
+  int64_t draw_stride;
+  bf16* da;
+  int64_t da_stride;
+  bf16* db;
+  int64_t db_stride;
+  float* dw;     // conv weight gradient [3S][K]
+  float* dgate;  // [2H]: A_log, then dt_bias
+};
+struct EvWork {
+  bf16* dconv;   // [n_c][3S] gradient of the conv output
+  float* dpre;   // [n_q][S] gradient of the query convs' pre-activation
+  float* gpart;  // [n_c][2H]
+  float* qpart;  // [events_query_blocks][S][K]
+  float* cpart;  // conv backward partials
+  float* qsum;   // [S][K]
+};
+int events_query_blocks(int n_q);
+void launch_events_fwd(const EvArgs& a, const bf16* conv, bf16* q, bf16* k, bf16* v, float* g, float* beta,
+                       hipStream_t stream);
+void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content_bounds, int n_content_docs,
+                       const EvWork& w, hipStream_t stream);
 // gated RMSNorm over D = 128 with an optional row gather (gdn_glue.hip)
 int gnorm_bwd_blocks(int64_t rows, int H);  // workgroups of the backward (dw partials per workgroup)
 void launch_gnorm_fwd(const bf16* y, const int32_t* index, int64_t rows, int H, const bf16* z, int64_t z_stride,

@@ -182,6 +182,69 @@ int cqgdn_gated_norm_bwd(const void* y, const int32_t* index, const int32_t* zer
                          size_t workspace_bytes, void* stream);
 
 /*
+ * One layer's event plan as device int32 arrays: the DeltaPlan fields the
+ * GatedDelta layer reads (ops/gated_delta_layout.py:13-27, built at :54-176),
+ * plus inverse maps the host derives once per plan.  Content rows are
+ * 0 .. n_content-1; the value n_content stands for "none" / the zero row, as in
+ * the reference's torch.cat((x, zeros)).index_select idiom.
+ */
+typedef struct cqgdn_event_plan {
+  int32_t n_content, n_queries, n_events, conv_kernel; /* conv_kernel K: 2..4 */
+  const int32_t* content_order;  /* [n_content] hidden row of each content write (plan.content_order) */
+  const int32_t* event_q;        /* [n_events] q source: content row, or n_content + query (plan.event_q) */
+  const int32_t* event_write;    /* [n_events] content row written, n_content if read-only (plan.event_write) */
+  const int32_t* query_source;   /* [n_queries] hidden row of each query (plan.query_source) */
+  const int32_t* query_history;  /* [n_queries][K-1] content rows of each query's conv history */
+  const int32_t* content_bounds; /* [n_content_docs + 1] document bounds of the content conv */
+  int32_t n_content_docs;
+  int32_t n_history_rows;        /* entries of history_rows */
+  const int32_t* q_ptr;          /* [n_content + 1] CSR: the events whose q is content row c ... */
+  const int32_t* q_list;         /*   ... in event order */
+  const int32_t* write_event;    /* [n_content] the event writing content row c, -1 if none */
+  const int32_t* query_event;    /* [n_queries] the event reading query j */
+  const int32_t* history_ptr;    /* [n_content + 1] CSR: j * (K-1) + i with query_history[j][i] == c ... */
+  const int32_t* history_list;   /*   ... ascending */
+  const int32_t* history_rows;   /* content rows with at least one history entry */
+} cqgdn_event_plan;
+
+/*
+ * The recurrence's event inputs from the layer's projection, in two launches:
+ * the packed causal conv (with SiLU) over the content rows, read from the
+ * projection through content_order; then per event q (a content row of the conv
+ * output, or a CQ query whose conv reads its own row and its history rows), k
+ * and v (the written content row, or zeros), g = -exp(A_log) softplus(a +
+ * dt_bias) and beta = sigmoid(b) (zeros for read-only events).  Replaces
+ * models/backbone_qwen35.py:166-194 (index_select, conv1d, the query conv, the
+ * cat/index_select gathers and the gate math).
+ *   raw: bf16 rows of 3S channels (q | k | v, S = H * 128) raw_stride apart;
+ *   a, b: bf16 rows of H gate inputs, a_stride / b_stride apart (all three may be
+ *   column slices of the fused projection); conv_weight: bf16 [3S][K];
+ *   A_log, dt_bias: fp32 [H]; q, k, v: bf16 [n_events][H][128]; g, beta: fp32
+ *   [n_events][H]; workspace: >= cqgdn_event_inputs_fwd_workspace_size bytes.
+ */
+size_t cqgdn_event_inputs_fwd_workspace_size(int n_content, int H);
+int cqgdn_event_inputs_fwd(const cqgdn_event_plan* plan, int H, const void* raw, int64_t raw_stride, const void* a,
+                           int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
+                           const float* A_log, const float* dt_bias, void* q, void* k, void* v, float* g, float* beta,
+                           void* workspace, size_t workspace_bytes, void* stream);
+/*
+ * Backward of cqgdn_event_inputs_fwd from the recurrence's gradients dq, dk, dv
+ * (bf16 [n_events][H][128]) and dg, dbeta (fp32 [n_events][H]).  Writes the
+ * raw, a and b gradient rows of every content and query row (d_raw, d_a, d_b,
+ * same layouts as raw, a, b; other rows are not touched), dweight fp32 [3S][K]
+ * and dgate fp32 [2H] (A_log, then dt_bias).  The scatters walk the plan's
+ * inverse maps, so every output is written once, without atomics, and the
+ * result is deterministic.
+ */
+size_t cqgdn_event_inputs_bwd_workspace_size(int n_content, int n_queries, int H, int conv_kernel);
+int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, const void* raw, int64_t raw_stride, const void* a,
+                           int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
+                           const float* A_log, const float* dt_bias, const void* dq, const void* dk, const void* dv,
+                           const float* dg, const float* dbeta, void* d_raw, int64_t d_raw_stride, void* d_a,
+                           int64_t d_a_stride, void* d_b, int64_t d_b_stride, float* dweight, float* dgate,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Chunk-local cumsum of g fp32 [T][H] over the chunk table, forward or reverse
  * (`chunk_local_cumsum` and reverse_cumsum(), ops/gated_delta_net.py:77-87,158-164).
  */

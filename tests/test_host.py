@@ -166,3 +166,36 @@ def test_layer_forward_backward_on_cpu_with_oracle_recurrence():
     assert y.shape == x.shape
     y.square().sum().backward()
     assert torch.isfinite(x.grad).all() and model.in_proj_all.weight.grad.abs().sum() > 0
+
+
+def test_event_plan_inverse_maps_against_brute_force():
+    """The host-built inverse maps of the fused layer kernels (q readers per content row, the
+    writer of each content row, the reader of each query, the query-history entries per content
+    row) against direct scans of the plan, on a packed two-document plan; bad plans raise."""
+    from cqgdn import events, layer
+
+    plan = layer.concat_plans(layer.cq_layer_plan(60, 17, image_groups=(9, 5), seed=1),
+                              layer.cq_layer_plan(45, 11, image_groups=(7,), seed=2))
+    ep = events.event_plan(plan, 4, "cpu")
+    t = {k: v.long() for k, v in ep.tensors.items()}
+    n_c, n_q = ep.n_content, ep.n_queries
+    eq, ew, qh = plan.event_q.tolist(), plan.event_write.tolist(), plan.query_history.tolist()
+    assert (ep.content_bounds, ep.covers_all) == ((0, 60, 105), True)
+    for c in range(n_c):
+        readers = t["q_list"][t["q_ptr"][c]:t["q_ptr"][c + 1]].tolist()
+        assert readers == [e for e, src in enumerate(eq) if src == c]
+        writers = [e for e, w in enumerate(ew) if w == c]
+        assert writers == [int(t["write_event"][c])]
+        hist = t["history_list"][t["history_ptr"][c]:t["history_ptr"][c + 1]].tolist()
+        assert hist == [j * 3 + i for j in range(n_q) for i in range(3) if qh[j][i] == c]
+        assert (c in t["history_rows"].tolist()) == bool(hist)
+    for j in range(n_q):
+        assert eq[int(t["query_event"][j])] == n_c + j
+    assert sorted(set(range(len(eq))) - set(plan.hidden_event.tolist())) == ep.unread_events.long().tolist()
+    # the second document's conv history never reaches into the first document
+    assert all(c >= 60 or c == n_c for j in range(17, n_q) for c in qh[j])
+    bad = layer.cq_layer_plan(20, 3, image_groups=(4,))
+    bad.event_write = bad.event_write.clone()
+    bad.event_write[bad.event_write == 5] = 4  # two writers of content row 4
+    with pytest.raises(ValueError, match="written by more than one event"):
+        events.event_plan(bad, 4, "cpu")
