@@ -207,6 +207,36 @@ def layer_case(torch, device, content, queries, iterations=12):
                 median_ms=timed(True), torch_glue_median_ms=timed(False))
 
 
+def layer_decode_case(torch, device, N, iterations=200):
+    """One decode step of the layer between its projections (events.layer_decode_step:
+    conv step, query conv, gates, two-event recurrence, gated norm) for N sequences at H = 16;
+    the mean over ``iterations`` back-to-back steps timed with HIP events."""
+    from cqgdn import events
+
+    H, K = 16, 4
+    S, P = H * 128, 4 * H * 128 + 2 * H
+    gen = torch.Generator().manual_seed(70)
+    w = (torch.rand(3 * S, K, generator=gen) - 0.5).bfloat16().to(device)
+    A_log = torch.rand(H, generator=gen).mul(15.99).add(0.01).log().to(device)
+    dt_bias, nw = torch.ones(H, device=device), torch.ones(128, device=device)
+    proj = (torch.randn(N, 2, P, generator=gen) * 0.5).bfloat16().to(device)
+    cache = {"conv": torch.zeros(N, K - 1, 3 * S, dtype=torch.bfloat16, device=device),
+             "state": (torch.randn(N, H, 128, 128, generator=gen) * 0.01).to(device)}
+    step = lambda: events.layer_decode_step(proj, w, A_log, dt_bias, nw, cache, heads=H)
+    for _ in range(10):
+        step()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iterations):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / iterations
+    state_bytes = 2 * N * H * 128 * 128 * 4
+    return dict(sequences=N, us_per_step=round(us, 2), state_gbps=round(state_bytes / us / 1e3, 1))
+
+
 COPY_BYTES = 256 << 20
 
 
@@ -297,6 +327,8 @@ def main():
         extra["config3_documents"] = len(bounds3) - 1
         del step3
         log("whole GatedDelta layer, width 2048 (content 2048 and 8192, image-CQ plans)")
+        log("layer decode step, width 2048 (N = 1 and 64 sequences)")
+        extra["layer_decode_w2048"] = [layer_decode_case(torch, device, n) for n in (1, 64)]
         extra["layer_w2048"] = [dict(layer_case(torch, device, c, nq), reference_ascend910b_ms=ref)
                                 for c, nq, ref in ((2048, 1675, 10.46), (8192, 7819, 38.60))]
         log("config 2 prefill")

@@ -110,10 +110,12 @@ def event_plan(plan, kernel: int, device) -> EventPlan:
     read = torch.zeros(n_e, dtype=torch.bool)
     read[real] = True
     dev = lambda t: t.to(torch.int32).to(device)
+    pad = lambda t: torch.cat((t, t.new_full((1,), -1)))  # a list array is never null, even when empty
     tensors = dict(content_order=dev(order), event_q=dev(eq), event_write=dev(ew), query_source=dev(qs),
                    query_history=dev(qh), content_bounds=dev(torch.tensor(tuple(plan.content_bounds))),
-                   q_ptr=dev(q_ptr), q_list=dev(q_list), write_event=dev(write_event), query_event=dev(query_event),
-                   history_ptr=dev(h_ptr), history_list=dev(h_list), history_rows=dev(h_rows))
+                   q_ptr=dev(q_ptr), q_list=dev(pad(q_list)), write_event=dev(write_event),
+                   query_event=dev(query_event), history_ptr=dev(h_ptr), history_list=dev(pad(h_list)),
+                   history_rows=dev(pad(h_rows)))
     p = lambda name: tensors[name].data_ptr() if tensors[name].numel() else None
     cs = _lib.EventPlan(n_c, n_q, n_e, kernel, p("content_order"), p("event_q"), p("event_write"), p("query_source"),
                         p("query_history"), p("content_bounds"), len(plan.content_bounds) - 1, h_rows.numel(),
@@ -205,3 +207,77 @@ def layer_core(proj, conv_weight, A_log, dt_bias, norm_weight, plan, *, heads, e
         raise ValueError("proj rows do not match the plan's hidden rows")
     return _LayerCore.apply(proj, conv_weight, A_log, dt_bias, norm_weight, ep, heads, eps,
                             128 ** -0.5 if scale is None else float(scale))
+
+
+@torch.no_grad()
+def layer_prefill(proj, conv_weight, A_log, dt_bias, norm_weight, plan, *, heads, eps=1e-6, scale=None):
+    """Inference prefill of the layer with the cache a decoder continues from
+    (models/backbone_qwen35.py:163-211 with ``cache``): the event inputs as in training, the
+    precise forward with each document's final state, the gated norm with the output gather.
+
+    Returns ``(out [rows, S], cache)``: ``cache["state"]`` fp32 [n_docs, H, V, K] value-first (the
+    decode layout) and ``cache["conv"]`` bf16 [1, K-1, 3S], the raw q|k|v rows of the K-1 content
+    rows before the last one, zero-filled in front, as the reference keeps them (its last content
+    row is the uncommitted target, models/decoding.py:117-121)."""
+    S = heads * 128
+    if proj.dim() != 2 or proj.shape[1] != 4 * S + 2 * heads or proj.dtype != torch.bfloat16:
+        raise ValueError("proj must be bf16 [rows, 4*H*128 + 2*H]")
+    gdn._require_gpu(proj, conv_weight)
+    proj = proj.contiguous()
+    K = conv_weight.shape[1]
+    ep = event_plan(plan, K, proj.device)
+    dev, st, P, n_h, E = proj.device, gdn._stream(proj.device), proj.shape[1], proj.shape[0], ep.n_events
+    w = conv_weight.contiguous()
+    alog, dtb, nw = A_log.float().contiguous(), dt_bias.float().contiguous(), norm_weight.float().contiguous()
+    q, k, v = (torch.empty(E, heads, 128, dtype=proj.dtype, device=dev) for _ in range(3))
+    gb = torch.empty(2, E, heads, dtype=torch.float32, device=dev)
+    fws = torch.empty(_lib.lib().cqgdn_event_inputs_fwd_workspace_size(ep.n_content, heads), dtype=torch.uint8,
+                      device=dev)
+    gdn.call("cqgdn_event_inputs_fwd", ctypes.byref(ep.cstruct), heads, gdn._ptr(proj), P,
+             proj[:, 4 * S:].data_ptr(), P, proj[:, 4 * S + heads:].data_ptr(), P, gdn._ptr(w), gdn._ptr(alog),
+             gdn._ptr(dtb), gdn._ptr(q), gdn._ptr(k), gdn._ptr(v), gdn._ptr(gb[0]), gdn._ptr(gb[1]), gdn._ptr(fws),
+             fws.numel(), st)
+    y, state, _ = gdn._forward(q[None], k[None], v[None], gb[0][None], gb[1][None], ep.event_bounds, True,
+                               128 ** -0.5 if scale is None else float(scale), training=False, want_state=True,
+                               precise=True)
+    out = torch.empty(n_h, heads, 128, dtype=proj.dtype, device=dev)
+    rstd = torch.empty(n_h, heads, dtype=torch.float32, device=dev)
+    gdn.call("cqgdn_gated_norm_fwd", gdn._ptr(y), gdn._ptr(ep.hidden_index), n_h, heads, proj[:, 3 * S:].data_ptr(),
+             P, gdn._ptr(nw), float(eps), gdn._ptr(out), gdn._ptr(rstd), st)
+    count = K - 1
+    history = proj.new_zeros(1, count, 3 * S)
+    order = ep.tensors["content_order"]
+    tail = order[max(0, ep.n_content - 1 - count):max(ep.n_content - 1, 0)].long()
+    if tail.numel():
+        history[0, count - tail.numel():] = proj.index_select(0, tail)[:, :3 * S]
+    return out.reshape(n_h, S), {"state": state.transpose(-1, -2).contiguous(), "conv": history}
+
+
+@torch.no_grad()
+def layer_decode_step(proj, conv_weight, A_log, dt_bias, norm_weight, cache, *, heads, eps=1e-6, scale=None):
+    """One decode step (models/decoding.py:16-78 between the projection and out_proj) for N
+    sequences: proj [N, 2, 4S + 2H] bf16 (row 0 the sampled content token, row 1 the text-mask
+    query; [2, P] for one sequence); ``cache["conv"]`` bf16 [N, K-1, 3S] and ``cache["state"]`` fp32
+    [N, H, V, K] are updated in place.  Returns the gated-norm rows [N, 2, S] ([2, S])."""
+    S = heads * 128
+    single = proj.dim() == 2
+    p3 = proj[None] if single else proj
+    N, P = p3.shape[0], p3.shape[2]
+    K = conv_weight.shape[1]
+    if p3.shape[1] != 2 or P != 4 * S + 2 * heads or p3.dtype != torch.bfloat16:
+        raise ValueError("proj must be bf16 [N, 2, 4*H*128 + 2*H]")
+    hist, state = cache["conv"], cache["state"]
+    if hist.shape != (N, K - 1, 3 * S) or hist.dtype != torch.bfloat16 or not hist.is_contiguous():
+        raise ValueError("cache['conv'] must be contiguous bf16 [N, K-1, 3*H*128]")
+    if state.shape != (N, heads, 128, 128) or state.dtype != torch.float32 or not state.is_contiguous():
+        raise ValueError("cache['state'] must be contiguous fp32 [N, H, 128, 128] (value-first)")
+    gdn._require_gpu(p3, conv_weight, hist, state)
+    p3 = p3.contiguous()
+    w = conv_weight.contiguous()
+    alog, dtb, nw = A_log.float().contiguous(), dt_bias.float().contiguous(), norm_weight.float().contiguous()
+    out = torch.empty(N, 2, S, dtype=p3.dtype, device=p3.device)
+    ws = torch.empty(_lib.lib().cqgdn_layer_decode_workspace_size(N, heads), dtype=torch.uint8, device=p3.device)
+    gdn.call("cqgdn_layer_decode_step", N, heads, K, gdn._ptr(p3), P, gdn._ptr(hist), gdn._ptr(w), gdn._ptr(alog),
+             gdn._ptr(dtb), gdn._ptr(nw), float(eps), 128 ** -0.5 if scale is None else float(scale),
+             gdn._ptr(state), gdn._ptr(out), gdn._ptr(ws), ws.numel(), gdn._stream(p3.device))
+    return out[0] if single else out

@@ -194,9 +194,10 @@ class GatedDeltaLayer(torch.nn.Module):
         zeros = k.new_zeros(1, h, d)
         k = torch.cat((k, zeros), dim=0).index_select(0, plan.event_write)[None]
         v = torch.cat((v, zeros), dim=0).index_select(0, plan.event_write)[None]
-        a = a.index_select(0, plan.content_order).float()
-        g = -self.A_log.float().exp() * F.softplus(a + self.dt_bias.float())
-        beta = beta.index_select(0, plan.content_order).sigmoid().float()
+        control = torch.float64 if proj.dtype == torch.float64 else torch.float32
+        a = a.index_select(0, plan.content_order).to(control)
+        g = -self.A_log.to(control).exp() * F.softplus(a + self.dt_bias.to(control))
+        beta = beta.index_select(0, plan.content_order).sigmoid().to(control)
         control_zero = g.new_zeros(1, h)
         g = torch.cat((g, control_zero)).index_select(0, plan.event_write)[None]
         beta = torch.cat((beta, control_zero)).index_select(0, plan.event_write)[None]

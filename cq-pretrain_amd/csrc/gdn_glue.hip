@@ -363,6 +363,88 @@ void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content
   hipLaunchKernelGGL(add_f32_kernel, dim3((S * a.K + 255) / 256), dim3(256), 0, stream, d.dw, w.qsum, S * a.K);
 }
 
+// ---------------------------------------------------------------------------
+// One decode step of the layer for N independent sequences (models/decoding.py:16-78):
+// row 0 of a sequence is the sampled content token C, row 1 the text-mask query Q.
+//   C: pre = raw_C w[., K-1] + sum_j hist[j] w[., j] over the 3S channels, silu; the
+//      history shifts by one row and takes raw_C
+//   Q: the query conv of raw_Q's q channels over the updated history, silu
+//   q (both rows) and k (C) l2-normalized; v = C's conv output; g, beta from C's a, b;
+//   event 1 (Q) is read-only: k = v = 0, g = beta = 0.
+// One workgroup per sequence, S / 8 threads, 8 channels per thread in each of q|k|v.
+template <int K>
+__global__ __launch_bounds__(512) void decode_prep_kernel(DecArgs a) {
+  const int n = blockIdx.x, S = a.H * GN_D, c0 = threadIdx.x * 8;
+  const bf16* rc = a.proj + (int64_t)n * 2 * a.row_stride;
+  const bf16* rq = rc + a.row_stride;
+  bf16* hist = a.hist + (int64_t)n * (K - 1) * 3 * S;
+  f32x8 part[3], query = f32x8{};
+#pragma unroll
+  for (int p = 0; p < 3; ++p) {
+    const int c = p * S + c0;
+    f32x8 wk[K];
+    ld_taps<K>(a.w, c, wk);
+    const bf16x8 xc8 = ld8(rc + c);
+    const f32x8 xc = cvtf8(xc8);
+    bf16x8 h8[K - 1];
+    f32x8 pre = wk[K - 1] * xc;
+#pragma unroll
+    for (int j = 0; j < K - 1; ++j) {
+      h8[j] = ld8(hist + (int64_t)j * 3 * S + c);
+      pre += wk[j] * cvtf8(h8[j]);
+    }
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) pre[ch] *= sigm(pre[ch]);
+    part[p] = pre;
+    if (p == 0) {  // the query's conv sees the history after C entered it
+      f32x8 pq = wk[K - 1] * cvtf8(ld8(rq + c));
+#pragma unroll
+      for (int j = 0; j < K - 1; ++j) pq += wk[j] * (j + 1 < K - 1 ? cvtf8(h8[j + 1]) : xc);
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch) pq[ch] *= sigm(pq[ch]);
+      query = pq;
+    }
+#pragma unroll
+    for (int j = 0; j + 1 < K - 1; ++j) st8(hist + (int64_t)j * 3 * S + c, h8[j + 1]);
+    st8(hist + (int64_t)(K - 2) * 3 * S + c, xc8);
+  }
+  float sq = 0.f, sk = 0.f, sqq = 0.f;
+#pragma unroll
+  for (int ch = 0; ch < 8; ++ch) {
+    sq += part[0][ch] * part[0][ch];
+    sk += part[1][ch] * part[1][ch];
+    sqq += query[ch] * query[ch];
+  }
+  const float rq_c = __builtin_amdgcn_rsqf(sum16(sq) + 1e-6f), rk = __builtin_amdgcn_rsqf(sum16(sk) + 1e-6f);
+  const float rq_q = __builtin_amdgcn_rsqf(sum16(sqq) + 1e-6f);
+  const int64_t e0 = (int64_t)n * 2 * S + c0, e1 = e0 + S;
+  st8(a.q + e0, cvt8(part[0] * rq_c));
+  st8(a.q + e1, cvt8(query * rq_q));
+  st8(a.k + e0, cvt8(part[1] * rk));
+  st8(a.k + e1, bf16x8{});
+  st8(a.v + e0, cvt8(part[2]));
+  st8(a.v + e1, bf16x8{});
+  if (threadIdx.x < a.H) {
+    const int h = threadIdx.x;
+    const float av = (float)rc[4 * S + h] + a.dt_bias[h];
+    const int64_t gi = (int64_t)n * 2 * a.H + h;
+    a.g[gi] = -__expf(a.A_log[h]) * softplus_f(av);
+    a.beta[gi] = sigm((float)rc[4 * S + a.H + h]);
+    a.g[gi + a.H] = 0.f;
+    a.beta[gi + a.H] = 0.f;
+  }
+}
+
+void launch_decode_prep(const DecArgs& a, hipStream_t stream) {
+  if (a.N == 0) return;
+  const dim3 grid(a.N), block(a.H * 16);
+  switch (a.K) {
+    case 2: hipLaunchKernelGGL(decode_prep_kernel<2>, grid, block, 0, stream, a); break;
+    case 3: hipLaunchKernelGGL(decode_prep_kernel<3>, grid, block, 0, stream, a); break;
+    default: hipLaunchKernelGGL(decode_prep_kernel<4>, grid, block, 0, stream, a); break;
+  }
+}
+
 int gnorm_bwd_blocks(int64_t rows, int H) {
   const int64_t blocks = (rows * H + GN_ITEMS - 1) / GN_ITEMS;
   return (int)(blocks < 1024 ? blocks : 1024);

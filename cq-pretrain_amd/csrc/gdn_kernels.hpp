@@ -110,6 +110,21 @@ void launch_events_fwd(const EvArgs& a, const bf16* conv, bf16* q, bf16* k, bf16
                        hipStream_t stream);
 void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content_bounds, int n_content_docs,
                        const EvWork& w, hipStream_t stream);
+// One decode step's recurrence inputs (gdn_glue.hip).  proj rows: [N][2][row_stride]
+// (C, then Q; columns q|k|v, z, a, b); hist: bf16 [N][K-1][3S], updated in place;
+// outputs q, k, v bf16 [N][2][H][128] and g, beta fp32 [N][2][H].
+struct DecArgs {
+  int N, H, K;
+  const bf16* proj;
+  int64_t row_stride;
+  bf16* hist;
+  const bf16* w;  // conv weight [3S][K]
+  const float* A_log;
+  const float* dt_bias;
+  bf16 *q, *k, *v;
+  float *g, *beta;
+};
+void launch_decode_prep(const DecArgs& a, hipStream_t stream);
 // gated RMSNorm over D = 128 with an optional row gather (gdn_glue.hip)
 int gnorm_bwd_blocks(int64_t rows, int H);  // workgroups of the backward (dw partials per workgroup)
 void launch_gnorm_fwd(const bf16* y, const int32_t* index, int64_t rows, int H, const bf16* z, int64_t z_stride,

@@ -245,6 +245,26 @@ int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, const void* raw,
                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * One decode step of the GatedDelta layer for N independent sequences, each
+ * advancing by one sampled content token C and one text-mask query Q.  Replaces
+ * delta_step (models/decoding.py:16-78) between the layer's projection and
+ * out_proj, in three launches: the conv step of C over the conv history (which
+ * then shifts in C's raw row) and Q's query conv over the updated history, the
+ * l2 norms and gates; the recurrence over the two events (Q read-only); the
+ * gated norm with z from the projection rows.
+ *   proj: bf16 [N][2][proj_stride] (row 0 = C, row 1 = Q; columns q|k|v, z, a, b
+ *   of the fused projection); conv_history: bf16 [N][K-1][3S], updated in place;
+ *   conv_weight: bf16 [3S][K]; A_log, dt_bias: fp32 [H]; norm_weight: fp32 [128];
+ *   scale: the q scale (the reference uses 128^-0.5); state: fp32 [N][H][V][K]
+ *   value-first (as cqgdn_recurrent), updated in place; out: bf16 [N][2][H][128].
+ */
+size_t cqgdn_layer_decode_workspace_size(int N, int H);
+int cqgdn_layer_decode_step(int N, int H, int conv_kernel, const void* proj, int64_t proj_stride, void* conv_history,
+                            const void* conv_weight, const float* A_log, const float* dt_bias,
+                            const float* norm_weight, float eps, float scale, float* state, void* out, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/*
  * Chunk-local cumsum of g fp32 [T][H] over the chunk table, forward or reverse
  * (`chunk_local_cumsum` and reverse_cumsum(), ops/gated_delta_net.py:77-87,158-164).
  */

@@ -28,6 +28,8 @@ reference's own algorithms:
                           document, optional SiLU) behind ``ops/gated_delta_net.py:252-289``
 * ``gated_rms_norm``    - the layer's gated norm, ``models/backbone_qwen35.py:107-114`` behind
                           ``ops/gated_delta_net.py:67-74``
+* ``layer_decode_step`` - one decode step of the layer between its projections,
+                          ``models/decoding.py:16-78`` (CPU path), composed of the pieces above
 
 How each function is pinned (tests/test_oracle.py): closed forms on tiny inputs
 (one event, orthonormal keys, pure decay), chunked == per-event recurrence to
@@ -323,6 +325,36 @@ def gated_rms_norm(y, z, weight, eps=1e-6):
     y, z = y.double(), z.double()
     normalized = y * torch.rsqrt(y.square().mean(-1, keepdim=True) + eps)
     return normalized * weight.double() * torch.nn.functional.silu(z)
+
+
+def layer_decode_step(raw, z, a, b, conv_weight, A_log, dt_bias, norm_weight, history, state, eps=1e-6):
+    """One decode step of the GatedDelta layer between its projections, the CPU path of
+    models/decoding.py:16-78, in float64 for N sequences.
+
+    raw [N, 2, 3S] (row 0 the sampled content token C, row 1 the text-mask query Q), z
+    [N, 2, H, D], a, b [N, 2, H]; history [N, K-1, 3S]; state [N, H, V, K] value-first.
+    C's conv reads the history, which then shifts in C's raw row; Q's query conv reads the
+    shifted history; the recurrence applies C and then the read-only Q.
+    Returns (out [N, 2, H, D], history, state) without touching the inputs.
+    """
+    n, H, K = raw.shape[0], A_log.shape[0], conv_weight.shape[1]
+    S = H * 128
+    silu, w, x = torch.nn.functional.silu, conv_weight.double(), raw.double()
+    hist = history.double()
+    conv = silu(x[:, 0] * w[:, -1] + sum(hist[:, j] * w[:, j] for j in range(K - 1)))
+    hist = torch.cat((hist[:, 1:], x[:, :1]), dim=1)
+    query = silu(x[:, 1, :S] * w[:S, -1] + sum(hist[:, j, :S] * w[:S, j] for j in range(K - 1)))
+    cq, k, v = conv.split(S, -1)
+    zero = torch.zeros_like(k)
+    q = torch.stack((cq, query), 1).reshape(n, 2, H, 128)
+    k = torch.stack((k, zero), 1).reshape(n, 2, H, 128)
+    v = torch.stack((v, zero), 1).reshape(n, 2, H, 128)
+    g = -A_log.double().exp() * torch.nn.functional.softplus(a[:, 0].double() + dt_bias.double())
+    beta = b[:, 0].double().sigmoid()
+    g, beta = torch.stack((g, torch.zeros_like(g)), 1), torch.stack((beta, torch.zeros_like(beta)), 1)
+    st = state.double().clone()
+    y = decode_step(l2norm(q), l2norm(k), v, g, beta, st)
+    return gated_rms_norm(y, z, norm_weight, eps), hist, st
 
 
 def error_stats(actual, expected, tolerance=0.035):

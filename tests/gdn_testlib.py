@@ -51,3 +51,33 @@ def assemble(chunks, spans, T):
 def perm32(x):
     """Storage position of logical column x in the kernels' perm32 order (gdn_common.hpp)."""
     return (x & ~31) | (((x >> 2) & 3) << 3) | (((x >> 4) & 1) << 2) | (x & 3)
+
+
+def decode_plans(n, kernel=4):
+    """Plans of a single document for the prefill -> decode invariant (models/decoding.py:105-121).
+
+    ``prefill``: content rows 0..n, each a single-token group written by its own event, except
+    row n, the uncommitted target (read-only event), as CQDecoder prepares its prefill.
+    ``one_shot``: the same rows with row n written (the decode step's C) and one CQ query read
+    after it (the decode step's Q, hidden row n + 1), whose conv history is rows n-K+2 .. n.
+    """
+    from cqgdn import layer
+
+    long = lambda xs: torch.tensor(xs, dtype=torch.long)
+
+    def make(writes_last, query):
+        nc = n + 1
+        eq, ew = list(range(nc)), list(range(n)) + [n if writes_last else nc]
+        qs, qh, hidden = [], [], list(range(nc))
+        if query:
+            eq.append(nc)
+            ew.append(nc)
+            qs, qh = [nc], [list(range(n - kernel + 2, n + 1))]
+            hidden.append(nc)
+        return layer.LayerPlan(
+            content_order=torch.arange(nc), event_q=long(eq), event_write=long(ew), query_source=long(qs),
+            query_history=long(qh).reshape(len(qs), kernel - 1), content_cu=torch.tensor([0, nc], dtype=torch.int32),
+            content_bounds=(0, nc), event_cu=long([0, len(eq)]), event_bounds=(0, len(eq)),
+            hidden_length=len(hidden), hidden_event=long(hidden))
+
+    return make(False, False), make(True, True)

@@ -568,3 +568,65 @@ def test_layer_core_matches_float64_restatement(gdn, docs):
         assert_close_bf16(name, pd.grad[:, sl].cpu(), p64.grad[:, sl])
     for name, a, p in zip(("d_conv_weight", "d_A_log", "d_dt_bias", "d_norm_weight"), dp, params):
         assert_close_bf16(name, a.grad.cpu(), p.grad)
+
+
+def _decode_params(gen, H, K=4):
+    S = H * 128
+    w = (torch.rand(3 * S, K, generator=gen) - 0.5).bfloat16()
+    A_log = torch.rand(H, generator=gen).mul(3).add(0.01).log()
+    dt_bias = torch.randn(H, generator=gen) * 0.5
+    nw = 1 + 0.1 * torch.randn(128, generator=gen)
+    return w, A_log, dt_bias, nw
+
+
+def test_layer_decode_step_matches_oracle(gdn):
+    """Three consecutive decode steps (models/decoding.py:16-78) of three sequences through
+    cqgdn_layer_decode_step against the float64 oracle step: the gated-norm rows of C and Q, the
+    conv history (bit-exact: it holds raw rows) and the value-first state."""
+    from cqgdn import events
+
+    print("case layer decode: N=3, H=16, K=4, 3 steps", flush=True)
+    gen = torch.Generator().manual_seed(61)
+    N, H, K = 3, 16, 4
+    S, P = H * 128, 4 * H * 128 + 2 * H
+    w, A_log, dt_bias, nw = _decode_params(gen, H, K)
+    hist = (torch.randn(N, K - 1, 3 * S, generator=gen) * 0.7).bfloat16()
+    state = torch.randn(N, H, 128, 128, generator=gen) * 0.05
+    cache = {"conv": hist.to(DEV), "state": state.to(DEV)}
+    ref_hist, ref_state = hist.double(), state.double()
+    dev = [t.to(DEV) for t in (w, A_log, dt_bias, nw)]
+    for step in range(3):
+        proj = (torch.randn(N, 2, P, generator=gen) * 0.7).bfloat16()
+        out = events.layer_decode_step(proj.to(DEV), *dev, cache, heads=H)
+        torch.cuda.synchronize()
+        args = (proj[..., :3 * S], proj[..., 3 * S:4 * S].reshape(N, 2, H, 128), proj[..., 4 * S:4 * S + H],
+                proj[..., 4 * S + H:], w, A_log, dt_bias, nw)
+        ref_out, ref_hist, ref_state = O.layer_decode_step(*args, ref_hist, ref_state)
+        assert_close_bf16(f"out step {step}", out.cpu(), ref_out.reshape(N, 2, S))
+        assert torch.equal(cache["conv"].cpu().double(), ref_hist), "conv history differs"
+        assert_close_bf16(f"state step {step}", cache["state"].cpu(), ref_state)
+
+
+def test_layer_prefill_then_decode_matches_one_shot(gdn):
+    """Prefill with the uncommitted target (the CQDecoder convention, models/decoding.py:117-121),
+    then one decode step, equals the one-shot prefill of the plan where the step's content token
+    commits and its query reads after it: the C and Q rows and the final state, through two
+    independent routes (chunked precise forward vs the streaming decode step)."""
+    from cqgdn import events
+    from gdn_testlib import decode_plans
+
+    print("case prefill -> decode: 150 content rows, H=16", flush=True)
+    gen = torch.Generator().manual_seed(62)
+    n, H, K = 150, 16, 4
+    S, P = H * 128, 4 * H * 128 + 2 * H
+    w, A_log, dt_bias, nw = (t.to(DEV) for t in _decode_params(gen, H, K))
+    pre_plan, one_plan = decode_plans(n, K)
+    proj = (torch.randn(n + 2, P, generator=gen) * 0.7).bfloat16().to(DEV)
+    _, cache = events.layer_prefill(proj[:n + 1], w, A_log, dt_bias, nw, pre_plan, heads=H)
+    assert torch.equal(cache["conv"][0], proj[n - K + 1:n, :3 * S])
+    out = events.layer_decode_step(proj[n:n + 2], w, A_log, dt_bias, nw, cache, heads=H)
+    one, one_cache = events.layer_prefill(proj, w, A_log, dt_bias, nw, one_plan, heads=H)
+    torch.cuda.synchronize()
+    assert_close_bf16("C and Q rows", out.cpu(), one[n:n + 2].double().cpu())
+    assert_close_bf16("state", cache["state"].cpu(), one_cache["state"].double().cpu())
+    assert torch.equal(cache["conv"][0], proj[n - K + 2:n + 1, :3 * S])
