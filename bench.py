@@ -277,7 +277,7 @@ def main():
         profile_workload(torch, step, args.steps)
         return
     kernels = {} if args.no_extra else kernel_table(torch, _lib, workmodel, step, bounds)
-    dominant = max(kernels, key=lambda k: kernels[k]["us"]) if kernels else "bwd_dqk"
+    dominant = max(kernels, key=lambda k: kernels[k]["us"]) if kernels else "bwd_dkw"
 
     # timed region: K steps, the dominant kernel's launches bracketed by HIP events on its stream
     with _lib.KernelTimer(dominant, args.steps) as timer:

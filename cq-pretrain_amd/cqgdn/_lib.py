@@ -15,9 +15,9 @@ LIB_PATH = Path(__file__).resolve().with_name("libcqgdn.so")
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 NORMALIZE, TRAINING, PRECISE = 1, 2, 4
-FWD_BUFFERS, BWD_BUFFERS = 12, 9
+FWD_BUFFERS, BWD_BUFFERS = 12, 6
 FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "UT", "KgT", "hT", "vnT", "vscale")
-BWD_NAMES = ("dvlT", "XT", "dh", "dVn", "dKp", "dW", "dGp", "knP", "WT")
+BWD_NAMES = ("dvlT", "XT", "dh", "dVn", "knP", "WT")
 
 # every symbol include/cqgdn.h declares, with (restype, argtypes)
 _P, _I, _I64, _U, _F, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint, ctypes.c_float, ctypes.c_size_t
@@ -63,7 +63,7 @@ class EventPlan(ctypes.Structure):
                 ("history_list", _P), ("history_rows", _P)]
 
 
-KERNELS = ("fwd_prep", "fwd_scan", "fwd_out", "bwd_local", "bwd_scan", "bwd_dqk", "bwd_wy", "recurrent")
+KERNELS = ("fwd_prep", "fwd_scan", "fwd_out", "bwd_local", "bwd_scan", "bwd_dkw", "recurrent")
 
 _LIB = None
 
@@ -122,7 +122,7 @@ def bwd_offsets(T: int, H: int, n_chunks: int) -> dict:
 class KernelTimer:
     """Time every launch of one library kernel with hipEvents on its own stream.
 
-    Usage: ``with KernelTimer("bwd_dqk", 64) as t: ...``; afterwards ``t.ms``
+    Usage: ``with KernelTimer("bwd_dkw", 64) as t: ...``; afterwards ``t.ms``
     holds the per-launch durations (the exit waits for the recorded events).
     """
 

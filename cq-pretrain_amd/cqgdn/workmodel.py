@@ -14,8 +14,8 @@ split over the kernels by the contractions each one performs:
   fwd_out    Q S, Q K^T, P v_new                                            2 c d^2 + 4 c^2 d
   bwd_local  dv_local = P^T dO, X = Q^T dO (P and -W^T recomputed, not counted)  2 c^2 d + 2 c d^2
   bwd_scan   dS += W^T dv_new, dv_new += Kg dS                              4 c d^2
-  bwd_dqk    dP, dQ and dK from P, dQ from S, dK from dS, dW = -dv_new S^T  6 c^2 d + 6 c d^2
-  bwd_wy     dT (2), d(beta gamma K), d(beta V), dA = -T^T dT T^T, dK from dA  12 c^2 d + 4 c^3
+  bwd_dkw    dP, dQ and dK from P, dQ from S, dK from dS, dW = -dv_new S^T;
+             dT (2), d(beta gamma K), d(beta V), dA = -T^T dT T^T, dK from dA  18 c^2 d + 6 c d^2 + 4 c^3
 
 HBM bytes are the kernel's declared inputs and outputs, each read or written
 once, in the workspace layouts of gdn_layout.hpp: event-indexed rows scale with
@@ -35,7 +35,7 @@ PEAK_BF16_FLOPS = 2.5e15  # MI355X dense bf16 MFMA
 PEAK_HBM_BYTES = 8.0e12  # MI355X HBM3E
 
 FWD_KERNELS = ("fwd_prep", "fwd_scan", "fwd_out")
-BWD_KERNELS = ("bwd_local", "bwd_scan", "bwd_dqk", "bwd_wy")
+BWD_KERNELS = ("bwd_local", "bwd_scan", "bwd_dkw")
 SCAN_KERNELS = ("fwd_scan", "bwd_scan")
 
 
@@ -56,8 +56,7 @@ def flops_per_chunk(kernel, c, d=D):
         "fwd_out": 2 * cd2 + 4 * c2d,
         "bwd_local": 2 * c2d + 2 * cd2,
         "bwd_scan": 4 * cd2,
-        "bwd_dqk": 6 * c2d + 6 * cd2,
-        "bwd_wy": 12 * c2d + 4 * c3,
+        "bwd_dkw": 18 * c2d + 6 * cd2 + 4 * c3,
     }[kernel]
 
 
@@ -80,10 +79,8 @@ def bytes_per_chunk(kernel, c, d=D):
         "bwd_local": 3 * e + 2 * s + tm + tile + sq + e + tile,
         # Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh, dv_new (both value-slice-major)
         "bwd_scan": e + s + tile + sq + tile + sq + tile,
-        # qn, kn, rq, gcum, h^T, v_new^T, dO, dh, dv_new -> dq, dK partial (fp32), dW, dG partial
-        "bwd_dqk": 2 * e + 2 * s + sq + tile + e + sq + tile + e + e32 + e + s,
-        # kn, v, beta, gcum, rk, T, dW, dv_new, dK partial, dG partial -> dk, dv, dg, dbeta
-        "bwd_wy": e + e + 3 * s + tm + e + tile + e32 + s + 2 * e + 2 * s,
+        # qn, kn, rq, rk, gcum, h^T, v_new^T, dO, dh, dv_new, v, beta, T -> dq, dk, dv, dg, dbeta
+        "bwd_dkw": 2 * e + 3 * s + sq + tile + e + sq + tile + e + s + tm + 3 * e + 2 * s,
     }[kernel]
 
 

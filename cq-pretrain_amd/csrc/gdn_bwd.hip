@@ -7,18 +7,17 @@
 //   bwd_local  (grid NC x H)  dv_local = scale P^T dO ;  X = scale (gam Qn)^T dO
 //   bwd_scan   (serial, reverse)  dVn = dv_local + kdec * (Kn dS_{c+1})
 //                                 dS_c = exp(G_last) dS_{c+1} + X - W^T dVn
-//   bwd_dqk    (grid NC x H)  dQn = scale gam (dO S_c^T) + (scale dP Gam) Kn   (dP = dO Vn^T)
-//                             dKn(part) = (scale dP Gam)^T Qn + kdec (Vn dS_{c+1}^T)
-//                             dW = -dVn S_c^T ; dG terms of the output and state update;
-//                             l2norm backward of dq
-//   bwd_wy     (grid NC x H)  dT = dW (beta gam Kn)^T + dVn (beta V)^T ; dA = -(T^T dT T^T)
-//                             dKn += beta (dA Gam) Kn + (dA Gam)^T (beta Kn) + beta gam (T^T dW)
-//                             dV = beta (T^T dVn) ; dbeta ; dG ; reverse cumsum -> dg ;
-//                             l2norm backward of dk
+//   bwd_dkw    (grid NC x H), in one workgroup:
+//              dQn = scale gam (dO S_c^T) + (scale dP Gam) Kn   (dP = dO Vn^T); l2norm backward of dq
+//              dKn(part) = (scale dP Gam)^T Qn + kdec (Vn dS_{c+1}^T)
+//              dW = -dVn S_c^T ; dG terms of the output and state update
+//              dT = dW (beta gam Kn)^T + dVn (beta V)^T ; dA = -(T^T dT T^T)
+//              dKn += beta (dA Gam) Kn + (dA Gam)^T (beta Kn) + beta gam (T^T dW)
+//              dV = beta (T^T dVn) ; dbeta ; dG ; reverse cumsum -> dg ; l2norm backward of dk
 //
 // This is the reference's backward op chain (ops/gated_delta_net.py:188-214:
 // chunk_bwd_dv_local, chunk_gated_delta_rule_bwd_dhu, chunk_bwd_dqkwg,
-// prepare_wy_repr_bwd_da/_full, reverse_cumsum, l2_bwd) regrouped into four
+// prepare_wy_repr_bwd_da/_full, reverse_cumsum, l2_bwd) regrouped into three
 // kernels.  All reductions run in a fixed order (no atomics), so results are
 // bitwise reproducible from run to run.
 #include "gdn_common.hpp"
@@ -29,7 +28,6 @@ namespace cqgdn {
 
 constexpr int LDK = 136;  // bf16 row stride, 64 x 128 tiles
 constexpr int LDT = 72;   // bf16 row stride, 128 x 64 and 64 x 64 tiles
-constexpr int LDQ = 132;  // fp32 row stride, 64 x 128 staging
 
 // ---------------------------------------------------------------------------
 // bwd_local
@@ -453,14 +451,29 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// bwd_dqk
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
+// bwd_dkw: the dq/dK/dW part and then the WY part in one workgroup per (chunk, head), so the
+// dK partial (registers), dW (LDS), the dG partial (a register of wave 0) and the
+// K tile never leave the chip.  LDS regions are reused as their first users die
+// (81,408 bytes: two workgroups per CU):
+//   R1  Q rows            -> V rows (wy)
+//   R2  K rows            (both parts)
+//   R3  dPm               -> T (wy)
+//   R4a dO rows           -> dVn tile (value-slice-major) + q.dq row dots
+//                         -> dT / beta dM staging + beta, dbeta and k.dK partials (wy)
+//   R4b v_new^T           -> dW rows [t][k]   -> Y^T staging (wy)
+// The l2norm backward of dq runs on the phase-2 registers (per-wave row dots in
+// LDS), so no fp32 staging tile is needed and dQ's registers carry the dK partial.
+constexpr int DKW_R1 = 0, DKW_R2 = 64 * LDK * 2, DKW_R3 = DKW_R2 + 64 * LDK * 2, DKW_R4A = DKW_R3 + 64 * LDT * 2,
+              DKW_R4B = DKW_R4A + 64 * LDK * 2, DKW_BYTES = DKW_R4B + 128 * LDT * 2;
+
+__global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     const bf16* __restrict__ qn, const bf16* __restrict__ kn, const float* __restrict__ rq,
-    const float* __restrict__ gc, const bf16* __restrict__ hT, const bf16* __restrict__ vnT,
-    const bf16* __restrict__ dout, const bf16* __restrict__ dh, const bf16* __restrict__ dVn,
-    const int32_t* __restrict__ chunks, int H, float scale, int normalize, bf16* __restrict__ dq,
-    float* __restrict__ dKp, bf16* __restrict__ dW, float* __restrict__ dGp) {
+    const float* __restrict__ rk, const float* __restrict__ gc, const bf16* __restrict__ hT,
+    const bf16* __restrict__ vnT, const bf16* __restrict__ dout, const bf16* __restrict__ dh,
+    const bf16* __restrict__ dVn, const bf16* __restrict__ vin, const float* __restrict__ beta,
+    const bf16* __restrict__ Tm, const int32_t* __restrict__ chunks, int H, float scale, int normalize,
+    bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv, float* __restrict__ dg,
+    float* __restrict__ dbeta) {
   // grid (H, NC), chunks first to last: the reverse state scan wrote the first
   // chunks last, so they are the likeliest still in the memory-side cache
   const int h = blockIdx.x, c = blockIdx.y;
@@ -469,27 +482,21 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
 
-  // Q, K and dPm are also read transposed (ld8_tr), so no transposed copies are
-  // kept and two workgroups fit a CU's LDS
-  __shared__ __attribute__((aligned(16))) bf16 Qs[64 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 Ks[64 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 dPm[64 * LDT];  // [t][s]
-  __shared__ __attribute__((aligned(16))) uint8_t un[(64 * LDK + 128 * LDT) * 2];  // dOs | VnT, later DQs
+  __shared__ __attribute__((aligned(16))) uint8_t lds[DKW_BYTES];
   __shared__ float Gs[64];
   __shared__ float dgw[4][64];
-  __shared__ float red[4];
-  bf16* dOs = reinterpret_cast<bf16*>(un);
-  bf16* VnT = dOs + 64 * LDK;  // v_new^T [v][t], read transposed as v_new rows
-  float* DQs = reinterpret_cast<float*>(un);
-  float rs_t;  // rsqrt norm of q at event t = tid / 4, loaded with the inputs
+  __shared__ float Rs[64];  // rsqrt norms of q (1 without normalize)
+  bf16* Qs = reinterpret_cast<bf16*>(lds + DKW_R1);
+  bf16* Ks = reinterpret_cast<bf16*>(lds + DKW_R2);
+  bf16* dPm = reinterpret_cast<bf16*>(lds + DKW_R3);
+  bf16* dOs = reinterpret_cast<bf16*>(lds + DKW_R4A);
+  bf16* VnT = reinterpret_cast<bf16*>(lds + DKW_R4B);  // v_new^T [v][t], read transposed as v_new rows
+  bf16* dVs = dOs;                                    // dVn tile, from phase 3 on
+  float* dqdot = reinterpret_cast<float*>(lds + DKW_R4A + CH * D * 2);  // [4][64] after the dVn tile
+  bf16* dWs = VnT;                                    // dW rows [t][k], from phase 4 on
 
-  // Global operands are requested one phase ahead of their use, so the kernel
-  // pays about one memory round trip.  This wave's state fragments: rows
-  // k = 16 (2 wave + mm) + r of h (with the phase-0 rows) and of dS_{c+1}
-  // (before phase 2), value block kb (32 kb + 8 q4 .. + 8).  Together the four
-  // waves hold all of both, so <h, dS> needs no second read.
-  // The h fragments (8 values of one key row) are column gathers of the
-  // forward's h^T [v][k].
+  // This wave's state fragments: rows k = 16 (2 wave + mm) + r of h
+  // (column gathers of h^T) and of dS_{c+1}, value block kb.
   const bf16* ht = hT + cb * (D * D);
   const bf16* dhc = dh + cb * (D * D);
   bf16x8 bh[2][4], bd[2][4];
@@ -503,9 +510,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
     const bool in = t < ci.len;
     const int tc = clamp_row(t, ci.len);
     const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
-    if (p == 0) Gs[t] = gc[(size_t)(ci.start + tc) * H + h];
-    rs_t = normalize ? rq[(size_t)(ci.start + tc) * H + h] : 1.f;
-    // v_new^T tile (columns past a tail chunk's length are zero in the forward's tile)
+    if (p == 0) {
+      Gs[t] = gc[(size_t)(ci.start + tc) * H + h];
+      Rs[t] = normalize ? rq[(size_t)(ci.start + tc) * H + h] : 1.f;
+    }
     const bf16* vt = vnT + cb * (D * CH);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -516,17 +524,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      const bf16x8 xq = keep_if(in, ld8(qn + row + col));
-      const bf16x8 xk = keep_if(in, ld8(kn + row + col));
-      st8(Qs + t * LDK + col, xq);
-      st8(Ks + t * LDK + col, xk);
+      st8(Qs + t * LDK + col, keep_if(in, ld8(qn + row + col)));
+      st8(Ks + t * LDK + col, keep_if(in, ld8(kn + row + col)));
       st8(dOs + t * LDK + col, keep_if(in, ld8(dout + row + col)));
-
     }
   }
   __syncthreads();
   const float glast = Gs[ci.len - 1];
-  float* dg = dgw[wave];
+  float* dgl = dgw[wave];
 
   // ---- phase 1: P, dP for t-tile = wave, s-tiles <= wave ----
   {
@@ -539,8 +544,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
           p = mfma(ld8(Qs + (16 * wave + r) * LDK + 32 * kb + 8 * q4), ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4), p);
-          dp = mfma(ld8(dOs + (16 * wave + r) * LDK + 32 * kb + 8 * q4),
-                    ld8_tr(VnT, LDT, 32 * kb, 16 * n), dp);
+          dp = mfma(ld8(dOs + (16 * wave + r) * LDK + 32 * kb + 8 * q4), ld8_tr(VnT, LDT, 32 * kb, 16 * n), dp);
         }
         const int s = 16 * n + r;
         float colE = 0.f;
@@ -555,7 +559,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
         }
         colE += __shfl_xor(colE, 16, 64);
         colE += __shfl_xor(colE, 32, 64);
-        if (q4 == 0) dg[s] -= colE;
+        if (q4 == 0) dgl[s] -= colE;
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) dPm[(16 * wave + 4 * q4 + i) * LDT + 16 * n + r] = (bf16)dpm[i];
@@ -563,7 +567,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float x = sum16(rowE[i]);
-      if (r == 0) dg[16 * wave + 4 * q4 + i] += x;
+      if (r == 0) dgl[16 * wave + 4 * q4 + i] += x;
     }
   }
   __syncthreads();
@@ -574,7 +578,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
     for (int kb = 0; kb < 4; ++kb)
       bd[mm][kb] = ld8(dhc + (2 * kb + (q4 >> 1)) * (D * 16) + (16 * (2 * wave + mm) + r) * 16 + 8 * (q4 & 1));
 
-  // ---- phase 2: dQ (rows t, k-tiles 2w, 2w+1) ----
+  // ---- phase 2: dQ (rows t, k-tiles 2w, 2w+1); dG_t from the output term ----
   f32x4 dQ[2][4];
   {
     f32x4 a1[2][4];
@@ -600,7 +604,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
         for (int mm = 0; mm < 2; ++mm)
           dQ[mm][n] = mfma(a, ld8_tr(Ks, LDK, 32 * kb, 16 * (2 * wave + mm)), dQ[mm][n]);
       }
-    // dQ += scale * gam_t * (dO h^T); dG_t += sum_k Qn * that
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
 #pragma unroll
@@ -615,23 +618,54 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
           x += (float)Qs[t * LDK + 16 * (2 * wave + mm) + r] * inter;
         }
         x = sum16(x);
-        if (r == 0) dg[t] += x;
+        if (r == 0) dgl[t] += x;
       }
     }
   }
 
-  // dVn for phase 4: its value-slice-major tile is copied global -> LDS
-  // asynchronously into the dO tile (free once every wave has finished phase 2)
-  // while phase 3 runs.  Fragment reads of it are contiguous 512-byte runs.
-  __syncthreads();
-  bf16* dVs = dOs;
+  // ---- l2norm backward of dq on the phase-2 registers: this wave's parts of the row dots q_t . dq_t ----
+  float pdot[4][4];
+#pragma unroll
+  for (int n = 0; n < 4; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * n + 4 * q4 + i;
+      float x = 0.f;
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) x += (float)Qs[t * LDK + 16 * (2 * wave + mm) + r] * dQ[mm][n][i];
+      pdot[n][i] = sum16(x);
+    }
+  __syncthreads();  // every read of the dO rows is done: the dVn tile and the row dots may replace them
   {
     const bf16* dvs = dVn + cb * (CH * D);
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
   }
+  if (r == 0) {
+#pragma unroll
+    for (int n = 0; n < 4; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dqdot[wave * 64 + 16 * n + 4 * q4 + i] = pdot[n][i];  // after the tile's 16 KB
+  }
+  __syncthreads();
+  // dq = rq (dQ - q (q . dQ)), stored from the C layout (16 lanes: 32 contiguous bytes of a row)
+#pragma unroll
+  for (int n = 0; n < 4; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * n + 4 * q4 + i;
+      const float dot = dqdot[t] + dqdot[64 + t] + dqdot[128 + t] + dqdot[192 + t];
+      const float rs = Rs[t];
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) {
+        const int k = 16 * (2 * wave + mm) + r;
+        const float x = normalize ? (dQ[mm][n][i] - (float)Qs[t * LDK + k] * dot) * rs : dQ[mm][n][i];
+        if (t < ci.len) dq[((size_t)(ci.start + t) * H + h) * D + k] = (bf16)x;
+      }
+    }
 
-  // ---- phase 3: dK^T (k rows, t columns) ----
+  // ---- phase 3: dK^T partial (k rows, t columns), kept in registers for the wy part ----
+  f32x4 fkp[2][4];
   {
     float esum = 0.f;
 #pragma unroll
@@ -652,8 +686,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-        for (int n = 0; n < 4; ++n)
-          a4[n] = mfma(bd[mm][kb], ld8_tr(VnT, LDT, 32 * kb, 16 * n), a4[n]);
+        for (int n = 0; n < 4; ++n) a4[n] = mfma(bd[mm][kb], ld8_tr(VnT, LDT, 32 * kb, 16 * n), a4[n]);
       }
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
@@ -664,14 +697,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
         float e = st[0] * kk[0] + st[1] * kk[1] + st[2] * kk[2] + st[3] * kk[3];
         e += __shfl_xor(e, 16, 64);
         e += __shfl_xor(e, 32, 64);
-        if (q4 == 0) dg[t] -= e;
+        if (q4 == 0) dgl[t] -= e;
         esum += (q4 == 0) ? e : 0.f;
-        if (t < ci.len)
-          *reinterpret_cast<f32x4*>(dKp + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4) = a3[n] + st;
+        fkp[mm][n] = keep_if(t < ci.len, a3[n] + st);
       }
     }
     esum = sum16(esum);
-    if (lane == 0) dg[ci.len - 1] += esum;
     // <h, dS_{c+1}> over this wave's quarter of both
     float x = 0.f;
 #pragma unroll
@@ -680,16 +711,32 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
       for (int kb = 0; kb < 4; ++kb) {
         const f32x8 a = cvtf8(bh[mm][kb]), b = cvtf8(bd[mm][kb]);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) x += a[s] * b[s];
+        for (int s8 = 0; s8 < 8; ++s8) x += a[s8] * b[s8];
       }
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
-    if (lane == 0) red[wave] = x;
+    if (lane == 0) dgl[ci.len - 1] += esum + __expf(glast) * x;
+  }
+  __syncthreads();  // the dVn copies have landed; every read of Q, dPm and v_new^T is done
+
+  // the wy part's V rows, T rows and beta, requested now and stored over Q and dPm after phase 4
+  bf16x8 pv[4], pt[2];
+  float pb;
+  {
+    const int t = tid >> 2, p = tid & 3;
+    const bool in = t < ci.len;
+    const int tc = clamp_row(t, ci.len);
+    const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
+    pb = keep_if(in, beta[(size_t)(ci.start + tc) * H + h]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) pv[j] = keep_if(in, ld8(vin + row + 32 * j + 8 * p));
+    const bf16* tm = Tm + cb * (CH * CH);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) pt[j] = ld8(tm + t * CH + 32 * j + 8 * p);
   }
 
-  __syncthreads();  // the dVn copies have landed (the barrier waits for them)
-
-  // ---- phase 4: dW = -dVn S^T (rows t; bwd_wy gathers its transposed view) ----
+  // ---- phase 4: dW = -dVn S^T into LDS rows [t][k]; the wy part's dVn fragments ----
+  bf16x8 fdv[4], fvt[2][2];
   {
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
@@ -704,127 +751,53 @@ __global__ __launch_bounds__(256, 2) void bwd_dqk_kernel(
         f32x4 w = zero4();  // dW^T[k = 16 m + 4 q4 + i][t]
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) w = mfma(bh[mm][kb], av[kb], w);
-        if (t < ci.len) st4(dW + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4, w);
+        st4(dWs + t * LDK + 16 * m + 4 * q4, w);
       }
     }
+    const int t = 16 * wave + r;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+      fdv[kb] = keep_if(t < ci.len, ld8(dVs + (2 * kb + (q4 >> 1)) * (CH * 16) + t * 16 + 8 * (q4 & 1)));
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) fvt[mm][kb] = ld8_tr(dVs + (2 * wave + mm) * (CH * 16), 16, 32 * kb, 0);
   }
-  __syncthreads();  // all reads of dOs / VnT are done: DQs may overwrite them
+  __syncthreads();  // dW rows complete, dG partials complete, the dVn tile consumed
 
-  // ---- phase 5: l2norm backward of dq, dG partial ----
+  // ---- the WY part, on the chip-resident operands ----
+  const float dgp_t = (tid < 64) ? dgw[0][tid] + dgw[1][tid] + dgw[2][tid] + dgw[3][tid] : 0.f;
+  bf16* Vs = Qs;
+  bf16* Ts = dPm;
+  bf16* S1 = dOs;                                                              // dT[t][s], then beta dM [i][j]
+  bf16* S2 = VnT;                                                              // Y^T[j][t], over dW rows
+  float* Bs = reinterpret_cast<float*>(lds + DKW_R4A + 64 * LDT * 2);          // after S1
+  float* dbw = Bs + 64;                                                        // [4][64]
+  float* dkdot = dbw + 256;                                                    // [4][64]
+  {
+    const int t = tid >> 2, p = tid & 3;
+    if (p == 0) Bs[t] = pb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) st8(Vs + t * LDK + 32 * j + 8 * p, pv[j]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) st8(Ts + t * LDT + 32 * j + 8 * p, pt[j]);
+  }
+  __syncthreads();  // dgp_t has been read everywhere it is needed
+  dgw[wave][lane] = 0.f;
+  dbw[wave * 64 + lane] = 0.f;
+  __syncthreads();
+  float* dbl = dbw + wave * 64;
+
+  // ---- wy phase 1: dT = dW (beta gam K)^T + dVn (beta V)^T -> S1 = dT[t][s]; dW fragments ----
+  bf16x8 fwt[2][2];
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) DQs[(16 * n + 4 * q4 + i) * LDQ + 16 * (2 * wave + mm) + r] = dQ[mm][n][i];
-  __syncthreads();
+    for (int kb = 0; kb < 2; ++kb) fwt[mm][kb] = ld8_tr(dWs, LDK, 32 * kb, 16 * (2 * wave + mm));
   {
-    const int t = tid >> 2, p = tid & 3;
-    const bool in = t < ci.len;
-    f32x8 dqn[4], qv[4];
-    float dot = 0.f;
+    bf16x8 fdw[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = 32 * j + 8 * p;
-      const f32x4 lo = *reinterpret_cast<const f32x4*>(DQs + t * LDQ + col);
-      const f32x4 hi = *reinterpret_cast<const f32x4*>(DQs + t * LDQ + col + 4);
-      dqn[j] = f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      qv[j] = cvtf8(ld8(Qs + t * LDK + col));
-#pragma unroll
-      for (int s = 0; s < 8; ++s) dot += qv[j][s] * dqn[j][s];
-    }
-    dot += __shfl_xor(dot, 1, 64);
-    dot += __shfl_xor(dot, 2, 64);
-    if (in) {
-      const size_t row = ((size_t)(ci.start + t) * H + h) * D;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const f32x8 out = normalize ? (dqn[j] - qv[j] * dot) * rs_t : dqn[j];
-        st8(dq + row + 32 * j + 8 * p, cvt8(out));
-      }
-    }
-  }
-  if (tid < 64) {
-    const int t = tid;
-    float tot = dgw[0][t] + dgw[1][t] + dgw[2][t] + dgw[3][t];
-    if (t == ci.len - 1) tot += __expf(glast) * (red[0] + red[1] + red[2] + red[3]);
-    if (t < ci.len) dGp[(size_t)(ci.start + t) * H + h] = tot;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// bwd_wy
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void bwd_wy_kernel(
-    const bf16* __restrict__ kn, const bf16* __restrict__ vin, const float* __restrict__ beta,
-    const float* __restrict__ gc, const float* __restrict__ rk, const bf16* __restrict__ Tm,
-    const bf16* __restrict__ dW, const bf16* __restrict__ dVn,
-    const float* __restrict__ dKp, const float* __restrict__ dGp,
-    const int32_t* __restrict__ chunks, int H, int normalize, bf16* __restrict__ dk, bf16* __restrict__ dv,
-    float* __restrict__ dg, float* __restrict__ dbeta) {
-  // grid (H, NC), chunks last to first: bwd_dqk wrote the last chunks last
-  const int h = blockIdx.x, c = gridDim.y - 1 - blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = lane & 15, q4 = lane >> 4;
-  const ChunkInfo ci = chunk_info(chunks, c);
-  const size_t cb = (size_t)c * H + h;
-
-  // K, T and beta*dM are also read transposed (ld8_tr) and dK stays in
-  // registers, so two workgroups fit a CU's LDS
-  __shared__ __attribute__((aligned(16))) bf16 Ks[64 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 Vs[64 * LDK];
-  __shared__ __attribute__((aligned(16))) bf16 Ts[64 * LDT];  // T[t][s]
-  __shared__ __attribute__((aligned(16))) bf16 S1[64 * LDT];  // dT[t][s], then beta*dM [i][j]
-  __shared__ __attribute__((aligned(16))) bf16 S2[64 * LDT];  // Y^T[j][t]
-  __shared__ float Gs[64], Bs[64];
-  __shared__ float dgw[4][64], dbw[4][64];
-  __shared__ float dkdot[4][64];  // per-wave parts of k_t . dK_t
-
-  // Global operands are requested one phase ahead of their use.  With the
-  // inputs: this wave's rows t = 16 wave + r of dW and dVn (phase 1), and the
-  // dG partial of event tid (phase 5).
-  bf16x8 fdw[4], fdv[4];
-  {
-    const int t = 16 * wave + r;
-    const size_t row = ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D + 8 * q4;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      fdw[kb] = keep_if(t < ci.len, ld8(dW + row + 32 * kb));
-      fdv[kb] = keep_if(t < ci.len, ld8(dVn + cb * (CH * D) + (2 * kb + (q4 >> 1)) * (CH * 16) + t * 16 + 8 * (q4 & 1)));
-    }
-  }
-  const float dgp_t = keep_if(lane < ci.len, dGp[(size_t)(ci.start + clamp_row(lane, ci.len)) * H + h]);
-
-  {
-    const int t = tid >> 2, p = tid & 3;
-    const bool in = t < ci.len;
-    const int tc = clamp_row(t, ci.len);
-    const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
-    if (p == 0) {
-      Gs[t] = gc[(size_t)(ci.start + tc) * H + h];
-      Bs[t] = keep_if(in, beta[(size_t)(ci.start + tc) * H + h]);
-    }
-    dgw[wave][lane] = 0.f;
-    dbw[wave][lane] = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int col = 32 * j + 8 * p;
-      st8(Ks + t * LDK + col, keep_if(in, ld8(kn + row + col)));
-      st8(Vs + t * LDK + col, keep_if(in, ld8(vin + row + col)));
-    }
-    const bf16* tm = Tm + cb * (CH * CH);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int col = 32 * j + 8 * p;
-      st8(Ts + t * LDT + col, ld8(tm + t * CH + col));
-    }
-  }
-  __syncthreads();
-  float* dgl = dgw[wave];
-  float* dbl = dbw[wave];
-
-  // ---- phase 1: dT = dW (beta gam K)^T + dVn (beta V)^T, rows t = t-tile wave -> S1 = dT[t][s] ----
-  {
+    for (int kb = 0; kb < 4; ++kb) fdw[kb] = ld8(dWs + (16 * wave + r) * LDK + 32 * kb + 8 * q4);
     f32x4 ak[4], av[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) ak[n] = av[n] = zero4();
@@ -843,43 +816,12 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
       for (int i = 0; i < 4; ++i) S1[(16 * wave + 4 * q4 + i) * LDT + s] = (bf16)(ak[n][i] * fk + av[n][i] * fv);
     }
   }
-  __syncthreads();
-
-  // phase-4 operands, requested before phase 2: rows k (or v) = 16 (2 wave + mm) + r
-  // of dW^T and dVn^T, the dK partial rows t = 16 n + r at those columns, and
-  // the rsqrt norms of k at those rows.  Both transposed operands are column
-  // gathers: dW^T of the dW rows (events past the chunk re-read its last row;
-  // they meet T's identity rows past the chunk and zero K rows, so they add
-  // nothing to a kept result), dVn^T of the value-slice-major dVn tile (slice m
-  // is a [64][16] matrix).
-  bf16x8 fwt[2][2], fvt[2][2];
-  f32x4 fkp[2][4];
   float rsn[4];
-  {
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
-      rsn[n] = normalize ? rk[(size_t)(ci.start + clamp_row(16 * n + r, ci.len)) * H + h] : 1.f;
-    const bf16* dwr = dW + ((size_t)ci.start * H + h) * D;
-    const bf16* dvs = dVn + cb * (CH * D);
-#pragma unroll
-    for (int mm = 0; mm < 2; ++mm) {
-      const int m = 2 * wave + mm;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        fwt[mm][kb] = gather8_col_rows(dwr, H * D, 32 * kb, 16 * m, ci.len);
-        fvt[mm][kb] = gather8_col(dvs + m * (CH * 16), 16, 32 * kb, 0);
-      }
-#pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const int t = 16 * n + r;
-        fkp[mm][n] = keep_if(t < ci.len, *reinterpret_cast<const f32x4*>(
-                                             dKp + ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D + 16 * m +
-                                             4 * q4));
-      }
-    }
-  }
+  for (int n = 0; n < 4; ++n) rsn[n] = normalize ? rk[(size_t)(ci.start + clamp_row(16 * n + r, ci.len)) * H + h] : 1.f;
+  __syncthreads();  // S1 complete; every wave holds its dW fragments (S2 may overwrite the rows)
 
-  // ---- phase 2: Y = dT T^T (rows t = t-tile wave) -> S2 = Y^T[j][t] ----
+  // ---- wy phase 2: Y = dT T^T -> S2 = Y^T[j][t] ----
   {
     bf16x8 a[2];
 #pragma unroll
@@ -897,9 +839,9 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   }
   __syncthreads();
 
-  // ---- phase 3: dA = -T^T Y (rows i = i-tile wave), dM, dbeta and dG from A ----
+  // ---- wy phase 3: dA = -T^T Y, dM, dbeta and dG from A ----
   {
-    const int kb0 = wave >= 2 ? 1 : 0;  // T[t][i] = 0 for t < i
+    const int kb0 = wave >= 2 ? 1 : 0;
     bf16x8 at[2], ak[4];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) at[kb] = ld8_tr(Ts, LDT, 32 * kb, 16 * wave);
@@ -951,7 +893,7 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
   }
   __syncthreads();
 
-  // ---- phase 4b: dV^T (v rows 2w, 2w+1; s columns): dv = beta (T^T dVn) ----
+  // ---- wy phase 4b: dv = beta (T^T dVn) ----
   {
     float colB[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -984,7 +926,7 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
     }
   }
 
-  // ---- phase 4a: dK (rows t = 16n + r, k columns 16 (2w + mm) + 4 q4 ..) in registers ----
+  // ---- wy phase 4a: dK in registers ----
   f32x4 dkr[2][4];
   {
     float colB[4] = {0.f, 0.f, 0.f, 0.f}, colG[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1000,10 +942,10 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
         const bf16x8 w = fwt[mm][kb];
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
-          if (n >= 2 * kb) ak[n] = mfma(a, ld8(S1 + (16 * n + r) * LDT + 32 * kb + 8 * q4), ak[n]);  // j < i
+          if (n >= 2 * kb) ak[n] = mfma(a, ld8(S1 + (16 * n + r) * LDT + 32 * kb + 8 * q4), ak[n]);
           if (kb >= 1 || n < 2) {
-            ak[n] = mfma(a, ld8_tr(S1, LDT, 32 * kb, 16 * n), ak[n]);  // i > j
-            aw[n] = mfma(w, ld8_tr(Ts, LDT, 32 * kb, 16 * n), aw[n]);  // t >= s
+            ak[n] = mfma(a, ld8_tr(S1, LDT, 32 * kb, 16 * n), ak[n]);
+            aw[n] = mfma(w, ld8_tr(Ts, LDT, 32 * kb, 16 * n), aw[n]);
           }
         }
       }
@@ -1030,7 +972,6 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
         dgl[16 * n + r] += xg;
       }
     }
-    // this wave's part of the row dots k_t . dK_t (its 32 columns of each row)
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       const int t = 16 * n + r;
@@ -1042,16 +983,16 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
       }
       pd += __shfl_xor(pd, 16, 64);
       pd += __shfl_xor(pd, 32, 64);
-      if (q4 == 0) dkdot[wave][t] = pd;
+      if (q4 == 0) dkdot[wave * 64 + t] = pd;
     }
   }
   __syncthreads();
 
-  // ---- phase 5: l2norm backward of dk (dk = rk (dK - k (k . dK))); dg (reverse cumsum), dbeta ----
+  // ---- wy phase 5: l2norm backward of dk; dg (reverse cumsum of the chunk's dG); dbeta ----
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
     const int t = 16 * n + r;
-    const float dot = dkdot[0][t] + dkdot[1][t] + dkdot[2][t] + dkdot[3][t];
+    const float dot = dkdot[t] + dkdot[64 + t] + dkdot[128 + t] + dkdot[192 + t];
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const int m = 2 * wave + mm;
@@ -1064,7 +1005,6 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
     const int t = tid;
     const bool in = t < ci.len;
     float x = keep_if(in, dgp_t + dgw[0][t] + dgw[1][t] + dgw[2][t] + dgw[3][t]);
-    // reverse (suffix) cumsum within the chunk
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const float o = __shfl_down(x, off, 64);
@@ -1072,7 +1012,7 @@ __global__ __launch_bounds__(256) void bwd_wy_kernel(
     }
     if (in) {
       dg[(size_t)(ci.start + t) * H + h] = x;
-      dbeta[(size_t)(ci.start + t) * H + h] = dbw[0][t] + dbw[1][t] + dbw[2][t] + dbw[3][t];
+      dbeta[(size_t)(ci.start + t) * H + h] = dbw[t] + dbw[64 + t] + dbw[128 + t] + dbw[192 + t];
     }
   }
 }
@@ -1082,7 +1022,6 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
   auto F = [&](int i) { return reinterpret_cast<const bf16*>(a.fws + a.foff[i]); };
   auto Ff = [&](int i) { return reinterpret_cast<const float*>(a.fws + a.foff[i]); };
   auto B = [&](int i) { return reinterpret_cast<bf16*>(a.bws + a.boff[i]); };
-  auto Bf = [&](int i) { return reinterpret_cast<float*>(a.bws + a.boff[i]); };
   const dim3 grid_p(a.H, a.n_chunks);  // chunk-major dispatch (the kernels pick the chunk order)
   {
     TimedLaunch tl(K_BWD_LOCAL, stream);
@@ -1094,16 +1033,10 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(bwd_scan_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, B(B_KNP),
                        Ff(F_GC), B(B_DVLT), B(B_XT), B(B_WT), a.chunks, a.doc_chunk, a.H, B(B_DH), B(B_DVN));
   }
-  {
-    TimedLaunch tl(K_BWD_DQK, stream);
-    hipLaunchKernelGGL(bwd_dqk_kernel, grid_p, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_GC),
-                       F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.chunks, a.H, a.scale, (int)a.normalize, a.dq,
-                       Bf(B_DKP), B(B_DW), Bf(B_DGP));
-  }
-  TimedLaunch tl(K_BWD_WY, stream);
-  hipLaunchKernelGGL(bwd_wy_kernel, grid_p, dim3(256), 0, stream, F(F_KN), a.v, a.beta, Ff(F_GC), Ff(F_RK),
-                     F(F_TM), B(B_DW), B(B_DVN), Bf(B_DKP), Bf(B_DGP), a.chunks, a.H,
-                     (int)a.normalize, a.dk, a.dv, a.dg, a.dbeta);
+  TimedLaunch tl(K_BWD_DKW, stream);
+  hipLaunchKernelGGL(bwd_dkw_kernel, grid_p, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_RK), Ff(F_GC),
+                     F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.v, a.beta, F(F_TM), a.chunks, a.H, a.scale,
+                     (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta);
 }
 
 }  // namespace cqgdn

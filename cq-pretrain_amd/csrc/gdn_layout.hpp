@@ -39,9 +39,6 @@ enum BwdBuf {
   B_XT,        // bf16 [NC][H][D][D]   X = scale*(gam*Qn)^T dO, (v, k)
   B_DH,        // bf16 [NC][H][8][D][16]  gradient of the state leaving the chunk, value-slice-major (s, k, v%16)
   B_DVN,       // bf16 [NC][H][8][64][16] d v_new, value-slice-major (s, t, v%16)
-  B_DKP,       // f32  [T][H][D]       partial dKn (output and state terms)
-  B_DW,        // bf16 [T][H][D]       dW rows (t, k)
-  B_DGP,       // f32  [T][H]          partial dG (before the reverse cumsum)
   B_KNP,       // bf16 [T][H][D]       Kn in perm32 column order (reverse scan operand), written by bwd_local
   B_WT,        // bf16 [NC][H][D][64]  -W transposed (k, t), perm32 column order (reverse scan operand), by bwd_local
   B_COUNT
@@ -74,9 +71,6 @@ inline void bwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[B_XT] = chunk * 128 * 128 * 2;
   s[B_DH] = chunk * 128 * 128 * 2;
   s[B_DVN] = chunk * 64 * 128 * 2;
-  s[B_DKP] = ev * 128 * 4;
-  s[B_DW] = ev * 128 * 2;
-  s[B_DGP] = ev * 4;
   s[B_KNP] = ev * 128 * 2;
   s[B_WT] = chunk * 128 * 64 * 2;
 }

@@ -14,8 +14,7 @@ enum KernelId {
   K_FWD_OUT,
   K_BWD_LOCAL,
   K_BWD_SCAN,
-  K_BWD_DQK,
-  K_BWD_WY,
+  K_BWD_DKW,
   K_RECURRENT,
   K_COUNT
 };

@@ -12,7 +12,7 @@
 namespace cqgdn {
 
 const char* const kKernelNames[K_COUNT] = {"fwd_prep",  "fwd_scan", "fwd_out", "bwd_local",
-                                           "bwd_scan",  "bwd_dqk",  "bwd_wy",  "recurrent"};
+                                           "bwd_scan",  "bwd_dkw",  "recurrent"};
 
 namespace {
 

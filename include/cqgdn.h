@@ -68,7 +68,7 @@ int64_t cqgdn_chunk_table(const int64_t* bounds, int n_bounds, int32_t* table, i
  * unmodified, to cqgdn_bwd.
  */
 #define CQGDN_FWD_BUFFERS 12
-#define CQGDN_BWD_BUFFERS 9
+#define CQGDN_BWD_BUFFERS 6
 size_t cqgdn_fwd_workspace_size(int64_t T, int H, int64_t n_chunks);
 int cqgdn_fwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets, int count);
 size_t cqgdn_bwd_workspace_size(int64_t T, int H, int64_t n_chunks);
@@ -276,7 +276,7 @@ int cqgdn_chunk_local_cumsum(const float* g, float* out, int64_t T, int H, const
  * price one kernel against its roofline).  cqgdn_timer_arm(name, n) makes the
  * library bracket each of the next n launches of the named kernel with
  * hipEventRecord on the stream it is launched on; name = NULL disarms.  Names:
- * fwd_prep, fwd_scan, fwd_out, bwd_local, bwd_scan, bwd_dqk, bwd_wy,
+ * fwd_prep, fwd_scan, fwd_out, bwd_local, bwd_scan, bwd_dkw,
  * recurrent.  cqgdn_timer_read waits for the recorded
  * events, writes up to `capacity` per-launch durations in milliseconds,
  * stores the number of launches recorded, and disarms.  One kernel is armed

@@ -111,7 +111,7 @@ def test_recurrent_and_helpers_reject_invalid_arguments(lib):
 
 def test_timer_arguments(lib):
     assert lib.cqgdn_timer_arm(b"no_such_kernel", 4) == _lib.EINVAL
-    assert lib.cqgdn_timer_arm(b"bwd_dqk", 0) == _lib.EINVAL
+    assert lib.cqgdn_timer_arm(b"bwd_dkw", 0) == _lib.EINVAL
     assert lib.cqgdn_timer_arm(None, 0) == _lib.OK
     n = ctypes.c_int(-1)
     assert lib.cqgdn_timer_read(None, 0, ctypes.byref(n)) == _lib.OK and n.value == 0

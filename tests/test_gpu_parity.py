@@ -138,7 +138,7 @@ def test_backward_intermediates(gdn):
         if binter["dh"][c].abs().max() > 0:
             assert rel_l2(dh[c], binter["dh"][c]) < TOL_INTER, c
         assert rel_l2(dVn[c, :, :n], binter["dVn"][c]) < 2 * TOL_INTER, c
-        assert not dVn[c, :, n:].any(), c  # rows past the tail are zero (bwd_wy reads them unmasked)
+        assert not dVn[c, :, n:].any(), c  # rows past the tail are zero (bwd_dkw reads them unmasked)
 
 
 def test_cq_config1_shape_fwd_bwd(gdn):
