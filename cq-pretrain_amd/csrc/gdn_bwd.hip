@@ -463,6 +463,9 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
 //   R4b v_new^T           -> dW rows [t][k]   -> Y^T staging (wy)
 // The l2norm backward of dq runs on the phase-2 registers (per-wave row dots in
 // LDS), so no fp32 staging tile is needed and dQ's registers carry the dK partial.
+// Barriers order LDS only (s_waitcnt lgkmcnt(0); s_barrier): global stores stay
+// in flight across them, and the one barrier that needs the dVn tile's copies
+// waits for vector memory explicitly.
 constexpr int DKW_R1 = 0, DKW_R2 = 64 * LDK * 2, DKW_R3 = DKW_R2 + 64 * LDK * 2, DKW_R4A = DKW_R3 + 64 * LDT * 2,
               DKW_R4B = DKW_R4A + 64 * LDK * 2, DKW_BYTES = DKW_R4B + 128 * LDT * 2;
 
@@ -529,7 +532,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       st8(dOs + t * LDK + col, keep_if(in, ld8(dout + row + col)));
     }
   }
-  __syncthreads();
+  lds_barrier();
   const float glast = Gs[ci.len - 1];
   float* dgl = dgw[wave];
 
@@ -570,7 +573,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       if (r == 0) dgl[16 * wave + 4 * q4 + i] += x;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm)
@@ -635,19 +638,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       for (int mm = 0; mm < 2; ++mm) x += (float)Qs[t * LDK + 16 * (2 * wave + mm) + r] * dQ[mm][n][i];
       pdot[n][i] = sum16(x);
     }
-  __syncthreads();  // every read of the dO rows is done: the dVn tile and the row dots may replace them
-  {
-    const bf16* dvs = dVn + cb * (CH * D);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
-  }
+  lds_barrier();  // every read of the dO rows is done: the row dots and then the dVn tile may replace them
   if (r == 0) {
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
       for (int i = 0; i < 4; ++i) dqdot[wave * 64 + 16 * n + 4 * q4 + i] = pdot[n][i];  // after the tile's 16 KB
   }
-  __syncthreads();
+  lds_barrier();
   // dq = rq (dQ - q (q . dQ)), stored from the C layout (16 lanes: 32 contiguous bytes of a row)
 #pragma unroll
   for (int n = 0; n < 4; ++n)
@@ -663,6 +661,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         if (t < ci.len) dq[((size_t)(ci.start + t) * H + h) * D + k] = (bf16)x;
       }
     }
+  // the dVn tile, copied global -> LDS while phase 3 runs (after the dq stores, which retire first)
+  {
+    const bf16* dvs = dVn + cb * (CH * D);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
+  }
 
   // ---- phase 3: dK^T partial (k rows, t columns), kept in registers for the wy part ----
   f32x4 fkp[2][4];
@@ -717,7 +721,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     for (int off = 1; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
     if (lane == 0) dgl[ci.len - 1] += esum + __expf(glast) * x;
   }
-  __syncthreads();  // the dVn copies have landed; every read of Q, dPm and v_new^T is done
+  wait_vmem_all();  // the dVn tile has landed (the dq stores issued before it have retired too)
+  lds_barrier();    // every read of Q, dPm and v_new^T is done
 
   // the wy part's V rows, T rows and beta, requested now and stored over Q and dPm after phase 4
   bf16x8 pv[4], pt[2];
@@ -763,7 +768,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) fvt[mm][kb] = ld8_tr(dVs + (2 * wave + mm) * (CH * 16), 16, 32 * kb, 0);
   }
-  __syncthreads();  // dW rows complete, dG partials complete, the dVn tile consumed
+  lds_barrier();  // dW rows complete, dG partials complete, the dVn tile consumed
 
   // ---- the WY part, on the chip-resident operands ----
   const float dgp_t = (tid < 64) ? dgw[0][tid] + dgw[1][tid] + dgw[2][tid] + dgw[3][tid] : 0.f;
@@ -782,10 +787,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int j = 0; j < 2; ++j) st8(Ts + t * LDT + 32 * j + 8 * p, pt[j]);
   }
-  __syncthreads();  // dgp_t has been read everywhere it is needed
+  lds_barrier();  // dgp_t has been read everywhere it is needed
   dgw[wave][lane] = 0.f;
   dbw[wave * 64 + lane] = 0.f;
-  __syncthreads();
+  lds_barrier();
   float* dbl = dbw + wave * 64;
 
   // ---- wy phase 1: dT = dW (beta gam K)^T + dVn (beta V)^T -> S1 = dT[t][s]; dW fragments ----
@@ -819,7 +824,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   float rsn[4];
 #pragma unroll
   for (int n = 0; n < 4; ++n) rsn[n] = normalize ? rk[(size_t)(ci.start + clamp_row(16 * n + r, ci.len)) * H + h] : 1.f;
-  __syncthreads();  // S1 complete; every wave holds its dW fragments (S2 may overwrite the rows)
+  lds_barrier();  // S1 complete; every wave holds its dW fragments (S2 may overwrite the rows)
 
   // ---- wy phase 2: Y = dT T^T -> S2 = Y^T[j][t] ----
   {
@@ -837,7 +842,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       st4(S2 + (16 * n + r) * LDT + 16 * wave + 4 * q4, acc);
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- wy phase 3: dA = -T^T Y, dM, dbeta and dG from A ----
   {
@@ -891,7 +896,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- wy phase 4b: dv = beta (T^T dVn) ----
   {
@@ -986,7 +991,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       if (q4 == 0) dkdot[wave * 64 + t] = pd;
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- wy phase 5: l2norm backward of dk; dg (reverse cumsum of the chunk's dG); dbeta ----
 #pragma unroll

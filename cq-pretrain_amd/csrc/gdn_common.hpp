@@ -281,12 +281,21 @@ __device__ __forceinline__ void dma16(const void* src, void* lds) {
 }
 
 // ---- wave reductions -------------------------------------------------------
-// sum over the 16 lanes that share q4 (the 16 columns of a C tile)
+// x of another lane of the same 16-lane row, by a DPP control (VALU only, no LDS)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+// sum over the 16 lanes that share q4 (the 16 columns of a C tile), as a pairwise
+// tree of DPP moves: lane ^ 1 and lane ^ 2 (quad_perm), then lane ^ 15 (row_mirror)
+// and lane ^ 7 (row_half_mirror).  Every level adds a + b on one lane and b + a on
+// its partner, so all 16 lanes hold the same bits.
 __device__ __forceinline__ float sum16(float x) {
-  x += __shfl_xor(x, 1, 64);
-  x += __shfl_xor(x, 2, 64);
-  x += __shfl_xor(x, 4, 64);
-  x += __shfl_xor(x, 8, 64);
+  x += dpp_f<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+  x += dpp_f<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+  x += dpp_f<0x140>(x);  // row_mirror
+  x += dpp_f<0x141>(x);  // row_half_mirror
   return x;
 }
 
