@@ -717,8 +717,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
         for (int s8 = 0; s8 < 8; ++s8) x += a[s8] * b[s8];
       }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) x += __shfl_xor(x, off, 64);
+    x = sum16(x);
+    x += __shfl_xor(x, 16, 64);
+    x += __shfl_xor(x, 32, 64);
     if (lane == 0) dgl[ci.len - 1] += esum + __expf(glast) * x;
   }
   wait_vmem_all();  // the dVn tile has landed (the dq stores issued before it have retired too)

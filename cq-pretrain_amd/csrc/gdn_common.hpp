@@ -299,6 +299,13 @@ __device__ __forceinline__ float sum16(float x) {
   return x;
 }
 
+// sum over the 4 lanes of a quad (lanes 4a .. 4a + 3), the first two levels of sum16
+__device__ __forceinline__ float sum4(float x) {
+  x += dpp_f<0xB1>(x);
+  x += dpp_f<0x4E>(x);
+  return x;
+}
+
 // Rows past a tail chunk's length re-read the chunk's last row (always in bounds)
 // and are zeroed after the load.  A load issued under a condition is waited for
 // on its own (the compiler branches around it); unconditional loads of a phase

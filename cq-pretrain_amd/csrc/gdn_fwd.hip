@@ -124,8 +124,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int s = 0; s < 8; ++s) ss += x[j][s] * x[j][s];
-        ss += __shfl_xor(ss, 1, 64);
-        ss += __shfl_xor(ss, 2, 64);
+        ss = sum4(ss);
         rs = rsqrtf(ss + 1e-6f);
       }
       if (in) {
@@ -146,8 +145,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int s = 0; s < 8; ++s) ss += x[j][s] * x[j][s];
-        ss += __shfl_xor(ss, 1, 64);
-        ss += __shfl_xor(ss, 2, 64);
+        ss = sum4(ss);
         rs = rsqrtf(ss + 1e-6f);
       }
 #pragma unroll
@@ -209,8 +207,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
       float part = 0.f;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) part += Af[(b0 + i) * LDA + b0 + 4 * jj + p] * tc[jj];
-      part += __shfl_xor(part, 1, 64);
-      part += __shfl_xor(part, 2, 64);
+      part = sum4(part);
       const float val = (i > lc) ? -part : ((i == lc) ? 1.f : 0.f);
       if ((i & 3) == p) tc[i >> 2] = val;
     }

@@ -48,12 +48,12 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const bf16* __restrict__
     for (int jj = 0; jj < 8; ++jj) {
       s[jj] *= ge;
       float dot = s[jj][0] * kk[0] + s[jj][1] * kk[1] + s[jj][2] * kk[2] + s[jj][3] * kk[3];
-#pragma unroll
-      for (int off = 1; off < 32; off <<= 1) dot += __shfl_xor(dot, off, 64);
+      dot = sum16(dot);
+      dot += __shfl_xor(dot, 16, 64);
       s[jj] += kk * ((vv[jj] - dot) * be);
       float od = s[jj][0] * qq[0] + s[jj][1] * qq[1] + s[jj][2] * qq[2] + s[jj][3] * qq[3];
-#pragma unroll
-      for (int off = 1; off < 32; off <<= 1) od += __shfl_xor(od, off, 64);
+      od = sum16(od);
+      od += __shfl_xor(od, 16, 64);
       o[jj] = od;
     }
     if (c4 == 0) {
@@ -93,10 +93,7 @@ __global__ __launch_bounds__(256) void l2norm_fwd_kernel(const bf16* __restrict_
   float ss = 0.f;
 #pragma unroll
   for (int s = 0; s < 8; ++s) ss += a[s] * a[s];
-  ss += __shfl_xor(ss, 1, 16);
-  ss += __shfl_xor(ss, 2, 16);
-  ss += __shfl_xor(ss, 4, 16);
-  ss += __shfl_xor(ss, 8, 16);
+  ss = sum16(ss);
   const float rs = rsqrtf(ss + 1e-6f);
   st8(y + row * D + 8 * c, cvt8(a * rs));
   if (c == 0 && rstd) rstd[row] = rs;
@@ -113,10 +110,7 @@ __global__ __launch_bounds__(256) void l2norm_bwd_kernel(const bf16* __restrict_
   float dot = 0.f;
 #pragma unroll
   for (int s = 0; s < 8; ++s) dot += a[s] * b[s];
-  dot += __shfl_xor(dot, 1, 16);
-  dot += __shfl_xor(dot, 2, 16);
-  dot += __shfl_xor(dot, 4, 16);
-  dot += __shfl_xor(dot, 8, 16);
+  dot = sum16(dot);
   st8(dx + row * D + 8 * c, cvt8((b - a * dot) * rstd[row]));
 }
 
