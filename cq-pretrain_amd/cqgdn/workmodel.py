@@ -75,9 +75,9 @@ def bytes_per_chunk(kernel, c, d=D):
         "fwd_scan": e + 2 * tile + s + sq + tile,
         # qn, kn, gcum, h^T, v_new^T -> o
         "fwd_out": 2 * e + s + sq + tile + e,
-        # qn, kn, dO, gcum, beta, T -> dv_local^T, X^T, Kn perm32, -W^T
+        # qn, kn, dO, gcum, beta, T -> dv_local^T, X^T, kdec Kn perm32, -W^T
         "bwd_local": 3 * e + 2 * s + tm + tile + sq + e + tile,
-        # Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh, dv_new (both value-slice-major)
+        # kdec Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh, dv_new (both value-slice-major)
         "bwd_scan": e + s + tile + sq + tile + sq + tile,
         # qn, kn, rq, rk, gcum, h^T, v_new^T, dO, dh, dv_new, v, beta, T -> dq, dk, dv, dg, dbeta
         "bwd_dkw": 2 * e + 3 * s + sq + tile + e + sq + tile + e + s + tm + 3 * e + 2 * s,

@@ -90,15 +90,18 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
   }
   __syncthreads();
 
-  // perm32 copy of Kn from the tile: 16-byte piece p of column block j holds
-  // logical 32 j + 4 p .. + 3 and 32 j + 16 + 4 p .. + 3
+  // perm32 copy of kdec_t Kn_t (kdec_t = exp(G_last - G_t), the decay the
+  // reverse scan applies to Kn dS) from the tile: 16-byte piece p of column
+  // block j holds logical 32 j + 4 p .. + 3 and 32 j + 16 + 4 p .. + 3
   {
     const int t = tid >> 2, p = tid & 3;
     if (t < ci.len) {
+      const float kd = __expf(Gs[ci.len - 1] - Gs[t]);
       bf16* kp = knP + ((size_t)(ci.start + t) * H + h) * D + 8 * p;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        st8(kp + 32 * j, cat(ld4(Ks + t * LDK + 32 * j + 4 * p), ld4(Ks + t * LDK + 32 * j + 16 + 4 * p)));
+        st8(kp + 32 * j, cat(cvt4(cvtf4(ld4(Ks + t * LDK + 32 * j + 4 * p)) * kd),
+                             cvt4(cvtf4(ld4(Ks + t * LDK + 32 * j + 16 + 4 * p)) * kd)));
     }
   }
 
@@ -233,7 +236,8 @@ struct __attribute__((aligned(16))) BwdStage {
   bf16 wt[128 * 64];   // -W^T rows k
   bf16 dvl[16 * 64];   // dv_local^T rows of the slice
   bf16 xt[16 * 128];   // X^T rows of the slice
-  float g[64];         // G of every event (events past the tail repeat the last one)
+  float glast;         // G of the chunk's last event
+  float pad[3];
 };
 
 struct __attribute__((aligned(16))) BwdScratch {
@@ -244,8 +248,8 @@ static_assert(sizeof(BwdScratch) <= 128 * 64 * sizeof(bf16), "scratch must fit t
 __device__ __forceinline__ BwdScratch& bwd_scratch(BwdStage& st) { return *reinterpret_cast<BwdScratch*>(st.wt); }
 
 // Issue part `part` of the asynchronous copies of chunk c into stage S (no
-// wait on memory here): part 0 Kn and G (17 copies), part 1 -W^T, the
-// dv_local^T and X^T slices (22 copies).
+// wait on memory here): part 0 kdec Kn and G_last (17 copies), part 1 -W^T,
+// the dv_local^T and X^T slices (22 copies).
 constexpr int BWD_PART_COPIES[2] = {17, 22};
 __device__ __forceinline__ void bwd_issue(BwdStage& S, const int32_t* __restrict__ chunks, int c, int H, int h,
                                           int v0, int lane, int part, const bf16* __restrict__ knP,
@@ -260,8 +264,9 @@ __device__ __forceinline__ void bwd_issue(BwdStage& S, const int32_t* __restrict
       const int tt = min(t, ci.len - 1);
       dma16(knP + ((size_t)(ci.start + tt) * H + h) * D + 8 * col, S.kn + 512 * i);
     }
-    __builtin_amdgcn_global_load_lds(gc + (size_t)(ci.start + min(lane, ci.len - 1)) * H + h, (lds_void_ptr)S.g, 4,
-                                     0, 0);
+    if (lane == 0)  // one lane: a dword copy writes 4 bytes per active lane
+      __builtin_amdgcn_global_load_lds(gc + (size_t)(ci.start + ci.len - 1) * H + h, (lds_void_ptr)&S.glast, 4, 0,
+                                       0);
   } else {
     const bf16* wt = WT + cb * (D * CH);
 #pragma unroll
@@ -346,31 +351,25 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
         const char* wtb = base + offsetof(BwdStage, wt);
         const char* dvb = base + offsetof(BwdStage, dvl);
         const char* xtb = base + offsetof(BwdStage, xt);
-        const float* gs = reinterpret_cast<const float*>(base + offsetof(BwdStage, g));
         bf16x8 fk[4][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
           for (int i4 = 0; i4 < 4; ++i4) fk[i4][j] = *reinterpret_cast<const bf16x8*>(knb + kofs[j] + 4096 * i4);
-        f32x4 local[4], gt[4];
+        // dVn = dv_local + (kdec Kn) dS_{c+1}, accumulated onto dv_local
+        f32x4 dv[4];
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          local[i4] = cvtf4(*reinterpret_cast<const bf16x4*>(dvb + dofs[i4]));
-          gt[i4] = *reinterpret_cast<const f32x4*>(gs + 16 * i4 + 4 * q4);
-        }
-        const float glast = gs[63];
+        for (int i4 = 0; i4 < 4; ++i4) dv[i4] = cvtf4(*reinterpret_cast<const bf16x4*>(dvb + dofs[i4]));
+        const float glast = reinterpret_cast<const BwdStage*>(base)->glast;
         __builtin_amdgcn_sched_barrier(0);
         bf16x4 sh[8];
 #pragma unroll
         for (int m = 0; m < 8; ++m) sh[m] = cvt4(dS[m]);
-        f32x4 acc[4];
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) acc[i4] = zero4();
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const bf16x8 sb = cat(sh[2 * j], sh[2 * j + 1]);
 #pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) acc[i4] = mfma(fk[i4][j], sb, acc[i4]);
+          for (int i4 = 0; i4 < 4; ++i4) dv[i4] = mfma(fk[i4][j], sb, dv[i4]);
         }
         __builtin_amdgcn_sched_barrier(0);
         bf16x8 fw[8][2];
@@ -387,12 +386,6 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
 #pragma unroll
         for (int m = 0; m < 8; ++m) *reinterpret_cast<bf16x4*>(sb + sofs + 32 * m) = sh[m];
         __builtin_amdgcn_sched_barrier(0);
-        // dVn = dv_local + kdec * (Kn dS_{c+1})
-        f32x4 dv[4];
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) dv[i4][i] = acc[i4][i] * __expf(glast - gt[i4][i]) + local[i4][i];
         // dS_c = exp(G_last) dS_{c+1} + X + (-W^T) dVn
         const float gC = __expf(glast);
 #pragma unroll
@@ -503,34 +496,57 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   const bf16* ht = hT + cb * (D * D);
   const bf16* dhc = dh + cb * (D * D);
   bf16x8 bh[2][4], bd[2][4];
-#pragma unroll
-  for (int mm = 0; mm < 2; ++mm)
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) bh[mm][kb] = gather8_col(ht, D, 32 * kb, 16 * (2 * wave + mm));
-
+  // Every prologue load is issued before the first wait: the column gathers'
+  // loads, the gate and norm values (unconditional: rq is allocated either
+  // way), the v_new^T rows and the Q, K, dO rows; the gathers' lane exchange
+  // comes last.
   {
+    Col8 gh[2][4];
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) gh[mm][kb] = col8_load(ht, D, 32 * kb, 16 * (2 * wave + mm));
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
     const int tc = clamp_row(t, ci.len);
     const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
-    if (p == 0) {
-      Gs[t] = gc[(size_t)(ci.start + tc) * H + h];
-      Rs[t] = normalize ? rq[(size_t)(ci.start + tc) * H + h] : 1.f;
-    }
+    const float gv = gc[(size_t)(ci.start + tc) * H + h];
+    const float rv = rq[(size_t)(ci.start + tc) * H + h];
     const bf16* vt = vnT + cb * (D * CH);
+    bf16x8 xv[4], xq[4], xk[4], xo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int seg = 256 * i + tid, v = seg >> 3, part = seg & 7;
-      st8(VnT + v * LDT + 8 * part, ld8(vt + v * CH + 8 * part));
+      xv[i] = ld8(vt + v * CH + 8 * part);
     }
-    dgw[wave][lane] = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      st8(Qs + t * LDK + col, keep_if(in, ld8(qn + row + col)));
-      st8(Ks + t * LDK + col, keep_if(in, ld8(kn + row + col)));
-      st8(dOs + t * LDK + col, keep_if(in, ld8(dout + row + col)));
+      xq[j] = ld8(qn + row + col);
+      xk[j] = ld8(kn + row + col);
+      xo[j] = ld8(dout + row + col);
     }
+    dgw[wave][lane] = 0.f;
+    if (p == 0) {
+      Gs[t] = gv;
+      Rs[t] = normalize ? rv : 1.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int seg = 256 * i + tid, v = seg >> 3, part = seg & 7;
+      st8(VnT + v * LDT + 8 * part, xv[i]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = 32 * j + 8 * p;
+      st8(Qs + t * LDK + col, keep_if(in, xq[j]));
+      st8(Ks + t * LDK + col, keep_if(in, xk[j]));
+      st8(dOs + t * LDK + col, keep_if(in, xo[j]));
+    }
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) bh[mm][kb] = col8_combine(gh[mm][kb]);
   }
   lds_barrier();
   const float glast = Gs[ci.len - 1];
@@ -824,7 +840,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   }
   float rsn[4];
 #pragma unroll
-  for (int n = 0; n < 4; ++n) rsn[n] = normalize ? rk[(size_t)(ci.start + clamp_row(16 * n + r, ci.len)) * H + h] : 1.f;
+  for (int n = 0; n < 4; ++n) {
+    const float x = rk[(size_t)(ci.start + clamp_row(16 * n + r, ci.len)) * H + h];  // allocated either way
+    rsn[n] = normalize ? x : 1.f;
+  }
   lds_barrier();  // S1 complete; every wave holds its dW fragments (S2 may overwrite the rows)
 
   // ---- wy phase 2: Y = dT T^T -> S2 = Y^T[j][t] ----

@@ -214,42 +214,51 @@ __device__ __forceinline__ typename Vec<E>::x8 ld8_tr16(const E* tile, int ld, i
 // lane columns (r - 1, r) of row 2i + 1; the pair swaps the loaded dwords
 // through DPP and each keeps its own column's halves (v_perm).  Every load
 // instruction reads 8 runs of 32 bytes.
-__device__ __forceinline__ bf16x8 gather8_col(const bf16* M, int ld, int row0, int col0) {
+//
+// It comes in two steps, col8_load and col8_combine: the exchange has to wait
+// for the loads, so a caller with more loads to issue puts them between the two
+// steps and pays one memory round trip for all of them.
+struct Col8 {
+  uint32_t x[4];
+};
+__device__ __forceinline__ Col8 col8_load(const bf16* M, int ld, int row0, int col0) {
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4, odd = r & 1;
   const uint32_t* p = reinterpret_cast<const uint32_t*>(M + (size_t)(row0 + 8 * q4 + odd) * ld + col0 + r - odd);
-  // {S0 = partner, S1 = own}: even keeps own low halves, odd keeps own high halves
-  const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
-  uint32_t x[4];
+  Col8 g;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = p[i * ld];  // rows 2i + odd, ld / 2 dwords per row pair
-  u32x4 out;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t y = (uint32_t)__builtin_amdgcn_mov_dpp((int)x[i], 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-    out[i] = __builtin_amdgcn_perm(y, x[i], sel);
-  }
-  return __builtin_bit_cast(bf16x8, out);
+  for (int i = 0; i < 4; ++i) g.x[i] = p[i * ld];  // rows 2i + odd, ld / 2 dwords per row pair
+  return g;
 }
-
-// gather8_col over rows [0, nrows) of M (row stride ld): rows past nrows read
+// col8_load over rows [0, nrows) of M (row stride ld): rows past nrows read
 // row nrows - 1 instead (in bounds, values unspecified: the caller zeroes them
 // or multiplies them by zero).
-__device__ __forceinline__ bf16x8 gather8_col_rows(const bf16* M, int ld, int row0, int col0, int nrows) {
+__device__ __forceinline__ Col8 col8_load_rows(const bf16* M, int ld, int row0, int col0, int nrows) {
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4, odd = r & 1;
-  const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
-  uint32_t x[4];
+  Col8 g;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = min(row0 + 8 * q4 + 2 * i + odd, nrows - 1);
-    x[i] = *reinterpret_cast<const uint32_t*>(M + (size_t)row * ld + col0 + r - odd);
+    g.x[i] = *reinterpret_cast<const uint32_t*>(M + (size_t)row * ld + col0 + r - odd);
   }
+  return g;
+}
+__device__ __forceinline__ bf16x8 col8_combine(const Col8& g) {
+  const int odd = threadIdx.x & 1;
+  // {S0 = partner, S1 = own}: even keeps own low halves, odd keeps own high halves
+  const uint32_t sel = odd ? 0x03020706u : 0x05040100u;
   u32x4 out;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t y = (uint32_t)__builtin_amdgcn_mov_dpp((int)x[i], 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-    out[i] = __builtin_amdgcn_perm(y, x[i], sel);
+    const uint32_t y = (uint32_t)__builtin_amdgcn_mov_dpp((int)g.x[i], 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    out[i] = __builtin_amdgcn_perm(y, g.x[i], sel);
   }
   return __builtin_bit_cast(bf16x8, out);
+}
+__device__ __forceinline__ bf16x8 gather8_col(const bf16* M, int ld, int row0, int col0) {
+  return col8_combine(col8_load(M, ld, row0, col0));
+}
+__device__ __forceinline__ bf16x8 gather8_col_rows(const bf16* M, int ld, int row0, int col0, int nrows) {
+  return col8_combine(col8_load_rows(M, ld, row0, col0, nrows));
 }
 
 // ---- workgroup synchronization for loader/consumer kernels ----------------

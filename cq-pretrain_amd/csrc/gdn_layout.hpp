@@ -39,7 +39,7 @@ enum BwdBuf {
   B_XT,        // bf16 [NC][H][D][D]   X = scale*(gam*Qn)^T dO, (v, k)
   B_DH,        // bf16 [NC][H][8][D][16]  gradient of the state leaving the chunk, value-slice-major (s, k, v%16)
   B_DVN,       // bf16 [NC][H][8][64][16] d v_new, value-slice-major (s, t, v%16)
-  B_KNP,       // bf16 [T][H][D]       Kn in perm32 column order (reverse scan operand), written by bwd_local
+  B_KNP,       // bf16 [T][H][D]       exp(G_last - G_t) Kn_t in perm32 column order (reverse scan operand), by bwd_local
   B_WT,        // bf16 [NC][H][D][64]  -W transposed (k, t), perm32 column order (reverse scan operand), by bwd_local
   B_COUNT
 };
