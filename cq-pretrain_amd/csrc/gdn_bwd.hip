@@ -351,7 +351,11 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
         const char* wtb = base + offsetof(BwdStage, wt);
         const char* dvb = base + offsetof(BwdStage, dvl);
         const char* xtb = base + offsetof(BwdStage, xt);
-        bf16x8 fk[4][4];
+        // every operand read is issued ahead of the MFMAs that use them (the
+        // kdec Kn fragments first); the scheduling barriers keep the compiler
+        // from interleaving them one by one
+        bf16x8 fk[4][4], fw[8][2];
+        f32x4 xv[8];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -361,35 +365,32 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) dv[i4] = cvtf4(*reinterpret_cast<const bf16x4*>(dvb + dofs[i4]));
         const float glast = reinterpret_cast<const BwdStage*>(base)->glast;
-        __builtin_amdgcn_sched_barrier(0);
-        bf16x4 sh[8];
-#pragma unroll
-        for (int m = 0; m < 8; ++m) sh[m] = cvt4(dS[m]);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bf16x8 sb = cat(sh[2 * j], sh[2 * j + 1]);
-#pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) dv[i4] = mfma(fk[i4][j], sb, dv[i4]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        bf16x8 fw[8][2];
-        f32x4 xv[8];
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int m = 0; m < 8; ++m) fw[m][j] = *reinterpret_cast<const bf16x8*>(wtb + wofs[j] + 2048 * m);
 #pragma unroll
         for (int m = 0; m < 8; ++m) xv[m] = cvtf4(*reinterpret_cast<const bf16x4*>(xtb + xofs[m]));
+        __builtin_amdgcn_sched_barrier(0);
+        bf16x4 sh[8];
+#pragma unroll
+        for (int m = 0; m < 8; ++m) sh[m] = cvt4(dS[m]);
+        // beside it, the first two terms of dS_c = exp(G_last) dS_{c+1} + X + (-W^T) dVn
+        const float gC = __expf(glast);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bf16x8 sb = cat(sh[2 * j], sh[2 * j + 1]);
+#pragma unroll
+          for (int i4 = 0; i4 < 4; ++i4) dv[i4] = mfma(fk[i4][j], sb, dv[i4]);
+#pragma unroll
+          for (int m = 2 * j; m < 2 * j + 2; ++m) dS[m] = dS[m] * gC + xv[m];
+        }
+        __builtin_amdgcn_sched_barrier(0);
         // the -W^T fragments have been read (a wave's LDS operations complete in
         // order): the -W^T region now takes this step's outputs
         char* sb = base + offsetof(BwdStage, wt);
 #pragma unroll
         for (int m = 0; m < 8; ++m) *reinterpret_cast<bf16x4*>(sb + sofs + 32 * m) = sh[m];
-        __builtin_amdgcn_sched_barrier(0);
-        // dS_c = exp(G_last) dS_{c+1} + X + (-W^T) dVn
-        const float gC = __expf(glast);
-#pragma unroll
-        for (int m = 0; m < 8; ++m) dS[m] = dS[m] * gC + xv[m];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const bf16x8 nb = pack_perm(dv[2 * j], dv[2 * j + 1]);

@@ -544,7 +544,10 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
         const char* ub = base + offsetof(FwdStage<E>, ut);
         // all operand reads are issued ahead of the MFMAs that use them; the
         // scheduling barriers keep the compiler from interleaving them one by one
-        X8 fw[4][4];
+        // every operand read is issued ahead of the MFMAs that use them (the W
+        // fragments first); the scheduling barriers keep the compiler from
+        // interleaving them one by one
+        X8 fw[4][4], fk[8][2];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -552,32 +555,31 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
         f32x4 vn[4];
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) vn[i4] = cvtf4(*reinterpret_cast<const X4*>(ub + uofs[i4]));
+        const float glast = reinterpret_cast<const FwdStage<E>*>(base)->glast;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int m = 0; m < 8; ++m) fk[m][j] = *reinterpret_cast<const X8*>(kb + kofs[j] + 2048 * m);
         __builtin_amdgcn_sched_barrier(0);
         X4 sh[8];
 #pragma unroll
         for (int m = 0; m < 8; ++m) sh[m] = to4<E>(S[m]);
-        // v_new = U + (-W) S
+        // v_new = U + (-W) S; the state's decay runs beside it
+        const float gC = __expf(glast);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const X8 hb = cat(sh[2 * j], sh[2 * j + 1]);
 #pragma unroll
           for (int i4 = 0; i4 < 4; ++i4) vn[i4] = mfma(fw[i4][j], hb, vn[i4]);
+#pragma unroll
+          for (int m = 2 * j; m < 2 * j + 2; ++m) S[m] *= gC;
         }
         __builtin_amdgcn_sched_barrier(0);
-        X8 fk[8][2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int m = 0; m < 8; ++m) fk[m][j] = *reinterpret_cast<const X8*>(kb + kofs[j] + 2048 * m);
         // the KgT fragments have been read (a wave's LDS operations complete in
         // order): the KgT region now takes this step's outputs
         char* sb = base + offsetof(FwdStage<E>, kg);
 #pragma unroll
         for (int m = 0; m < 8; ++m) *reinterpret_cast<X4*>(sb + sofs + 32 * m) = sh[m];
-        const float gC = __expf(reinterpret_cast<const FwdStage<E>*>(base)->glast);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int m = 0; m < 8; ++m) S[m] *= gC;
         // S <- exp(G_last) S + (K exp(G_last - G))^T v_new
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
