@@ -281,6 +281,62 @@ __device__ __forceinline__ void wait_vmem_le() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
+// vmcnt(parts * P + stores * S) for counts known only at run time (parts and
+// stores in 0..2): the wait of a wave that has issued `parts` copy parts of P
+// operations and `stores` store groups of S since the operations it waits for.
+template <int P, int S>
+__device__ __forceinline__ void wait_vmem_parts(int parts, int stores) {
+  static_assert(2 * P + 2 * S < 64, "vmcnt is 6 bits");
+  switch (parts * 3 + stores) {
+    case 0: wait_vmem_le<0>(); break;
+    case 1: wait_vmem_le<S>(); break;
+    case 2: wait_vmem_le<2 * S>(); break;
+    case 3: wait_vmem_le<P>(); break;
+    case 4: wait_vmem_le<P + S>(); break;
+    case 5: wait_vmem_le<P + 2 * S>(); break;
+    case 6: wait_vmem_le<2 * P>(); break;
+    case 7: wait_vmem_le<2 * P + S>(); break;
+    default: wait_vmem_le<2 * P + 2 * S>(); break;
+  }
+}
+
+// Hand-off counters in LDS between the waves of one workgroup, in place of
+// s_barrier: a producer wave publishes a count once everything it covers is in
+// LDS (its own LDS operations complete in order, and an asynchronous copy has
+// landed once vmcnt says so); a consumer wave polls the count.  Every wait is
+// bounded: after FLAG_SPIN_LIMIT polls it gives up and returns false, so a
+// broken hand-off ends the kernel with wrong results instead of hanging it.
+// The casts name the LDS address space: through a plain volatile pointer the
+// accesses would become flat operations that wait for every vector memory
+// operation in flight (a loader's own copies included).
+constexpr int FLAG_SPIN_LIMIT = 1 << 20;
+typedef __attribute__((address_space(3))) volatile int lds_vint;
+typedef __attribute__((address_space(3))) volatile long long lds_vi64;
+__device__ __forceinline__ int lds_flag_read(const int* f) {
+  return __builtin_amdgcn_readfirstlane(*(lds_vint*)(f));
+}
+__device__ __forceinline__ void lds_flag_publish(int* f, int v) {
+  asm volatile("" ::: "memory");
+  *(lds_vint*)(f) = v;
+  asm volatile("" ::: "memory");
+}
+// two adjacent counts in one LDS read
+__device__ __forceinline__ int2 lds_flag_read2(const int* f) {
+  const long long v = *(lds_vi64*)(f);
+  return int2{(int)v, (int)(v >> 32)};
+}
+template <bool SLEEP>
+__device__ __forceinline__ bool lds_flag_wait_ge(const int* f, int target) {
+  for (int i = 0; i < FLAG_SPIN_LIMIT; ++i) {
+    if (lds_flag_read(f) >= target) {
+      asm volatile("" ::: "memory");
+      return true;
+    }
+    if (SLEEP) __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 // Asynchronous copy global -> LDS, 16 bytes per lane: lane l's 16 bytes land at

@@ -348,13 +348,19 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
 // step waits.  A workgroup serves one 16-wide value slice of one head with one
 // consumer wave (wave 0) and two loader waves.  Loaders copy each chunk's
 // operands global -> LDS asynchronously (global_load_lds) into a ring of
-// SC_STAGES stages, SC_DEPTH chunks ahead of use.  Each chunk's copies are
-// split between the two loaders (issuing them is what bounds a step: a CU
-// accepts about one 1 KB copy per 20-30 cycles, so one wave issuing all 35
-// takes longer than the consumer's MFMA work), and each loader waits for its
-// own part the step before the chunk is used.  The consumer only reads LDS and
-// writes its output tiles to LDS; loader 1 stores them.  So no wave holds
-// in-flight data in registers and the consumer never waits on memory.
+// SC_STAGES stages.  Each chunk's copies are split between the two loaders
+// (issuing them is what bounds a step: a CU accepts about one 1 KB copy per
+// 20-30 cycles, so one wave issuing all 35 takes longer than the consumer's
+// MFMA work).  The consumer only reads LDS and writes its output tiles to LDS;
+// loader 1 stores them.  So no wave holds in-flight data in registers and the
+// consumer never waits on memory.
+//
+// The waves hand stages to each other through counts in LDS, not s_barrier:
+// a loader publishes a chunk once its part has landed, the consumer publishes
+// a chunk once it is done with it, and each wave waits only for the count it
+// needs.  With a barrier per step, every step lasted as long as the slower of
+// the consumer and the loaders plus the barrier; this way the loaders run up
+// to four chunks ahead and the two sides overlap.
 //
 // LDS tiles are stored with 16-byte columns XOR-swizzled by row (chosen on the
 // source side of each copy), so the consumer's fragment reads, 16 rows at one
@@ -363,7 +369,6 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
 //   KgT [128 rows k][8 cols]  col' = col ^ ((k >> 1) & 7)
 //   U^T [16 rows v][8 cols]   col' = col ^ ((v >> 1) & 7)
 constexpr int SC_THREADS = 64 * 3;
-constexpr int SC_DEPTH = 3;
 constexpr int SC_STAGES = 4;
 constexpr int SC_SROW = 136;  // scratch row stride (elements), S^T [v][k]
 constexpr int SC_VROW = 72;   // scratch row stride (elements), v_new^T [v][t]
@@ -497,6 +502,23 @@ __device__ __forceinline__ void fwd_copy_out(const FwdScratch<E>& sc, int c, int
   }
 }
 
+// The consumer's view of the loaders' counts: both at once (one LDS read).
+__device__ __forceinline__ int2 fwd_read_ready(const int* flags) { return lds_flag_read2(flags); }
+// Wait until both loaders have published chunk target-1; `seen` gets the
+// smaller count read.  Bounded (see lds_flag_wait_ge): false if it gave up.
+__device__ __forceinline__ bool fwd_wait_ready(const int* flags, int target, int& seen) {
+  for (int i = 0; i < FLAG_SPIN_LIMIT; ++i) {
+    const int2 v = fwd_read_ready(flags);
+    const int mn = min(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y));
+    if (mn >= target) {
+      asm volatile("" ::: "memory");
+      seen = mn;
+      return true;
+    }
+  }
+  return false;
+}
+
 template <class E>
 __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
     const E* __restrict__ W, const E* __restrict__ UT, const E* __restrict__ KgT,
@@ -512,6 +534,12 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
   const int v0 = 16 * slice;
 
   __shared__ FwdStage<E> stage[SC_STAGES];
+  // hand-off counts: [0], [1] chunks whose part from loader 0 / 1 has landed
+  // (and, for loader 0, whose tail rows are zeroed); [2] chunks the consumer
+  // has finished (operands read, outputs in the stage's scratch)
+  __shared__ __attribute__((aligned(16))) int flags[4];
+  if (threadIdx.x < 4) flags[threadIdx.x] = 0;
+  __syncthreads();
 
   const int c_begin = doc_chunk[d], n = doc_chunk[d + 1] - c_begin;
   if (wave == 0) {
@@ -536,62 +564,67 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) uofs[i4] = 2 * (r * 64 + 8 * ((2 * i4 + (q4 >> 1)) ^ ((r >> 1) & 7)) + 4 * (q4 & 1));
     const int sofs = 2 * (r * SC_SROW + 4 * q4), vofs = 2 * (r * SC_VROW + 4 * q4);
-    for (int tau = -SC_DEPTH; tau < n; ++tau) {
-      if (tau >= 0) {
-        char* base = reinterpret_cast<char*>(&stage[tau & (SC_STAGES - 1)]);
-        const char* wb = base + offsetof(FwdStage<E>, w);
-        const char* kb = base + offsetof(FwdStage<E>, kg);
-        const char* ub = base + offsetof(FwdStage<E>, ut);
-        // all operand reads are issued ahead of the MFMAs that use them; the
-        // scheduling barriers keep the compiler from interleaving them one by one
-        // every operand read is issued ahead of the MFMAs that use them (the W
-        // fragments first); the scheduling barriers keep the compiler from
-        // interleaving them one by one
-        X8 fw[4][4], fk[8][2];
+    int seen = 0;    // both loaders' counts are at least this (last read)
+    bool ok = true;  // every hand-off wait succeeded
+    for (int tau = 0; tau < n; ++tau) {
+      if (ok && seen <= tau) ok = fwd_wait_ready(flags, tau + 1, seen);
+      if (!ok) {  // a broken hand-off: make every later output NaN
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) fw[i4][j] = *reinterpret_cast<const X8*>(wb + wofs[j] + 4096 * i4);
-        f32x4 vn[4];
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) vn[i4] = cvtf4(*reinterpret_cast<const X4*>(ub + uofs[i4]));
-        const float glast = reinterpret_cast<const FwdStage<E>*>(base)->glast;
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int m = 0; m < 8; ++m) fk[m][j] = *reinterpret_cast<const X8*>(kb + kofs[j] + 2048 * m);
-        __builtin_amdgcn_sched_barrier(0);
-        X4 sh[8];
-#pragma unroll
-        for (int m = 0; m < 8; ++m) sh[m] = to4<E>(S[m]);
-        // v_new = U + (-W) S; the state's decay runs beside it
-        const float gC = __expf(glast);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const X8 hb = cat(sh[2 * j], sh[2 * j + 1]);
-#pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) vn[i4] = mfma(fw[i4][j], hb, vn[i4]);
-#pragma unroll
-          for (int m = 2 * j; m < 2 * j + 2; ++m) S[m] *= gC;
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        // the KgT fragments have been read (a wave's LDS operations complete in
-        // order): the KgT region now takes this step's outputs
-        char* sb = base + offsetof(FwdStage<E>, kg);
-#pragma unroll
-        for (int m = 0; m < 8; ++m) *reinterpret_cast<X4*>(sb + sofs + 32 * m) = sh[m];
-        // S <- exp(G_last) S + (K exp(G_last - G))^T v_new
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const X8 vb = pack_permv<E>(vn[2 * j], vn[2 * j + 1]);
-#pragma unroll
-          for (int m = 0; m < 8; ++m) S[m] = mfma(fk[m][j], vb, S[m]);
-        }
-        char* vbp = sb + sizeof(FwdScratch<E>::s);
-#pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) *reinterpret_cast<X4*>(vbp + vofs + 32 * i4) = to4<E>(vn[i4]);
+        for (int m = 0; m < 8; ++m) S[m] = f32x4{NAN, NAN, NAN, NAN};
       }
-      lds_barrier();
+      char* base = reinterpret_cast<char*>(&stage[tau & (SC_STAGES - 1)]);
+      const char* wb = base + offsetof(FwdStage<E>, w);
+      const char* kb = base + offsetof(FwdStage<E>, kg);
+      const char* ub = base + offsetof(FwdStage<E>, ut);
+      // every operand read is issued ahead of the MFMAs that use them (the W
+      // fragments first); the scheduling barriers keep the compiler from
+      // interleaving them one by one
+      X8 fw[4][4], fk[8][2];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) fw[i4][j] = *reinterpret_cast<const X8*>(wb + wofs[j] + 4096 * i4);
+      f32x4 vn[4];
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) vn[i4] = cvtf4(*reinterpret_cast<const X4*>(ub + uofs[i4]));
+      const float glast = reinterpret_cast<const FwdStage<E>*>(base)->glast;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int m = 0; m < 8; ++m) fk[m][j] = *reinterpret_cast<const X8*>(kb + kofs[j] + 2048 * m);
+      const int2 pre = fwd_read_ready(flags);  // for the next step, read while this one computes
+      __builtin_amdgcn_sched_barrier(0);
+      X4 sh[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m) sh[m] = to4<E>(S[m]);
+      // v_new = U + (-W) S; the state's decay runs beside it
+      const float gC = __expf(glast);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const X8 hb = cat(sh[2 * j], sh[2 * j + 1]);
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) vn[i4] = mfma(fw[i4][j], hb, vn[i4]);
+#pragma unroll
+        for (int m = 2 * j; m < 2 * j + 2; ++m) S[m] *= gC;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // the KgT fragments have been read (a wave's LDS operations complete in
+      // order): the KgT region now takes this step's outputs
+      char* sb = base + offsetof(FwdStage<E>, kg);
+#pragma unroll
+      for (int m = 0; m < 8; ++m) *reinterpret_cast<X4*>(sb + sofs + 32 * m) = sh[m];
+      // S <- exp(G_last) S + (K exp(G_last - G))^T v_new
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const X8 vb = pack_permv<E>(vn[2 * j], vn[2 * j + 1]);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) S[m] = mfma(fk[m][j], vb, S[m]);
+      }
+      char* vbp = sb + sizeof(FwdScratch<E>::s);
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) *reinterpret_cast<X4*>(vbp + vofs + 32 * i4) = to4<E>(vn[i4]);
+      lds_flag_publish(&flags[2], tau + 1);
+      seen = max(seen, min(__builtin_amdgcn_readfirstlane(pre.x), __builtin_amdgcn_readfirstlane(pre.y)));
     }
     if (final_state) {
       float* sf = final_state + ((size_t)d * H + h) * D * D;
@@ -602,45 +635,36 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
         for (int i = 0; i < 4; ++i) sf[(16 * m + 4 * q4 + i) * D + v0 + r] = S[m][i] * inv;
     }
   } else {
-    // Step tau, both loaders: wait for their part of chunk tau+1, then refill
-    // stage (tau-1)%4 (the consumer's stage of the previous step) with their
-    // part of chunk tau+3.  Loader 0 zeroes the W rows past a tail; loader 1
-    // first stores the outputs of step tau-1 from that stage's KgT region.
-    // Loads and stores retire in issue order (one counter on gfx9), so a loader
-    // waits for its part of chunk tau+1 by letting exactly the operations it
-    // issued after that part stay in flight: its part of chunk tau+2 and, for
-    // loader 1, the stores of the copy-out before it.
+    // Iteration x, each loader: publish chunk x-2 as soon as its part has
+    // landed, then, once the consumer is done with chunk x-4, refill that
+    // chunk's stage (x % 4) with this loader's part of chunk x (loader 1 first
+    // stores chunk x-4's outputs from the stage's KgT region).  Loads and
+    // stores retire in issue order (one counter on gfx9), so a loader waits for
+    // chunk x-2 by letting exactly the operations it issued after that part
+    // stay in flight: its part of chunk x-1 and, for loader 1, the copy-out
+    // before it.
     const int j = wave - 1;
     const FwdCopyOffsets offs = fwd_copy_offsets<E>(j, H, h, lane);
-    for (int tau = -SC_DEPTH; tau < n; ++tau) {
-      const int xn = tau + 1, xo = tau - 1, xi = tau + SC_DEPTH;
-      if (xn >= 0 && xn < n) {
-        const bool later = xn + 1 < n;  // this loader's part of chunk tau+2 is in flight
+    bool ok = true;  // once a wait gives up, the rest run without waiting (the consumer poisons its outputs)
+    for (int x = 0; x < n + SC_STAGES; ++x) {
+      const int y = x - 2;
+      if (y >= 0 && y < n) {
+        const int parts = x - 1 < n;
         if (j == 0) {
-          if (later)
-            wait_vmem_le<FWD_PART_COPIES[0]>();
-          else
-            wait_vmem_all();
-          fwd_fix_tail(stage[xn & (SC_STAGES - 1)], chunks, c_begin + xn, lane);
+          wait_vmem_parts<FWD_PART_COPIES[0], FWD_OUT_STORES>(parts, 0);
+          fwd_fix_tail(stage[y & (SC_STAGES - 1)], chunks, c_begin + y, lane);
         } else {
-          const bool stored = tau >= 2;  // the copy-out of step tau-2 came after the part of chunk tau+1
-          if (later && stored)
-            wait_vmem_le<FWD_PART_COPIES[1] + FWD_OUT_STORES>();
-          else if (later)
-            wait_vmem_le<FWD_PART_COPIES[1]>();
-          else if (stored)
-            wait_vmem_le<FWD_OUT_STORES>();
-          else
-            wait_vmem_all();
+          wait_vmem_parts<FWD_PART_COPIES[1], FWD_OUT_STORES>(parts, x - 5 >= 0 && x - 5 < n);
         }
+        lds_flag_publish(&flags[j], y + 1);
       }
-      if (j == 1 && xo >= 0)
-        fwd_copy_out(fwd_scratch(stage[xo & (SC_STAGES - 1)]), c_begin + xo, H, h, v0, lane, hT, vnT);
-      if (xi < n) fwd_issue(stage[xi & (SC_STAGES - 1)], chunks, c_begin + xi, H, h, v0, lane, j, offs, W, UT, KgT, gc);
-      lds_barrier();
+      if (x >= SC_STAGES) {
+        if (ok) ok = lds_flag_wait_ge<true>(&flags[2], x - SC_STAGES + 1);
+        if (j == 1 && x - SC_STAGES < n)
+          fwd_copy_out(fwd_scratch(stage[x & (SC_STAGES - 1)]), c_begin + x - SC_STAGES, H, h, v0, lane, hT, vnT);
+      }
+      if (x < n) fwd_issue(stage[x & (SC_STAGES - 1)], chunks, c_begin + x, H, h, v0, lane, j, offs, W, UT, KgT, gc);
     }
-    if (n > 0 && j == 1)
-      fwd_copy_out(fwd_scratch(stage[(n - 1) & (SC_STAGES - 1)]), c_begin + n - 1, H, h, v0, lane, hT, vnT);
   }
 }
 
