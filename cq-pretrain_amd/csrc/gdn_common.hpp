@@ -337,6 +337,22 @@ __device__ __forceinline__ bool lds_flag_wait_ge(const int* f, int target) {
   return false;
 }
 
+// A scan consumer's wait for step target-1 from both of its loaders (counts
+// flags[0], flags[1]); `seen` gets the smaller count read.  Bounded (see
+// lds_flag_wait_ge): false if it gave up.
+__device__ __forceinline__ bool scan_wait_ready(const int* flags, int target, int& seen) {
+  for (int i = 0; i < FLAG_SPIN_LIMIT; ++i) {
+    const int2 v = lds_flag_read2(flags);
+    const int mn = min(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y));
+    if (mn >= target) {
+      asm volatile("" ::: "memory");
+      seen = mn;
+      return true;
+    }
+  }
+  return false;
+}
+
 typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 // Asynchronous copy global -> LDS, 16 bytes per lane: lane l's 16 bytes land at

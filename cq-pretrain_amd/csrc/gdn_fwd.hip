@@ -502,23 +502,6 @@ __device__ __forceinline__ void fwd_copy_out(const FwdScratch<E>& sc, int c, int
   }
 }
 
-// The consumer's view of the loaders' counts: both at once (one LDS read).
-__device__ __forceinline__ int2 fwd_read_ready(const int* flags) { return lds_flag_read2(flags); }
-// Wait until both loaders have published chunk target-1; `seen` gets the
-// smaller count read.  Bounded (see lds_flag_wait_ge): false if it gave up.
-__device__ __forceinline__ bool fwd_wait_ready(const int* flags, int target, int& seen) {
-  for (int i = 0; i < FLAG_SPIN_LIMIT; ++i) {
-    const int2 v = fwd_read_ready(flags);
-    const int mn = min(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y));
-    if (mn >= target) {
-      asm volatile("" ::: "memory");
-      seen = mn;
-      return true;
-    }
-  }
-  return false;
-}
-
 template <class E>
 __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
     const E* __restrict__ W, const E* __restrict__ UT, const E* __restrict__ KgT,
@@ -567,7 +550,7 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
     int seen = 0;    // both loaders' counts are at least this (last read)
     bool ok = true;  // every hand-off wait succeeded
     for (int tau = 0; tau < n; ++tau) {
-      if (ok && seen <= tau) ok = fwd_wait_ready(flags, tau + 1, seen);
+      if (ok && seen <= tau) ok = scan_wait_ready(flags, tau + 1, seen);
       if (!ok) {  // a broken hand-off: make every later output NaN
 #pragma unroll
         for (int m = 0; m < 8; ++m) S[m] = f32x4{NAN, NAN, NAN, NAN};
@@ -592,7 +575,7 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int m = 0; m < 8; ++m) fk[m][j] = *reinterpret_cast<const X8*>(kb + kofs[j] + 2048 * m);
-      const int2 pre = fwd_read_ready(flags);  // for the next step, read while this one computes
+      const int2 pre = lds_flag_read2(flags);  // for the next step, read while this one computes
       __builtin_amdgcn_sched_barrier(0);
       X4 sh[8];
 #pragma unroll
