@@ -218,8 +218,8 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
 // Reverse scan, organised like fwd_scan_kernel: one consumer wave per (head,
 // 16-wide value slice), two loader waves copying each chunk's operands
 // global -> LDS asynchronously into a 4-stage ring, BS_DEPTH chunks ahead, each
-// loader issuing its own part of every chunk (part 0: Kn and G; part 1: -W^T,
-// dv_local^T, X^T).  The consumer's output tiles (dS^T, dVn^T) go into the
+// loader issuing its own part of every chunk (part 0: kdec Kn, G_last, X^T;
+// part 1: -W^T, dv_local^T).  The consumer's output tiles (dS^T, dVn^T) go into the
 // stage region it has read (-W^T) and are stored by loader 1, which refills
 // that region right after.  Tiles use the same XOR swizzles as the forward
 // scan:
@@ -248,9 +248,10 @@ static_assert(sizeof(BwdScratch) <= 128 * 64 * sizeof(bf16), "scratch must fit t
 __device__ __forceinline__ BwdScratch& bwd_scratch(BwdStage& st) { return *reinterpret_cast<BwdScratch*>(st.wt); }
 
 // Issue part `part` of the asynchronous copies of chunk c into stage S (no
-// wait on memory here): part 0 kdec Kn and G_last (17 copies), part 1 -W^T,
-// the dv_local^T and X^T slices (22 copies).
-constexpr int BWD_PART_COPIES[2] = {17, 22};
+// wait on memory here): part 0 kdec Kn, G_last and the X^T slice (21 copies),
+// part 1 (loader 1, which also stores the outputs) -W^T and the dv_local^T
+// slice (18 copies).
+constexpr int BWD_PART_COPIES[2] = {21, 18};
 __device__ __forceinline__ void bwd_issue(BwdStage& S, const int32_t* __restrict__ chunks, int c, int H, int h,
                                           int v0, int lane, int part, const bf16* __restrict__ knP,
                                           const float* __restrict__ gc, const bf16* __restrict__ dvlT,
@@ -267,6 +268,12 @@ __device__ __forceinline__ void bwd_issue(BwdStage& S, const int32_t* __restrict
     if (lane == 0)  // one lane: a dword copy writes 4 bytes per active lane
       __builtin_amdgcn_global_load_lds(gc + (size_t)(ci.start + ci.len - 1) * H + h, (lds_void_ptr)&S.glast, 4, 0,
                                        0);
+    const bf16* xt = XT + cb * (D * D) + v0 * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int v = 4 * i + (lane >> 4), col = (lane & 15) ^ (v & 15);
+      dma16(xt + v * D + 8 * col, S.xt + 512 * i);
+    }
   } else {
     const bf16* wt = WT + cb * (D * CH);
 #pragma unroll
@@ -279,12 +286,6 @@ __device__ __forceinline__ void bwd_issue(BwdStage& S, const int32_t* __restrict
     for (int i = 0; i < 2; ++i) {
       const int v = 8 * i + (lane >> 3), col = (lane & 7) ^ ((v >> 1) & 7);
       dma16(dvl + v * CH + 8 * col, S.dvl + 512 * i);
-    }
-    const bf16* xt = XT + cb * (D * D) + v0 * D;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int v = 4 * i + (lane >> 4), col = (lane & 15) ^ (v & 15);
-      dma16(xt + v * D + 8 * col, S.xt + 512 * i);
     }
   }
 }

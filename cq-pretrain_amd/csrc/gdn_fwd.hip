@@ -400,19 +400,19 @@ __device__ __forceinline__ FwdScratch<E>& fwd_scratch(FwdStage<E>& st) {
 // every chunk of 64 events): part 0 the 16 W-row copies (from the chunk's first
 // event row), part 1 the 16 KgT copies and the 2 U^T copies (from the chunk's
 // tiles).  With them a full chunk's copy costs one address add.
+template <int PART>
 struct FwdCopyOffsets {
-  uint32_t o[18];
+  uint32_t o[PART == 0 ? 16 : 18];
 };
-template <class E>
-__device__ __forceinline__ FwdCopyOffsets fwd_copy_offsets(int part, int H, int h, int lane) {
-  FwdCopyOffsets f;
-  if (part == 0) {
+template <class E, int PART>
+__device__ __forceinline__ FwdCopyOffsets<PART> fwd_copy_offsets(int H, int h, int lane) {
+  FwdCopyOffsets<PART> f;
+  if constexpr (PART == 0) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int t = 4 * i + (lane >> 4), col = (lane & 15) ^ (t & 15);
       f.o[i] = (uint32_t)(((t * H + h) * D + 8 * col) * sizeof(E));
     }
-    f.o[16] = f.o[17] = 0;
   } else {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -436,14 +436,14 @@ __device__ __forceinline__ FwdCopyOffsets fwd_copy_offsets(int part, int H, int 
 // before it).  A tail chunk re-reads its last W row for the rows past its
 // length (zeroed by fwd_fix_tail).
 constexpr int FWD_PART_COPIES[2] = {17, 18};
-template <class E>
+template <class E, int PART>
 __device__ __forceinline__ void fwd_issue(FwdStage<E>& S, const int32_t* __restrict__ chunks, int c, int H, int h,
-                                          int v0, int lane, int part, const FwdCopyOffsets& f,
+                                          int v0, int lane, const FwdCopyOffsets<PART>& f,
                                           const E* __restrict__ W, const E* __restrict__ UT,
                                           const E* __restrict__ KgT, const float* __restrict__ gc) {
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
-  if (part == 0) {
+  if constexpr (PART == 0) {
     if (ci.len == CH) {
       const char* base = reinterpret_cast<const char*>(W + (size_t)ci.start * H * D);
 #pragma unroll
@@ -499,6 +499,43 @@ __device__ __forceinline__ void fwd_copy_out(const FwdScratch<E>& sc, int c, int
   for (int i = 0; i < 2; ++i) {
     const int seg = 64 * i + lane, v = seg >> 3, ts = seg & 7;
     st8(vnT + cb * (D * CH) + (v0 + v) * CH + 8 * ts, ld8(sc.v + v * SC_VROW + 8 * ts));
+  }
+}
+
+// Loader PART of the forward scan, iteration x: publish chunk x-2 as soon as
+// this loader's part of it has landed, then, once the consumer is done with
+// chunk x-4, refill that chunk's stage (x % 4) with this loader's part of
+// chunk x (loader 1 first stores chunk x-4's outputs from the stage's KgT
+// region).  Loads and stores retire in issue order (one counter on gfx9), so a
+// loader waits for chunk x-2 by letting exactly the operations it issued after
+// that part stay in flight: its part of chunk x-1 and, for loader 1, the
+// copy-out before it.
+template <class E, int PART>
+__device__ __forceinline__ void fwd_loader(FwdStage<E>* stage, int* flags, const int32_t* __restrict__ chunks,
+                                           int c_begin, int n, int H, int h, int v0, int lane,
+                                           const E* __restrict__ W, const E* __restrict__ UT,
+                                           const E* __restrict__ KgT, const float* __restrict__ gc,
+                                           E* __restrict__ hT, E* __restrict__ vnT) {
+  const FwdCopyOffsets<PART> offs = fwd_copy_offsets<E, PART>(H, h, lane);
+  bool ok = true;  // once a wait gives up, the rest run without waiting (the consumer poisons its outputs)
+  for (int x = 0; x < n + SC_STAGES; ++x) {
+    const int y = x - 2;
+    if (y >= 0 && y < n) {
+      const int parts = x - 1 < n;
+      if constexpr (PART == 0) {
+        wait_vmem_parts<FWD_PART_COPIES[0], FWD_OUT_STORES>(parts, 0);
+        fwd_fix_tail(stage[y & (SC_STAGES - 1)], chunks, c_begin + y, lane);
+      } else {
+        wait_vmem_parts<FWD_PART_COPIES[1], FWD_OUT_STORES>(parts, x - 5 >= 0 && x - 5 < n);
+      }
+      lds_flag_publish(&flags[PART], y + 1);
+    }
+    if (x >= SC_STAGES) {
+      if (ok) ok = lds_flag_wait_ge<true>(&flags[2], x - SC_STAGES + 1);
+      if (PART == 1 && x - SC_STAGES < n)
+        fwd_copy_out(fwd_scratch(stage[x & (SC_STAGES - 1)]), c_begin + x - SC_STAGES, H, h, v0, lane, hT, vnT);
+    }
+    if (x < n) fwd_issue<E, PART>(stage[x & (SC_STAGES - 1)], chunks, c_begin + x, H, h, v0, lane, offs, W, UT, KgT, gc);
   }
 }
 
@@ -618,36 +655,13 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
         for (int i = 0; i < 4; ++i) sf[(16 * m + 4 * q4 + i) * D + v0 + r] = S[m][i] * inv;
     }
   } else {
-    // Iteration x, each loader: publish chunk x-2 as soon as its part has
-    // landed, then, once the consumer is done with chunk x-4, refill that
-    // chunk's stage (x % 4) with this loader's part of chunk x (loader 1 first
-    // stores chunk x-4's outputs from the stage's KgT region).  Loads and
-    // stores retire in issue order (one counter on gfx9), so a loader waits for
-    // chunk x-2 by letting exactly the operations it issued after that part
-    // stay in flight: its part of chunk x-1 and, for loader 1, the copy-out
-    // before it.
-    const int j = wave - 1;
-    const FwdCopyOffsets offs = fwd_copy_offsets<E>(j, H, h, lane);
-    bool ok = true;  // once a wait gives up, the rest run without waiting (the consumer poisons its outputs)
-    for (int x = 0; x < n + SC_STAGES; ++x) {
-      const int y = x - 2;
-      if (y >= 0 && y < n) {
-        const int parts = x - 1 < n;
-        if (j == 0) {
-          wait_vmem_parts<FWD_PART_COPIES[0], FWD_OUT_STORES>(parts, 0);
-          fwd_fix_tail(stage[y & (SC_STAGES - 1)], chunks, c_begin + y, lane);
-        } else {
-          wait_vmem_parts<FWD_PART_COPIES[1], FWD_OUT_STORES>(parts, x - 5 >= 0 && x - 5 < n);
-        }
-        lds_flag_publish(&flags[j], y + 1);
-      }
-      if (x >= SC_STAGES) {
-        if (ok) ok = lds_flag_wait_ge<true>(&flags[2], x - SC_STAGES + 1);
-        if (j == 1 && x - SC_STAGES < n)
-          fwd_copy_out(fwd_scratch(stage[x & (SC_STAGES - 1)]), c_begin + x - SC_STAGES, H, h, v0, lane, hT, vnT);
-      }
-      if (x < n) fwd_issue(stage[x & (SC_STAGES - 1)], chunks, c_begin + x, H, h, v0, lane, j, offs, W, UT, KgT, gc);
-    }
+    // The loader's part is a template argument, so its copy offsets stay in
+    // registers (indexed by a run-time part they went to scratch memory, and
+    // reloading them waited for every copy in flight).
+    if (wave == 1)
+      fwd_loader<E, 0>(stage, flags, chunks, c_begin, n, H, h, v0, lane, W, UT, KgT, gc, hT, vnT);
+    else
+      fwd_loader<E, 1>(stage, flags, chunks, c_begin, n, H, h, v0, lane, W, UT, KgT, gc, hT, vnT);
   }
 }
 
