@@ -480,17 +480,25 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
 
-  __shared__ __attribute__((aligned(16))) uint8_t lds[DKW_BYTES];
+  // One array per region: the compiler then sees that the dVn tile's
+  // asynchronous copy writes R4a only, and lets phase 3's reads of the other
+  // regions run while it is in flight (with a single array it waited for the
+  // copy, and every store before it, ahead of phase 3's first LDS read).
+  __shared__ __attribute__((aligned(16))) uint8_t r1[DKW_R2 - DKW_R1];
+  __shared__ __attribute__((aligned(16))) uint8_t r2[DKW_R3 - DKW_R2];
+  __shared__ __attribute__((aligned(16))) uint8_t r3[DKW_R4A - DKW_R3];
+  __shared__ __attribute__((aligned(16))) uint8_t r4a[DKW_R4B - DKW_R4A];
+  __shared__ __attribute__((aligned(16))) uint8_t r4b[DKW_BYTES - DKW_R4B];
   __shared__ float Gs[64];
   __shared__ float dgw[4][64];
   __shared__ float Rs[64];  // rsqrt norms of q (1 without normalize)
-  bf16* Qs = reinterpret_cast<bf16*>(lds + DKW_R1);
-  bf16* Ks = reinterpret_cast<bf16*>(lds + DKW_R2);
-  bf16* dPm = reinterpret_cast<bf16*>(lds + DKW_R3);
-  bf16* dOs = reinterpret_cast<bf16*>(lds + DKW_R4A);
-  bf16* VnT = reinterpret_cast<bf16*>(lds + DKW_R4B);  // v_new^T [v][t], read transposed as v_new rows
+  bf16* Qs = reinterpret_cast<bf16*>(r1);
+  bf16* Ks = reinterpret_cast<bf16*>(r2);
+  bf16* dPm = reinterpret_cast<bf16*>(r3);
+  bf16* dOs = reinterpret_cast<bf16*>(r4a);
+  bf16* VnT = reinterpret_cast<bf16*>(r4b);  // v_new^T [v][t], read transposed as v_new rows
   bf16* dVs = dOs;                                    // dVn tile, from phase 3 on
-  float* dqdot = reinterpret_cast<float*>(lds + DKW_R4A + CH * D * 2);  // [4][64] after the dVn tile
+  float* dqdot = reinterpret_cast<float*>(r4a + CH * D * 2);  // [4][64] after the dVn tile
   bf16* dWs = VnT;                                    // dW rows [t][k], from phase 4 on
 
   // This wave's state fragments: rows k = 16 (2 wave + mm) + r of h
@@ -664,6 +672,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       for (int i = 0; i < 4; ++i) dqdot[wave * 64 + 16 * n + 4 * q4 + i] = pdot[n][i];  // after the tile's 16 KB
   }
   lds_barrier();
+  // The dS fragments (bd) requested after phase 1 have landed long since: wait
+  // for them here, where nothing else is in flight, so that their first use in
+  // phase 3 does not wait for the dq stores and the dVn copy issued below (the
+  // stores are conditional, so the compiler could only wait for everything).
+  wait_vmem_all();
   // dq = rq (dQ - q (q . dQ)), stored from the C layout (16 lanes: 32 contiguous bytes of a row)
 #pragma unroll
   for (int n = 0; n < 4; ++n)
@@ -795,7 +808,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   bf16* Ts = dPm;
   bf16* S1 = dOs;                                                              // dT[t][s], then beta dM [i][j]
   bf16* S2 = VnT;                                                              // Y^T[j][t], over dW rows
-  float* Bs = reinterpret_cast<float*>(lds + DKW_R4A + 64 * LDT * 2);          // after S1
+  float* Bs = reinterpret_cast<float*>(r4a + 64 * LDT * 2);                   // after S1
   float* dbw = Bs + 64;                                                        // [4][64]
   float* dkdot = dbw + 256;                                                    // [4][64]
   {
@@ -920,6 +933,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   }
   lds_barrier();
 
+  // The norms rsn requested in wy phase 1 have landed: wait here, before the
+  // conditional dv stores, so that phase 5 does not wait for those stores.
+  wait_vmem_all();
   // ---- wy phase 4b: dv = beta (T^T dVn) ----
   {
     float colB[4] = {0.f, 0.f, 0.f, 0.f};
