@@ -112,6 +112,11 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     const float gam_t = __expf(Gs[t]);
     const float kdec_t = __expf(glast - Gs[t]);
     const float b_t = Bs[t];
+    // Every load of the prologue (q and k rows, V fragments) was issued at
+    // once: wait for all of them here, before the first (conditional) store.
+    // Past conditional stores the compiler can only wait for everything, and
+    // the k rows' first use would then wait for the q stores as well.
+    wait_vmem_all();
     // q
     {
       f32x8 x[4];
