@@ -21,6 +21,8 @@
 #include "gdn_common.hpp"
 #include "gdn_kernels.hpp"
 
+#include <climits>
+
 namespace cqgdn {
 
 constexpr int CONV_ROWS = 16;     // rows per workgroup
@@ -37,17 +39,24 @@ __device__ __forceinline__ int lower_bound(const int32_t* __restrict__ bounds, i
 }
 
 // Tracks the start of the document holding row u as u increases from u0.
+// The next bound is kept in a register (nb), so a row that crosses no document
+// boundary costs a compare, not a load and its wait.
 struct DocCursor {
   const int32_t* bounds;
-  int n, next, start;
+  int n, next, start, nb;  // nb = bounds[next], or INT_MAX past the last bound
   __device__ DocCursor(const int32_t* b, int n_docs, int u0) : bounds(b), n(n_docs) {
     int i = lower_bound(b, n_docs, u0 + 1) - 1;  // last bound <= u0
     i = max(i, 0);
     start = b[i];
     next = i + 1 <= n_docs ? i + 1 : n_docs;
+    nb = next <= n ? b[next] : INT_MAX;
   }
   __device__ __forceinline__ void advance_to(int u) {
-    while (next <= n && bounds[next] <= u) start = bounds[next++];
+    while (nb <= u) {
+      start = nb;
+      ++next;
+      nb = next <= n ? bounds[next] : INT_MAX;
+    }
   }
 };
 
