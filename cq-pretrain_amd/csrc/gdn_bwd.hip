@@ -452,10 +452,14 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
 // (81,408 bytes: two workgroups per CU):
 //   R1  Q rows            -> V rows (wy)
 //   R2  K rows            (both parts)
-//   R3  dPm               -> T (wy)
+//   R3  dPm^T             -> T (wy)
 //   R4a dO rows           -> dVn tile (value-slice-major) + q.dq row dots
-//                         -> dT / beta dM staging + beta, dbeta and k.dK partials (wy)
+//                         -> dT^T / (beta dM)^T staging + beta, dbeta and k.dK partials (wy)
 //   R4b v_new^T           -> dW rows [t][k]   -> Y^T staging (wy)
+// dPm and the wy staging tiles are stored transposed: an MFMA result fragment
+// holds 4 consecutive rows of one column per lane, which then leave as one
+// 8-byte write instead of four 2-byte writes (readers swap row and transposed
+// reads accordingly).
 // The l2norm backward of dq runs on the phase-2 registers (per-wave row dots in
 // LDS), so no fp32 staging tile is needed and dQ's registers carry the dK partial.
 // Barriers order LDS only (s_waitcnt lgkmcnt(0); s_barrier): global stores stay
@@ -590,8 +594,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         colE += __shfl_xor(colE, 32, 64);
         if (q4 == 0) dgl[s] -= colE;
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dPm[(16 * wave + 4 * q4 + i) * LDT + 16 * n + r] = (bf16)dpm[i];
+      st4(dPm + (16 * n + r) * LDT + 16 * wave + 4 * q4, dpm);  // transposed: dPm^T[s][t], 4 rows t in 8 bytes
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -628,7 +631,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         if (n < 2 * kb) continue;
-        const bf16x8 a = ld8(dPm + (16 * n + r) * LDT + 32 * kb + 8 * q4);
+        const bf16x8 a = ld8_tr(dPm, LDT, 32 * kb, 16 * n);  // dPm rows t = 16 n + r
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm)
           dQ[mm][n] = mfma(a, ld8_tr(Ks, LDK, 32 * kb, 16 * (2 * wave + mm)), dQ[mm][n]);
@@ -715,7 +718,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
           if (n > 2 * kb + 1) continue;
-          a3[n] = mfma(a, ld8_tr(dPm, LDT, 32 * kb, 16 * n), a3[n]);
+          a3[n] = mfma(a, ld8(dPm + (16 * n + r) * LDT + 32 * kb + 8 * q4), a3[n]);  // dPm^T rows s
         }
       }
 #pragma unroll
@@ -806,7 +809,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   const float dgp_t = (tid < 64) ? dgw[0][tid] + dgw[1][tid] + dgw[2][tid] + dgw[3][tid] : 0.f;
   bf16* Vs = Qs;
   bf16* Ts = dPm;
-  bf16* S1 = dOs;                                                              // dT[t][s], then beta dM [i][j]
+  bf16* S1 = dOs;  // transposed: dT^T[s][t], then (beta dM)^T [j][i]
   bf16* S2 = VnT;                                                              // Y^T[j][t], over dW rows
   float* Bs = reinterpret_cast<float*>(r4a + 64 * LDT * 2);                   // after S1
   float* dbw = Bs + 64;                                                        // [4][64]
@@ -849,8 +852,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     for (int n = 0; n < 4; ++n) {
       const int s = 16 * n + r;
       const float fk = Bs[s] * __expf(Gs[s]), fv = Bs[s];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) S1[(16 * wave + 4 * q4 + i) * LDT + s] = (bf16)(ak[n][i] * fk + av[n][i] * fv);
+      st4(S1 + s * LDT + 16 * wave + 4 * q4, ak[n] * fk + av[n] * fv);
     }
   }
   float rsn[4];
@@ -865,7 +867,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   {
     bf16x8 a[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) a[kb] = ld8(S1 + (16 * wave + r) * LDT + 32 * kb + 8 * q4);
+    for (int kb = 0; kb < 2; ++kb) a[kb] = ld8_tr(S1, LDT, 32 * kb, 16 * wave);  // dT rows t = 16 wave + r
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       f32x4 acc = zero4();
@@ -918,8 +920,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         colE += __shfl_xor(colE, 32, 64);
         if (q4 == 0) dgl[j] -= colE;
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) S1[(16 * wave + 4 * q4 + e) * LDT + 16 * n + r] = (bf16)dmp[e];
+      st4(S1 + (16 * n + r) * LDT + 16 * wave + 4 * q4, dmp);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -985,9 +986,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         const bf16x8 w = fwt[mm][kb];
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
-          if (n >= 2 * kb) ak[n] = mfma(a, ld8(S1 + (16 * n + r) * LDT + 32 * kb + 8 * q4), ak[n]);
+          if (n >= 2 * kb) ak[n] = mfma(a, ld8_tr(S1, LDT, 32 * kb, 16 * n), ak[n]);
           if (kb >= 1 || n < 2) {
-            ak[n] = mfma(a, ld8_tr(S1, LDT, 32 * kb, 16 * n), ak[n]);
+            ak[n] = mfma(a, ld8(S1 + (16 * n + r) * LDT + 32 * kb + 8 * q4), ak[n]);
             aw[n] = mfma(w, ld8_tr(Ts, LDT, 32 * kb, 16 * n), aw[n]);
           }
         }
