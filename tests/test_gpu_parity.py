@@ -44,6 +44,9 @@ CASES = [
     (129, (0, 129), 16),
     (129, (0, 37, 129), 16),
     (257, (0, 1, 37, 64, 200, 257), 8),
+    # 4 and 5 chunks: the scans' first stage refill and their last copy-outs meet
+    (256, (0, 256), 4),
+    (300, (0, 300), 4),
 ]
 
 
