@@ -226,14 +226,20 @@ __global__ __launch_bounds__(512) void events_bwd_content_kernel(EvArgs a, EvGra
   }
 }
 
-// queries j = blockIdx.x, + gridDim.x, ... for 512 channels (blockIdx.y): dpre[j] = dq of
+constexpr int EVQ_WAVES = 4;
+// queries j = EVQ_WAVES blockIdx.x + wave, + EVQ_WAVES gridDim.x, ... for 512 channels (blockIdx.y): dpre[j] = dq of
 // the event reading j times silu'(pre); raw gradient of the query's own row (tap K-1; its
 // k/v channels and gates get zeros); query-conv weight partials [blockIdx.x][S][K].  The
 // next query's dq row and tap rows are requested before the current one computes.
 template <int K>
-__global__ __launch_bounds__(64) void events_bwd_query_kernel(EvArgs a, EvGrads d, float* __restrict__ dpre,
-                                                             float* __restrict__ wpart) {
-  const int S = a.H * GN_D, c = (blockIdx.y * 64 + threadIdx.x) * 8;
+__global__ __launch_bounds__(64 * EVQ_WAVES) void events_bwd_query_kernel(EvArgs a, EvGrads d,
+                                                                        float* __restrict__ dpre,
+                                                                        float* __restrict__ wpart) {
+  // EVQ_WAVES waves per workgroup, each walking its own queries (the index
+  // loads of a query are dependent, so queries in flight are what hides them);
+  // the waves' weight partials are summed in LDS in a fixed order.
+  const int S = a.H * GN_D, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = (blockIdx.y * 64 + lane) * 8;
   f32x8 wk[K], dw[K];
   ld_taps<K>(a.w, c, wk);
 #pragma unroll
@@ -248,13 +254,14 @@ __global__ __launch_bounds__(64) void events_bwd_query_kernel(EvArgs a, EvGrads 
       nx[i] = hr < a.n_c ? ld8(a.raw + (int64_t)a.order[hr] * a.raw_stride + c) : bf16x8{};
     }
   };
-  int j = blockIdx.x;
+  const int stride = EVQ_WAVES * (int)gridDim.x;
+  int j = EVQ_WAVES * blockIdx.x + wave;
   if (j < a.n_q) fetch(j);
-  for (; j < a.n_q; j += gridDim.x) {
+  for (; j < a.n_q; j += stride) {
     bf16x8 cq = nq, cx[K];
 #pragma unroll
     for (int i = 0; i < K; ++i) cx[i] = nx[i];
-    if (j + (int)gridDim.x < a.n_q) fetch(j + gridDim.x);
+    if (j + stride < a.n_q) fetch(j + stride);
     f32x8 x[K], pre = f32x8{};
 #pragma unroll
     for (int i = 0; i < K; ++i) {
@@ -277,16 +284,28 @@ __global__ __launch_bounds__(64) void events_bwd_query_kernel(EvArgs a, EvGrads 
     st8(dr + c, cvt8(dp * wk[K - 1]));
     st8(dr + S + c, bf16x8{});
     st8(dr + 2 * S + c, bf16x8{});
-    if (blockIdx.y == 0 && threadIdx.x < a.H) {
-      d.da[row * d.da_stride + threadIdx.x] = (bf16)0.f;
-      d.db[row * d.db_stride + threadIdx.x] = (bf16)0.f;
+    if (blockIdx.y == 0 && lane < a.H) {
+      d.da[row * d.da_stride + lane] = (bf16)0.f;
+      d.db[row * d.db_stride + lane] = (bf16)0.f;
     }
   }
-  float* p = wpart + ((int64_t)blockIdx.x * S + c) * K;
+  __shared__ f32x8 red[EVQ_WAVES - 1][K][64];  // waves 1 ..
+  if (wave > 0) {
 #pragma unroll
-  for (int ch = 0; ch < 8; ++ch)
+    for (int i = 0; i < K; ++i) red[wave - 1][i][lane] = dw[i];
+  }
+  __syncthreads();
+  if (wave == 0) {
 #pragma unroll
-    for (int i = 0; i < K; ++i) p[ch * K + i] = dw[i][ch];
+    for (int w = 0; w < EVQ_WAVES - 1; ++w)
+#pragma unroll
+      for (int i = 0; i < K; ++i) dw[i] += red[w][i][lane];
+    float* p = wpart + ((int64_t)blockIdx.x * S + c) * K;
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch)
+#pragma unroll
+      for (int i = 0; i < K; ++i) p[ch * K + i] = dw[i][ch];
+  }
 }
 
 // after the conv backward wrote the raw gradient of content row cr = hrows[blockIdx.x]:
@@ -340,9 +359,9 @@ void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content
   if (qb > 0) {
     const dim3 qgrid(qb, S / 512);
     switch (a.K) {
-      case 2: hipLaunchKernelGGL(events_bwd_query_kernel<2>, qgrid, dim3(64), 0, stream, a, d, w.dpre, w.qpart); break;
-      case 3: hipLaunchKernelGGL(events_bwd_query_kernel<3>, qgrid, dim3(64), 0, stream, a, d, w.dpre, w.qpart); break;
-      default: hipLaunchKernelGGL(events_bwd_query_kernel<4>, qgrid, dim3(64), 0, stream, a, d, w.dpre, w.qpart); break;
+      case 2: hipLaunchKernelGGL(events_bwd_query_kernel<2>, qgrid, dim3(64 * EVQ_WAVES), 0, stream, a, d, w.dpre, w.qpart); break;
+      case 3: hipLaunchKernelGGL(events_bwd_query_kernel<3>, qgrid, dim3(64 * EVQ_WAVES), 0, stream, a, d, w.dpre, w.qpart); break;
+      default: hipLaunchKernelGGL(events_bwd_query_kernel<4>, qgrid, dim3(64 * EVQ_WAVES), 0, stream, a, d, w.dpre, w.qpart); break;
     }
   }
   if (a.n_c > 0) {
