@@ -254,9 +254,6 @@ __device__ __forceinline__ bf16x8 col8_combine(const Col8& g) {
   }
   return __builtin_bit_cast(bf16x8, out);
 }
-__device__ __forceinline__ bf16x8 gather8_col(const bf16* M, int ld, int row0, int col0) {
-  return col8_combine(col8_load(M, ld, row0, col0));
-}
 __device__ __forceinline__ bf16x8 gather8_col_rows(const bf16* M, int ld, int row0, int col0, int nrows) {
   return col8_combine(col8_load_rows(M, ld, row0, col0, nrows));
 }
