@@ -276,8 +276,7 @@ def layer_decode_step(proj, conv_weight, A_log, dt_bias, norm_weight, cache, *, 
     w = conv_weight.contiguous()
     alog, dtb, nw = A_log.float().contiguous(), dt_bias.float().contiguous(), norm_weight.float().contiguous()
     out = torch.empty(N, 2, S, dtype=p3.dtype, device=p3.device)
-    ws = torch.empty(_lib.lib().cqgdn_layer_decode_workspace_size(N, heads), dtype=torch.uint8, device=p3.device)
     gdn.call("cqgdn_layer_decode_step", N, heads, K, gdn._ptr(p3), P, gdn._ptr(hist), gdn._ptr(w), gdn._ptr(alog),
              gdn._ptr(dtb), gdn._ptr(nw), float(eps), 128 ** -0.5 if scale is None else float(scale),
-             gdn._ptr(state), gdn._ptr(out), gdn._ptr(ws), ws.numel(), gdn._stream(p3.device))
+             gdn._ptr(state), gdn._ptr(out), None, 0, gdn._stream(p3.device))
     return out[0] if single else out

@@ -447,29 +447,10 @@ int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, const void* raw,
   return check_launch("cqgdn_event_inputs_bwd");
 }
 
-namespace {
-struct DecLayout {
-  size_t q, k, v, g, beta, y, rstd, total;
-};
-DecLayout dec_layout(int N, int H) {
-  const size_t rows = (size_t)N * 2, S = (size_t)H * CQGDN_HEAD_DIM;
-  DecLayout l{};
-  size_t o = 0;
-  l.q = o; o += align256(rows * S * sizeof(bf16));
-  l.k = o; o += align256(rows * S * sizeof(bf16));
-  l.v = o; o += align256(rows * S * sizeof(bf16));
-  l.g = o; o += align256(rows * H * sizeof(float));
-  l.beta = o; o += align256(rows * H * sizeof(float));
-  l.y = o; o += align256(rows * S * sizeof(bf16));
-  l.rstd = o; o += align256(rows * H * sizeof(float));
-  l.total = o;
-  return l;
-}
-}  // namespace
-
 size_t cqgdn_layer_decode_workspace_size(int N, int H) {
-  if (N <= 0 || H <= 0) return 0;
-  return dec_layout(N, H).total;
+  (void)N;
+  (void)H;
+  return 0;  // the step needs no workspace
 }
 
 int cqgdn_layer_decode_step(int N, int H, int conv_kernel, const void* proj, int64_t proj_stride, void* conv_history,
@@ -485,21 +466,12 @@ int cqgdn_layer_decode_step(int N, int H, int conv_kernel, const void* proj, int
   if (!proj || !conv_history || !conv_weight || !A_log || !dt_bias || !norm_weight || !state || !out ||
       !aligned(proj, 16) || !aligned(conv_history, 16) || !aligned(out, 16) || !aligned(norm_weight, 16))
     return fail(CQGDN_EINVAL, "null or misaligned buffer (proj, conv_history, out, norm_weight need 16 bytes)");
-  const DecLayout l = dec_layout(N, H);
-  if (!workspace || !aligned(workspace, 256) || workspace_bytes < l.total)
-    return fail(CQGDN_EINVAL, "workspace must be 256-byte aligned and >= cqgdn_layer_decode_workspace_size");
-  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  (void)workspace;  // none needed (see cqgdn_layer_decode_workspace_size)
+  (void)workspace_bytes;
   hipStream_t st = (hipStream_t)stream;
-  bf16 *q = reinterpret_cast<bf16*>(ws + l.q), *k = reinterpret_cast<bf16*>(ws + l.k),
-       *v = reinterpret_cast<bf16*>(ws + l.v), *y = reinterpret_cast<bf16*>(ws + l.y);
-  float *g = reinterpret_cast<float*>(ws + l.g), *beta = reinterpret_cast<float*>(ws + l.beta),
-        *rstd = reinterpret_cast<float*>(ws + l.rstd);
   const DecArgs a{N, H, conv_kernel, static_cast<const bf16*>(proj), proj_stride, static_cast<bf16*>(conv_history),
-                  static_cast<const bf16*>(conv_weight), A_log, dt_bias, q, k, v, g, beta};
-  launch_decode_prep(a, st);
-  launch_recurrent(q, k, v, g, beta, false, state, y, N, 2, H, scale, st);
-  launch_gnorm_fwd(y, nullptr, (int64_t)N * 2, H, static_cast<const bf16*>(proj) + 3 * S, proj_stride, norm_weight,
-                   eps, static_cast<bf16*>(out), rstd, st);
+                  static_cast<const bf16*>(conv_weight), A_log, dt_bias};
+  launch_decode_step(a, state, norm_weight, eps, scale, static_cast<bf16*>(out), st);
   return check_launch("cqgdn_layer_decode_step");
 }
 

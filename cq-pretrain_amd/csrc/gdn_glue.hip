@@ -382,6 +382,7 @@ void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content
   hipLaunchKernelGGL(add_f32_kernel, dim3((S * a.K + 255) / 256), dim3(256), 0, stream, d.dw, w.qsum, S * a.K);
 }
 
+
 // ---------------------------------------------------------------------------
 // One decode step of the layer for N independent sequences (models/decoding.py:16-78):
 // row 0 of a sequence is the sampled content token C, row 1 the text-mask query Q.
@@ -389,18 +390,28 @@ void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content
 //      history shifts by one row and takes raw_C
 //   Q: the query conv of raw_Q's q channels over the updated history, silu
 //   q (both rows) and k (C) l2-normalized; v = C's conv output; g, beta from C's a, b;
-//   event 1 (Q) is read-only: k = v = 0, g = beta = 0.
-// One workgroup per sequence, S / 8 threads, 8 channels per thread in each of q|k|v.
+//   event 1 (Q) is read-only: k = v = 0, g = beta = 0, so its state update is the
+//   identity and only its output is computed
+//   recurrence (as recurrent_kernel): S <- exp(g) S; S <- S + k ((v - S k) beta)^T; o = scale S q
+//   out = gated RMSNorm(o) with z from the row's projection (as gnorm_fwd_kernel)
+// One launch, one workgroup of 8 waves per (sequence, head): head h's q, k, v
+// channels, conv history and gates belong to its workgroup alone; the waves own
+// 16 state rows each (the layout of recurrent_kernel), so the head's whole output
+// is in the workgroup for the norm.  q, k, v and o are rounded to bf16 where the
+// separate kernels stored them, with the same 16- and 32-lane sums.
 template <int K>
-__global__ __launch_bounds__(512) void decode_prep_kernel(DecArgs a) {
-  const int n = blockIdx.x, S = a.H * GN_D, c0 = threadIdx.x * 8;
-  const bf16* rc = a.proj + (int64_t)n * 2 * a.row_stride;
-  const bf16* rq = rc + a.row_stride;
-  bf16* hist = a.hist + (int64_t)n * (K - 1) * 3 * S;
-  f32x8 part[3], query = f32x8{};
-#pragma unroll
-  for (int p = 0; p < 3; ++p) {
-    const int c = p * S + c0;
+__global__ __launch_bounds__(512) void decode_step_kernel(DecArgs a, float* __restrict__ state,
+                                                          const float* __restrict__ norm_w, float eps, float scale,
+                                                          bf16* __restrict__ out) {
+  const int n = blockIdx.x / a.H, h = blockIdx.x % a.H, S = a.H * GN_D;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bf16* rc = a.proj + (int64_t)n * 2 * a.row_stride;  // the sampled token's row
+  const bf16* rq = rc + a.row_stride;                       // the text-mask query's row
+  __shared__ __attribute__((aligned(16))) float qs[2][GN_D], ks[GN_D], vs[GN_D], ys[2][GN_D];
+  __shared__ float gb[2];
+  if (tid < 48) {  // block p (q, k, v) of head h's channels: 16 lanes x 8 channels
+    const int p = tid >> 4, l = tid & 15, c = p * S + h * GN_D + l * 8;
+    bf16* hist = a.hist + (int64_t)n * (K - 1) * 3 * S;
     f32x8 wk[K];
     ld_taps<K>(a.w, c, wk);
     const bf16x8 xc8 = ld8(rc + c);
@@ -414,53 +425,102 @@ __global__ __launch_bounds__(512) void decode_prep_kernel(DecArgs a) {
     }
 #pragma unroll
     for (int ch = 0; ch < 8; ++ch) pre[ch] *= sigm(pre[ch]);
-    part[p] = pre;
-    if (p == 0) {  // the query's conv sees the history after C entered it
-      f32x8 pq = wk[K - 1] * cvtf8(ld8(rq + c));
+    f32x8 query = f32x8{};
+    if (p == 0) {  // the query's conv sees the history after the token entered it
+      query = wk[K - 1] * cvtf8(ld8(rq + c));
 #pragma unroll
-      for (int j = 0; j < K - 1; ++j) pq += wk[j] * (j + 1 < K - 1 ? cvtf8(h8[j + 1]) : xc);
+      for (int j = 0; j < K - 1; ++j) query += wk[j] * (j + 1 < K - 1 ? cvtf8(h8[j + 1]) : xc);
 #pragma unroll
-      for (int ch = 0; ch < 8; ++ch) pq[ch] *= sigm(pq[ch]);
-      query = pq;
+      for (int ch = 0; ch < 8; ++ch) query[ch] *= sigm(query[ch]);
     }
 #pragma unroll
     for (int j = 0; j + 1 < K - 1; ++j) st8(hist + (int64_t)j * 3 * S + c, h8[j + 1]);
     st8(hist + (int64_t)(K - 2) * 3 * S + c, xc8);
-  }
-  float sq = 0.f, sk = 0.f, sqq = 0.f;
+    float sp = 0.f, sqq = 0.f;
 #pragma unroll
-  for (int ch = 0; ch < 8; ++ch) {
-    sq += part[0][ch] * part[0][ch];
-    sk += part[1][ch] * part[1][ch];
-    sqq += query[ch] * query[ch];
-  }
-  const float rq_c = __builtin_amdgcn_rsqf(sum16(sq) + 1e-6f), rk = __builtin_amdgcn_rsqf(sum16(sk) + 1e-6f);
-  const float rq_q = __builtin_amdgcn_rsqf(sum16(sqq) + 1e-6f);
-  const int64_t e0 = (int64_t)n * 2 * S + c0, e1 = e0 + S;
-  st8(a.q + e0, cvt8(part[0] * rq_c));
-  st8(a.q + e1, cvt8(query * rq_q));
-  st8(a.k + e0, cvt8(part[1] * rk));
-  st8(a.k + e1, bf16x8{});
-  st8(a.v + e0, cvt8(part[2]));
-  st8(a.v + e1, bf16x8{});
-  if (threadIdx.x < a.H) {
-    const int h = threadIdx.x;
+    for (int ch = 0; ch < 8; ++ch) {
+      sp += pre[ch] * pre[ch];
+      sqq += query[ch] * query[ch];
+    }
+    const float rp = __builtin_amdgcn_rsqf(sum16(sp) + 1e-6f), rqq = __builtin_amdgcn_rsqf(sum16(sqq) + 1e-6f);
+    const f32x8 qc = cvtf8(cvt8(pre * rp)), qq = cvtf8(cvt8(query * rqq)), vr = cvtf8(cvt8(pre));
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) {
+      if (p == 0) {
+        qs[0][l * 8 + ch] = qc[ch];
+        qs[1][l * 8 + ch] = qq[ch];
+      } else if (p == 1) {
+        ks[l * 8 + ch] = qc[ch];
+      } else {
+        vs[l * 8 + ch] = vr[ch];
+      }
+    }
+  } else if (tid == 64) {
     const float av = (float)rc[4 * S + h] + a.dt_bias[h];
-    const int64_t gi = (int64_t)n * 2 * a.H + h;
-    a.g[gi] = -__expf(a.A_log[h]) * softplus_f(av);
-    a.beta[gi] = sigm((float)rc[4 * S + a.H + h]);
-    a.g[gi + a.H] = 0.f;
-    a.beta[gi + a.H] = 0.f;
+    gb[0] = -__expf(a.A_log[h]) * softplus_f(av);
+    gb[1] = sigm((float)rc[4 * S + a.H + h]);
+  }
+  __syncthreads();
+  {
+    const int c4 = lane & 31, rbase = 16 * wave + (lane >> 5);  // rows rbase + 2 jj
+    float* sblk = state + ((size_t)n * a.H + h) * GN_D * GN_D;
+    f32x4 st[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      st[jj] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(sblk + (rbase + 2 * jj) * GN_D + 4 * c4));
+    const float ge = __expf(gb[0]), be = gb[1];
+    const f32x4 kk = *reinterpret_cast<const f32x4*>(&ks[4 * c4]);
+    const f32x4 qc = *reinterpret_cast<const f32x4*>(&qs[0][4 * c4]);
+    const f32x4 qq = *reinterpret_cast<const f32x4*>(&qs[1][4 * c4]);
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      st[jj] *= ge;
+      float dot = st[jj][0] * kk[0] + st[jj][1] * kk[1] + st[jj][2] * kk[2] + st[jj][3] * kk[3];
+      dot = sum16(dot);
+      dot += __shfl_xor(dot, 16, 64);
+      st[jj] += kk * ((vs[rbase + 2 * jj] - dot) * be);
+      float oc = st[jj][0] * qc[0] + st[jj][1] * qc[1] + st[jj][2] * qc[2] + st[jj][3] * qc[3];
+      oc = sum16(oc);
+      oc += __shfl_xor(oc, 16, 64);
+      float oq = st[jj][0] * qq[0] + st[jj][1] * qq[1] + st[jj][2] * qq[2] + st[jj][3] * qq[3];
+      oq = sum16(oq);
+      oq += __shfl_xor(oq, 16, 64);
+      if (c4 == 0) {
+        ys[0][rbase + 2 * jj] = (float)(bf16)(oc * scale);
+        ys[1][rbase + 2 * jj] = (float)(bf16)(oq * scale);
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      __builtin_nontemporal_store(st[jj], reinterpret_cast<f32x4*>(sblk + (rbase + 2 * jj) * GN_D + 4 * c4));
+  }
+  __syncthreads();
+  if (tid < 32) {  // gated RMSNorm of the token's (e = 0) and the query's (e = 1) output rows
+    const int e = tid >> 4, l = tid & 15;
+    const int64_t r = (int64_t)n * 2 + e;
+    const f32x4 y0 = *reinterpret_cast<const f32x4*>(&ys[e][l * 8]), y1 = *reinterpret_cast<const f32x4*>(&ys[e][l * 8 + 4]);
+    const f32x8 v = f32x8{y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
+    const f32x8 zz = cvtf8(ld8(a.proj + r * a.row_stride + 3 * S + h * GN_D + l * 8));
+    const f32x8 wv = ld_w8(norm_w, l);
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) ss += v[c] * v[c];
+    const float rs = __builtin_amdgcn_rsqf(sum16(ss) * (1.f / GN_D) + eps);
+    f32x8 o;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) o[c] = v[c] * rs * wv[c] * (zz[c] * sigm(zz[c]));
+    st8(out + (r * a.H + h) * GN_D + l * 8, cvt8(o));
   }
 }
 
-void launch_decode_prep(const DecArgs& a, hipStream_t stream) {
+void launch_decode_step(const DecArgs& a, float* state, const float* norm_w, float eps, float scale, bf16* out,
+                        hipStream_t stream) {
   if (a.N == 0) return;
-  const dim3 grid(a.N), block(a.H * 16);
+  const dim3 grid(a.N * a.H), block(512);
   switch (a.K) {
-    case 2: hipLaunchKernelGGL(decode_prep_kernel<2>, grid, block, 0, stream, a); break;
-    case 3: hipLaunchKernelGGL(decode_prep_kernel<3>, grid, block, 0, stream, a); break;
-    default: hipLaunchKernelGGL(decode_prep_kernel<4>, grid, block, 0, stream, a); break;
+    case 2: hipLaunchKernelGGL(decode_step_kernel<2>, grid, block, 0, stream, a, state, norm_w, eps, scale, out); break;
+    case 3: hipLaunchKernelGGL(decode_step_kernel<3>, grid, block, 0, stream, a, state, norm_w, eps, scale, out); break;
+    default: hipLaunchKernelGGL(decode_step_kernel<4>, grid, block, 0, stream, a, state, norm_w, eps, scale, out); break;
   }
 }
 

@@ -121,10 +121,10 @@ struct DecArgs {
   const bf16* w;  // conv weight [3S][K]
   const float* A_log;
   const float* dt_bias;
-  bf16 *q, *k, *v;
-  float *g, *beta;
 };
-void launch_decode_prep(const DecArgs& a, hipStream_t stream);
+// the whole decode step (prep, recurrence, gated norm) in one launch, one workgroup per (sequence, head)
+void launch_decode_step(const DecArgs& a, float* state, const float* norm_w, float eps, float scale, bf16* out,
+                        hipStream_t stream);
 // gated RMSNorm over D = 128 with an optional row gather (gdn_glue.hip)
 int gnorm_bwd_blocks(int64_t rows, int H);  // workgroups of the backward (dw partials per workgroup)
 void launch_gnorm_fwd(const bf16* y, const int32_t* index, int64_t rows, int H, const bf16* z, int64_t z_stride,

@@ -248,10 +248,12 @@ int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, const void* raw,
  * One decode step of the GatedDelta layer for N independent sequences, each
  * advancing by one sampled content token C and one text-mask query Q.  Replaces
  * delta_step (models/decoding.py:16-78) between the layer's projection and
- * out_proj, in three launches: the conv step of C over the conv history (which
- * then shifts in C's raw row) and Q's query conv over the updated history, the
- * l2 norms and gates; the recurrence over the two events (Q read-only); the
- * gated norm with z from the projection rows.
+ * out_proj, in one launch with one workgroup per (sequence, head): the conv step
+ * of C over the conv history (which then shifts in C's raw row) and Q's query
+ * conv over the updated history, the l2 norms and gates; the recurrence over
+ * the two events (Q read-only); the gated norm with z from the projection rows.
+ * It needs no workspace: cqgdn_layer_decode_workspace_size returns 0 and
+ * workspace may be NULL (both stay in the signature so that callers keep working).
  *   proj: bf16 [N][2][proj_stride] (row 0 = C, row 1 = Q; columns q|k|v, z, a, b
  *   of the fused projection); conv_history: bf16 [N][K-1][3S], updated in place;
  *   conv_weight: bf16 [3S][K]; A_log, dt_bias: fp32 [H]; norm_weight: fp32 [128];
