@@ -117,3 +117,20 @@ def test_timer_arguments(lib):
     assert lib.cqgdn_timer_read(None, 0, ctypes.byref(n)) == _lib.OK and n.value == 0
     with pytest.raises(ValueError):
         _lib.KernelTimer("nope", 1)
+
+
+def test_layer_decode_step_arguments(lib):
+    # one launch and no workspace: the size is 0 and a NULL workspace is accepted
+    assert lib.cqgdn_layer_decode_workspace_size(64, 16) == 0
+    p = ctypes.c_void_p(256)
+    w = ctypes.cast(p, ctypes.POINTER(ctypes.c_float))
+
+    def step(N=1, H=16, K=4, stride=4 * 16 * 128 + 32, ptr=p):
+        return lib.cqgdn_layer_decode_step(N, H, K, ptr, stride, p, p, w, w, w, 1e-6, 0.1, w, p, None, 0, None)
+
+    assert step(N=0) == _lib.OK  # nothing to do, nothing launched
+    assert step(H=12) == _lib.EINVAL
+    assert step(K=5) == _lib.EINVAL
+    assert step(stride=4 * 16 * 128) == _lib.EINVAL  # no room for the a, b columns
+    assert b"proj_stride" in lib.cqgdn_last_error()
+    assert step(ptr=ctypes.c_void_p(258)) == _lib.EINVAL  # misaligned projection rows
