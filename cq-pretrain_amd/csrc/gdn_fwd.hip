@@ -220,40 +220,36 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) Af[(b0 + 4 * jj + p) * LDA + col] = tc[jj];
   }
-  {
-    const int a = tid >> 4, bc = tid & 15;  // element (a, bc) of a 16 x 16 block
+  // The levels below the diagonal, d = 1, 2, 3, on fp32 MFMA (16x16x4): wave w <
+  // 4 - d owns the target block (ib, jb) = (w + d, w).  X = sum_{k=jb}^{ib-1}
+  // A_{ib,k} T_{k,jb} reads only lower levels (T_{jb,jb} in its diagonal block,
+  // T_{k,jb}, k > jb, transposed in block (jb, k)); X goes to the wave's own
+  // block (jb, ib), transposed, and comes back as the operand of T_{ib,jb} =
+  // -T_{ib,ib} X, which replaces it.  The block is the wave's alone (its LDS
+  // operations complete in order), so the levels need one barrier each.
 #pragma unroll
-    for (int d = 1; d < 4; ++d) {
-      __syncthreads();
-      float xv[3];
+  for (int d = 1; d < 4; ++d) {
+    __syncthreads();  // the diagonal blocks and the lower levels are complete
+    if (wave < 4 - d) {
+      const int jb = wave, ib = wave + d;
+      const float* arow = Af + (16 * ib + r) * LDA + q4;  // A_{ib, .} row r at this lane's k (4 kk + q4)
+      f32x4 x = zero4();
 #pragma unroll
-      for (int jb = 0; jb < 4 - d; ++jb) {  // target block (ib, jb) = (jb + d, jb)
-        const int ib = jb + d;
-        const float* arow = Af + (16 * ib + a) * LDA;
-        float x = 0.f;
+      for (int kk = 0; kk < 4; ++kk)
+        x = mfma4(arow[16 * jb + 4 * kk], Af[(16 * jb + 4 * kk + q4) * LDA + 16 * jb + r], x);
+      for (int kb = jb + 1; kb < ib; ++kb)
 #pragma unroll
-        for (int c = 0; c < 16; ++c) x += arow[16 * jb + c] * Af[(16 * jb + c) * LDA + 16 * jb + bc];
+        for (int kk = 0; kk < 4; ++kk)
+          x = mfma4(arow[16 * kb + 4 * kk], Af[(16 * jb + r) * LDA + 16 * kb + 4 * kk + q4], x);
+      float* blk = Af + (16 * jb + r) * LDA + 16 * ib;  // block (jb, ib), row r: X^T, then T_{ib,jb}^T
 #pragma unroll
-        for (int kb = jb + 1; kb < ib; ++kb)
+      for (int i = 0; i < 4; ++i) blk[4 * q4 + i] = x[i];
+      const float* trow = Af + (16 * ib + r) * LDA + 16 * ib + q4;  // T_{ib,ib} row r at k = 4 kk + q4
+      f32x4 y = zero4();
 #pragma unroll
-          for (int c = 0; c < 16; ++c) x += arow[16 * kb + c] * Af[(16 * jb + bc) * LDA + 16 * kb + c];
-        xv[jb] = x;
-      }
-      // X goes to block (jb, ib), which no read of this level's first step touches
+      for (int kk = 0; kk < 4; ++kk) y = mfma4(trow[4 * kk], blk[4 * kk + q4], y);
 #pragma unroll
-      for (int jb = 0; jb < 4 - d; ++jb) Af[(16 * jb + bc) * LDA + 16 * (jb + d) + a] = xv[jb];
-      __syncthreads();
-#pragma unroll
-      for (int jb = 0; jb < 4 - d; ++jb) {
-        const int ib = jb + d;
-        float y = 0.f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) y += Af[(16 * ib + a) * LDA + 16 * ib + e] * Af[(16 * jb + bc) * LDA + 16 * ib + e];
-        xv[jb] = -y;
-      }
-      __syncthreads();  // every read of X is done
-#pragma unroll
-      for (int jb = 0; jb < 4 - d; ++jb) Af[(16 * jb + bc) * LDA + 16 * (jb + d) + a] = xv[jb];
+      for (int i = 0; i < 4; ++i) blk[4 * q4 + i] = -y[i];
     }
   }
   __syncthreads();
