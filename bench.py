@@ -54,6 +54,9 @@ def parse_args():
     ap.add_argument("--profile", action="store_true",
                     help="profiler workload only: config-2 fwd+bwd steps, then a plain copy kernel of "
                          "known size (the scale of the HBM byte counters); prints no JSON")
+    ap.add_argument("--profile-layer", action="store_true",
+                    help="profiler workload only: warmup + steps fused fwd+bwd steps of the width-2048 "
+                         "layer at content 2048; prints no JSON")
     return ap.parse_args()
 
 
@@ -169,10 +172,10 @@ def decode_case(gdn, _lib, workmodel, torch, device, steps):
                 bytes_per_step=nbytes, working_set_mb=round(layers * n * H * D * D * 4 / 1e6, 1))
 
 
-def layer_case(torch, device, content, queries, iterations=12):
+def layer_setup(torch, device, content, queries):
     """Whole GatedDelta layer at width 2048 on an image-CQ plan with the event counts of the
-    reference's benchmark rows (scripts/benchmark_gdn.py:34-56): 3 warm-up steps, then the median
-    of ``iterations`` fwd+bwd steps, each bracketed by synchronize."""
+    reference's benchmark rows (scripts/benchmark_gdn.py:34-56).  Returns the plan and
+    ``step(fused)``, one fwd+bwd step of the layer."""
     from cqgdn import layer
 
     torch.manual_seed(872)
@@ -183,12 +186,23 @@ def layer_case(torch, device, content, queries, iterations=12):
     x = torch.randn(plan.hidden_length, 1, 2048, device=device, dtype=torch.bfloat16, requires_grad=True)
     upstream = torch.randn_like(x) / 100
 
+    def step(fused):
+        model.zero_grad(set_to_none=True)
+        x.grad = None
+        y = model(x, plan, fused=fused)
+        (y * upstream).sum().backward()
+
+    return plan, step
+
+
+def layer_case(torch, device, content, queries, iterations=12):
+    """The layer of ``layer_setup``: 3 warm-up steps, then the median of ``iterations`` fwd+bwd
+    steps, each bracketed by synchronize."""
+    plan, layer_step = layer_setup(torch, device, content, queries)
+
     def timed(fused):
         def step():
-            model.zero_grad(set_to_none=True)
-            x.grad = None
-            y = model(x, plan, fused=fused)
-            (y * upstream).sum().backward()
+            layer_step(fused)
 
         for _ in range(3):
             step()
@@ -267,6 +281,14 @@ def main():
     gdn.initialize()  # raises without a gfx950 GPU or without libcqgdn.so
     device = "cuda:0"
     sha = _lib.sha256()
+
+    if args.profile_layer:
+        _, layer_step = layer_setup(torch, device, 2048, 1675)
+        for i in range(args.warmup + args.steps):
+            layer_step(True)
+            torch.cuda.synchronize()
+            log(f"layer step {i} done")
+        return
 
     log("config 2 fwd+bwd")
     T, bounds, step, _ = training_case(gdn, synthetic, torch, 2, device)
