@@ -44,7 +44,7 @@ SIGNATURES = {
     "cqgdn_gated_norm_bwd": (_I, [_P, _P, _P, _I64, _I64, _I, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _SZ, _P]),
     "cqgdn_event_inputs_fwd_workspace_size": (_SZ, [_I, _I]),
     "cqgdn_event_inputs_fwd": (_I, [_P, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
-    "cqgdn_event_inputs_bwd_workspace_size": (_SZ, [_I, _I, _I, _I]),
+    "cqgdn_event_inputs_bwd_workspace_size": (_SZ, [_P, _I]),
     "cqgdn_event_inputs_bwd": (_I, [_P, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                                     _P, _I64, _P, _I64, _P, _P, _P, _SZ, _P]),
     "cqgdn_layer_decode_workspace_size": (_SZ, [_I, _I]),
@@ -60,7 +60,8 @@ class EventPlan(ctypes.Structure):
                 ("query_source", _P), ("query_history", _P), ("content_bounds", _P),
                 ("n_content_docs", ctypes.c_int32), ("n_history_rows", ctypes.c_int32), ("q_ptr", _P),
                 ("q_list", _P), ("write_event", _P), ("query_event", _P), ("history_ptr", _P),
-                ("history_list", _P), ("history_rows", _P)]
+                ("history_list", _P), ("history_rows", _P), ("n_fold_rows", ctypes.c_int32), ("fold_rows", _P),
+                ("fold_ptr", _P), ("fold_list", _P)]
 
 
 KERNELS = ("fwd_prep", "fwd_scan", "fwd_out", "bwd_local", "bwd_scan", "bwd_dkw", "recurrent")

@@ -79,7 +79,12 @@ def event_plan(plan, kernel: int, device) -> EventPlan:
     _check(ew.numel() == n_e, "event_q and event_write differ in length")
     rows = torch.cat((order, qs))
     _check(rows.numel() == 0 or (rows.min() >= 0 and rows.max() < n_h), "content/query rows outside the hidden rows")
-    _check(torch.unique(rows).numel() == rows.numel(), "content and query rows must be distinct")
+    # Content rows may share a hidden row: Bi_I+CQ_T plans write the generation prefix's
+    # rows again in their second branch (ops/gated_delta_layout.py:66-83).  Queries read
+    # rows of their own.
+    content_rows = torch.unique(order)
+    _check(torch.unique(qs).numel() == n_q and torch.unique(torch.cat((content_rows, qs))).numel() ==
+           content_rows.numel() + n_q, "query rows must be distinct from each other and from content rows")
     _check(n_e == 0 or (eq.min() >= 0 and eq.max() < n_c + n_q), "event_q out of range")
     _check(n_e == 0 or (ew.min() >= 0 and ew.max() <= n_c), "event_write out of range")
     _check(qh.numel() == 0 or (qh.min() >= 0 and qh.max() <= n_c), "query_history out of range")
@@ -109,20 +114,28 @@ def event_plan(plan, kernel: int, device) -> EventPlan:
     _check(torch.unique(real).numel() == real.numel(), "two hidden rows read the same event")
     read = torch.zeros(n_e, dtype=torch.bool)
     read[real] = True
+    shared = content_rows.numel() < n_c
+    if shared:  # hidden row -> the content rows reading it, ascending (the backward sums them)
+        slot = torch.searchsorted(content_rows, order)
+        fold_ptr, fold_list = _csr(slot, torch.arange(n_c), content_rows.numel())
+    else:
+        fold_ptr = fold_list = torch.zeros(0, dtype=torch.long)
     dev = lambda t: t.to(torch.int32).to(device)
     pad = lambda t: torch.cat((t, t.new_full((1,), -1)))  # a list array is never null, even when empty
     tensors = dict(content_order=dev(order), event_q=dev(eq), event_write=dev(ew), query_source=dev(qs),
                    query_history=dev(qh), content_bounds=dev(torch.tensor(tuple(plan.content_bounds))),
                    q_ptr=dev(q_ptr), q_list=dev(pad(q_list)), write_event=dev(write_event),
                    query_event=dev(query_event), history_ptr=dev(h_ptr), history_list=dev(pad(h_list)),
-                   history_rows=dev(pad(h_rows)))
+                   history_rows=dev(pad(h_rows)), fold_rows=dev(content_rows if shared else fold_ptr),
+                   fold_ptr=dev(fold_ptr), fold_list=dev(fold_list))
     p = lambda name: tensors[name].data_ptr() if tensors[name].numel() else None
     cs = _lib.EventPlan(n_c, n_q, n_e, kernel, p("content_order"), p("event_q"), p("event_write"), p("query_source"),
                         p("query_history"), p("content_bounds"), len(plan.content_bounds) - 1, h_rows.numel(),
                         p("q_ptr"), p("q_list"), p("write_event"), p("query_event"), p("history_ptr"),
-                        p("history_list"), p("history_rows"))
+                        p("history_list"), p("history_rows"), content_rows.numel() if shared else 0,
+                        p("fold_rows"), p("fold_ptr"), p("fold_list"))
     ep = EventPlan(device, kernel, n_h, n_c, n_q, n_e, tuple(plan.content_bounds), tuple(plan.event_bounds),
-                   dev(hidden), dev(torch.nonzero(~read).flatten()), n_c + n_q == n_h, tensors, cs)
+                   dev(hidden), dev(torch.nonzero(~read).flatten()), content_rows.numel() + n_q == n_h, tensors, cs)
     object.__setattr__(plan, "_cqgdn_event_plan", ep)
     return ep
 
@@ -130,7 +143,8 @@ def event_plan(plan, kernel: int, device) -> EventPlan:
 class _LayerCore(torch.autograd.Function):
     @staticmethod
     def forward(ctx, proj, conv_weight, A_log, dt_bias, norm_weight, ep, H, eps, scale):
-        S, n_h, P = H * 128, proj.shape[0], proj.shape[1]
+        # proj may be a column slice of a wider tensor: every read uses its row stride PS
+        S, n_h, PS = H * 128, proj.shape[0], proj.stride(0)
         dev, st = proj.device, gdn._stream(proj.device)
         w = conv_weight.contiguous()
         alog, dtb, nw = A_log.float().contiguous(), dt_bias.float().contiguous(), norm_weight.float().contiguous()
@@ -140,15 +154,15 @@ class _LayerCore(torch.autograd.Function):
         fws = torch.empty(_lib.lib().cqgdn_event_inputs_fwd_workspace_size(ep.n_content, H), dtype=torch.uint8,
                           device=dev)
         a_ptr, b_ptr = proj[:, 4 * S:].data_ptr(), proj[:, 4 * S + H:].data_ptr()
-        gdn.call("cqgdn_event_inputs_fwd", ctypes.byref(ep.cstruct), H, gdn._ptr(proj), P, a_ptr, P, b_ptr, P,
+        gdn.call("cqgdn_event_inputs_fwd", ctypes.byref(ep.cstruct), H, gdn._ptr(proj), PS, a_ptr, PS, b_ptr, PS,
                  gdn._ptr(w), gdn._ptr(alog), gdn._ptr(dtb), gdn._ptr(q), gdn._ptr(k), gdn._ptr(v),
                  gdn._ptr(gb[0]), gdn._ptr(gb[1]), gdn._ptr(fws), fws.numel(), st)
         y, _, rws = gdn._forward(q[None], k[None], v[None], gb[0][None], gb[1][None], ep.event_bounds, True, scale,
                                  training=True)
         out = torch.empty(n_h, H, 128, dtype=proj.dtype, device=dev)
         rstd = torch.empty(n_h, H, dtype=torch.float32, device=dev)
-        gdn.call("cqgdn_gated_norm_fwd", gdn._ptr(y), gdn._ptr(ep.hidden_index), n_h, H, proj[:, 3 * S:].data_ptr(), P,
-                 gdn._ptr(nw), float(eps), gdn._ptr(out), gdn._ptr(rstd), st)
+        gdn.call("cqgdn_gated_norm_fwd", gdn._ptr(y), gdn._ptr(ep.hidden_index), n_h, H, proj[:, 3 * S:].data_ptr(),
+                 PS, gdn._ptr(nw), float(eps), gdn._ptr(out), gdn._ptr(rstd), st)
         ctx.save_for_backward(proj, w, alog, dtb, nw, v, gb, rws, y, rstd)
         ctx.ep, ctx.H, ctx.scale = ep, H, scale
         ctx.dtypes = (conv_weight.dtype, A_log.dtype, dt_bias.dtype, norm_weight.dtype)
@@ -158,27 +172,28 @@ class _LayerCore(torch.autograd.Function):
     def backward(ctx, dout):
         proj, w, alog, dtb, nw, v, gb, rws, y, rstd = ctx.saved_tensors
         ep, H = ctx.ep, ctx.H
-        S, n_h, P = H * 128, proj.shape[0], proj.shape[1]
+        S, n_h, P, PS = H * 128, proj.shape[0], proj.shape[1], proj.stride(0)
         dev, st = proj.device, gdn._stream(proj.device)
+        # the gradient is a dense [rows, P] tensor (row stride P) whatever proj's stride
         full = ep.covers_all and P == 4 * S + 2 * H
-        d_proj = torch.empty_like(proj) if full else torch.zeros_like(proj)
+        d_proj = (torch.empty if full else torch.zeros)(n_h, P, dtype=proj.dtype, device=dev)
         do = dout.contiguous()
         dy = torch.empty(ep.n_events, H, 128, dtype=proj.dtype, device=dev)
         dnw = torch.empty(128, dtype=torch.float32, device=dev)
         nws = torch.empty(max(_lib.lib().cqgdn_gated_norm_bwd_workspace_size(n_h, H), 16), dtype=torch.uint8,
                           device=dev)
         gdn.call("cqgdn_gated_norm_bwd", gdn._ptr(y), gdn._ptr(ep.hidden_index), gdn._ptr(ep.unread_events),
-                 ep.unread_events.numel(), n_h, H, proj[:, 3 * S:].data_ptr(), P, gdn._ptr(nw), gdn._ptr(rstd),
+                 ep.unread_events.numel(), n_h, H, proj[:, 3 * S:].data_ptr(), PS, gdn._ptr(nw), gdn._ptr(rstd),
                  gdn._ptr(do), gdn._ptr(dy), d_proj[:, 3 * S:].data_ptr(), P, gdn._ptr(dnw), gdn._ptr(nws),
                  nws.numel(), st)
         dq, dk, dv, dg, db = gdn._backward(v[None], gb[0][None], gb[1][None], rws, dy, ep.event_bounds, True,
                                            ctx.scale)
         dw = torch.empty(w.shape, dtype=torch.float32, device=dev)
         dgate = torch.empty(2 * H, dtype=torch.float32, device=dev)
-        ews = torch.empty(_lib.lib().cqgdn_event_inputs_bwd_workspace_size(ep.n_content, ep.n_queries, H, ep.kernel),
+        ews = torch.empty(_lib.lib().cqgdn_event_inputs_bwd_workspace_size(ctypes.byref(ep.cstruct), H),
                           dtype=torch.uint8, device=dev)
-        gdn.call("cqgdn_event_inputs_bwd", ctypes.byref(ep.cstruct), H, gdn._ptr(proj), P,
-                 proj[:, 4 * S:].data_ptr(), P, proj[:, 4 * S + H:].data_ptr(), P, gdn._ptr(w), gdn._ptr(alog),
+        gdn.call("cqgdn_event_inputs_bwd", ctypes.byref(ep.cstruct), H, gdn._ptr(proj), PS,
+                 proj[:, 4 * S:].data_ptr(), PS, proj[:, 4 * S + H:].data_ptr(), PS, gdn._ptr(w), gdn._ptr(alog),
                  gdn._ptr(dtb), gdn._ptr(dq), gdn._ptr(dk), gdn._ptr(dv), gdn._ptr(dg), gdn._ptr(db),
                  gdn._ptr(d_proj), P, d_proj[:, 4 * S:].data_ptr(), P, d_proj[:, 4 * S + H:].data_ptr(), P,
                  gdn._ptr(dw), gdn._ptr(dgate), gdn._ptr(ews), ews.numel(), st)
@@ -200,8 +215,8 @@ def layer_core(proj, conv_weight, A_log, dt_bias, norm_weight, plan, *, heads, e
             norm_weight.shape != (128,):
         raise ValueError("parameter shapes do not match the head count")
     gdn._require_gpu(proj, conv_weight, A_log, dt_bias, norm_weight)
-    if proj.stride(0) % 8 or proj.data_ptr() % 16:
-        proj = proj.contiguous()
+    if proj.stride(0) < proj.shape[1] or proj.stride(0) % 8 or proj.data_ptr() % 16:
+        proj = proj.contiguous()  # the kernels read rows proj.stride(0) apart with 16-byte loads
     ep = event_plan(plan, conv_weight.shape[1], proj.device)
     if ep.n_hidden != proj.shape[0]:
         raise ValueError("proj rows do not match the plan's hidden rows")

@@ -150,16 +150,22 @@ def _require_gpu(*tensors):
 
 
 def reverse_cumsum(dg, bounds):
-    """Reverse chunk-local cumsum of dg [1,T,H] fp32 (ops/gated_delta_net.py:77-87)."""
+    """Reverse chunk-local cumsum (chunk 64) of dg in the reference's head-first layout [B,H,T]
+    (ops/gated_delta_net.py:77-87, called at :204 on the backward's head-first dg), fp32 out.
+
+    Packed bounds (B == 1) restart the chunks at every document; without bounds every batch
+    row is its own sequence."""
     _require_gpu(dg)
-    b, t, h = dg.shape
-    x = dg.reshape(b * t, h).float().contiguous()
+    b, h, t = dg.shape
+    x = dg.transpose(1, 2).reshape(b * t, h).float().contiguous()  # the kernel's time-first rows
     bounds = tuple(range(0, b * t + 1, t)) if bounds is None else bounds
+    if bounds[-1] != b * t:
+        raise ValueError("bounds must cover every token")
     _, table, _ = device_metadata(bounds, str(dg.device))
     out = torch.empty_like(x)
     call("cqgdn_chunk_local_cumsum", _ptr(x), _ptr(out), b * t, h, _ptr(table), table.shape[0], 1,
          _stream(dg.device))
-    return out.reshape(b, t, h)
+    return out.reshape(b, t, h).transpose(1, 2).contiguous()
 
 
 @lru_cache(maxsize=128)

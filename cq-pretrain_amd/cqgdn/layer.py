@@ -112,6 +112,76 @@ def cq_layer_plan(content: int, queries: int, image_groups=(249, 249), kernel: i
     )
 
 
+def two_branch_plan(content: int, queries: int, prefix: int, suffix: int, image_groups=(), suffix_groups=(8,),
+                    kernel: int = 4, seed: int = 0) -> LayerPlan:
+    """A plan with the two branches of a Bi_I+CQ_T step (ops/gated_delta_layout.py:55-83, 108-150).
+
+    Branch 0 is ``cq_layer_plan(content, queries, image_groups)``: hidden rows 0 .. content-1
+    plus the queries.  Branch 1, the masked-generation branch, is a document of its own whose
+    first ``prefix`` items re-write hidden rows 0 .. prefix-1 (without emitting outputs, as the
+    reference's ``i >= plan.prefix`` flag) and whose ``suffix`` items are new hidden rows
+    content .. content+suffix-1, with multi-token groups of ``suffix_groups`` sizes at seeded
+    places.  Query hidden rows follow all keys (keys + j).  So content_order repeats hidden rows
+    0 .. prefix-1, and the layer's backward must sum their gradients."""
+    base = cq_layer_plan(content, queries, image_groups, kernel, seed)
+    rnd = random.Random(seed + 1)
+    keys = content + suffix
+    n1 = prefix + suffix
+    hidden1 = list(range(prefix)) + list(range(content, keys))
+    emit1 = [False] * prefix + [True] * suffix
+    # groups of branch 1: single tokens, and the multi-token groups placed in the suffix
+    sizes, pos, groups = list(suffix_groups), 0, []
+    starts = sorted(rnd.sample(range(prefix, n1 - sum(sizes) + 1), len(sizes))) if sizes else []
+    shift, at = 0, {}
+    for st, size in zip(starts, sizes):
+        at[st + shift] = size
+        shift += size
+    while pos < n1:
+        size = at.get(pos, 1)
+        groups.append(list(range(pos, pos + size)))
+        pos += size
+    nc = content + n1
+    ev0 = base.event_q.numel()
+    q0 = base.event_q.clone()
+    eq0 = torch.where(q0 < content, q0, q0 - content + nc)  # query rows move past branch 1's content rows
+    ew0 = torch.where(base.event_write < content, base.event_write, torch.full_like(base.event_write, nc))
+    event_q, event_write, out = [], [], {}
+    for members in groups:
+        for i in members:
+            ci = content + i
+            if len(members) == 1 and emit1[i]:
+                out[hidden1[i]] = ev0 + len(event_q)
+            event_q.append(ci)
+            event_write.append(ci)
+        if len(members) > 1:
+            for i in members:
+                if emit1[i]:
+                    out[hidden1[i]] = ev0 + len(event_q)
+                event_q.append(content + i)
+                event_write.append(nc)
+    hidden_event = torch.empty(keys + queries, dtype=torch.long)
+    hidden_event[:content] = base.hidden_event[:content]
+    for r, e in out.items():
+        hidden_event[r] = e
+    hidden_event[keys:] = base.hidden_event[content:]
+    qh = base.query_history
+    long = lambda xs: torch.tensor(xs, dtype=torch.long)
+    n_events = ev0 + len(event_q)
+    return LayerPlan(
+        content_order=torch.cat((base.content_order, long(hidden1))),
+        event_q=torch.cat((eq0, long(event_q))),
+        event_write=torch.cat((ew0, long(event_write))),
+        query_source=torch.arange(keys, keys + queries),
+        query_history=torch.where(qh < content, qh, torch.full_like(qh, nc)),
+        content_cu=torch.tensor([0, content, nc], dtype=torch.int32),
+        content_bounds=(0, content, nc),
+        event_cu=torch.tensor([0, ev0, n_events], dtype=torch.long),
+        event_bounds=(0, ev0, n_events),
+        hidden_length=keys + queries,
+        hidden_event=hidden_event,
+    )
+
+
 def concat_plans(*plans: LayerPlan) -> LayerPlan:
     """Pack single-document plans into one plan of several documents (the layout
     ops/gated_delta_layout.py:105-150 produces for a packed batch): hidden rows, content

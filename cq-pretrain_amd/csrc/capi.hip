@@ -282,7 +282,7 @@ int cqgdn_conv1d_bwd(const void* x, const void* weight, const void* dy, const in
     return fail(CQGDN_EINVAL, "workspace must be 16-byte aligned and >= cqgdn_conv1d_bwd_workspace_size bytes");
   launch_conv_bwd(static_cast<const bf16*>(x), nullptr, C, static_cast<const bf16*>(weight),
                   static_cast<const bf16*>(dy), bounds, n_docs, (int)T, C, K, activation != 0, static_cast<bf16*>(dx),
-                  C, dweight, static_cast<float*>(workspace), (hipStream_t)stream);
+                  nullptr, C, dweight, static_cast<float*>(workspace), (hipStream_t)stream);
   return check_launch("cqgdn_conv1d_bwd");
 }
 
@@ -356,6 +356,9 @@ int ev_args(const cqgdn_event_plan* p, int H, const void* raw, int64_t raw_strid
   if (p->n_queries > 0 && (!p->query_source || !p->query_history || !p->query_event))
     return fail(CQGDN_EINVAL, "query index arrays are null");
   if (p->n_history_rows > 0 && !p->history_rows) return fail(CQGDN_EINVAL, "history_rows is null");
+  if (p->n_fold_rows < 0 || p->n_fold_rows > p->n_content ||
+      (p->n_fold_rows > 0 && (!p->fold_rows || !p->fold_ptr || !p->fold_list)))
+    return fail(CQGDN_EINVAL, "fold rows: n_fold_rows must be in 0..n_content with non-null fold arrays");
   out = EvArgs{H, p->conv_kernel, p->n_content, p->n_queries, p->n_events, p->n_history_rows,
                p->content_order, p->event_q, p->event_write, p->query_source, p->query_history,
                p->q_ptr, p->q_list, p->write_event, p->query_event, p->history_ptr, p->history_list,
@@ -394,12 +397,14 @@ int cqgdn_event_inputs_fwd(const cqgdn_event_plan* plan, int H, const void* raw,
 
 namespace {
 struct EvLayout {
-  size_t dconv, dpre, gpart, qpart, cpart, qsum, total;
+  size_t dconv, dpre, gpart, qpart, cpart, qsum, dcont, dcgate, total;
 };
-EvLayout ev_layout(int n_content, int n_queries, int H, int K) {
+EvLayout ev_layout(int n_content, int n_queries, int H, int K, bool fold) {
   const size_t S = (size_t)H * CQGDN_HEAD_DIM;
   EvLayout l{};
   size_t o = 0;
+  l.dcont = o; o += fold ? align256((size_t)n_content * 3 * S * sizeof(bf16)) : 0;
+  l.dcgate = o; o += fold ? align256((size_t)n_content * 2 * H * sizeof(float)) : 0;
   l.dconv = o; o += align256((size_t)n_content * 3 * S * sizeof(bf16));
   l.dpre = o; o += align256((size_t)n_queries * S * sizeof(float));
   l.gpart = o; o += align256((size_t)n_content * 2 * H * sizeof(float));
@@ -411,9 +416,11 @@ EvLayout ev_layout(int n_content, int n_queries, int H, int K) {
 }
 }  // namespace
 
-size_t cqgdn_event_inputs_bwd_workspace_size(int n_content, int n_queries, int H, int conv_kernel) {
-  if (n_content < 0 || n_queries < 0 || H <= 0 || conv_kernel < 2 || conv_kernel > 4) return 0;
-  return ev_layout(n_content, n_queries, H, conv_kernel).total;
+size_t cqgdn_event_inputs_bwd_workspace_size(const cqgdn_event_plan* plan, int H) {
+  if (!plan || plan->n_content < 0 || plan->n_queries < 0 || H <= 0 || plan->conv_kernel < 2 ||
+      plan->conv_kernel > 4)
+    return 0;
+  return ev_layout(plan->n_content, plan->n_queries, H, plan->conv_kernel, plan->n_fold_rows > 0).total;
 }
 
 int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, const void* raw, int64_t raw_stride, const void* a,
@@ -433,13 +440,17 @@ int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, const void* raw,
     return fail(CQGDN_EINVAL, "d_raw (16-byte aligned), d_a, d_b, dweight (16-byte aligned), dgate must be non-null");
   if (d_raw_stride < 3 * S || d_raw_stride % 8 || d_a_stride < H || d_b_stride < H)
     return fail(CQGDN_EINVAL, "gradient strides must match the input layouts");
-  const EvLayout l = ev_layout(plan->n_content, plan->n_queries, H, plan->conv_kernel);
+  const bool fold = plan->n_fold_rows > 0;
+  const EvLayout l = ev_layout(plan->n_content, plan->n_queries, H, plan->conv_kernel, fold);
   if (!workspace || !aligned(workspace, 256) || workspace_bytes < l.total)
     return fail(CQGDN_EINVAL, "workspace must be 256-byte aligned and >= cqgdn_event_inputs_bwd_workspace_size");
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   const EvGrads d{static_cast<const bf16*>(dq), static_cast<const bf16*>(dk), static_cast<const bf16*>(dv), dg, dbeta,
                   static_cast<bf16*>(d_raw), d_raw_stride, static_cast<bf16*>(d_a), d_a_stride,
-                  static_cast<bf16*>(d_b), d_b_stride, dweight, dgate};
+                  static_cast<bf16*>(d_b), d_b_stride, dweight, dgate,
+                  fold ? reinterpret_cast<bf16*>(ws + l.dcont) : nullptr,
+                  fold ? reinterpret_cast<float*>(ws + l.dcgate) : nullptr, plan->n_fold_rows, plan->fold_rows,
+                  plan->fold_ptr, plan->fold_list};
   const EvWork w{reinterpret_cast<bf16*>(ws + l.dconv), reinterpret_cast<float*>(ws + l.dpre),
                  reinterpret_cast<float*>(ws + l.gpart), reinterpret_cast<float*>(ws + l.qpart),
                  reinterpret_cast<float*>(ws + l.cpart), reinterpret_cast<float*>(ws + l.qsum)};

@@ -8,7 +8,8 @@
 //
 // x, y, dy, dx: bf16 [T][C] (time-first, B = 1, packed documents); w: bf16
 // [C][K], K <= 4.  Row u of x may be read through a row map (x row xrows[u],
-// xs elements apart) and row t of dx written to dx row xrows[t] (dxs apart):
+// xs elements apart) and row t of dx written through its own map (dx row
+// dxrows[t], dxs apart; null: row t):
 // the layer's content gather updates = raw.index_select(0, content_order)
 // (models/backbone_qwen35.py:167) and its backward, consumed in the loads and
 // stores.  A thread owns 8 consecutive channels (16-byte accesses, a
@@ -133,7 +134,7 @@ __device__ __forceinline__ void conv_bwd_strip(const bf16* __restrict__ x, const
                                                int64_t xstr, const typename ConvVec<CH>::f (&wk)[K],
                                                const bf16* __restrict__ dy, const int32_t* __restrict__ bounds,
                                                int n_docs, int T, int C, int c, int s, int e, int act,
-                                               bf16* __restrict__ dx, int64_t dxs,
+                                               bf16* __restrict__ dx, const int32_t* __restrict__ dxrows, int64_t dxs,
                                                typename ConvVec<CH>::f (&dwa)[K]) {
   typedef typename ConvVec<CH>::b bv;
   typedef typename ConvVec<CH>::f fv;
@@ -210,7 +211,7 @@ __device__ __forceinline__ void conv_bwd_strip(const bf16* __restrict__ x, const
 #pragma unroll
         for (int m = 1; m < K; ++m)
           if (!DOCS || st[(j + 1 + m) % K] == st[(j + 1) % K]) acc += wk[K - 1 - m] * dp[(j + 1 + m) % K];
-        *reinterpret_cast<bv*>(dx + (rows ? (int64_t)rows[t] : (int64_t)t) * dxs + c) =
+        *reinterpret_cast<bv*>(dx + (dxrows ? (int64_t)dxrows[t] : (int64_t)t) * dxs + c) =
             __builtin_convertvector(acc, bv);
       }
     }
@@ -222,7 +223,8 @@ __global__ __launch_bounds__(64) void conv_bwd_kernel(const bf16* __restrict__ x
                                                      int64_t xs, const bf16* __restrict__ w,
                                                      const bf16* __restrict__ dy, const int32_t* __restrict__ bounds,
                                                      int n_docs, int T, int C, int rows, int act,
-                                                     bf16* __restrict__ dx, int64_t dxs, float* __restrict__ dw_part) {
+                                                     bf16* __restrict__ dx, const int32_t* __restrict__ dxrows,
+                                                     int64_t dxs, float* __restrict__ dw_part) {
   constexpr int CH = CONV_BWD_CH;
   typedef typename ConvVec<CH>::f fv;
   const int c = (blockIdx.y * 64 + threadIdx.x) * CH;
@@ -243,9 +245,9 @@ __global__ __launch_bounds__(64) void conv_bwd_kernel(const bf16* __restrict__ x
   const int i = lower_bound(bounds, n_docs, u0 + 1);
   const bool docs = __builtin_amdgcn_readfirstlane(i <= n_docs && bounds[i] < uend);
   if (docs)
-    conv_bwd_strip<K, CH, true>(x, xrows, xs, wk, dy, bounds, n_docs, T, C, c, s, e, act, dx, dxs, dwa);
+    conv_bwd_strip<K, CH, true>(x, xrows, xs, wk, dy, bounds, n_docs, T, C, c, s, e, act, dx, dxrows, dxs, dwa);
   else
-    conv_bwd_strip<K, CH, false>(x, xrows, xs, wk, dy, bounds, n_docs, T, C, c, s, e, act, dx, dxs, dwa);
+    conv_bwd_strip<K, CH, false>(x, xrows, xs, wk, dy, bounds, n_docs, T, C, c, s, e, act, dx, dxrows, dxs, dwa);
   float* part = dw_part + ((size_t)blockIdx.x * C + c) * K;
 #pragma unroll
   for (int ch = 0; ch < CH; ++ch)
@@ -304,14 +306,14 @@ void launch_conv_fwd(const bf16* x, const int32_t* xrows, int64_t xs, const bf16
 }
 
 void launch_conv_bwd(const bf16* x, const int32_t* xrows, int64_t xs, const bf16* w, const bf16* dy,
-                     const int32_t* bounds, int n_docs, int T, int C, int K, int act, bf16* dx, int64_t dxs, float* dw,
-                     float* part, hipStream_t stream) {
+                     const int32_t* bounds, int n_docs, int T, int C, int K, int act, bf16* dx, const int32_t* dxrows,
+                     int64_t dxs, float* dw, float* part, hipStream_t stream) {
   const int rows = conv_strip_rows(T), strips = conv_strips(T);
   const dim3 grid(strips, (C / CONV_BWD_CH + 63) / 64);
   switch (K) {
-    case 2: hipLaunchKernelGGL(conv_bwd_kernel<2>, grid, dim3(64), 0, stream, x, xrows, xs, w, dy, bounds, n_docs, T, C, rows, act, dx, dxs, part); break;
-    case 3: hipLaunchKernelGGL(conv_bwd_kernel<3>, grid, dim3(64), 0, stream, x, xrows, xs, w, dy, bounds, n_docs, T, C, rows, act, dx, dxs, part); break;
-    default: hipLaunchKernelGGL(conv_bwd_kernel<4>, grid, dim3(64), 0, stream, x, xrows, xs, w, dy, bounds, n_docs, T, C, rows, act, dx, dxs, part); break;
+    case 2: hipLaunchKernelGGL(conv_bwd_kernel<2>, grid, dim3(64), 0, stream, x, xrows, xs, w, dy, bounds, n_docs, T, C, rows, act, dx, dxrows, dxs, part); break;
+    case 3: hipLaunchKernelGGL(conv_bwd_kernel<3>, grid, dim3(64), 0, stream, x, xrows, xs, w, dy, bounds, n_docs, T, C, rows, act, dx, dxrows, dxs, part); break;
+    default: hipLaunchKernelGGL(conv_bwd_kernel<4>, grid, dim3(64), 0, stream, x, xrows, xs, w, dy, bounds, n_docs, T, C, rows, act, dx, dxrows, dxs, part); break;
   }
   launch_colsum(part, strips, C * K, dw, stream);
 }

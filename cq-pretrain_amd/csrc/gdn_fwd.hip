@@ -486,20 +486,25 @@ __device__ __forceinline__ void fwd_fix_tail(FwdStage<E>& S, const int32_t* __re
 // global stores of one copy-out (4 of h^T, 2 of v_new^T)
 constexpr int FWD_OUT_STORES = 6;
 
-// scratch of one step -> hT [v0..v0+15][k], vnT [v0..v0+15][t]
+// scratch of one step -> hT [v0..v0+15][k], vnT [v0..v0+15][t]; NaN instead once
+// a hand-off wait has given up (the scratch may then hold another step's values)
 template <class E>
 __device__ __forceinline__ void fwd_copy_out(const FwdScratch<E>& sc, int c, int H, int h, int v0, int lane,
-                                             E* __restrict__ hT, E* __restrict__ vnT) {
+                                             bool poison, E* __restrict__ hT, E* __restrict__ vnT) {
+  typedef typename Vec<E>::x8 X8;
   const size_t cb = (size_t)c * H + h;
+  const X8 nan8 = to8<E>(f32x8{NAN, NAN, NAN, NAN, NAN, NAN, NAN, NAN});
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int seg = 64 * i + lane, v = seg >> 4, ks = seg & 15;
-    st8(hT + cb * (D * D) + (v0 + v) * D + 8 * ks, ld8(sc.s + v * SC_SROW + 8 * ks));
+    const X8 x = ld8(sc.s + v * SC_SROW + 8 * ks);
+    st8(hT + cb * (D * D) + (v0 + v) * D + 8 * ks, poison ? nan8 : x);
   }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int seg = 64 * i + lane, v = seg >> 3, ts = seg & 7;
-    st8(vnT + cb * (D * CH) + (v0 + v) * CH + 8 * ts, ld8(sc.v + v * SC_VROW + 8 * ts));
+    const X8 x = ld8(sc.v + v * SC_VROW + 8 * ts);
+    st8(vnT + cb * (D * CH) + (v0 + v) * CH + 8 * ts, poison ? nan8 : x);
   }
 }
 
@@ -518,7 +523,10 @@ __device__ __forceinline__ void fwd_loader(FwdStage<E>* stage, int* flags, const
                                            const E* __restrict__ KgT, const float* __restrict__ gc,
                                            E* __restrict__ hT, E* __restrict__ vnT) {
   const FwdCopyOffsets<PART> offs = fwd_copy_offsets<E, PART>(H, h, lane);
-  bool ok = true;  // once a wait gives up, the rest run without waiting (the consumer poisons its outputs)
+  // Once a wait gives up, the rest run without waiting, and flags[3] tells the
+  // consumer, which turns its state (and so every later output) to NaN: stages
+  // refilled without the wait may be overwritten while it reads them.
+  bool ok = true;
   for (int x = 0; x < n + SC_STAGES; ++x) {
     const int y = x - 2;
     if (y >= 0 && y < n) {
@@ -532,9 +540,16 @@ __device__ __forceinline__ void fwd_loader(FwdStage<E>* stage, int* flags, const
       lds_flag_publish(&flags[PART], y + 1);
     }
     if (x >= SC_STAGES) {
-      if (ok) ok = lds_flag_wait_ge<true>(&flags[2], x - SC_STAGES + 1);
+      if (ok) {
+        ok = lds_flag_wait_ge<true>(&flags[2], x - SC_STAGES + 1);
+        if (!ok) {  // published (and complete in LDS) before this wave refills any stage
+          lds_flag_publish(&flags[3], 1);
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+      }
       if (PART == 1 && x - SC_STAGES < n)
-        fwd_copy_out(fwd_scratch(stage[x & (SC_STAGES - 1)]), c_begin + x - SC_STAGES, H, h, v0, lane, hT, vnT);
+        fwd_copy_out(fwd_scratch(stage[x & (SC_STAGES - 1)]), c_begin + x - SC_STAGES, H, h, v0, lane,
+                     lds_flag_read(&flags[3]) != 0, hT, vnT);
     }
     if (x < n) fwd_issue<E, PART>(stage[x & (SC_STAGES - 1)], chunks, c_begin + x, H, h, v0, lane, offs, W, UT, KgT, gc);
   }
@@ -557,7 +572,8 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
   __shared__ FwdStage<E> stage[SC_STAGES];
   // hand-off counts: [0], [1] chunks whose part from loader 0 / 1 has landed
   // (and, for loader 0, whose tail rows are zeroed); [2] chunks the consumer
-  // has finished (operands read, outputs in the stage's scratch)
+  // has finished (operands read, outputs in the stage's scratch); [3] nonzero
+  // once a loader's wait for the consumer has given up
   __shared__ __attribute__((aligned(16))) int flags[4];
   if (threadIdx.x < 4) flags[threadIdx.x] = 0;
   __syncthreads();
@@ -585,10 +601,12 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) uofs[i4] = 2 * (r * 64 + 8 * ((2 * i4 + (q4 >> 1)) ^ ((r >> 1) & 7)) + 4 * (q4 & 1));
     const int sofs = 2 * (r * SC_SROW + 4 * q4), vofs = 2 * (r * SC_VROW + 4 * q4);
-    int seen = 0;    // both loaders' counts are at least this (last read)
-    bool ok = true;  // every hand-off wait succeeded
+    int seen = 0;       // both loaders' counts are at least this (last read)
+    bool ok = true;     // every hand-off wait succeeded
+    int poisoned = 0;   // flags[3] as last read
     for (int tau = 0; tau < n; ++tau) {
       if (ok && seen <= tau) ok = scan_wait_ready(flags, tau + 1, seen);
+      if (poisoned) ok = false;
       if (!ok) {  // a broken hand-off: make every later output NaN
 #pragma unroll
         for (int m = 0; m < 8; ++m) S[m] = f32x4{NAN, NAN, NAN, NAN};
@@ -614,6 +632,7 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
 #pragma unroll
         for (int m = 0; m < 8; ++m) fk[m][j] = *reinterpret_cast<const X8*>(kb + kofs[j] + 2048 * m);
       const int2 pre = lds_flag_read2(flags);  // for the next step, read while this one computes
+      poisoned = lds_flag_read(&flags[3]);
       __builtin_amdgcn_sched_barrier(0);
       X4 sh[8];
 #pragma unroll

@@ -219,8 +219,13 @@ __global__ __launch_bounds__(512) void events_bwd_content_kernel(EvArgs a, EvGra
       const float sb = sigm((float)a.gb[row * a.gb_stride + h]);
       db = d.dbeta[(int64_t)we * a.H + h] * sb * (1.f - sb);
     }
-    d.da[row * d.da_stride + h] = (bf16)da;
-    d.db[row * d.db_stride + h] = (bf16)db;
+    if (d.dcont) {
+      d.dcgate[(int64_t)cr * 2 * a.H + h] = da;
+      d.dcgate[(int64_t)cr * 2 * a.H + a.H + h] = db;
+    } else {
+      d.da[row * d.da_stride + h] = (bf16)da;
+      d.db[row * d.db_stride + h] = (bf16)db;
+    }
     gpart[(int64_t)cr * 2 * a.H + h] = dA;
     gpart[(int64_t)cr * 2 * a.H + a.H + h] = da;
   }
@@ -326,8 +331,31 @@ __global__ __launch_bounds__(512) void events_bwd_history_kernel(EvArgs a, EvGra
       if (i == t) wi = wk[t];
     acc += f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]} * wi;
   }
-  bf16* dr = d.draw + (int64_t)a.order[cr] * d.draw_stride + c;
+  bf16* dr = d.dcont ? d.dcont + (int64_t)cr * 3 * S + c : d.draw + (int64_t)a.order[cr] * d.draw_stride + c;
   st8(dr, cvt8(cvtf8(ld8(dr)) + acc));
+}
+
+// Hidden row fold_rows[blockIdx.x], read by several content rows: its raw q|k|v
+// gradient is the sum of theirs (ascending content row, fixed order), and its a
+// and b gradients likewise -- the backward of the reference's
+// raw.index_select(0, content_order) when content_order repeats a row.
+__global__ __launch_bounds__(512) void events_bwd_fold_kernel(EvArgs a, EvGrads d) {
+  const int row = d.fold_rows[blockIdx.x], S = a.H * GN_D;
+  const int p0 = d.fold_ptr[blockIdx.x], p1 = d.fold_ptr[blockIdx.x + 1];
+  bf16* dr = d.draw + (int64_t)row * d.draw_stride;
+  for (int c = threadIdx.x * 8; c < 3 * S; c += blockDim.x * 8) {
+    f32x8 acc = f32x8{};
+    for (int p = p0; p < p1; ++p) acc += cvtf8(ld8(d.dcont + (int64_t)d.fold_list[p] * 3 * S + c));
+    st8(dr + c, cvt8(acc));
+  }
+  if (threadIdx.x < 2 * a.H) {
+    float acc = 0.f;
+    for (int p = p0; p < p1; ++p) acc += d.dcgate[(int64_t)d.fold_list[p] * 2 * a.H + threadIdx.x];
+    if (threadIdx.x < a.H)
+      d.da[(int64_t)row * d.da_stride + threadIdx.x] = (bf16)acc;
+    else
+      d.db[(int64_t)row * d.db_stride + threadIdx.x - a.H] = (bf16)acc;
+  }
 }
 
 __global__ __launch_bounds__(256) void add_f32_kernel(float* __restrict__ dst, const float* __restrict__ src, int n) {
@@ -365,8 +393,12 @@ void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content
     }
   }
   if (a.n_c > 0) {
-    launch_conv_bwd(a.raw, a.order, a.raw_stride, a.w, w.dconv, content_bounds, n_content_docs, a.n_c, 3 * S, a.K, 1,
-                    d.draw, d.draw_stride, d.dw, w.cpart, stream);
+    if (d.dcont)  // per-content-row gradients, folded into the hidden rows below
+      launch_conv_bwd(a.raw, a.order, a.raw_stride, a.w, w.dconv, content_bounds, n_content_docs, a.n_c, 3 * S,
+                      a.K, 1, d.dcont, nullptr, 3 * S, d.dw, w.cpart, stream);
+    else
+      launch_conv_bwd(a.raw, a.order, a.raw_stride, a.w, w.dconv, content_bounds, n_content_docs, a.n_c, 3 * S,
+                      a.K, 1, d.draw, a.order, d.draw_stride, d.dw, w.cpart, stream);
   } else {
     launch_colsum(w.cpart, 0, 3 * S * a.K, d.dw, stream);  // zeros
   }
@@ -377,6 +409,8 @@ void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content
       default: hipLaunchKernelGGL(events_bwd_history_kernel<4>, dim3(a.n_hrows), block, 0, stream, a, d, w.dpre); break;
     }
   }
+  if (d.dcont && d.n_fold > 0)
+    hipLaunchKernelGGL(events_bwd_fold_kernel, dim3(d.n_fold), dim3(512), 0, stream, a, d);
   launch_colsum(w.gpart, a.n_c, 2 * H, d.dgate, stream);
   launch_colsum(w.qpart, qb, S * a.K, w.qsum, stream);
   hipLaunchKernelGGL(add_f32_kernel, dim3((S * a.K + 255) / 256), dim3(256), 0, stream, d.dw, w.qsum, S * a.K);

@@ -50,12 +50,12 @@ void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* 
                       hipStream_t stream);
 // packed depthwise causal conv1d (gdn_conv.hip); bounds: int32 [n_docs + 1] on the device
 int conv_strips(int64_t T);  // row strips of the conv backward (dw partials per strip)
-// x row u is x + (xrows ? xrows[u] : u) * xs; dx row t likewise with dxs; y and dy are [T][C]
+// x row u is x + (xrows ? xrows[u] : u) * xs; dx row t is dx + (dxrows ? dxrows[t] : t) * dxs; y and dy are [T][C]
 void launch_conv_fwd(const bf16* x, const int32_t* xrows, int64_t xs, const bf16* w, const int32_t* bounds,
                      int n_docs, int T, int C, int K, int act, bf16* y, hipStream_t stream);
 void launch_conv_bwd(const bf16* x, const int32_t* xrows, int64_t xs, const bf16* w, const bf16* dy,
-                     const int32_t* bounds, int n_docs, int T, int C, int K, int act, bf16* dx, int64_t dxs, float* dw,
-                     float* part, hipStream_t stream);
+                     const int32_t* bounds, int n_docs, int T, int C, int K, int act, bf16* dx, const int32_t* dxrows,
+                     int64_t dxs, float* dw, float* part, hipStream_t stream);
 // out[j] = sum over p < parts of part[p][j], fixed order (gdn_conv.hip); n % 4 == 0, 16-byte aligned part
 void launch_colsum(const float* part, int parts, int n, float* out, hipStream_t stream);
 // Event inputs of one GatedDelta layer (gdn_glue.hip).  S = H * 128 channels per
@@ -96,6 +96,16 @@ struct EvGrads {
   int64_t db_stride;
   float* dw;     // conv weight gradient [3S][K]
   float* dgate;  // [2H]: A_log, then dt_bias
+  // When content rows share hidden rows (a plan whose content_order repeats a
+  // row): the content rows' raw and gate gradients go to these per-content-row
+  // buffers instead of the hidden rows, and the fold pass sums them into draw,
+  // da, db over the fold CSR.  Null otherwise.
+  bf16* dcont;   // [n_c][3S]
+  float* dcgate; // [n_c][2H]: da, then db
+  int n_fold;                 // distinct hidden rows of content_order (when dcont is set)
+  const int32_t* fold_rows;   // [n_fold] those hidden rows
+  const int32_t* fold_ptr;    // [n_fold + 1] CSR: the content rows reading fold_rows[i] ...
+  const int32_t* fold_list;   //   ... ascending
 };
 struct EvWork {
   bf16* dconv;   // [n_c][3S] gradient of the conv output

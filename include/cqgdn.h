@@ -205,6 +205,15 @@ typedef struct cqgdn_event_plan {
   const int32_t* history_ptr;    /* [n_content + 1] CSR: j * (K-1) + i with query_history[j][i] == c ... */
   const int32_t* history_list;   /*   ... ascending */
   const int32_t* history_rows;   /* content rows with at least one history entry */
+  /* Content rows sharing a hidden row: the reference's Bi_I+CQ_T plans re-write the
+   * generation prefix's hidden rows in a second branch (ops/gated_delta_layout.py:66-83),
+   * so content_order repeats them.  n_fold_rows = 0 when content_order repeats no row;
+   * otherwise the distinct hidden rows of content_order, with a CSR of the content rows
+   * reading each, over which the backward sums their gradients (fixed order). */
+  int32_t n_fold_rows;
+  const int32_t* fold_rows;      /* [n_fold_rows] distinct hidden rows of content_order */
+  const int32_t* fold_ptr;       /* [n_fold_rows + 1] CSR: the content rows reading fold_rows[i] ... */
+  const int32_t* fold_list;      /*   ... ascending */
 } cqgdn_event_plan;
 
 /*
@@ -234,9 +243,11 @@ int cqgdn_event_inputs_fwd(const cqgdn_event_plan* plan, int H, const void* raw,
  * same layouts as raw, a, b; other rows are not touched), dweight fp32 [3S][K]
  * and dgate fp32 [2H] (A_log, then dt_bias).  The scatters walk the plan's
  * inverse maps, so every output is written once, without atomics, and the
- * result is deterministic.
+ * result is deterministic.  A hidden row read by several content rows
+ * (n_fold_rows > 0) receives the sum of their gradients.  The workspace size
+ * depends on the plan (it holds per-content-row gradients when rows are shared).
  */
-size_t cqgdn_event_inputs_bwd_workspace_size(int n_content, int n_queries, int H, int conv_kernel);
+size_t cqgdn_event_inputs_bwd_workspace_size(const cqgdn_event_plan* plan, int H);
 int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, const void* raw, int64_t raw_stride, const void* a,
                            int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
                            const float* A_log, const float* dt_bias, const void* dq, const void* dk, const void* dv,

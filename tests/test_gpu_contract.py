@@ -1,0 +1,332 @@
+"""GPU parity of contract shapes the reference accepts, through the public API against the oracle.
+
+* ``delta`` at H = 32, the largest local head count of ops/gated_delta_net.py:235, and the fused
+  layer and its decode step at H = 32;
+* packed batches holding empty documents (host_bounds allows b == a, ops/gated_delta_net.py:112):
+  outputs, gradients, and prefill final states (an empty document's state is its initial state);
+* config 4 at its own shape: 64 sequences, H = 16, fp32 state, 256 consecutive ``recurrent``
+  steps against the float64 oracle step (models/decoding.py:71-77);
+* the CQ read-only invariant of tests/test_qwen35_cq.py:71-89, bit-exact, on the bf16 training
+  path of ``delta`` and through ``events.layer_core``: perturbed query rows leave every content
+  output bit-identical, a perturbed image group leaves every output read before the group's first
+  write bit-identical, and an image group's outputs see its last token;
+* the fused layer on plans whose content rows share hidden rows (the two-branch Bi_I+CQ_T plans
+  of ops/gated_delta_layout.py:66-83), and on a projection that is a column slice of a wider tensor.
+"""
+
+import pytest
+import torch
+
+from gdn_testlib import TOL_BF16, TOL_STATE, assert_close_bf16, rel_l2
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def inputs(T, H, seed, readonly=None):
+    from cqgdn import synthetic
+
+    return synthetic.make_inputs(T, H, 128, seed=seed, readonly=readonly)
+
+
+def fwd_bwd(gdn, xs, bounds, do):
+    xd = [x.to(DEV).requires_grad_() for x in xs]
+    kw = {}
+    if bounds is not None:
+        kw = dict(cu_seqlens=torch.tensor(bounds, device=DEV), cu_seqlens_cpu=list(bounds))
+    y, _ = gdn.delta(*xd, use_qk_l2norm_in_kernel=True, **kw)
+    y.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    return y.detach().cpu(), [x.grad.cpu() for x in xd]
+
+
+def check_against_oracle(xs, bounds, do, y, grads):
+    q, k, v, g, b = (x.double() for x in xs)
+    assert_close_bf16("o", y, O.chunk_delta(q, k, v, g, b, bounds))
+    ref = O.chunk_delta_backward(q, k, v, g, b, do.double(), bounds)
+    for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta"), grads, ref):
+        assert_close_bf16(name, x, r)
+
+
+@pytest.mark.parametrize("T,bounds", [(200, (0, 70, 200)), (130, None)])
+def test_delta_h32_matches_oracle(gdn, T, bounds):
+    """H = 32 (ops/gated_delta_net.py:235): fwd+bwd against the float64 oracle."""
+    print(f"case H=32 T={T} bounds={bounds}", flush=True)
+    xs = inputs(T, 32, seed=3200 + T)
+    do = torch.randn(1, T, 32, 128, generator=torch.Generator().manual_seed(32)).bfloat16()
+    y, grads = fwd_bwd(gdn, xs, bounds, do)
+    check_against_oracle(xs, bounds, do, y, grads)
+
+
+@pytest.mark.parametrize("bounds", [(0, 0, 130, 257), (0, 0, 130, 130, 257, 257), (0, 64, 64, 65)])
+def test_packed_batch_with_empty_documents(gdn, bounds):
+    """Empty documents (b == a in the bounds) at the start, middle and end of a packed batch."""
+    T, H = bounds[-1], 8
+    print(f"case empty documents bounds={bounds}", flush=True)
+    xs = inputs(T, H, seed=77 + len(bounds))
+    do = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(78)).bfloat16()
+    y, grads = fwd_bwd(gdn, xs, bounds, do)
+    check_against_oracle(xs, bounds, do, y, grads)
+    # prefill: per-document final states; an empty document's state is its initial state
+    n_docs = len(bounds) - 1
+    s0 = torch.randn(n_docs, H, 128, 128, generator=torch.Generator().manual_seed(79)) * 0.05
+    for init in (None, s0):
+        _, states = gdn.prefill(*[x.to(DEV) for x in xs], bounds,
+                                initial_state=None if init is None else init.to(DEV))
+        torch.cuda.synchronize()
+        q, k, v, g, b = (x.double() for x in xs)
+        _, ref_states = O.chunk_delta(q, k, v, g, b, bounds, output_final_state=True,
+                                      initial_state=None if init is None else init.double())
+        for d, (a, e) in enumerate(zip(bounds, bounds[1:])):
+            if a == e:
+                want = torch.zeros(H, 128, 128) if init is None else init[d]
+                assert torch.equal(states[d].cpu(), want), f"empty document {d} changed its state"
+            else:
+                r = rel_l2(states[d], ref_states[d])
+                print(f"  document {d} final state rel_l2={r:.3e}", flush=True)
+                assert r <= TOL_STATE
+
+
+def test_config4_decode_256_steps_matches_oracle(gdn):
+    """Config 4 at its own shape: B = 64 sequences, H = 16, fp32 state [64,16,128,128] ~ N(0, 0.02),
+    q/k l2-normalised bf16, beta = sigmoid(N(0,1)), g = -softplus(N(0,1)), 256 consecutive
+    ``recurrent`` steps against the float64 oracle step.  Every step's output within the bf16 bar,
+    the state within 1e-3 (fp32) after the last step."""
+    N, H, steps = 64, 16, 256
+    print(f"case config 4: N={N} H={H} steps={steps}", flush=True)
+    gen = torch.Generator().manual_seed(4)
+    state0 = torch.randn(N, H, 128, 128, generator=gen) * 0.02
+    st = state0.to(DEV)
+    ins, outs = [], []
+    for step in range(steps):
+        q = O.l2norm(torch.randn(N, 1, H, 128, generator=gen)).bfloat16()
+        k = O.l2norm(torch.randn(N, 1, H, 128, generator=gen)).bfloat16()
+        v = torch.randn(N, 1, H, 128, generator=gen).bfloat16()
+        b = torch.randn(N, 1, H, generator=gen).sigmoid()
+        g = -torch.nn.functional.softplus(torch.randn(N, 1, H, generator=gen))
+        out = torch.empty(N, 1, H, 128, dtype=torch.bfloat16, device=DEV)
+        gdn.recurrent(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), b.to(DEV), st, out)
+        ins.append((q, k, v, g, b))
+        outs.append(out)
+    torch.cuda.synchronize()
+    print("  gpu steps done", flush=True)
+    ref_state = state0.double()
+    worst = 0.0
+    for step, ((q, k, v, g, b), out) in enumerate(zip(ins, outs)):
+        ref = O.decode_step(q.double(), k.double(), v.double(), g.double(), b.double(), ref_state)
+        r = rel_l2(out, ref)
+        worst = max(worst, r)
+        assert r <= TOL_BF16, f"step {step}: output rel_l2={r:.3e}"
+    rs = rel_l2(st, ref_state)
+    print(f"  worst output rel_l2={worst:.3e}, final state rel_l2={rs:.3e}", flush=True)
+    assert rs <= TOL_STATE
+
+
+def test_cq_invariant_bf16_training_delta(gdn):
+    """tests/test_qwen35_cq.py:71-77 on the bf16 training path: perturbing the read-only query
+    rows (q * 10 + noise) leaves every content output bit-identical; the gradients still flow."""
+    from cqgdn import synthetic
+
+    mask = synthetic.cq_readonly_mask(2048, 1, 256, seed=5)  # one query block inside the content
+    T = mask.numel()
+    print(f"case CQ invariant, training delta, T={T}", flush=True)
+    xs = inputs(T, 16, seed=55, readonly=mask)
+    do = torch.randn(1, T, 16, 128, generator=torch.Generator().manual_seed(56)).bfloat16()
+    y1, _ = fwd_bwd(gdn, xs, None, do)
+    q2 = xs[0].clone()
+    noise = torch.randn(q2[:, mask].shape, generator=torch.Generator().manual_seed(57))
+    q2[:, mask] = (q2[:, mask].float() * 10 + noise * 10).bfloat16()
+    y2, g2 = fwd_bwd(gdn, [q2, *xs[1:]], None, do)
+    assert torch.equal(y1[:, ~mask], y2[:, ~mask])
+    assert not torch.equal(y1[:, mask], y2[:, mask])
+    assert all(torch.isfinite(g.float()).all() for g in g2)
+
+
+def _layer_params(H, gen):
+    S = H * 128
+    w = (torch.rand(3 * S, 4, generator=gen) - 0.5).bfloat16()
+    A_log = torch.rand(H, generator=gen).mul(3).add(0.01).log()
+    dt_bias = torch.randn(H, generator=gen) * 0.5
+    nw = 1 + 0.1 * torch.randn(128, generator=gen)
+    return [t.to(DEV) for t in (w, A_log, dt_bias, nw)]
+
+
+def test_cq_invariant_layer_core(gdn):
+    """tests/test_qwen35_cq.py:71-89 through the fused layer (events.layer_core): query rows
+    perturbed by N(0,1) * 10 leave every content row bit-identical; an image group perturbed the
+    same way leaves every row whose output event precedes the group's first write bit-identical
+    (the queries of earlier or equal sigma and the content before it); the group's first image
+    output sees its last token."""
+    from cqgdn import events, layer
+
+    H, S = 16, 2048
+    plan = layer.cq_layer_plan(600, 160, image_groups=(64, 40), seed=8).to(DEV)
+    print(f"case CQ invariant, layer_core: {plan.hidden_length} rows", flush=True)
+    gen = torch.Generator().manual_seed(81)
+    params = _layer_params(H, gen)
+    proj = (torch.randn(plan.hidden_length, 4 * S + 2 * H, generator=gen) * 0.7).bfloat16()
+    n_c = plan.content_order.numel()
+
+    def run(p):
+        with torch.no_grad():
+            out = events.layer_core(p.to(DEV), *params, plan, heads=H)
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    base = run(proj)
+    changed = proj.clone()
+    changed[n_c:] += (torch.randn(changed[n_c:].shape, generator=gen) * 10).bfloat16()
+    after = run(changed)
+    assert torch.equal(base[:n_c], after[:n_c])
+    assert not torch.equal(base[n_c:], after[n_c:])
+    # the second image group (content rows written as one multi-token group)
+    ew, hidden = plan.event_write.cpu(), plan.hidden_event.cpu()
+    rows = _image_group_rows(plan, size=40)
+    first_write = int(torch.nonzero(torch.isin(ew, rows)).min())
+    keep = hidden < first_write
+    assert int(keep.sum()) > 100 and bool(keep[n_c:].any())  # content and queries on both sides
+    changed = proj.clone()
+    changed[rows] += (torch.randn(changed[rows].shape, generator=gen) * 10).bfloat16()
+    after = run(changed)
+    assert torch.equal(base[keep], after[keep])
+    assert not torch.equal(base[~keep], after[~keep])
+    changed = proj.clone()
+    changed[rows[-1]] += (torch.randn(changed[rows[-1]].shape, generator=gen) * 3).bfloat16()
+    after = run(changed)
+    assert float((base[rows[0]].float() - after[rows[0]].float()).abs().max()) > 1e-8
+
+
+def _image_group_rows(plan, size):
+    """Hidden rows of the multi-token group of ``size`` members: each such group's members are
+    read again right after the group is written, so its re-reads are one run of consecutive
+    events (runs of two groups are separated by the second group's writes)."""
+    ew, eq = plan.event_write.cpu(), plan.event_q.cpu()
+    n_c = plan.content_order.numel()
+    reread = ((ew == n_c) & (eq < n_c)).tolist()
+    runs, cur = [], []
+    for e, flag in enumerate(reread):
+        if flag:
+            cur.append(int(eq[e]))
+        elif cur:
+            runs.append(cur)
+            cur = []
+    if cur:
+        runs.append(cur)
+    rows = next(r for r in runs if len(r) == size)
+    return plan.content_order.cpu()[torch.tensor(rows)]
+
+
+def _restatement(plan, proj, H, gen):
+    """Output and projection/parameter gradients of layer_core and of the reference's layer code in
+    float64 on the CPU (oracle conv, recurrence and norm), from the same bf16 projection."""
+    from cqgdn import events, layer
+
+    S = H * 128
+    model = layer.GatedDeltaLayer(width=64, heads=H).double()
+    with torch.no_grad():
+        model.conv_weight.copy_(model.conv_weight.bfloat16().double())
+        model.dt_bias.copy_(torch.randn(H, generator=gen) * 0.5)
+        model.norm_weight.copy_(1 + 0.1 * torch.randn(128, generator=gen))
+    dout = (torch.randn(plan.hidden_length, S, generator=gen) * 0.1).bfloat16()
+    params = [model.conv_weight, model.A_log, model.dt_bias, model.norm_weight]
+    pd = proj.to(DEV).detach().requires_grad_()
+    dp = [model.conv_weight.detach().bfloat16().to(DEV).requires_grad_()] + \
+        [t.detach().float().to(DEV).requires_grad_() for t in params[1:]]
+    out = events.layer_core(pd, *dp, plan, heads=H)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    p64 = proj.double().requires_grad_()
+    rec = lambda q, k, v, g, b, p: O.recurrent_delta(q, k, v, g, b, p.event_bounds, normalize=True)
+    cv = lambda u, w, bounds: O.causal_conv1d(u, w, bounds)
+    ref = model.core(p64, plan, recurrence=rec, conv=cv, norm=O.gated_rms_norm, fused=False)
+    ref.backward(dout.double())
+    return (out, pd.grad, dp), (ref, p64.grad, params)
+
+
+def _compare_layer(got, want, H):
+    S = H * 128
+    (out, dproj, dp), (ref, rproj, params) = got, want
+    assert_close_bf16("out", out.detach().cpu(), ref.detach())
+    cols = {"d_qkv": slice(0, 3 * S), "d_z": slice(3 * S, 4 * S), "d_a": slice(4 * S, 4 * S + H),
+            "d_b": slice(4 * S + H, 4 * S + 2 * H)}
+    for name, sl in cols.items():
+        assert_close_bf16(name, dproj[:, sl].cpu(), rproj[:, sl])
+    for name, a, p in zip(("d_conv_weight", "d_A_log", "d_dt_bias", "d_norm_weight"), dp, params):
+        assert_close_bf16(name, a.grad.cpu(), p.grad)
+
+
+def test_layer_core_shared_hidden_rows(gdn):
+    """A two-branch plan built like ops/gated_delta_layout.py:66-83 (Bi_I+CQ_T): the generation
+    branch re-writes the prefix's hidden rows as its own content rows, so content_order repeats
+    rows; the projection gradient of such a row is the sum over its content rows."""
+    from cqgdn import layer
+
+    H = 16
+    plan = layer.two_branch_plan(260, 70, prefix=40, suffix=50, image_groups=(30,), seed=9)
+    order = plan.content_order
+    assert torch.unique(order).numel() < order.numel()
+    print(f"case layer core, shared hidden rows: {plan.hidden_length} rows, {order.numel()} content", flush=True)
+    gen = torch.Generator().manual_seed(91)
+    proj = (torch.randn(plan.hidden_length, 4 * H * 128 + 2 * H, generator=gen) * 0.7).bfloat16()
+    _compare_layer(*_restatement(plan, proj, H, gen), H)
+
+
+def test_layer_core_h32_and_column_sliced_projection(gdn):
+    """H = 32 through the fused layer, with the projection a column slice of a wider tensor (its row
+    stride is larger than its width): results equal the contiguous projection's."""
+    from cqgdn import events, layer
+
+    H, S = 32, 4096
+    P = 4 * S + 2 * H
+    plan = layer.cq_layer_plan(160, 40, image_groups=(20,), seed=10)
+    print(f"case layer core H=32: {plan.hidden_length} rows", flush=True)
+    gen = torch.Generator().manual_seed(101)
+    proj = (torch.randn(plan.hidden_length, P, generator=gen) * 0.7).bfloat16()
+    _compare_layer(*_restatement(plan, proj, H, gen), H)
+    # the same projection inside a wider tensor (row stride P + 72), against the contiguous one
+    params = _layer_params(H, gen)
+    wide = torch.zeros(plan.hidden_length, P + 72, dtype=torch.bfloat16)
+    wide[:, 24:24 + P] = proj
+    dout = (torch.randn(plan.hidden_length, S, generator=gen) * 0.1).bfloat16().to(DEV)
+    res = []
+    for src in (proj.to(DEV), wide.to(DEV)):
+        src = src.detach().requires_grad_()
+        p = src if src.shape[1] == P else src[:, 24:24 + P]
+        out = events.layer_core(p, *params, plan, heads=H)
+        out.backward(dout)
+        g = src.grad if src.shape[1] == P else src.grad[:, 24:24 + P]
+        res.append((out.detach(), g))
+    torch.cuda.synchronize()
+    assert torch.equal(res[0][0], res[1][0])
+    assert torch.equal(res[0][1], res[1][1])
+
+
+def test_layer_decode_step_h32(gdn):
+    """The layer's decode step at H = 32 against the float64 oracle step, two steps, N = 2."""
+    from cqgdn import events
+
+    N, H, K = 2, 32, 4
+    S, P = H * 128, 4 * H * 128 + 2 * H
+    print("case layer decode H=32", flush=True)
+    gen = torch.Generator().manual_seed(111)
+    w = (torch.rand(3 * S, K, generator=gen) - 0.5).bfloat16()
+    A_log = torch.rand(H, generator=gen).mul(3).add(0.01).log()
+    dt_bias = torch.randn(H, generator=gen) * 0.5
+    nw = 1 + 0.1 * torch.randn(128, generator=gen)
+    hist = (torch.randn(N, K - 1, 3 * S, generator=gen) * 0.7).bfloat16()
+    state = torch.randn(N, H, 128, 128, generator=gen) * 0.05
+    cache = {"conv": hist.to(DEV), "state": state.to(DEV)}
+    ref_hist, ref_state = hist.double(), state.double()
+    dev = [t.to(DEV) for t in (w, A_log, dt_bias, nw)]
+    for step in range(2):
+        proj = (torch.randn(N, 2, P, generator=gen) * 0.7).bfloat16()
+        out = events.layer_decode_step(proj.to(DEV), *dev, cache, heads=H)
+        torch.cuda.synchronize()
+        args = (proj[..., :3 * S], proj[..., 3 * S:4 * S].reshape(N, 2, H, 128), proj[..., 4 * S:4 * S + H],
+                proj[..., 4 * S + H:], w, A_log, dt_bias, nw)
+        ref_out, ref_hist, ref_state = O.layer_decode_step(*args, ref_hist, ref_state)
+        assert_close_bf16(f"out step {step}", out.cpu(), ref_out.reshape(N, 2, S))
+        assert torch.equal(cache["conv"].cpu().double(), ref_hist)
+        assert_close_bf16(f"state step {step}", cache["state"].cpu(), ref_state)

@@ -348,9 +348,16 @@ def test_l2norm_and_cumsum_kernels(gdn):
     assert_close_bf16("l2_bwd", gdn.l2_bwd(y, rstd, dy.to(DEV)).cpu(), xx.grad)
     g = torch.randn(1, 300, 4, generator=gen)
     bounds = (0, 10, 200, 300)
-    out = gdn.reverse_cumsum(g.to(DEV), bounds)
+    # the reference's head-first layout [B, H, T] (ops/gated_delta_net.py:77-87, :204)
+    out = gdn.reverse_cumsum(g.transpose(1, 2).contiguous().to(DEV), bounds)
     ref = O.chunk_local_cumsum(g.double(), bounds, reverse=True)
-    assert rel_l2(out, ref) < 1e-6
+    assert out.shape == (1, 4, 300)
+    assert rel_l2(out.transpose(1, 2), ref) < 1e-6
+    # unpacked batch: every row its own sequence
+    g2 = torch.randn(3, 4, 130, generator=gen)
+    out2 = gdn.reverse_cumsum(g2.to(DEV), None)
+    ref2 = torch.stack([O.chunk_local_cumsum(g2[i].T[None].double(), (0, 130), reverse=True)[0].T for i in range(3)])
+    assert rel_l2(out2, ref2) < 1e-6
 
 
 def test_forward_backward_bitwise_deterministic(gdn):

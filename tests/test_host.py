@@ -199,3 +199,30 @@ def test_event_plan_inverse_maps_against_brute_force():
     bad.event_write[bad.event_write == 5] = 4  # two writers of content row 4
     with pytest.raises(ValueError, match="written by more than one event"):
         events.event_plan(bad, 4, "cpu")
+
+
+def test_event_plan_fold_map_of_shared_hidden_rows():
+    """A two-branch plan (Bi_I+CQ_T, ops/gated_delta_layout.py:66-83) re-writes hidden rows
+    0 .. prefix-1 in its second branch: the fold map lists every distinct hidden row of
+    content_order with the content rows reading it (ascending), against a direct scan; plans
+    without shared rows carry no fold map; a query row may not be a content row."""
+    from cqgdn import events, layer
+
+    plan = layer.two_branch_plan(50, 12, prefix=10, suffix=15, image_groups=(6,), suffix_groups=(4,), seed=3)
+    ep = events.event_plan(plan, 4, "cpu")
+    t = {k: v.long() for k, v in ep.tensors.items()}
+    order = plan.content_order.tolist()
+    rows = sorted(set(order))
+    assert ep.cstruct.n_fold_rows == len(rows) and t["fold_rows"].tolist() == rows
+    for i, r in enumerate(rows):
+        assert t["fold_list"][t["fold_ptr"][i]:t["fold_ptr"][i + 1]].tolist() == [c for c, x in enumerate(order)
+                                                                                   if x == r]
+    assert [len([c for c in order if c == r]) for r in range(10)] == [2] * 10  # the prefix, twice
+    assert ep.covers_all and ep.content_bounds == (0, 50, 75)
+    single = events.event_plan(layer.cq_layer_plan(30, 5, image_groups=(4,), seed=1), 4, "cpu")
+    assert single.cstruct.n_fold_rows == 0
+    bad = layer.cq_layer_plan(20, 3, image_groups=(4,))
+    bad.query_source = bad.query_source.clone()
+    bad.query_source[0] = 2  # a query reading a content row's hidden row
+    with pytest.raises(ValueError, match="query rows must be distinct"):
+        events.event_plan(bad, 4, "cpu")

@@ -34,11 +34,20 @@ def _check(cond, msg):
         raise ProtocolError(msg)
 
 
-def simulate(n, seed, wait_count=None, wait_for_consumer=True):
-    """Run the hand-off for a document of n chunks; raise ProtocolError on a violation."""
+def simulate(n, seed, wait_count=None, wait_for_consumer=True, spin_limit=None, hold=None, poison_copy_out=True):
+    """Run the hand-off for a document of n chunks; raise ProtocolError on a violation.
+
+    ``spin_limit``: a loader's wait for the consumer gives up after that many polls (the kernel's
+    bounded wait); it then publishes the poison flag before refilling.  ``hold = (step, time)``
+    stalls the consumer at that step, so that waits do give up.  With a give-up the model checks
+    that nothing is silently wrong: a consumer step that read an overwritten stage is followed by
+    NaN states, and a copy-out of anything but its own chunk's outputs stores NaN
+    (``poison_copy_out=False`` drops the latter, which must be caught)."""
     rnd = random.Random(seed)
     slots = [{"part": [None, None], "scratch": None} for _ in range(STAGES)]
     flags = [0, 0, 0]  # loader 0, loader 1, consumer
+    poison = [False]  # flags[3]
+    gave_up = [False]
     inflight = [[], []]  # per loader: [finish time, on_retire] in issue order
     now = [0.0]
 
@@ -67,11 +76,23 @@ def simulate(n, seed, wait_count=None, wait_for_consumer=True):
                 _check(slots[y % STAGES]["part"][j] == y, f"loader {j} published chunk {y} before it landed")
                 flags[j] = y + 1
             if x >= STAGES:
-                if wait_for_consumer:
-                    yield lambda: flags[2] >= x - STAGES + 1
+                if wait_for_consumer and not (spin_limit and poison[0] and gave_up[0]):
+                    polls = [0]
+
+                    def ready(target=x - STAGES + 1, polls=polls):
+                        polls[0] += 1
+                        return flags[2] >= target or (spin_limit is not None and polls[0] > spin_limit)
+
+                    yield ready
+                    if flags[2] < x - STAGES + 1:  # gave up: poison first, then refill without waiting
+                        poison[0] = gave_up[0] = True
                 if j == 1 and x - STAGES < n:
                     got = slots[x % STAGES]["scratch"]
-                    _check(got == x - STAGES, f"copy-out of chunk {x - STAGES} read outputs of {got}")
+                    nan = poison_copy_out and poison[0]
+                    if got != x - STAGES and not nan:
+                        if spin_limit is None:
+                            _check(False, f"copy-out of chunk {x - STAGES} read outputs of {got}")
+                        _check(False, f"silently wrong copy-out of chunk {x - STAGES} ({got})")
                     for _ in range(OUT_STORES):
                         issue(j)
             if x < n:
@@ -82,13 +103,26 @@ def simulate(n, seed, wait_count=None, wait_for_consumer=True):
                     issue(j, done)
 
     def consumer():
+        ok, bad_state, seen_poison = True, False, False
         for tau in range(n):
             yield lambda: min(flags[0], flags[1]) >= tau + 1
+            if seen_poison:
+                ok = False  # the state turns to NaN
+            _check(ok or spin_limit is not None, "a wait gave up without a spin limit")
+            _check(not (bad_state and ok), f"state silently wrong at chunk {tau}")
             slot = slots[tau % STAGES]
-            _check(slot["part"] == [tau, tau], f"consumer read chunk {tau} before it landed: {slot['part']}")
+            intact = slot["part"] == [tau, tau]  # the operand reads, issued at the step's start
+            if spin_limit is None:
+                _check(intact, f"consumer read chunk {tau} before it landed: {slot['part']}")
+            seen_poison = poison[0]  # read after the operands, applied at the next step
+            if hold is not None and tau == hold[0]:
+                until = now[0] + hold[1]
+                yield lambda: now[0] >= until
             yield None  # computing
-            _check(slot["part"] == [tau, tau], f"chunk {tau} overwritten while the consumer read it")
-            slot["scratch"] = tau
+            if spin_limit is None:
+                _check(slot["part"] == [tau, tau], f"chunk {tau} overwritten while the consumer read it")
+            bad_state = bad_state or not intact
+            slot["scratch"] = tau if (ok and intact) else ("nan" if not ok else ("bad", tau))
             flags[2] = tau + 1
 
     waves = [consumer(), loader(0), loader(1)]
@@ -119,6 +153,7 @@ def simulate(n, seed, wait_count=None, wait_for_consumer=True):
     now[0] = float("inf")
     retire()
     _check(flags == [n, n, n], f"final counts {flags}")
+    return gave_up[0]
 
 
 @pytest.mark.parametrize("n", [0, 1, 2, 3, 4, 5, 6, 9, 17])
@@ -143,3 +178,18 @@ def test_refill_without_waiting_for_the_consumer_is_caught():
     with pytest.raises(ProtocolError):
         for seed in range(40):
             simulate(9, seed, wait_for_consumer=False)
+
+
+def test_loader_timeout_poisons_instead_of_corrupting():
+    """A loader whose wait for the consumer gives up publishes the poison flag before it refills a
+    stage: the consumer's later states and every later copy-out are NaN, never silently wrong."""
+    gave_up = 0
+    for seed in range(60):
+        gave_up += simulate(12, seed, spin_limit=3, hold=(2, 3000.0))
+    assert gave_up > 0  # the hold made waits give up
+
+
+def test_copy_out_without_poison_check_is_caught():
+    with pytest.raises(ProtocolError, match="silently wrong"):
+        for seed in range(60):
+            simulate(12, seed, spin_limit=3, hold=(2, 3000.0), poison_copy_out=False)
