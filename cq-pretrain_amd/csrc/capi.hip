@@ -3,6 +3,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "cqgdn.h"
@@ -48,6 +49,38 @@ int check_common(int64_t T, int H, int64_t n_chunks, int n_docs, const int32_t* 
   if (n_chunks > 0 && (!chunk_table || !doc_chunk)) return fail(CQGDN_EINVAL, "chunk_table/doc_chunk are null");
   if (n_chunks > INT32_MAX / 2 || (int64_t)n_chunks * H > 2147483647LL)
     return fail(CQGDN_EUNSUPPORTED, "too many chunks (%lld)", (long long)n_chunks);
+  return CQGDN_OK;
+}
+
+int fwd_impl(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T, int H,
+             const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
+             unsigned flags, const float* initial_state, float* final_state, void* o, void* workspace,
+             size_t workspace_bytes, void* stream);
+
+// The workspace of cqgdn_fwd_static: one array per GPU, held until the process
+// ends.  Host code never uses its name as an address (on the host it only
+// stands for the symbol): each device's address is looked up once, with that
+// device current, and kept in g_static_ws.
+__device__ __align__(256) uint8_t scratch[CQGDN_STATIC_WORKSPACE_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_static_mu;
+void* g_static_ws[kMaxDevices] = {};
+
+int static_workspace(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(CQGDN_EHIP, "cqgdn_fwd_static: no current HIP device (or device %d >= %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_static_mu);
+  if (!g_static_ws[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(CQGDN_EHIP, "cqgdn_fwd_static: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_static_ws[dev] = p;
+  }
+  *out = g_static_ws[dev];
   return CQGDN_OK;
 }
 
@@ -117,6 +150,38 @@ int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const
               const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
               unsigned flags, const float* initial_state, float* final_state, void* o, void* workspace,
               size_t workspace_bytes, void* stream) {
+  return fwd_impl(q, k, v, g, beta, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags, initial_state,
+                  final_state, o, workspace, workspace_bytes, stream);
+}
+
+int cqgdn_fwd_static(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T,
+                     int H, const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs,
+                     float scale, unsigned flags, const float* initial_state, float* final_state, void* o,
+                     void* stream) {
+  if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
+  if (flags & CQGDN_TRAINING)
+    return fail(CQGDN_EINVAL, "cqgdn_fwd_static is an inference forward: its workspace does not outlive the call, "
+                              "so it cannot feed cqgdn_bwd (CQGDN_TRAINING)");
+  const size_t need = cqgdn_fwd_workspace_size(T, H, n_chunks);
+  if (need > (size_t)CQGDN_STATIC_WORKSPACE_BYTES)
+    return fail(CQGDN_EINVAL,
+                "T=%lld events x H=%d heads need a %zu-byte workspace, more than the %zu-byte static one: use "
+                "cqgdn_fwd with a caller workspace",
+                (long long)T, H, need, (size_t)CQGDN_STATIC_WORKSPACE_BYTES);
+  void* ws = nullptr;
+  if (T > 0)
+    if (const int e = static_workspace(&ws)) return e;
+  return fwd_impl(q, k, v, g, beta, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags, initial_state,
+                  final_state, o, ws, need, stream);
+}
+
+}  // extern "C"
+
+namespace {
+int fwd_impl(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T, int H,
+             const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
+             unsigned flags, const float* initial_state, float* final_state, void* o, void* workspace,
+             size_t workspace_bytes, void* stream) {
   if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
   if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING | CQGDN_PRECISE))
     return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
@@ -160,6 +225,9 @@ int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const
   launch_fwd(a, (hipStream_t)stream);
   return check_launch("cqgdn_fwd");
 }
+}  // namespace
+
+extern "C" {
 
 int cqgdn_bwd(const void* v, const float* g, const float* beta, const void* dout, int64_t T, int H,
               const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,

@@ -95,6 +95,25 @@ int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const
               size_t workspace_bytes, void* stream);
 
 /*
+ * cqgdn_fwd for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The same forward, with the same arguments minus the workspace: it
+ * uses the library's own static workspace of CQGDN_STATIC_WORKSPACE_BYTES per GPU
+ * (a file-scope device array, held until the process ends) and calls no allocator.
+ * It rejects with CQGDN_EINVAL any call whose cqgdn_fwd_workspace_size exceeds that
+ * (at H = 16 and one document: up to 1,911 events), and CQGDN_TRAINING (the workspace does not
+ * outlive the call, so it cannot feed cqgdn_bwd).  Every call on one GPU shares
+ * that GPU's workspace, which keeps the last call's contents: calls that overlap
+ * on one GPU (two streams, or two threads) race and must be serialized by the
+ * caller.  Nothing in the workspace needs to start at zero.
+ */
+#define CQGDN_STATIC_WORKSPACE_BYTES (64u << 20)
+int cqgdn_fwd_static(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T,
+                     int H, const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs,
+                     float scale, unsigned flags, const float* initial_state, float* final_state, void* o,
+                     void* stream);
+
+/*
  * Chunked GDN backward from the forward workspace (which must come from a
  * cqgdn_fwd call with CQGDN_TRAINING on the same inputs).  Replaces the
  * backward op chain of _Delta.backward (ops/gated_delta_net.py:188-214:

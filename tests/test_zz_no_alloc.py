@@ -1,0 +1,74 @@
+"""cqgdn_fwd_static, the forward that allocates nothing (include/cqgdn.h), through the C ABI.
+
+It must give exactly what cqgdn_fwd gives with a caller workspace (same kernels, same inputs),
+on two calls in a row -- the second smaller, so it runs over what the first left in the shared
+static workspace -- and reject what it cannot serve: a workspace larger than its static one, and a
+training forward."""
+
+import ctypes
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def _run(gdn, lib, xs, bounds, static, initial_state=None):
+    from cqgdn import _lib
+
+    q, k, v, g, b = (x.to(DEV).contiguous() for x in xs)
+    T, H = q.shape[1], q.shape[2]
+    _, table, doc = gdn.device_metadata(bounds, DEV)
+    nc, nd = table.shape[0], len(bounds) - 1
+    o = torch.empty_like(v)
+    state = torch.empty(nd, H, 128, 128, dtype=torch.float32, device=DEV)
+    init = None if initial_state is None else initial_state.to(DEV).contiguous()
+    flags = _lib.NORMALIZE | _lib.PRECISE
+    P = gdn._ptr
+    common = (P(q), P(k), P(v), P(g), P(b), T, H, P(table), nc, P(doc), nd, 128 ** -0.5, flags, P(init), P(state),
+              P(o))
+    if static:
+        rc = lib.cqgdn_fwd_static(*common, gdn._stream(q.device))
+    else:
+        ws = torch.empty(lib.cqgdn_fwd_workspace_size(T, H, nc), dtype=torch.uint8, device=DEV)
+        rc = lib.cqgdn_fwd(*common, P(ws), ws.numel(), gdn._stream(q.device))
+    assert rc == 0, lib.cqgdn_last_error().decode()
+    torch.cuda.synchronize()
+    return o, state
+
+
+def test_static_forward_matches_workspace_forward(gdn):
+    from cqgdn import _lib, synthetic
+
+    lib = _lib.lib()
+    cases = [(1900, (0, 700, 1900), 16, None), (300, (0, 129, 300), 16, 0.05)]  # the second one smaller
+    for T, bounds, H, s0 in cases:
+        print(f"case static forward T={T} bounds={bounds} H={H}", flush=True)
+        xs = synthetic.make_inputs(T, H, 128, seed=T)
+        init = None if s0 is None else torch.randn(len(bounds) - 1, H, 128, 128,
+                                                   generator=torch.Generator().manual_seed(5)) * s0
+        o_ws, st_ws = _run(gdn, lib, xs, bounds, False, init)
+        o_st, st_st = _run(gdn, lib, xs, bounds, True, init)
+        assert torch.equal(o_ws, o_st)
+        assert torch.equal(st_ws, st_st)
+        assert torch.isfinite(o_st.float()).all()
+
+
+def test_static_forward_rejects_what_it_cannot_serve(gdn):
+    from cqgdn import _lib, synthetic
+
+    lib = _lib.lib()
+    T, H = 2048, 16  # needs more than the 64 MiB static workspace
+    q, k, v, g, b = (x.to(DEV) for x in synthetic.make_inputs(T, H, 128, seed=1))
+    _, table, doc = gdn.device_metadata((0, T), DEV)
+    o = torch.empty_like(v)
+    P = gdn._ptr
+    assert lib.cqgdn_fwd_workspace_size(T, H, table.shape[0]) > _lib.STATIC_WORKSPACE_BYTES
+    rc = lib.cqgdn_fwd_static(P(q), P(k), P(v), P(g), P(b), T, H, P(table), table.shape[0], P(doc), 1,
+                              128 ** -0.5, _lib.NORMALIZE | _lib.PRECISE, None, None, P(o), None)
+    assert rc == _lib.EINVAL and b"static one" in lib.cqgdn_last_error()
+    rc = lib.cqgdn_fwd_static(P(q), P(k), P(v), P(g), P(b), 64, H, P(table), 1, P(doc), 1, 128 ** -0.5,
+                              _lib.NORMALIZE | _lib.TRAINING, None, None, P(o), None)
+    assert rc == _lib.EINVAL and b"TRAINING" in lib.cqgdn_last_error()
