@@ -187,6 +187,9 @@ int fwd_impl(const void* q, const void* k, const void* v, const float* g, const 
     return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
   if ((flags & CQGDN_TRAINING) && (flags & CQGDN_PRECISE))
     return fail(CQGDN_EINVAL, "CQGDN_PRECISE is an inference forward: it cannot be combined with CQGDN_TRAINING");
+  if ((flags & CQGDN_TRAINING) && (initial_state || final_state))
+    return fail(CQGDN_EINVAL, "a CQGDN_TRAINING forward starts from a zero state and returns no final state "
+                              "(as the reference's training adapter, ops/gated_delta_net.py:231-232)");
   if (T == 0) {
     if (final_state && n_docs > 0) {
       // every document is empty: its final state is its initial state (or zero)

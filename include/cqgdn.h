@@ -87,7 +87,8 @@ int cqgdn_bwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets
  *   o              : [T][H][D] bf16 output (time-first)
  *   workspace      : >= cqgdn_fwd_workspace_size() bytes, 256-byte aligned
  *   flags          : CQGDN_NORMALIZE | (CQGDN_TRAINING or CQGDN_PRECISE); the reference's
- *                    prefill (ops/gated_delta_net.py:292-311) maps to NORMALIZE | PRECISE
+ *                    prefill (ops/gated_delta_net.py:292-311) maps to NORMALIZE | PRECISE.
+ *                    A CQGDN_TRAINING forward takes no initial_state and no final_state.
  */
 int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T, int H,
               const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,

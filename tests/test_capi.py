@@ -57,7 +57,8 @@ def test_workspace_offsets_are_aligned_and_disjoint(lib, T, H, nc):
         offs = list(offs_fn(T, H, nc).values())
         assert len(offs) == n and offs[0] == 0
         assert all(o % 256 == 0 for o in offs)
-        assert all(b > a for a, b in zip(offs, offs[1:])) and total > offs[-1]
+        # in order; the segment-map buffers are empty when no document has two segments
+        assert all(b >= a for a, b in zip(offs, offs[1:])) and total >= offs[-1]
     # the largest per-chunk buffer is a [D][D] bf16 state per chunk and head
     offs = _lib.fwd_offsets(T, H, nc)
     assert offs["vnT"] - offs["hT"] >= nc * H * 128 * 128 * 2
@@ -134,3 +135,14 @@ def test_layer_decode_step_arguments(lib):
     assert step(stride=4 * 16 * 128) == _lib.EINVAL  # no room for the a, b columns
     assert b"proj_stride" in lib.cqgdn_last_error()
     assert step(ptr=ctypes.c_void_p(258)) == _lib.EINVAL  # misaligned projection rows
+
+
+def test_training_forward_rejects_states(lib):
+    """A CQGDN_TRAINING forward starts from a zero state and returns none (the reference's training
+    adapter rejects both, ops/gated_delta_net.py:231-232); the check comes before any launch."""
+    from cqgdn import _lib
+
+    dummy = ctypes.c_void_p(16)
+    rc = lib.cqgdn_fwd(dummy, dummy, dummy, dummy, dummy, 64, 4, dummy, 1, dummy, 1, 0.088, _lib.TRAINING, dummy, None,
+                       dummy, dummy, 1 << 30, None)
+    assert rc == _lib.EINVAL and b"zero state" in lib.cqgdn_last_error()
