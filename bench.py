@@ -10,16 +10,18 @@ and state; timing follows the reference's GDN benchmark (warm-up, then
 synchronize around the timed loop, scripts/benchmark_gdn.py:51-56).
 
 Printed: one JSON line with the contract keys, plus
-  roofline      the dominant kernel priced against its bound (HIP events on the
-                stream it runs on, recorded inside the timed region)
+  roofline      the dominant kernel priced against bf16 MFMA (HIP events on the
+                stream it runs on, recorded inside the timed region), with its HBM rate beside
   cpu_baseline  the fp32 chunked torch oracle on this host's cores (a bounded
-                sample: one config-2 fwd+bwd)
+                sample: one config-2 fwd+bwd; rows: one config-0 forward and the
+                config-4 decode step)
   extra         config-1 and config-3 fwd+bwd, per-kernel table (MFMA / HBM
                 fractions), the whole GatedDelta layer at width 2048 (content 2048 and
                 8192 on image-CQ plans, beside the reference's published Ascend 910B
                 medians), prefill, and the decode step (B=64, 256 steps, GB/s)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+       python bench.py --profile | --profile-layer | --profile-decode   (profiler workloads)
 """
 
 from __future__ import annotations
@@ -57,6 +59,9 @@ def parse_args():
     ap.add_argument("--profile-layer", action="store_true",
                     help="profiler workload only: warmup + steps fused fwd+bwd steps of the width-2048 "
                          "layer at content 2048; prints no JSON")
+    ap.add_argument("--profile-decode", action="store_true",
+                    help="profiler workload only: the config-4 decode loop (B=64, --decode-steps steps over "
+                         "8 rotated layer states), then a plain copy kernel of known size; prints no JSON")
     return ap.parse_args()
 
 
@@ -120,14 +125,17 @@ def traffic_for(kernel, sha):
     return None
 
 
-def cpu_baseline(torch):
-    """fp32 chunked torch oracle, fwd+bwd via autograd, on this host's cores: one config-2 step."""
+def cpu_baseline(torch, decode_steps=8):
+    """The CPU rows of the plan (fp32 torch oracle on this host's cores, one thread per core the
+    process may use): config 2 fwd+bwd via autograd (the reported baseline, same unit as
+    ``value``), plus the config 0 forward and the config 4 decode step (``rows``)."""
     from cqgdn import synthetic
     from oracle import gdn_oracle as O
 
     cores = len(os.sched_getaffinity(0))
     prev = torch.get_num_threads()
     torch.set_num_threads(cores)
+    rows = {}
     try:
         T, mask, bounds = synthetic.config_events(2, seed=0)
         xs = [x.float().requires_grad_() for x in synthetic.make_inputs(T, H, D, seed=2, readonly=mask)]
@@ -136,12 +144,39 @@ def cpu_baseline(torch):
         y = O.chunk_delta(*xs, bounds, normalize=True)
         y.backward(do)
         sec = time.perf_counter() - t0
+        del xs, y, do
+        # config 0: forward only, T=2048, zero initial state, final state returned
+        T0, _, b0 = synthetic.config_events(0)
+        x0 = [x.float() for x in synthetic.make_inputs(T0, H, D, seed=0)]
+        with torch.no_grad():
+            O.chunk_delta(*x0, b0, normalize=True, output_final_state=True)  # warm-up
+            t0 = time.perf_counter()
+            O.chunk_delta(*x0, b0, normalize=True, output_final_state=True)
+            rows["config0_fwd_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+        # config 4: the per-step recurrence (models/decoding.py:71-77) at B=64, H=16, fp32 state
+        gen = torch.Generator().manual_seed(4)
+        n = 64
+        state = torch.randn(n, H, D, D, generator=gen) * 0.02
+        q = O.l2norm(torch.randn(n, 1, H, D, generator=gen))
+        k = O.l2norm(torch.randn(n, 1, H, D, generator=gen))
+        v = torch.randn(n, 1, H, D, generator=gen)
+        g = -torch.nn.functional.softplus(torch.randn(n, 1, H, generator=gen))
+        b = torch.randn(n, 1, H, generator=gen).sigmoid()
+        with torch.no_grad():
+            O.decode_step(q, k, v, g, b, state)  # warm-up
+            t0 = time.perf_counter()
+            for _ in range(decode_steps):
+                O.decode_step(q, k, v, g, b, state)
+            rows["config4_decode_us_per_step"] = round((time.perf_counter() - t0) / decode_steps * 1e6, 1)
     finally:
         torch.set_num_threads(prev)
     return dict(value=round(sec * 1e3, 1), unit="ms/layer", cores=cores, kind="port",
                 sample="one fwd+bwd of config 2 (T=9216, H=16, d=128): oracle/gdn_oracle.chunk_delta in fp32 "
                        "(chunk 64) with torch autograd for the backward, "
-                       f"torch.set_num_threads({cores})")
+                       f"torch.set_num_threads({cores}); rows: one config-0 forward (T=2048, final state) and "
+                       f"the mean of {decode_steps} config-4 decode steps (B=64, H=16, fp32 state, "
+                       "oracle/gdn_oracle.decode_step), same threads",
+                rows=rows)
 
 
 def decode_case(gdn, _lib, workmodel, torch, device, steps):
@@ -191,34 +226,45 @@ def layer_setup(torch, device, content, queries):
         x.grad = None
         y = model(x, plan, fused=fused)
         (y * upstream).sum().backward()
+        return dict(y=y.detach().float(), dx=x.grad.detach().float(),
+                    dw=model.in_proj_all.weight.grad.detach().float())
 
     return plan, step
 
 
 def layer_case(torch, device, content, queries, iterations=12):
-    """The layer of ``layer_setup``: 3 warm-up steps, then the median of ``iterations`` fwd+bwd
-    steps, each bracketed by synchronize."""
+    """The layer of ``layer_setup`` measured as the reference's layer benchmark does
+    (scripts/benchmark_gdn.py:44-64): 3 warm-up steps, peak-memory statistics reset, the median
+    of ``iterations`` fwd+bwd steps (each bracketed by synchronize), the peak allocated bytes
+    (model, inputs, activations and workspaces of this layer: what the earlier cases of the run
+    still hold is subtracted, as the reference measures in a process of its own), and the relative
+    RMS of y, dx and the input-projection gradient dw between the two paths."""
+    base = torch.cuda.memory_allocated()  # held by the earlier cases: not the layer's
     plan, layer_step = layer_setup(torch, device, content, queries)
 
     def timed(fused):
-        def step():
-            layer_step(fused)
-
         for _ in range(3):
-            step()
+            layer_step(fused)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
         durations = []
         for _ in range(iterations):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            step()
+            out = layer_step(fused)
             torch.cuda.synchronize()
             durations.append((time.perf_counter() - t0) * 1e3)
-        return round(statistics.median(durations), 4)
+        return round(statistics.median(durations), 4), torch.cuda.max_memory_allocated() - base, out
 
     # fused: everything between the projections in the fused kernels (events.layer_core);
     # torch_glue: the reference's torch code around the hip delta, conv and gated norm
+    ms_f, peak_f, out_f = timed(True)
+    ms_g, peak_g, out_g = timed(False)
+    rel = {name: round(float((out_f[name] - out_g[name]).square().mean().sqrt()
+                             / out_f[name].square().mean().sqrt().clamp_min(1e-12)), 7) for name in out_f}
     return dict(content_tokens=content, query_tokens=queries, events=len(plan.event_q),
-                median_ms=timed(True), torch_glue_median_ms=timed(False))
+                median_ms=ms_f, torch_glue_median_ms=ms_g, peak_bytes=peak_f, torch_glue_peak_bytes=peak_g,
+                relative_rms_fused_vs_torch_glue=rel)
 
 
 def layer_decode_case(torch, device, N, iterations=200):
@@ -260,6 +306,11 @@ def profile_workload(torch, step, steps):
         step()
         torch.cuda.synchronize()
         log(f"profile step {i} done")
+    copy_workload(torch)
+
+
+def copy_workload(torch):
+    """3 plain device copies of COPY_BYTES (read and written): the scale of the byte counters."""
     src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda:0")
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -282,6 +333,12 @@ def main():
     device = "cuda:0"
     sha = _lib.sha256()
 
+    if args.profile_decode:
+        log("config 4 decode (profile)")
+        r = decode_case(gdn, _lib, workmodel, torch, device, args.decode_steps)
+        log(f"decode: {r['kernel_us']} us per step by events; copy kernel next")
+        copy_workload(torch)
+        return
     if args.profile_layer:
         _, layer_step = layer_setup(torch, device, 2048, 1675)
         for i in range(args.warmup + args.steps):
@@ -312,11 +369,14 @@ def main():
     ms = elapsed / args.steps * 1e3
     launch_s = statistics.mean(timer.ms) * 1e-3
     flops, nbytes = workmodel.kernel_work(dominant, bounds, H)
-    roof = workmodel.roofline(dominant, flops, nbytes, launch_s)
-    roof = dict(kernel=dominant, bound=roof["bound"], achieved=round(roof["achieved"], 2), peak=roof["peak"],
-                unit=roof["unit"], frac=round(roof["frac"], 4), traffic=traffic_for(dominant, sha),
-                algorithmic_bytes=nbytes, algorithmic_flops=int(flops), launch_us=round(launch_s * 1e6, 2),
-                launches=len(timer.ms))
+    # the chunk kernels are dense contractions priced against bf16 MFMA; the HBM figures beside
+    roof = dict(kernel=dominant, bound="mfma", achieved=round(flops / launch_s / 1e12, 2),
+                peak=workmodel.PEAK_BF16_FLOPS / 1e12, unit="TFLOP/s",
+                frac=round(flops / launch_s / workmodel.PEAK_BF16_FLOPS, 4), traffic=traffic_for(dominant, sha),
+                algorithmic_flops=int(flops), algorithmic_bytes=nbytes,
+                hbm_achieved_gbps=round(nbytes / launch_s / 1e9, 1),
+                hbm_frac=round(nbytes / launch_s / workmodel.PEAK_HBM_BYTES, 4),
+                launch_us=round(launch_s * 1e6, 2), launches=len(timer.ms))
     total_flops = sum(workmodel.kernel_work(k, bounds, H)[0]
                       for k in workmodel.FWD_KERNELS + workmodel.BWD_KERNELS)
 

@@ -96,13 +96,3 @@ def decode_bytes(n_seq, heads, events=1, d=D):
     """HBM bytes of one ``recurrent`` launch over n_seq sequences of ``events`` events."""
     per = 2 * d * d * 4 + events * (3 * d * 2 + 2 * 4 + d * 2)
     return n_seq * heads * per
-
-
-def roofline(kernel, flops, nbytes, seconds):
-    """Bound, achieved rate and fraction of peak for one launch that took ``seconds``."""
-    t_mfma, t_hbm = flops / PEAK_BF16_FLOPS, nbytes / PEAK_HBM_BYTES
-    if t_mfma >= t_hbm:
-        return dict(bound="mfma", achieved=flops / seconds / 1e12, peak=PEAK_BF16_FLOPS / 1e12, unit="TFLOP/s",
-                    frac=flops / seconds / PEAK_BF16_FLOPS)
-    return dict(bound="hbm", achieved=nbytes / seconds / 1e9, peak=PEAK_HBM_BYTES / 1e9, unit="GB/s",
-                frac=nbytes / seconds / PEAK_HBM_BYTES)

@@ -330,3 +330,50 @@ def test_layer_decode_step_h32(gdn):
         assert_close_bf16(f"out step {step}", out.cpu(), ref_out.reshape(N, 2, S))
         assert torch.equal(cache["conv"].cpu().double(), ref_hist)
         assert_close_bf16(f"state step {step}", cache["state"].cpu(), ref_state)
+
+
+def test_whole_layer_at_benchmark_plan_matches_float64_recurrence(gdn):
+    """The fused layer at the first row of the reference's layer benchmark (scripts/benchmark_gdn.py:34-64):
+    width 2048, content 2048 with 1675 CQ queries and two image groups -- the 4221-event image-CQ plan
+    bench.py times -- against the same bf16 layer run by the reference's torch code whose recurrence is
+    the float64 chunked oracle on the CPU: y, dx and the input-projection gradient within 2e-2."""
+    from cqgdn import layer
+
+    print("case whole layer at the benchmark plan: content 2048, 1675 queries, 4221 events", flush=True)
+    torch.manual_seed(872)
+    model = layer.GatedDeltaLayer().to(DEV, torch.bfloat16)
+    model.A_log.data = model.A_log.data.float()
+    model.norm_weight.data = model.norm_weight.data.float()
+    plan = layer.cq_layer_plan(2048, 1675).to(DEV)
+    assert len(plan.event_q) == 4221
+    gen = torch.Generator().manual_seed(873)
+    x = torch.randn(plan.hidden_length, 1, 2048, generator=gen).bfloat16().to(DEV)
+    up = (torch.randn(plan.hidden_length, 1, 2048, generator=gen) / 100).bfloat16().to(DEV)
+
+    def run(recurrence):
+        model.zero_grad(set_to_none=True)
+        xx = x.clone().requires_grad_()
+        y = model(xx, plan, recurrence=recurrence)
+        (y * up).sum().backward()
+        torch.cuda.synchronize()
+        return y.detach().float().cpu(), xx.grad.float().cpu(), model.in_proj_all.weight.grad.float().cpu()
+
+    def oracle(q, k, v, g, b, p):
+        ins = [t.detach().double().cpu().requires_grad_() for t in (q, k, v, g, b)]
+        out = O.chunk_delta(*ins, p.event_bounds, normalize=True)
+
+        class Bridge(torch.autograd.Function):  # float64 CPU recurrence inside the bf16 GPU graph
+            @staticmethod
+            def forward(ctx, *dev_ins):
+                return out.detach().to(q.device, q.dtype)
+
+            @staticmethod
+            def backward(ctx, dy):
+                grads = torch.autograd.grad(out, ins, dy.double().cpu())
+                return tuple(gr.to(t.device, t.dtype) for gr, t in zip(grads, (q, k, v, g, b)))
+
+        return Bridge.apply(q, k, v, g, b)
+
+    got, want = run(None), run(oracle)
+    for name, a, b in zip(("y", "dx", "dW_in"), got, want):
+        assert_close_bf16(name, a, b.double())
