@@ -201,7 +201,27 @@ def decode_case(gdn, _lib, workmodel, torch, device, steps):
         sec = (time.perf_counter() - t0) / steps
     nbytes = workmodel.decode_bytes(n, H)
     kern = statistics.mean(t.ms) * 1e-3
+    # the same loop captured once in a HIP graph and replayed: what a serving loop pays per step
+    # without a Python call and a ctypes round trip per launch (the step records no memset)
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(layers):
+            gdn.recurrent(q, k, v, g, b, states[i], out)
+    torch.cuda.current_stream().wait_stream(side)
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            gdn.recurrent(q, k, v, g, b, states[i % layers], out)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    graph.replay()
+    torch.cuda.synchronize()
+    gsec = (time.perf_counter() - t0) / steps
     return dict(us_per_step=round(sec * 1e6, 2), gbps=round(nbytes / sec / 1e9, 1),
+                graph_us_per_step=round(gsec * 1e6, 2), graph_gbps=round(nbytes / gsec / 1e9, 1),
+                graph_hbm_frac=round(nbytes / gsec / workmodel.PEAK_HBM_BYTES, 4),
                 kernel_us=round(kern * 1e6, 2), kernel_gbps=round(nbytes / kern / 1e9, 1),
                 kernel_hbm_frac=round(nbytes / kern / workmodel.PEAK_HBM_BYTES, 4),
                 bytes_per_step=nbytes, working_set_mb=round(layers * n * H * D * D * 4 / 1e6, 1))

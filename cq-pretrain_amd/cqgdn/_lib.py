@@ -14,7 +14,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().with_name("libcqgdn.so")
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
-NORMALIZE, TRAINING, PRECISE = 1, 2, 4
+NORMALIZE, TRAINING, PRECISE, NO_OUTPUT = 1, 2, 4, 8
 STATIC_WORKSPACE_BYTES = 64 << 20  # CQGDN_STATIC_WORKSPACE_BYTES
 FWD_BUFFERS, BWD_BUFFERS = 12, 6
 FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "UT", "KgT", "hT", "vnT", "vscale")

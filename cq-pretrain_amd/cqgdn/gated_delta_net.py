@@ -5,9 +5,13 @@ functions (``initialize``, ``call``, ``CALLS``, ``host_bounds``, ``chunk_indices
 ``device_metadata``, ``reverse_cumsum``, ``delta``, ``prefill``, ``recurrent``,
 ``gated_norm``, ``conv``, ``provenance``) with the same argument meaning, layouts
 and error behaviour.  The device work runs in hand-written gfx950 HIP kernels of
-``libcqgdn.so`` (C ABI in include/cqgdn.h), enqueued on the current stream; the
-chunked forward always keeps w, h and v_new for the backward (the reference's
-``cached`` mode), so the serial state scan never runs twice.
+``libcqgdn.so`` (C ABI in include/cqgdn.h), enqueued on the current stream.  Two
+modes, as the reference's (``DELTA_HIP_MODE``, read at import like
+``DELTA_ASCENDC_MODE``, ops/gated_delta_net.py:20): ``cached`` (the default here) keeps
+the forward's workspace (w, h, v_new and the rest) for the backward, so the serial
+state scan runs once; ``fused`` keeps only the inputs between the forward and the
+backward, which rebuilds the workspace (chunk preparation and state scan again)
+before it runs, trading that time for the workspace's memory across layers.
 
 PyTorch only supplies device memory and streams.  Every contract violation raises
 ``ValueError``/``NotImplementedError`` before any launch, like the reference.
@@ -31,10 +35,10 @@ _INITIALIZED = False
 
 
 def initialize():
-    """Load libcqgdn and check the device (ops/gated_delta_net.py:24-59)."""
+    """Load libcqgdn and check the device and the mode (ops/gated_delta_net.py:24-59)."""
     global _INITIALIZED
-    if MODE != "cached":
-        raise ValueError(f"Unknown DELTA_HIP_MODE={MODE}: the hip backend always keeps w/h/v_new")
+    if MODE not in ("fused", "cached"):
+        raise ValueError(f"Unknown DELTA_HIP_MODE={MODE}")
     _lib.lib()
     if torch.cuda.is_available():
         arch = torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName
@@ -225,17 +229,18 @@ def device_metadata(bounds, device):
 
 
 def _flatten(q, k, v, g, beta, bounds):
-    """Packed [1,T,...] views; unpacked batches become one document per row."""
+    """Packed [1,T,...] views; unpacked batches become one document per row.  q, k, v in bf16, the
+    kernels' operand type (fp16 inputs are rounded to it: bf16 keeps every fp16 magnitude in range)."""
     b, t = q.shape[0], q.shape[1]
     if bounds is None:
         bounds = tuple(range(0, b * t + 1, t)) if t > 0 else (0,) * (b + 1)
-    q, k, v = (x.reshape(1, b * t, *x.shape[2:]).contiguous() for x in (q, k, v))
+    q, k, v = (x.reshape(1, b * t, *x.shape[2:]).to(torch.bfloat16).contiguous() for x in (q, k, v))
     g, beta = (x.reshape(1, b * t, x.shape[-1]).float().contiguous() for x in (g, beta))
     return q, k, v, g, beta, bounds
 
 
 def _forward(q, k, v, g, beta, bounds, normalize, scale, training, initial_state=None, want_state=False,
-             precise=False):
+             precise=False, output=True):
     t, h = q.shape[1], q.shape[2]
     if q.shape[0] != 1 or bounds[0] != 0 or bounds[-1] != t:
         raise ValueError("packed forward needs batch 1 and bounds (0, ..., T) covering every event")
@@ -247,10 +252,10 @@ def _forward(q, k, v, g, beta, bounds, normalize, scale, training, initial_state
     cu, table, doc = device_metadata(bounds, str(q.device))
     n_chunks, n_docs = table.shape[0], len(bounds) - 1
     ws = torch.empty(_lib.lib().cqgdn_fwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=q.device)
-    o = torch.empty_like(v)
+    o = torch.empty_like(v) if output else None
     state = torch.empty(n_docs, h, 128, 128, dtype=torch.float32, device=q.device) if want_state else None
     flags = (_lib.NORMALIZE if normalize else 0) | (_lib.TRAINING if training else 0) | \
-        (_lib.PRECISE if precise else 0)
+        (_lib.PRECISE if precise else 0) | (0 if output else _lib.NO_OUTPUT)
     call("cqgdn_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), t, h, _ptr(table), n_chunks, _ptr(doc),
          n_docs, float(scale), flags, _ptr(initial_state), _ptr(state), _ptr(o), _ptr(ws), ws.numel(),
          _stream(q.device))
@@ -264,13 +269,21 @@ class _Delta(torch.autograd.Function):
         ctx.shapes = [x.shape for x in (q, k, v, g, beta)]
         qf, kf, vf, gf, bf, bounds = _flatten(q, k, v, g, beta, bounds)
         o, _, ws = _forward(qf, kf, vf, gf, bf, bounds, normalize, scale, training=True)
-        ctx.save_for_backward(vf, gf, bf, ws)
+        ctx.mode = MODE
+        if MODE == "fused":  # the inputs only: the backward rebuilds the workspace
+            ctx.save_for_backward(qf, kf, vf, gf, bf)
+        else:
+            ctx.save_for_backward(vf, gf, bf, ws)
         ctx.bounds, ctx.scale, ctx.normalize = bounds, scale, normalize
-        return o.reshape(v.shape)
+        return o.reshape(v.shape).to(v.dtype)
 
     @staticmethod
     def backward(ctx, dy):
-        v, g, beta, ws = ctx.saved_tensors
+        if ctx.mode == "fused":
+            q, k, v, g, beta = ctx.saved_tensors
+            _, _, ws = _forward(q, k, v, g, beta, ctx.bounds, ctx.normalize, ctx.scale, training=True, output=False)
+        else:
+            v, g, beta, ws = ctx.saved_tensors
         grads = _backward(v, g, beta, ws, dy, ctx.bounds, ctx.normalize, ctx.scale)
         grads = [x.reshape(shape).to(dtype) for x, shape, dtype in zip(grads, ctx.shapes, ctx.input_dtypes)]
         return *grads, None, None, None
@@ -308,9 +321,11 @@ def delta(
 ):
     """Chunked GDN for training, same contract as ops/gated_delta_net.py:217-249.
 
-    q, k, v: [B,T,H,128] bf16 time-first; g, beta: [B,T,H] (computed in fp32).
+    q, k, v: [B,T,H,128] bf16 or fp16 time-first; g, beta: [B,T,H] (computed in fp32).
     Packed documents: B == 1 with ``cu_seqlens`` (device) and ``cu_seqlens_cpu``
-    (host) bounds; the state resets at each document.  Returns ``(o, None)``.
+    (host) bounds; the state resets at each document.  Returns ``(o, None)``, o and the
+    gradients in the input dtypes.  The kernels' MFMA operands are bf16 either way (fp16
+    inputs are rounded to bf16 once, which keeps every value's range).
     """
     if initial_state is not None or output_final_state:
         raise NotImplementedError("This training adapter requires zero initial state and no state output")
@@ -321,8 +336,6 @@ def delta(
     bounds = host_bounds(cu_seqlens, cu_seqlens_cpu)
     if bounds is not None and (q.shape[0] != 1 or bounds[-1] != q.shape[1]):
         raise ValueError("Packed inputs must have batch 1 and boundaries covering every token")
-    if q.dtype != torch.bfloat16:
-        raise NotImplementedError("the hip GDN kernels compute in bf16; fp16 inputs are not built yet")
     if g.shape != q.shape[:3] or beta.shape != q.shape[:3]:
         raise ValueError("g and beta must be [B,T,H]")
     _require_gpu(q, k, v, g, beta)

@@ -183,8 +183,10 @@ int fwd_impl(const void* q, const void* k, const void* v, const float* g, const 
              unsigned flags, const float* initial_state, float* final_state, void* o, void* workspace,
              size_t workspace_bytes, void* stream) {
   if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
-  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING | CQGDN_PRECISE))
+  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING | CQGDN_PRECISE | CQGDN_NO_OUTPUT))
     return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
+  if ((flags & CQGDN_NO_OUTPUT) && !(flags & CQGDN_TRAINING))
+    return fail(CQGDN_EINVAL, "CQGDN_NO_OUTPUT rebuilds a training workspace: it needs CQGDN_TRAINING");
   if ((flags & CQGDN_TRAINING) && (flags & CQGDN_PRECISE))
     return fail(CQGDN_EINVAL, "CQGDN_PRECISE is an inference forward: it cannot be combined with CQGDN_TRAINING");
   if ((flags & CQGDN_TRAINING) && (initial_state || final_state))
@@ -198,13 +200,14 @@ int fwd_impl(const void* q, const void* k, const void* v, const float* g, const 
     }
     return ok();
   }
-  if (!q || !k || !v || !g || !beta || !o || !workspace) return fail(CQGDN_EINVAL, "null tensor pointer");
+  if (!q || !k || !v || !g || !beta || (!o && !(flags & CQGDN_NO_OUTPUT)) || !workspace)
+    return fail(CQGDN_EINVAL, "null tensor pointer");
   const size_t need = cqgdn_fwd_workspace_size(T, H, n_chunks);
   if (workspace_bytes < need)
     return fail(CQGDN_EINVAL, "forward workspace too small: %zu < %zu bytes", workspace_bytes, need);
   if (!aligned(workspace, 256)) return fail(CQGDN_EINVAL, "workspace must be 256-byte aligned");
   for (const void* p : {q, k, v, (const void*)o})
-    if (!aligned(p, 16)) return fail(CQGDN_EINVAL, "q/k/v/o must be 16-byte aligned");
+    if (p && !aligned(p, 16)) return fail(CQGDN_EINVAL, "q/k/v/o must be 16-byte aligned");
   FwdArgs a{};
   a.q = static_cast<const bf16*>(q);
   a.k = static_cast<const bf16*>(k);
@@ -220,6 +223,7 @@ int fwd_impl(const void* q, const void* k, const void* v, const float* g, const 
   a.scale = scale;
   a.normalize = (flags & CQGDN_NORMALIZE) != 0;
   a.precise = (flags & CQGDN_PRECISE) != 0;
+  a.no_output = (flags & CQGDN_NO_OUTPUT) != 0;
   a.initial_state = initial_state;
   a.final_state = final_state;
   a.o = static_cast<bf16*>(o);

@@ -877,6 +877,7 @@ static void launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stre
     hipLaunchKernelGGL(fwd_scan_kernel<E>, grid_s, dim3(SC_THREADS), 0, stream, ws[F_W], ws[F_UT], ws[F_KGT], gcum,
                        a.chunks, a.doc_chunk, a.H, vscale, a.initial_state, a.final_state, ws[F_HT], ws[F_VNT]);
   }
+  if (a.no_output) return;
   TimedLaunch tl(K_FWD_OUT, stream);
   hipLaunchKernelGGL(fwd_out_kernel<E>, dim3(a.H, a.n_chunks), dim3(256), 0, stream, ws[F_QN], ws[F_KN], gcum, ws[F_HT], ws[F_VNT],
                      a.chunks, a.H, a.scale, vscale, a.o);

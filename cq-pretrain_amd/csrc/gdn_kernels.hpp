@@ -20,6 +20,7 @@ struct FwdArgs {
   float scale;
   bool normalize;
   bool precise;                // fp16 operands (inference only); operands in the workspace are then fp16
+  bool no_output;              // rebuild the workspace only (the backward's recompute): no output kernel
   const float* initial_state;  // [n_docs][H][K][V] or null
   float* final_state;          // [n_docs][H][K][V] or null
   bf16* o;                     // [T][H][D]

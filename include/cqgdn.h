@@ -45,6 +45,10 @@ extern "C" {
  * states within 1e-3 of an fp32 computation; V and the initial state are scaled by a power of
  * two inside the call so every fp16 operand stays in range.  Not combinable with CQGDN_TRAINING. */
 #define CQGDN_PRECISE 4u
+/* With CQGDN_TRAINING: rebuild only the workspace cqgdn_bwd reads, without the output kernel (o is
+ * not written and may be NULL).  The backward's recompute of the reference's `fused` mode, which
+ * keeps no w / h / v_new between the forward and the backward (ops/gated_delta_net.py:143-156,192-194). */
+#define CQGDN_NO_OUTPUT 8u
 
 /* Library version string, e.g. "cqgdn 0.1.0 gfx950". */
 const char* cqgdn_version(void);

@@ -42,7 +42,7 @@ def test_header_constants_match_binding():
     text = HEADER.read_text()
     for name, value in (("CQGDN_FWD_BUFFERS", _lib.FWD_BUFFERS), ("CQGDN_BWD_BUFFERS", _lib.BWD_BUFFERS),
                         ("CQGDN_NORMALIZE", _lib.NORMALIZE), ("CQGDN_TRAINING", _lib.TRAINING),
-                        ("CQGDN_PRECISE", _lib.PRECISE),
+                        ("CQGDN_PRECISE", _lib.PRECISE), ("CQGDN_NO_OUTPUT", _lib.NO_OUTPUT),
                         ("CQGDN_EINVAL", _lib.EINVAL), ("CQGDN_EUNSUPPORTED", _lib.EUNSUPPORTED),
                         ("CQGDN_EHIP", _lib.EHIP)):
         m = re.search(rf"#define {name} (\d+)", text)

@@ -377,3 +377,81 @@ def test_whole_layer_at_benchmark_plan_matches_float64_recurrence(gdn):
     got, want = run(None), run(oracle)
     for name, a, b in zip(("y", "dx", "dW_in"), got, want):
         assert_close_bf16(name, a, b.double())
+
+
+def test_decode_steps_replay_in_a_hip_graph(gdn):
+    """The decode loop of config 4's shape captured once in a HIP graph (as a serving loop runs it):
+    every replay -- with eager work and synchronizations of the program between them -- gives exactly
+    the states and outputs of the same steps run eagerly from the same starting states."""
+    N, H, E, steps = 16, 16, 2, 6
+    print(f"case decode graph: N={N} H={H} E={E} steps={steps}", flush=True)
+    gen = torch.Generator().manual_seed(44)
+    q = O.l2norm(torch.randn(N, E, H, 128, generator=gen)).bfloat16().to(DEV)
+    k = O.l2norm(torch.randn(N, E, H, 128, generator=gen)).bfloat16().to(DEV)
+    v = torch.randn(N, E, H, 128, generator=gen).bfloat16().to(DEV)
+    g = (-torch.nn.functional.softplus(torch.randn(N, E, H, generator=gen))).to(DEV)
+    b = torch.randn(N, E, H, generator=gen).sigmoid().to(DEV)
+    init = [(torch.randn(N, H, 128, 128, generator=gen) * 0.02).to(DEV) for _ in range(2)]
+    outs = [torch.empty(N, E, H, 128, dtype=torch.bfloat16, device=DEV) for _ in range(steps)]
+
+    def run(states):
+        for i in range(steps):
+            gdn.recurrent(q, k, v, g, b, states[i % 2], outs[i])
+
+    eager_states = [s.clone() for s in init]
+    run(eager_states)
+    torch.cuda.synchronize()
+    eager_outs = [o.clone() for o in outs]
+    states = [s.clone() for s in init]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run([s.clone() for s in init])  # warm-up off the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(states)
+    for replay in range(3):
+        for s, s0 in zip(states, init):
+            s.copy_(s0)
+        for o in outs:
+            o.fill_(0)
+        _ = (torch.randn(256, 256, device=DEV) @ torch.randn(256, 256, device=DEV)).sum().item()  # eager work between
+        graph.replay()
+        torch.cuda.synchronize()
+        for s, e in zip(states, eager_states):
+            assert torch.equal(s, e), f"replay {replay}: state differs"
+        for o, e in zip(outs, eager_outs):
+            assert torch.equal(o, e), f"replay {replay}: output differs"
+
+
+def test_fused_mode_matches_cached_mode(gdn, monkeypatch):
+    """DELTA_HIP_MODE=fused keeps only the inputs between the forward and the backward and rebuilds
+    the workspace in the backward (the reference's default mode, ops/gated_delta_net.py:143-156,192-194):
+    output and every gradient equal the cached mode's exactly (same kernels on the same inputs)."""
+    bounds = (0, 130, 300)
+    print(f"case fused vs cached mode, bounds={bounds}", flush=True)
+    xs = inputs(300, 16, seed=88)
+    do = torch.randn(1, 300, 16, 128, generator=torch.Generator().manual_seed(89)).bfloat16()
+    res = {}
+    for mode in ("cached", "fused"):
+        monkeypatch.setattr(gdn, "MODE", mode)
+        res[mode] = fwd_bwd(gdn, xs, bounds, do)
+    (y_c, g_c), (y_f, g_f) = res["cached"], res["fused"]
+    assert torch.equal(y_c, y_f)
+    for a, b in zip(g_c, g_f):
+        assert torch.equal(a, b)
+    check_against_oracle(xs, bounds, do, y_f, g_f)
+
+
+def test_delta_fp16_inputs_match_oracle(gdn):
+    """fp16 q/k/v, which the reference's delta accepts (ops/gated_delta_net.py:233-234): output and
+    gradients come back in the input dtypes and match the float64 oracle of the same fp16 values."""
+    T, bounds, H = 257, (0, 100, 257), 8
+    print(f"case fp16 inputs T={T} bounds={bounds}", flush=True)
+    q, k, v, g, b = inputs(T, H, seed=1616)
+    q, k, v = (x.float().half() for x in (q, k, v))
+    do = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(17)).half()
+    y, grads = fwd_bwd(gdn, [q, k, v, g, b], bounds, do)
+    assert y.dtype == torch.float16 and [x.dtype for x in grads] == [torch.float16] * 3 + [torch.float32] * 2
+    check_against_oracle([q, k, v, g, b], bounds, do, y, grads)

@@ -76,8 +76,21 @@ def test_delta_argument_checks_match_reference():
     cu = torch.tensor([0, 3])
     with pytest.raises(ValueError, match="covering every token"):
         gdn.delta(q, k, v, g, b, cu_seqlens=cu, cu_seqlens_cpu=[0, 3])
-    with pytest.raises(NotImplementedError, match="fp16"):
+    with pytest.raises(ValueError, match="QKV must share"):
+        gdn.delta(q.half(), k, v, g, b)
+    # fp16 q/k/v pass the checks (the reference accepts bf16 or fp16); on the CPU the GPU check rejects them
+    with pytest.raises(ValueError, match="ROCm GPU"):
         gdn.delta(q.half(), k.half(), v.half(), g, b)
+
+
+def test_mode_is_checked_like_the_reference(monkeypatch):
+    """DELTA_HIP_MODE accepts the reference's two modes (ops/gated_delta_net.py:20,57-58)."""
+    for mode in ("fused", "cached"):
+        monkeypatch.setattr(gdn, "MODE", mode)
+        gdn.initialize()
+    monkeypatch.setattr(gdn, "MODE", "eager")
+    with pytest.raises(ValueError, match="Unknown DELTA_HIP_MODE"):
+        gdn.initialize()
 
 
 def test_no_cpu_fallback():
