@@ -428,6 +428,16 @@ def main():
         extra["config3_tflops"] = round(f3 / (ms3 * 1e-3) / 1e12, 2)
         extra["config3_documents"] = len(bounds3) - 1
         del step3
+        log("config 2 fwd+bwd, fused mode (the backward rebuilds the forward workspace)")
+        gdn.MODE = "fused"
+        try:
+            _, _, stepf, _ = training_case(gdn, synthetic, torch, 2, device)
+            for _ in range(args.warmup):
+                stepf()
+            extra["config2_fused_mode_ms"] = round(time_steps(torch, stepf, args.steps) * 1e3, 4)
+        finally:
+            gdn.MODE = "cached"
+        del stepf
         log("whole GatedDelta layer, width 2048 (content 2048 and 8192, image-CQ plans)")
         log("layer decode step, width 2048 (N = 1 and 64 sequences)")
         extra["layer_decode_w2048"] = [layer_decode_case(torch, device, n) for n in (1, 64)]
