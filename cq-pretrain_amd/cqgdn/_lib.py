@@ -44,13 +44,13 @@ SIGNATURES = {
     "cqgdn_gated_norm_fwd": (_I, [_P, _P, _I64, _I, _P, _I64, _P, _F, _P, _P, _P]),
     "cqgdn_gated_norm_bwd_workspace_size": (_SZ, [_I64, _I]),
     "cqgdn_gated_norm_bwd": (_I, [_P, _P, _P, _I64, _I64, _I, _P, _I64, _P, _P, _P, _P, _P, _I64, _P, _P, _SZ, _P]),
-    "cqgdn_event_inputs_fwd_workspace_size": (_SZ, [_I, _I]),
-    "cqgdn_event_inputs_fwd": (_I, [_P, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
-    "cqgdn_event_inputs_bwd_workspace_size": (_SZ, [_P, _I]),
-    "cqgdn_event_inputs_bwd": (_I, [_P, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
+    "cqgdn_event_inputs_fwd_workspace_size": (_SZ, [_I, _I, _I]),
+    "cqgdn_event_inputs_fwd": (_I, [_P, _I, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "cqgdn_event_inputs_bwd_workspace_size": (_SZ, [_P, _I, _I]),
+    "cqgdn_event_inputs_bwd": (_I, [_P, _I, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64,
                                     _P, _I64, _P, _I64, _P, _P, _P, _SZ, _P]),
     "cqgdn_layer_decode_workspace_size": (_SZ, [_I, _I]),
-    "cqgdn_layer_decode_step": (_I, [_I, _I, _I, _P, _I64, _P, _P, _P, _P, _P, _F, _F, _P, _P, _P, _SZ, _P]),
+    "cqgdn_layer_decode_step": (_I, [_I, _I, _I, _I, _P, _I64, _P, _P, _P, _P, _P, _F, _F, _P, _P, _P, _SZ, _P]),
     "cqgdn_timer_arm": (_I, [ctypes.c_char_p, _I]),
     "cqgdn_timer_read": (_I, [_P, _I, _P]),
 }

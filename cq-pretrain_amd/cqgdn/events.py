@@ -4,9 +4,11 @@
 ``in_proj_all`` and ``out_proj``: the content gather and packed causal conv, the CQ
 query conv from the content history, the q/k/v/g/beta event gathers and the gate
 math, the recurrence, the output gather and the gated RMSNorm.  It takes the fused
-projection as one [rows, 4S + 2H] tensor (S = H * 128; columns q|k|v, z, a, b as
-``in_proj_all(...).split`` lays them out) and returns the normalized [rows, S] rows
-for ``out_proj``.  Forward: cqgdn_event_inputs_fwd (the conv pass and the event
+projection as one [rows, 2SK + 2SV + 2H] tensor (H value heads, HK key heads,
+SK = HK * 128, SV = H * 128; columns q|k|v, z, a, b as ``in_proj_all(...).split``
+lays them out) and returns the normalized [rows, SV] rows for ``out_proj``.  With
+fewer key heads than value heads, value head j reads key head j // (H // HK), as
+the reference's repeat_interleave does (models/backbone_qwen35.py:182-183).  Forward: cqgdn_event_inputs_fwd (the conv pass and the event
 pass), the recurrence, cqgdn_gated_norm_fwd.  Backward: the norm, the recurrence and
 cqgdn_event_inputs_bwd write one projection-gradient tensor, each element once:
 every gather of the reference is consumed inside a kernel's loads, and every
@@ -140,42 +142,56 @@ def event_plan(plan, kernel: int, device) -> EventPlan:
     return ep
 
 
+def _columns(H, HK):
+    """Column offsets of the fused projection: (C, z, a, b, P) with C = 2SK + SV the conv channels."""
+    C = (2 * HK + H) * 128
+    return C, C, C + H * 128, C + H * 128 + H, C + H * 128 + 2 * H
+
+
+def _check_heads(heads, key_heads):
+    ok = (4, 8, 16, 32)
+    if heads not in ok or key_heads not in ok or heads % key_heads:
+        raise ValueError(f"heads={heads}, key_heads={key_heads}: supported are 4, 8, 16, 32, key heads dividing heads")
+
+
 class _LayerCore(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, proj, conv_weight, A_log, dt_bias, norm_weight, ep, H, eps, scale):
+    def forward(ctx, proj, conv_weight, A_log, dt_bias, norm_weight, ep, H, HK, eps, scale):
         # proj may be a column slice of a wider tensor: every read uses its row stride PS
         S, n_h, PS = H * 128, proj.shape[0], proj.stride(0)
+        C, zc, ac, bc, _ = _columns(H, HK)
         dev, st = proj.device, gdn._stream(proj.device)
         w = conv_weight.contiguous()
         alog, dtb, nw = A_log.float().contiguous(), dt_bias.float().contiguous(), norm_weight.float().contiguous()
         E = ep.n_events
         q, k, v = (torch.empty(E, H, 128, dtype=proj.dtype, device=dev) for _ in range(3))
         gb = torch.empty(2, E, H, dtype=torch.float32, device=dev)
-        fws = torch.empty(_lib.lib().cqgdn_event_inputs_fwd_workspace_size(ep.n_content, H), dtype=torch.uint8,
+        fws = torch.empty(_lib.lib().cqgdn_event_inputs_fwd_workspace_size(ep.n_content, H, HK), dtype=torch.uint8,
                           device=dev)
-        a_ptr, b_ptr = proj[:, 4 * S:].data_ptr(), proj[:, 4 * S + H:].data_ptr()
-        gdn.call("cqgdn_event_inputs_fwd", ctypes.byref(ep.cstruct), H, gdn._ptr(proj), PS, a_ptr, PS, b_ptr, PS,
+        a_ptr, b_ptr = proj[:, ac:].data_ptr(), proj[:, bc:].data_ptr()
+        gdn.call("cqgdn_event_inputs_fwd", ctypes.byref(ep.cstruct), H, HK, gdn._ptr(proj), PS, a_ptr, PS, b_ptr, PS,
                  gdn._ptr(w), gdn._ptr(alog), gdn._ptr(dtb), gdn._ptr(q), gdn._ptr(k), gdn._ptr(v),
                  gdn._ptr(gb[0]), gdn._ptr(gb[1]), gdn._ptr(fws), fws.numel(), st)
         y, _, rws = gdn._forward(q[None], k[None], v[None], gb[0][None], gb[1][None], ep.event_bounds, True, scale,
                                  training=True)
         out = torch.empty(n_h, H, 128, dtype=proj.dtype, device=dev)
         rstd = torch.empty(n_h, H, dtype=torch.float32, device=dev)
-        gdn.call("cqgdn_gated_norm_fwd", gdn._ptr(y), gdn._ptr(ep.hidden_index), n_h, H, proj[:, 3 * S:].data_ptr(),
+        gdn.call("cqgdn_gated_norm_fwd", gdn._ptr(y), gdn._ptr(ep.hidden_index), n_h, H, proj[:, zc:].data_ptr(),
                  PS, gdn._ptr(nw), float(eps), gdn._ptr(out), gdn._ptr(rstd), st)
         ctx.save_for_backward(proj, w, alog, dtb, nw, v, gb, rws, y, rstd)
-        ctx.ep, ctx.H, ctx.scale = ep, H, scale
+        ctx.ep, ctx.H, ctx.HK, ctx.scale = ep, H, HK, scale
         ctx.dtypes = (conv_weight.dtype, A_log.dtype, dt_bias.dtype, norm_weight.dtype)
         return out.reshape(n_h, S)
 
     @staticmethod
     def backward(ctx, dout):
         proj, w, alog, dtb, nw, v, gb, rws, y, rstd = ctx.saved_tensors
-        ep, H = ctx.ep, ctx.H
-        S, n_h, P, PS = H * 128, proj.shape[0], proj.shape[1], proj.stride(0)
+        ep, H, HK = ctx.ep, ctx.H, ctx.HK
+        n_h, P, PS = proj.shape[0], proj.shape[1], proj.stride(0)
+        C, zc, ac, bc, width = _columns(H, HK)
         dev, st = proj.device, gdn._stream(proj.device)
         # the gradient is a dense [rows, P] tensor (row stride P) whatever proj's stride
-        full = ep.covers_all and P == 4 * S + 2 * H
+        full = ep.covers_all and P == width
         d_proj = (torch.empty if full else torch.zeros)(n_h, P, dtype=proj.dtype, device=dev)
         do = dout.contiguous()
         dy = torch.empty(ep.n_events, H, 128, dtype=proj.dtype, device=dev)
@@ -183,60 +199,68 @@ class _LayerCore(torch.autograd.Function):
         nws = torch.empty(max(_lib.lib().cqgdn_gated_norm_bwd_workspace_size(n_h, H), 16), dtype=torch.uint8,
                           device=dev)
         gdn.call("cqgdn_gated_norm_bwd", gdn._ptr(y), gdn._ptr(ep.hidden_index), gdn._ptr(ep.unread_events),
-                 ep.unread_events.numel(), n_h, H, proj[:, 3 * S:].data_ptr(), PS, gdn._ptr(nw), gdn._ptr(rstd),
-                 gdn._ptr(do), gdn._ptr(dy), d_proj[:, 3 * S:].data_ptr(), P, gdn._ptr(dnw), gdn._ptr(nws),
+                 ep.unread_events.numel(), n_h, H, proj[:, zc:].data_ptr(), PS, gdn._ptr(nw), gdn._ptr(rstd),
+                 gdn._ptr(do), gdn._ptr(dy), d_proj[:, zc:].data_ptr(), P, gdn._ptr(dnw), gdn._ptr(nws),
                  nws.numel(), st)
         dq, dk, dv, dg, db = gdn._backward(v[None], gb[0][None], gb[1][None], rws, dy, ep.event_bounds, True,
                                            ctx.scale)
         dw = torch.empty(w.shape, dtype=torch.float32, device=dev)
         dgate = torch.empty(2 * H, dtype=torch.float32, device=dev)
-        ews = torch.empty(_lib.lib().cqgdn_event_inputs_bwd_workspace_size(ctypes.byref(ep.cstruct), H),
+        ews = torch.empty(_lib.lib().cqgdn_event_inputs_bwd_workspace_size(ctypes.byref(ep.cstruct), H, HK),
                           dtype=torch.uint8, device=dev)
-        gdn.call("cqgdn_event_inputs_bwd", ctypes.byref(ep.cstruct), H, gdn._ptr(proj), PS,
-                 proj[:, 4 * S:].data_ptr(), PS, proj[:, 4 * S + H:].data_ptr(), PS, gdn._ptr(w), gdn._ptr(alog),
+        gdn.call("cqgdn_event_inputs_bwd", ctypes.byref(ep.cstruct), H, HK, gdn._ptr(proj), PS,
+                 proj[:, ac:].data_ptr(), PS, proj[:, bc:].data_ptr(), PS, gdn._ptr(w), gdn._ptr(alog),
                  gdn._ptr(dtb), gdn._ptr(dq), gdn._ptr(dk), gdn._ptr(dv), gdn._ptr(dg), gdn._ptr(db),
-                 gdn._ptr(d_proj), P, d_proj[:, 4 * S:].data_ptr(), P, d_proj[:, 4 * S + H:].data_ptr(), P,
+                 gdn._ptr(d_proj), P, d_proj[:, ac:].data_ptr(), P, d_proj[:, bc:].data_ptr(), P,
                  gdn._ptr(dw), gdn._ptr(dgate), gdn._ptr(ews), ews.numel(), st)
         cw, ca, cd, cn = ctx.dtypes
-        return d_proj, dw.to(cw), dgate[:H].to(ca), dgate[H:].to(cd), dnw.to(cn), None, None, None, None
+        return d_proj, dw.to(cw), dgate[:H].to(ca), dgate[H:].to(cd), dnw.to(cn), None, None, None, None, None
 
 
-def layer_core(proj, conv_weight, A_log, dt_bias, norm_weight, plan, *, heads, eps=1e-6, scale=None):
-    """GatedDelta between its projections: proj [rows, 4S + 2H] bf16 (q|k|v, z, a, b columns of
-    ``in_proj_all``), conv_weight [3S, K] bf16, A_log / dt_bias [H], norm_weight [128];
-    returns the gated-norm rows [rows, S] that feed ``out_proj`` (models/backbone_qwen35.py:158-246,
-    training path, key heads == value heads)."""
-    S = heads * 128
-    if proj.dim() != 2 or proj.shape[1] != 4 * S + 2 * heads or proj.stride(1) != 1:
-        raise ValueError("proj must be [rows, 4*H*128 + 2*H] with unit column stride")
+def layer_core(proj, conv_weight, A_log, dt_bias, norm_weight, plan, *, heads, key_heads=None, eps=1e-6,
+               scale=None):
+    """GatedDelta between its projections: proj [rows, 2SK + 2SV + 2H] bf16 (q|k|v, z, a, b columns
+    of ``in_proj_all``; SK = key_heads * 128, SV = heads * 128), conv_weight [2SK + SV, K] bf16,
+    A_log / dt_bias [H], norm_weight [128]; returns the gated-norm rows [rows, SV] that feed
+    ``out_proj`` (models/backbone_qwen35.py:158-246, training path).  ``key_heads`` (the
+    reference's linear_heads per rank) defaults to ``heads``."""
+    HK = heads if key_heads is None else int(key_heads)
+    _check_heads(heads, HK)
+    C, _, _, _, width = _columns(heads, HK)
+    if proj.dim() != 2 or proj.shape[1] != width or proj.stride(1) != 1:
+        raise ValueError("proj must be [rows, (2*key_heads + 2*heads)*128 + 2*heads] with unit column stride")
     if proj.dtype != torch.bfloat16 or conv_weight.dtype != torch.bfloat16:
         raise NotImplementedError("the fused layer kernels compute on bf16 projections and conv weights")
-    if conv_weight.shape[0] != 3 * S or A_log.shape != (heads,) or dt_bias.shape != (heads,) or \
+    if conv_weight.shape[0] != C or A_log.shape != (heads,) or dt_bias.shape != (heads,) or \
             norm_weight.shape != (128,):
-        raise ValueError("parameter shapes do not match the head count")
+        raise ValueError("parameter shapes do not match the head counts")
     gdn._require_gpu(proj, conv_weight, A_log, dt_bias, norm_weight)
     if proj.stride(0) < proj.shape[1] or proj.stride(0) % 8 or proj.data_ptr() % 16:
         proj = proj.contiguous()  # the kernels read rows proj.stride(0) apart with 16-byte loads
     ep = event_plan(plan, conv_weight.shape[1], proj.device)
     if ep.n_hidden != proj.shape[0]:
         raise ValueError("proj rows do not match the plan's hidden rows")
-    return _LayerCore.apply(proj, conv_weight, A_log, dt_bias, norm_weight, ep, heads, eps,
+    return _LayerCore.apply(proj, conv_weight, A_log, dt_bias, norm_weight, ep, heads, HK, eps,
                             128 ** -0.5 if scale is None else float(scale))
 
 
 @torch.no_grad()
-def layer_prefill(proj, conv_weight, A_log, dt_bias, norm_weight, plan, *, heads, eps=1e-6, scale=None):
+def layer_prefill(proj, conv_weight, A_log, dt_bias, norm_weight, plan, *, heads, key_heads=None, eps=1e-6,
+                  scale=None):
     """Inference prefill of the layer with the cache a decoder continues from
     (models/backbone_qwen35.py:163-211 with ``cache``): the event inputs as in training, the
     precise forward with each document's final state, the gated norm with the output gather.
 
-    Returns ``(out [rows, S], cache)``: ``cache["state"]`` fp32 [n_docs, H, V, K] value-first (the
-    decode layout) and ``cache["conv"]`` bf16 [1, K-1, 3S], the raw q|k|v rows of the K-1 content
-    rows before the last one, zero-filled in front, as the reference keeps them (its last content
-    row is the uncommitted target, models/decoding.py:117-121)."""
+    Heads and columns as in ``layer_core``.  Returns ``(out [rows, SV], cache)``: ``cache["state"]``
+    fp32 [n_docs, H, V, K] value-first (the decode layout) and ``cache["conv"]`` bf16 [1, K-1, C],
+    the raw q|k|v rows of the K-1 content rows before the last one, zero-filled in front, as the
+    reference keeps them (its last content row is the uncommitted target, models/decoding.py:117-121)."""
+    HK = heads if key_heads is None else int(key_heads)
+    _check_heads(heads, HK)
     S = heads * 128
-    if proj.dim() != 2 or proj.shape[1] != 4 * S + 2 * heads or proj.dtype != torch.bfloat16:
-        raise ValueError("proj must be bf16 [rows, 4*H*128 + 2*H]")
+    C, zc, ac, bc, width = _columns(heads, HK)
+    if proj.dim() != 2 or proj.shape[1] != width or proj.dtype != torch.bfloat16:
+        raise ValueError("proj must be bf16 [rows, (2*key_heads + 2*heads)*128 + 2*heads]")
     gdn._require_gpu(proj, conv_weight)
     proj = proj.contiguous()
     K = conv_weight.shape[1]
@@ -246,10 +270,10 @@ def layer_prefill(proj, conv_weight, A_log, dt_bias, norm_weight, plan, *, heads
     alog, dtb, nw = A_log.float().contiguous(), dt_bias.float().contiguous(), norm_weight.float().contiguous()
     q, k, v = (torch.empty(E, heads, 128, dtype=proj.dtype, device=dev) for _ in range(3))
     gb = torch.empty(2, E, heads, dtype=torch.float32, device=dev)
-    fws = torch.empty(_lib.lib().cqgdn_event_inputs_fwd_workspace_size(ep.n_content, heads), dtype=torch.uint8,
-                      device=dev)
-    gdn.call("cqgdn_event_inputs_fwd", ctypes.byref(ep.cstruct), heads, gdn._ptr(proj), P,
-             proj[:, 4 * S:].data_ptr(), P, proj[:, 4 * S + heads:].data_ptr(), P, gdn._ptr(w), gdn._ptr(alog),
+    fws = torch.empty(_lib.lib().cqgdn_event_inputs_fwd_workspace_size(ep.n_content, heads, HK),
+                      dtype=torch.uint8, device=dev)
+    gdn.call("cqgdn_event_inputs_fwd", ctypes.byref(ep.cstruct), heads, HK, gdn._ptr(proj), P,
+             proj[:, ac:].data_ptr(), P, proj[:, bc:].data_ptr(), P, gdn._ptr(w), gdn._ptr(alog),
              gdn._ptr(dtb), gdn._ptr(q), gdn._ptr(k), gdn._ptr(v), gdn._ptr(gb[0]), gdn._ptr(gb[1]), gdn._ptr(fws),
              fws.numel(), st)
     y, state, _ = gdn._forward(q[None], k[None], v[None], gb[0][None], gb[1][None], ep.event_bounds, True,
@@ -257,33 +281,38 @@ def layer_prefill(proj, conv_weight, A_log, dt_bias, norm_weight, plan, *, heads
                                precise=True)
     out = torch.empty(n_h, heads, 128, dtype=proj.dtype, device=dev)
     rstd = torch.empty(n_h, heads, dtype=torch.float32, device=dev)
-    gdn.call("cqgdn_gated_norm_fwd", gdn._ptr(y), gdn._ptr(ep.hidden_index), n_h, heads, proj[:, 3 * S:].data_ptr(),
+    gdn.call("cqgdn_gated_norm_fwd", gdn._ptr(y), gdn._ptr(ep.hidden_index), n_h, heads, proj[:, zc:].data_ptr(),
              P, gdn._ptr(nw), float(eps), gdn._ptr(out), gdn._ptr(rstd), st)
     count = K - 1
-    history = proj.new_zeros(1, count, 3 * S)
+    history = proj.new_zeros(1, count, C)
     order = ep.tensors["content_order"]
     tail = order[max(0, ep.n_content - 1 - count):max(ep.n_content - 1, 0)].long()
     if tail.numel():
-        history[0, count - tail.numel():] = proj.index_select(0, tail)[:, :3 * S]
+        history[0, count - tail.numel():] = proj.index_select(0, tail)[:, :C]
     return out.reshape(n_h, S), {"state": state.transpose(-1, -2).contiguous(), "conv": history}
 
 
 @torch.no_grad()
-def layer_decode_step(proj, conv_weight, A_log, dt_bias, norm_weight, cache, *, heads, eps=1e-6, scale=None):
+def layer_decode_step(proj, conv_weight, A_log, dt_bias, norm_weight, cache, *, heads, key_heads=None, eps=1e-6,
+                      scale=None):
     """One decode step (models/decoding.py:16-78 between the projection and out_proj) for N
-    sequences: proj [N, 2, 4S + 2H] bf16 (row 0 the sampled content token, row 1 the text-mask
-    query; [2, P] for one sequence); ``cache["conv"]`` bf16 [N, K-1, 3S] and ``cache["state"]`` fp32
-    [N, H, V, K] are updated in place.  Returns the gated-norm rows [N, 2, S] ([2, S])."""
+    sequences: proj [N, 2, P] bf16 (row 0 the sampled content token, row 1 the text-mask query;
+    [2, P] for one sequence; heads and columns as in ``layer_core``); ``cache["conv"]`` bf16
+    [N, K-1, C] and ``cache["state"]`` fp32 [N, H, V, K] are updated in place.  Returns the
+    gated-norm rows [N, 2, SV] ([2, SV])."""
+    HK = heads if key_heads is None else int(key_heads)
+    _check_heads(heads, HK)
     S = heads * 128
+    C, _, _, _, width = _columns(heads, HK)
     single = proj.dim() == 2
     p3 = proj[None] if single else proj
     N, P = p3.shape[0], p3.shape[2]
     K = conv_weight.shape[1]
-    if p3.shape[1] != 2 or P != 4 * S + 2 * heads or p3.dtype != torch.bfloat16:
-        raise ValueError("proj must be bf16 [N, 2, 4*H*128 + 2*H]")
+    if p3.shape[1] != 2 or P != width or p3.dtype != torch.bfloat16:
+        raise ValueError("proj must be bf16 [N, 2, (2*key_heads + 2*heads)*128 + 2*heads]")
     hist, state = cache["conv"], cache["state"]
-    if hist.shape != (N, K - 1, 3 * S) or hist.dtype != torch.bfloat16 or not hist.is_contiguous():
-        raise ValueError("cache['conv'] must be contiguous bf16 [N, K-1, 3*H*128]")
+    if hist.shape != (N, K - 1, C) or hist.dtype != torch.bfloat16 or not hist.is_contiguous():
+        raise ValueError("cache['conv'] must be contiguous bf16 [N, K-1, (2*key_heads + heads)*128]")
     if state.shape != (N, heads, 128, 128) or state.dtype != torch.float32 or not state.is_contiguous():
         raise ValueError("cache['state'] must be contiguous fp32 [N, H, 128, 128] (value-first)")
     gdn._require_gpu(p3, conv_weight, hist, state)
@@ -291,7 +320,7 @@ def layer_decode_step(proj, conv_weight, A_log, dt_bias, norm_weight, cache, *, 
     w = conv_weight.contiguous()
     alog, dtb, nw = A_log.float().contiguous(), dt_bias.float().contiguous(), norm_weight.float().contiguous()
     out = torch.empty(N, 2, S, dtype=p3.dtype, device=p3.device)
-    gdn.call("cqgdn_layer_decode_step", N, heads, K, gdn._ptr(p3), P, gdn._ptr(hist), gdn._ptr(w), gdn._ptr(alog),
+    gdn.call("cqgdn_layer_decode_step", N, heads, HK, K, gdn._ptr(p3), P, gdn._ptr(hist), gdn._ptr(w), gdn._ptr(alog),
              gdn._ptr(dtb), gdn._ptr(nw), float(eps), 128 ** -0.5 if scale is None else float(scale),
              gdn._ptr(state), gdn._ptr(out), None, 0, gdn._stream(p3.device))
     return out[0] if single else out

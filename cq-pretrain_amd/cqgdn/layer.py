@@ -212,10 +212,12 @@ def concat_plans(*plans: LayerPlan) -> LayerPlan:
 class GatedDeltaLayer(torch.nn.Module):
     """GatedDelta with fused projections (models/backbone_qwen35.py:121-154), one TP rank."""
 
-    def __init__(self, width=2048, heads=16, head_dim=128, conv_kernel=4, eps=1e-6):
+    def __init__(self, width=2048, heads=16, head_dim=128, conv_kernel=4, eps=1e-6, key_heads=None):
         super().__init__()
+        # heads: value heads (linear_value_heads); key_heads: q/k heads (linear_heads), default heads
+        self.key_heads = heads if key_heads is None else key_heads
         self.heads, self.head_dim, self.kernel = heads, head_dim, conv_kernel
-        key = value = heads * head_dim
+        key, value = self.key_heads * head_dim, heads * head_dim
         self.in_proj_all = torch.nn.Linear(width, 2 * key + 2 * value + 2 * heads, bias=False)
         self.conv_weight = torch.nn.Parameter(torch.empty(2 * key + value, conv_kernel).uniform_(-0.5, 0.5))
         self.A_log = torch.nn.Parameter(torch.rand(heads).mul(15.99).add(0.01).log())
@@ -232,26 +234,26 @@ class GatedDeltaLayer(torch.nn.Module):
         return self.out_proj(self.core(proj, plan, recurrence, conv, norm, fused))[:, None]
 
     def core(self, proj, plan: LayerPlan, recurrence=None, conv=None, norm=None, fused=True):
-        """Everything between the projections: proj [rows, 4S + 2H] -> gated-norm rows [rows, S].
+        """Everything between the projections: proj [rows, 2SK + 2SV + 2H] -> gated-norm rows [rows, SV].
 
         With ``fused`` and no hooks this is ``events.layer_core`` (the fused HIP kernels).
         Otherwise it is the reference's torch code with the hip delta, conv and gated norm, which
         ``recurrence(q, k, v, g, beta, plan)``, ``conv(x, weight, bounds)`` and
         ``norm(y, z, weight, eps)`` replace when given (tests pass float64 CPU restatements)."""
-        h, d = self.heads, self.head_dim
-        size = h * d
+        h, hk, d = self.heads, self.key_heads, self.head_dim
+        size, vsize = hk * d, h * d
         if fused and recurrence is None and conv is None and norm is None:
             return events.layer_core(proj, self.conv_weight, self.A_log, self.dt_bias, self.norm_weight, plan,
-                                     heads=h, eps=self.eps)
-        raw, z, a, beta = proj.split((2 * size + size, size, h, h), -1)
+                                     heads=h, key_heads=hk, eps=self.eps)
+        raw, z, a, beta = proj.split((2 * size + vsize, vsize, h, h), -1)
         updates = raw.index_select(0, plan.content_order)
         if conv is None:
             convolved = gdn.conv(updates[None], self.conv_weight, activation="silu", cu_seqlens=plan.content_cu,
                                  cu_seqlens_cpu=plan.content_bounds)[0][0]
         else:
             convolved = conv(updates[None], self.conv_weight, plan.content_bounds)[0]
-        q, k, v = convolved.split((size, size, size), -1)
-        q, k, v = q.reshape(-1, h, d), k.reshape(-1, h, d), v.reshape(-1, h, d)
+        q, k, v = convolved.split((size, size, vsize), -1)
+        q, k, v = q.reshape(-1, hk, d), k.reshape(-1, hk, d), v.reshape(-1, h, d)
         # the CQ query conv reads the content history only
         raw_q = raw[:, :size].index_select(0, plan.query_source)
         weight = self.conv_weight[:size]
@@ -259,7 +261,9 @@ class GatedDeltaLayer(torch.nn.Module):
         history = torch.cat((updates[:, :size], updates.new_zeros(1, size)), dim=0)
         for j in range(self.kernel - 1):
             query = query + history.index_select(0, plan.query_history[:, j]) * weight[:, j]
-        query = F.silu(query).reshape(-1, h, d)
+        query = F.silu(query).reshape(-1, hk, d)
+        if h != hk:
+            q, k, query = (t.repeat_interleave(h // hk, dim=1) for t in (q, k, query))
         q = torch.cat((q, query), dim=0).index_select(0, plan.event_q)[None]
         zeros = k.new_zeros(1, h, d)
         k = torch.cat((k, zeros), dim=0).index_select(0, plan.event_write)[None]

@@ -411,15 +411,28 @@ int cqgdn_gated_norm_bwd(const void* y, const int32_t* index, const int32_t* zer
 namespace {
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 
-int ev_args(const cqgdn_event_plan* p, int H, const void* raw, int64_t raw_stride, const void* a, int64_t a_stride,
-            const void* b, int64_t b_stride, const void* w, const float* A_log, const float* dt_bias, EvArgs& out) {
+// log2(H / HK) for supported value and key head counts, -1 otherwise
+int head_group_shift(int H, int HK) {
+  auto pow2 = [](int x) { return x == 4 || x == 8 || x == 16 || x == 32; };
+  if (!pow2(H) || !pow2(HK) || HK > H) return -1;
+  int s = 0;
+  while ((HK << s) < H) ++s;
+  return s;
+}
+
+int ev_args(const cqgdn_event_plan* p, int H, int HK, const void* raw, int64_t raw_stride, const void* a,
+            int64_t a_stride, const void* b, int64_t b_stride, const void* w, const float* A_log,
+            const float* dt_bias, EvArgs& out) {
   if (!p) return fail(CQGDN_EINVAL, "plan is null");
-  if (H != 4 && H != 8 && H != 16 && H != 32) return fail(CQGDN_EINVAL, "H=%d: supported local heads are 4, 8, 16, 32", H);
+  const int gshift = head_group_shift(H, HK);
+  if (gshift < 0)
+    return fail(CQGDN_EINVAL, "H=%d key_heads=%d: supported local heads are 4, 8, 16, 32, key heads dividing H", H, HK);
   if (p->n_content < 0 || p->n_queries < 0 || p->n_events < 0 || p->n_content_docs < 0 || p->n_history_rows < 0)
     return fail(CQGDN_EINVAL, "negative plan sizes");
   if (p->conv_kernel < 2 || p->conv_kernel > 4) return fail(CQGDN_EINVAL, "conv_kernel=%d not in 2..4", p->conv_kernel);
-  const int64_t S = (int64_t)H * CQGDN_HEAD_DIM;
-  if (raw_stride < 3 * S || raw_stride % 8) return fail(CQGDN_EINVAL, "raw_stride must be >= 3*H*128 and a multiple of 8");
+  const int64_t C = (int64_t)(2 * HK + H) * CQGDN_HEAD_DIM;
+  if (raw_stride < C || raw_stride % 8)
+    return fail(CQGDN_EINVAL, "raw_stride must be >= (2*key_heads + H)*128 and a multiple of 8");
   if (a_stride < H || b_stride < H) return fail(CQGDN_EINVAL, "a_stride and b_stride must be >= H");
   if (!raw || !a || !b || !w || !A_log || !dt_bias || !aligned(raw, 16))
     return fail(CQGDN_EINVAL, "raw (16-byte aligned), a, b, conv_weight, A_log, dt_bias must be non-null");
@@ -434,7 +447,7 @@ int ev_args(const cqgdn_event_plan* p, int H, const void* raw, int64_t raw_strid
   if (p->n_fold_rows < 0 || p->n_fold_rows > p->n_content ||
       (p->n_fold_rows > 0 && (!p->fold_rows || !p->fold_ptr || !p->fold_list)))
     return fail(CQGDN_EINVAL, "fold rows: n_fold_rows must be in 0..n_content with non-null fold arrays");
-  out = EvArgs{H, p->conv_kernel, p->n_content, p->n_queries, p->n_events, p->n_history_rows,
+  out = EvArgs{H, HK, gshift, p->conv_kernel, p->n_content, p->n_queries, p->n_events, p->n_history_rows,
                p->content_order, p->event_q, p->event_write, p->query_source, p->query_history,
                p->q_ptr, p->q_list, p->write_event, p->query_event, p->history_ptr, p->history_list,
                p->history_rows, static_cast<const bf16*>(raw), raw_stride, static_cast<const bf16*>(a), a_stride,
@@ -443,29 +456,30 @@ int ev_args(const cqgdn_event_plan* p, int H, const void* raw, int64_t raw_strid
 }
 }  // namespace
 
-size_t cqgdn_event_inputs_fwd_workspace_size(int n_content, int H) {
-  if (n_content < 0 || H <= 0) return 0;
-  return align256((size_t)n_content * 3 * H * CQGDN_HEAD_DIM * sizeof(bf16)) + 256;
+size_t cqgdn_event_inputs_fwd_workspace_size(int n_content, int H, int key_heads) {
+  if (n_content < 0 || H <= 0 || key_heads <= 0) return 0;
+  return align256((size_t)n_content * (2 * key_heads + H) * CQGDN_HEAD_DIM * sizeof(bf16)) + 256;
 }
 
-int cqgdn_event_inputs_fwd(const cqgdn_event_plan* plan, int H, const void* raw, int64_t raw_stride, const void* a,
-                           int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
+int cqgdn_event_inputs_fwd(const cqgdn_event_plan* plan, int H, int key_heads, const void* raw, int64_t raw_stride,
+                           const void* a, int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
                            const float* A_log, const float* dt_bias, void* q, void* k, void* v, float* g, float* beta,
                            void* workspace, size_t workspace_bytes, void* stream) {
   EvArgs ea;
-  if (const int e = ev_args(plan, H, raw, raw_stride, a, a_stride, b, b_stride, conv_weight, A_log, dt_bias, ea))
+  if (const int e = ev_args(plan, H, key_heads, raw, raw_stride, a, a_stride, b, b_stride, conv_weight, A_log,
+                            dt_bias, ea))
     return e;
   if (plan->n_events > 0 && (!q || !k || !v || !g || !beta || !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16)))
     return fail(CQGDN_EINVAL, "q, k, v (16-byte aligned), g, beta must be non-null");
   if (!workspace || !aligned(workspace, 256) ||
-      workspace_bytes < cqgdn_event_inputs_fwd_workspace_size(plan->n_content, H))
+      workspace_bytes < cqgdn_event_inputs_fwd_workspace_size(plan->n_content, H, key_heads))
     return fail(CQGDN_EINVAL, "workspace must be 256-byte aligned and >= cqgdn_event_inputs_fwd_workspace_size");
-  const int S = H * CQGDN_HEAD_DIM;
+  const int C = (2 * key_heads + H) * CQGDN_HEAD_DIM;
   bf16* conv = static_cast<bf16*>(workspace);
   hipStream_t st = (hipStream_t)stream;
   if (plan->n_content > 0)
     launch_conv_fwd(ea.raw, ea.order, raw_stride, ea.w, plan->content_bounds, plan->n_content_docs, plan->n_content,
-                    3 * S, plan->conv_kernel, 1, conv, st);
+                    C, plan->conv_kernel, 1, conv, st);
   launch_events_fwd(ea, conv, static_cast<bf16*>(q), static_cast<bf16*>(k), static_cast<bf16*>(v), g, beta, st);
   return check_launch("cqgdn_event_inputs_fwd");
 }
@@ -474,49 +488,50 @@ namespace {
 struct EvLayout {
   size_t dconv, dpre, gpart, qpart, cpart, qsum, dcont, dcgate, total;
 };
-EvLayout ev_layout(int n_content, int n_queries, int H, int K, bool fold) {
-  const size_t S = (size_t)H * CQGDN_HEAD_DIM;
+EvLayout ev_layout(int n_content, int n_queries, int H, int HK, int K, bool fold) {
+  const size_t SK = (size_t)HK * CQGDN_HEAD_DIM, C = 2 * SK + (size_t)H * CQGDN_HEAD_DIM;
   EvLayout l{};
   size_t o = 0;
-  l.dcont = o; o += fold ? align256((size_t)n_content * 3 * S * sizeof(bf16)) : 0;
+  l.dcont = o; o += fold ? align256((size_t)n_content * C * sizeof(bf16)) : 0;
   l.dcgate = o; o += fold ? align256((size_t)n_content * 2 * H * sizeof(float)) : 0;
-  l.dconv = o; o += align256((size_t)n_content * 3 * S * sizeof(bf16));
-  l.dpre = o; o += align256((size_t)n_queries * S * sizeof(float));
+  l.dconv = o; o += align256((size_t)n_content * C * sizeof(bf16));
+  l.dpre = o; o += align256((size_t)n_queries * SK * sizeof(float));
   l.gpart = o; o += align256((size_t)n_content * 2 * H * sizeof(float));
-  l.qpart = o; o += align256((size_t)events_query_blocks(n_queries) * S * K * sizeof(float));
-  l.cpart = o; o += align256((size_t)(n_content > 0 ? conv_strips(n_content) : 0) * 3 * S * K * sizeof(float));
-  l.qsum = o; o += align256(S * K * sizeof(float));
+  l.qpart = o; o += align256((size_t)events_query_blocks(n_queries) * SK * K * sizeof(float));
+  l.cpart = o; o += align256((size_t)(n_content > 0 ? conv_strips(n_content) : 0) * C * K * sizeof(float));
+  l.qsum = o; o += align256(SK * K * sizeof(float));
   l.total = o + 256;
   return l;
 }
 }  // namespace
 
-size_t cqgdn_event_inputs_bwd_workspace_size(const cqgdn_event_plan* plan, int H) {
-  if (!plan || plan->n_content < 0 || plan->n_queries < 0 || H <= 0 || plan->conv_kernel < 2 ||
+size_t cqgdn_event_inputs_bwd_workspace_size(const cqgdn_event_plan* plan, int H, int key_heads) {
+  if (!plan || plan->n_content < 0 || plan->n_queries < 0 || H <= 0 || key_heads <= 0 || plan->conv_kernel < 2 ||
       plan->conv_kernel > 4)
     return 0;
-  return ev_layout(plan->n_content, plan->n_queries, H, plan->conv_kernel, plan->n_fold_rows > 0).total;
+  return ev_layout(plan->n_content, plan->n_queries, H, key_heads, plan->conv_kernel, plan->n_fold_rows > 0).total;
 }
 
-int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, const void* raw, int64_t raw_stride, const void* a,
-                           int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
+int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, int key_heads, const void* raw, int64_t raw_stride,
+                           const void* a, int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
                            const float* A_log, const float* dt_bias, const void* dq, const void* dk, const void* dv,
                            const float* dg, const float* dbeta, void* d_raw, int64_t d_raw_stride, void* d_a,
                            int64_t d_a_stride, void* d_b, int64_t d_b_stride, float* dweight, float* dgate,
                            void* workspace, size_t workspace_bytes, void* stream) {
   EvArgs ea;
-  if (const int e = ev_args(plan, H, raw, raw_stride, a, a_stride, b, b_stride, conv_weight, A_log, dt_bias, ea))
+  if (const int e = ev_args(plan, H, key_heads, raw, raw_stride, a, a_stride, b, b_stride, conv_weight, A_log,
+                            dt_bias, ea))
     return e;
-  const int64_t S = (int64_t)H * CQGDN_HEAD_DIM;
+  const int64_t C = (int64_t)(2 * key_heads + H) * CQGDN_HEAD_DIM;
   if (plan->n_events > 0 && (!dq || !dk || !dv || !dg || !dbeta || !aligned(dq, 16) || !aligned(dk, 16) ||
                              !aligned(dv, 16)))
     return fail(CQGDN_EINVAL, "dq, dk, dv (16-byte aligned), dg, dbeta must be non-null");
   if (!d_raw || !d_a || !d_b || !dweight || !dgate || !aligned(d_raw, 16) || !aligned(dweight, 16))
     return fail(CQGDN_EINVAL, "d_raw (16-byte aligned), d_a, d_b, dweight (16-byte aligned), dgate must be non-null");
-  if (d_raw_stride < 3 * S || d_raw_stride % 8 || d_a_stride < H || d_b_stride < H)
+  if (d_raw_stride < C || d_raw_stride % 8 || d_a_stride < H || d_b_stride < H)
     return fail(CQGDN_EINVAL, "gradient strides must match the input layouts");
   const bool fold = plan->n_fold_rows > 0;
-  const EvLayout l = ev_layout(plan->n_content, plan->n_queries, H, plan->conv_kernel, fold);
+  const EvLayout l = ev_layout(plan->n_content, plan->n_queries, H, key_heads, plan->conv_kernel, fold);
   if (!workspace || !aligned(workspace, 256) || workspace_bytes < l.total)
     return fail(CQGDN_EINVAL, "workspace must be 256-byte aligned and >= cqgdn_event_inputs_bwd_workspace_size");
   uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -539,23 +554,25 @@ size_t cqgdn_layer_decode_workspace_size(int N, int H) {
   return 0;  // the step needs no workspace
 }
 
-int cqgdn_layer_decode_step(int N, int H, int conv_kernel, const void* proj, int64_t proj_stride, void* conv_history,
-                            const void* conv_weight, const float* A_log, const float* dt_bias,
+int cqgdn_layer_decode_step(int N, int H, int key_heads, int conv_kernel, const void* proj, int64_t proj_stride,
+                            void* conv_history, const void* conv_weight, const float* A_log, const float* dt_bias,
                             const float* norm_weight, float eps, float scale, float* state, void* out, void* workspace,
                             size_t workspace_bytes, void* stream) {
-  if (N < 0 || (H != 4 && H != 8 && H != 16 && H != 32) || conv_kernel < 2 || conv_kernel > 4)
-    return fail(CQGDN_EINVAL, "invalid sizes N=%d H=%d conv_kernel=%d", N, H, conv_kernel);
+  const int gshift = head_group_shift(H, key_heads);
+  if (N < 0 || gshift < 0 || conv_kernel < 2 || conv_kernel > 4)
+    return fail(CQGDN_EINVAL, "invalid sizes N=%d H=%d key_heads=%d conv_kernel=%d", N, H, key_heads, conv_kernel);
   if (N == 0) return ok();
-  const int64_t S = (int64_t)H * CQGDN_HEAD_DIM;
-  if (proj_stride < 4 * S + 2 * H || proj_stride % 8)
-    return fail(CQGDN_EINVAL, "proj_stride must be >= 4*H*128 + 2*H and a multiple of 8");
+  const int64_t C = (int64_t)(2 * key_heads + H) * CQGDN_HEAD_DIM, SV = (int64_t)H * CQGDN_HEAD_DIM;
+  if (proj_stride < C + SV + 2 * H || proj_stride % 8)
+    return fail(CQGDN_EINVAL, "proj_stride must be >= (2*key_heads + 2*H)*128 + 2*H and a multiple of 8");
   if (!proj || !conv_history || !conv_weight || !A_log || !dt_bias || !norm_weight || !state || !out ||
       !aligned(proj, 16) || !aligned(conv_history, 16) || !aligned(out, 16) || !aligned(norm_weight, 16))
     return fail(CQGDN_EINVAL, "null or misaligned buffer (proj, conv_history, out, norm_weight need 16 bytes)");
   (void)workspace;  // none needed (see cqgdn_layer_decode_workspace_size)
   (void)workspace_bytes;
   hipStream_t st = (hipStream_t)stream;
-  const DecArgs a{N, H, conv_kernel, static_cast<const bf16*>(proj), proj_stride, static_cast<bf16*>(conv_history),
+  const DecArgs a{N, H, key_heads, gshift, conv_kernel, static_cast<const bf16*>(proj), proj_stride,
+                  static_cast<bf16*>(conv_history),
                   static_cast<const bf16*>(conv_weight), A_log, dt_bias};
   launch_decode_step(a, state, norm_weight, eps, scale, static_cast<bf16*>(out), st);
   return check_launch("cqgdn_layer_decode_step");

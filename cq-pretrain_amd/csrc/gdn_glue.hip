@@ -122,8 +122,17 @@ __global__ __launch_bounds__(256) void zero_rows_kernel(bf16* __restrict__ x, co
 // conv output, the CQ query conv from the content history, the q/k/v gathers by
 // event_q / event_write and the gate math, in one pass over the events; the
 // backward walks the inverse maps, so every output row is written once and no
-// atomics are used.  A workgroup has S / 8 threads (S = H * 128 channels, 8 per
-// thread); EvArgs documents the index arrays.
+// atomics are used.  A workgroup has SV / 8 threads (SV = H * 128 value
+// channels, 8 per thread); EvArgs documents the index arrays and the channel
+// layout.  With fewer key heads than value heads the event rows repeat each
+// key head for its G value heads, and the backward sums each group's q and k
+// gradients (in fp32) into the key head's channels.
+
+// key channel of value channel c: the same column of key head (c / 128) >> gshift
+__device__ __forceinline__ int key_channel(int c, int gshift) { return (((c >> 7) >> gshift) << 7) | (c & 127); }
+
+// first value channel of key channel c's group (the others follow 128 apart)
+__device__ __forceinline__ int group_channel(int c, int gshift) { return (((c >> 7) << gshift) << 7) | (c & 127); }
 
 __device__ __forceinline__ float softplus_f(float x) {  // torch's softplus (threshold 20)
   return x > 20.f ? x : log1pf(__expf(x));
@@ -158,27 +167,28 @@ template <int K>
 __global__ __launch_bounds__(512) void events_fwd_kernel(EvArgs a, const bf16* __restrict__ conv, bf16* __restrict__ q,
                                                         bf16* __restrict__ k, bf16* __restrict__ v,
                                                         float* __restrict__ g, float* __restrict__ beta) {
-  const int e = blockIdx.x, S = a.H * GN_D, c = threadIdx.x * 8;
+  const int e = blockIdx.x, SK = a.HK * GN_D, SV = a.H * GN_D, C = 2 * SK + SV, c = threadIdx.x * 8;
+  const int ck = key_channel(c, a.gshift);
   const int sq = a.eq[e], sw = a.ew[e];
   bf16x8 q8;
   if (sq < a.n_c) {
-    q8 = ld8(conv + (int64_t)sq * 3 * S + c);
+    q8 = ld8(conv + (int64_t)sq * C + ck);
   } else {
     f32x8 wk[K], x[K];
-    ld_taps<K>(a.w, c, wk);
-    f32x8 pre = query_pre<K>(a, sq - a.n_c, c, wk, x);
+    ld_taps<K>(a.w, ck, wk);
+    f32x8 pre = query_pre<K>(a, sq - a.n_c, ck, wk, x);
 #pragma unroll
     for (int ch = 0; ch < 8; ++ch) pre[ch] *= sigm(pre[ch]);
     q8 = cvt8(pre);
   }
   bf16x8 k8 = bf16x8{}, v8 = bf16x8{};
   if (sw < a.n_c) {
-    k8 = ld8(conv + (int64_t)sw * 3 * S + S + c);
-    v8 = ld8(conv + (int64_t)sw * 3 * S + 2 * S + c);
+    k8 = ld8(conv + (int64_t)sw * C + SK + ck);
+    v8 = ld8(conv + (int64_t)sw * C + 2 * SK + c);
   }
-  st8(q + (int64_t)e * S + c, q8);
-  st8(k + (int64_t)e * S + c, k8);
-  st8(v + (int64_t)e * S + c, v8);
+  st8(q + (int64_t)e * SV + c, q8);
+  st8(k + (int64_t)e * SV + c, k8);
+  st8(v + (int64_t)e * SV + c, v8);
   if (threadIdx.x < a.H) {
     const int h = threadIdx.x;
     float gv = 0.f, bv = 0.f;
@@ -194,18 +204,26 @@ __global__ __launch_bounds__(512) void events_fwd_kernel(EvArgs a, const bf16* _
 }
 
 // content row cr: dconv[cr] = (sum of dq over the events reading q of cr, dk and dv of
-// the event writing cr); gate gradients into the a/b columns of hidden row order[cr];
-// dA_log / dt_bias partials [cr][2H]
+// the event writing cr; q and k summed over each key head's value heads); gate
+// gradients into the a/b columns of hidden row order[cr]; dA_log / dt_bias partials [cr][2H]
 __global__ __launch_bounds__(512) void events_bwd_content_kernel(EvArgs a, EvGrads d, bf16* __restrict__ dconv,
                                                                 float* __restrict__ gpart) {
-  const int cr = blockIdx.x, S = a.H * GN_D, c = threadIdx.x * 8;
+  const int cr = blockIdx.x, SK = a.HK * GN_D, SV = a.H * GN_D, c = threadIdx.x * 8;
   const int we = a.winv[cr];
-  f32x8 acc = f32x8{};
-  for (int p = a.qptr[cr]; p < a.qptr[cr + 1]; ++p) acc += cvtf8(ld8(d.dq + (int64_t)a.qlist[p] * S + c));
-  bf16* out = dconv + (int64_t)cr * 3 * S;
-  st8(out + c, cvt8(acc));
-  st8(out + S + c, we >= 0 ? ld8(d.dk + (int64_t)we * S + c) : bf16x8{});
-  st8(out + 2 * S + c, we >= 0 ? ld8(d.dv + (int64_t)we * S + c) : bf16x8{});
+  bf16* out = dconv + (int64_t)cr * (2 * SK + SV);
+  if (c < SK) {  // key channel c
+    const int G = 1 << a.gshift, c0 = group_channel(c, a.gshift);
+    f32x8 acc = f32x8{}, kacc = f32x8{};
+    for (int p = a.qptr[cr]; p < a.qptr[cr + 1]; ++p) {
+      const bf16* row = d.dq + (int64_t)a.qlist[p] * SV + c0;
+      for (int g = 0; g < G; ++g) acc += cvtf8(ld8(row + g * GN_D));
+    }
+    if (we >= 0)
+      for (int g = 0; g < G; ++g) kacc += cvtf8(ld8(d.dk + (int64_t)we * SV + c0 + g * GN_D));
+    st8(out + c, cvt8(acc));
+    st8(out + SK + c, cvt8(kacc));
+  }
+  st8(out + 2 * SK + c, we >= 0 ? ld8(d.dv + (int64_t)we * SV + c) : bf16x8{});
   if (threadIdx.x < a.H) {
     const int h = threadIdx.x;
     const int64_t row = a.order[cr];
@@ -232,10 +250,10 @@ __global__ __launch_bounds__(512) void events_bwd_content_kernel(EvArgs a, EvGra
 }
 
 constexpr int EVQ_WAVES = 4;
-// queries j = EVQ_WAVES blockIdx.x + wave, + EVQ_WAVES gridDim.x, ... for 512 channels (blockIdx.y): dpre[j] = dq of
-// the event reading j times silu'(pre); raw gradient of the query's own row (tap K-1; its
-// k/v channels and gates get zeros); query-conv weight partials [blockIdx.x][S][K].  The
-// next query's dq row and tap rows are requested before the current one computes.
+// queries j = EVQ_WAVES blockIdx.x + wave, + EVQ_WAVES gridDim.x, ... for 512 key channels (blockIdx.y): dpre[j] =
+// dq of the event reading j (summed over the key head's value heads) times silu'(pre); raw gradient of
+// the query's own row (tap K-1; its k/v channels and gates get zeros); query-conv weight partials
+// [blockIdx.x][SK][K].  The next query's dq rows and tap rows are requested before the current one computes.
 template <int K>
 __global__ __launch_bounds__(64 * EVQ_WAVES) void events_bwd_query_kernel(EvArgs a, EvGrads d,
                                                                         float* __restrict__ dpre,
@@ -243,15 +261,18 @@ __global__ __launch_bounds__(64 * EVQ_WAVES) void events_bwd_query_kernel(EvArgs
   // EVQ_WAVES waves per workgroup, each walking its own queries (the index
   // loads of a query are dependent, so queries in flight are what hides them);
   // the waves' weight partials are summed in LDS in a fixed order.
-  const int S = a.H * GN_D, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int c = (blockIdx.y * 64 + lane) * 8;
+  const int SK = a.HK * GN_D, SV = a.H * GN_D, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = (blockIdx.y * 64 + lane) * 8, G = 1 << a.gshift, c0 = group_channel(c, a.gshift);
   f32x8 wk[K], dw[K];
   ld_taps<K>(a.w, c, wk);
 #pragma unroll
   for (int i = 0; i < K; ++i) dw[i] = f32x8{};
-  bf16x8 nq = bf16x8{}, nx[K];
+  bf16x8 nq[EV_MAX_GROUP], nx[K];
   auto fetch = [&](int j) {
-    nq = ld8(d.dq + (int64_t)a.qev[j] * S + c);
+    const bf16* row = d.dq + (int64_t)a.qev[j] * SV + c0;
+#pragma unroll
+    for (int g = 0; g < EV_MAX_GROUP; ++g)
+      if (g < G) nq[g] = ld8(row + g * GN_D);
     nx[K - 1] = ld8(a.raw + (int64_t)a.qsource[j] * a.raw_stride + c);
 #pragma unroll
     for (int i = 0; i < K - 1; ++i) {
@@ -263,7 +284,9 @@ __global__ __launch_bounds__(64 * EVQ_WAVES) void events_bwd_query_kernel(EvArgs
   int j = EVQ_WAVES * blockIdx.x + wave;
   if (j < a.n_q) fetch(j);
   for (; j < a.n_q; j += stride) {
-    bf16x8 cq = nq, cx[K];
+    bf16x8 cq[EV_MAX_GROUP], cx[K];
+#pragma unroll
+    for (int g = 0; g < EV_MAX_GROUP; ++g) cq[g] = nq[g];
 #pragma unroll
     for (int i = 0; i < K; ++i) cx[i] = nx[i];
     if (j + stride < a.n_q) fetch(j + stride);
@@ -273,13 +296,16 @@ __global__ __launch_bounds__(64 * EVQ_WAVES) void events_bwd_query_kernel(EvArgs
       x[i] = cvtf8(cx[i]);
       pre += wk[i] * x[i];
     }
-    f32x8 dp = cvtf8(cq);
+    f32x8 dp = cvtf8(cq[0]);
+#pragma unroll
+    for (int g = 1; g < EV_MAX_GROUP; ++g)
+      if (g < G) dp += cvtf8(cq[g]);
 #pragma unroll
     for (int ch = 0; ch < 8; ++ch) {
       const float sg = sigm(pre[ch]);
       dp[ch] *= sg * (1.f + pre[ch] * (1.f - sg));
     }
-    float* dpj = dpre + (int64_t)j * S + c;
+    float* dpj = dpre + (int64_t)j * SK + c;
     *reinterpret_cast<f32x4*>(dpj) = f32x4{dp[0], dp[1], dp[2], dp[3]};
     *reinterpret_cast<f32x4*>(dpj + 4) = f32x4{dp[4], dp[5], dp[6], dp[7]};
 #pragma unroll
@@ -287,8 +313,8 @@ __global__ __launch_bounds__(64 * EVQ_WAVES) void events_bwd_query_kernel(EvArgs
     const int64_t row = a.qsource[j];
     bf16* dr = d.draw + row * d.draw_stride;
     st8(dr + c, cvt8(dp * wk[K - 1]));
-    st8(dr + S + c, bf16x8{});
-    st8(dr + 2 * S + c, bf16x8{});
+    st8(dr + SK + c, bf16x8{});
+    for (int g = 0; g < G; ++g) st8(dr + 2 * SK + g * SK + c, bf16x8{});  // the SV = G SK value channels
     if (blockIdx.y == 0 && lane < a.H) {
       d.da[row * d.da_stride + lane] = (bf16)0.f;
       d.db[row * d.db_stride + lane] = (bf16)0.f;
@@ -305,7 +331,7 @@ __global__ __launch_bounds__(64 * EVQ_WAVES) void events_bwd_query_kernel(EvArgs
     for (int w = 0; w < EVQ_WAVES - 1; ++w)
 #pragma unroll
       for (int i = 0; i < K; ++i) dw[i] += red[w][i][lane];
-    float* p = wpart + ((int64_t)blockIdx.x * S + c) * K;
+    float* p = wpart + ((int64_t)blockIdx.x * SK + c) * K;
 #pragma unroll
     for (int ch = 0; ch < 8; ++ch)
 #pragma unroll
@@ -315,15 +341,16 @@ __global__ __launch_bounds__(64 * EVQ_WAVES) void events_bwd_query_kernel(EvArgs
 
 // after the conv backward wrote the raw gradient of content row cr = hrows[blockIdx.x]:
 // add the query convs' history taps, sum over (j, i) with qhist[j][i] == cr of dpre[j] w[., i]
+// (key channels c: SK / 8 threads)
 template <int K>
 __global__ __launch_bounds__(512) void events_bwd_history_kernel(EvArgs a, EvGrads d, const float* __restrict__ dpre) {
-  const int cr = a.hrows[blockIdx.x], S = a.H * GN_D, c = threadIdx.x * 8;
+  const int cr = a.hrows[blockIdx.x], SK = a.HK * GN_D, C = 2 * SK + a.H * GN_D, c = threadIdx.x * 8;
   f32x8 wk[K];
   ld_taps<K>(a.w, c, wk);
   f32x8 acc = f32x8{};
   for (int p = a.hptr[cr]; p < a.hptr[cr + 1]; ++p) {
     const int code = a.hlist[p], j = code / (K - 1), i = code - j * (K - 1);
-    const float* dpj = dpre + (int64_t)j * S + c;
+    const float* dpj = dpre + (int64_t)j * SK + c;
     const f32x4 lo = *reinterpret_cast<const f32x4*>(dpj), hi = *reinterpret_cast<const f32x4*>(dpj + 4);
     f32x8 wi = wk[0];
 #pragma unroll
@@ -331,7 +358,7 @@ __global__ __launch_bounds__(512) void events_bwd_history_kernel(EvArgs a, EvGra
       if (i == t) wi = wk[t];
     acc += f32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]} * wi;
   }
-  bf16* dr = d.dcont ? d.dcont + (int64_t)cr * 3 * S + c : d.draw + (int64_t)a.order[cr] * d.draw_stride + c;
+  bf16* dr = d.dcont ? d.dcont + (int64_t)cr * C + c : d.draw + (int64_t)a.order[cr] * d.draw_stride + c;
   st8(dr, cvt8(cvtf8(ld8(dr)) + acc));
 }
 
@@ -340,12 +367,12 @@ __global__ __launch_bounds__(512) void events_bwd_history_kernel(EvArgs a, EvGra
 // and b gradients likewise -- the backward of the reference's
 // raw.index_select(0, content_order) when content_order repeats a row.
 __global__ __launch_bounds__(512) void events_bwd_fold_kernel(EvArgs a, EvGrads d) {
-  const int row = d.fold_rows[blockIdx.x], S = a.H * GN_D;
+  const int row = d.fold_rows[blockIdx.x], C = (2 * a.HK + a.H) * GN_D;
   const int p0 = d.fold_ptr[blockIdx.x], p1 = d.fold_ptr[blockIdx.x + 1];
   bf16* dr = d.draw + (int64_t)row * d.draw_stride;
-  for (int c = threadIdx.x * 8; c < 3 * S; c += blockDim.x * 8) {
+  for (int c = threadIdx.x * 8; c < C; c += blockDim.x * 8) {
     f32x8 acc = f32x8{};
-    for (int p = p0; p < p1; ++p) acc += cvtf8(ld8(d.dcont + (int64_t)d.fold_list[p] * 3 * S + c));
+    for (int p = p0; p < p1; ++p) acc += cvtf8(ld8(d.dcont + (int64_t)d.fold_list[p] * C + c));
     st8(dr + c, cvt8(acc));
   }
   if (threadIdx.x < 2 * a.H) {
@@ -378,14 +405,14 @@ void launch_events_fwd(const EvArgs& a, const bf16* conv, bf16* q, bf16* k, bf16
 
 void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content_bounds, int n_content_docs,
                        const EvWork& w, hipStream_t stream) {
-  const int S = a.H * GN_D, H = a.H;
-  const dim3 block(H * 16);
+  const int SK = a.HK * GN_D, C = 2 * SK + a.H * GN_D, H = a.H;
+  const dim3 block(H * 16), kblock(a.HK * 16);
   if (a.n_c > 0) {
     hipLaunchKernelGGL(events_bwd_content_kernel, dim3(a.n_c), block, 0, stream, a, d, w.dconv, w.gpart);
   }
   const int qb = events_query_blocks(a.n_q);
   if (qb > 0) {
-    const dim3 qgrid(qb, S / 512);
+    const dim3 qgrid(qb, SK / 512);
     switch (a.K) {
       case 2: hipLaunchKernelGGL(events_bwd_query_kernel<2>, qgrid, dim3(64 * EVQ_WAVES), 0, stream, a, d, w.dpre, w.qpart); break;
       case 3: hipLaunchKernelGGL(events_bwd_query_kernel<3>, qgrid, dim3(64 * EVQ_WAVES), 0, stream, a, d, w.dpre, w.qpart); break;
@@ -394,26 +421,26 @@ void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content
   }
   if (a.n_c > 0) {
     if (d.dcont)  // per-content-row gradients, folded into the hidden rows below
-      launch_conv_bwd(a.raw, a.order, a.raw_stride, a.w, w.dconv, content_bounds, n_content_docs, a.n_c, 3 * S,
-                      a.K, 1, d.dcont, nullptr, 3 * S, d.dw, w.cpart, stream);
+      launch_conv_bwd(a.raw, a.order, a.raw_stride, a.w, w.dconv, content_bounds, n_content_docs, a.n_c, C,
+                      a.K, 1, d.dcont, nullptr, C, d.dw, w.cpart, stream);
     else
-      launch_conv_bwd(a.raw, a.order, a.raw_stride, a.w, w.dconv, content_bounds, n_content_docs, a.n_c, 3 * S,
+      launch_conv_bwd(a.raw, a.order, a.raw_stride, a.w, w.dconv, content_bounds, n_content_docs, a.n_c, C,
                       a.K, 1, d.draw, a.order, d.draw_stride, d.dw, w.cpart, stream);
   } else {
-    launch_colsum(w.cpart, 0, 3 * S * a.K, d.dw, stream);  // zeros
+    launch_colsum(w.cpart, 0, C * a.K, d.dw, stream);  // zeros
   }
   if (a.n_hrows > 0) {
     switch (a.K) {
-      case 2: hipLaunchKernelGGL(events_bwd_history_kernel<2>, dim3(a.n_hrows), block, 0, stream, a, d, w.dpre); break;
-      case 3: hipLaunchKernelGGL(events_bwd_history_kernel<3>, dim3(a.n_hrows), block, 0, stream, a, d, w.dpre); break;
-      default: hipLaunchKernelGGL(events_bwd_history_kernel<4>, dim3(a.n_hrows), block, 0, stream, a, d, w.dpre); break;
+      case 2: hipLaunchKernelGGL(events_bwd_history_kernel<2>, dim3(a.n_hrows), kblock, 0, stream, a, d, w.dpre); break;
+      case 3: hipLaunchKernelGGL(events_bwd_history_kernel<3>, dim3(a.n_hrows), kblock, 0, stream, a, d, w.dpre); break;
+      default: hipLaunchKernelGGL(events_bwd_history_kernel<4>, dim3(a.n_hrows), kblock, 0, stream, a, d, w.dpre); break;
     }
   }
   if (d.dcont && d.n_fold > 0)
     hipLaunchKernelGGL(events_bwd_fold_kernel, dim3(d.n_fold), dim3(512), 0, stream, a, d);
   launch_colsum(w.gpart, a.n_c, 2 * H, d.dgate, stream);
-  launch_colsum(w.qpart, qb, S * a.K, w.qsum, stream);
-  hipLaunchKernelGGL(add_f32_kernel, dim3((S * a.K + 255) / 256), dim3(256), 0, stream, d.dw, w.qsum, S * a.K);
+  launch_colsum(w.qpart, qb, SK * a.K, w.qsum, stream);  // the query conv's taps: the q channels, first in dw
+  hipLaunchKernelGGL(add_f32_kernel, dim3((SK * a.K + 255) / 256), dim3(256), 0, stream, d.dw, w.qsum, SK * a.K);
 }
 
 
@@ -428,24 +455,28 @@ void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content
 //   identity and only its output is computed
 //   recurrence (as recurrent_kernel): S <- exp(g) S; S <- S + k ((v - S k) beta)^T; o = scale S q
 //   out = gated RMSNorm(o) with z from the row's projection (as gnorm_fwd_kernel)
-// One launch, one workgroup of 8 waves per (sequence, head): head h's q, k, v
-// channels, conv history and gates belong to its workgroup alone; the waves own
+// One launch, one workgroup of 8 waves per (sequence, value head h): head h's v
+// channels and gates belong to its workgroup alone, and so do the q and k
+// channels of its key head when key and value heads are equal; the waves own
 // 16 state rows each (the layout of recurrent_kernel), so the head's whole output
 // is in the workgroup for the norm.  q, k, v and o are rounded to bf16 where the
-// separate kernels stored them, with the same 16- and 32-lane sums.
+// separate kernels stored them, with the same 16- and 32-lane sums.  With G > 1
+// value heads per key head, G workgroups read one key head's q and k history, so
+// none of them shifts it: hist_shift_qk_kernel does, in a second launch.
 template <int K>
 __global__ __launch_bounds__(512) void decode_step_kernel(DecArgs a, float* __restrict__ state,
                                                           const float* __restrict__ norm_w, float eps, float scale,
                                                           bf16* __restrict__ out) {
-  const int n = blockIdx.x / a.H, h = blockIdx.x % a.H, S = a.H * GN_D;
+  const int n = blockIdx.x / a.H, h = blockIdx.x % a.H, SK = a.HK * GN_D, SV = a.H * GN_D, C = 2 * SK + SV;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bf16* rc = a.proj + (int64_t)n * 2 * a.row_stride;  // the sampled token's row
   const bf16* rq = rc + a.row_stride;                       // the text-mask query's row
   __shared__ __attribute__((aligned(16))) float qs[2][GN_D], ks[GN_D], vs[GN_D], ys[2][GN_D];
   __shared__ float gb[2];
   if (tid < 48) {  // block p (q, k, v) of head h's channels: 16 lanes x 8 channels
-    const int p = tid >> 4, l = tid & 15, c = p * S + h * GN_D + l * 8;
-    bf16* hist = a.hist + (int64_t)n * (K - 1) * 3 * S;
+    const int p = tid >> 4, l = tid & 15;
+    const int c = (p == 2 ? 2 * SK + h * GN_D : p * SK + (h >> a.gshift) * GN_D) + l * 8;
+    bf16* hist = a.hist + (int64_t)n * (K - 1) * C;
     f32x8 wk[K];
     ld_taps<K>(a.w, c, wk);
     const bf16x8 xc8 = ld8(rc + c);
@@ -454,7 +485,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(DecArgs a, float* __re
     f32x8 pre = wk[K - 1] * xc;
 #pragma unroll
     for (int j = 0; j < K - 1; ++j) {
-      h8[j] = ld8(hist + (int64_t)j * 3 * S + c);
+      h8[j] = ld8(hist + (int64_t)j * C + c);
       pre += wk[j] * cvtf8(h8[j]);
     }
 #pragma unroll
@@ -467,9 +498,11 @@ __global__ __launch_bounds__(512) void decode_step_kernel(DecArgs a, float* __re
 #pragma unroll
       for (int ch = 0; ch < 8; ++ch) query[ch] *= sigm(query[ch]);
     }
+    if (p == 2 || a.gshift == 0) {
 #pragma unroll
-    for (int j = 0; j + 1 < K - 1; ++j) st8(hist + (int64_t)j * 3 * S + c, h8[j + 1]);
-    st8(hist + (int64_t)(K - 2) * 3 * S + c, xc8);
+      for (int j = 0; j + 1 < K - 1; ++j) st8(hist + (int64_t)j * C + c, h8[j + 1]);
+      st8(hist + (int64_t)(K - 2) * C + c, xc8);
+    }
     float sp = 0.f, sqq = 0.f;
 #pragma unroll
     for (int ch = 0; ch < 8; ++ch) {
@@ -490,9 +523,9 @@ __global__ __launch_bounds__(512) void decode_step_kernel(DecArgs a, float* __re
       }
     }
   } else if (tid == 64) {
-    const float av = (float)rc[4 * S + h] + a.dt_bias[h];
+    const float av = (float)rc[C + SV + h] + a.dt_bias[h];
     gb[0] = -__expf(a.A_log[h]) * softplus_f(av);
-    gb[1] = sigm((float)rc[4 * S + a.H + h]);
+    gb[1] = sigm((float)rc[C + SV + a.H + h]);
   }
   __syncthreads();
   {
@@ -534,7 +567,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(DecArgs a, float* __re
     const int64_t r = (int64_t)n * 2 + e;
     const f32x4 y0 = *reinterpret_cast<const f32x4*>(&ys[e][l * 8]), y1 = *reinterpret_cast<const f32x4*>(&ys[e][l * 8 + 4]);
     const f32x8 v = f32x8{y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
-    const f32x8 zz = cvtf8(ld8(a.proj + r * a.row_stride + 3 * S + h * GN_D + l * 8));
+    const f32x8 zz = cvtf8(ld8(a.proj + r * a.row_stride + C + h * GN_D + l * 8));
     const f32x8 wv = ld_w8(norm_w, l);
     float ss = 0.f;
 #pragma unroll
@@ -547,6 +580,15 @@ __global__ __launch_bounds__(512) void decode_step_kernel(DecArgs a, float* __re
   }
 }
 
+// The q and k history channels of sequence blockIdx.x shift by one row and take the
+// sampled token's raw row (after decode_step_kernel has read them; 2 SK / 8 threads).
+__global__ __launch_bounds__(1024) void hist_shift_qk_kernel(DecArgs a) {
+  const int n = blockIdx.x, C = (2 * a.HK + a.H) * GN_D, c = threadIdx.x * 8;
+  bf16* hist = a.hist + (int64_t)n * (a.K - 1) * C + c;
+  for (int j = 0; j + 1 < a.K - 1; ++j) st8(hist + (int64_t)j * C, ld8(hist + (int64_t)(j + 1) * C));
+  st8(hist + (int64_t)(a.K - 2) * C, ld8(a.proj + (int64_t)n * 2 * a.row_stride + c));
+}
+
 void launch_decode_step(const DecArgs& a, float* state, const float* norm_w, float eps, float scale, bf16* out,
                         hipStream_t stream) {
   if (a.N == 0) return;
@@ -556,6 +598,7 @@ void launch_decode_step(const DecArgs& a, float* state, const float* norm_w, flo
     case 3: hipLaunchKernelGGL(decode_step_kernel<3>, grid, block, 0, stream, a, state, norm_w, eps, scale, out); break;
     default: hipLaunchKernelGGL(decode_step_kernel<4>, grid, block, 0, stream, a, state, norm_w, eps, scale, out); break;
   }
+  if (a.gshift > 0) hipLaunchKernelGGL(hist_shift_qk_kernel, dim3(a.N), dim3(a.HK * 32), 0, stream, a);
 }
 
 int gnorm_bwd_blocks(int64_t rows, int H) {

@@ -62,8 +62,13 @@ void launch_colsum(const float* part, int parts, int n, float* out, hipStream_t 
 // Event inputs of one GatedDelta layer (gdn_glue.hip).  S = H * 128 channels per
 // q/k/v part; index arrays are device int32 (content rows are 0 .. n_c-1, n_c is
 // the zero row / "none").
+// Heads: H value heads and HK key heads, G = H / HK = 1 << gshift value heads per
+// key head (value head j reads key head j >> gshift, as the reference's
+// repeat_interleave(h // hk) does).  Projection and conv channels are
+// q [0, SK) | k [SK, 2 SK) | v [2 SK, 2 SK + SV), SK = HK * 128, SV = H * 128.
+constexpr int EV_MAX_GROUP = 8;  // H / HK with both in {4, 8, 16, 32}
 struct EvArgs {
-  int H, K, n_c, n_q, E, n_hrows;
+  int H, HK, gshift, K, n_c, n_q, E, n_hrows;
   const int32_t* order;    // [n_c] hidden row of content row c
   const int32_t* eq;       // [E] q source: content row, or n_c + query
   const int32_t* ew;       // [E] content row written, n_c for read-only events
@@ -76,18 +81,18 @@ struct EvArgs {
   const int32_t* hptr;     // [n_c + 1] CSR: entries j * (K-1) + i with qhist[j][i] == c ...
   const int32_t* hlist;    //   ... ascending
   const int32_t* hrows;    // [n_hrows] content rows with history entries
-  const bf16* raw;         // projection rows, channels [0, 3S) = q | k | v
+  const bf16* raw;         // projection rows, channels q | k | v
   int64_t raw_stride;
   const bf16* ga;          // a (H per row)
   int64_t ga_stride;
   const bf16* gb;          // b (H per row)
   int64_t gb_stride;
-  const bf16* w;           // conv weight [3S][K]
+  const bf16* w;           // conv weight [2 SK + SV][K]
   const float* A_log;      // [H]
   const float* dt_bias;    // [H]
 };
 struct EvGrads {
-  const bf16 *dq, *dk, *dv;  // [E][S]
+  const bf16 *dq, *dk, *dv;  // [E][SV] (value heads)
   const float *dg, *dbeta;   // [E][H]
   bf16* draw;                // gradient rows of raw (every hidden row of order / qsource is written)
   int64_t draw_stride;
@@ -95,13 +100,13 @@ struct EvGrads {
   int64_t da_stride;
   bf16* db;
   int64_t db_stride;
-  float* dw;     // conv weight gradient [3S][K]
+  float* dw;     // conv weight gradient [2 SK + SV][K]
   float* dgate;  // [2H]: A_log, then dt_bias
   // When content rows share hidden rows (a plan whose content_order repeats a
   // row): the content rows' raw and gate gradients go to these per-content-row
   // buffers instead of the hidden rows, and the fold pass sums them into draw,
   // da, db over the fold CSR.  Null otherwise.
-  bf16* dcont;   // [n_c][3S]
+  bf16* dcont;   // [n_c][2 SK + SV]
   float* dcgate; // [n_c][2H]: da, then db
   int n_fold;                 // distinct hidden rows of content_order (when dcont is set)
   const int32_t* fold_rows;   // [n_fold] those hidden rows
@@ -109,27 +114,26 @@ struct EvGrads {
   const int32_t* fold_list;   //   ... ascending
 };
 struct EvWork {
-  bf16* dconv;   // [n_c][3S] gradient of the conv output
-  float* dpre;   // [n_q][S] gradient of the query convs' pre-activation
+  bf16* dconv;   // [n_c][2 SK + SV] gradient of the conv output
+  float* dpre;   // [n_q][SK] gradient of the query convs' pre-activation
   float* gpart;  // [n_c][2H]
-  float* qpart;  // [events_query_blocks][S][K]
+  float* qpart;  // [events_query_blocks][SK][K]
   float* cpart;  // conv backward partials
-  float* qsum;   // [S][K]
+  float* qsum;   // [SK][K]
 };
 int events_query_blocks(int n_q);
 void launch_events_fwd(const EvArgs& a, const bf16* conv, bf16* q, bf16* k, bf16* v, float* g, float* beta,
                        hipStream_t stream);
 void launch_events_bwd(const EvArgs& a, const EvGrads& d, const int32_t* content_bounds, int n_content_docs,
                        const EvWork& w, hipStream_t stream);
-// One decode step's recurrence inputs (gdn_glue.hip).  proj rows: [N][2][row_stride]
-// (C, then Q; columns q|k|v, z, a, b); hist: bf16 [N][K-1][3S], updated in place;
-// outputs q, k, v bf16 [N][2][H][128] and g, beta fp32 [N][2][H].
+// One decode step of the layer (gdn_glue.hip).  proj rows: [N][2][row_stride]
+// (C, then Q; columns q|k|v, z, a, b); hist updated in place.
 struct DecArgs {
-  int N, H, K;
+  int N, H, HK, gshift, K;  // heads as in EvArgs
   const bf16* proj;
   int64_t row_stride;
-  bf16* hist;
-  const bf16* w;  // conv weight [3S][K]
+  bf16* hist;     // [N][K-1][2 SK + SV]
+  const bf16* w;  // conv weight [2 SK + SV][K]
   const float* A_log;
   const float* dt_bias;
 };

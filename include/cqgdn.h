@@ -249,31 +249,38 @@ typedef struct cqgdn_event_plan {
  * dt_bias) and beta = sigmoid(b) (zeros for read-only events).  Replaces
  * models/backbone_qwen35.py:166-194 (index_select, conv1d, the query conv, the
  * cat/index_select gathers and the gate math).
- *   raw: bf16 rows of 3S channels (q | k | v, S = H * 128) raw_stride apart;
- *   a, b: bf16 rows of H gate inputs, a_stride / b_stride apart (all three may be
- *   column slices of the fused projection); conv_weight: bf16 [3S][K];
- *   A_log, dt_bias: fp32 [H]; q, k, v: bf16 [n_events][H][128]; g, beta: fp32
- *   [n_events][H]; workspace: >= cqgdn_event_inputs_fwd_workspace_size bytes.
+ *   H value heads and key_heads key heads (both 4, 8, 16 or 32, key_heads
+ *   dividing H; the reference's linear_value_heads and linear_heads per rank):
+ *   value head j reads key head j / (H / key_heads), as the reference's
+ *   repeat_interleave (models/backbone_qwen35.py:182-183), so q and k come out
+ *   with H heads like v;
+ *   raw: bf16 rows of C = SK + SK + SV channels (q | k | v, SK = key_heads * 128,
+ *   SV = H * 128) raw_stride apart; a, b: bf16 rows of H gate inputs, a_stride /
+ *   b_stride apart (all three may be column slices of the fused projection);
+ *   conv_weight: bf16 [C][K]; A_log, dt_bias: fp32 [H]; q, k, v: bf16
+ *   [n_events][H][128]; g, beta: fp32 [n_events][H]; workspace: >=
+ *   cqgdn_event_inputs_fwd_workspace_size bytes.
  */
-size_t cqgdn_event_inputs_fwd_workspace_size(int n_content, int H);
-int cqgdn_event_inputs_fwd(const cqgdn_event_plan* plan, int H, const void* raw, int64_t raw_stride, const void* a,
-                           int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
+size_t cqgdn_event_inputs_fwd_workspace_size(int n_content, int H, int key_heads);
+int cqgdn_event_inputs_fwd(const cqgdn_event_plan* plan, int H, int key_heads, const void* raw, int64_t raw_stride,
+                           const void* a, int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
                            const float* A_log, const float* dt_bias, void* q, void* k, void* v, float* g, float* beta,
                            void* workspace, size_t workspace_bytes, void* stream);
 /*
  * Backward of cqgdn_event_inputs_fwd from the recurrence's gradients dq, dk, dv
  * (bf16 [n_events][H][128]) and dg, dbeta (fp32 [n_events][H]).  Writes the
  * raw, a and b gradient rows of every content and query row (d_raw, d_a, d_b,
- * same layouts as raw, a, b; other rows are not touched), dweight fp32 [3S][K]
- * and dgate fp32 [2H] (A_log, then dt_bias).  The scatters walk the plan's
+ * same layouts as raw, a, b; other rows are not touched), dweight fp32 [C][K]
+ * and dgate fp32 [2H] (A_log, then dt_bias).  A key head's q and k gradients
+ * are the sums over its value heads.  The scatters walk the plan's
  * inverse maps, so every output is written once, without atomics, and the
  * result is deterministic.  A hidden row read by several content rows
  * (n_fold_rows > 0) receives the sum of their gradients.  The workspace size
  * depends on the plan (it holds per-content-row gradients when rows are shared).
  */
-size_t cqgdn_event_inputs_bwd_workspace_size(const cqgdn_event_plan* plan, int H);
-int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, const void* raw, int64_t raw_stride, const void* a,
-                           int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
+size_t cqgdn_event_inputs_bwd_workspace_size(const cqgdn_event_plan* plan, int H, int key_heads);
+int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, int key_heads, const void* raw, int64_t raw_stride,
+                           const void* a, int64_t a_stride, const void* b, int64_t b_stride, const void* conv_weight,
                            const float* A_log, const float* dt_bias, const void* dq, const void* dk, const void* dv,
                            const float* dg, const float* dbeta, void* d_raw, int64_t d_raw_stride, void* d_a,
                            int64_t d_a_stride, void* d_b, int64_t d_b_stride, float* dweight, float* dgate,
@@ -283,21 +290,23 @@ int cqgdn_event_inputs_bwd(const cqgdn_event_plan* plan, int H, const void* raw,
  * One decode step of the GatedDelta layer for N independent sequences, each
  * advancing by one sampled content token C and one text-mask query Q.  Replaces
  * delta_step (models/decoding.py:16-78) between the layer's projection and
- * out_proj, in one launch with one workgroup per (sequence, head): the conv step
+ * out_proj, in one launch with one workgroup per (sequence, value head): the conv step
  * of C over the conv history (which then shifts in C's raw row) and Q's query
  * conv over the updated history, the l2 norms and gates; the recurrence over
  * the two events (Q read-only); the gated norm with z from the projection rows.
  * It needs no workspace: cqgdn_layer_decode_workspace_size returns 0 and
  * workspace may be NULL (both stay in the signature so that callers keep working).
+ *   Heads and channels as in cqgdn_event_inputs_fwd (with fewer key heads than
+ *   value heads a second, small launch shifts the key heads' conv history);
  *   proj: bf16 [N][2][proj_stride] (row 0 = C, row 1 = Q; columns q|k|v, z, a, b
- *   of the fused projection); conv_history: bf16 [N][K-1][3S], updated in place;
- *   conv_weight: bf16 [3S][K]; A_log, dt_bias: fp32 [H]; norm_weight: fp32 [128];
+ *   of the fused projection); conv_history: bf16 [N][K-1][C], updated in place;
+ *   conv_weight: bf16 [C][K]; A_log, dt_bias: fp32 [H]; norm_weight: fp32 [128];
  *   scale: the q scale (the reference uses 128^-0.5); state: fp32 [N][H][V][K]
  *   value-first (as cqgdn_recurrent), updated in place; out: bf16 [N][2][H][128].
  */
 size_t cqgdn_layer_decode_workspace_size(int N, int H);
-int cqgdn_layer_decode_step(int N, int H, int conv_kernel, const void* proj, int64_t proj_stride, void* conv_history,
-                            const void* conv_weight, const float* A_log, const float* dt_bias,
+int cqgdn_layer_decode_step(int N, int H, int key_heads, int conv_kernel, const void* proj, int64_t proj_stride,
+                            void* conv_history, const void* conv_weight, const float* A_log, const float* dt_bias,
                             const float* norm_weight, float eps, float scale, float* state, void* out, void* workspace,
                             size_t workspace_bytes, void* stream);
 

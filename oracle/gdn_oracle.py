@@ -331,24 +331,28 @@ def layer_decode_step(raw, z, a, b, conv_weight, A_log, dt_bias, norm_weight, hi
     """One decode step of the GatedDelta layer between its projections, the CPU path of
     models/decoding.py:16-78, in float64 for N sequences.
 
-    raw [N, 2, 3S] (row 0 the sampled content token C, row 1 the text-mask query Q), z
-    [N, 2, H, D], a, b [N, 2, H]; history [N, K-1, 3S]; state [N, H, V, K] value-first.
+    raw [N, 2, C] (row 0 the sampled content token C, row 1 the text-mask query Q; channels
+    q | k | v, C = 2 SK + SV with SK = HK * 128 key channels and SV = H * 128 value channels), z
+    [N, 2, H, D], a, b [N, 2, H]; history [N, K-1, C]; state [N, H, V, K] value-first.
     C's conv reads the history, which then shifts in C's raw row; Q's query conv reads the
-    shifted history; the recurrence applies C and then the read-only Q.
+    shifted history; with HK < H key heads, q and k repeat each key head for H // HK value
+    heads (models/decoding.py:52-53); the recurrence applies C and then the read-only Q.
     Returns (out [N, 2, H, D], history, state) without touching the inputs.
     """
     n, H, K = raw.shape[0], A_log.shape[0], conv_weight.shape[1]
-    S = H * 128
+    SV = H * 128
+    SK = (raw.shape[-1] - SV) // 2
     silu, w, x = torch.nn.functional.silu, conv_weight.double(), raw.double()
     hist = history.double()
     conv = silu(x[:, 0] * w[:, -1] + sum(hist[:, j] * w[:, j] for j in range(K - 1)))
     hist = torch.cat((hist[:, 1:], x[:, :1]), dim=1)
-    query = silu(x[:, 1, :S] * w[:S, -1] + sum(hist[:, j, :S] * w[:S, j] for j in range(K - 1)))
-    cq, k, v = conv.split(S, -1)
-    zero = torch.zeros_like(k)
-    q = torch.stack((cq, query), 1).reshape(n, 2, H, 128)
-    k = torch.stack((k, zero), 1).reshape(n, 2, H, 128)
-    v = torch.stack((v, zero), 1).reshape(n, 2, H, 128)
+    query = silu(x[:, 1, :SK] * w[:SK, -1] + sum(hist[:, j, :SK] * w[:SK, j] for j in range(K - 1)))
+    cq, k, v = conv.split((SK, SK, SV), -1)
+    zero_k, zero_v = torch.zeros_like(k), torch.zeros_like(v)
+    rep = H // (SK // 128)
+    q = torch.stack((cq, query), 1).reshape(n, 2, SK // 128, 128).repeat_interleave(rep, dim=2)
+    k = torch.stack((k, zero_k), 1).reshape(n, 2, SK // 128, 128).repeat_interleave(rep, dim=2)
+    v = torch.stack((v, zero_v), 1).reshape(n, 2, H, 128)
     g = -A_log.double().exp() * torch.nn.functional.softplus(a[:, 0].double() + dt_bias.double())
     beta = b[:, 0].double().sigmoid()
     g, beta = torch.stack((g, torch.zeros_like(g)), 1), torch.stack((beta, torch.zeros_like(beta)), 1)

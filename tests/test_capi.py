@@ -126,11 +126,17 @@ def test_layer_decode_step_arguments(lib):
     p = ctypes.c_void_p(256)
     w = ctypes.cast(p, ctypes.POINTER(ctypes.c_float))
 
-    def step(N=1, H=16, K=4, stride=4 * 16 * 128 + 32, ptr=p):
-        return lib.cqgdn_layer_decode_step(N, H, K, ptr, stride, p, p, w, w, w, 1e-6, 0.1, w, p, None, 0, None)
+    def step(N=1, H=16, HK=16, K=4, stride=4 * 16 * 128 + 32, ptr=p):
+        return lib.cqgdn_layer_decode_step(N, H, HK, K, ptr, stride, p, p, w, w, w, 1e-6, 0.1, w, p, None, 0, None)
 
     assert step(N=0) == _lib.OK  # nothing to do, nothing launched
     assert step(H=12) == _lib.EINVAL
+    assert step(HK=32) == _lib.EINVAL  # more key heads than value heads
+    assert step(HK=2) == _lib.EINVAL
+    # H = 32, key heads 8: C = (2 * 8 + 32) * 128 conv channels, then z (32 * 128), a and b (32 each)
+    assert step(H=32, HK=8, stride=(16 + 64) * 128 + 64 - 8) == _lib.EINVAL
+    assert b"proj_stride" in lib.cqgdn_last_error()
+    assert step(N=0, H=32, HK=8) == _lib.OK
     assert step(K=5) == _lib.EINVAL
     assert step(stride=4 * 16 * 128) == _lib.EINVAL  # no room for the a, b columns
     assert b"proj_stride" in lib.cqgdn_last_error()

@@ -218,13 +218,13 @@ def _image_group_rows(plan, size):
     return plan.content_order.cpu()[torch.tensor(rows)]
 
 
-def _restatement(plan, proj, H, gen):
+def _restatement(plan, proj, H, gen, HK=None):
     """Output and projection/parameter gradients of layer_core and of the reference's layer code in
     float64 on the CPU (oracle conv, recurrence and norm), from the same bf16 projection."""
     from cqgdn import events, layer
 
     S = H * 128
-    model = layer.GatedDeltaLayer(width=64, heads=H).double()
+    model = layer.GatedDeltaLayer(width=64, heads=H, key_heads=HK).double()
     with torch.no_grad():
         model.conv_weight.copy_(model.conv_weight.bfloat16().double())
         model.dt_bias.copy_(torch.randn(H, generator=gen) * 0.5)
@@ -234,7 +234,7 @@ def _restatement(plan, proj, H, gen):
     pd = proj.to(DEV).detach().requires_grad_()
     dp = [model.conv_weight.detach().bfloat16().to(DEV).requires_grad_()] + \
         [t.detach().float().to(DEV).requires_grad_() for t in params[1:]]
-    out = events.layer_core(pd, *dp, plan, heads=H)
+    out = events.layer_core(pd, *dp, plan, heads=H, key_heads=HK)
     out.backward(dout.to(DEV))
     torch.cuda.synchronize()
     p64 = proj.double().requires_grad_()
@@ -245,12 +245,12 @@ def _restatement(plan, proj, H, gen):
     return (out, pd.grad, dp), (ref, p64.grad, params)
 
 
-def _compare_layer(got, want, H):
-    S = H * 128
+def _compare_layer(got, want, H, HK=None):
+    S, C = H * 128, (2 * (HK or H) + H) * 128
     (out, dproj, dp), (ref, rproj, params) = got, want
     assert_close_bf16("out", out.detach().cpu(), ref.detach())
-    cols = {"d_qkv": slice(0, 3 * S), "d_z": slice(3 * S, 4 * S), "d_a": slice(4 * S, 4 * S + H),
-            "d_b": slice(4 * S + H, 4 * S + 2 * H)}
+    cols = {"d_q": slice(0, (C - S) // 2), "d_k": slice((C - S) // 2, C - S), "d_v": slice(C - S, C),
+            "d_z": slice(C, C + S), "d_a": slice(C + S, C + S + H), "d_b": slice(C + S + H, C + S + 2 * H)}
     for name, sl in cols.items():
         assert_close_bf16(name, dproj[:, sl].cpu(), rproj[:, sl])
     for name, a, p in zip(("d_conv_weight", "d_A_log", "d_dt_bias", "d_norm_weight"), dp, params):
@@ -455,3 +455,87 @@ def test_delta_fp16_inputs_match_oracle(gdn):
     y, grads = fwd_bwd(gdn, [q, k, v, g, b], bounds, do)
     assert y.dtype == torch.float16 and [x.dtype for x in grads] == [torch.float16] * 3 + [torch.float32] * 2
     check_against_oracle([q, k, v, g, b], bounds, do, y, grads)
+
+
+# ---- fewer key heads than value heads (models/backbone_qwen35.py:182-183, models/decoding.py:52-53)
+
+@pytest.mark.parametrize("H,HK,kind", [(32, 16, "image-CQ"), (16, 4, "two-branch")])
+def test_layer_core_fewer_key_heads(gdn, H, HK, kind):
+    """layer_core with H value heads and HK < H key heads (the Qwen3.5-9B shape per rank is 32 and
+    16) against the reference's layer code in float64, which repeat_interleaves q, k and the query
+    conv output: the output, every projection-gradient column block (the q and k blocks sum their
+    value heads' gradients) and the parameter gradients.  The two-branch plan repeats hidden rows."""
+    from cqgdn import layer
+
+    if kind == "image-CQ":
+        plan = layer.cq_layer_plan(200, 50, image_groups=(24,), seed=12)
+    else:
+        plan = layer.two_branch_plan(220, 60, prefix=30, suffix=40, image_groups=(20,), seed=13)
+    print(f"case layer core H={H} key heads={HK} ({kind}): {plan.hidden_length} rows", flush=True)
+    gen = torch.Generator().manual_seed(121 + H)
+    P = (2 * HK + 2 * H) * 128 + 2 * H
+    proj = (torch.randn(plan.hidden_length, P, generator=gen) * 0.7).bfloat16()
+    _compare_layer(*_restatement(plan, proj, H, gen, HK), H, HK)
+
+
+def _gqa_decode_params(H, HK, K, gen):
+    C = (2 * HK + H) * 128
+    w = (torch.rand(C, K, generator=gen) - 0.5).bfloat16()
+    A_log = torch.rand(H, generator=gen).mul(3).add(0.01).log()
+    dt_bias = torch.randn(H, generator=gen) * 0.5
+    nw = 1 + 0.1 * torch.randn(128, generator=gen)
+    return w, A_log, dt_bias, nw
+
+
+def test_layer_decode_step_fewer_key_heads(gdn):
+    """The layer's decode step with 32 value heads and 16 key heads against the float64 oracle step,
+    three steps, N = 3: outputs, the value-first state, and the conv history bit-exact (its key
+    channels are shifted by the second launch, after every workgroup of the step has read them)."""
+    from cqgdn import events
+
+    N, H, HK, K = 3, 32, 16, 4
+    S, C = H * 128, (2 * HK + H) * 128
+    P = C + S + 2 * H
+    print(f"case layer decode H={H} key heads={HK}", flush=True)
+    gen = torch.Generator().manual_seed(131)
+    w, A_log, dt_bias, nw = _gqa_decode_params(H, HK, K, gen)
+    hist = (torch.randn(N, K - 1, C, generator=gen) * 0.7).bfloat16()
+    state = torch.randn(N, H, 128, 128, generator=gen) * 0.05
+    cache = {"conv": hist.to(DEV), "state": state.to(DEV)}
+    ref_hist, ref_state = hist.double(), state.double()
+    dev = [t.to(DEV) for t in (w, A_log, dt_bias, nw)]
+    for step in range(3):
+        proj = (torch.randn(N, 2, P, generator=gen) * 0.7).bfloat16()
+        out = events.layer_decode_step(proj.to(DEV), *dev, cache, heads=H, key_heads=HK)
+        torch.cuda.synchronize()
+        args = (proj[..., :C], proj[..., C:C + S].reshape(N, 2, H, 128), proj[..., C + S:C + S + H],
+                proj[..., C + S + H:], w, A_log, dt_bias, nw)
+        ref_out, ref_hist, ref_state = O.layer_decode_step(*args, ref_hist, ref_state)
+        assert_close_bf16(f"out step {step}", out.cpu(), ref_out.reshape(N, 2, S))
+        assert torch.equal(cache["conv"].cpu().double(), ref_hist), "conv history differs"
+        assert_close_bf16(f"state step {step}", cache["state"].cpu(), ref_state)
+
+
+def test_layer_prefill_then_decode_fewer_key_heads(gdn):
+    """Prefill with the uncommitted target and one decode step equal the one-shot prefill of the
+    extended plan, with 16 value heads and 8 key heads."""
+    from cqgdn import events
+    from gdn_testlib import decode_plans
+
+    n, H, HK, K = 150, 16, 8, 4
+    S, C = H * 128, (2 * HK + H) * 128
+    P = C + S + 2 * H
+    print(f"case prefill -> decode H={H} key heads={HK}", flush=True)
+    gen = torch.Generator().manual_seed(141)
+    w, A_log, dt_bias, nw = (t.to(DEV) for t in _gqa_decode_params(H, HK, K, gen))
+    pre_plan, one_plan = decode_plans(n, K)
+    proj = (torch.randn(n + 2, P, generator=gen) * 0.7).bfloat16().to(DEV)
+    kw = dict(heads=H, key_heads=HK)
+    _, cache = events.layer_prefill(proj[:n + 1], w, A_log, dt_bias, nw, pre_plan, **kw)
+    assert torch.equal(cache["conv"][0], proj[n - K + 1:n, :C])
+    out = events.layer_decode_step(proj[n:n + 2], w, A_log, dt_bias, nw, cache, **kw)
+    one, one_cache = events.layer_prefill(proj, w, A_log, dt_bias, nw, one_plan, **kw)
+    torch.cuda.synchronize()
+    assert_close_bf16("C and Q rows", out.cpu(), one[n:n + 2].double().cpu())
+    assert_close_bf16("state", cache["state"].cpu(), one_cache["state"].double().cpu())
+    assert torch.equal(cache["conv"][0], proj[n - K + 2:n + 1, :C])

@@ -323,25 +323,28 @@ def test_gated_rms_norm_against_library_and_closed_form():
     assert not torch.allclose(planted, want, atol=1e-3)
 
 
-def test_layer_decode_step_equals_the_training_layer_on_the_extended_plan():
+@pytest.mark.parametrize("H,HK", [(4, 4), (8, 4)])
+def test_layer_decode_step_equals_the_training_layer_on_the_extended_plan(H, HK):
     """Prefill (state after the committed rows, conv history = the K-1 raw rows before the
     uncommitted target, models/backbone_qwen35.py:201-209) followed by one oracle decode step
     equals the training-path layer (the reference's layer code in float64 with the oracle conv,
     recurrence and norm) on the plan where the step's content token commits and its query reads
-    after it: the C and Q outputs and the final state.  A planted history without the shift
-    (Q's conv not seeing C) is caught."""
+    after it: the C and Q outputs and the final state, with equal key and value heads and with
+    two value heads per key head (the reference's repeat_interleave on both paths).  A planted
+    history without the shift (Q's conv not seeing C) is caught."""
     from cqgdn import layer
     from gdn_testlib import decode_plans
 
     torch.manual_seed(9)
-    H, n, K = 4, 20, 4
-    S = H * 128
-    model = layer.GatedDeltaLayer(width=32, heads=H).double()
+    n, K = 20, 4
+    S, SK = H * 128, HK * 128
+    C = 2 * SK + S
+    model = layer.GatedDeltaLayer(width=32, heads=H, key_heads=HK).double()
     with torch.no_grad():
         model.dt_bias.copy_(torch.randn(H) * 0.5)
         model.norm_weight.copy_(1 + 0.1 * torch.randn(128))
     pre_plan, one_plan = decode_plans(n, K)
-    proj = torch.randn(n + 2, 4 * S + 2 * H, dtype=F64) * 0.7
+    proj = torch.randn(n + 2, C + S + 2 * H, dtype=F64) * 0.7
     cv = lambda u, w, bounds: O.causal_conv1d(u, w, bounds)
     norm = O.gated_rms_norm
     states = {}
@@ -354,17 +357,18 @@ def test_layer_decode_step_equals_the_training_layer_on_the_extended_plan():
     model.core(proj[:n + 1], pre_plan, recurrence=rec, conv=cv, norm=norm, fused=False)
     want = model.core(proj, one_plan, recurrence=rec, conv=cv, norm=norm, fused=False)
     state0 = states[n + 1].transpose(-1, -2)  # value-first
-    history = proj[None, n - K + 1:n, :3 * S]
+    history = proj[None, n - K + 1:n, :C]
     rows = proj[None, n:n + 2]
-    args = (rows[..., :3 * S], rows[..., 3 * S:4 * S].reshape(1, 2, H, 128), rows[..., 4 * S:4 * S + H],
-            rows[..., 4 * S + H:], model.conv_weight, model.A_log, model.dt_bias, model.norm_weight)
+    args = (rows[..., :C], rows[..., C:C + S].reshape(1, 2, H, 128), rows[..., C + S:C + S + H],
+            rows[..., C + S + H:], model.conv_weight, model.A_log, model.dt_bias, model.norm_weight)
     out, hist, state = O.layer_decode_step(*args, history, state0)
     assert torch.allclose(out.reshape(2, S), want[n:n + 2], atol=1e-10)
     assert torch.allclose(state[0], states[n + 2][0].transpose(-1, -2), atol=1e-10)
-    assert torch.equal(hist[0], proj[n - K + 2:n + 1, :3 * S])
+    assert torch.equal(hist[0], proj[n - K + 2:n + 1, :C])
     # planted: Q's conv over the history before C entered it
-    hist_old = proj[n - K + 1:n, :S]
-    w = model.conv_weight[:S]
-    wrong_q = torch.nn.functional.silu(proj[n + 1, :S] * w[:, -1] + sum(hist_old[j] * w[:, j] for j in range(K - 1)))
-    right_q = torch.nn.functional.silu(proj[n + 1, :S] * w[:, -1] + sum(hist[0, j, :S] * w[:, j] for j in range(K - 1)))
+    hist_old = proj[n - K + 1:n, :SK]
+    w = model.conv_weight[:SK]
+    wrong_q = torch.nn.functional.silu(proj[n + 1, :SK] * w[:, -1] + sum(hist_old[j] * w[:, j] for j in range(K - 1)))
+    right_q = torch.nn.functional.silu(proj[n + 1, :SK] * w[:, -1] +
+                                       sum(hist[0, j, :SK] * w[:, j] for j in range(K - 1)))
     assert not torch.allclose(wrong_q, right_q, atol=1e-3)
