@@ -493,16 +493,16 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   __shared__ __attribute__((aligned(16))) uint8_t r3[DKW_R4A - DKW_R3];
   __shared__ __attribute__((aligned(16))) uint8_t r4a[DKW_R4B - DKW_R4A];
   __shared__ __attribute__((aligned(16))) uint8_t r4b[DKW_BYTES - DKW_R4B];
-  __shared__ float Gs[64];
+  __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ float dgw[4][64];
-  __shared__ float Rs[64];  // rsqrt norms of q (1 without normalize)
+  __shared__ __attribute__((aligned(16))) float Rs[64];  // rsqrt norms of q (1 without normalize)
   bf16* Qs = reinterpret_cast<bf16*>(r1);
   bf16* Ks = reinterpret_cast<bf16*>(r2);
   bf16* dPm = reinterpret_cast<bf16*>(r3);
   bf16* dOs = reinterpret_cast<bf16*>(r4a);
   bf16* VnT = reinterpret_cast<bf16*>(r4b);  // v_new^T [v][t], read transposed as v_new rows
   bf16* dVs = dOs;                                    // dVn tile, from phase 3 on
-  float* dqdot = reinterpret_cast<float*>(r4a + CH * D * 2);  // [4][64] after the dVn tile
+  float* dqdot = reinterpret_cast<float*>(r4a + CH * D * 2);  // [64][4 waves] after the dVn tile
   bf16* dWs = VnT;                                    // dW rows [t][k], from phase 4 on
 
   // This wave's state fragments: rows k = 16 (2 wave + mm) + r of h
@@ -590,8 +590,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
           rowE[i] += e;
           colE += e;
         }
-        colE += __shfl_xor(colE, 16, 64);
-        colE += __shfl_xor(colE, 32, 64);
+        colE = sum_rows4(colE);
         if (q4 == 0) dgl[s] -= colE;
       }
       st4(dPm + (16 * n + r) * LDT + 16 * wave + 4 * q4, dpm);  // transposed: dPm^T[s][t], 4 rows t in 8 bytes
@@ -638,16 +637,20 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       }
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
+      const f32x4 g4 = *reinterpret_cast<const f32x4*>(&Gs[16 * n + 4 * q4]);
+      f32x4 qc[2];
+#pragma unroll
+      for (int mm = 0; mm < 2; ++mm) qc[mm] = cvtf4(ld4_c(Qs, LDK, 16 * n, 16 * (2 * wave + mm)));
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = 16 * n + 4 * q4 + i;
-        const float f = scale * __expf(Gs[t]);
+        const float f = scale * __expf(g4[i]);
         float x = 0.f;
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm) {
           const float inter = a1[mm][n][i] * f;
           dQ[mm][n][i] += inter;
-          x += (float)Qs[t * LDK + 16 * (2 * wave + mm) + r] * inter;
+          x += qc[mm][i] * inter;
         }
         x = sum16(x);
         if (r == 0) dgl[t] += x;
@@ -658,21 +661,24 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   // ---- l2norm backward of dq on the phase-2 registers: this wave's parts of the row dots q_t . dq_t ----
   float pdot[4][4];
 #pragma unroll
-  for (int n = 0; n < 4; ++n)
+  for (int n = 0; n < 4; ++n) {
+    f32x4 qc[2];
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) qc[mm] = cvtf4(ld4_c(Qs, LDK, 16 * n, 16 * (2 * wave + mm)));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int t = 16 * n + 4 * q4 + i;
       float x = 0.f;
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) x += (float)Qs[t * LDK + 16 * (2 * wave + mm) + r] * dQ[mm][n][i];
+      for (int mm = 0; mm < 2; ++mm) x += qc[mm][i] * dQ[mm][n][i];
       pdot[n][i] = sum16(x);
     }
+  }
   lds_barrier();  // every read of the dO rows is done: the row dots and then the dVn tile may replace them
   if (r == 0) {
 #pragma unroll
     for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dqdot[wave * 64 + 16 * n + 4 * q4 + i] = pdot[n][i];  // after the tile's 16 KB
+      for (int i = 0; i < 4; ++i) dqdot[4 * (16 * n + 4 * q4 + i) + wave] = pdot[n][i];  // after the tile's 16 KB
   }
   lds_barrier();
   // The dS fragments (bd) requested after phase 1 have landed long since: wait
@@ -682,19 +688,24 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   wait_vmem_all();
   // dq = rq (dQ - q (q . dQ)), stored from the C layout (16 lanes: 32 contiguous bytes of a row)
 #pragma unroll
-  for (int n = 0; n < 4; ++n)
+  for (int n = 0; n < 4; ++n) {
+    const f32x4 rs = *reinterpret_cast<const f32x4*>(&Rs[16 * n + 4 * q4]);
+    f32x4 qc[2];
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm) qc[mm] = cvtf4(ld4_c(Qs, LDK, 16 * n, 16 * (2 * wave + mm)));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * n + 4 * q4 + i;
-      const float dot = dqdot[t] + dqdot[64 + t] + dqdot[128 + t] + dqdot[192 + t];
-      const float rs = Rs[t];
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dqdot[4 * t]);
+      const float dot = d4[0] + d4[1] + d4[2] + d4[3];
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
         const int k = 16 * (2 * wave + mm) + r;
-        const float x = normalize ? (dQ[mm][n][i] - (float)Qs[t * LDK + k] * dot) * rs : dQ[mm][n][i];
+        const float x = normalize ? (dQ[mm][n][i] - qc[mm][i] * dot) * rs[i] : dQ[mm][n][i];
         if (t < ci.len) dq[((size_t)(ci.start + t) * H + h) * D + k] = (bf16)x;
       }
     }
+  }
   // the dVn tile, copied global -> LDS while phase 3 runs (after the dq stores, which retire first)
   {
     const bf16* dvs = dVn + cb * (CH * D);
@@ -733,8 +744,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         const f32x4 st = a4[n] * kd;
         const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
         float e = st[0] * kk[0] + st[1] * kk[1] + st[2] * kk[2] + st[3] * kk[3];
-        e += __shfl_xor(e, 16, 64);
-        e += __shfl_xor(e, 32, 64);
+        e = sum_rows4(e);
         if (q4 == 0) dgl[t] -= e;
         esum += (q4 == 0) ? e : 0.f;
         fkp[mm][n] = keep_if(t < ci.len, a3[n] + st);
@@ -746,14 +756,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const f32x8 a = cvtf8(bh[mm][kb]), b = cvtf8(bd[mm][kb]);
-#pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8) x += a[s8] * b[s8];
-      }
+      for (int kb = 0; kb < 4; ++kb) x = dot8(bh[mm][kb], bd[mm][kb], x);
     x = sum16(x);
-    x += __shfl_xor(x, 16, 64);
-    x += __shfl_xor(x, 32, 64);
+    x = sum_rows4(x);
     if (lane == 0) dgl[ci.len - 1] += esum + __expf(glast) * x;
   }
   wait_vmem_all();  // the dVn tile has landed (the dq stores issued before it have retired too)
@@ -813,7 +818,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   bf16* S2 = VnT;                                                              // Y^T[j][t], over dW rows
   float* Bs = reinterpret_cast<float*>(r4a + 64 * LDT * 2);                   // after S1
   float* dbw = Bs + 64;                                                        // [4][64]
-  float* dkdot = dbw + 256;                                                    // [4][64]
+  float* dkdot = dbw + 256;                                                    // [64][4 waves]
   {
     const int t = tid >> 2, p = tid & 3;
     if (p == 0) Bs[t] = pb;
@@ -916,8 +921,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
           rowE[e] += e2;
           colE += e2;
         }
-        colE += __shfl_xor(colE, 16, 64);
-        colE += __shfl_xor(colE, 32, 64);
+        colE = sum_rows4(colE);
         if (q4 == 0) dgl[j] -= colE;
       }
       st4(S1 + (16 * n + r) * LDT + 16 * wave + 4 * q4, dmp);
@@ -964,8 +968,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       float xb = colB[n];
-      xb += __shfl_xor(xb, 16, 64);
-      xb += __shfl_xor(xb, 32, 64);
+      xb = sum_rows4(xb);
       if (q4 == 0) dbl[16 * n + r] += xb;
     }
   }
@@ -1007,10 +1010,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       float xb = colB[n], xg = colG[n];
-      xb += __shfl_xor(xb, 16, 64);
-      xb += __shfl_xor(xb, 32, 64);
-      xg += __shfl_xor(xg, 16, 64);
-      xg += __shfl_xor(xg, 32, 64);
+      xb = sum_rows4(xb);
+      xg = sum_rows4(xg);
       if (q4 == 0) {
         dbl[16 * n + r] += xb;
         dgl[16 * n + r] += xg;
@@ -1025,9 +1026,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * (2 * wave + mm) + 4 * q4));
         pd += kk[0] * dkr[mm][n][0] + kk[1] * dkr[mm][n][1] + kk[2] * dkr[mm][n][2] + kk[3] * dkr[mm][n][3];
       }
-      pd += __shfl_xor(pd, 16, 64);
-      pd += __shfl_xor(pd, 32, 64);
-      if (q4 == 0) dkdot[wave * 64 + t] = pd;
+      pd = sum_rows4(pd);
+      if (q4 == 0) dkdot[4 * t + wave] = pd;
     }
   }
   lds_barrier();
@@ -1036,7 +1036,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
     const int t = 16 * n + r;
-    const float dot = dkdot[t] + dkdot[64 + t] + dkdot[128 + t] + dkdot[192 + t];
+    const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dkdot[4 * t]);
+    const float dot = d4[0] + d4[1] + d4[2] + d4[3];
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const int m = 2 * wave + mm;

@@ -120,6 +120,18 @@ __device__ __forceinline__ bf16x8 ld8_tr(const bf16* tile, int ld, int k0, int n
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// C-layout column from a row-major LDS tile: lane (q4, r) gets tile[row0 + 4 q4 + e][col0 + r],
+// e = 0..3 -- the rows and column an MFMA result fragment holds -- in one ds_read_b64_tr_b16:
+// lane a of each 16-lane group addresses the 4 elements tile[row0 + 4 q4 + (a >> 2)][col0 +
+// 4 (a & 3) ..], and the instruction hands lane j element e of lane (j >> 2) + 4 e, column
+// j & 3 (the layout ld8_tr relies on).  ld and col0 multiples of 4.
+__device__ __forceinline__ bf16x4 ld4_c(const bf16* tile, int ld, int row0, int col0) {
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
+  const bf16* p = tile + (row0 + 4 * q4 + (r >> 2)) * ld + col0 + 4 * (r & 3);
+  return __builtin_bit_cast(bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p)));
+}
+
 // ---- fp16 operands ----------------------------------------------------------
 // The precise (inference) forward keeps its MFMA operands in fp16: 11 mantissa
 // bits instead of bf16's 8, at the same MFMA rate (v_mfma_f32_16x16x32_f16).
@@ -381,6 +393,32 @@ __device__ __forceinline__ float sum16(float x) {
   x += dpp_f<0x140>(x);  // row_mirror
   x += dpp_f<0x141>(x);  // row_half_mirror
   return x;
+}
+
+// sum over the four 16-lane rows (lanes r, r + 16, r + 32, r + 48: the 4 row groups of a
+// C tile), with v_permlane16_swap and v_permlane32_swap (VALU; no LDS round trip).  With
+// both operands holding x, a swap leaves rows {x0, x0, x2, x2} in the first and {x1, x1,
+// x3, x3} in the second (permlane16; permlane32 likewise with the two halves), so adding
+// them gives every lane the same bits: (x0 + x1) + (x2 + x3), as x + xor16(x), then + xor32.
+// Written as assembly with two tied operands because this compiler's builtin drops the
+// second result when both inputs are the same value; the s_nops give the swaps their
+// VALU hazard distance on both sides.
+__device__ __forceinline__ float sum_rows4(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  x = a + b;
+  float c = x, d = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(c), "+v"(d));
+  return c + d;
+}
+
+// c + sum of a[e] b[e] over 8 bf16 pairs, as four v_dot2_f32_bf16 (products and sums in fp32)
+__device__ __forceinline__ float dot8(bf16x8 a, bf16x8 b, float c) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int e = 0; e < 8; e += 2)
+    c = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{a[e], a[e + 1]}, bf16x2{b[e], b[e + 1]}, c, false);
+  return c;
 }
 
 // sum over the 4 lanes of a quad (lanes 4a .. 4a + 3), the first two levels of sum16
