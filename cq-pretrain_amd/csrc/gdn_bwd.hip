@@ -566,39 +566,55 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   const float glast = Gs[ci.len - 1];
   float* dgl = dgw[wave];
 
-  // ---- phase 1: P, dP for t-tile = wave, s-tiles <= wave ----
+  // ---- phase 1: P, dP over the ten causal (t-tile, s-tile) pairs: wave w takes t-tile w with
+  //      s-tiles 0 .. min(w, 2) and wave 0 also the (3, 3) diagonal, at most three pairs a wave ----
   {
+    // dPm of t-tile tt, s-tile n; its row sums are added to rowE, its column sums to dgl
+    auto pair = [&](int tt, int n, float(&rowE)[4]) -> f32x4 {
+      f32x4 p = zero4(), dp = zero4();
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        p = mfma(ld8(Qs + (16 * tt + r) * LDK + 32 * kb + 8 * q4), ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4), p);
+        dp = mfma(ld8(dOs + (16 * tt + r) * LDK + 32 * kb + 8 * q4), ld8_tr(VnT, LDT, 32 * kb, 16 * n), dp);
+      }
+      const int s = 16 * n + r;
+      const f32x4 g4 = *reinterpret_cast<const f32x4*>(&Gs[16 * tt + 4 * q4]);
+      const float gs = Gs[s];
+      float colE = 0.f;
+      f32x4 dpm;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * tt + 4 * q4 + i;
+        const float gam = (s <= t) ? __expf(g4[i] - gs) : 0.f;
+        dpm[i] = scale * dp[i] * gam;
+        const float e = dpm[i] * p[i];
+        rowE[i] += e;
+        colE += e;
+      }
+      colE = sum_rows4(colE);
+      if (q4 == 0) dgl[s] -= colE;
+      return dpm;
+    };
     float rowE[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      f32x4 dpm = zero4();
-      if (n <= wave) {
-        f32x4 p = zero4(), dp = zero4();
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          p = mfma(ld8(Qs + (16 * wave + r) * LDK + 32 * kb + 8 * q4), ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4), p);
-          dp = mfma(ld8(dOs + (16 * wave + r) * LDK + 32 * kb + 8 * q4), ld8_tr(VnT, LDT, 32 * kb, 16 * n), dp);
-        }
-        const int s = 16 * n + r;
-        float colE = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = 16 * wave + 4 * q4 + i;
-          const float gam = (s <= t) ? __expf(Gs[t] - Gs[s]) : 0.f;
-          dpm[i] = scale * dp[i] * gam;
-          const float e = dpm[i] * p[i];
-          rowE[i] += e;
-          colE += e;
-        }
-        colE = sum_rows4(colE);
-        if (q4 == 0) dgl[s] -= colE;
-      }
+      if (n == 3 && wave == 3) continue;  // the (3, 3) tile is wave 0's
+      const f32x4 dpm = (n <= wave) ? pair(wave, n, rowE) : zero4();
       st4(dPm + (16 * n + r) * LDT + 16 * wave + 4 * q4, dpm);  // transposed: dPm^T[s][t], 4 rows t in 8 bytes
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float x = sum16(rowE[i]);
       if (r == 0) dgl[16 * wave + 4 * q4 + i] += x;
+    }
+    if (wave == 0) {
+      float rowE3[4] = {0.f, 0.f, 0.f, 0.f};
+      st4(dPm + (48 + r) * LDT + 48 + 4 * q4, pair(3, 3, rowE3));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = sum16(rowE3[i]);
+        if (r == 0) dgl[48 + 4 * q4 + i] += x;
+      }
     }
   }
   lds_barrier();
@@ -687,6 +703,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   // stores are conditional, so the compiler could only wait for everything).
   wait_vmem_all();
   // dq = rq (dQ - q (q . dQ)), stored from the C layout (16 lanes: 32 contiguous bytes of a row)
+  const int rowb = H * D * 2;  // bytes per event row
+  {
+  const __amdgpu_buffer_rsrc_t dq_rs = chunk_rows_rsrc(dq, ci.start, ci.len, H, h);
+  const int dq_lane = 4 * q4 * rowb + (32 * wave + r) * 2;
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
     const f32x4 rs = *reinterpret_cast<const f32x4*>(&Rs[16 * n + 4 * q4]);
@@ -700,11 +720,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       const float dot = d4[0] + d4[1] + d4[2] + d4[3];
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
-        const int k = 16 * (2 * wave + mm) + r;
         const float x = normalize ? (dQ[mm][n][i] - qc[mm][i] * dot) * rs[i] : dQ[mm][n][i];
-        if (t < ci.len) dq[((size_t)(ci.start + t) * H + h) * D + k] = (bf16)x;
+        buf_st1(dq_rs, dq_lane + 32 * mm, (16 * n + i) * rowb, x);  // row t = 16 n + 4 q4 + i, column k
       }
     }
+  }
   }
   // the dVn tile, copied global -> LDS while phase 3 runs (after the dq stores, which retire first)
   {
@@ -786,17 +806,16 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       const int t = 16 * n + r;
-      bf16x8 av[4];  // -dVn row t, value block kb
+      bf16x8 av[4];  // dVn row t, value block kb
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-        av[kb] = keep_if(t < ci.len, neg8(ld8(dVs + (2 * kb + (q4 >> 1)) * (CH * 16) + t * 16 + 8 * (q4 & 1))));
+      for (int kb = 0; kb < 4; ++kb) av[kb] = ld8(dVs + (2 * kb + (q4 >> 1)) * (CH * 16) + t * 16 + 8 * (q4 & 1));
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) {
         const int m = 2 * wave + mm;
-        f32x4 w = zero4();  // dW^T[k = 16 m + 4 q4 + i][t]
+        f32x4 w = zero4();  // -dW^T[k = 16 m + 4 q4 + i][t] = (dVn S^T)^T, zero past the chunk
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) w = mfma(bh[mm][kb], av[kb], w);
-        st4(dWs + t * LDK + 16 * m + 4 * q4, w);
+        st4(dWs + t * LDK + 16 * m + 4 * q4, keep_if(t < ci.len, w));
       }
     }
     const int t = 16 * wave + r;
@@ -808,7 +827,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) fvt[mm][kb] = ld8_tr(dVs + (2 * wave + mm) * (CH * 16), 16, 32 * kb, 0);
   }
-  lds_barrier();  // dW rows complete, dG partials complete, the dVn tile consumed
+  lds_barrier();  // -dW rows complete, dG partials complete, the dVn tile consumed
 
   // ---- the WY part, on the chip-resident operands ----
   const float dgp_t = (tid < 64) ? dgw[0][tid] + dgw[1][tid] + dgw[2][tid] + dgw[3][tid] : 0.f;
@@ -856,7 +875,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       const int s = 16 * n + r;
-      const float fk = Bs[s] * __expf(Gs[s]), fv = Bs[s];
+      const float fk = -(Bs[s] * __expf(Gs[s])), fv = Bs[s];  // ak holds -dW (beta gam K)^T
       st4(S1 + s * LDT + 16 * wave + 4 * q4, ak[n] * fk + av[n] * fv);
     }
   }
@@ -886,54 +905,77 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   }
   lds_barrier();
 
-  // ---- wy phase 3: dA = -T^T Y, dM, dbeta and dG from A ----
+  // ---- wy phase 3: dA = -T^T Y, dM, dbeta and dG from A, over the causal (i-tile, j-tile) pairs
+  //      shared out as in phase 1 ----
   {
-    const int kb0 = wave >= 2 ? 1 : 0;
-    bf16x8 at[2], ak[4];
+    // (beta dM)^T of i-tile it, j-tile n (at, ak: T^T and K fragments of i-tile it)
+    auto pair = [&](int it, int n, const bf16x8(&at)[2], const bf16x8(&ak)[4], float(&rowB)[4],
+                    float(&rowE)[4]) -> f32x4 {
+      f32x4 da = zero4(), kk = zero4();
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) at[kb] = ld8_tr(Ts, LDT, 32 * kb, 16 * wave);
+      for (int kb = 0; kb < 2; ++kb)
+        if (kb >= (it >= 2 ? 1 : 0)) da = mfma(at[kb], ld8(S2 + (16 * n + r) * LDT + 32 * kb + 8 * q4), da);
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) ak[kb] = ld8(Ks + (16 * wave + r) * LDK + 32 * kb + 8 * q4);
-    float rowB[4] = {0.f, 0.f, 0.f, 0.f}, rowE[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < 4; ++kb) kk = mfma(ak[kb], ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4), kk);
+      const int j = 16 * n + r;
+      const f32x4 g4 = *reinterpret_cast<const f32x4*>(&Gs[16 * it + 4 * q4]);
+      const f32x4 b4 = *reinterpret_cast<const f32x4*>(&Bs[16 * it + 4 * q4]);
+      const float gj = Gs[j];
+      float colE = 0.f;
+      f32x4 dmp;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      f32x4 dmp = zero4();
-      if (n <= wave) {
-        f32x4 da = zero4(), kk = zero4();
+      for (int e = 0; e < 4; ++e) {
+        const int i = 16 * it + 4 * q4 + e;
+        const bool strict = j < i;
+        const float gam = strict ? __expf(g4[e] - gj) : 0.f;
+        const float dA = strict ? -da[e] : 0.f;
+        const float dM = dA * gam;
+        const float Aij = b4[e] * kk[e] * gam;
+        dmp[e] = b4[e] * dM;
+        rowB[e] += dM * kk[e];
+        const float e2 = dA * Aij;
+        rowE[e] += e2;
+        colE += e2;
+      }
+      colE = sum_rows4(colE);
+      if (q4 == 0) dgl[j] -= colE;
+      return dmp;
+    };
+    auto rows = [&](int it, const float(&rowB)[4], const float(&rowE)[4]) {
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-          if (kb >= kb0) da = mfma(at[kb], ld8(S2 + (16 * n + r) * LDT + 32 * kb + 8 * q4), da);
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) kk = mfma(ak[kb], ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4), kk);
-        const int j = 16 * n + r;
-        float colE = 0.f;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = 16 * wave + 4 * q4 + e;
-          const bool strict = j < i;
-          const float gam = strict ? __expf(Gs[i] - Gs[j]) : 0.f;
-          const float dA = strict ? -da[e] : 0.f;
-          const float dM = dA * gam;
-          const float Aij = Bs[i] * kk[e] * gam;
-          dmp[e] = Bs[i] * dM;
-          rowB[e] += dM * kk[e];
-          const float e2 = dA * Aij;
-          rowE[e] += e2;
-          colE += e2;
+      for (int e = 0; e < 4; ++e) {
+        const float xb = sum16(rowB[e]);
+        const float xe = sum16(rowE[e]);
+        if (r == 0) {
+          dbl[16 * it + 4 * q4 + e] += xb;
+          dgl[16 * it + 4 * q4 + e] += xe;
         }
-        colE = sum_rows4(colE);
-        if (q4 == 0) dgl[j] -= colE;
       }
-      st4(S1 + (16 * n + r) * LDT + 16 * wave + 4 * q4, dmp);
-    }
+    };
+    {
+      bf16x8 at[2], ak[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float xb = sum16(rowB[e]);
-      const float xe = sum16(rowE[e]);
-      if (r == 0) {
-        dbl[16 * wave + 4 * q4 + e] += xb;
-        dgl[16 * wave + 4 * q4 + e] += xe;
+      for (int kb = 0; kb < 2; ++kb) at[kb] = ld8_tr(Ts, LDT, 32 * kb, 16 * wave);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) ak[kb] = ld8(Ks + (16 * wave + r) * LDK + 32 * kb + 8 * q4);
+      float rowB[4] = {0.f, 0.f, 0.f, 0.f}, rowE[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        if (n == 3 && wave == 3) continue;  // the (3, 3) tile is wave 0's
+        const f32x4 dmp = (n <= wave) ? pair(wave, n, at, ak, rowB, rowE) : zero4();
+        st4(S1 + (16 * n + r) * LDT + 16 * wave + 4 * q4, dmp);
       }
+      rows(wave, rowB, rowE);
+    }
+    if (wave == 0) {
+      bf16x8 at[2], ak[4];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) at[kb] = ld8_tr(Ts, LDT, 32 * kb, 48);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) ak[kb] = ld8(Ks + (48 + r) * LDK + 32 * kb + 8 * q4);
+      float rowB[4] = {0.f, 0.f, 0.f, 0.f}, rowE[4] = {0.f, 0.f, 0.f, 0.f};
+      st4(S1 + (48 + r) * LDT + 48 + 4 * q4, pair(3, 3, at, ak, rowB, rowE));
+      rows(3, rowB, rowE);
     }
   }
   lds_barrier();
@@ -943,6 +985,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   wait_vmem_all();
   // ---- wy phase 4b: dv = beta (T^T dVn) ----
   {
+    const __amdgpu_buffer_rsrc_t dv_rs = chunk_rows_rsrc(dv, ci.start, ci.len, H, h);
     float colB[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
@@ -962,7 +1005,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         const int s = 16 * n + r;
         const f32x4 vv = cvtf4(ld4(Vs + s * LDK + 16 * m + 4 * q4));
         colB[n] += acc[n][0] * vv[0] + acc[n][1] * vv[1] + acc[n][2] * vv[2] + acc[n][3] * vv[3];
-        if (s < ci.len) st4(dv + ((size_t)(ci.start + s) * H + h) * D + 16 * m + 4 * q4, acc[n] * Bs[s]);
+        buf_st4(dv_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, acc[n] * Bs[s]);  // row s
       }
     }
 #pragma unroll
@@ -1001,10 +1044,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         const int t = 16 * n + r;
         const float bg = Bs[t] * __expf(Gs[t]);
         const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
+        // aw holds -(T^T dW): every use takes its sign back
         const float x = aw[n][0] * kk[0] + aw[n][1] * kk[1] + aw[n][2] * kk[2] + aw[n][3] * kk[3];
-        colB[n] += __expf(Gs[t]) * x;
-        colG[n] += bg * x;
-        dkr[mm][n] = ak[n] + aw[n] * bg + fkp[mm][n];
+        colB[n] -= __expf(Gs[t]) * x;
+        colG[n] -= bg * x;
+        dkr[mm][n] = ak[n] + aw[n] * -bg + fkp[mm][n];
       }
     }
 #pragma unroll
@@ -1033,6 +1077,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   lds_barrier();
 
   // ---- wy phase 5: l2norm backward of dk; dg (reverse cumsum of the chunk's dG); dbeta ----
+  const __amdgpu_buffer_rsrc_t dk_rs = chunk_rows_rsrc(dk, ci.start, ci.len, H, h);
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
     const int t = 16 * n + r;
@@ -1043,7 +1088,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       const int m = 2 * wave + mm;
       const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
       const f32x4 out = normalize ? (dkr[mm][n] - kk * dot) * rsn[n] : dkr[mm][n];
-      if (t < ci.len) st4(dk + ((size_t)(ci.start + t) * H + h) * D + 16 * m + 4 * q4, out);
+      buf_st4(dk_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, out);  // row t
     }
   }
   if (tid < 64) {

@@ -438,6 +438,25 @@ __device__ __forceinline__ V keep_if(bool in, V x) {
   return in ? x : V{};
 }
 
+// ---- chunk-row stores through a buffer resource ----------------------------
+// A raw buffer resource over the rows of one chunk in an [events][H][128] bf16
+// tensor: based at head h of the chunk's first event, it ends after the last
+// valid row, so the hardware's range check drops stores to rows past the chunk's
+// length (no per-lane branch).  A store's address is a per-lane VGPR offset plus a
+// wave-uniform SGPR offset (the row), instead of a 64-bit address per lane.
+// 0x00020000 is the resource's fourth dword for a raw buffer on gfx9-family parts.
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rows_rsrc(bf16* base, int start, int len, int H, int h) {
+  return __builtin_amdgcn_make_buffer_rsrc(base + ((size_t)start * H + h) * D, (short)0, (len - 1) * H * D * 2 + D * 2,
+                                           0x00020000);
+}
+__device__ __forceinline__ void buf_st1(__amdgpu_buffer_rsrc_t rs, int voff, int soff, float x) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16)x), rs, voff, soff, 0);
+}
+__device__ __forceinline__ void buf_st4(__amdgpu_buffer_rsrc_t rs, int voff, int soff, f32x4 x) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, cvt4(x)), rs, voff, soff, 0);
+}
+
 // Per-chunk metadata: chunk_table[c] = (start event, length).  A chunk never
 // crosses a document boundary; doc_chunk[d] .. doc_chunk[d+1] are the chunks of
 // document d, in time order.
