@@ -13,9 +13,10 @@
 using namespace cqgdn;
 
 namespace {
-
 thread_local std::string g_error;
+}  // namespace
 
+namespace cqgdn {
 int fail(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
@@ -30,6 +31,9 @@ int ok() {
   g_error.clear();
   return CQGDN_OK;
 }
+}  // namespace cqgdn
+
+namespace {
 
 int check_launch(const char* what) {
   const hipError_t e = hipGetLastError();

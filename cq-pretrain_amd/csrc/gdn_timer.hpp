@@ -19,6 +19,11 @@ enum KernelId {
   K_COUNT
 };
 
+// the C ABI's error state (capi.hip): fail() records a message for
+// cqgdn_last_error and returns code; ok() clears it and returns CQGDN_OK
+int fail(int code, const char* fmt, ...);
+int ok();
+
 // names accepted by cqgdn_timer_arm, indexed by KernelId
 extern const char* const kKernelNames[K_COUNT];
 

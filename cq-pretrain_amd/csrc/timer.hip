@@ -70,22 +70,24 @@ int cqgdn_timer_arm(const char* kernel, int max_launches) {
   std::lock_guard<std::mutex> lock(t.mu);
   t.armed.store(-1);
   release(t);
-  if (!kernel) return CQGDN_OK;  // disarm
+  if (!kernel) return ok();  // disarm
   int id = -1;
   for (int i = 0; i < K_COUNT; ++i)
     if (std::strcmp(kernel, kKernelNames[i]) == 0) id = i;
-  if (id < 0 || max_launches <= 0 || max_launches > (1 << 16)) return CQGDN_EINVAL;
+  if (id < 0) return fail(CQGDN_EINVAL, "cqgdn_timer_arm: unknown kernel '%.64s'", kernel);
+  if (max_launches <= 0 || max_launches > (1 << 16))
+    return fail(CQGDN_EINVAL, "cqgdn_timer_arm: max_launches %d not in 1..65536", max_launches);
   t.events.resize(2 * (size_t)max_launches);
   for (size_t i = 0; i < t.events.size(); ++i) {
     if (hipEventCreate(&t.events[i]) != hipSuccess) {
       t.events.resize(i);
       release(t);
-      return CQGDN_EHIP;
+      return fail(CQGDN_EHIP, "cqgdn_timer_arm: hipEventCreate failed");
     }
   }
   t.capacity = max_launches;
   t.armed.store(id);
-  return CQGDN_OK;
+  return ok();
 }
 
 int cqgdn_timer_read(float* launch_ms, int capacity, int* launches) {
@@ -105,7 +107,7 @@ int cqgdn_timer_read(float* launch_ms, int capacity, int* launches) {
   }
   if (launches) *launches = (rc == CQGDN_OK) ? n : 0;
   release(t);
-  return rc;
+  return rc == CQGDN_OK ? ok() : fail(rc, "cqgdn_timer_read: a timed launch or its events failed");
 }
 
 }  // extern "C"
