@@ -313,8 +313,29 @@ def layer_decode_case(torch, device, N, iterations=200):
     end.record()
     torch.cuda.synchronize()
     us = start.elapsed_time(end) * 1e3 / iterations
+    # the same steps captured once in a HIP graph and replayed: the step without a Python call
+    # and a ctypes round trip per launch (what a serving loop pays)
+    graph_steps = 50
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(graph_steps):
+            step()
+    graph.replay()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(4):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    gus = start.elapsed_time(end) * 1e3 / (4 * graph_steps)
     state_bytes = 2 * N * H * 128 * 128 * 4
-    return dict(sequences=N, us_per_step=round(us, 2), state_gbps=round(state_bytes / us / 1e3, 1))
+    return dict(sequences=N, us_per_step=round(us, 2), state_gbps=round(state_bytes / us / 1e3, 1),
+                graph_us_per_step=round(gus, 2), graph_state_gbps=round(state_bytes / gus / 1e3, 1))
 
 
 COPY_BYTES = 256 << 20

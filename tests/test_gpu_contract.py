@@ -539,3 +539,48 @@ def test_layer_prefill_then_decode_fewer_key_heads(gdn):
     assert_close_bf16("C and Q rows", out.cpu(), one[n:n + 2].double().cpu())
     assert_close_bf16("state", cache["state"].cpu(), one_cache["state"].double().cpu())
     assert torch.equal(cache["conv"][0], proj[n - K + 2:n + 1, :C])
+
+
+def test_layer_decode_steps_replay_in_a_hip_graph(gdn):
+    """Layer decode steps captured once in a HIP graph, with fewer key heads than value heads (so the
+    capture holds the step kernel and the key-history shift): every replay -- with eager work and
+    synchronizations between them -- gives exactly the outputs, conv history and states of the same
+    steps run eagerly from the same starting cache."""
+    from cqgdn import events
+
+    N, H, HK, K, steps = 2, 16, 8, 4, 4
+    S, C = H * 128, (2 * HK + H) * 128
+    P = C + S + 2 * H
+    print(f"case layer decode graph: N={N} H={H} key heads={HK} steps={steps}", flush=True)
+    gen = torch.Generator().manual_seed(151)
+    w, A_log, dt_bias, nw = (t.to(DEV) for t in _gqa_decode_params(H, HK, K, gen))
+    projs = [(torch.randn(N, 2, P, generator=gen) * 0.7).bfloat16().to(DEV) for _ in range(steps)]
+    hist0 = (torch.randn(N, K - 1, C, generator=gen) * 0.7).bfloat16().to(DEV)
+    state0 = (torch.randn(N, H, 128, 128, generator=gen) * 0.05).to(DEV)
+    kw = dict(heads=H, key_heads=HK)
+
+    def run(cache):
+        return [events.layer_decode_step(p, w, A_log, dt_bias, nw, cache, **kw) for p in projs]
+
+    eager_cache = {"conv": hist0.clone(), "state": state0.clone()}
+    eager_outs = [o.clone() for o in run(eager_cache)]
+    torch.cuda.synchronize()
+    cache = {"conv": hist0.clone(), "state": state0.clone()}
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run({"conv": hist0.clone(), "state": state0.clone()})  # warm-up off the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = run(cache)
+    for replay in range(3):
+        cache["conv"].copy_(hist0)
+        cache["state"].copy_(state0)
+        _ = (torch.randn(256, 256, device=DEV) @ torch.randn(256, 256, device=DEV)).sum().item()  # eager work between
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager_outs)):
+            assert torch.equal(o, e), f"replay {replay}: output of step {i} differs"
+        assert torch.equal(cache["conv"], eager_cache["conv"]), f"replay {replay}: conv history differs"
+        assert torch.equal(cache["state"], eager_cache["state"]), f"replay {replay}: state differs"
