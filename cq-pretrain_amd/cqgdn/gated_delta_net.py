@@ -48,11 +48,12 @@ def initialize():
 
 
 def _stream(device):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 def _ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    # a plain int: the C-ABI signatures declare c_void_p, which ctypes converts from int
+    return t.data_ptr() if t is not None else None
 
 
 def call(name, *args):
@@ -228,14 +229,21 @@ def device_metadata(bounds, device):
             doc.to(device, non_blocking=True))
 
 
+def _as(x, dtype):
+    """x contiguous in ``dtype``; x itself when it already is (no torch call on the hot path)."""
+    return x if x.dtype == dtype and x.is_contiguous() else x.to(dtype).contiguous()
+
+
 def _flatten(q, k, v, g, beta, bounds):
     """Packed [1,T,...] views; unpacked batches become one document per row.  q, k, v in bf16, the
     kernels' operand type (fp16 inputs are rounded to it: bf16 keeps every fp16 magnitude in range)."""
     b, t = q.shape[0], q.shape[1]
     if bounds is None:
         bounds = tuple(range(0, b * t + 1, t)) if t > 0 else (0,) * (b + 1)
-    q, k, v = (x.reshape(1, b * t, *x.shape[2:]).to(torch.bfloat16).contiguous() for x in (q, k, v))
-    g, beta = (x.reshape(1, b * t, x.shape[-1]).float().contiguous() for x in (g, beta))
+    if b != 1:
+        q, k, v, g, beta = (x.reshape(1, b * t, *x.shape[2:]) for x in (q, k, v, g, beta))
+    q, k, v = (_as(x, torch.bfloat16) for x in (q, k, v))
+    g, beta = (_as(x, torch.float32) for x in (g, beta))
     return q, k, v, g, beta, bounds
 
 
@@ -275,7 +283,7 @@ class _Delta(torch.autograd.Function):
         else:
             ctx.save_for_backward(vf, gf, bf, ws)
         ctx.bounds, ctx.scale, ctx.normalize = bounds, scale, normalize
-        return o.reshape(v.shape).to(v.dtype)
+        return o if o.shape == v.shape and o.dtype == v.dtype else o.reshape(v.shape).to(v.dtype)
 
     @staticmethod
     def backward(ctx, dy):
@@ -285,7 +293,8 @@ class _Delta(torch.autograd.Function):
         else:
             v, g, beta, ws = ctx.saved_tensors
         grads = _backward(v, g, beta, ws, dy, ctx.bounds, ctx.normalize, ctx.scale)
-        grads = [x.reshape(shape).to(dtype) for x, shape, dtype in zip(grads, ctx.shapes, ctx.input_dtypes)]
+        grads = [x if x.shape == shape and x.dtype == dtype else x.reshape(shape).to(dtype)
+                 for x, shape, dtype in zip(grads, ctx.shapes, ctx.input_dtypes)]
         return *grads, None, None, None
 
 
@@ -294,7 +303,9 @@ def _backward(v, g, beta, ws, dy, bounds, normalize, scale):
     t, h = v.shape[1], v.shape[2]
     cu, table, doc = device_metadata(bounds, str(v.device))
     n_chunks, n_docs = table.shape[0], len(bounds) - 1
-    dy = dy.reshape(v.shape).to(v.dtype).contiguous()
+    if dy.shape != v.shape:
+        dy = dy.reshape(v.shape)
+    dy = _as(dy, v.dtype)
     bws = torch.empty(_lib.lib().cqgdn_bwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=v.device)
     dq, dk, dv = torch.empty_like(v), torch.empty_like(v), torch.empty_like(v)
     dg, db = torch.empty_like(g), torch.empty_like(beta)
