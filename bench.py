@@ -246,10 +246,15 @@ def layer_setup(torch, device, content, queries):
         x.grad = None
         y = model(x, plan, fused=fused)
         (y * upstream).sum().backward()
+        return y
+
+    def outputs(y):
+        """The last step's y, dx and input-projection gradient in fp32 (outside the timed steps,
+        as the reference takes them)."""
         return dict(y=y.detach().float(), dx=x.grad.detach().float(),
                     dw=model.in_proj_all.weight.grad.detach().float())
 
-    return plan, step
+    return plan, step, outputs
 
 
 def layer_case(torch, device, content, queries, iterations=12):
@@ -260,7 +265,7 @@ def layer_case(torch, device, content, queries, iterations=12):
     still hold is subtracted, as the reference measures in a process of its own), and the relative
     RMS of y, dx and the input-projection gradient dw between the two paths."""
     base = torch.cuda.memory_allocated()  # held by the earlier cases: not the layer's
-    plan, layer_step = layer_setup(torch, device, content, queries)
+    plan, layer_step, layer_outputs = layer_setup(torch, device, content, queries)
 
     def timed(fused):
         for _ in range(3):
@@ -271,10 +276,11 @@ def layer_case(torch, device, content, queries, iterations=12):
         for _ in range(iterations):
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            out = layer_step(fused)
+            y = layer_step(fused)
             torch.cuda.synchronize()
             durations.append((time.perf_counter() - t0) * 1e3)
-        return round(statistics.median(durations), 4), torch.cuda.max_memory_allocated() - base, out
+        peak = torch.cuda.max_memory_allocated() - base
+        return round(statistics.median(durations), 4), peak, layer_outputs(y)
 
     # fused: everything between the projections in the fused kernels (events.layer_core);
     # torch_glue: the reference's torch code around the hip delta, conv and gated norm
@@ -381,7 +387,7 @@ def main():
         copy_workload(torch)
         return
     if args.profile_layer:
-        _, layer_step = layer_setup(torch, device, 2048, 1675)
+        _, layer_step, _ = layer_setup(torch, device, 2048, 1675)
         for i in range(args.warmup + args.steps):
             layer_step(True)
             torch.cuda.synchronize()
