@@ -128,7 +128,7 @@ def traffic_for(kernel, sha):
 def cpu_baseline(torch, decode_steps=8):
     """The CPU rows of the plan (fp32 torch oracle on this host's cores, one thread per core the
     process may use): config 2 fwd+bwd via autograd (the reported baseline, same unit as
-    ``value``), plus the config 0 forward and the config 4 decode step (``rows``)."""
+    ``value``), plus the config 0 forward, the config 1 fwd+bwd and the config 4 decode step (``rows``)."""
     from cqgdn import synthetic
     from oracle import gdn_oracle as O
 
@@ -145,6 +145,14 @@ def cpu_baseline(torch, decode_steps=8):
         y.backward(do)
         sec = time.perf_counter() - t0
         del xs, y, do
+        # config 1: fwd+bwd via autograd, T=2304 (2048 content + 256 read-only)
+        T1, mask1, bounds1 = synthetic.config_events(1, seed=0)
+        x1 = [x.float().requires_grad_() for x in synthetic.make_inputs(T1, H, D, seed=1, readonly=mask1)]
+        do1 = torch.randn(1, T1, H, D, generator=torch.Generator().manual_seed(101))
+        t0 = time.perf_counter()
+        O.chunk_delta(*x1, bounds1, normalize=True).backward(do1)
+        rows["config1_fwd_bwd_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+        del x1, do1
         # config 0: forward only, T=2048, zero initial state, final state returned
         T0, _, b0 = synthetic.config_events(0)
         x0 = [x.float() for x in synthetic.make_inputs(T0, H, D, seed=0)]
@@ -173,7 +181,8 @@ def cpu_baseline(torch, decode_steps=8):
     return dict(value=round(sec * 1e3, 1), unit="ms/layer", cores=cores, kind="port",
                 sample="one fwd+bwd of config 2 (T=9216, H=16, d=128): oracle/gdn_oracle.chunk_delta in fp32 "
                        "(chunk 64) with torch autograd for the backward, "
-                       f"torch.set_num_threads({cores}); rows: one config-0 forward (T=2048, final state) and "
+                       f"torch.set_num_threads({cores}); rows: one config-0 forward (T=2048, final state), one "
+                       "config-1 fwd+bwd (T=2304) and "
                        f"the mean of {decode_steps} config-4 decode steps (B=64, H=16, fp32 state, "
                        "oracle/gdn_oracle.decode_step), same threads",
                 rows=rows)
