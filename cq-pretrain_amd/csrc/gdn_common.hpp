@@ -450,6 +450,17 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rows_rsrc(bf16* base, in
   return __builtin_amdgcn_make_buffer_rsrc(base + ((size_t)start * H + h) * D, (short)0, (len - 1) * H * D * 2 + D * 2,
                                            0x00020000);
 }
+// a raw buffer resource over ``bytes`` bytes from ``base``
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ void buf_stf(__amdgpu_buffer_rsrc_t rs, int voff, int soff, float x) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, x), rs, voff, soff, 0);
+}
+template <class X8>
+__device__ __forceinline__ void buf_st16(__amdgpu_buffer_rsrc_t rs, int voff, int soff, X8 x) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), rs, voff, soff, 0);
+}
 __device__ __forceinline__ void buf_st1(__amdgpu_buffer_rsrc_t rs, int voff, int soff, float x) {
   __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16)x), rs, voff, soff, 0);
 }

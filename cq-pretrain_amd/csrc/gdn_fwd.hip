@@ -60,7 +60,10 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
   // round trip: the gates (wave 0), this thread's pieces of its q and k rows,
   // and this wave's operand fragments of V for U = T (beta V), column gathers
   // for value tiles 2 wave, 2 wave + 1 (rows past the chunk re-read its last
-  // row; their beta is zero).
+  // row; their beta is zero).  Each phase waits only for what it reads: the
+  // gathers' lane exchange runs where U is formed, and the stores of the row
+  // phase go through buffer resources (rows past the chunk dropped by the range
+  // check), so no store is conditional and the compiler can count what is in flight.
   const int t_r = tid >> 2, p_r = tid & 3;  // row phase: thread (t, p) owns columns 8p + 32j, j = 0..3
   const size_t row_r = ((size_t)(ci.start + clamp_row(t_r, ci.len)) * H + h) * D;
   float gv = 0.f, bv = 0.f;
@@ -69,7 +72,8 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     gv = g[ev];
     bv = beta[ev];
   }
-  bf16x8 lq[4], lk[4], vf[2][2];
+  bf16x8 lq[4], lk[4];
+  Col8 vg[2][2];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     lq[j] = ld8(q + row_r + 32 * j + 8 * p_r);
@@ -80,8 +84,11 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
 #pragma unroll
     for (int nn = 0; nn < 2; ++nn)
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) vf[nn][kb] = gather8_col_rows(vb, H * D, 32 * kb, 16 * (2 * wave + nn), ci.len);
+      for (int kb = 0; kb < 2; ++kb) vg[nn][kb] = col8_load_rows(vb, H * D, 32 * kb, 16 * (2 * wave + nn), ci.len);
   }
+  const int rowe = H * D * (int)sizeof(E);  // bytes per event row of qn, kn, W
+  const int rows_bytes = ((ci.len - 1) * H + 1) * D * (int)sizeof(E);
+  const int gate_bytes = ((ci.len - 1) * H + 1) * (int)sizeof(float);
 
   // ---- gates: chunk-local cumsum of g (wave 0, one event per lane) ----
   if (wave == 0) {
@@ -95,7 +102,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     }
     Gs[lane] = gv;
     Bs[lane] = bv;
-    if (in) gc[(size_t)(ci.start + lane) * H + h] = gv;
+    buf_stf(buf_rsrc(gc + (size_t)ci.start * H + h, gate_bytes), lane * H * 4, 0, gv);  // rows past the chunk dropped
   }
   __syncthreads();
   const float glast = Gs[ci.len - 1];
@@ -108,15 +115,14 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
   {
     const int t = t_r, p = p_r;
     const bool in = t < ci.len;
-    const size_t row = row_r;
     const float gam_t = __expf(Gs[t]);
     const float kdec_t = __expf(glast - Gs[t]);
     const float b_t = Bs[t];
-    // Every load of the prologue (q and k rows, V fragments) was issued at
-    // once: wait for all of them here, before the first (conditional) store.
-    // Past conditional stores the compiler can only wait for everything, and
-    // the k rows' first use would then wait for the q stores as well.
-    wait_vmem_all();
+    const __amdgpu_buffer_rsrc_t qn_rs = buf_rsrc(qn + ((size_t)ci.start * H + h) * D, rows_bytes);
+    const __amdgpu_buffer_rsrc_t kn_rs = buf_rsrc(kn + ((size_t)ci.start * H + h) * D, rows_bytes);
+    const __amdgpu_buffer_rsrc_t rq_rs = buf_rsrc(rq + (size_t)ci.start * H + h, gate_bytes);
+    const __amdgpu_buffer_rsrc_t rk_rs = buf_rsrc(rk + (size_t)ci.start * H + h, gate_bytes);
+    const int rvo = t * rowe + 8 * p * (int)sizeof(E);  // this thread's piece of row t
     // q
     {
       f32x8 x[4];
@@ -132,11 +138,9 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
         ss = sum4(ss);
         rs = rsqrtf(ss + 1e-6f);
       }
-      if (in) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) st8(qn + row + 32 * j + 8 * p, to8<E>(x[j] * rs));
-        if (p == 0) rq[(size_t)(ci.start + t) * H + h] = rs;
-      }
+      for (int j = 0; j < 4; ++j) buf_st16(qn_rs, rvo + 32 * j * (int)sizeof(E), 0, to8<E>(x[j] * rs));
+      buf_stf(rq_rs, t * H * 4, 0, rs);  // the four threads of row t store the same value
     }
     // k
     {
@@ -159,11 +163,11 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
         const X8 xb = to8<E>(xn);
         const int col = 32 * j + 8 * p;
         st8(Ks + t * LDK + col, xb);
-        if (in) st8(kn + row + col, xb);
+        buf_st16(kn_rs, rvo + 32 * j * (int)sizeof(E), 0, xb);
         kb8[j] = to8<E>(xn * (b_t * gam_t));
         kg8[j] = to8<E>(xn * kdec_t);
       }
-      if (in && p == 0) rk[(size_t)(ci.start + t) * H + h] = rs;
+      buf_stf(rk_rs, t * H * 4, 0, rs);
     }
   }
   __syncthreads();
@@ -298,7 +302,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
       const f32x4 b1 = *reinterpret_cast<const f32x4*>(Bs + 32 * kb + 8 * q4 + 4);
       const f32x8 bb = f32x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]} * vs;
 #pragma unroll
-      for (int nn = 0; nn < 2; ++nn) bvf[nn][kb] = to8<E>(cvtf8(vf[nn][kb]) * bb);
+      for (int nn = 0; nn < 2; ++nn) bvf[nn][kb] = to8<E>(cvtf8(col8_combine(vg[nn][kb])) * bb);
     }
     E* ut = UT + cb * (D * CH);
 #pragma unroll
@@ -315,6 +319,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
         st4(ut + (16 * (2 * wave + nn) + r) * CH + 16 * tt + 4 * q4, au);
       }
     }
+    const __amdgpu_buffer_rsrc_t w_rs = buf_rsrc(W + ((size_t)ci.start * H + h) * D, rows_bytes);
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const int m = 2 * wave + mm;
@@ -326,8 +331,9 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
         f32x4 acc = zero4();
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) acc = mfma(ak[kb], ld8(Ts + (16 * n + r) * LDT + 32 * kb + 8 * q4), acc);
-        const int t = 16 * n + r;
-        if (t < ci.len) st4(W + ((size_t)(ci.start + t) * H + h) * D + perm32(16 * m + 4 * q4), -acc);
+        // row t = 16 n + r (rows past the chunk fall outside w_rs)
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, to4<E>(-acc)), w_rs,
+                                              r * rowe + perm32(16 * m + 4 * q4) * (int)sizeof(E), 16 * n * rowe, 0);
       }
     }
   }
