@@ -53,7 +53,21 @@ CASES = [
 @pytest.mark.parametrize("T,bounds,H", CASES)
 def test_forward_intermediates_and_output(gdn, T, bounds, H):
     print(f"case T={T} bounds={bounds} H={H}", flush=True)
-    xs = inputs(T, H, seed=900 + T)
+    check_forward(gdn, T, bounds, H, seed=900 + T)
+
+
+# fwd_prep gives each workgroup up to three chunks (as many as full rounds of three
+# workgroups per CU the chunk-heads make); on a 256-CU device these take two and
+# three chunks per workgroup, and the last workgroup of each head has one chunk fewer
+@pytest.mark.parametrize("T,bounds,H", [(6454, (0, 3000, 6454), 16), (9300, (0, 9300), 16)])
+def test_forward_chunks_shared_by_workgroups(gdn, T, bounds, H):
+    print(f"case T={T} bounds={bounds} H={H}", flush=True)
+    check_forward(gdn, T, bounds, H, seed=T)
+
+
+def check_forward(gdn, T, bounds, H, seed):
+    """The forward's output and stored intermediates against the oracle's."""
+    xs = inputs(T, H, seed=seed)
     o, _, ws = run_fwd(gdn, xs, bounds)
     q, k, v, g, b = (x.double() for x in xs)
     ref, inter = O.chunk_delta(q, k, v, g, b, bounds, return_intermediates=True)
