@@ -30,21 +30,23 @@ constexpr int LDA = 65;   // row stride (fp32) of the 64 x 64 solve matrix
 // ---------------------------------------------------------------------------
 // E: operand element type (bf16, or f16 for the precise forward).  vscale: null,
 // or the power-of-two factor applied to V (fp16 range, see vscale_final_kernel).
-// NPER: chunks per workgroup (see the chunk loop below).
-template <class E, bool NORMALIZE, int NPER>
+template <class E, bool NORMALIZE>
 __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const int32_t* __restrict__ chunks,
     int H, const float* __restrict__ vscale, E* __restrict__ qn, E* __restrict__ kn, float* __restrict__ rq,
     float* __restrict__ rk, float* __restrict__ gc, E* __restrict__ Tm, E* __restrict__ W,
-    E* __restrict__ UT, E* __restrict__ KgT, int n_chunks) {
+    E* __restrict__ UT, E* __restrict__ KgT) {
   typedef typename Vec<E>::x8 X8;
   typedef typename Vec<E>::x4 X4;
-  // grid (H, G), G = ceil(n_chunks / NPER): workgroup (h, y) takes chunks
-  // n_chunks - 1 - y, then G earlier, up to NPER of them.  The chunks run last
-  // to first, so the state scan, which reads the first chunks first, finds them
-  // the most recently written (still in the memory-side cache).
-  const int h = blockIdx.x;
+  // grid (H, NC), chunks dispatched last to first: the state scan reads the
+  // first chunks first, and they are then the most recently written (still in
+  // the memory-side cache)
+  const int h = blockIdx.x, c = gridDim.y - 1 - blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, q4 = lane >> 4;
+  const ChunkInfo ci = chunk_info(chunks, c);
+  const size_t cb = (size_t)c * H + h;
 
   __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ __attribute__((aligned(16))) float Bs[64];
@@ -53,81 +55,54 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
   __shared__ __attribute__((aligned(16))) E Ts[64 * LDT];
   const float vs = vscale ? *vscale : 1.f;
 
-  // A chunk's inputs are requested before the stores that precede their use (a
-  // wait for a load also waits for every store issued before it): the gates (wave
-  // 0), this thread's pieces of its q and k rows, and this wave's operand
-  // fragments of V for U = T (beta V), column gathers for value tiles 2 wave,
-  // 2 wave + 1 (rows past the chunk re-read its last row; their beta is zero).
-  // The first chunk's come first thing; each next chunk's are requested into the
-  // same registers as soon as the current chunk has consumed them (its gates and
-  // rows after the row phase, its V where U is formed), so they land while the
-  // current chunk computes, and the workgroups on a CU do not all wait for memory
-  // at once.  The chunk loop is unrolled (NPER is a constant), so the compiler
-  // counts exactly what is in flight; every store goes through a buffer resource
-  // (rows past the chunk dropped by the range check) and none is conditional.
+  // Every global load is issued first, before any store (a wait for a load
+  // also waits for every store issued before it), so the kernel pays one memory
+  // round trip: the gates (wave 0), this thread's pieces of its q and k rows,
+  // and this wave's operand fragments of V for U = T (beta V), column gathers
+  // for value tiles 2 wave, 2 wave + 1 (rows past the chunk re-read its last
+  // row; their beta is zero).  Each phase waits only for what it reads: the
+  // gathers' lane exchange runs where U is formed, and the stores of the row
+  // phase go through buffer resources (rows past the chunk dropped by the range
+  // check), so no store is conditional and the compiler can count what is in flight.
+  const int t_r = tid >> 2, p_r = tid & 3;  // row phase: thread (t, p) owns columns 8p + 32j, j = 0..3
+  const size_t row_r = ((size_t)(ci.start + clamp_row(t_r, ci.len)) * H + h) * D;
   float gv = 0.f, bv = 0.f;
+  if (wave == 0) {
+    const size_t ev = (size_t)(ci.start + clamp_row(lane, ci.len)) * H + h;
+    gv = g[ev];
+    bv = beta[ev];
+  }
   bf16x8 lq[4], lk[4];
   Col8 vg[2][2];
-  // row phase: thread (t, p) = (tid / 4, tid % 4) owns columns 8p + 32j, j = 0..3
-  auto issue_rows = [&](int c, int tid) {
-    const int lane = tid & 63;
-    const ChunkInfo ci = chunk_info(chunks, c);
-    const size_t row_r = ((size_t)(ci.start + clamp_row(tid >> 2, ci.len)) * H + h) * D + 8 * (tid & 3);
-    if (tid < 64) {
-      const size_t ev = (size_t)(ci.start + clamp_row(lane, ci.len)) * H + h;
-      gv = g[ev];
-      bv = beta[ev];
-    }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      lq[j] = ld8(q + row_r + 32 * j);
-      lk[j] = ld8(k + row_r + 32 * j);
-    }
-  };
-  auto issue_v = [&](int c, int tid) {
-    const int wave = tid >> 6;
-    const ChunkInfo ci = chunk_info(chunks, c);
+  for (int j = 0; j < 4; ++j) {
+    lq[j] = ld8(q + row_r + 32 * j + 8 * p_r);
+    lk[j] = ld8(k + row_r + 32 * j + 8 * p_r);
+  }
+  {
     const bf16* vb = v + ((size_t)ci.start * H + h) * D;
 #pragma unroll
     for (int nn = 0; nn < 2; ++nn)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) vg[nn][kb] = col8_load_rows(vb, H * D, 32 * kb, 16 * (2 * wave + nn), ci.len);
-  };
-  issue_rows(n_chunks - 1 - (int)blockIdx.y, threadIdx.x);
-  issue_v(n_chunks - 1 - (int)blockIdx.y, threadIdx.x);
+  }
   const int rowe = H * D * (int)sizeof(E);  // bytes per event row of qn, kn, W
-
-#pragma unroll
-  for (int i = 0; i < NPER; ++i) {
-  // the lane indices, opaque to the compiler per chunk: addresses derived from
-  // them are formed in each chunk rather than held in registers across chunks
-  int tid_o = threadIdx.x;
-  asm volatile("" : "+v"(tid_o));
-  const int tid = tid_o, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 15, q4 = lane >> 4;
-  const int t_r = tid >> 2, p_r = tid & 3;
-  const int y = blockIdx.y + i * gridDim.y;
-  if (i > 0 && y >= n_chunks) return;
-  const int c = n_chunks - 1 - y;
-  // the next chunk (this one again past the last: requested, never used)
-  const int cn = y + (int)gridDim.y < n_chunks ? c - (int)gridDim.y : c;
-  const ChunkInfo ci = chunk_info(chunks, c);
-  const size_t cb = (size_t)c * H + h;
   const int rows_bytes = ((ci.len - 1) * H + 1) * D * (int)sizeof(E);
   const int gate_bytes = ((ci.len - 1) * H + 1) * (int)sizeof(float);
 
   // ---- gates: chunk-local cumsum of g (wave 0, one event per lane) ----
   if (wave == 0) {
     const bool in = lane < ci.len;
-    float gs = keep_if(in, gv);
+    gv = keep_if(in, gv);
+    bv = keep_if(in, bv);
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-      const float o = __shfl_up(gs, off, 64);
-      if (lane >= off) gs += o;
+      const float o = __shfl_up(gv, off, 64);
+      if (lane >= off) gv += o;
     }
-    Gs[lane] = gs;
-    Bs[lane] = keep_if(in, bv);
-    buf_stf(buf_rsrc(gc + (size_t)ci.start * H + h, gate_bytes), lane * H * 4, 0, gs);  // rows past the chunk dropped
+    Gs[lane] = gv;
+    Bs[lane] = bv;
+    buf_stf(buf_rsrc(gc + (size_t)ci.start * H + h, gate_bytes), lane * H * 4, 0, gv);  // rows past the chunk dropped
   }
   __syncthreads();
   const float glast = Gs[ci.len - 1];
@@ -223,7 +198,6 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
   // every read of K is done: beta gam K takes its rows (read again only after the solve)
 #pragma unroll
   for (int j = 0; j < 4; ++j) st8(Ks + t_r * LDK + 32 * j + 8 * p_r, kb8[j]);
-  if (i + 1 < NPER) issue_rows(cn, tid);  // the next chunk's gates and rows
 
   // ---- T = (I + A)^-1, blocked by 16, in fp32 ----
   // The four diagonal blocks by forward substitution (column c = tid/4 of block
@@ -330,7 +304,6 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
 #pragma unroll
       for (int nn = 0; nn < 2; ++nn) bvf[nn][kb] = to8<E>(cvtf8(col8_combine(vg[nn][kb])) * bb);
     }
-    if (i + 1 < NPER) issue_v(cn, tid);  // the next chunk's V, ahead of this chunk's U, W and KgT stores
     E* ut = UT + cb * (D * CH);
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
@@ -372,8 +345,6 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
       const int seg = 256 * i + tid, kr = seg >> 3, part = seg & 7;
       st8(kgt + kr * CH + 8 * part, ld8(kgs + kr * CH + 8 * part));
     }
-  }
-  // (the next chunk writes Gs, Bs and Ks after the barrier above, Af after two more)
   }
 }
 
@@ -643,6 +614,8 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
       if (ok && seen <= tau) ok = scan_wait_ready(flags, tau + 1, seen);
       if (poisoned) ok = false;
       if (!ok) {  // a broken hand-off: make every later output NaN
+        // (the empty asm keeps this a branch: as selects it cost 32 VALU operations a step)
+        asm volatile("");
 #pragma unroll
         for (int m = 0; m < 8; ++m) S[m] = f32x4{NAN, NAN, NAN, NAN};
       }
@@ -887,19 +860,6 @@ __global__ __launch_bounds__(256) void vscale_final_kernel(const float* __restri
 // ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
-// compute units of the current device (cached per device; 256 on MI355X)
-static int device_cus() {
-  static int cached[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 template <class E>
 static void launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stream) {
   E* ws[F_COUNT];
@@ -909,24 +869,15 @@ static void launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stre
   float* gcum = reinterpret_cast<float*>(ws[F_GC]);
   {
     TimedLaunch tl(K_FWD_PREP, stream);
-    // chunks per workgroup: as many as full rounds of resident workgroups (three
-    // per CU) the chunk-heads make, at most three
-    const int rounds = a.n_chunks * a.H / (3 * device_cus());
-    const int nper = std::max(1, std::min(3, std::min(rounds, a.n_chunks)));
-    const dim3 grid_p(a.H, (a.n_chunks + nper - 1) / nper);
-    auto launch = [&](auto kernel) {
-      hipLaunchKernelGGL(kernel, grid_p, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta, a.chunks, a.H, vscale,
-                         ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W], ws[F_UT], ws[F_KGT], a.n_chunks);
-    };
-    if (a.normalize) {
-      if (nper == 3) launch(fwd_prep_kernel<E, true, 3>);
-      else if (nper == 2) launch(fwd_prep_kernel<E, true, 2>);
-      else launch(fwd_prep_kernel<E, true, 1>);
-    } else {
-      if (nper == 3) launch(fwd_prep_kernel<E, false, 3>);
-      else if (nper == 2) launch(fwd_prep_kernel<E, false, 2>);
-      else launch(fwd_prep_kernel<E, false, 1>);
-    }
+    const dim3 grid_p(a.H, a.n_chunks);
+    if (a.normalize)
+      hipLaunchKernelGGL((fwd_prep_kernel<E, true>), grid_p, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
+                         a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W],
+                         ws[F_UT], ws[F_KGT]);
+    else
+      hipLaunchKernelGGL((fwd_prep_kernel<E, false>), grid_p, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
+                         a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W],
+                         ws[F_UT], ws[F_KGT]);
   }
   const dim3 grid_s(a.H * (D / 16), a.n_docs);
   {
