@@ -34,6 +34,8 @@ SIGNATURES = {
     "cqgdn_fwd_static": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _P, _P, _P]),
     "cqgdn_bwd": (_I, [_P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _SZ, _P, _SZ, _P, _P, _P, _P, _P,
                        _P]),
+    "cqgdn_bwd_recompute": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _SZ, _P, _SZ, _P,
+                                 _P, _P, _P, _P, _P]),
     "cqgdn_recurrent": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _F, _P]),
     "cqgdn_l2norm_fwd": (_I, [_P, _P, _P, _I64, _P]),
     "cqgdn_l2norm_bwd": (_I, [_P, _P, _P, _P, _I64, _P]),

@@ -287,19 +287,20 @@ class _Delta(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy):
-        if ctx.mode == "fused":
+        if ctx.mode == "fused":  # one call rebuilds the forward workspace and runs the backward
             q, k, v, g, beta = ctx.saved_tensors
-            _, _, ws = _forward(q, k, v, g, beta, ctx.bounds, ctx.normalize, ctx.scale, training=True, output=False)
+            grads = _backward(v, g, beta, None, dy, ctx.bounds, ctx.normalize, ctx.scale, recompute=(q, k))
         else:
             v, g, beta, ws = ctx.saved_tensors
-        grads = _backward(v, g, beta, ws, dy, ctx.bounds, ctx.normalize, ctx.scale)
+            grads = _backward(v, g, beta, ws, dy, ctx.bounds, ctx.normalize, ctx.scale)
         grads = [x if x.shape == shape and x.dtype == dtype else x.reshape(shape).to(dtype)
                  for x, shape, dtype in zip(grads, ctx.shapes, ctx.input_dtypes)]
         return *grads, None, None, None
 
 
-def _backward(v, g, beta, ws, dy, bounds, normalize, scale):
-    """dq, dk, dv, dg, dbeta of the packed chunked forward whose TRAINING workspace is ``ws``."""
+def _backward(v, g, beta, ws, dy, bounds, normalize, scale, recompute=None):
+    """dq, dk, dv, dg, dbeta of the packed chunked forward whose TRAINING workspace is ``ws``; with
+    ``recompute=(q, k)`` (``ws`` None) the workspace is rebuilt inside the same call (fused mode)."""
     t, h = v.shape[1], v.shape[2]
     cu, table, doc = device_metadata(bounds, str(v.device))
     n_chunks, n_docs = table.shape[0], len(bounds) - 1
@@ -310,9 +311,16 @@ def _backward(v, g, beta, ws, dy, bounds, normalize, scale):
     dq, dk, dv = torch.empty_like(v), torch.empty_like(v), torch.empty_like(v)
     dg, db = torch.empty_like(g), torch.empty_like(beta)
     flags = (_lib.NORMALIZE if normalize else 0) | _lib.TRAINING
-    call("cqgdn_bwd", _ptr(v), _ptr(g), _ptr(beta), _ptr(dy), t, h, _ptr(table), n_chunks, _ptr(doc), n_docs,
-         float(scale), flags, _ptr(ws), ws.numel(), _ptr(bws), bws.numel(), _ptr(dq), _ptr(dk), _ptr(dv),
-         _ptr(dg), _ptr(db), _stream(v.device))
+    if recompute is None:
+        call("cqgdn_bwd", _ptr(v), _ptr(g), _ptr(beta), _ptr(dy), t, h, _ptr(table), n_chunks, _ptr(doc), n_docs,
+             float(scale), flags, _ptr(ws), ws.numel(), _ptr(bws), bws.numel(), _ptr(dq), _ptr(dk), _ptr(dv),
+             _ptr(dg), _ptr(db), _stream(v.device))
+    else:
+        q, k = recompute
+        ws = torch.empty(_lib.lib().cqgdn_fwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=v.device)
+        call("cqgdn_bwd_recompute", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(dy), t, h, _ptr(table),
+             n_chunks, _ptr(doc), n_docs, float(scale), flags, _ptr(ws), ws.numel(), _ptr(bws), bws.numel(),
+             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(db), _stream(v.device))
     return dq, dk, dv, dg, db
 
 

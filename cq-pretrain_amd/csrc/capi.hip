@@ -59,7 +59,8 @@ int check_common(int64_t T, int H, int64_t n_chunks, int n_docs, const int32_t* 
 int fwd_impl(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T, int H,
              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
              unsigned flags, const float* initial_state, float* final_state, void* o, void* workspace,
-             size_t workspace_bytes, void* stream);
+             size_t workspace_bytes, void* stream, hipStream_t scan_stream = nullptr,
+             hipEvent_t scan_fork = nullptr, hipEvent_t scan_join = nullptr);
 
 // The workspace of cqgdn_fwd_static: one array per GPU, held until the process
 // ends.  Host code never uses its name as an address (on the host it only
@@ -185,7 +186,8 @@ namespace {
 int fwd_impl(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T, int H,
              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
              unsigned flags, const float* initial_state, float* final_state, void* o, void* workspace,
-             size_t workspace_bytes, void* stream) {
+             size_t workspace_bytes, void* stream, hipStream_t scan_stream, hipEvent_t scan_fork,
+             hipEvent_t scan_join) {
   if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
   if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING | CQGDN_PRECISE | CQGDN_NO_OUTPUT))
     return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
@@ -233,17 +235,21 @@ int fwd_impl(const void* q, const void* k, const void* v, const float* g, const 
   a.o = static_cast<bf16*>(o);
   a.ws = static_cast<uint8_t*>(workspace);
   cqgdn_fwd_buffer_offsets(T, H, n_chunks, a.off, F_COUNT);
-  launch_fwd(a, (hipStream_t)stream);
+  a.scan_stream = scan_stream;
+  a.scan_fork = scan_fork;
+  a.scan_join = scan_join;
+  if (const hipError_t e = launch_fwd(a, (hipStream_t)stream))
+    return fail(CQGDN_EHIP, "cqgdn_fwd: ordering the state scan's stream: %s", hipGetErrorString(e));
   return check_launch("cqgdn_fwd");
 }
-}  // namespace
 
-extern "C" {
-
-int cqgdn_bwd(const void* v, const float* g, const float* beta, const void* dout, int64_t T, int H,
-              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
-              unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes, void* bwd_workspace,
-              size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta, void* stream) {
+// cqgdn_bwd's checks and launch; with launch == false only the checks (for a caller
+// that must know the backward's arguments are valid before it launches anything).
+int bwd_impl(const void* v, const float* g, const float* beta, const void* dout, int64_t T, int H,
+             const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
+             unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes, void* bwd_workspace,
+             size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta, void* stream,
+             bool launch, hipEvent_t dkw_after) {
   if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
   if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING)) return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
   if (T == 0) return ok();
@@ -256,6 +262,7 @@ int cqgdn_bwd(const void* v, const float* g, const float* beta, const void* dout
   if (!aligned(fwd_workspace, 256) || !aligned(bwd_workspace, 256)) return fail(CQGDN_EINVAL, "workspaces must be 256-byte aligned");
   for (const void* p : {v, dout, (const void*)dq, (const void*)dk, (const void*)dv})
     if (!aligned(p, 16)) return fail(CQGDN_EINVAL, "v/do/dq/dk/dv must be 16-byte aligned");
+  if (!launch) return ok();
   BwdArgs a{};
   a.v = static_cast<const bf16*>(v);
   a.dout = static_cast<const bf16*>(dout);
@@ -278,8 +285,79 @@ int cqgdn_bwd(const void* v, const float* g, const float* beta, const void* dout
   a.dv = static_cast<bf16*>(dv);
   a.dg = dg;
   a.dbeta = dbeta;
-  launch_bwd(a, (hipStream_t)stream);
+  a.dkw_after = dkw_after;
+  if (const hipError_t e = launch_bwd(a, (hipStream_t)stream))
+    return fail(CQGDN_EHIP, "cqgdn_bwd: waiting for the forward scan's stream: %s", hipGetErrorString(e));
   return check_launch("cqgdn_bwd");
+}
+
+// The side stream and its two events that cqgdn_bwd_recompute runs the forward
+// scan on: one set per (thread, device), created on first use and kept until the
+// process ends.  Per thread, so that a caller capturing a HIP graph never shares
+// them with another thread's calls.
+struct ScanSide {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+
+int scan_side(ScanSide** out) {
+  thread_local ScanSide sides[kMaxDevices];
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(CQGDN_EHIP, "cqgdn_bwd_recompute: no current HIP device (or device %d >= %d)", dev, kMaxDevices);
+  ScanSide& s = sides[dev];
+  if (!s.stream) {
+    hipError_t e = hipEventCreateWithFlags(&s.fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s.join, hipEventDisableTiming);
+    // default priority (the caller's streams are too); non-blocking: no implicit
+    // ordering against the null stream, the events order everything
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+      s.stream = nullptr;
+      return fail(CQGDN_EHIP, "cqgdn_bwd_recompute: creating its scan stream and events: %s", hipGetErrorString(e));
+    }
+  }
+  *out = &s;
+  return CQGDN_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int cqgdn_bwd(const void* v, const float* g, const float* beta, const void* dout, int64_t T, int H,
+              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
+              unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes, void* bwd_workspace,
+              size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta, void* stream) {
+  return bwd_impl(v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags, fwd_workspace,
+                  fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg, dbeta, stream, true,
+                  nullptr);
+}
+
+int cqgdn_bwd_recompute(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                        const void* dout, int64_t T, int H, const int32_t* chunk_table, int64_t n_chunks,
+                        const int32_t* doc_chunk, int n_docs, float scale, unsigned flags, void* fwd_workspace,
+                        size_t fwd_workspace_bytes, void* bwd_workspace, size_t bwd_workspace_bytes, void* dq,
+                        void* dk, void* dv, float* dg, float* dbeta, void* stream) {
+  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING)) return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
+  // every argument is checked before anything is launched
+  if (const int e = bwd_impl(v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags,
+                             fwd_workspace, fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg,
+                             dbeta, stream, false, nullptr))
+    return e;
+  if (T == 0) return ok();
+  if (!q || !k) return fail(CQGDN_EINVAL, "null tensor pointer");
+  for (const void* p : {q, k})
+    if (!aligned(p, 16)) return fail(CQGDN_EINVAL, "q/k/v/o must be 16-byte aligned");
+  ScanSide* side = nullptr;
+  if (const int e = scan_side(&side)) return e;
+  const unsigned fflags = (flags & CQGDN_NORMALIZE) | CQGDN_TRAINING | CQGDN_NO_OUTPUT;
+  if (const int e = fwd_impl(q, k, v, g, beta, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, fflags, nullptr,
+                             nullptr, nullptr, fwd_workspace, fwd_workspace_bytes, stream, side->stream, side->fork,
+                             side->join))
+    return e;
+  return bwd_impl(v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags, fwd_workspace,
+                  fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg, dbeta, stream, true,
+                  side->join);
 }
 
 int cqgdn_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta, int beta_is_bf16,

@@ -1108,7 +1108,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 }
 
 // ---------------------------------------------------------------------------
-void launch_bwd(const BwdArgs& a, hipStream_t stream) {
+hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
   auto F = [&](int i) { return reinterpret_cast<const bf16*>(a.fws + a.foff[i]); };
   auto Ff = [&](int i) { return reinterpret_cast<const float*>(a.fws + a.foff[i]); };
   auto B = [&](int i) { return reinterpret_cast<bf16*>(a.bws + a.boff[i]); };
@@ -1123,10 +1123,13 @@ void launch_bwd(const BwdArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(bwd_scan_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, B(B_KNP),
                        Ff(F_GC), B(B_DVLT), B(B_XT), B(B_WT), a.chunks, a.doc_chunk, a.H, B(B_DH), B(B_DVN));
   }
+  if (a.dkw_after)
+    if (const hipError_t e = hipStreamWaitEvent(stream, a.dkw_after, 0)) return e;
   TimedLaunch tl(K_BWD_DKW, stream);
   hipLaunchKernelGGL(bwd_dkw_kernel, grid_p, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_RK), Ff(F_GC),
                      F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.v, a.beta, F(F_TM), a.chunks, a.H, a.scale,
                      (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta);
+  return hipSuccess;
 }
 
 }  // namespace cqgdn

@@ -258,11 +258,14 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
   }
   __syncthreads();
   {
-    // T in the operand type: Ts rows [t][s], then the global copy from those rows
-    const int col = tid >> 2, p = tid & 3, bcb = col >> 4;
+    // T in the operand type: Ts rows [t][s], then the global copy from those rows.
+    // The lanes of a wave run along one row (rows 4 jj + wave), so every read and
+    // write of the copy touches 32 distinct banks (the solve matrix's row stride
+    // is 65 words: its transposed blocks are read down consecutive rows).
+    const int col = tid & 63, bcb = col >> 4;
 #pragma unroll
     for (int jj = 0; jj < 16; ++jj) {
-      const int t = 4 * jj + p, bt = t >> 4;
+      const int t = 4 * jj + wave, bt = t >> 4;
       const float val = (bt == bcb) ? Af[t * LDA + col]
                                     : (bt > bcb ? Af[(16 * bcb + (col & 15)) * LDA + 16 * bt + (t & 15)] : 0.f);
       Ts[t * LDT + col] = (E)val;
@@ -278,11 +281,14 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     }
   }
 
-  // Kg^T tile [k][perm32(t)] over the solve's matrix (free now), stored below
+  // Kg^T tile [k][perm32(t)] over the solve's matrix (free now), stored below.
+  // Row k's columns are XORed with 16 ((k / 8) % 4) (16-byte blocks stay whole):
+  // the four threads of event t write rows 8 apart, which then fall in disjoint
+  // banks instead of one.
   E* kgs = reinterpret_cast<E*>(Af);
   static_assert(sizeof(Af) >= D * CH * sizeof(E), "the KgT tile must fit the solve matrix");
   {
-    const int t = tid >> 2, p = tid & 3, tp = perm32(t);
+    const int t = tid >> 2, p = tid & 3, tp = perm32(t) ^ (16 * p);  // (k / 8) % 4 = p for k = 32 j + 8 p + s
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -343,7 +349,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int seg = 256 * i + tid, kr = seg >> 3, part = seg & 7;
-      st8(kgt + kr * CH + 8 * part, ld8(kgs + kr * CH + 8 * part));
+      st8(kgt + kr * CH + 8 * part, ld8(kgs + kr * CH + 8 * (part ^ (2 * ((kr >> 3) & 3)))));
     }
   }
 }
@@ -861,7 +867,7 @@ __global__ __launch_bounds__(256) void vscale_final_kernel(const float* __restri
 // host launchers
 // ---------------------------------------------------------------------------
 template <class E>
-static void launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stream) {
+static hipError_t launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stream) {
   E* ws[F_COUNT];
   for (int i = 0; i < F_COUNT; ++i) ws[i] = reinterpret_cast<E*>(a.ws + a.off[i]);
   float* rq = reinterpret_cast<float*>(ws[F_RQ]);
@@ -880,29 +886,35 @@ static void launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stre
                          ws[F_UT], ws[F_KGT]);
   }
   const dim3 grid_s(a.H * (D / 16), a.n_docs);
+  hipStream_t ss = stream;
+  if (a.scan_stream) {
+    if (const hipError_t e = hipEventRecord(a.scan_fork, stream)) return e;
+    if (const hipError_t e = hipStreamWaitEvent(a.scan_stream, a.scan_fork, 0)) return e;
+    ss = a.scan_stream;
+  }
   {
-    TimedLaunch tl(K_FWD_SCAN, stream);
-    hipLaunchKernelGGL(fwd_scan_kernel<E>, grid_s, dim3(SC_THREADS), 0, stream, ws[F_W], ws[F_UT], ws[F_KGT], gcum,
+    TimedLaunch tl(K_FWD_SCAN, ss);
+    hipLaunchKernelGGL(fwd_scan_kernel<E>, grid_s, dim3(SC_THREADS), 0, ss, ws[F_W], ws[F_UT], ws[F_KGT], gcum,
                        a.chunks, a.doc_chunk, a.H, vscale, a.initial_state, a.final_state, ws[F_HT], ws[F_VNT]);
   }
-  if (a.no_output) return;
+  if (a.scan_stream)
+    if (const hipError_t e = hipEventRecord(a.scan_join, a.scan_stream)) return e;
+  if (a.no_output) return hipSuccess;
   TimedLaunch tl(K_FWD_OUT, stream);
   hipLaunchKernelGGL(fwd_out_kernel<E>, dim3(a.H, a.n_chunks), dim3(256), 0, stream, ws[F_QN], ws[F_KN], gcum, ws[F_HT], ws[F_VNT],
                      a.chunks, a.H, a.scale, vscale, a.o);
+  return hipSuccess;
 }
 
-void launch_fwd(const FwdArgs& a, hipStream_t stream) {
-  if (!a.precise) {
-    launch_fwd_t<bf16>(a, nullptr, stream);
-    return;
-  }
+hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
+  if (!a.precise) return launch_fwd_t<bf16>(a, nullptr, stream);
   float* vsc = reinterpret_cast<float*>(a.ws + a.off[F_VSC]);
   const size_t nv8 = (size_t)a.T * a.H * (D / 8);
   const size_t ns = a.initial_state ? (size_t)a.n_docs * a.H * D * D : 0;
   hipLaunchKernelGGL(vscale_partial_kernel, dim3(VS_BLOCKS), dim3(256), 0, stream, a.v, nv8, a.initial_state, ns,
                      vsc + 1);
   hipLaunchKernelGGL(vscale_final_kernel, dim3(1), dim3(256), 0, stream, vsc + 1, VS_BLOCKS, vsc);
-  launch_fwd_t<f16>(a, vsc, stream);
+  return launch_fwd_t<f16>(a, vsc, stream);
 }
 
 }  // namespace cqgdn

@@ -26,6 +26,10 @@ struct FwdArgs {
   bf16* o;                     // [T][H][D]
   uint8_t* ws;
   size_t off[F_COUNT];
+  // optional: the state scan runs on scan_stream, after scan_fork (recorded on the
+  // caller's stream behind fwd_prep); scan_join is recorded behind it
+  hipStream_t scan_stream;
+  hipEvent_t scan_fork, scan_join;
 };
 
 struct BwdArgs {
@@ -42,10 +46,13 @@ struct BwdArgs {
   size_t boff[B_COUNT];
   bf16 *dq, *dk, *dv;
   float *dg, *dbeta;
+  hipEvent_t dkw_after;  // optional: bwd_dkw waits for this event (the forward scan's join)
 };
 
-void launch_fwd(const FwdArgs& a, hipStream_t stream);
-void launch_bwd(const BwdArgs& a, hipStream_t stream);
+// Both return the first error of their stream-ordering calls (hipSuccess without them);
+// launch errors are left for hipGetLastError.
+hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
+hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream);
 void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* g, const void* beta,
                       bool beta_bf16, float* state, bf16* out, int N, int E, int H, float scale,
                       hipStream_t stream);

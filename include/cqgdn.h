@@ -133,6 +133,25 @@ int cqgdn_bwd(const void* v, const float* g, const float* beta, const void* dout
               size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta, void* stream);
 
 /*
+ * The backward of the reference's `fused` mode in one call: the forward workspace is
+ * rebuilt from q, k, v, g, beta (cqgdn_fwd with CQGDN_TRAINING | CQGDN_NO_OUTPUT) and
+ * then consumed by the backward (cqgdn_bwd).  Replaces _Delta.backward when no w / h / v_new
+ * were kept (ops/gated_delta_net.py:188-194: recompute_w_u_fwd and
+ * chunk_gated_delta_rule_fwd_h, then the chain of :195-214).  Arguments as cqgdn_fwd and
+ * cqgdn_bwd; fwd_workspace is written here and needs no contents on entry.
+ * The rebuilt forward state scan runs on a second stream beside the backward's local
+ * kernel and reverse scan (neither reads h or v_new; each scan holds half of the CUs),
+ * and the last backward kernel waits for it.  That stream and its two events are
+ * created on a thread's first call on a device and kept until the process ends; the
+ * call orders them against `stream` with events, so it can be captured in a HIP graph.
+ */
+int cqgdn_bwd_recompute(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                        const void* dout, int64_t T, int H, const int32_t* chunk_table, int64_t n_chunks,
+                        const int32_t* doc_chunk, int n_docs, float scale, unsigned flags, void* fwd_workspace,
+                        size_t fwd_workspace_bytes, void* bwd_workspace, size_t bwd_workspace_bytes, void* dq,
+                        void* dk, void* dv, float* dg, float* dbeta, void* stream);
+
+/*
  * Recurrent GDN step(s): for each of N independent sequences, E events applied
  * in order to a value-first fp32 state [N][H][V][K], updated in place, as the
  * decode path does with the FLA kernel fused_recurrent_gated_delta_rule_fwd_kernel

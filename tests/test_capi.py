@@ -100,6 +100,30 @@ def test_fwd_rejects_invalid_arguments_before_launch(lib):
     assert _fwd(lib, flags=8) == _lib.EINVAL
 
 
+def _bwd_recompute(lib, **kw):
+    p = ctypes.c_void_p(256)
+    T, H, nc = kw.pop("T", 64), 4, 1
+    args = dict(q=p, k=p, v=p, g=p, beta=p, dout=p, T=T, H=H, table=p, n_chunks=nc, doc=p, n_docs=1, scale=0.1,
+                flags=_lib.NORMALIZE | _lib.TRAINING, fws=p, fws_bytes=lib.cqgdn_fwd_workspace_size(64, H, nc),
+                bws=p, bws_bytes=lib.cqgdn_bwd_workspace_size(64, H, nc), dq=p, dk=p, dv=p, dg=p, db=p, stream=None)
+    args.update(kw)
+    return lib.cqgdn_bwd_recompute(*args.values())
+
+
+def test_bwd_recompute_checks_every_argument_before_launch(lib):
+    """The fused-mode backward (forward rebuilt in the same call) rejects bad arguments of either
+    half before anything runs; every case here returns before the first HIP call."""
+    assert _bwd_recompute(lib, flags=_lib.TRAINING | 8) == _lib.EINVAL  # CQGDN_NO_OUTPUT is implied, not a flag here
+    assert _bwd_recompute(lib, T=-1) == _lib.EINVAL
+    assert _bwd_recompute(lib, q=None) == _lib.EINVAL
+    assert _bwd_recompute(lib, k=ctypes.c_void_p(258)) == _lib.EINVAL  # misaligned
+    assert _bwd_recompute(lib, dq=None) == _lib.EINVAL
+    assert _bwd_recompute(lib, bws_bytes=100) == _lib.EINVAL
+    assert b"backward workspace" in lib.cqgdn_last_error()
+    assert _bwd_recompute(lib, fws_bytes=100) == _lib.EINVAL
+    assert _bwd_recompute(lib, T=0, n_chunks=0) == _lib.OK  # nothing to do
+
+
 def test_recurrent_and_helpers_reject_invalid_arguments(lib):
     p = ctypes.c_void_p(256)
     assert lib.cqgdn_recurrent(p, p, p, p, p, 0, p, p, -1, 1, 4, 0.1, None) == _lib.EINVAL

@@ -444,6 +444,59 @@ def test_fused_mode_matches_cached_mode(gdn, monkeypatch):
     check_against_oracle(xs, bounds, do, y_f, g_f)
 
 
+def test_fused_mode_matches_cached_mode_at_config2_size(gdn, monkeypatch):
+    """At config 2's size (T = 9216, H = 16) the fused backward's rebuilt state scan runs beside its
+    local kernel and reverse scan for about 100 us; the last kernel must see its h and v_new, so every
+    gradient equals the cached mode's bitwise (the cached mode is checked against the oracle at this
+    size in test_gpu_parity.py)."""
+    from cqgdn import synthetic
+
+    T, mask, bounds = synthetic.config_events(2, seed=0)
+    print(f"case fused vs cached mode, config 2 T={T}", flush=True)
+    xs = inputs(T, 16, seed=2, readonly=mask)
+    do = torch.randn(1, T, 16, 128, generator=torch.Generator().manual_seed(102)).bfloat16()
+    res = {}
+    for mode in ("cached", "fused"):
+        monkeypatch.setattr(gdn, "MODE", mode)
+        res[mode] = fwd_bwd(gdn, xs, bounds, do)
+    (y_c, g_c), (y_f, g_f) = res["cached"], res["fused"]
+    assert torch.equal(y_c, y_f)
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dbeta"), g_c, g_f):
+        assert torch.equal(a, b), name
+
+
+def test_bwd_recompute_graph_replay(gdn):
+    """cqgdn_bwd_recompute (the fused-mode backward: forward rebuilt in the call, its state scan on a
+    second stream joined back by events) captured in a HIP graph: each replay, with eager work
+    between, equals the eager call bitwise."""
+    T, bounds, H = 700, (0, 300, 700), 8
+    print(f"case bwd_recompute graph replay T={T} bounds={bounds} H={H}", flush=True)
+    q, k, v, g, b = (x.to(DEV).contiguous() for x in inputs(T, H, seed=4242))
+    dy = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(4243)).bfloat16().to(DEV)
+
+    def run():
+        return gdn._backward(v, g, b, None, dy, bounds, True, 128 ** -0.5, recompute=(q, k))
+
+    eager = [x.clone() for x in run()]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()  # warm-up off the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = run()
+    for replay in range(3):
+        for o in outs:
+            o.fill_(0)
+        _ = (torch.randn(256, 256, device=DEV) @ torch.randn(256, 256, device=DEV)).sum().item()  # eager work between
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, o, e in zip(("dq", "dk", "dv", "dg", "dbeta"), outs, eager):
+            assert torch.equal(o, e), f"replay {replay}: {name} differs"
+
+
 def test_delta_fp16_inputs_match_oracle(gdn):
     """fp16 q/k/v, which the reference's delta accepts (ops/gated_delta_net.py:233-234): output and
     gradients come back in the input dtypes and match the float64 oracle of the same fp16 values."""
