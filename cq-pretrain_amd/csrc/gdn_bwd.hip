@@ -602,19 +602,17 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       const f32x4 dpm = (n <= wave) ? pair(wave, n, rowE) : zero4();
       st4(dPm + (16 * n + r) * LDT + 16 * wave + 4 * q4, dpm);  // transposed: dPm^T[s][t], 4 rows t in 8 bytes
     }
+    sum16x4(rowE);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float x = sum16(rowE[i]);
-      if (r == 0) dgl[16 * wave + 4 * q4 + i] += x;
-    }
+    for (int i = 0; i < 4; ++i)
+      if (r == 0) dgl[16 * wave + 4 * q4 + i] += rowE[i];
     if (wave == 0) {
       float rowE3[4] = {0.f, 0.f, 0.f, 0.f};
       st4(dPm + (48 + r) * LDT + 48 + 4 * q4, pair(3, 3, rowE3));
+      sum16x4(rowE3);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x = sum16(rowE3[i]);
-        if (r == 0) dgl[48 + 4 * q4 + i] += x;
-      }
+      for (int i = 0; i < 4; ++i)
+        if (r == 0) dgl[48 + 4 * q4 + i] += rowE3[i];
     }
   }
   lds_barrier();
@@ -657,20 +655,22 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       f32x4 qc[2];
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm) qc[mm] = cvtf4(ld4_c(Qs, LDK, 16 * n, 16 * (2 * wave + mm)));
+      float x[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = 16 * n + 4 * q4 + i;
         const float f = scale * __expf(g4[i]);
-        float x = 0.f;
+        x[i] = 0.f;
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm) {
           const float inter = a1[mm][n][i] * f;
           dQ[mm][n][i] += inter;
-          x += qc[mm][i] * inter;
+          x[i] += qc[mm][i] * inter;
         }
-        x = sum16(x);
-        if (r == 0) dgl[t] += x;
       }
+      sum16x4(x);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (r == 0) dgl[16 * n + 4 * q4 + i] += x[i];
     }
   }
 
@@ -683,11 +683,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     for (int mm = 0; mm < 2; ++mm) qc[mm] = cvtf4(ld4_c(Qs, LDK, 16 * n, 16 * (2 * wave + mm)));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float x = 0.f;
+      pdot[n][i] = 0.f;
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) x += qc[mm][i] * dQ[mm][n][i];
-      pdot[n][i] = sum16(x);
+      for (int mm = 0; mm < 2; ++mm) pdot[n][i] += qc[mm][i] * dQ[mm][n][i];
     }
+    sum16x4(pdot[n]);
   }
   lds_barrier();  // every read of the dO rows is done: the row dots and then the dVn tile may replace them
   if (r == 0) {
@@ -942,13 +942,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       return dmp;
     };
     auto rows = [&](int it, const float(&rowB)[4], const float(&rowE)[4]) {
+      float xb[4] = {rowB[0], rowB[1], rowB[2], rowB[3]}, xe[4] = {rowE[0], rowE[1], rowE[2], rowE[3]};
+      sum16x4(xb);
+      sum16x4(xe);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float xb = sum16(rowB[e]);
-        const float xe = sum16(rowE[e]);
         if (r == 0) {
-          dbl[16 * it + 4 * q4 + e] += xb;
-          dgl[16 * it + 4 * q4 + e] += xe;
+          dbl[16 * it + 4 * q4 + e] += xb[e];
+          dgl[16 * it + 4 * q4 + e] += xe[e];
         }
       }
     };

@@ -403,12 +403,16 @@ __device__ __forceinline__ float sum16(float x) {
 // Written as assembly with two tied operands because this compiler's builtin drops the
 // second result when both inputs are the same value; the s_nops give the swaps their
 // VALU hazard distance on both sides.
+// The leading s_nop 1 gives the swap's operands, which a VALU copy has just written, the
+// two wait states a VALU write needs before a permlane reads it (the compiler cannot place
+// hazard waits inside inline assembly); the swap's results may be read at once (this
+// compiler's own schedule for the builtin reads them in the next instruction).
 __device__ __forceinline__ float sum_rows4(float x) {
   float a = x, b = x;
-  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
   x = a + b;
   float c = x, d = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(c), "+v"(d));
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(c), "+v"(d));
   return c + d;
 }
 
@@ -419,6 +423,21 @@ __device__ __forceinline__ float dot8(bf16x8 a, bf16x8 b, float c) {
   for (int e = 0; e < 8; e += 2)
     c = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{a[e], a[e + 1]}, bf16x2{b[e], b[e + 1]}, c, false);
   return c;
+}
+
+// sum16 of four independent values, level by level (each value gets the same operations in
+// the same order as sum16): a DPP move then reads a register written three instructions
+// earlier, so the levels need no wait states between them (one value at a time, every level
+// waits two cycles for the previous one)
+__device__ __forceinline__ void sum16x4(float (&x)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] += dpp_f<0xB1>(x[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] += dpp_f<0x4E>(x[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] += dpp_f<0x140>(x[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] += dpp_f<0x141>(x[i]);
 }
 
 // sum over the 4 lanes of a quad (lanes 4a .. 4a + 3), the first two levels of sum16
