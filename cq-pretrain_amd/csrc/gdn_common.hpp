@@ -416,6 +416,16 @@ __device__ __forceinline__ float sum_rows4(float x) {
   return c + d;
 }
 
+// x + x from lane ^ 16 (the sum over 16-lane rows 2i and 2i + 1), bit for bit the same as
+// x + __shfl_xor(x, 16) (the addition commutes), on the VALU: v_permlane16_swap with both
+// operands holding x leaves row 2i's value in one and row 2i + 1's in the other, instead of
+// a ds_bpermute round trip through the LDS pipeline
+__device__ __forceinline__ float sum_xor16(float x) {
+  float a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return a + b;
+}
+
 // c + sum of a[e] b[e] over 8 bf16 pairs, as four v_dot2_f32_bf16 (products and sums in fp32)
 __device__ __forceinline__ float dot8(bf16x8 a, bf16x8 b, float c) {
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));

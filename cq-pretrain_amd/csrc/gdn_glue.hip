@@ -539,22 +539,34 @@ __global__ __launch_bounds__(512) void decode_step_kernel(DecArgs a, float* __re
     const f32x4 kk = *reinterpret_cast<const f32x4*>(&ks[4 * c4]);
     const f32x4 qc = *reinterpret_cast<const f32x4*>(&qs[0][4 * c4]);
     const f32x4 qq = *reinterpret_cast<const f32x4*>(&qs[1][4 * c4]);
+    // four rows at a time: row sums level by level, cross-row steps on the VALU (as in
+    // recurrent_kernel)
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      st[jj] *= ge;
-      float dot = st[jj][0] * kk[0] + st[jj][1] * kk[1] + st[jj][2] * kk[2] + st[jj][3] * kk[3];
-      dot = sum16(dot);
-      dot += __shfl_xor(dot, 16, 64);
-      st[jj] += kk * ((vs[rbase + 2 * jj] - dot) * be);
-      float oc = st[jj][0] * qc[0] + st[jj][1] * qc[1] + st[jj][2] * qc[2] + st[jj][3] * qc[3];
-      oc = sum16(oc);
-      oc += __shfl_xor(oc, 16, 64);
-      float oq = st[jj][0] * qq[0] + st[jj][1] * qq[1] + st[jj][2] * qq[2] + st[jj][3] * qq[3];
-      oq = sum16(oq);
-      oq += __shfl_xor(oq, 16, 64);
-      if (c4 == 0) {
-        ys[0][rbase + 2 * jj] = (float)(bf16)(oc * scale);
-        ys[1][rbase + 2 * jj] = (float)(bf16)(oq * scale);
+    for (int j0 = 0; j0 < 8; j0 += 4) {
+      float dot[4], oc[4], oq[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f32x4& sj = st[j0 + i];
+        sj *= ge;
+        dot[i] = sj[0] * kk[0] + sj[1] * kk[1] + sj[2] * kk[2] + sj[3] * kk[3];
+      }
+      sum16x4(dot);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f32x4& sj = st[j0 + i];
+        sj += kk * ((vs[rbase + 2 * (j0 + i)] - sum_xor16(dot[i])) * be);
+        oc[i] = sj[0] * qc[0] + sj[1] * qc[1] + sj[2] * qc[2] + sj[3] * qc[3];
+        oq[i] = sj[0] * qq[0] + sj[1] * qq[1] + sj[2] * qq[2] + sj[3] * qq[3];
+      }
+      sum16x4(oc);
+      sum16x4(oq);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float c = sum_xor16(oc[i]), qv = sum_xor16(oq[i]);
+        if (c4 == 0) {
+          ys[0][rbase + 2 * (j0 + i)] = (float)(bf16)(c * scale);
+          ys[1][rbase + 2 * (j0 + i)] = (float)(bf16)(qv * scale);
+        }
       }
     }
 #pragma unroll

@@ -44,17 +44,27 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const bf16* __restrict__
     float vv[8], o[8];
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj) vv[jj] = (float)v[ev * D + rbase + 2 * jj];
+    // four rows at a time: their row sums run level by level (no wait states between DPP
+    // levels) and the cross-row step is a VALU swap, not an LDS-pipeline permute
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj) {
-      s[jj] *= ge;
-      float dot = s[jj][0] * kk[0] + s[jj][1] * kk[1] + s[jj][2] * kk[2] + s[jj][3] * kk[3];
-      dot = sum16(dot);
-      dot += __shfl_xor(dot, 16, 64);
-      s[jj] += kk * ((vv[jj] - dot) * be);
-      float od = s[jj][0] * qq[0] + s[jj][1] * qq[1] + s[jj][2] * qq[2] + s[jj][3] * qq[3];
-      od = sum16(od);
-      od += __shfl_xor(od, 16, 64);
-      o[jj] = od;
+    for (int j0 = 0; j0 < 8; j0 += 4) {
+      float dot[4], od[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f32x4& sj = s[j0 + i];
+        sj *= ge;
+        dot[i] = sj[0] * kk[0] + sj[1] * kk[1] + sj[2] * kk[2] + sj[3] * kk[3];
+      }
+      sum16x4(dot);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        f32x4& sj = s[j0 + i];
+        sj += kk * ((vv[j0 + i] - sum_xor16(dot[i])) * be);
+        od[i] = sj[0] * qq[0] + sj[1] * qq[1] + sj[2] * qq[2] + sj[3] * qq[3];
+      }
+      sum16x4(od);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[j0 + i] = sum_xor16(od[i]);
     }
     if (c4 == 0) {
 #pragma unroll
