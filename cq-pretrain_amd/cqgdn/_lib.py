@@ -16,8 +16,8 @@ LIB_PATH = Path(__file__).resolve().with_name("libcqgdn.so")
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 NORMALIZE, TRAINING, PRECISE, NO_OUTPUT = 1, 2, 4, 8
 STATIC_WORKSPACE_BYTES = 64 << 20  # CQGDN_STATIC_WORKSPACE_BYTES
-FWD_BUFFERS, BWD_BUFFERS = 12, 6
-FWD_NAMES = ("qn", "kn", "rq", "rk", "gcum", "T", "W", "UT", "KgT", "hT", "vnT", "vscale")
+FWD_BUFFERS, BWD_BUFFERS = 10, 6
+FWD_NAMES = ("rq", "rk", "gcum", "T", "W", "UT", "KgT", "hT", "vnT", "vscale")
 BWD_NAMES = ("dvlT", "XT", "dh", "dVn", "knP", "WT")
 
 # every symbol include/cqgdn.h declares, with (restype, argtypes)
@@ -32,8 +32,8 @@ SIGNATURES = {
     "cqgdn_bwd_buffer_offsets": (_I, [_I64, _I, _I64, _P, _I]),
     "cqgdn_fwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _P, _P, _P, _SZ, _P]),
     "cqgdn_fwd_static": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _P, _P, _P]),
-    "cqgdn_bwd": (_I, [_P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _SZ, _P, _SZ, _P, _P, _P, _P, _P,
-                       _P]),
+    "cqgdn_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _SZ, _P, _SZ, _P, _P, _P, _P,
+                       _P, _P]),
     "cqgdn_bwd_recompute": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _SZ, _P, _SZ, _P,
                                  _P, _P, _P, _P, _P]),
     "cqgdn_recurrent": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _F, _P]),

@@ -178,14 +178,14 @@ class _LayerCore(torch.autograd.Function):
         rstd = torch.empty(n_h, H, dtype=torch.float32, device=dev)
         gdn.call("cqgdn_gated_norm_fwd", gdn._ptr(y), gdn._ptr(ep.hidden_index), n_h, H, proj[:, zc:].data_ptr(),
                  PS, gdn._ptr(nw), float(eps), gdn._ptr(out), gdn._ptr(rstd), st)
-        ctx.save_for_backward(proj, w, alog, dtb, nw, v, gb, rws, y, rstd)
+        ctx.save_for_backward(proj, w, alog, dtb, nw, q, k, v, gb, rws, y, rstd)
         ctx.ep, ctx.H, ctx.HK, ctx.scale = ep, H, HK, scale
         ctx.dtypes = (conv_weight.dtype, A_log.dtype, dt_bias.dtype, norm_weight.dtype)
         return out.reshape(n_h, S)
 
     @staticmethod
     def backward(ctx, dout):
-        proj, w, alog, dtb, nw, v, gb, rws, y, rstd = ctx.saved_tensors
+        proj, w, alog, dtb, nw, q, k, v, gb, rws, y, rstd = ctx.saved_tensors
         ep, H, HK = ctx.ep, ctx.H, ctx.HK
         n_h, P, PS = proj.shape[0], proj.shape[1], proj.stride(0)
         C, zc, ac, bc, width = _columns(H, HK)
@@ -202,8 +202,8 @@ class _LayerCore(torch.autograd.Function):
                  ep.unread_events.numel(), n_h, H, proj[:, zc:].data_ptr(), PS, gdn._ptr(nw), gdn._ptr(rstd),
                  gdn._ptr(do), gdn._ptr(dy), d_proj[:, zc:].data_ptr(), P, gdn._ptr(dnw), gdn._ptr(nws),
                  nws.numel(), st)
-        dq, dk, dv, dg, db = gdn._backward(v[None], gb[0][None], gb[1][None], rws, dy, ep.event_bounds, True,
-                                           ctx.scale)
+        dq, dk, dv, dg, db = gdn._backward(q[None], k[None], v[None], gb[0][None], gb[1][None], rws, dy,
+                                           ep.event_bounds, True, ctx.scale)
         dw = torch.empty(w.shape, dtype=torch.float32, device=dev)
         dgate = torch.empty(2 * H, dtype=torch.float32, device=dev)
         ews = torch.empty(_lib.lib().cqgdn_event_inputs_bwd_workspace_size(ctypes.byref(ep.cstruct), H, HK),

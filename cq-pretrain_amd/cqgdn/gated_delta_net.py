@@ -281,7 +281,7 @@ class _Delta(torch.autograd.Function):
         if MODE == "fused":  # the inputs only: the backward rebuilds the workspace
             ctx.save_for_backward(qf, kf, vf, gf, bf)
         else:
-            ctx.save_for_backward(vf, gf, bf, ws)
+            ctx.save_for_backward(qf, kf, vf, gf, bf, ws)
         ctx.bounds, ctx.scale, ctx.normalize = bounds, scale, normalize
         return o if o.shape == v.shape and o.dtype == v.dtype else o.reshape(v.shape).to(v.dtype)
 
@@ -289,18 +289,18 @@ class _Delta(torch.autograd.Function):
     def backward(ctx, dy):
         if ctx.mode == "fused":  # one call rebuilds the forward workspace and runs the backward
             q, k, v, g, beta = ctx.saved_tensors
-            grads = _backward(v, g, beta, None, dy, ctx.bounds, ctx.normalize, ctx.scale, recompute=(q, k))
+            grads = _backward(q, k, v, g, beta, None, dy, ctx.bounds, ctx.normalize, ctx.scale)
         else:
-            v, g, beta, ws = ctx.saved_tensors
-            grads = _backward(v, g, beta, ws, dy, ctx.bounds, ctx.normalize, ctx.scale)
+            q, k, v, g, beta, ws = ctx.saved_tensors
+            grads = _backward(q, k, v, g, beta, ws, dy, ctx.bounds, ctx.normalize, ctx.scale)
         grads = [x if x.shape == shape and x.dtype == dtype else x.reshape(shape).to(dtype)
                  for x, shape, dtype in zip(grads, ctx.shapes, ctx.input_dtypes)]
         return *grads, None, None, None
 
 
-def _backward(v, g, beta, ws, dy, bounds, normalize, scale, recompute=None):
+def _backward(q, k, v, g, beta, ws, dy, bounds, normalize, scale):
     """dq, dk, dv, dg, dbeta of the packed chunked forward whose TRAINING workspace is ``ws``; with
-    ``recompute=(q, k)`` (``ws`` None) the workspace is rebuilt inside the same call (fused mode)."""
+    ``ws`` None the workspace is rebuilt inside the same call (fused mode)."""
     t, h = v.shape[1], v.shape[2]
     cu, table, doc = device_metadata(bounds, str(v.device))
     n_chunks, n_docs = table.shape[0], len(bounds) - 1
@@ -311,12 +311,11 @@ def _backward(v, g, beta, ws, dy, bounds, normalize, scale, recompute=None):
     dq, dk, dv = torch.empty_like(v), torch.empty_like(v), torch.empty_like(v)
     dg, db = torch.empty_like(g), torch.empty_like(beta)
     flags = (_lib.NORMALIZE if normalize else 0) | _lib.TRAINING
-    if recompute is None:
-        call("cqgdn_bwd", _ptr(v), _ptr(g), _ptr(beta), _ptr(dy), t, h, _ptr(table), n_chunks, _ptr(doc), n_docs,
+    if ws is not None:
+        call("cqgdn_bwd", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(dy), t, h, _ptr(table), n_chunks, _ptr(doc), n_docs,
              float(scale), flags, _ptr(ws), ws.numel(), _ptr(bws), bws.numel(), _ptr(dq), _ptr(dk), _ptr(dv),
              _ptr(dg), _ptr(db), _stream(v.device))
     else:
-        q, k = recompute
         ws = torch.empty(_lib.lib().cqgdn_fwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=v.device)
         call("cqgdn_bwd_recompute", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(dy), t, h, _ptr(table),
              n_chunks, _ptr(doc), n_docs, float(scale), flags, _ptr(ws), ws.numel(), _ptr(bws), bws.numel(),

@@ -245,7 +245,8 @@ int fwd_impl(const void* q, const void* k, const void* v, const float* g, const 
 
 // cqgdn_bwd's checks and launch; with launch == false only the checks (for a caller
 // that must know the backward's arguments are valid before it launches anything).
-int bwd_impl(const void* v, const float* g, const float* beta, const void* dout, int64_t T, int H,
+int bwd_impl(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dout,
+             int64_t T, int H,
              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
              unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes, void* bwd_workspace,
              size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta, void* stream,
@@ -253,17 +254,20 @@ int bwd_impl(const void* v, const float* g, const float* beta, const void* dout,
   if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
   if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING)) return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
   if (T == 0) return ok();
-  if (!v || !g || !beta || !dout || !fwd_workspace || !bwd_workspace || !dq || !dk || !dv || !dg || !dbeta)
+  if (!q || !k || !v || !g || !beta || !dout || !fwd_workspace || !bwd_workspace || !dq || !dk || !dv || !dg ||
+      !dbeta)
     return fail(CQGDN_EINVAL, "null tensor pointer");
   const size_t fneed = cqgdn_fwd_workspace_size(T, H, n_chunks);
   const size_t bneed = cqgdn_bwd_workspace_size(T, H, n_chunks);
   if (fwd_workspace_bytes < fneed) return fail(CQGDN_EINVAL, "forward workspace too small: %zu < %zu", fwd_workspace_bytes, fneed);
   if (bwd_workspace_bytes < bneed) return fail(CQGDN_EINVAL, "backward workspace too small: %zu < %zu", bwd_workspace_bytes, bneed);
   if (!aligned(fwd_workspace, 256) || !aligned(bwd_workspace, 256)) return fail(CQGDN_EINVAL, "workspaces must be 256-byte aligned");
-  for (const void* p : {v, dout, (const void*)dq, (const void*)dk, (const void*)dv})
-    if (!aligned(p, 16)) return fail(CQGDN_EINVAL, "v/do/dq/dk/dv must be 16-byte aligned");
+  for (const void* p : {q, k, v, dout, (const void*)dq, (const void*)dk, (const void*)dv})
+    if (!aligned(p, 16)) return fail(CQGDN_EINVAL, "q/k/v/do/dq/dk/dv must be 16-byte aligned");
   if (!launch) return ok();
   BwdArgs a{};
+  a.q = static_cast<const bf16*>(q);
+  a.k = static_cast<const bf16*>(k);
   a.v = static_cast<const bf16*>(v);
   a.dout = static_cast<const bf16*>(dout);
   a.g = g;
@@ -324,11 +328,12 @@ int scan_side(ScanSide** out) {
 
 extern "C" {
 
-int cqgdn_bwd(const void* v, const float* g, const float* beta, const void* dout, int64_t T, int H,
-              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
-              unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes, void* bwd_workspace,
-              size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta, void* stream) {
-  return bwd_impl(v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags, fwd_workspace,
+int cqgdn_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dout,
+              int64_t T, int H, const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs,
+              float scale, unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes,
+              void* bwd_workspace, size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta,
+              void* stream) {
+  return bwd_impl(q, k, v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags, fwd_workspace,
                   fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg, dbeta, stream, true,
                   nullptr);
 }
@@ -340,14 +345,11 @@ int cqgdn_bwd_recompute(const void* q, const void* k, const void* v, const float
                         void* dk, void* dv, float* dg, float* dbeta, void* stream) {
   if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING)) return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
   // every argument is checked before anything is launched
-  if (const int e = bwd_impl(v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags,
+  if (const int e = bwd_impl(q, k, v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags,
                              fwd_workspace, fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg,
                              dbeta, stream, false, nullptr))
     return e;
   if (T == 0) return ok();
-  if (!q || !k) return fail(CQGDN_EINVAL, "null tensor pointer");
-  for (const void* p : {q, k})
-    if (!aligned(p, 16)) return fail(CQGDN_EINVAL, "q/k/v/o must be 16-byte aligned");
   ScanSide* side = nullptr;
   if (const int e = scan_side(&side)) return e;
   const unsigned fflags = (flags & CQGDN_NORMALIZE) | CQGDN_TRAINING | CQGDN_NO_OUTPUT;
@@ -355,9 +357,9 @@ int cqgdn_bwd_recompute(const void* q, const void* k, const void* v, const float
                              nullptr, nullptr, fwd_workspace, fwd_workspace_bytes, stream, side->stream, side->fork,
                              side->join))
     return e;
-  return bwd_impl(v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags, fwd_workspace,
-                  fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg, dbeta, stream, true,
-                  side->join);
+  return bwd_impl(q, k, v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags,
+                  fwd_workspace, fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg, dbeta, stream,
+                  true, side->join);
 }
 
 int cqgdn_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta, int beta_is_bf16,

@@ -33,8 +33,9 @@ constexpr int LDT = 72;   // bf16 row stride, 128 x 64 and 64 x 64 tiles
 // bwd_local
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
-    const bf16* __restrict__ qn, const bf16* __restrict__ kn, const bf16* __restrict__ dout,
-    const float* __restrict__ gc, const float* __restrict__ beta, const bf16* __restrict__ Tm,
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ rq,
+    const float* __restrict__ rk, const bf16* __restrict__ dout, const float* __restrict__ gc,
+    const float* __restrict__ beta, const bf16* __restrict__ Tm,
     const int32_t* __restrict__ chunks, int H, float scale, bf16* __restrict__ dvlT, bf16* __restrict__ XT,
     bf16* __restrict__ knP, bf16* __restrict__ WT) {
   // grid (H, NC), chunks dispatched first to last: the reverse state scan that
@@ -67,24 +68,25 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
     const int tc = clamp_row(t, ci.len);
-    const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
+    const size_t ev = (size_t)(ci.start + tc) * H + h, row = ev * D;
+    const float rqt = rq[ev], rkt = rk[ev];
     bf16x8 xq[4], xk[4], xd[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      xq[j] = ld8(qn + row + col);
-      xk[j] = ld8(kn + row + col);
+      xq[j] = ld8(q + row + col);
+      xk[j] = ld8(k + row + col);
       xd[j] = ld8(dout + row + col);
     }
     if (p == 0) {
-      Gs[t] = gc[(size_t)(ci.start + tc) * H + h];
-      Bs[t] = keep_if(in, beta[(size_t)(ci.start + tc) * H + h]);
+      Gs[t] = gc[ev];
+      Bs[t] = keep_if(in, beta[ev]);
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      st8(Qs + t * LDK + col, keep_if(in, xq[j]));
-      st8(Ks + t * LDK + col, keep_if(in, xk[j]));
+      st8(Qs + t * LDK + col, keep_if(in, scaled8<bf16>(xq[j], rqt)));
+      st8(Ks + t * LDK + col, keep_if(in, scaled8<bf16>(xk[j], rkt)));
       st8(dOs + t * LDK + col, keep_if(in, xd[j]));
     }
   }
@@ -469,7 +471,7 @@ constexpr int DKW_R1 = 0, DKW_R2 = 64 * LDK * 2, DKW_R3 = DKW_R2 + 64 * LDK * 2,
               DKW_R4B = DKW_R4A + 64 * LDK * 2, DKW_BYTES = DKW_R4B + 128 * LDT * 2;
 
 __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
-    const bf16* __restrict__ qn, const bf16* __restrict__ kn, const float* __restrict__ rq,
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ rq,
     const float* __restrict__ rk, const float* __restrict__ gc, const bf16* __restrict__ hT,
     const bf16* __restrict__ vnT, const bf16* __restrict__ dout, const bf16* __restrict__ dh,
     const bf16* __restrict__ dVn, const bf16* __restrict__ vin, const float* __restrict__ beta,
@@ -523,9 +525,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
     const int tc = clamp_row(t, ci.len);
-    const size_t row = ((size_t)(ci.start + tc) * H + h) * D;
-    const float gv = gc[(size_t)(ci.start + tc) * H + h];
-    const float rv = rq[(size_t)(ci.start + tc) * H + h];
+    const size_t ev = (size_t)(ci.start + tc) * H + h, row = ev * D;
+    const float gv = gc[ev];
+    const float rv = rq[ev], rkv = rk[ev];
     const bf16* vt = vnT + cb * (D * CH);
     bf16x8 xv[4], xq[4], xk[4], xo[4];
 #pragma unroll
@@ -536,8 +538,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      xq[j] = ld8(qn + row + col);
-      xk[j] = ld8(kn + row + col);
+      xq[j] = ld8(q + row + col);
+      xk[j] = ld8(k + row + col);
       xo[j] = ld8(dout + row + col);
     }
     dgw[wave][lane] = 0.f;
@@ -553,8 +555,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      st8(Qs + t * LDK + col, keep_if(in, xq[j]));
-      st8(Ks + t * LDK + col, keep_if(in, xk[j]));
+      st8(Qs + t * LDK + col, keep_if(in, scaled8<bf16>(xq[j], rv)));
+      st8(Ks + t * LDK + col, keep_if(in, scaled8<bf16>(xk[j], rkv)));
       st8(dOs + t * LDK + col, keep_if(in, xo[j]));
     }
 #pragma unroll
@@ -1116,8 +1118,9 @@ hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
   const dim3 grid_p(a.H, a.n_chunks);  // chunk-major dispatch (the kernels pick the chunk order)
   {
     TimedLaunch tl(K_BWD_LOCAL, stream);
-    hipLaunchKernelGGL(bwd_local_kernel, dim3(a.H, a.n_chunks), dim3(256), 0, stream, F(F_QN), F(F_KN), a.dout,
-                       Ff(F_GC), a.beta, F(F_TM), a.chunks, a.H, a.scale, B(B_DVLT), B(B_XT), B(B_KNP), B(B_WT));
+    hipLaunchKernelGGL(bwd_local_kernel, dim3(a.H, a.n_chunks), dim3(256), 0, stream, a.q, a.k, Ff(F_RQ),
+                       Ff(F_RK), a.dout, Ff(F_GC), a.beta, F(F_TM), a.chunks, a.H, a.scale, B(B_DVLT), B(B_XT),
+                       B(B_KNP), B(B_WT));
   }
   {
     TimedLaunch tl(K_BWD_SCAN, stream);
@@ -1127,7 +1130,7 @@ hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
   if (a.dkw_after)
     if (const hipError_t e = hipStreamWaitEvent(stream, a.dkw_after, 0)) return e;
   TimedLaunch tl(K_BWD_DKW, stream);
-  hipLaunchKernelGGL(bwd_dkw_kernel, grid_p, dim3(256), 0, stream, F(F_QN), F(F_KN), Ff(F_RQ), Ff(F_RK), Ff(F_GC),
+  hipLaunchKernelGGL(bwd_dkw_kernel, grid_p, dim3(256), 0, stream, a.q, a.k, Ff(F_RQ), Ff(F_RK), Ff(F_GC),
                      F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.v, a.beta, F(F_TM), a.chunks, a.H, a.scale,
                      (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta);
   return hipSuccess;

@@ -179,6 +179,14 @@ template <class E>
 __device__ __forceinline__ typename Vec<E>::x8 zero8v() {
   return to8<E>(f32x8{});
 }
+// Eight values of a q or k input row as a kernel operand: E of float(x) * r,
+// with r = rsqrt(sum x^2 + eps) of the row (1 without the in-kernel l2norm,
+// where the product is exact).  fwd_prep forms its operands this way, so every
+// kernel that reads q or k rounds them identically.
+template <class E>
+__device__ __forceinline__ typename Vec<E>::x8 scaled8(bf16x8 x, float r) {
+  return to8<E>(cvtf8(x) * r);
+}
 // two C tiles -> one permuted-map operand (as pack_perm, for either element type)
 template <class E>
 __device__ __forceinline__ typename Vec<E>::x8 pack_permv(f32x4 lo, f32x4 hi) {

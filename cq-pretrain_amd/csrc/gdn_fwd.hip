@@ -34,7 +34,7 @@ template <class E, bool NORMALIZE>
 __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const int32_t* __restrict__ chunks,
-    int H, const float* __restrict__ vscale, E* __restrict__ qn, E* __restrict__ kn, float* __restrict__ rq,
+    int H, const float* __restrict__ vscale, float* __restrict__ rq,
     float* __restrict__ rk, float* __restrict__ gc, E* __restrict__ Tm, E* __restrict__ W,
     E* __restrict__ UT, E* __restrict__ KgT) {
   typedef typename Vec<E>::x8 X8;
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) vg[nn][kb] = col8_load_rows(vb, H * D, 32 * kb, 16 * (2 * wave + nn), ci.len);
   }
-  const int rowe = H * D * (int)sizeof(E);  // bytes per event row of qn, kn, W
+  const int rowe = H * D * (int)sizeof(E);  // bytes per event row of W
   const int rows_bytes = ((ci.len - 1) * H + 1) * D * (int)sizeof(E);
   const int gate_bytes = ((ci.len - 1) * H + 1) * (int)sizeof(float);
 
@@ -118,12 +118,9 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     const float gam_t = __expf(Gs[t]);
     const float kdec_t = __expf(glast - Gs[t]);
     const float b_t = Bs[t];
-    const __amdgpu_buffer_rsrc_t qn_rs = buf_rsrc(qn + ((size_t)ci.start * H + h) * D, rows_bytes);
-    const __amdgpu_buffer_rsrc_t kn_rs = buf_rsrc(kn + ((size_t)ci.start * H + h) * D, rows_bytes);
     const __amdgpu_buffer_rsrc_t rq_rs = buf_rsrc(rq + (size_t)ci.start * H + h, gate_bytes);
     const __amdgpu_buffer_rsrc_t rk_rs = buf_rsrc(rk + (size_t)ci.start * H + h, gate_bytes);
-    const int rvo = t * rowe + 8 * p * (int)sizeof(E);  // this thread's piece of row t
-    // q
+    // q: only its scale is stored; each reader forms its own operand rows (scaled8)
     {
       f32x8 x[4];
 #pragma unroll
@@ -138,8 +135,6 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
         ss = sum4(ss);
         rs = rsqrtf(ss + 1e-6f);
       }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) buf_st16(qn_rs, rvo + 32 * j * (int)sizeof(E), 0, to8<E>(x[j] * rs));
       buf_stf(rq_rs, t * H * 4, 0, rs);  // the four threads of row t store the same value
     }
     // k
@@ -163,7 +158,6 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
         const X8 xb = to8<E>(xn);
         const int col = 32 * j + 8 * p;
         st8(Ks + t * LDK + col, xb);
-        buf_st16(kn_rs, rvo + 32 * j * (int)sizeof(E), 0, xb);
         kb8[j] = to8<E>(xn * (b_t * gam_t));
         kg8[j] = to8<E>(xn * kdec_t);
       }
@@ -704,8 +698,9 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
 // ---------------------------------------------------------------------------
 template <class E>
 __global__ __launch_bounds__(256) void fwd_out_kernel(
-    const E* __restrict__ qn, const E* __restrict__ kn, const float* __restrict__ gc,
-    const E* __restrict__ hT, const E* __restrict__ vnT, const int32_t* __restrict__ chunks, int H,
+    const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ rq,
+    const float* __restrict__ rk, const float* __restrict__ gc, const E* __restrict__ hT,
+    const E* __restrict__ vnT, const int32_t* __restrict__ chunks, int H,
     float scale, const float* __restrict__ vscale, bf16* __restrict__ o) {
   typedef typename Vec<E>::x8 X8;
   // grid (H, NC), chunks last to first: the state scan wrote the last chunks
@@ -736,14 +731,22 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
   {
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
-    const size_t row = ((size_t)(ci.start + clamp_row(t, ci.len)) * H + h) * D;
+    const size_t ev = (size_t)(ci.start + clamp_row(t, ci.len)) * H + h, row = ev * D;
+    const float rqt = rq[ev], rkt = rk[ev];
+    bf16x8 xq[4], xk[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      st8(Qs + t * LDK + col, keep_if(in, ld8(qn + row + col)));
-      st8(Ks + t * LDK + col, keep_if(in, ld8(kn + row + col)));
+      xq[j] = ld8(q + row + col);
+      xk[j] = ld8(k + row + col);
     }
-    if (p == 0) Gs[t] = gc[(size_t)(ci.start + (in ? t : ci.len - 1)) * H + h];
+    if (p == 0) Gs[t] = gc[ev];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = 32 * j + 8 * p;
+      st8(Qs + t * LDK + col, keep_if(in, scaled8<E>(xq[j], rqt)));
+      st8(Ks + t * LDK + col, keep_if(in, scaled8<E>(xk[j], rkt)));
+    }
   }
   __syncthreads();
 
@@ -878,11 +881,11 @@ static hipError_t launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_
     const dim3 grid_p(a.H, a.n_chunks);
     if (a.normalize)
       hipLaunchKernelGGL((fwd_prep_kernel<E, true>), grid_p, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
-                         a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W],
+                         a.chunks, a.H, vscale, rq, rk, gcum, ws[F_TM], ws[F_W],
                          ws[F_UT], ws[F_KGT]);
     else
       hipLaunchKernelGGL((fwd_prep_kernel<E, false>), grid_p, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
-                         a.chunks, a.H, vscale, ws[F_QN], ws[F_KN], rq, rk, gcum, ws[F_TM], ws[F_W],
+                         a.chunks, a.H, vscale, rq, rk, gcum, ws[F_TM], ws[F_W],
                          ws[F_UT], ws[F_KGT]);
   }
   const dim3 grid_s(a.H * (D / 16), a.n_docs);
@@ -901,8 +904,8 @@ static hipError_t launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_
     if (const hipError_t e = hipEventRecord(a.scan_join, a.scan_stream)) return e;
   if (a.no_output) return hipSuccess;
   TimedLaunch tl(K_FWD_OUT, stream);
-  hipLaunchKernelGGL(fwd_out_kernel<E>, dim3(a.H, a.n_chunks), dim3(256), 0, stream, ws[F_QN], ws[F_KN], gcum, ws[F_HT], ws[F_VNT],
-                     a.chunks, a.H, a.scale, vscale, a.o);
+  hipLaunchKernelGGL(fwd_out_kernel<E>, dim3(a.H, a.n_chunks), dim3(256), 0, stream, a.q, a.k, rq, rk, gcum,
+                     ws[F_HT], ws[F_VNT], a.chunks, a.H, a.scale, vscale, a.o);
   return hipSuccess;
 }
 

@@ -33,7 +33,7 @@ struct FwdArgs {
 };
 
 struct BwdArgs {
-  const bf16 *v, *dout;
+  const bf16 *q, *k, *v, *dout;
   const float *g, *beta;
   const int32_t* chunks;
   const int32_t* doc_chunk;

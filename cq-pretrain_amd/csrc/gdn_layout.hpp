@@ -2,12 +2,15 @@
 //
 // In the precise forward (CQGDN_PRECISE) every buffer listed as bf16 holds fp16.
 //
-// The forward workspace holds everything the backward re-reads (the reference
-// saves q,k,v,gcum,beta,A in fused mode and also w,h,v_new in cached mode,
-// ops/gated_delta_net.py:184); keeping h and v_new avoids re-running the serial
-// state scan in the backward.  Buffers are addressed by event (time-first
-// [T][H][D], the caller's TND order) or by chunk ([NC][H][...], one 64-event
-// block per chunk, rows past a tail chunk's length are zero).  Value-slice-major
+// The forward workspace holds everything the backward re-reads apart from the
+// inputs (the reference saves q,k,v,gcum,beta,A in fused mode and also
+// w,h,v_new in cached mode, ops/gated_delta_net.py:184); keeping h and v_new
+// avoids re-running the serial state scan in the backward.  No normalized copy
+// of q and k is kept: every reader scales its q and k rows by rq / rk on the way
+// into LDS, with the rounding fwd_prep applies (bf16 or fp16 of float(x) * r).
+// Buffers are addressed by event (time-first [T][H][D], the caller's TND
+// order) or by chunk ([NC][H][...], one 64-event block per chunk, rows past a
+// tail chunk's length are zero).  Value-slice-major
 // buffers ([8][rows][16]: slice s holds values 16 s .. 16 s + 15 of every row)
 // are written by the state scans, whose workgroups each own one 16-wide value
 // slice: a scan step stores one contiguous block, and a reader's MFMA fragment
@@ -19,10 +22,8 @@
 namespace cqgdn {
 
 enum FwdBuf {
-  F_QN = 0,  // bf16 [T][H][D]   l2-normalized q (unscaled)
-  F_KN,      // bf16 [T][H][D]   l2-normalized k
-  F_RQ,      // f32  [T][H]      rsqrt(sum q^2 + eps)
-  F_RK,      // f32  [T][H]      rsqrt(sum k^2 + eps)
+  F_RQ = 0,  // f32  [T][H]      rsqrt(sum q^2 + eps) (1 without the in-kernel l2norm)
+  F_RK,      // f32  [T][H]      rsqrt(sum k^2 + eps) (1 without the in-kernel l2norm)
   F_GC,      // f32  [T][H]      chunk-local cumsum of g
   F_TM,      // bf16 [NC][H][64][64]  T = (I + A)^-1, row-major (t, s)
   F_W,       // bf16 [T][H][D]   -W, W = T (beta*exp(G)*K), rows (t, k), perm32 column order
@@ -51,8 +52,6 @@ inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 inline void fwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   const size_t ev = (size_t)T * H, chunk = (size_t)NC * H;
-  s[F_QN] = ev * 128 * 2;
-  s[F_KN] = ev * 128 * 2;
   s[F_RQ] = ev * 4;
   s[F_RK] = ev * 4;
   s[F_GC] = ev * 4;

@@ -69,9 +69,10 @@ int64_t cqgdn_chunk_table(const int64_t* bounds, int n_bounds, int32_t* table, i
  * Forward workspace: size in bytes, and the byte offset of each of its
  * CQGDN_FWD_BUFFERS internal buffers (order documented in gdn_layout.hpp) so
  * that tests can inspect intermediates.  The same workspace must be passed,
- * unmodified, to cqgdn_bwd.
+ * unmodified, to cqgdn_bwd, with the same q and k (the workspace keeps their
+ * per-row l2 scales, not normalized copies).
  */
-#define CQGDN_FWD_BUFFERS 12
+#define CQGDN_FWD_BUFFERS 10
 #define CQGDN_BWD_BUFFERS 6
 size_t cqgdn_fwd_workspace_size(int64_t T, int H, int64_t n_chunks);
 int cqgdn_fwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets, int count);
@@ -106,7 +107,7 @@ int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const
  * uses the library's own static workspace of CQGDN_STATIC_WORKSPACE_BYTES per GPU
  * (a file-scope device array, held until the process ends) and calls no allocator.
  * It rejects with CQGDN_EINVAL any call whose cqgdn_fwd_workspace_size exceeds that
- * (at H = 16 and one document: up to 1,911 events), and CQGDN_TRAINING (the workspace does not
+ * (at H = 16 and one document: up to 2,496 events), and CQGDN_TRAINING (the workspace does not
  * outlive the call, so it cannot feed cqgdn_bwd).  Every call on one GPU shares
  * that GPU's workspace, which keeps the last call's contents: calls that overlap
  * on one GPU (two streams, or two threads) race and must be serialized by the
@@ -124,13 +125,16 @@ int cqgdn_fwd_static(const void* q, const void* k, const void* v, const float* g
  * backward op chain of _Delta.backward (ops/gated_delta_net.py:188-214:
  * chunk_bwd_dv_local, chunk_gated_delta_rule_bwd_dhu, chunk_bwd_dqkwg,
  * prepare_wy_repr_bwd_da, prepare_wy_repr_bwd_full, reverse_cumsum, l2_bwd).
- * Gradients are written in the input layouts: dq, dk, dv bf16 [T][H][D];
- * dg, dbeta fp32 [T][H].
+ * The reference keeps the normalized q, k and their rstd (ctx.save_for_backward,
+ * :184); this call takes the inputs q, k and forms the normalized rows from the
+ * rstd kept in the workspace, rounded as the forward rounded them.  Gradients are
+ * written in the input layouts: dq, dk, dv bf16 [T][H][D]; dg, dbeta fp32 [T][H].
  */
-int cqgdn_bwd(const void* v, const float* g, const float* beta, const void* dout, int64_t T, int H,
-              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
-              unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes, void* bwd_workspace,
-              size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta, void* stream);
+int cqgdn_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dout,
+              int64_t T, int H, const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs,
+              float scale, unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes,
+              void* bwd_workspace, size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta,
+              void* stream);
 
 /*
  * The backward of the reference's `fused` mode in one call: the forward workspace is

@@ -97,10 +97,12 @@ static void rejections() {
   CHECK(cqgdn_fwd_static(p, p, p, f, f, 1 << 20, 16, table, 1, doc, 1, 1.f, 0, nullptr, nullptr, p, nullptr) ==
         CQGDN_EINVAL);  // table inconsistent with T / larger than the static workspace
   // cqgdn_bwd
-  CHECK(cqgdn_bwd(p, f, f, p, 64, 16, table, 1, doc, 1, 1.f, CQGDN_NORMALIZE | CQGDN_TRAINING, p, 16, p, 1 << 20, p,
-                  p, p, f, f, nullptr) == CQGDN_EINVAL);  // forward workspace too small
-  CHECK(cqgdn_bwd(p, f, f, p, 64, 16, table, 1, doc, 1, 1.f, CQGDN_PRECISE, p, 1 << 30, p, 1 << 30, p, p, p, f, f,
-                  nullptr) == CQGDN_EINVAL);  // flag not accepted by the backward
+  CHECK(cqgdn_bwd(p, p, p, f, f, p, 64, 16, table, 1, doc, 1, 1.f, CQGDN_NORMALIZE | CQGDN_TRAINING, p, 16, p,
+                  1 << 20, p, p, p, f, f, nullptr) == CQGDN_EINVAL);  // forward workspace too small
+  CHECK(cqgdn_bwd(p, p, p, f, f, p, 64, 16, table, 1, doc, 1, 1.f, CQGDN_PRECISE, p, 1 << 30, p, 1 << 30, p, p, p,
+                  f, f, nullptr) == CQGDN_EINVAL);  // flag not accepted by the backward
+  CHECK(cqgdn_bwd(nullptr, p, p, f, f, p, 64, 16, table, 1, doc, 1, 1.f, CQGDN_NORMALIZE | CQGDN_TRAINING, p,
+                  1 << 30, p, 1 << 30, p, p, p, f, f, nullptr) == CQGDN_EINVAL);  // q is read by the backward
   // recurrent, l2norm, cumsum, conv, gated norm
   CHECK(cqgdn_recurrent(p, p, p, f, p, 0, f, p, -1, 1, 16, 1.f, nullptr) == CQGDN_EINVAL);
   CHECK(cqgdn_recurrent(nullptr, p, p, f, p, 0, f, p, 1, 1, 16, 1.f, nullptr) == CQGDN_EINVAL);

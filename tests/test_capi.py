@@ -100,6 +100,27 @@ def test_fwd_rejects_invalid_arguments_before_launch(lib):
     assert _fwd(lib, flags=8) == _lib.EINVAL
 
 
+def test_bwd_checks_its_inputs_before_launch(lib):
+    """The cached-mode backward reads q and k (the workspace keeps only their l2 scales), so
+    they are checked like the other inputs; every case returns before the first HIP call."""
+    p = ctypes.c_void_p(256)
+    T, H, nc = 64, 4, 1
+
+    def bwd(**kw):
+        args = dict(q=p, k=p, v=p, g=p, beta=p, dout=p, T=T, H=H, table=p, n_chunks=nc, doc=p, n_docs=1, scale=0.1,
+                    flags=_lib.NORMALIZE | _lib.TRAINING, fws=p, fws_bytes=lib.cqgdn_fwd_workspace_size(T, H, nc),
+                    bws=p, bws_bytes=lib.cqgdn_bwd_workspace_size(T, H, nc), dq=p, dk=p, dv=p, dg=p, db=p,
+                    stream=None)
+        args.update(kw)
+        return lib.cqgdn_bwd(*args.values())
+
+    assert bwd(q=None) == _lib.EINVAL and b"null" in lib.cqgdn_last_error()
+    assert bwd(k=None) == _lib.EINVAL
+    assert bwd(k=ctypes.c_void_p(258)) == _lib.EINVAL and b"aligned" in lib.cqgdn_last_error()
+    assert bwd(fws_bytes=100) == _lib.EINVAL and b"forward workspace" in lib.cqgdn_last_error()
+    assert bwd(T=0, n_chunks=0) == _lib.OK  # nothing to do
+
+
 def _bwd_recompute(lib, **kw):
     p = ctypes.c_void_p(256)
     T, H, nc = kw.pop("T", 64), 4, 1

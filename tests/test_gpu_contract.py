@@ -475,7 +475,7 @@ def test_bwd_recompute_graph_replay(gdn):
     dy = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(4243)).bfloat16().to(DEV)
 
     def run():
-        return gdn._backward(v, g, b, None, dy, bounds, True, 128 ** -0.5, recompute=(q, k))
+        return gdn._backward(q, k, v, g, b, None, dy, bounds, True, 128 ** -0.5)
 
     eager = [x.clone() for x in run()]
     torch.cuda.synchronize()

@@ -135,7 +135,7 @@ def test_backward_intermediates(gdn):
     dq, dk, dv = (torch.empty_like(v) for _ in range(3))
     dg, db = torch.empty_like(g), torch.empty_like(b)
     P = gdn._ptr
-    gdn.call("cqgdn_bwd", P(v), P(g), P(b), P(do_dev), T, H, P(table), nc, P(doc), len(bounds) - 1,
+    gdn.call("cqgdn_bwd", P(q), P(k), P(v), P(g), P(b), P(do_dev), T, H, P(table), nc, P(doc), len(bounds) - 1,
              128 ** -0.5, 3, P(ws), ws.numel(), P(bws), bws.numel(), P(dq), P(dk), P(dv), P(dg), P(db),
              gdn._stream(q.device))
     torch.cuda.synchronize()

@@ -60,7 +60,7 @@ def test_static_forward_rejects_what_it_cannot_serve(gdn):
     from cqgdn import _lib, synthetic
 
     lib = _lib.lib()
-    T, H = 2048, 16  # needs more than the 64 MiB static workspace
+    T, H = 4096, 16  # needs more than the 64 MiB static workspace
     q, k, v, g, b = (x.to(DEV) for x in synthetic.make_inputs(T, H, 128, seed=1))
     _, table, doc = gdn.device_metadata((0, T), DEV)
     o = torch.empty_like(v)
