@@ -75,11 +75,15 @@ def training_case(gdn, synthetic, torch, config, device):
     gen = torch.Generator().manual_seed(100 + config)
     do = torch.randn(1, T, H, D, generator=gen).bfloat16().to(device)
     leaves = [x.requires_grad_() for x in xs]
+    # packed documents (config 3) go in as cu_seqlens, one state reset per document
+    packed = {}
+    if len(bounds) > 2:
+        packed = dict(cu_seqlens=torch.tensor(bounds, dtype=torch.int64, device=device), cu_seqlens_cpu=list(bounds))
 
     def step():
         for x in leaves:
             x.grad = None
-        y, _ = gdn.delta(*leaves, use_qk_l2norm_in_kernel=True)
+        y, _ = gdn.delta(*leaves, use_qk_l2norm_in_kernel=True, **packed)
         y.backward(do)
 
     return T, bounds, step, xs
