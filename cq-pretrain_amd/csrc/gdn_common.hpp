@@ -89,6 +89,12 @@ __host__ __device__ __forceinline__ int perm32(int x) {
 // natural map, k-contiguous storage: 8 consecutive elements at p (16-byte aligned)
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ bf16x4 ld4(const bf16* p) { return *reinterpret_cast<const bf16x4*>(p); }
+// The same 16 bytes loaded with the non-temporal hint (global_load ... nt): for
+// input rows a kernel reads once, so that they do not displace, in the caches
+// down to the memory-side cache, the data the next kernel reads.
+__device__ __forceinline__ bf16x8 ld8_nt(const bf16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p));
+}
 // permuted map, k-contiguous storage: p points at element k0 + 4*q4
 __device__ __forceinline__ bf16x8 ld8p(const bf16* p) { return cat(ld4(p), ld4(p + 16)); }
 // natural map, strided storage: element s at p[s * stride]

@@ -64,6 +64,9 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
   // gathers' lane exchange runs where U is formed, and the stores of the row
   // phase go through buffer resources (rows past the chunk dropped by the range
   // check), so no store is conditional and the compiler can count what is in flight.
+  // q and k are loaded non-temporally: nothing reads them again before the state
+  // scan, whose operands (written here) then keep more of the memory-side cache.
+  // (V's column gathers share lines between lanes and stay ordinary loads.)
   const int t_r = tid >> 2, p_r = tid & 3;  // row phase: thread (t, p) owns columns 8p + 32j, j = 0..3
   const size_t row_r = ((size_t)(ci.start + clamp_row(t_r, ci.len)) * H + h) * D;
   float gv = 0.f, bv = 0.f;
@@ -76,8 +79,8 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
   Col8 vg[2][2];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    lq[j] = ld8(q + row_r + 32 * j + 8 * p_r);
-    lk[j] = ld8(k + row_r + 32 * j + 8 * p_r);
+    lq[j] = ld8_nt(q + row_r + 32 * j + 8 * p_r);
+    lk[j] = ld8_nt(k + row_r + 32 * j + 8 * p_r);
   }
   {
     const bf16* vb = v + ((size_t)ci.start * H + h) * D;
