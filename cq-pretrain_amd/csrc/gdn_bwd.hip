@@ -307,17 +307,21 @@ __device__ __forceinline__ void bwd_fix_tail(BwdStage& S, const int32_t* __restr
 constexpr int BWD_OUT_STORES = 6;
 
 // scratch of one step -> dS_{c+1} and dVn in value-slice-major blocks (the
-// slice's [k][16] and [t][16], read transposed from the [v][k] / [v][t] scratch)
+// slice's [k][16] and [t][16], read transposed from the [v][k] / [v][t] scratch).
+// Each store instruction writes 1 KB of contiguous lines, with the non-temporal
+// hint: the scan still has the earlier chunks' operands to read (bwd_local wrote
+// them first to last, so they are the oldest in the memory-side cache), and
+// bwd_dkw reads these outputs only after the scan.
 __device__ __forceinline__ void bwd_copy_out(const BwdScratch& sc, int c, int H, int h, int slice, int lane,
                                              bf16* __restrict__ dhS, bf16* __restrict__ dVnS) {
   const size_t cb = (size_t)c * H + h;
   const int r = lane & 15, q4 = lane >> 4, half = 8 * (q4 & 1), row = 16 * (q4 >> 1) + r;
   bf16* ds = dhS + cb * (D * D) + slice * (D * 16);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) st8(ds + (32 * i + row) * 16 + half, ld8_tr16(sc.s, BS_SROW, 32 * i));
+  for (int i = 0; i < 4; ++i) st8_nt(ds + (32 * i + row) * 16 + half, ld8_tr16(sc.s, BS_SROW, 32 * i));
   bf16* vs = dVnS + cb * (CH * D) + slice * (CH * 16);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) st8(vs + (32 * i + row) * 16 + half, ld8_tr16(sc.v, BS_VROW, 32 * i));
+  for (int i = 0; i < 2; ++i) st8_nt(vs + (32 * i + row) * 16 + half, ld8_tr16(sc.v, BS_VROW, 32 * i));
 }
 
 __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(

@@ -95,6 +95,11 @@ __device__ __forceinline__ bf16x4 ld4(const bf16* p) { return *reinterpret_cast<
 __device__ __forceinline__ bf16x8 ld8_nt(const bf16* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p));
 }
+// 16 bytes stored with the non-temporal hint: for whole rows written while the
+// caches hold data the same kernel has yet to read.
+__device__ __forceinline__ void st8_nt(bf16* p, bf16x8 x) {
+  __builtin_nontemporal_store(x, reinterpret_cast<bf16x8*>(p));
+}
 // permuted map, k-contiguous storage: p points at element k0 + 4*q4
 __device__ __forceinline__ bf16x8 ld8p(const bf16* p) { return cat(ld4(p), ld4(p + 16)); }
 // natural map, strided storage: element s at p[s * stride]
