@@ -70,12 +70,15 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
     const int tc = clamp_row(t, ci.len);
     const size_t ev = (size_t)(ci.start + tc) * H + h, row = ev * D;
     const float rqt = rq[ev], rkt = rk[ev];
+    // q and k non-temporally: what this kernel writes (the reverse scan's operands,
+    // 188 MB at T = 9216, H = 16) and what the scan writes do not both fit the
+    // 256 MB memory-side cache, and q, k are read next only by bwd_dkw, after the scan
     bf16x8 xq[4], xk[4], xd[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      xq[j] = ld8(q + row + col);
-      xk[j] = ld8(k + row + col);
+      xq[j] = ld8_nt(q + row + col);
+      xk[j] = ld8_nt(k + row + col);
       xd[j] = ld8(dout + row + col);
     }
     if (p == 0) {
