@@ -632,7 +632,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     for (int kb = 0; kb < 4; ++kb)
       bd[mm][kb] = ld8(dhc + (2 * kb + (q4 >> 1)) * (D * 16) + (16 * (2 * wave + mm) + r) * 16 + 8 * (q4 & 1));
 
-  // ---- phase 2: dQ (rows t, k-tiles 2w, 2w+1); dG_t from the output term ----
+  // ---- phase 2: dQ^T (k-tiles 2w, 2w+1 as rows, t columns); dG_t from the output term ----
+  // Each MFMA takes the operands of dQ = dO h^T + (dP Gam) K swapped, so a lane holds 4
+  // consecutive k of one row t: dQ[mm][n][i] = dq[t = 16 n + r][k = 16 (2w + mm) + 4 q4 + i].
+  // The row's gate and norm are then one value per lane, its sums over k run over the
+  // 4 lanes of a column (permlane swaps), and dq leaves as 8-byte pieces of rows.
   f32x4 dQ[2][4];
   {
     f32x4 a1[2][4];
@@ -646,7 +650,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       for (int n = 0; n < 4; ++n) {
         const bf16x8 a = ld8(dOs + (16 * n + r) * LDK + 32 * kb + 8 * q4);
 #pragma unroll
-        for (int mm = 0; mm < 2; ++mm) a1[mm][n] = mfma(a, bh[mm][kb], a1[mm][n]);
+        for (int mm = 0; mm < 2; ++mm) a1[mm][n] = mfma(bh[mm][kb], a, a1[mm][n]);
       }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -656,54 +660,46 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         const bf16x8 a = ld8_tr(dPm, LDT, 32 * kb, 16 * n);  // dPm rows t = 16 n + r
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm)
-          dQ[mm][n] = mfma(a, ld8_tr(Ks, LDK, 32 * kb, 16 * (2 * wave + mm)), dQ[mm][n]);
+          dQ[mm][n] = mfma(ld8_tr(Ks, LDK, 32 * kb, 16 * (2 * wave + mm)), a, dQ[mm][n]);
       }
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      const f32x4 g4 = *reinterpret_cast<const f32x4*>(&Gs[16 * n + 4 * q4]);
-      f32x4 qc[2];
+      const float f = scale * __expf(Gs[16 * n + r]);
+      f32x4 qr[2];  // q[t][k] at this lane's k
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) qc[mm] = cvtf4(ld4_c(Qs, LDK, 16 * n, 16 * (2 * wave + mm)));
-      float x[4];
+      for (int mm = 0; mm < 2; ++mm) qr[mm] = cvtf4(ld4(Qs + (16 * n + r) * LDK + 16 * (2 * wave + mm) + 4 * q4));
+      float x = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float f = scale * __expf(g4[i]);
-        x[i] = 0.f;
+      for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-        for (int mm = 0; mm < 2; ++mm) {
+        for (int i = 0; i < 4; ++i) {
           const float inter = a1[mm][n][i] * f;
           dQ[mm][n][i] += inter;
-          x[i] += qc[mm][i] * inter;
+          x += qr[mm][i] * inter;
         }
-      }
-      sum16x4(x);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (r == 0) dgl[16 * n + 4 * q4 + i] += x[i];
+      x = sum_rows4(x);
+      if (q4 == 0) dgl[16 * n + r] += x;
     }
   }
 
   // ---- l2norm backward of dq on the phase-2 registers: this wave's parts of the row dots q_t . dq_t ----
-  float pdot[4][4];
+  float pdot[4];
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
-    f32x4 qc[2];
+    f32x4 qr[2];
 #pragma unroll
-    for (int mm = 0; mm < 2; ++mm) qc[mm] = cvtf4(ld4_c(Qs, LDK, 16 * n, 16 * (2 * wave + mm)));
+    for (int mm = 0; mm < 2; ++mm) qr[mm] = cvtf4(ld4(Qs + (16 * n + r) * LDK + 16 * (2 * wave + mm) + 4 * q4));
+    float x = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      pdot[n][i] = 0.f;
+    for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) pdot[n][i] += qc[mm][i] * dQ[mm][n][i];
-    }
-    sum16x4(pdot[n]);
+      for (int i = 0; i < 4; ++i) x += qr[mm][i] * dQ[mm][n][i];
+    pdot[n] = sum_rows4(x);
   }
   lds_barrier();  // every read of the dO rows is done: the row dots and then the dVn tile may replace them
-  if (r == 0) {
+  if (q4 == 0) {
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dqdot[4 * (16 * n + 4 * q4 + i) + wave] = pdot[n][i];  // after the tile's 16 KB
+    for (int n = 0; n < 4; ++n) dqdot[4 * (16 * n + r) + wave] = pdot[n];  // after the tile's 16 KB
   }
   lds_barrier();
   // The dS fragments (bd) requested after phase 1 have landed long since: wait
@@ -711,27 +707,22 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   // phase 3 does not wait for the dq stores and the dVn copy issued below (the
   // stores are conditional, so the compiler could only wait for everything).
   wait_vmem_all();
-  // dq = rq (dQ - q (q . dQ)), stored from the C layout (16 lanes: 32 contiguous bytes of a row)
+  // dq = rq (dQ - q (q . dQ)): each lane stores 4 consecutive k of row t = 16 n + r
   const int rowb = H * D * 2;  // bytes per event row
   {
   const __amdgpu_buffer_rsrc_t dq_rs = chunk_rows_rsrc(dq, ci.start, ci.len, H, h);
-  const int dq_lane = 4 * q4 * rowb + (32 * wave + r) * 2;
 #pragma unroll
   for (int n = 0; n < 4; ++n) {
-    const f32x4 rs = *reinterpret_cast<const f32x4*>(&Rs[16 * n + 4 * q4]);
-    f32x4 qc[2];
+    const int t = 16 * n + r;
+    const float rs = Rs[t];
+    const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dqdot[4 * t]);
+    const float dot = d4[0] + d4[1] + d4[2] + d4[3];
 #pragma unroll
-    for (int mm = 0; mm < 2; ++mm) qc[mm] = cvtf4(ld4_c(Qs, LDK, 16 * n, 16 * (2 * wave + mm)));
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = 16 * n + 4 * q4 + i;
-      const f32x4 d4 = *reinterpret_cast<const f32x4*>(&dqdot[4 * t]);
-      const float dot = d4[0] + d4[1] + d4[2] + d4[3];
-#pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        const float x = normalize ? (dQ[mm][n][i] - qc[mm][i] * dot) * rs[i] : dQ[mm][n][i];
-        buf_st1(dq_rs, dq_lane + 32 * mm, (16 * n + i) * rowb, x);  // row t = 16 n + 4 q4 + i, column k
-      }
+    for (int mm = 0; mm < 2; ++mm) {
+      const int k0 = 16 * (2 * wave + mm) + 4 * q4;
+      const f32x4 qr = cvtf4(ld4(Qs + t * LDK + k0));
+      const f32x4 x = normalize ? (dQ[mm][n] - qr * dot) * rs : dQ[mm][n];
+      buf_st4(dq_rs, r * rowb + k0 * 2, 16 * n * rowb, x);  // row t, columns k0 .. k0 + 3
     }
   }
   }
