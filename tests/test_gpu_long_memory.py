@@ -1,0 +1,94 @@
+"""GPU parity with long-memory gates: the state carried across many chunks.
+
+The benchmark distribution g = -softplus(N(0,1)) decays the state by about e^-50 per
+64-event chunk, so what a chunk receives from the chunks before it is almost only the
+last few events' contribution (tests/test_oracle.py::test_long_memory_inputs_carry_state_across_chunks
+measures it).  A trained layer's gates can be close to zero
+(g = -exp(A_log) * softplus(a + dt_bias), models/backbone_qwen35.py:190), and then
+the carried term e^{G_C} S of every scan step dominates.  These cases scale g by 2e-3
+(about e^-0.1 per chunk) and compare the drop-in path with the float64 oracle:
+outputs and gradients (both backward modes) to the reference's bf16 gate, final
+states (prefill, with an initial state) to 1e-3.
+"""
+
+import pytest
+import torch
+
+from gdn_testlib import TOL_STATE, assert_close_bf16, rel_l2
+from oracle import gdn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+G_SCALE = 2e-3
+
+
+def long_memory_inputs(T, H, seed, readonly=None):
+    from cqgdn import synthetic
+
+    q, k, v, g, b = synthetic.make_inputs(T, H, 128, seed=seed, readonly=readonly)
+    return [q, k, v, g * G_SCALE, b]
+
+
+def fwd_bwd(gdn, xs, bounds, do):
+    xd = [x.to(DEV).requires_grad_() for x in xs]
+    cu = torch.tensor(bounds, device=DEV)
+    y, _ = gdn.delta(*xd, use_qk_l2norm_in_kernel=True, cu_seqlens=cu, cu_seqlens_cpu=torch.tensor(bounds))
+    y.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    return y.detach().cpu(), [x.grad.cpu() for x in xd]
+
+
+@pytest.mark.parametrize("mode", ["cached", "fused"])
+@pytest.mark.parametrize("T,bounds,H", [(700, (0, 300, 700), 8), (2304, (0, 2304), 16)])
+def test_long_memory_fwd_bwd_matches_oracle(gdn, monkeypatch, mode, T, bounds, H):
+    print(f"case long memory T={T} bounds={bounds} H={H} mode={mode}", flush=True)
+    monkeypatch.setattr(gdn, "MODE", mode)
+    xs = long_memory_inputs(T, H, seed=6100 + T)
+    do = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(6200 + T)).bfloat16()
+    y, grads = fwd_bwd(gdn, xs, bounds, do)
+    q, k, v, g, b = (x.double() for x in xs)
+    ref = O.chunk_delta(q, k, v, g, b, bounds)
+    ref_grads = O.chunk_delta_backward(q, k, v, g, b, do.double(), bounds)
+    assert_close_bf16("o", y, ref)
+    for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta"), grads, ref_grads):
+        assert_close_bf16(name, x, r)
+
+
+def test_long_memory_with_cq_queries_matches_oracle(gdn):
+    """Config 1's event layout (2048 content events, then a 256-event read-only query block) with
+    long-memory gates: the queries read the state the whole content built up."""
+    from cqgdn import synthetic
+
+    T, mask, bounds = synthetic.config_events(1, seed=0)
+    print(f"case long memory config-1 layout T={T}", flush=True)
+    xs = long_memory_inputs(T, 16, seed=6300, readonly=mask)
+    do = torch.randn(1, T, 16, 128, generator=torch.Generator().manual_seed(6301)).bfloat16()
+    y, grads = fwd_bwd(gdn, xs, bounds, do)
+    q, k, v, g, b = (x.double() for x in xs)
+    ref = O.chunk_delta(q, k, v, g, b, bounds)
+    ref_grads = O.chunk_delta_backward(q, k, v, g, b, do.double(), bounds)
+    assert_close_bf16("o", y, ref)
+    assert_close_bf16("o (query block)", y[:, mask], ref[:, mask])
+    for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta"), grads, ref_grads):
+        assert_close_bf16(name, x, r)
+
+
+def test_long_memory_prefill_final_states(gdn):
+    """prefill() with long-memory gates, with and without an initial state: the final states (which
+    now hold every document's whole history) within 1e-3 of the float64 oracle."""
+    T, H, bounds = 900, 16, (0, 1, 260, 900)
+    print(f"case long memory prefill T={T} bounds={bounds}", flush=True)
+    xs = long_memory_inputs(T, H, seed=6400)
+    q, k, v, g, b = (x.to(DEV) for x in xs)
+    qd, kd, vd, gd, bd = (x.double() for x in xs)
+    s0 = torch.randn(len(bounds) - 1, H, 128, 128, generator=torch.Generator().manual_seed(6401)) * 0.02
+    for init in (None, s0):
+        o, state = gdn.prefill(q, k, v, g, b, bounds, initial_state=None if init is None else init.to(DEV))
+        torch.cuda.synchronize()
+        ref, ref_state = O.chunk_delta(qd, kd, vd, gd, bd, bounds, output_final_state=True,
+                                       initial_state=None if init is None else init.double())
+        assert_close_bf16("o", o.cpu(), ref)
+        r = rel_l2(state, ref_state)
+        print(f"  initial state {'yes' if init is not None else 'no'}: final state rel_l2={r:.3e}", flush=True)
+        assert r <= TOL_STATE
