@@ -375,12 +375,13 @@ def prefill(q, k, v, g, beta, bounds, initial_state=None):
 
     Runs the precise forward (fp16 MFMA operands, CQGDN_PRECISE), whose final states
     stay within 1e-3 relative of an fp32 computation.
-    q, k, v: [1,T,H,128] bf16 (l2norm applied inside, scale 128^-0.5); g, beta [1,T,H].
-    Returns ``(o [1,T,H,128] time-first, state [n_docs,H,K,V] fp32)``.
+    q, k, v: [1,T,H,128] bf16 or fp16 (l2norm applied inside, scale 128^-0.5); g, beta [1,T,H].
+    fp16 values are rounded to bf16 once at the boundary, as in ``delta``.
+    Returns ``(o [1,T,H,128] time-first in the dtype of q, state [n_docs,H,K,V] fp32)``.
     """
     bounds = tuple(int(b) for b in bounds)
-    if q.dtype != torch.bfloat16 or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError("prefill needs bf16 q/k/v")
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("prefill needs bf16 or fp16 q/k/v")
     if q.shape[0] != 1 or bounds[0] != 0 or bounds[-1] != q.shape[1]:
         raise ValueError("prefill needs batch 1 and bounds covering every token")
     _require_gpu(q, k, v, g, beta)
@@ -389,16 +390,17 @@ def prefill(q, k, v, g, beta, bounds, initial_state=None):
         initial_state = initial_state.float().contiguous()
     o, state, _ = _forward(qf, kf, vf, gf, bf, bounds, True, q.shape[-1] ** -0.5, training=False,
                            initial_state=initial_state, want_state=True, precise=True)
-    return o, state
+    return _as(o, q.dtype), state
 
 
 @torch.no_grad()
 def recurrent(q, k, v, g, beta, state, out):
     """One recurrent decode pass over t events, state updated in place (ops/gated_delta_net.py:314-352).
 
-    q, k (l2-normalized), v, out: [t,H,128] bf16; g: [t,H] fp32; beta: [t,H] fp32 or
-    bf16; state: [1,H,V,K] fp32 value-first.  Batched decode passes q of shape
-    [N,t,H,128], g/beta [N,t,H] and state [N,H,V,K].
+    q, k (l2-normalized), v, out: [t,H,128], all bf16 or all fp16 (read and written as
+    such; the arithmetic is fp32 either way); g: [t,H] fp32; beta: [t,H] fp32 or bf16;
+    state: [1,H,V,K] fp32 value-first.  Batched decode passes q of shape [N,t,H,128],
+    g/beta [N,t,H] and state [N,H,V,K].
     """
     if q.dim() == 3:
         n, (t, h, d) = 1, q.shape
@@ -406,8 +408,10 @@ def recurrent(q, k, v, g, beta, state, out):
         n, t, h, d = q.shape
     if d != 128 or state.shape != (n, h, 128, 128) or state.dtype != torch.float32:
         raise ValueError("recurrent needs d=128 and a value-first fp32 state [N,H,128,128]")
-    if out.shape != q.shape or k.shape != q.shape or v.shape != q.shape or q.dtype != torch.bfloat16:
-        raise ValueError("q/k/v/out must share shape and be bf16")
+    if out.shape != q.shape or k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("q/k/v/out must share shape")
+    if q.dtype not in (torch.bfloat16, torch.float16) or any(x.dtype != q.dtype for x in (k, v, out)):
+        raise ValueError("q/k/v/out must share one dtype, bf16 or fp16")
     if beta.dtype not in (torch.float32, torch.bfloat16):
         raise ValueError("beta must be fp32 or bf16")
     for x in (q, k, v, g, beta, state, out):
@@ -415,7 +419,8 @@ def recurrent(q, k, v, g, beta, state, out):
             raise ValueError("recurrent operands must be contiguous (the state is updated in place)")
     _require_gpu(q, k, v, g, beta, state, out)
     g = g.float() if g.dtype != torch.float32 else g
-    call("cqgdn_recurrent", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), int(beta.dtype == torch.bfloat16),
+    dtype_flags = int(beta.dtype == torch.bfloat16) | (2 if q.dtype == torch.float16 else 0)
+    call("cqgdn_recurrent", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), dtype_flags,
          _ptr(state), _ptr(out), n, t, h, d ** -0.5, _stream(q.device))
     return out
 

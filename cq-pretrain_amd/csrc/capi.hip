@@ -362,16 +362,18 @@ int cqgdn_bwd_recompute(const void* q, const void* k, const void* v, const float
                   true, side->join);
 }
 
-int cqgdn_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta, int beta_is_bf16,
+int cqgdn_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta, int dtype_flags,
                     float* state, void* out, int N, int E, int H, float scale, void* stream) {
   if (N < 0 || E < 0 || H <= 0) return fail(CQGDN_EINVAL, "invalid sizes N=%d E=%d H=%d", N, E, H);
+  if (dtype_flags & ~(CQGDN_RECURRENT_BETA_BF16 | CQGDN_RECURRENT_FP16))
+    return fail(CQGDN_EINVAL, "unknown dtype flags 0x%x", dtype_flags);
   if (N == 0 || E == 0) return ok();
   if (!q || !k || !v || !g || !beta || !state || !out) return fail(CQGDN_EINVAL, "null tensor pointer");
   for (const void* p : {q, k, (const void*)state})
     if (!aligned(p, 16)) return fail(CQGDN_EINVAL, "q/k/state must be 16-byte aligned");
   if ((int64_t)N * H * 2 > 2147483647LL) return fail(CQGDN_EUNSUPPORTED, "too many sequences");
-  launch_recurrent(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v), g, beta,
-                   beta_is_bf16 != 0, state, static_cast<bf16*>(out), N, E, H, scale, (hipStream_t)stream);
+  launch_recurrent(q, k, v, g, beta, (dtype_flags & CQGDN_RECURRENT_BETA_BF16) != 0,
+                   (dtype_flags & CQGDN_RECURRENT_FP16) != 0, state, out, N, E, H, scale, (hipStream_t)stream);
   return check_launch("cqgdn_recurrent");
 }
 

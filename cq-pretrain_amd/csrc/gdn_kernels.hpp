@@ -53,8 +53,8 @@ struct BwdArgs {
 // launch errors are left for hipGetLastError.
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream);
-void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* g, const void* beta,
-                      bool beta_bf16, float* state, bf16* out, int N, int E, int H, float scale,
+void launch_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta,
+                      bool beta_bf16, bool fp16, float* state, void* out, int N, int E, int H, float scale,
                       hipStream_t stream);
 // packed depthwise causal conv1d (gdn_conv.hip); bounds: int32 [n_docs + 1] on the device
 int conv_strips(int64_t T);  // row strips of the conv backward (dw partials per strip)

@@ -17,12 +17,14 @@ namespace cqgdn {
 // 1 KB of contiguous state (two whole rows), and the row dot products are
 // reduced over the 32 lanes of a row.  The state is streamed with
 // non-temporal accesses: it is not reused before the next call.
+// X: the element type of q, k, v and out (bf16, or fp16 read and written as
+// such); every product and sum is in fp32 either way.
 // ---------------------------------------------------------------------------
-template <bool BETA_BF16>
-__global__ __launch_bounds__(256) void recurrent_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
-                                                        const bf16* __restrict__ v, const float* __restrict__ g,
+template <class X, bool BETA_BF16>
+__global__ __launch_bounds__(256) void recurrent_kernel(const X* __restrict__ q, const X* __restrict__ k,
+                                                        const X* __restrict__ v, const float* __restrict__ g,
                                                         const void* __restrict__ beta, float* __restrict__ state,
-                                                        bf16* __restrict__ out, int E, int H, float scale) {
+                                                        X* __restrict__ out, int E, int H, float scale) {
   const int blk = blockIdx.x;              // (n, h, half)
   const int half = blk & 1, nh = blk >> 1;  // nh = n * H + h
   const int n = nh / H, h = nh % H;
@@ -68,7 +70,7 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const bf16* __restrict__
     }
     if (c4 == 0) {
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) out[ev * D + rbase + 2 * jj] = (bf16)(o[jj] * scale);
+      for (int jj = 0; jj < 8; ++jj) out[ev * D + rbase + 2 * jj] = (X)(o[jj] * scale);
     }
   }
 #pragma unroll
@@ -76,16 +78,28 @@ __global__ __launch_bounds__(256) void recurrent_kernel(const bf16* __restrict__
     __builtin_nontemporal_store(s[jj], reinterpret_cast<f32x4*>(sblk + (rbase + 2 * jj) * D + 4 * c4));
 }
 
-void launch_recurrent(const bf16* q, const bf16* k, const bf16* v, const float* g, const void* beta,
-                      bool beta_bf16, float* state, bf16* out, int N, int E, int H, float scale,
+void launch_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta,
+                      bool beta_bf16, bool fp16, float* state, void* out, int N, int E, int H, float scale,
                       hipStream_t stream) {
   const dim3 grid(2 * N * H);
   TimedLaunch tl(K_RECURRENT, stream);
-  if (beta_bf16)
-    hipLaunchKernelGGL(recurrent_kernel<true>, grid, dim3(256), 0, stream, q, k, v, g, beta, state, out, E, H, scale);
+  auto run = [&](auto x) {
+    typedef decltype(x) X;
+    const X* qx = static_cast<const X*>(q);
+    const X* kx = static_cast<const X*>(k);
+    const X* vx = static_cast<const X*>(v);
+    X* ox = static_cast<X*>(out);
+    if (beta_bf16)
+      hipLaunchKernelGGL((recurrent_kernel<X, true>), grid, dim3(256), 0, stream, qx, kx, vx, g, beta, state, ox, E,
+                         H, scale);
+    else
+      hipLaunchKernelGGL((recurrent_kernel<X, false>), grid, dim3(256), 0, stream, qx, kx, vx, g, beta, state, ox, E,
+                         H, scale);
+  };
+  if (fp16)
+    run(f16{});
   else
-    hipLaunchKernelGGL(recurrent_kernel<false>, grid, dim3(256), 0, stream, q, k, v, g, beta, state, out, E, H,
-                       scale);
+    run(bf16{});
 }
 
 // ---------------------------------------------------------------------------

@@ -161,10 +161,14 @@ int cqgdn_bwd_recompute(const void* q, const void* k, const void* v, const float
  * decode path does with the FLA kernel fused_recurrent_gated_delta_rule_fwd_kernel
  * (ops/gated_delta_net.py:314-352; math of models/decoding.py:71-77):
  *   S <- exp(g) S ; S <- S + beta k (v - S k)^T ; o = scale S q
- * q, k (already l2-normalized), v, out: bf16 [N][E][H][D]; g: fp32 [N][E][H];
- * beta: [N][E][H], fp32 or bf16 (beta_is_bf16).  The reference call is N = 1.
+ * q, k (already l2-normalized), v, out: [N][E][H][D], bf16 (or fp16 with
+ * CQGDN_RECURRENT_FP16); g: fp32 [N][E][H]; beta: [N][E][H], fp32 (or bf16 with
+ * CQGDN_RECURRENT_BETA_BF16).  dtype_flags 0 and 1 keep their meaning of the
+ * former beta_is_bf16 argument.  The reference call is N = 1.
  */
-int cqgdn_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta, int beta_is_bf16,
+#define CQGDN_RECURRENT_BETA_BF16 1
+#define CQGDN_RECURRENT_FP16 2
+int cqgdn_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta, int dtype_flags,
                     float* state, void* out, int N, int E, int H, float scale, void* stream);
 
 /*

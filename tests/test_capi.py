@@ -150,6 +150,7 @@ def test_recurrent_and_helpers_reject_invalid_arguments(lib):
     assert lib.cqgdn_recurrent(p, p, p, p, p, 0, p, p, -1, 1, 4, 0.1, None) == _lib.EINVAL
     assert lib.cqgdn_recurrent(None, p, p, p, p, 0, p, p, 1, 1, 4, 0.1, None) == _lib.EINVAL
     assert lib.cqgdn_recurrent(p, p, p, p, p, 0, p, p, 0, 1, 4, 0.1, None) == _lib.OK  # nothing to do
+    assert lib.cqgdn_recurrent(p, p, p, p, p, 4, p, p, 1, 1, 4, 0.1, None) == _lib.EINVAL  # unknown dtype flag
     assert lib.cqgdn_l2norm_fwd(p, p, None, -1, None) == _lib.EINVAL
     assert lib.cqgdn_l2norm_bwd(None, p, p, p, 4, None) == _lib.EINVAL
     assert lib.cqgdn_chunk_local_cumsum(None, p, 4, 4, p, 1, 0, None) == _lib.EINVAL

@@ -226,7 +226,10 @@ def _restatement(plan, proj, H, gen, HK=None):
     S = H * 128
     model = layer.GatedDeltaLayer(width=64, heads=H, key_heads=HK).double()
     with torch.no_grad():
-        model.conv_weight.copy_(model.conv_weight.bfloat16().double())
+        # every parameter drawn from the test's generator (the module's own init uses the
+        # global RNG): the case is the same on every run
+        model.conv_weight.copy_((torch.rand(model.conv_weight.shape, generator=gen) - 0.5).bfloat16().double())
+        model.A_log.copy_(torch.rand(model.A_log.shape, generator=gen).mul(15.99).add(0.01).log())
         model.dt_bias.copy_(torch.randn(H, generator=gen) * 0.5)
         model.norm_weight.copy_(1 + 0.1 * torch.randn(128, generator=gen))
     dout = (torch.randn(plan.hidden_length, S, generator=gen) * 0.1).bfloat16()
@@ -508,6 +511,38 @@ def test_delta_fp16_inputs_match_oracle(gdn):
     y, grads = fwd_bwd(gdn, [q, k, v, g, b], bounds, do)
     assert y.dtype == torch.float16 and [x.dtype for x in grads] == [torch.float16] * 3 + [torch.float32] * 2
     check_against_oracle([q, k, v, g, b], bounds, do, y, grads)
+
+
+def test_prefill_and_recurrent_fp16_inputs_match_oracle(gdn):
+    """fp16 q/k/v through the inference entry points as through delta: prefill returns its output
+    in fp16 with fp32 states, and recurrent writes its fp16 output in place; both match the
+    float64 oracle of the same fp16 values (outputs to 2e-2, states to 1e-3)."""
+    T, bounds, H = 300, (0, 120, 300), 8
+    print(f"case fp16 prefill T={T} bounds={bounds} then 3 decode steps", flush=True)
+    q, k, v, g, b = inputs(T, H, seed=1717)
+    q, k, v = (x.float().half() for x in (q, k, v))
+    o, state = gdn.prefill(*(x.to(DEV) for x in (q, k, v, g, b)), bounds)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float16 and state.dtype == torch.float32
+    ref, ref_state = O.chunk_delta(*(x.double() for x in (q, k, v, g, b)), bounds, output_final_state=True)
+    assert_close_bf16("o", o.cpu(), ref)
+    assert rel_l2(state, ref_state) <= TOL_STATE
+    # decode both documents three steps from their prefill states (value-first)
+    gen = torch.Generator().manual_seed(1718)
+    st = state.transpose(-1, -2).contiguous()
+    ref_st = ref_state.transpose(-1, -2).contiguous()
+    for step in range(3):
+        qs = O.l2norm(torch.randn(2, 1, H, 128, generator=gen)).half()
+        ks = O.l2norm(torch.randn(2, 1, H, 128, generator=gen)).half()
+        vs = torch.randn(2, 1, H, 128, generator=gen).half()
+        gs = -torch.nn.functional.softplus(torch.randn(2, 1, H, generator=gen))
+        bs = torch.randn(2, 1, H, generator=gen).sigmoid()
+        out = torch.empty(2, 1, H, 128, dtype=torch.float16, device=DEV)
+        gdn.recurrent(*(x.to(DEV) for x in (qs, ks, vs, gs, bs)), st, out)
+        expected = O.decode_step(qs.double(), ks.double(), vs.double(), gs.double(), bs.double(), ref_st)
+        torch.cuda.synchronize()
+        assert_close_bf16(f"decode o step {step}", out.cpu(), expected)
+        assert rel_l2(st, ref_st) <= TOL_STATE
 
 
 # ---- fewer key heads than value heads (models/backbone_qwen35.py:182-183, models/decoding.py:52-53)

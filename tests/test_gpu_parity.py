@@ -571,7 +571,10 @@ def test_layer_core_matches_float64_restatement(gdn, docs):
     gen = torch.Generator().manual_seed(40 + docs)
     model = layer.GatedDeltaLayer(width=64, heads=H).double()
     with torch.no_grad():
-        model.conv_weight.copy_(model.conv_weight.bfloat16().double())
+        # every parameter drawn from the test's generator (the module's own init uses the
+        # global RNG): the case is the same on every run
+        model.conv_weight.copy_((torch.rand(model.conv_weight.shape, generator=gen) - 0.5).bfloat16().double())
+        model.A_log.copy_(torch.rand(model.A_log.shape, generator=gen).mul(15.99).add(0.01).log())
         model.dt_bias.copy_(torch.randn(H, generator=gen) * 0.5)
         model.norm_weight.copy_(1 + 0.1 * torch.randn(128, generator=gen))
     proj = (torch.randn(plan.hidden_length, 4 * S + 2 * H, generator=gen) * 0.7).bfloat16()
