@@ -92,3 +92,31 @@ def test_long_memory_prefill_final_states(gdn):
         r = rel_l2(state, ref_state)
         print(f"  initial state {'yes' if init is not None else 'no'}: final state rel_l2={r:.3e}", flush=True)
         assert r <= TOL_STATE
+
+
+def test_long_memory_decode_steps_match_oracle(gdn):
+    """``recurrent`` over 192 consecutive steps with long-memory gates (the state keeps hundreds of
+    steps of history), 8 sequences, H = 16: every output within the bf16 bar and the fp32 state within
+    1e-3 of the float64 oracle step (models/decoding.py:71-77) after the last step."""
+    N, H, steps = 8, 16, 192
+    print(f"case long memory decode N={N} H={H} steps={steps}", flush=True)
+    gen = torch.Generator().manual_seed(6500)
+    state0 = torch.randn(N, H, 128, 128, generator=gen) * 0.02
+    st = state0.to(DEV)
+    ref_state = state0.double()
+    worst = 0.0
+    for step in range(steps):
+        q = O.l2norm(torch.randn(N, 1, H, 128, generator=gen)).bfloat16()
+        k = O.l2norm(torch.randn(N, 1, H, 128, generator=gen)).bfloat16()
+        v = torch.randn(N, 1, H, 128, generator=gen).bfloat16()
+        b = torch.randn(N, 1, H, generator=gen).sigmoid()
+        g = -torch.nn.functional.softplus(torch.randn(N, 1, H, generator=gen)) * G_SCALE
+        out = torch.empty(N, 1, H, 128, dtype=torch.bfloat16, device=DEV)
+        gdn.recurrent(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), b.to(DEV), st, out)
+        ref = O.decode_step(q.double(), k.double(), v.double(), g.double(), b.double(), ref_state)
+        worst = max(worst, rel_l2(out, ref))
+    torch.cuda.synchronize()
+    rs = rel_l2(st, ref_state)
+    print(f"  worst output rel_l2={worst:.3e}, final state rel_l2={rs:.3e}", flush=True)
+    assert worst <= 2e-2
+    assert rs <= TOL_STATE
