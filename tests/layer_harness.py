@@ -1,37 +1,38 @@
-"""A whole GatedDelta layer around the hip recurrence, for the layer benchmark.
+"""Test and benchmark harness: a whole GatedDelta layer and DeltaPlans to drive it.
 
-The reference publishes GDN timings for the whole layer at width 2048
-(scripts/benchmark_gdn.py:34-56): fused input projection, causal conv over the
-content, the CQ query conv from the content history, the event gathers, the
-gates, the recurrence, the output gather, gated RMSNorm and out_proj.
-``GatedDeltaLayer`` follows that forward (models/backbone_qwen35.py:156-246,
-the training path without a state cache).  By default everything between the
-two projections runs in the fused kernels of ``events.layer_core``; with
-``fused=False`` it is the reference's torch code around this package's
-``delta``, ``conv`` and ``gated_norm``.
+Nothing in the drop-in path imports this module; the tests and ``bench.py`` do.
 
-``cq_layer_plan`` builds a synthetic single-document event plan with the
-structure of ops/gated_delta_layout.py:56-176 (content writes in sigma order,
-queries read before their group, every member of a multi-token image group
-read again after the group is written) and the event counts of the
-reference's image-CQ benchmark rows.
+* ``GatedDeltaLayer`` is the whole layer the reference's layer benchmark times at
+  width 2048 (scripts/benchmark_gdn.py:34-56): fused input projection, causal conv
+  over the content, the CQ query conv from the content history, the event gathers,
+  the gates, the recurrence, the output gather with the padding fill, gated RMSNorm
+  and out_proj (models/backbone_qwen35.py:156-246, the training path without a state
+  cache).  By default everything between the two projections runs in the fused
+  kernels of ``events.layer_core``; ``core(..., fused=False)`` is the reference's
+  layer code restated around hooks for the conv, the recurrence and the norm, which
+  the parity tests fill with the float64 oracle.
+* ``planner_plan`` builds the DeltaPlan the reference's planner
+  (ops/gated_delta_layout.py:54-176) builds for a described microbatch: documents,
+  padding positions, sigma groups, CQ queries (conditional or not) and the
+  masked-generation branch.  ``cq_layer_plan``, ``two_branch_plan`` and
+  ``concat_plans`` build synthetic plans of the same structure at benchmark sizes.
 """
 
 from __future__ import annotations
 
 import random
-from dataclasses import dataclass
+from dataclasses import dataclass, fields
 
 import torch
 import torch.nn.functional as F
 
-from . import events
-from . import gated_delta_net as gdn
+from cqgdn import events
+from cqgdn import gated_delta_net as gdn
 
 
 @dataclass
 class LayerPlan:
-    """The fields of the reference's DeltaPlan that the layer's forward reads."""
+    """The reference's DeltaPlan (ops/gated_delta_layout.py:12-27), field for field."""
 
     content_order: torch.Tensor  # hidden row of each content write, in write order
     event_q: torch.Tensor  # per event: row of cat(content q, query q)
@@ -43,10 +44,126 @@ class LayerPlan:
     event_cu: torch.Tensor
     event_bounds: tuple
     hidden_length: int
-    hidden_event: torch.Tensor  # per hidden row: the event whose output it takes
+    hidden_event: torch.Tensor  # per hidden row: the event whose output it takes (0 for padding rows)
+    output_event: torch.Tensor = None  # emitting events, in event order
+    output_hidden: torch.Tensor = None  # the hidden row each of them feeds
+    padding_hidden: torch.Tensor = None  # hidden rows no event feeds; their outputs are zero
+
+    def __post_init__(self):
+        if self.output_event is None:  # every hidden row emits (the synthetic plans)
+            order = torch.argsort(self.hidden_event)
+            self.output_event = self.hidden_event[order]
+            self.output_hidden = order
+            self.padding_hidden = torch.zeros(0, dtype=torch.long)
 
     def to(self, device):
-        return LayerPlan(**{k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in vars(self).items()})
+        return LayerPlan(**{f.name: (getattr(self, f.name).to(device) if isinstance(getattr(self, f.name), torch.Tensor)
+                                     else getattr(self, f.name)) for f in fields(self)})
+
+
+def planner_plan(sigma, segments, queries=(), unconditional=None, generation=(), prefix=0, generation_image=(),
+                 kernel=4) -> LayerPlan:
+    """The plan ops/gated_delta_layout.py:54-176 builds for one microbatch (B = 1), described by:
+
+    * ``sigma[i]``, ``segments[i]``: the write order key and the document of content position i
+      (segment < 0: a padding position; it is neither written nor read, and its hidden row is padding);
+    * ``queries``: the target position of each CQ query (hidden row ``keys + j``); ``unconditional[j]``
+      marks a query that reads before any write of its document, with an empty conv history
+      (``:86-95``, ``:114-118``).  A query whose target sits in padding is counted in document 0
+      (``:92-93``); one whose document or sigma group has no content is never read (its row is padding);
+    * ``generation``, ``prefix``, ``generation_image``: the masked-generation branch of a Bi_I+CQ_T step
+      (``:66-83``).  Its items are the generation positions in their own group order (consecutive
+      image items form one group); the first ``prefix`` items write hidden rows 0 .. prefix-1 again
+      without emitting, the rest are new rows ``len(sigma) ..``.
+
+    Events: per branch, per document in order of first appearance, per group in ascending key:
+    the group's queries (branch 0 only, each a read-only event), then each member's write, then,
+    for a multi-member group, one read-only re-read per member, which carries the member's output.
+    """
+    s = len(sigma)
+    suffix = len(generation) - prefix if len(generation) else 0
+    keys = s + suffix
+    unconditional = list(unconditional) if unconditional is not None else [False] * len(queries)
+    main = [(i, segments[i], sigma[i], True) for i in range(s) if segments[i] >= 0]
+    branches = [main]
+    if len(generation):
+        keys_of, key, prev_image = [], -1, False
+        for image in generation_image:
+            key += 0 if (image and prev_image) else 1
+            keys_of.append(key)
+            prev_image = image
+        branches.append([(i if i < prefix else s + i - prefix, segments[p], keys_of[i], i >= prefix)
+                         for i, p in enumerate(generation) if segments[p] >= 0])
+    if not branches[0]:
+        branches[0] = [(0, 0, 0, True)]  # an all-padding microbatch still has one written row
+    # queries by document, then by the group key they read before (None: before every group)
+    attached = {}
+    for j, p in enumerate(queries):
+        doc = max(segments[p], 0)
+        attached.setdefault(doc, {}).setdefault(None if unconditional[j] else sigma[p], []).append(keys + j)
+    order, reads, writes, emit_event, emit_hidden, q_rows, q_hist = [], [], [], [], [], [], []
+    c_bounds, e_bounds = [0], [0]
+
+    def add_event(read, write, out_row=None):
+        reads.append(read)
+        writes.append(write)
+        if out_row is not None:
+            emit_event.append(len(reads) - 1)
+            emit_hidden.append(out_row)
+
+    for b, items in enumerate(branches):
+        docs = {}
+        for item in items:
+            docs.setdefault(item[1], []).append(item)
+        for doc, members in docs.items():
+            groups = {}
+            for item in sorted(members, key=lambda it: (it[2], it[0])):
+                groups.setdefault(item[2], []).append(item)
+            pending = dict(attached.get(doc, {})) if b == 0 else {}
+            if None in pending:
+                first = next(iter(groups))
+                pending[first] = pending.pop(None) + pending.get(first, [])
+            written = []  # this document's content rows so far (the query conv's history)
+            for key, group in groups.items():
+                for row in pending.get(key, []):
+                    hist = written[-(kernel - 1):] if kernel > 1 else []
+                    q_hist.append([None] * (kernel - 1 - len(hist)) + hist)
+                    q_rows.append(row)
+                    add_event(("q", len(q_rows) - 1), None, row)
+                idx = []
+                for hidden_row, _, _, emits in group:
+                    ci = len(order)
+                    order.append(hidden_row)
+                    idx.append((ci, hidden_row, emits))
+                    written.append(ci)
+                    add_event(("c", ci), ci, hidden_row if (len(group) == 1 and emits) else None)
+                if len(group) > 1:
+                    for ci, hidden_row, emits in idx:
+                        add_event(("c", ci), None, hidden_row if emits else None)
+            c_bounds.append(len(order))
+            e_bounds.append(len(reads))
+    nc, n_h = len(order), keys + len(queries)
+    long = lambda xs: torch.tensor(xs, dtype=torch.long)
+    hidden_event = torch.zeros(n_h, dtype=torch.long)
+    hidden_event[long(emit_hidden)] = long(emit_event)
+    padding = torch.ones(n_h, dtype=torch.bool)
+    padding[long(emit_hidden)] = False
+    return LayerPlan(
+        content_order=long(order),
+        event_q=long([i if kind == "c" else nc + i for kind, i in reads]),
+        event_write=long([nc if w is None else w for w in writes]),
+        query_source=long(q_rows),
+        query_history=long([[nc if c is None else c for c in h] for h in q_hist]).reshape(len(q_rows), kernel - 1),
+        content_cu=torch.tensor(c_bounds, dtype=torch.int32),
+        content_bounds=tuple(c_bounds),
+        event_cu=long(e_bounds),
+        event_bounds=tuple(e_bounds),
+        hidden_length=n_h,
+        hidden_event=hidden_event,
+        output_event=long(emit_event),
+        output_hidden=long(emit_hidden),
+        padding_hidden=padding.nonzero().flatten(),
+    )
 
 
 def cq_layer_plan(content: int, queries: int, image_groups=(249, 249), kernel: int = 4, seed: int = 0) -> LayerPlan:
@@ -281,6 +398,8 @@ class GatedDeltaLayer(torch.nn.Module):
         else:
             y = recurrence(q, k, v, g, beta, plan)
         selected = y[0].index_select(0, plan.hidden_event).to(proj.dtype)
+        if plan.padding_hidden is not None and plan.padding_hidden.numel():
+            selected.index_fill_(0, plan.padding_hidden, 0)
         if norm is None:
             out = gdn.gated_norm(selected, z.reshape(-1, h, d), self.norm_weight, self.eps)
         else:

@@ -17,7 +17,7 @@
 import pytest
 import torch
 
-from gdn_testlib import TOL_BF16, TOL_STATE, assert_close_bf16, rel_l2
+from gdn_testlib import TOL_BF16, TOL_STATE, assert_close_bf16, compare_layer, layer_parity, rel_l2
 from oracle import gdn_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -159,7 +159,8 @@ def test_cq_invariant_layer_core(gdn):
     same way leaves every row whose output event precedes the group's first write bit-identical
     (the queries of earlier or equal sigma and the content before it); the group's first image
     output sees its last token."""
-    from cqgdn import events, layer
+    from cqgdn import events
+    import layer_harness as layer
 
     H, S = 16, 2048
     plan = layer.cq_layer_plan(600, 160, image_groups=(64, 40), seed=8).to(DEV)
@@ -218,76 +219,40 @@ def _image_group_rows(plan, size):
     return plan.content_order.cpu()[torch.tensor(rows)]
 
 
-def _restatement(plan, proj, H, gen, HK=None):
-    """Output and projection/parameter gradients of layer_core and of the reference's layer code in
-    float64 on the CPU (oracle conv, recurrence and norm), from the same bf16 projection."""
-    from cqgdn import events, layer
-
-    S = H * 128
-    model = layer.GatedDeltaLayer(width=64, heads=H, key_heads=HK).double()
-    with torch.no_grad():
-        # every parameter drawn from the test's generator (the module's own init uses the
-        # global RNG): the case is the same on every run
-        model.conv_weight.copy_((torch.rand(model.conv_weight.shape, generator=gen) - 0.5).bfloat16().double())
-        model.A_log.copy_(torch.rand(model.A_log.shape, generator=gen).mul(15.99).add(0.01).log())
-        model.dt_bias.copy_(torch.randn(H, generator=gen) * 0.5)
-        model.norm_weight.copy_(1 + 0.1 * torch.randn(128, generator=gen))
-    dout = (torch.randn(plan.hidden_length, S, generator=gen) * 0.1).bfloat16()
-    params = [model.conv_weight, model.A_log, model.dt_bias, model.norm_weight]
-    pd = proj.to(DEV).detach().requires_grad_()
-    dp = [model.conv_weight.detach().bfloat16().to(DEV).requires_grad_()] + \
-        [t.detach().float().to(DEV).requires_grad_() for t in params[1:]]
-    out = events.layer_core(pd, *dp, plan, heads=H, key_heads=HK)
-    out.backward(dout.to(DEV))
-    torch.cuda.synchronize()
-    p64 = proj.double().requires_grad_()
-    rec = lambda q, k, v, g, b, p: O.recurrent_delta(q, k, v, g, b, p.event_bounds, normalize=True)
-    cv = lambda u, w, bounds: O.causal_conv1d(u, w, bounds)
-    ref = model.core(p64, plan, recurrence=rec, conv=cv, norm=O.gated_rms_norm, fused=False)
-    ref.backward(dout.double())
-    return (out, pd.grad, dp), (ref, p64.grad, params)
-
-
-def _compare_layer(got, want, H, HK=None):
-    S, C = H * 128, (2 * (HK or H) + H) * 128
-    (out, dproj, dp), (ref, rproj, params) = got, want
-    assert_close_bf16("out", out.detach().cpu(), ref.detach())
-    cols = {"d_q": slice(0, (C - S) // 2), "d_k": slice((C - S) // 2, C - S), "d_v": slice(C - S, C),
-            "d_z": slice(C, C + S), "d_a": slice(C + S, C + S + H), "d_b": slice(C + S + H, C + S + 2 * H)}
-    for name, sl in cols.items():
-        assert_close_bf16(name, dproj[:, sl].cpu(), rproj[:, sl])
-    for name, a, p in zip(("d_conv_weight", "d_A_log", "d_dt_bias", "d_norm_weight"), dp, params):
-        assert_close_bf16(name, a.grad.cpu(), p.grad)
-
-
-def test_layer_core_shared_hidden_rows(gdn):
+@pytest.mark.parametrize("seed", range(4))
+def test_layer_core_shared_hidden_rows(gdn, seed):
     """A two-branch plan built like ops/gated_delta_layout.py:66-83 (Bi_I+CQ_T): the generation
     branch re-writes the prefix's hidden rows as its own content rows, so content_order repeats
     rows; the projection gradient of such a row is the sum over its content rows."""
-    from cqgdn import layer
+    import layer_harness as layer
 
     H = 16
     plan = layer.two_branch_plan(260, 70, prefix=40, suffix=50, image_groups=(30,), seed=9)
     order = plan.content_order
     assert torch.unique(order).numel() < order.numel()
-    print(f"case layer core, shared hidden rows: {plan.hidden_length} rows, {order.numel()} content", flush=True)
-    gen = torch.Generator().manual_seed(91)
+    print(f"case layer core, shared hidden rows: {plan.hidden_length} rows, {order.numel()} content, seed {seed}",
+          flush=True)
+    gen = torch.Generator().manual_seed(91 + 1000 * seed)
     proj = (torch.randn(plan.hidden_length, 4 * H * 128 + 2 * H, generator=gen) * 0.7).bfloat16()
-    _compare_layer(*_restatement(plan, proj, H, gen), H)
+    compare_layer(*layer_parity(plan, proj, H, gen), H)
 
 
-def test_layer_core_h32_and_column_sliced_projection(gdn):
+@pytest.mark.parametrize("seed", range(4))
+def test_layer_core_h32_and_column_sliced_projection(gdn, seed):
     """H = 32 through the fused layer, with the projection a column slice of a wider tensor (its row
     stride is larger than its width): results equal the contiguous projection's."""
-    from cqgdn import events, layer
+    from cqgdn import events
+    import layer_harness as layer
 
     H, S = 32, 4096
     P = 4 * S + 2 * H
     plan = layer.cq_layer_plan(160, 40, image_groups=(20,), seed=10)
-    print(f"case layer core H=32: {plan.hidden_length} rows", flush=True)
-    gen = torch.Generator().manual_seed(101)
+    print(f"case layer core H=32: {plan.hidden_length} rows, seed {seed}", flush=True)
+    gen = torch.Generator().manual_seed(101 + 1000 * seed)
     proj = (torch.randn(plan.hidden_length, P, generator=gen) * 0.7).bfloat16()
-    _compare_layer(*_restatement(plan, proj, H, gen), H)
+    compare_layer(*layer_parity(plan, proj, H, gen), H)
+    if seed:
+        return
     # the same projection inside a wider tensor (row stride P + 72), against the contiguous one
     params = _layer_params(H, gen)
     wide = torch.zeros(plan.hidden_length, P + 72, dtype=torch.bfloat16)
@@ -340,7 +305,7 @@ def test_whole_layer_at_benchmark_plan_matches_float64_recurrence(gdn):
     width 2048, content 2048 with 1675 CQ queries and two image groups -- the 4221-event image-CQ plan
     bench.py times -- against the same bf16 layer run by the reference's torch code whose recurrence is
     the float64 chunked oracle on the CPU: y, dx and the input-projection gradient within 2e-2."""
-    from cqgdn import layer
+    import layer_harness as layer
 
     print("case whole layer at the benchmark plan: content 2048, 1675 queries, 4221 events", flush=True)
     torch.manual_seed(872)
@@ -547,23 +512,24 @@ def test_prefill_and_recurrent_fp16_inputs_match_oracle(gdn):
 
 # ---- fewer key heads than value heads (models/backbone_qwen35.py:182-183, models/decoding.py:52-53)
 
+@pytest.mark.parametrize("seed", range(4))
 @pytest.mark.parametrize("H,HK,kind", [(32, 16, "image-CQ"), (16, 4, "two-branch")])
-def test_layer_core_fewer_key_heads(gdn, H, HK, kind):
+def test_layer_core_fewer_key_heads(gdn, H, HK, kind, seed):
     """layer_core with H value heads and HK < H key heads (the Qwen3.5-9B shape per rank is 32 and
     16) against the reference's layer code in float64, which repeat_interleaves q, k and the query
     conv output: the output, every projection-gradient column block (the q and k blocks sum their
     value heads' gradients) and the parameter gradients.  The two-branch plan repeats hidden rows."""
-    from cqgdn import layer
+    import layer_harness as layer
 
     if kind == "image-CQ":
         plan = layer.cq_layer_plan(200, 50, image_groups=(24,), seed=12)
     else:
         plan = layer.two_branch_plan(220, 60, prefix=30, suffix=40, image_groups=(20,), seed=13)
-    print(f"case layer core H={H} key heads={HK} ({kind}): {plan.hidden_length} rows", flush=True)
-    gen = torch.Generator().manual_seed(121 + H)
+    print(f"case layer core H={H} key heads={HK} ({kind}): {plan.hidden_length} rows, seed {seed}", flush=True)
+    gen = torch.Generator().manual_seed(121 + H + 1000 * seed)
     P = (2 * HK + 2 * H) * 128 + 2 * H
     proj = (torch.randn(plan.hidden_length, P, generator=gen) * 0.7).bfloat16()
-    _compare_layer(*_restatement(plan, proj, H, gen, HK), H, HK)
+    compare_layer(*layer_parity(plan, proj, H, gen, HK), H, HK)
 
 
 def _gqa_decode_params(H, HK, K, gen):

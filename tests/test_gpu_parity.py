@@ -10,7 +10,8 @@ read-only bit-exactness (tests/test_qwen35_cq.py:71-89) and document isolation
 import pytest
 import torch
 
-from gdn_testlib import TOL_BF16, TOL_INTER, TOL_STATE, assemble, assert_close_bf16, perm32, rel_l2, view
+from gdn_testlib import (TOL_BF16, TOL_INTER, TOL_STATE, assemble, assert_close_bf16, compare_layer, layer_parity, perm32,
+                         rel_l2, view)
 from oracle import gdn_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -399,7 +400,7 @@ def test_whole_layer_matches_oracle_recurrence(gdn):
     (events.layer_core) against the same bf16 layer run by the reference's torch code whose
     recurrence is the float64 CPU oracle: output, dx and the input-projection gradient (the
     quantities the reference's layer benchmark compares, scripts/benchmark_gdn.py:58-63)."""
-    from cqgdn import layer
+    import layer_harness as layer
 
     print("case whole layer: content 300, 120 queries, image groups (40, 24)", flush=True)
     torch.manual_seed(5)
@@ -552,52 +553,26 @@ def test_gated_norm_backward_deterministic(gdn):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("seed", range(4))
 @pytest.mark.parametrize("docs", [1, 2])
-def test_layer_core_matches_float64_restatement(gdn, docs):
+def test_layer_core_matches_float64_restatement(gdn, docs, seed):
     """events.layer_core (conv over gathered rows, query conv, event gathers and gates, the
     recurrence, output gather and gated norm, and their inverse-map backward) against the
     reference's layer code in float64 on the CPU with the oracle conv, recurrence and norm, from
     the same bf16 projection: output rows and the gradients of the projection (every column:
-    q|k|v, z, a, b), the conv weight, A_log, dt_bias and the norm weight."""
-    from cqgdn import events, layer
+    q|k|v, z, a, b), the conv weight, A_log, dt_bias (conditioned control error) and the norm weight."""
+    import layer_harness as layer
 
-    print(f"case layer core: {docs} document(s)", flush=True)
+    print(f"case layer core: {docs} document(s), seed {seed}", flush=True)
     if docs == 1:
         plan = layer.cq_layer_plan(300, 90, image_groups=(40, 24), seed=4)
     else:
         plan = layer.concat_plans(layer.cq_layer_plan(200, 50, image_groups=(30,), seed=5),
                                   layer.cq_layer_plan(150, 40, image_groups=(20, 10), seed=6))
     H, S = 16, 2048
-    gen = torch.Generator().manual_seed(40 + docs)
-    model = layer.GatedDeltaLayer(width=64, heads=H).double()
-    with torch.no_grad():
-        # every parameter drawn from the test's generator (the module's own init uses the
-        # global RNG): the case is the same on every run
-        model.conv_weight.copy_((torch.rand(model.conv_weight.shape, generator=gen) - 0.5).bfloat16().double())
-        model.A_log.copy_(torch.rand(model.A_log.shape, generator=gen).mul(15.99).add(0.01).log())
-        model.dt_bias.copy_(torch.randn(H, generator=gen) * 0.5)
-        model.norm_weight.copy_(1 + 0.1 * torch.randn(128, generator=gen))
+    gen = torch.Generator().manual_seed(40 + docs + 1000 * seed)
     proj = (torch.randn(plan.hidden_length, 4 * S + 2 * H, generator=gen) * 0.7).bfloat16()
-    dout = (torch.randn(plan.hidden_length, S, generator=gen) * 0.1).bfloat16()
-    params = [model.conv_weight, model.A_log, model.dt_bias, model.norm_weight]
-    pd = proj.to(DEV).requires_grad_()
-    dp = [model.conv_weight.detach().bfloat16().to(DEV).requires_grad_()] + \
-        [t.detach().float().to(DEV).requires_grad_() for t in params[1:]]
-    out = events.layer_core(pd, *dp, plan, heads=H)
-    out.backward(dout.to(DEV))
-    torch.cuda.synchronize()
-    p64 = proj.double().requires_grad_()
-    rec = lambda q, k, v, g, b, p: O.recurrent_delta(q, k, v, g, b, p.event_bounds, normalize=True)
-    cv = lambda u, w, bounds: O.causal_conv1d(u, w, bounds)
-    ref = model.core(p64, plan, recurrence=rec, conv=cv, norm=O.gated_rms_norm, fused=False)
-    ref.backward(dout.double())
-    assert_close_bf16("out", out.detach().cpu(), ref.detach())
-    cols = {"d_qkv": slice(0, 3 * S), "d_z": slice(3 * S, 4 * S), "d_a": slice(4 * S, 4 * S + H),
-            "d_b": slice(4 * S + H, 4 * S + 2 * H)}
-    for name, sl in cols.items():
-        assert_close_bf16(name, pd.grad[:, sl].cpu(), p64.grad[:, sl])
-    for name, a, p in zip(("d_conv_weight", "d_A_log", "d_dt_bias", "d_norm_weight"), dp, params):
-        assert_close_bf16(name, a.grad.cpu(), p.grad)
+    compare_layer(*layer_parity(plan, proj, H, gen), H)
 
 
 def _decode_params(gen, H, K=4):

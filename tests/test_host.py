@@ -147,7 +147,7 @@ def test_layer_plan_structure():
     """Synthetic image-CQ plan: counts of the reference's benchmark rows, each content row written
     once in order, read-only events write the zero row, the query conv sees earlier content only,
     every hidden row takes one event's output."""
-    from cqgdn import layer
+    import layer_harness as layer
 
     for content, queries, events in ((2048, 1675, 4221), (8192, 7819, 16509)):
         p = layer.cq_layer_plan(content, queries)
@@ -167,7 +167,7 @@ def test_layer_plan_structure():
 
 def test_layer_forward_backward_on_cpu_with_oracle_recurrence():
     """The whole-layer mirror runs fwd+bwd on the CPU with the oracle as its recurrence."""
-    from cqgdn import layer
+    import layer_harness as layer
 
     torch.manual_seed(0)
     model = layer.GatedDeltaLayer(width=64, heads=4).double()
@@ -185,7 +185,8 @@ def test_event_plan_inverse_maps_against_brute_force():
     """The host-built inverse maps of the fused layer kernels (q readers per content row, the
     writer of each content row, the reader of each query, the query-history entries per content
     row) against direct scans of the plan, on a packed two-document plan; bad plans raise."""
-    from cqgdn import events, layer
+    from cqgdn import events
+    import layer_harness as layer
 
     plan = layer.concat_plans(layer.cq_layer_plan(60, 17, image_groups=(9, 5), seed=1),
                               layer.cq_layer_plan(45, 11, image_groups=(7,), seed=2))
@@ -219,7 +220,8 @@ def test_event_plan_fold_map_of_shared_hidden_rows():
     0 .. prefix-1 in its second branch: the fold map lists every distinct hidden row of
     content_order with the content rows reading it (ascending), against a direct scan; plans
     without shared rows carry no fold map; a query row may not be a content row."""
-    from cqgdn import events, layer
+    from cqgdn import events
+    import layer_harness as layer
 
     plan = layer.two_branch_plan(50, 12, prefix=10, suffix=15, image_groups=(6,), suffix_groups=(4,), seed=3)
     ep = events.event_plan(plan, 4, "cpu")

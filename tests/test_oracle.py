@@ -352,7 +352,7 @@ def test_layer_decode_step_equals_the_training_layer_on_the_extended_plan(H, HK)
     after it: the C and Q outputs and the final state, with equal key and value heads and with
     two value heads per key head (the reference's repeat_interleave on both paths).  A planted
     history without the shift (Q's conv not seeing C) is caught."""
-    from cqgdn import layer
+    import layer_harness as layer
     from gdn_testlib import decode_plans
 
     torch.manual_seed(9)
