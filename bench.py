@@ -36,7 +36,7 @@ import time
 from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
-for _p in (ROOT, ROOT / "cq-pretrain_amd"):
+for _p in (ROOT, ROOT / "cq-pretrain_amd", ROOT / "tests"):
     if str(_p) not in sys.path:
         sys.path.insert(0, str(_p))
 
@@ -243,8 +243,9 @@ def decode_case(gdn, _lib, workmodel, torch, device, steps):
 def layer_setup(torch, device, content, queries):
     """Whole GatedDelta layer at width 2048 on an image-CQ plan with the event counts of the
     reference's benchmark rows (scripts/benchmark_gdn.py:34-56).  Returns the plan and
-    ``step(fused)``, one fwd+bwd step of the layer."""
-    from cqgdn import layer
+    ``step(fused)``, one fwd+bwd step of the layer (the layer and the plan come from the test
+    harness, tests/layer_harness.py)."""
+    import layer_harness as layer
 
     torch.manual_seed(872)
     model = layer.GatedDeltaLayer().to(device, torch.bfloat16)

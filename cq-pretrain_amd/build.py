@@ -1,10 +1,13 @@
-"""Build libcqgdn.so (gfx950 HIP kernels + the C ABI of include/cqgdn.h) in-tree.
+"""Build libcqgdn.so (gfx950 HIP kernels + the C ABI of include/cqgdn.h) and its PyTorch-ROCm
+operator library libcqgdn_torch.so (csrc/torch_ops.cpp, TORCH_LIBRARY(cqgdn)) in-tree.
 
 Usage: python cq-pretrain_amd/build.py [--jobs N]
 
 Every csrc/*.hip is compiled to an object under _build/ (git-ignored), then linked
 into cqgdn/libcqgdn.so next to the Python host package, so the library travels
-with the source tree.  hipcc cross-compiles for gfx950 without a GPU.
+with the source tree.  hipcc cross-compiles for gfx950 without a GPU.  The operator
+library is host C++ against the installed PyTorch-ROCm headers, compiled with the
+host compiler and linked to libcqgdn.so (found next to it at run time).
 """
 
 from __future__ import annotations
@@ -22,6 +25,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 OUT = PKG / "cqgdn" / "libcqgdn.so"
+OPS_OUT = PKG / "cqgdn" / "libcqgdn_torch.so"
 BUILD = PKG / "_build"
 
 ARCH = os.environ.get("CQGDN_ARCH", "gfx950")
@@ -68,14 +72,40 @@ def build(jobs: int | None = None, extra: list[str] | None = None, verbose: bool
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         objects = list(pool.map(lambda s: _compile(s, extra), sources))
     tmp = OUT.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-soname,libcqgdn.so", "-o", str(tmp),
+           *map(str, objects)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, OUT)
     if verbose:
         print(f"built {OUT.relative_to(ROOT)} from {len(sources)} sources for {ARCH}")
+    build_ops(verbose)
     return OUT
+
+
+def build_ops(verbose: bool = True) -> Path:
+    """csrc/torch_ops.cpp -> cqgdn/libcqgdn_torch.so, linked to libcqgdn.so (rpath $ORIGIN)."""
+    import torch
+    from torch.utils import cpp_extension
+
+    torch_dir = Path(torch.__file__).resolve().parent
+    includes = [torch_dir / "include", torch_dir / "include" / "torch" / "csrc" / "api" / "include",
+                Path("/opt/rocm/include"), INCLUDE]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = OPS_OUT.with_suffix(".so.tmp")
+    cmd = [os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-shared", "-fPIC", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", *(f"-I{p}" for p in includes),
+           str(CSRC / "torch_ops.cpp"), "-o", str(tmp),
+           *(f"-L{p}" for p in cpp_extension.library_paths()), "-lc10", "-lc10_hip", "-ltorch_cpu",
+           f"-L{OUT.parent}", "-lcqgdn", "-Wl,-rpath,$ORIGIN"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"torch_ops.cpp failed to build:\n{proc.stderr}")
+    os.replace(tmp, OPS_OUT)
+    if verbose:
+        print(f"built {OPS_OUT.relative_to(ROOT)} (TORCH_LIBRARY cqgdn)")
+    return OPS_OUT
 
 
 def main() -> None:

@@ -1,6 +1,12 @@
-"""ctypes binding of libcqgdn.so (the C ABI declared in include/cqgdn.h).
+"""Bindings of libcqgdn.so (the C ABI declared in include/cqgdn.h).
 
-The library is loaded from this package directory (built in-tree by
+* ``lib()``: the ctypes binding of every C-ABI symbol (workspace sizes, host helpers, the layer
+  kernels, instrumentation);
+* ``ops()``: ``torch.ops.cqgdn``, the PyTorch-ROCm operators of libcqgdn_torch.so
+  (csrc/torch_ops.cpp, TORCH_LIBRARY(cqgdn)) through which the per-step calls go: the training
+  forward and backward, the recurrent decode and the layer decode step.
+
+Both libraries are loaded from this package directory (built in-tree by
 ``cq-pretrain_amd/build.py``).  There is no fallback: a missing library, or a
 call that returns an error code, raises.
 """
@@ -12,6 +18,7 @@ import hashlib
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libcqgdn.so")
+OPS_PATH = LIB_PATH.with_name("libcqgdn_torch.so")
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 NORMALIZE, TRAINING, PRECISE, NO_OUTPUT = 1, 2, 4, 8
@@ -32,6 +39,7 @@ SIGNATURES = {
     "cqgdn_bwd_buffer_offsets": (_I, [_I64, _I, _I64, _P, _I]),
     "cqgdn_fwd": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _P, _P, _P, _SZ, _P]),
     "cqgdn_fwd_static": (_I, [_P, _P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _P, _P, _P]),
+    "cqgdn_fwd_static_init": (_I, []),
     "cqgdn_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _SZ, _P, _SZ, _P, _P, _P, _P,
                        _P, _P]),
     "cqgdn_bwd_recompute": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I, _P, _I64, _P, _I, _F, _U, _P, _SZ, _P, _SZ, _P,
@@ -71,6 +79,7 @@ class EventPlan(ctypes.Structure):
 KERNELS = ("fwd_prep", "fwd_scan", "fwd_out", "bwd_local", "bwd_scan", "bwd_dkw", "recurrent")
 
 _LIB = None
+_OPS = None
 
 
 class CqgdnError(RuntimeError):
@@ -91,6 +100,21 @@ def lib():
             fn.restype, fn.argtypes = res, args
         _LIB = handle
     return _LIB
+
+
+def ops():
+    """``torch.ops.cqgdn`` (fwd, bwd, recurrent, layer_decode_step), loaded once; raise if unbuilt."""
+    global _OPS
+    if _OPS is None:
+        lib()  # the operator library links libcqgdn.so: load it (and check it exists) first
+        if not OPS_PATH.exists():
+            raise RuntimeError(f"{OPS_PATH} is missing: build it with `python cq-pretrain_amd/build.py` "
+                               "(the hip GDN backend has no fallback)")
+        import torch
+
+        torch.ops.load_library(str(OPS_PATH))
+        _OPS = torch.ops.cqgdn
+    return _OPS
 
 
 def check(rc: int, what: str) -> None:

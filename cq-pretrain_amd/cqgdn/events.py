@@ -300,27 +300,10 @@ def layer_decode_step(proj, conv_weight, A_log, dt_bias, norm_weight, cache, *, 
     [2, P] for one sequence; heads and columns as in ``layer_core``); ``cache["conv"]`` bf16
     [N, K-1, C] and ``cache["state"]`` fp32 [N, H, V, K] are updated in place.  Returns the
     gated-norm rows [N, 2, SV] ([2, SV])."""
-    HK = heads if key_heads is None else int(key_heads)
-    _check_heads(heads, HK)
-    S = heads * 128
-    C, _, _, _, width = _columns(heads, HK)
+    # the contract checks (shapes, dtypes, contiguity, device) run inside the operator, before the launch
     single = proj.dim() == 2
-    p3 = proj[None] if single else proj
-    N, P = p3.shape[0], p3.shape[2]
-    K = conv_weight.shape[1]
-    if p3.shape[1] != 2 or P != width or p3.dtype != torch.bfloat16:
-        raise ValueError("proj must be bf16 [N, 2, (2*key_heads + 2*heads)*128 + 2*heads]")
-    hist, state = cache["conv"], cache["state"]
-    if hist.shape != (N, K - 1, C) or hist.dtype != torch.bfloat16 or not hist.is_contiguous():
-        raise ValueError("cache['conv'] must be contiguous bf16 [N, K-1, (2*key_heads + heads)*128]")
-    if state.shape != (N, heads, 128, 128) or state.dtype != torch.float32 or not state.is_contiguous():
-        raise ValueError("cache['state'] must be contiguous fp32 [N, H, 128, 128] (value-first)")
-    gdn._require_gpu(p3, conv_weight, hist, state)
-    p3 = p3.contiguous()
-    w = conv_weight.contiguous()
-    alog, dtb, nw = A_log.float().contiguous(), dt_bias.float().contiguous(), norm_weight.float().contiguous()
-    out = torch.empty(N, 2, S, dtype=p3.dtype, device=p3.device)
-    gdn.call("cqgdn_layer_decode_step", N, heads, HK, K, gdn._ptr(p3), P, gdn._ptr(hist), gdn._ptr(w), gdn._ptr(alog),
-             gdn._ptr(dtb), gdn._ptr(nw), float(eps), 128 ** -0.5 if scale is None else float(scale),
-             gdn._ptr(state), gdn._ptr(out), None, 0, gdn._stream(p3.device))
+    gdn.CALLS["cqgdn_layer_decode_step"] += 1
+    out = _lib.ops().layer_decode_step(proj[None] if single else proj, conv_weight, A_log, dt_bias, norm_weight,
+                                       cache["conv"], cache["state"], heads, heads if key_heads is None else key_heads,
+                                       eps, 128 ** -0.5 if scale is None else scale)
     return out[0] if single else out

@@ -258,15 +258,12 @@ def _forward(q, k, v, g, beta, bounds, normalize, scale, training, initial_state
     if initial_state is not None and initial_state.shape != (len(bounds) - 1, h, 128, 128):
         raise ValueError("initial_state must be [n_docs, H, 128, 128] fp32")
     cu, table, doc = device_metadata(bounds, str(q.device))
-    n_chunks, n_docs = table.shape[0], len(bounds) - 1
-    ws = torch.empty(_lib.lib().cqgdn_fwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=q.device)
-    o = torch.empty_like(v) if output else None
-    state = torch.empty(n_docs, h, 128, 128, dtype=torch.float32, device=q.device) if want_state else None
     flags = (_lib.NORMALIZE if normalize else 0) | (_lib.TRAINING if training else 0) | \
         (_lib.PRECISE if precise else 0) | (0 if output else _lib.NO_OUTPUT)
-    call("cqgdn_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), t, h, _ptr(table), n_chunks, _ptr(doc),
-         n_docs, float(scale), flags, _ptr(initial_state), _ptr(state), _ptr(o), _ptr(ws), ws.numel(),
-         _stream(q.device))
+    CALLS["cqgdn_fwd"] += 1
+    o, state, ws = _lib.ops().fwd(q, k, v, g, beta, table, doc, float(scale), flags, initial_state, want_state)
+    o = o if output else None
+    state = state if want_state else None
     return o, state, ws
 
 
@@ -301,25 +298,13 @@ class _Delta(torch.autograd.Function):
 def _backward(q, k, v, g, beta, ws, dy, bounds, normalize, scale):
     """dq, dk, dv, dg, dbeta of the packed chunked forward whose TRAINING workspace is ``ws``; with
     ``ws`` None the workspace is rebuilt inside the same call (fused mode)."""
-    t, h = v.shape[1], v.shape[2]
     cu, table, doc = device_metadata(bounds, str(v.device))
-    n_chunks, n_docs = table.shape[0], len(bounds) - 1
     if dy.shape != v.shape:
         dy = dy.reshape(v.shape)
     dy = _as(dy, v.dtype)
-    bws = torch.empty(_lib.lib().cqgdn_bwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=v.device)
-    dq, dk, dv = torch.empty_like(v), torch.empty_like(v), torch.empty_like(v)
-    dg, db = torch.empty_like(g), torch.empty_like(beta)
     flags = (_lib.NORMALIZE if normalize else 0) | _lib.TRAINING
-    if ws is not None:
-        call("cqgdn_bwd", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(dy), t, h, _ptr(table), n_chunks, _ptr(doc), n_docs,
-             float(scale), flags, _ptr(ws), ws.numel(), _ptr(bws), bws.numel(), _ptr(dq), _ptr(dk), _ptr(dv),
-             _ptr(dg), _ptr(db), _stream(v.device))
-    else:
-        ws = torch.empty(_lib.lib().cqgdn_fwd_workspace_size(t, h, n_chunks), dtype=torch.uint8, device=v.device)
-        call("cqgdn_bwd_recompute", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(dy), t, h, _ptr(table),
-             n_chunks, _ptr(doc), n_docs, float(scale), flags, _ptr(ws), ws.numel(), _ptr(bws), bws.numel(),
-             _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(db), _stream(v.device))
+    CALLS["cqgdn_bwd" if ws is not None else "cqgdn_bwd_recompute"] += 1
+    dq, dk, dv, dg, db = _lib.ops().bwd(q, k, v, g, beta, dy, table, doc, float(scale), flags, ws)
     return dq, dk, dv, dg, db
 
 
@@ -402,26 +387,9 @@ def recurrent(q, k, v, g, beta, state, out):
     state: [1,H,V,K] fp32 value-first.  Batched decode passes q of shape [N,t,H,128],
     g/beta [N,t,H] and state [N,H,V,K].
     """
-    if q.dim() == 3:
-        n, (t, h, d) = 1, q.shape
-    else:
-        n, t, h, d = q.shape
-    if d != 128 or state.shape != (n, h, 128, 128) or state.dtype != torch.float32:
-        raise ValueError("recurrent needs d=128 and a value-first fp32 state [N,H,128,128]")
-    if out.shape != q.shape or k.shape != q.shape or v.shape != q.shape:
-        raise ValueError("q/k/v/out must share shape")
-    if q.dtype not in (torch.bfloat16, torch.float16) or any(x.dtype != q.dtype for x in (k, v, out)):
-        raise ValueError("q/k/v/out must share one dtype, bf16 or fp16")
-    if beta.dtype not in (torch.float32, torch.bfloat16):
-        raise ValueError("beta must be fp32 or bf16")
-    for x in (q, k, v, g, beta, state, out):
-        if not x.is_contiguous():
-            raise ValueError("recurrent operands must be contiguous (the state is updated in place)")
-    _require_gpu(q, k, v, g, beta, state, out)
-    g = g.float() if g.dtype != torch.float32 else g
-    dtype_flags = int(beta.dtype == torch.bfloat16) | (2 if q.dtype == torch.float16 else 0)
-    call("cqgdn_recurrent", _ptr(q), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), dtype_flags,
-         _ptr(state), _ptr(out), n, t, h, d ** -0.5, _stream(q.device))
+    # the contract checks (ValueError texts of the reference's adapter) run inside the operator
+    CALLS["cqgdn_recurrent"] += 1
+    _lib.ops().recurrent(q, k, v, g, beta, state, out, 128 ** -0.5)
     return out
 
 

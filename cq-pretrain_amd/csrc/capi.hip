@@ -159,6 +159,11 @@ int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const
                   final_state, o, workspace, workspace_bytes, stream);
 }
 
+int cqgdn_fwd_static_init(void) {
+  void* ws = nullptr;
+  return static_workspace(&ws);
+}
+
 int cqgdn_fwd_static(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T,
                      int H, const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs,
                      float scale, unsigned flags, const float* initial_state, float* final_state, void* o,

@@ -112,12 +112,23 @@ int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const
  * that GPU's workspace, which keeps the last call's contents: calls that overlap
  * on one GPU (two streams, or two threads) race and must be serialized by the
  * caller.  Nothing in the workspace needs to start at zero.
+ *
+ * The array is reserved when the runtime loads the code object that holds it, which
+ * happens at its first address lookup on a device: call cqgdn_fwd_static_init() once
+ * per device at set-up (with that device current) so that no cqgdn_fwd_static call
+ * reserves memory; without it, the first cqgdn_fwd_static call on a device does the
+ * lookup.  Processes that never call either reserve nothing.
  */
 #define CQGDN_STATIC_WORKSPACE_BYTES (64u << 20)
 int cqgdn_fwd_static(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T,
                      int H, const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs,
                      float scale, unsigned flags, const float* initial_state, float* final_state, void* o,
                      void* stream);
+
+/* Set-up of cqgdn_fwd_static on the current device (no counterpart in the reference; for the
+ * same callers): looks up the device's static workspace once, reserving its
+ * CQGDN_STATIC_WORKSPACE_BYTES, and keeps its address for later calls.  Idempotent. */
+int cqgdn_fwd_static_init(void);
 
 /*
  * Chunked GDN backward from the forward workspace (which must come from a

@@ -198,3 +198,21 @@ def test_training_forward_rejects_states(lib):
     rc = lib.cqgdn_fwd(dummy, dummy, dummy, dummy, dummy, 64, 4, dummy, 1, dummy, 1, 0.088, _lib.TRAINING, dummy, None,
                        dummy, dummy, 1 << 30, None)
     assert rc == _lib.EINVAL and b"zero state" in lib.cqgdn_last_error()
+
+
+def test_torch_operators_are_registered():
+    """libcqgdn_torch.so registers TORCH_LIBRARY(cqgdn) with the four per-step operators, whose schemas
+    mark the decode state, the conv history and the decode output as written in place."""
+    import torch
+
+    ops = _lib.ops()
+    schemas = {name: str(getattr(ops, name).default._schema)
+               for name in ("fwd", "bwd", "recurrent", "layer_decode_step")}
+    assert "Tensor? initial_state" in schemas["fwd"] and schemas["fwd"].endswith("-> (Tensor, Tensor, Tensor)")
+    assert "Tensor? ws" in schemas["bwd"]
+    assert "Tensor(a!) state, Tensor(b!) out" in schemas["recurrent"]
+    assert "Tensor(a!) history, Tensor(b!) state" in schemas["layer_decode_step"]
+    # CPU tensors are rejected with the reference's ValueError before anything runs
+    q = torch.zeros(1, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="ROCm GPU"):
+        ops.recurrent(q, q, q, torch.zeros(1, 4), torch.zeros(1, 4), torch.zeros(1, 4, 128, 128), q.clone(), 0.1)

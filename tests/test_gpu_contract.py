@@ -301,10 +301,17 @@ def test_layer_decode_step_h32(gdn):
 
 
 def test_whole_layer_at_benchmark_plan_matches_float64_recurrence(gdn):
-    """The fused layer at the first row of the reference's layer benchmark (scripts/benchmark_gdn.py:34-64):
+    """The layer at the first row of the reference's layer benchmark (scripts/benchmark_gdn.py:34-64):
     width 2048, content 2048 with 1675 CQ queries and two image groups -- the 4221-event image-CQ plan
-    bench.py times -- against the same bf16 layer run by the reference's torch code whose recurrence is
-    the float64 chunked oracle on the CPU: y, dx and the input-projection gradient within 2e-2."""
+    bench.py times -- in bf16 on the GPU, three ways:
+
+    * ``oracle``: the reference's torch code around the float64 chunked oracle recurrence (on the CPU);
+    * ``hip``: the same torch code around this backend's ``delta`` (the reference's provider-against-
+      provider comparison, one glue, two recurrences);
+    * ``fused``: everything between the projections in the fused kernels (``events.layer_core``).
+
+    y, dx and the input-projection gradient dw of ``hip`` and ``fused`` against ``oracle`` within 2e-2,
+    with the reference benchmark's relative RMS (rms(a - b) / rms(b), b the oracle path) printed for each."""
     import layer_harness as layer
 
     print("case whole layer at the benchmark plan: content 2048, 1675 queries, 4221 events", flush=True)
@@ -318,10 +325,10 @@ def test_whole_layer_at_benchmark_plan_matches_float64_recurrence(gdn):
     x = torch.randn(plan.hidden_length, 1, 2048, generator=gen).bfloat16().to(DEV)
     up = (torch.randn(plan.hidden_length, 1, 2048, generator=gen) / 100).bfloat16().to(DEV)
 
-    def run(recurrence):
+    def run(recurrence, fused):
         model.zero_grad(set_to_none=True)
         xx = x.clone().requires_grad_()
-        y = model(xx, plan, recurrence=recurrence)
+        y = model(xx, plan, recurrence=recurrence, fused=fused)
         (y * up).sum().backward()
         torch.cuda.synchronize()
         return y.detach().float().cpu(), xx.grad.float().cpu(), model.in_proj_all.weight.grad.float().cpu()
@@ -342,9 +349,13 @@ def test_whole_layer_at_benchmark_plan_matches_float64_recurrence(gdn):
 
         return Bridge.apply(q, k, v, g, b)
 
-    got, want = run(None), run(oracle)
-    for name, a, b in zip(("y", "dx", "dW_in"), got, want):
-        assert_close_bf16(name, a, b.double())
+    want = run(oracle, False)
+    for label, got in (("hip", run(None, False)), ("fused", run(None, True))):
+        rms = {n: float((b.double() - a.double()).square().mean().sqrt() / b.double().square().mean().sqrt())
+               for n, a, b in zip(("y", "dx", "dw"), got, want)}
+        print(f"  {label} vs oracle, relative RMS: y={rms['y']:.2e} dx={rms['dx']:.2e} dw={rms['dw']:.2e}", flush=True)
+        for name, a, b in zip(("y", "dx", "dW_in"), got, want):
+            assert_close_bf16(f"{label} {name}", a, b.double())
 
 
 def test_decode_steps_replay_in_a_hip_graph(gdn):
