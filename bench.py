@@ -56,6 +56,8 @@ def parse_args():
     ap.add_argument("--profile", action="store_true",
                     help="profiler workload only: config-2 fwd+bwd steps, then a plain copy kernel of "
                          "known size (the scale of the HBM byte counters); prints no JSON")
+    ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3),
+                    help="with --profile: the benchmark configuration whose fwd+bwd steps are profiled")
     ap.add_argument("--profile-layer", action="store_true",
                     help="profiler workload only: warmup + steps fused fwd+bwd steps of the width-2048 "
                          "layer at content 2048; prints no JSON")
@@ -205,17 +207,22 @@ def decode_case(gdn, _lib, workmodel, torch, device, steps):
     out = torch.empty_like(q)
     for st in states:
         gdn.recurrent(q, k, v, g, b, st, out)
+    # one Python call per step, as a decode loop makes them
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        gdn.recurrent(q, k, v, g, b, states[i % layers], out)
+    torch.cuda.synchronize()
+    sec = (time.perf_counter() - t0) / steps
+    # the kernel's own duration, by events around each launch (a separate pass: the events
+    # cost host time of their own)
     with _lib.KernelTimer("recurrent", steps) as t:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
         for i in range(steps):
             gdn.recurrent(q, k, v, g, b, states[i % layers], out)
-        torch.cuda.synchronize()
-        sec = (time.perf_counter() - t0) / steps
     nbytes = workmodel.decode_bytes(n, H)
     kern = statistics.mean(t.ms) * 1e-3
     # the same loop captured once in a HIP graph and replayed: what a serving loop pays per step
-    # without a Python call and a ctypes round trip per launch (the step records no memset)
+    # without a Python call per launch (the step records no memset)
     graph = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -362,7 +369,7 @@ COPY_BYTES = 256 << 20
 
 
 def profile_workload(torch, step, steps):
-    """Workload run under rocprofv3: ``steps`` config-2 fwd+bwd steps, then 3 copies of COPY_BYTES."""
+    """Workload run under rocprofv3: ``steps`` fwd+bwd steps, then 3 copies of COPY_BYTES."""
     for i in range(steps):
         step()
         torch.cuda.synchronize()
@@ -408,14 +415,19 @@ def main():
             log(f"layer step {i} done")
         return
 
+    if args.profile:
+        log(f"config {args.config} fwd+bwd (profile)")
+        _, _, step, _ = training_case(gdn, synthetic, torch, args.config, device)
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        profile_workload(torch, step, args.steps)
+        return
     log("config 2 fwd+bwd")
     T, bounds, step, _ = training_case(gdn, synthetic, torch, 2, device)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    if args.profile:
-        profile_workload(torch, step, args.steps)
-        return
     kernels = {} if args.no_extra else kernel_table(torch, _lib, workmodel, step, bounds)
     dominant = max(kernels, key=lambda k: kernels[k]["us"]) if kernels else "bwd_dkw"
 

@@ -478,15 +478,25 @@ def test_bwd_recompute_graph_replay(gdn):
 
 def test_delta_fp16_inputs_match_oracle(gdn):
     """fp16 q/k/v, which the reference's delta accepts (ops/gated_delta_net.py:233-234): output and
-    gradients come back in the input dtypes and match the float64 oracle of the same fp16 values."""
+    gradients come back in the input dtypes and match the float64 oracle of the same fp16 values.
+    The values are drawn in fp32 and rounded to fp16, so most of them are not bf16 values: the
+    backend's one rounding of fp16 inputs to bf16 operands is part of the measured error."""
     T, bounds, H = 257, (0, 100, 257), 8
     print(f"case fp16 inputs T={T} bounds={bounds}", flush=True)
-    q, k, v, g, b = inputs(T, H, seed=1616)
-    q, k, v = (x.float().half() for x in (q, k, v))
+    gen = torch.Generator().manual_seed(1616)
+    _, _, _, g, b = inputs(T, H, seed=1616)
+    q, k, v = (torch.randn(1, T, H, 128, generator=gen).half() for _ in range(3))
+    assert not torch.equal(q.bfloat16().half(), q)  # genuinely fp16 values
     do = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(17)).half()
     y, grads = fwd_bwd(gdn, [q, k, v, g, b], bounds, do)
     assert y.dtype == torch.float16 and [x.dtype for x in grads] == [torch.float16] * 3 + [torch.float32] * 2
-    check_against_oracle([q, k, v, g, b], bounds, do, y, grads)
+    # measured on MI355X: rel_l2 4.6e-3 .. 5.0e-3 and max_rel up to 7.5e-3 for o and all five gradients,
+    # the level of bf16 inputs; the gate is 1e-2, half the bf16 bar
+    xs = [x.double() for x in (q, k, v, g, b)]
+    assert_close_bf16("o", y, O.chunk_delta(*xs, bounds), tol=1e-2)
+    ref = O.chunk_delta_backward(*xs, do.double(), bounds)
+    for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta"), grads, ref):
+        assert_close_bf16(name, x, r, tol=1e-2)
 
 
 def test_prefill_and_recurrent_fp16_inputs_match_oracle(gdn):
