@@ -10,8 +10,9 @@ and state; timing follows the reference's GDN benchmark (warm-up, then
 synchronize around the timed loop, scripts/benchmark_gdn.py:51-56).
 
 Printed: one JSON line with the contract keys, plus
-  roofline      the dominant kernel priced against bf16 MFMA (HIP events on the
-                stream it runs on, recorded inside the timed region), with its HBM rate beside
+  roofline      the dominant kernel against the roofline that bounds it (HBM below the
+                312 FLOP/byte ridge, bf16 MFMA above; HIP events on the stream it runs on,
+                recorded inside the timed region), with the other resource's figures beside
   cpu_baseline  the fp32 chunked torch oracle on this host's cores (a bounded
                 sample: one config-2 fwd+bwd; rows: one config-0 forward and the
                 config-4 decode step)
@@ -442,13 +443,25 @@ def main():
     ms = elapsed / args.steps * 1e3
     launch_s = statistics.mean(timer.ms) * 1e-3
     flops, nbytes = workmodel.kernel_work(dominant, bounds, H)
-    # the chunk kernels are dense contractions priced against bf16 MFMA; the HBM figures beside
-    roof = dict(kernel=dominant, bound="mfma", achieved=round(flops / launch_s / 1e12, 2),
-                peak=workmodel.PEAK_BF16_FLOPS / 1e12, unit="TFLOP/s",
-                frac=round(flops / launch_s / workmodel.PEAK_BF16_FLOPS, 4), traffic=traffic_for(dominant, sha),
-                algorithmic_flops=int(flops), algorithmic_bytes=nbytes,
-                hbm_achieved_gbps=round(nbytes / launch_s / 1e9, 1),
-                hbm_frac=round(nbytes / launch_s / workmodel.PEAK_HBM_BYTES, 4),
+    # The bound is the resource the roofline model says limits the kernel: its algorithmic FLOPs
+    # over its algorithmic bytes (about 75 FLOP/byte for bwd_dkw) against MI355X's ridge, 2.5 PFLOP/s
+    # bf16 over 8 TB/s = 312 FLOP/byte.  Below the ridge the attainable rate is bytes-bound, so
+    # `achieved` is algorithmic GB/s against 8 TB/s; the bf16 MFMA figures (the north_star's
+    # utilization metric) stay beside it.
+    intensity = flops / nbytes
+    ridge = workmodel.PEAK_BF16_FLOPS / workmodel.PEAK_HBM_BYTES
+    mfma = dict(mfma_achieved_tflops=round(flops / launch_s / 1e12, 2),
+                mfma_frac=round(flops / launch_s / workmodel.PEAK_BF16_FLOPS, 4))
+    hbm = dict(hbm_achieved_gbps=round(nbytes / launch_s / 1e9, 1),
+               hbm_frac=round(nbytes / launch_s / workmodel.PEAK_HBM_BYTES, 4))
+    if intensity < ridge:
+        roof = dict(kernel=dominant, bound="hbm", achieved=hbm["hbm_achieved_gbps"],
+                    peak=workmodel.PEAK_HBM_BYTES / 1e9, unit="GB/s", frac=hbm["hbm_frac"])
+    else:
+        roof = dict(kernel=dominant, bound="mfma", achieved=mfma["mfma_achieved_tflops"],
+                    peak=workmodel.PEAK_BF16_FLOPS / 1e12, unit="TFLOP/s", frac=mfma["mfma_frac"])
+    roof.update(traffic=traffic_for(dominant, sha), algorithmic_flops=int(flops), algorithmic_bytes=nbytes,
+                flop_per_byte=round(intensity, 1), ridge_flop_per_byte=round(ridge, 1), **mfma, **hbm,
                 launch_us=round(launch_s * 1e6, 2), launches=len(timer.ms))
     total_flops = sum(workmodel.kernel_work(k, bounds, H)[0]
                       for k in workmodel.FWD_KERNELS + workmodel.BWD_KERNELS)
