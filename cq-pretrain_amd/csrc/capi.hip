@@ -3,6 +3,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -255,7 +256,8 @@ int bwd_impl(const void* q, const void* k, const void* v, const float* g, const 
              const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs, float scale,
              unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes, void* bwd_workspace,
              size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta, void* stream,
-             bool launch, hipEvent_t dkw_after) {
+             bool launch, hipEvent_t dkw_after, hipStream_t side = nullptr, hipEvent_t side_fork = nullptr,
+             hipEvent_t side_join = nullptr) {
   if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
   if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING)) return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
   if (T == 0) return ok();
@@ -295,6 +297,9 @@ int bwd_impl(const void* q, const void* k, const void* v, const float* g, const 
   a.dg = dg;
   a.dbeta = dbeta;
   a.dkw_after = dkw_after;
+  a.side = side;
+  a.side_fork = side_fork;
+  a.side_join = side_join;
   if (const hipError_t e = launch_bwd(a, (hipStream_t)stream))
     return fail(CQGDN_EHIP, "cqgdn_bwd: waiting for the forward scan's stream: %s", hipGetErrorString(e));
   return check_launch("cqgdn_bwd");
@@ -307,6 +312,7 @@ int bwd_impl(const void* q, const void* k, const void* v, const float* g, const 
 struct ScanSide {
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
+  int cus = 0;  // compute units of the device
 };
 
 int scan_side(ScanSide** out) {
@@ -321,6 +327,7 @@ int scan_side(ScanSide** out) {
     // default priority (the caller's streams are too); non-blocking: no implicit
     // ordering against the null stream, the events order everything
     if (e == hipSuccess) e = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) {
       s.stream = nullptr;
       return fail(CQGDN_EHIP, "cqgdn_bwd_recompute: creating its scan stream and events: %s", hipGetErrorString(e));
@@ -338,9 +345,25 @@ int cqgdn_bwd(const void* q, const void* k, const void* v, const float* g, const
               float scale, unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes,
               void* bwd_workspace, size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta,
               void* stream) {
+  // bwd_dkw beside the reverse scan when every scan workgroup (one per head, value
+  // slice and document, each holding a whole CU) is resident at once; otherwise
+  // after it.  CQGDN_DKW_BESIDE_SCAN=0 in the environment keeps it after the scan.
+  const char* env = getenv("CQGDN_DKW_BESIDE_SCAN");
+  const bool wanted = !(env && env[0] == '0');
+  if (!wanted || T == 0)
+    return bwd_impl(q, k, v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags,
+                    fwd_workspace, fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg, dbeta,
+                    stream, true, nullptr);
+  if (const int e = bwd_impl(q, k, v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags,
+                             fwd_workspace, fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg,
+                             dbeta, stream, false, nullptr))
+    return e;
+  ScanSide* side = nullptr;
+  if (const int e = scan_side(&side)) return e;
+  const bool beside = (int64_t)H * 8 * n_docs <= side->cus;
   return bwd_impl(q, k, v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags, fwd_workspace,
                   fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg, dbeta, stream, true,
-                  nullptr);
+                  nullptr, beside ? side->stream : nullptr, side->fork, side->join);
 }
 
 int cqgdn_bwd_recompute(const void* q, const void* k, const void* v, const float* g, const float* beta,

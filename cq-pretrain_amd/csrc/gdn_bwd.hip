@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
     const float* __restrict__ rk, const bf16* __restrict__ dout, const float* __restrict__ gc,
     const float* __restrict__ beta, const bf16* __restrict__ Tm,
     const int32_t* __restrict__ chunks, int H, float scale, bf16* __restrict__ dvlT, bf16* __restrict__ XT,
-    bf16* __restrict__ knP, bf16* __restrict__ WT) {
+    bf16* __restrict__ knP, bf16* __restrict__ WT, int* __restrict__ sync) {
   // grid (H, NC), chunks dispatched first to last: the reverse state scan that
   // follows reads the last chunks first, and they are then the most recently
   // written (still in the memory-side cache).  The scan's other two operands,
@@ -47,6 +47,12 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
+  // the counts of the reverse scan's hand-off to bwd_dkw start at zero: this (chunk,
+  // head)'s, and (one workgroup) the count of resident scan workgroups after them
+  if (tid == 0) {
+    sync[cb] = 0;
+    if (c == 0 && h == 0) sync[(size_t)gridDim.y * H] = 0;
+  }
 
   // Row tiles only (every transposed operand is read with ds_read_b64_tr_b16),
   // 52 KB, so three workgroups share a CU.  The outputs are staged over them
@@ -313,24 +319,36 @@ constexpr int BWD_OUT_STORES = 6;
 // slice's [k][16] and [t][16], read transposed from the [v][k] / [v][t] scratch).
 // Each store instruction writes 1 KB of contiguous lines, with the non-temporal
 // hint: the scan still has the earlier chunks' operands to read (bwd_local wrote
-// them first to last, so they are the oldest in the memory-side cache), and
-// bwd_dkw reads these outputs only after the scan.
+// them first to last, so they are the oldest in the memory-side cache).  The
+// stores are device-scope (sc1): bwd_dkw may read them while the scan runs.
 __device__ __forceinline__ void bwd_copy_out(const BwdScratch& sc, int c, int H, int h, int slice, int lane,
                                              bf16* __restrict__ dhS, bf16* __restrict__ dVnS) {
   const size_t cb = (size_t)c * H + h;
   const int r = lane & 15, q4 = lane >> 4, half = 8 * (q4 & 1), row = 16 * (q4 >> 1) + r;
-  bf16* ds = dhS + cb * (D * D) + slice * (D * 16);
+  const __amdgpu_buffer_rsrc_t ds = buf_rsrc(dhS + cb * (D * D) + slice * (D * 16), D * 16 * 2);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) st8_nt(ds + (32 * i + row) * 16 + half, ld8_tr16(sc.s, BS_SROW, 32 * i));
-  bf16* vs = dVnS + cb * (CH * D) + slice * (CH * 16);
+  for (int i = 0; i < 4; ++i) buf_st16_nt_sc1(ds, ((32 * i + row) * 16 + half) * 2, ld8_tr16(sc.s, BS_SROW, 32 * i));
+  const __amdgpu_buffer_rsrc_t vs = buf_rsrc(dVnS + cb * (CH * D) + slice * (CH * 16), CH * 16 * 2);
 #pragma unroll
-  for (int i = 0; i < 2; ++i) st8_nt(vs + (32 * i + row) * 16 + half, ld8_tr16(sc.v, BS_VROW, 32 * i));
+  for (int i = 0; i < 2; ++i) buf_st16_nt_sc1(vs, ((32 * i + row) * 16 + half) * 2, ld8_tr16(sc.v, BS_VROW, 32 * i));
+}
+
+// One slice's dS / dVn of chunk c are stored (their stores have completed): add to
+// the chunk's count, which bwd_dkw waits to see at 8, from one lane.
+__device__ __forceinline__ void bwd_publish(int* __restrict__ ready, int c, int H, int h, int lane) {
+  asm volatile("" ::: "memory");
+  if (lane == 0) count_add(ready + (size_t)c * H + h);
+  asm volatile("" ::: "memory");
 }
 
 __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
     const bf16* __restrict__ knP, const float* __restrict__ gc, const bf16* __restrict__ dvlT,
     const bf16* __restrict__ XT, const bf16* __restrict__ WT, const int32_t* __restrict__ chunks,
-    const int32_t* __restrict__ doc_chunk, int H, bf16* __restrict__ dhS, bf16* __restrict__ dVnS) {
+    const int32_t* __restrict__ doc_chunk, int H, bf16* __restrict__ dhS, bf16* __restrict__ dVnS,
+    int* __restrict__ ready, int* __restrict__ resident) {
+  // ready / resident: null, or the hand-off counts of a bwd_dkw running beside this
+  // scan (each workgroup adds one to resident when it starts, and one to a chunk's
+  // ready count once its outputs of that chunk are stored)
   const int h = blockIdx.x % H, slice = blockIdx.x / H, d = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q4 = lane >> 4;
@@ -341,6 +359,7 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
   const int c_end = doc_chunk[d + 1], n = c_end - doc_chunk[d];
   // step tau handles chunk c_end - 1 - tau (chunks in reverse)
   if (wave == 0) {
+    if (resident && lane == 0) count_add(resident);
     f32x4 dS[8];  // dS[m][i] = dState[k = 16m + 4q4 + i][v = v0 + r]
 #pragma unroll
     for (int m = 0; m < 8; ++m) dS[m] = zero4();
@@ -419,7 +438,10 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
     // first stores step tau-1's outputs from that stage's -W^T region).  Loads
     // and stores retire in issue order, so a loader waits by letting exactly
     // the operations it issued after that part stay in flight (as in the
-    // forward scan).
+    // forward scan).  Loader 1's wait at step tau >= 3 also covers the copy-out
+    // of step tau-3 (issued before step tau+1's part), so with a bwd_dkw beside
+    // the scan it then announces that step's chunk: one atomic add, in flight
+    // with the step's other operations and counted in the next wait.
     const int j = wave - 1;
     for (int tau = -BS_DEPTH; tau < n; ++tau) {
       const int xn = tau + 1, xo = tau - 1, xi = tau + BS_DEPTH;
@@ -432,15 +454,21 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
             wait_vmem_all();
           bwd_fix_tail(stage[xn & (BS_STAGES - 1)], chunks, c_end - 1 - xn, lane);
         } else {
-          const bool stored = tau >= 2;  // the copy-out of step tau-2 came after this part
-          if (later && stored)
+          const bool stored = tau >= 2;                 // the copy-out of step tau-2 came after this part
+          const bool announced = ready && tau >= 4;     // and step tau-1's announcement (of step tau-4)
+          if (later && announced)
+            wait_vmem_le<BWD_PART_COPIES[1] + BWD_OUT_STORES + 1>();
+          else if (later && stored)
             wait_vmem_le<BWD_PART_COPIES[1] + BWD_OUT_STORES>();
           else if (later)
             wait_vmem_le<BWD_PART_COPIES[1]>();
+          else if (announced)
+            wait_vmem_le<BWD_OUT_STORES + 1>();
           else if (stored)
             wait_vmem_le<BWD_OUT_STORES>();
           else
             wait_vmem_all();
+          if (ready && tau >= 3) bwd_publish(ready, c_end - 1 - (tau - 3), H, h, lane);
         }
       }
       if (j == 1 && xo >= 0)
@@ -449,8 +477,14 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
         bwd_issue(stage[xi & (BS_STAGES - 1)], chunks, c_end - 1 - xi, H, h, v0, lane, j, knP, gc, dvlT, XT, WT);
       lds_barrier();
     }
-    if (n > 0 && j == 1)
+    if (n > 0 && j == 1) {
       bwd_copy_out(bwd_scratch(stage[(n - 1) & (BS_STAGES - 1)]), c_end - n, H, h, slice, lane, dhS, dVnS);
+      if (ready) {
+        // the loop announced steps 0 .. n-5; the rest once every store has completed
+        wait_vmem_all();
+        for (int s = max(n - 4, 0); s < n; ++s) bwd_publish(ready, c_end - 1 - s, H, h, lane);
+      }
+    }
   }
 }
 
@@ -484,10 +518,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     const bf16* __restrict__ dVn, const bf16* __restrict__ vin, const float* __restrict__ beta,
     const bf16* __restrict__ Tm, const int32_t* __restrict__ chunks, int H, float scale, int normalize,
     bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv, float* __restrict__ dg,
-    float* __restrict__ dbeta) {
-  // grid (H, NC), chunks first to last: the reverse state scan wrote the first
-  // chunks last, so they are the likeliest still in the memory-side cache
-  const int h = blockIdx.x, c = blockIdx.y;
+    float* __restrict__ dbeta, const int* __restrict__ ready) {
+  // grid (H, NC).  After the reverse scan: chunks first to last (the scan wrote the
+  // first chunks last, so they are the likeliest still in the memory-side cache).
+  // Beside the scan (ready != null): chunks last to first, the order the scan
+  // finishes them, each workgroup waiting for its chunk's count after phase 1.
+  const int h = blockIdx.x, c = ready ? gridDim.y - 1 - blockIdx.y : blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);
@@ -505,6 +541,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ float dgw[4][64];
   __shared__ __attribute__((aligned(16))) float Rs[64];  // rsqrt norms of q (1 without normalize)
+  __shared__ float pzs;  // 1, or NaN when the wait for the reverse scan gave up (every output is poisoned)
   bf16* Qs = reinterpret_cast<bf16*>(r1);
   bf16* Ks = reinterpret_cast<bf16*>(r2);
   bf16* dPm = reinterpret_cast<bf16*>(r3);
@@ -517,7 +554,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   // This wave's state fragments: rows k = 16 (2 wave + mm) + r of h
   // (column gathers of h^T) and of dS_{c+1}, value block kb.
   const bf16* ht = hT + cb * (D * D);
-  const bf16* dhc = dh + cb * (D * D);
   bf16x8 bh[2][4], bd[2][4];
   // Every prologue load is issued before the first wait: the column gathers'
   // loads, the gate and norm values (unconditional: rq is allocated either
@@ -624,13 +660,23 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         if (r == 0) dgl[48 + 4 * q4 + i] += rowE3[i];
     }
   }
+  // dS_{c+1} and dVn are the reverse scan's: beside it, wait until all eight value
+  // slices of this chunk are stored (wave 1 has the fewest phase-1 pairs)
+  if (wave == 1) {
+    bool ok = true;
+    if (ready && lane == 0) ok = count_wait_ge(ready + cb, D / 16);
+    if (lane == 0) pzs = ok ? 1.f : __builtin_nanf("");
+  }
   lds_barrier();
+  const float pz = pzs;
+  const __amdgpu_buffer_rsrc_t dh_rs = buf_rsrc(dh + cb * (D * D), D * D * 2);
 
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
-      bd[mm][kb] = ld8(dhc + (2 * kb + (q4 >> 1)) * (D * 16) + (16 * (2 * wave + mm) + r) * 16 + 8 * (q4 & 1));
+      bd[mm][kb] = buf_ld16_sc1<bf16x8>(
+          dh_rs, ((2 * kb + (q4 >> 1)) * (D * 16) + (16 * (2 * wave + mm) + r) * 16 + 8 * (q4 & 1)) * 2);
 
   // ---- phase 2: dQ^T (k-tiles 2w, 2w+1 as rows, t columns); dG_t from the output term ----
   // Each MFMA takes the operands of dQ = dO h^T + (dP Gam) K swapped, so a lane holds 4
@@ -722,7 +768,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       const int k0 = 16 * (2 * wave + mm) + 4 * q4;
       const f32x4 qr = cvtf4(ld4(Qs + t * LDK + k0));
       const f32x4 x = normalize ? (dQ[mm][n] - qr * dot) * rs : dQ[mm][n];
-      buf_st4(dq_rs, r * rowb + k0 * 2, 16 * n * rowb, x);  // row t, columns k0 .. k0 + 3
+      buf_st4(dq_rs, r * rowb + k0 * 2, 16 * n * rowb, x * pz);  // row t, columns k0 .. k0 + 3
     }
   }
   }
@@ -730,7 +776,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   {
     const bf16* dvs = dVn + cb * (CH * D);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
+    for (int i = 0; i < 4; ++i) dma16_sc1(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
   }
 
   // ---- phase 3: dK^T partial (k rows, t columns), kept in registers for the wy part ----
@@ -1006,7 +1052,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         const int s = 16 * n + r;
         const f32x4 vv = cvtf4(ld4(Vs + s * LDK + 16 * m + 4 * q4));
         colB[n] += acc[n][0] * vv[0] + acc[n][1] * vv[1] + acc[n][2] * vv[2] + acc[n][3] * vv[3];
-        buf_st4(dv_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, acc[n] * Bs[s]);  // row s
+        buf_st4(dv_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, acc[n] * (Bs[s] * pz));  // row s
       }
     }
 #pragma unroll
@@ -1089,7 +1135,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       const int m = 2 * wave + mm;
       const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
       const f32x4 out = normalize ? (dkr[mm][n] - kk * dot) * rsn[n] : dkr[mm][n];
-      buf_st4(dk_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, out);  // row t
+      buf_st4(dk_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, out * pz);  // row t
     }
   }
   if (tid < 64) {
@@ -1102,35 +1148,65 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       if (t + off < 64) x += o;
     }
     if (in) {
-      dg[(size_t)(ci.start + t) * H + h] = x;
-      dbeta[(size_t)(ci.start + t) * H + h] = dbw[t] + dbw[64 + t] + dbw[128 + t] + dbw[192 + t];
+      dg[(size_t)(ci.start + t) * H + h] = x * pz;
+      dbeta[(size_t)(ci.start + t) * H + h] = (dbw[t] + dbw[64 + t] + dbw[128 + t] + dbw[192 + t]) * pz;
     }
   }
 }
 
 // ---------------------------------------------------------------------------
+// One wave on bwd_dkw's stream that ends once every reverse-scan workgroup has
+// started (each adds one to *resident), so that bwd_dkw, launched behind it, can
+// only take the CUs the scan leaves free and never holds one a scan workgroup
+// still waits for.  Bounded: after COUNT_SPIN_LIMIT polls it ends anyway, and
+// bwd_dkw's own bounded waits then decide.
+__global__ __launch_bounds__(64) void scan_resident_gate_kernel(const int* __restrict__ resident, int expected) {
+  if (threadIdx.x == 0) count_wait_ge(resident, expected);
+}
+
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
   auto F = [&](int i) { return reinterpret_cast<const bf16*>(a.fws + a.foff[i]); };
   auto Ff = [&](int i) { return reinterpret_cast<const float*>(a.fws + a.foff[i]); };
   auto B = [&](int i) { return reinterpret_cast<bf16*>(a.bws + a.boff[i]); };
   const dim3 grid_p(a.H, a.n_chunks);  // chunk-major dispatch (the kernels pick the chunk order)
+  int* sync = reinterpret_cast<int*>(a.bws + a.boff[B_SYNC]);
+  int* ready = sync;                                 // [NC][H]
+  int* resident = sync + (size_t)a.n_chunks * a.H;  // one count
+  const bool beside = a.side != nullptr;
   {
     TimedLaunch tl(K_BWD_LOCAL, stream);
     hipLaunchKernelGGL(bwd_local_kernel, dim3(a.H, a.n_chunks), dim3(256), 0, stream, a.q, a.k, Ff(F_RQ),
                        Ff(F_RK), a.dout, Ff(F_GC), a.beta, F(F_TM), a.chunks, a.H, a.scale, B(B_DVLT), B(B_XT),
-                       B(B_KNP), B(B_WT));
+                       B(B_KNP), B(B_WT), sync);
+  }
+  if (beside) {
+    if (const hipError_t e = hipEventRecord(a.side_fork, stream)) return e;
+    if (const hipError_t e = hipStreamWaitEvent(a.side, a.side_fork, 0)) return e;
   }
   {
     TimedLaunch tl(K_BWD_SCAN, stream);
     hipLaunchKernelGGL(bwd_scan_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, B(B_KNP),
-                       Ff(F_GC), B(B_DVLT), B(B_XT), B(B_WT), a.chunks, a.doc_chunk, a.H, B(B_DH), B(B_DVN));
+                       Ff(F_GC), B(B_DVLT), B(B_XT), B(B_WT), a.chunks, a.doc_chunk, a.H, B(B_DH), B(B_DVN),
+                       beside ? ready : nullptr, beside ? resident : nullptr);
+  }
+  if (beside) {
+    hipLaunchKernelGGL(scan_resident_gate_kernel, dim3(1), dim3(64), 0, a.side, resident,
+                       a.H * (D / 16) * a.n_docs);
+    {
+      TimedLaunch tl(K_BWD_DKW, a.side);
+      hipLaunchKernelGGL(bwd_dkw_kernel, grid_p, dim3(256), 0, a.side, a.q, a.k, Ff(F_RQ), Ff(F_RK), Ff(F_GC),
+                         F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.v, a.beta, F(F_TM), a.chunks, a.H, a.scale,
+                         (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta, (const int*)ready);
+    }
+    if (const hipError_t e = hipEventRecord(a.side_join, a.side)) return e;
+    return hipStreamWaitEvent(stream, a.side_join, 0);
   }
   if (a.dkw_after)
     if (const hipError_t e = hipStreamWaitEvent(stream, a.dkw_after, 0)) return e;
   TimedLaunch tl(K_BWD_DKW, stream);
   hipLaunchKernelGGL(bwd_dkw_kernel, grid_p, dim3(256), 0, stream, a.q, a.k, Ff(F_RQ), Ff(F_RK), Ff(F_GC),
                      F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.v, a.beta, F(F_TM), a.chunks, a.H, a.scale,
-                     (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta);
+                     (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta, (const int*)nullptr);
   return hipSuccess;
 }
 

@@ -516,6 +516,45 @@ __device__ __forceinline__ void buf_st4(__amdgpu_buffer_rsrc_t rs, int voff, int
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, cvt4(x)), rs, voff, soff, 0);
 }
 
+// ---- hand-off between two kernels running at the same time ----------------
+// The eight XCDs' L2 caches are not coherent with one another.  Data that one
+// running kernel hands to another is stored and loaded with the cache-policy bit
+// sc1 (device scope), as relaxed agent-scope atomics are: the store writes
+// through to the device-coherent level, and the load does not take a line that
+// another XCD may have changed.  The count announcing the data is an agent-scope
+// atomic add, issued only after the data's stores have completed (vmcnt), and
+// read with an agent-scope load before any of the data is loaded.
+constexpr int CPOL_NT = 2, CPOL_SC1 = 16;  // aux bits of the buffer and load-to-LDS intrinsics (gfx950)
+__device__ __forceinline__ void dma16_sc1(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)lds, 16, 0, CPOL_SC1);
+}
+template <class X8>
+__device__ __forceinline__ X8 buf_ld16_sc1(__amdgpu_buffer_rsrc_t rs, int voff) {
+  return __builtin_bit_cast(X8, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, CPOL_SC1));
+}
+// 16 bytes stored with the non-temporal hint at device scope
+template <class X8>
+__device__ __forceinline__ void buf_st16_nt_sc1(__amdgpu_buffer_rsrc_t rs, int voff, X8 x) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), rs, voff, 0, CPOL_NT | CPOL_SC1);
+}
+__device__ __forceinline__ void count_add(int* p) {
+  __hip_atomic_fetch_add(p, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int count_read(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Poll *p until it reaches target, sleeping between polls; bounded: false after
+// COUNT_SPIN_LIMIT polls (tens of milliseconds), so a hand-off that never comes
+// ends the waiting kernel with poisoned results instead of hanging it.
+constexpr int COUNT_SPIN_LIMIT = 1 << 20;
+__device__ __forceinline__ bool count_wait_ge(const int* p, int target) {
+  for (int i = 0; i < COUNT_SPIN_LIMIT; ++i) {
+    if (count_read(p) >= target) return true;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  return false;
+}
+
 // Per-chunk metadata: chunk_table[c] = (start event, length).  A chunk never
 // crosses a document boundary; doc_chunk[d] .. doc_chunk[d+1] are the chunks of
 // document d, in time order.

@@ -47,6 +47,10 @@ struct BwdArgs {
   bf16 *dq, *dk, *dv;
   float *dg, *dbeta;
   hipEvent_t dkw_after;  // optional: bwd_dkw waits for this event (the forward scan's join)
+  // optional: bwd_dkw runs on `side` beside the reverse scan (after side_fork, recorded
+  // on the caller's stream behind bwd_local; side_join is recorded behind it)
+  hipStream_t side;
+  hipEvent_t side_fork, side_join;
 };
 
 // Both return the first error of their stream-ordering calls (hipSuccess without them);

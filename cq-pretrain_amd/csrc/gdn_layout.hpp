@@ -42,6 +42,9 @@ enum BwdBuf {
   B_DVN,       // bf16 [NC][H][8][64][16] d v_new, value-slice-major (s, t, v%16)
   B_KNP,       // bf16 [T][H][D]       exp(G_last - G_t) Kn_t in perm32 column order (reverse scan operand), by bwd_local
   B_WT,        // bf16 [NC][H][D][64]  -W transposed (k, t), perm32 column order (reverse scan operand), by bwd_local
+  B_SYNC,      // i32  [NC][H] + 64     per (chunk, head): reverse-scan value slices whose dS / dVn are stored,
+               //                       then at [NC][H] the count of resident reverse-scan workgroups
+               //                       (bwd_dkw beside the scan; zeroed by bwd_local)
   B_COUNT
 };
 
@@ -72,6 +75,7 @@ inline void bwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[B_DVN] = chunk * 64 * 128 * 2;
   s[B_KNP] = ev * 128 * 2;
   s[B_WT] = chunk * 128 * 64 * 2;
+  s[B_SYNC] = (chunk + 64) * 4;
 }
 
 // Offsets of every buffer; returns the total size in bytes.

@@ -73,7 +73,7 @@ int64_t cqgdn_chunk_table(const int64_t* bounds, int n_bounds, int32_t* table, i
  * per-row l2 scales, not normalized copies).
  */
 #define CQGDN_FWD_BUFFERS 10
-#define CQGDN_BWD_BUFFERS 6
+#define CQGDN_BWD_BUFFERS 7
 size_t cqgdn_fwd_workspace_size(int64_t T, int H, int64_t n_chunks);
 int cqgdn_fwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets, int count);
 size_t cqgdn_bwd_workspace_size(int64_t T, int H, int64_t n_chunks);

@@ -17,7 +17,7 @@
 import pytest
 import torch
 
-from gdn_testlib import TOL_BF16, TOL_STATE, assert_close_bf16, compare_layer, layer_parity, rel_l2
+from gdn_testlib import TOL_BF16, TOL_STATE, assert_close_bf16, compare_layer, layer_parity, rel_l2, view
 from oracle import gdn_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -467,6 +467,99 @@ def test_bwd_recompute_graph_replay(gdn):
     with torch.cuda.graph(graph):
         outs = run()
     for replay in range(3):
+        for o in outs:
+            o.fill_(0)
+        _ = (torch.randn(256, 256, device=DEV) @ torch.randn(256, 256, device=DEV)).sum().item()  # eager work between
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, o, e in zip(("dq", "dk", "dv", "dg", "dbeta"), outs, eager):
+            assert torch.equal(o, e), f"replay {replay}: {name} differs"
+
+
+def _bwd_direct(gdn, xs, bounds, do, beside, monkeypatch):
+    """cqgdn_bwd through the C ABI with its workspace in hand; beside=False sets CQGDN_DKW_BESIDE_SCAN=0."""
+    from cqgdn import _lib
+
+    monkeypatch.setenv("CQGDN_DKW_BESIDE_SCAN", "1" if beside else "0")
+    T, H = xs[0].shape[1], xs[0].shape[2]
+    q, k, v, g, b = (x.to(DEV).contiguous() for x in xs)
+    do_dev = do.to(DEV)
+    _, _, ws = gdn._forward(q, k, v, g, b, bounds, True, 128 ** -0.5, training=True)
+    _, table, doc = gdn.device_metadata(bounds, DEV)
+    nc = table.shape[0]
+    bws = torch.full((_lib.lib().cqgdn_bwd_workspace_size(T, H, nc),), 0x5A, dtype=torch.uint8, device=DEV)
+    dq, dk, dv = (torch.empty_like(v) for _ in range(3))
+    dg, db = torch.empty_like(g), torch.empty_like(b)
+    P = gdn._ptr
+    gdn.call("cqgdn_bwd", P(q), P(k), P(v), P(g), P(b), P(do_dev), T, H, P(table), nc, P(doc), len(bounds) - 1,
+             128 ** -0.5, 3, P(ws), ws.numel(), P(bws), bws.numel(), P(dq), P(dk), P(dv), P(dg), P(db),
+             gdn._stream(q.device))
+    torch.cuda.synchronize()
+    sync = view(bws, _lib.bwd_offsets(T, H, nc)["sync"], torch.int32, (nc * H + 1,)).cpu()
+    return [x.cpu() for x in (dq, dk, dv, dg, db)], sync[:-1].view(nc, H), int(sync[-1])
+
+
+@pytest.mark.parametrize("kind", ["config2", "two_docs", "three_docs"])
+def test_bwd_dkw_beside_scan_matches_after_scan(gdn, kind, monkeypatch):
+    """cqgdn_bwd runs bwd_dkw on a second stream beside the reverse scan when every scan workgroup (one
+    per head, 16-wide value slice and document) is resident at once: each chunk-head waits, bounded,
+    until all eight value slices have announced its dS and dVn (device-scope stores, then an atomic
+    count).  Otherwise, and with CQGDN_DKW_BESIDE_SCAN=0, bwd_dkw runs after the scan.  Both orders give
+    bit-identical gradients.  The workspace's counts show which path ran: beside the scan every
+    chunk-head's count ends at 8 and the resident count at the scan's workgroup count; after it both
+    stay at bwd_local's zeros."""
+    from cqgdn import synthetic
+
+    H = 16
+    if kind == "config2":
+        T, mask, bounds = synthetic.config_events(2, seed=0)
+        xs = inputs(T, H, seed=21, readonly=mask)
+    elif kind == "two_docs":
+        T, bounds = 1500, (0, 700, 1500)
+        xs = inputs(T, H, seed=22)
+    else:
+        T, bounds = 1200, (0, 300, 777, 1200)
+        xs = inputs(T, H, seed=23)
+    n_docs = len(bounds) - 1
+    fits = H * 8 * n_docs <= torch.cuda.get_device_properties(0).multi_processor_count
+    print(f"case bwd_dkw beside the reverse scan ({kind}): T={T} docs={n_docs} fits={fits}", flush=True)
+    do = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(24)).bfloat16()
+    after, ready_a, resident_a = _bwd_direct(gdn, xs, bounds, do, False, monkeypatch)
+    beside, ready_b, resident_b = _bwd_direct(gdn, xs, bounds, do, True, monkeypatch)
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dbeta"), after, beside):
+        assert not torch.isnan(a.float()).any(), name
+        assert torch.equal(a, b), name
+    assert not ready_a.any() and resident_a == 0
+    if fits:
+        assert bool((ready_b == 8).all()) and resident_b == H * 8 * n_docs, (ready_b.unique(), resident_b)
+    else:
+        assert not ready_b.any() and resident_b == 0
+
+
+def test_bwd_beside_scan_graph_replay(gdn):
+    """The cached backward with bwd_dkw beside the reverse scan (second stream, fork and join events,
+    the counts zeroed by bwd_local inside the call) captured in a HIP graph: each replay, with eager
+    work between, equals the eager call bitwise."""
+    T, bounds, H = 900, (0, 900), 16
+    print(f"case cached bwd beside the scan, graph replay T={T} H={H}", flush=True)
+    q, k, v, g, b = (x.to(DEV).contiguous() for x in inputs(T, H, seed=4343))
+    dy = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(4344)).bfloat16().to(DEV)
+    _, _, ws = gdn._forward(q, k, v, g, b, bounds, True, 128 ** -0.5, training=True)
+
+    def run():
+        return gdn._backward(q, k, v, g, b, ws, dy, bounds, True, 128 ** -0.5)
+
+    eager = [x.clone() for x in run()]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()  # warm-up off the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = run()
+    for replay in range(4):
         for o in outs:
             o.fill_(0)
         _ = (torch.randn(256, 256, device=DEV) @ torch.randn(256, 256, device=DEV)).sum().item()  # eager work between
