@@ -73,6 +73,59 @@ constexpr int kMaxDevices = 64;
 std::mutex g_static_mu;
 void* g_static_ws[kMaxDevices] = {};
 
+// The side stream and its two events: cqgdn_bwd_recompute runs the forward scan
+// on it, cqgdn_bwd its bwd_dkw beside the reverse scan.
+// One set per (thread, device), created on first use and kept until the process
+// ends.  Per thread, so that a caller capturing a HIP graph never shares them with
+// another thread's calls.
+struct ScanSide {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  int cus = 0;  // compute units of the device
+};
+
+int scan_side(ScanSide** out) {
+  thread_local ScanSide sides[kMaxDevices];
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return fail(CQGDN_EHIP, "cqgdn_bwd_recompute: no current HIP device (or device %d >= %d)", dev, kMaxDevices);
+  ScanSide& s = sides[dev];
+  if (!s.stream) {
+    hipError_t e = hipEventCreateWithFlags(&s.fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s.join, hipEventDisableTiming);
+    // default priority (the caller's streams are too); non-blocking: no implicit
+    // ordering against the null stream, the events order everything
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) {
+      s.stream = nullptr;
+      return fail(CQGDN_EHIP, "cqgdn_bwd_recompute: creating its scan stream and events: %s", hipGetErrorString(e));
+    }
+  }
+  *out = &s;
+  return CQGDN_OK;
+}
+
+constexpr int kBesideMinChunks = 64;
+
+// The side stream for a kernel beside a state scan, or null (*out) when that kernel
+// runs after the scan: each scan workgroup (one per head, 16-wide value slice and
+// document) holds a whole CU, and the kernel beside waits for the scan's chunks,
+// so every scan workgroup must be resident at once; `env` = "0" in the
+// environment keeps the kernel after the scan.
+int side_beside_scan(const char* env, int64_t T, int H, int64_t n_chunks, int n_docs, ScanSide** out) {
+  *out = nullptr;
+  const char* e = getenv(env);
+  if ((e && e[0] == '0') || T <= 0 || H <= 0 || n_docs <= 0) return CQGDN_OK;
+  // documents of fewer chunks than this on average: the scan is too short for
+  // the side stream's extra launches and events to pay
+  if (n_chunks < (int64_t)kBesideMinChunks * n_docs) return CQGDN_OK;
+  ScanSide* side = nullptr;
+  if (const int err = scan_side(&side)) return err;
+  if ((int64_t)H * 8 * n_docs <= side->cus) *out = side;
+  return CQGDN_OK;
+}
+
 int static_workspace(void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
@@ -305,37 +358,6 @@ int bwd_impl(const void* q, const void* k, const void* v, const float* g, const 
   return check_launch("cqgdn_bwd");
 }
 
-// The side stream and its two events that cqgdn_bwd_recompute runs the forward
-// scan on: one set per (thread, device), created on first use and kept until the
-// process ends.  Per thread, so that a caller capturing a HIP graph never shares
-// them with another thread's calls.
-struct ScanSide {
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-  int cus = 0;  // compute units of the device
-};
-
-int scan_side(ScanSide** out) {
-  thread_local ScanSide sides[kMaxDevices];
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
-    return fail(CQGDN_EHIP, "cqgdn_bwd_recompute: no current HIP device (or device %d >= %d)", dev, kMaxDevices);
-  ScanSide& s = sides[dev];
-  if (!s.stream) {
-    hipError_t e = hipEventCreateWithFlags(&s.fork, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&s.join, hipEventDisableTiming);
-    // default priority (the caller's streams are too); non-blocking: no implicit
-    // ordering against the null stream, the events order everything
-    if (e == hipSuccess) e = hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&s.cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess) {
-      s.stream = nullptr;
-      return fail(CQGDN_EHIP, "cqgdn_bwd_recompute: creating its scan stream and events: %s", hipGetErrorString(e));
-    }
-  }
-  *out = &s;
-  return CQGDN_OK;
-}
 }  // namespace
 
 extern "C" {
@@ -345,25 +367,18 @@ int cqgdn_bwd(const void* q, const void* k, const void* v, const float* g, const
               float scale, unsigned flags, const void* fwd_workspace, size_t fwd_workspace_bytes,
               void* bwd_workspace, size_t bwd_workspace_bytes, void* dq, void* dk, void* dv, float* dg, float* dbeta,
               void* stream) {
-  // bwd_dkw beside the reverse scan when every scan workgroup (one per head, value
-  // slice and document, each holding a whole CU) is resident at once; otherwise
-  // after it.  CQGDN_DKW_BESIDE_SCAN=0 in the environment keeps it after the scan.
-  const char* env = getenv("CQGDN_DKW_BESIDE_SCAN");
-  const bool wanted = !(env && env[0] == '0');
-  if (!wanted || T == 0)
-    return bwd_impl(q, k, v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags,
-                    fwd_workspace, fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg, dbeta,
-                    stream, true, nullptr);
+  // bwd_dkw beside the reverse scan when every scan workgroup is resident at once
+  // (CQGDN_DKW_BESIDE_SCAN=0 keeps it after the scan); every argument is checked
+  // before the side stream is looked up
   if (const int e = bwd_impl(q, k, v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags,
                              fwd_workspace, fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg,
                              dbeta, stream, false, nullptr))
     return e;
   ScanSide* side = nullptr;
-  if (const int e = scan_side(&side)) return e;
-  const bool beside = (int64_t)H * 8 * n_docs <= side->cus;
+  if (const int e = side_beside_scan("CQGDN_DKW_BESIDE_SCAN", T, H, n_chunks, n_docs, &side)) return e;
   return bwd_impl(q, k, v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags, fwd_workspace,
                   fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg, dbeta, stream, true,
-                  nullptr, beside ? side->stream : nullptr, side->fork, side->join);
+                  nullptr, side ? side->stream : nullptr, side ? side->fork : nullptr, side ? side->join : nullptr);
 }
 
 int cqgdn_bwd_recompute(const void* q, const void* k, const void* v, const float* g, const float* beta,

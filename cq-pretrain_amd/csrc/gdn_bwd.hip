@@ -319,18 +319,28 @@ constexpr int BWD_OUT_STORES = 6;
 // slice's [k][16] and [t][16], read transposed from the [v][k] / [v][t] scratch).
 // Each store instruction writes 1 KB of contiguous lines, with the non-temporal
 // hint: the scan still has the earlier chunks' operands to read (bwd_local wrote
-// them first to last, so they are the oldest in the memory-side cache).  The
-// stores are device-scope (sc1): bwd_dkw may read them while the scan runs.
+// them first to last, so they are the oldest in the memory-side cache).  With
+// bwd_dkw beside the scan (SC1) the stores are device-scope: bwd_dkw reads them
+// while the scan runs.
+template <bool SC1>
 __device__ __forceinline__ void bwd_copy_out(const BwdScratch& sc, int c, int H, int h, int slice, int lane,
                                              bf16* __restrict__ dhS, bf16* __restrict__ dVnS) {
   const size_t cb = (size_t)c * H + h;
   const int r = lane & 15, q4 = lane >> 4, half = 8 * (q4 & 1), row = 16 * (q4 >> 1) + r;
-  const __amdgpu_buffer_rsrc_t ds = buf_rsrc(dhS + cb * (D * D) + slice * (D * 16), D * 16 * 2);
+  bf16* ds = dhS + cb * (D * D) + slice * (D * 16);
+  bf16* vs = dVnS + cb * (CH * D) + slice * (CH * 16);
+  if constexpr (SC1) {
+    const __amdgpu_buffer_rsrc_t dr = buf_rsrc(ds, D * 16 * 2), vr = buf_rsrc(vs, CH * 16 * 2);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) buf_st16_nt_sc1(ds, ((32 * i + row) * 16 + half) * 2, ld8_tr16(sc.s, BS_SROW, 32 * i));
-  const __amdgpu_buffer_rsrc_t vs = buf_rsrc(dVnS + cb * (CH * D) + slice * (CH * 16), CH * 16 * 2);
+    for (int i = 0; i < 4; ++i) buf_st16_nt_sc1(dr, ((32 * i + row) * 16 + half) * 2, ld8_tr16(sc.s, BS_SROW, 32 * i));
 #pragma unroll
-  for (int i = 0; i < 2; ++i) buf_st16_nt_sc1(vs, ((32 * i + row) * 16 + half) * 2, ld8_tr16(sc.v, BS_VROW, 32 * i));
+    for (int i = 0; i < 2; ++i) buf_st16_nt_sc1(vr, ((32 * i + row) * 16 + half) * 2, ld8_tr16(sc.v, BS_VROW, 32 * i));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st8_nt(ds + (32 * i + row) * 16 + half, ld8_tr16(sc.s, BS_SROW, 32 * i));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) st8_nt(vs + (32 * i + row) * 16 + half, ld8_tr16(sc.v, BS_VROW, 32 * i));
+  }
 }
 
 // One slice's dS / dVn of chunk c are stored (their stores have completed): add to
@@ -471,14 +481,21 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
           if (ready && tau >= 3) bwd_publish(ready, c_end - 1 - (tau - 3), H, h, lane);
         }
       }
-      if (j == 1 && xo >= 0)
-        bwd_copy_out(bwd_scratch(stage[xo & (BS_STAGES - 1)]), c_end - 1 - xo, H, h, slice, lane, dhS, dVnS);
+      if (j == 1 && xo >= 0) {
+        if (ready)
+          bwd_copy_out<true>(bwd_scratch(stage[xo & (BS_STAGES - 1)]), c_end - 1 - xo, H, h, slice, lane, dhS, dVnS);
+        else
+          bwd_copy_out<false>(bwd_scratch(stage[xo & (BS_STAGES - 1)]), c_end - 1 - xo, H, h, slice, lane, dhS, dVnS);
+      }
       if (xi < n)
         bwd_issue(stage[xi & (BS_STAGES - 1)], chunks, c_end - 1 - xi, H, h, v0, lane, j, knP, gc, dvlT, XT, WT);
       lds_barrier();
     }
     if (n > 0 && j == 1) {
-      bwd_copy_out(bwd_scratch(stage[(n - 1) & (BS_STAGES - 1)]), c_end - n, H, h, slice, lane, dhS, dVnS);
+      if (ready)
+        bwd_copy_out<true>(bwd_scratch(stage[(n - 1) & (BS_STAGES - 1)]), c_end - n, H, h, slice, lane, dhS, dVnS);
+      else
+        bwd_copy_out<false>(bwd_scratch(stage[(n - 1) & (BS_STAGES - 1)]), c_end - n, H, h, slice, lane, dhS, dVnS);
       if (ready) {
         // the loop announced steps 0 .. n-5; the rest once every store has completed
         wait_vmem_all();
@@ -671,12 +688,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   const float pz = pzs;
   const __amdgpu_buffer_rsrc_t dh_rs = buf_rsrc(dh + cb * (D * D), D * D * 2);
 
+  // (device-scope loads beside the scan, which may still be running)
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-      bd[mm][kb] = buf_ld16_sc1<bf16x8>(
-          dh_rs, ((2 * kb + (q4 >> 1)) * (D * 16) + (16 * (2 * wave + mm) + r) * 16 + 8 * (q4 & 1)) * 2);
+    for (int kb = 0; kb < 4; ++kb) {
+      const int i = (2 * kb + (q4 >> 1)) * (D * 16) + (16 * (2 * wave + mm) + r) * 16 + 8 * (q4 & 1);
+      bd[mm][kb] = ready ? buf_ld16_sc1<bf16x8>(dh_rs, i * 2) : ld8(dh + cb * (D * D) + i);
+    }
 
   // ---- phase 2: dQ^T (k-tiles 2w, 2w+1 as rows, t columns); dG_t from the output term ----
   // Each MFMA takes the operands of dQ = dO h^T + (dP Gam) K swapped, so a lane holds 4
@@ -776,7 +795,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   {
     const bf16* dvs = dVn + cb * (CH * D);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16_sc1(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
+    for (int i = 0; i < 4; ++i) {
+      if (ready)
+        dma16_sc1(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
+      else
+        dma16(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
+    }
   }
 
   // ---- phase 3: dK^T partial (k rows, t columns), kept in registers for the wy part ----
@@ -1164,6 +1188,10 @@ __global__ __launch_bounds__(64) void scan_resident_gate_kernel(const int* __res
   if (threadIdx.x == 0) count_wait_ge(resident, expected);
 }
 
+static void launch_resident_gate(const int* resident, int expected, hipStream_t stream) {
+  hipLaunchKernelGGL(scan_resident_gate_kernel, dim3(1), dim3(64), 0, stream, resident, expected);
+}
+
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
   auto F = [&](int i) { return reinterpret_cast<const bf16*>(a.fws + a.foff[i]); };
   auto Ff = [&](int i) { return reinterpret_cast<const float*>(a.fws + a.foff[i]); };
@@ -1190,8 +1218,7 @@ hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
                        beside ? ready : nullptr, beside ? resident : nullptr);
   }
   if (beside) {
-    hipLaunchKernelGGL(scan_resident_gate_kernel, dim3(1), dim3(64), 0, a.side, resident,
-                       a.H * (D / 16) * a.n_docs);
+    launch_resident_gate(resident, a.H * (D / 16) * a.n_docs, a.side);
     {
       TimedLaunch tl(K_BWD_DKW, a.side);
       hipLaunchKernelGGL(bwd_dkw_kernel, grid_p, dim3(256), 0, a.side, a.q, a.k, Ff(F_RQ), Ff(F_RK), Ff(F_GC),

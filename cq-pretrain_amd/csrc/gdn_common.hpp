@@ -532,7 +532,7 @@ template <class X8>
 __device__ __forceinline__ X8 buf_ld16_sc1(__amdgpu_buffer_rsrc_t rs, int voff) {
   return __builtin_bit_cast(X8, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, CPOL_SC1));
 }
-// 16 bytes stored with the non-temporal hint at device scope
+// 16 bytes stored at device scope with the non-temporal hint
 template <class X8>
 __device__ __forceinline__ void buf_st16_nt_sc1(__amdgpu_buffer_rsrc_t rs, int voff, X8 x) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), rs, voff, 0, CPOL_NT | CPOL_SC1);
@@ -543,14 +543,16 @@ __device__ __forceinline__ void count_add(int* p) {
 __device__ __forceinline__ int count_read(const int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Poll *p until it reaches target, sleeping between polls; bounded: false after
-// COUNT_SPIN_LIMIT polls (tens of milliseconds), so a hand-off that never comes
-// ends the waiting kernel with poisoned results instead of hanging it.
-constexpr int COUNT_SPIN_LIMIT = 1 << 20;
+// Poll *p until it reaches target, sleeping about 8,000 cycles (a few
+// microseconds) between polls: hundreds of waiting workgroups polling a few
+// lines faster than that slow the scan they wait for.  Bounded: false after
+// COUNT_SPIN_LIMIT polls (about a second), so a hand-off that never comes ends
+// the waiting kernel with poisoned results instead of hanging it.
+constexpr int COUNT_SPIN_LIMIT = 1 << 18;
 __device__ __forceinline__ bool count_wait_ge(const int* p, int target) {
   for (int i = 0; i < COUNT_SPIN_LIMIT; ++i) {
     if (count_read(p) >= target) return true;
-    __builtin_amdgcn_s_sleep(2);
+    __builtin_amdgcn_s_sleep(127);
   }
   return false;
 }

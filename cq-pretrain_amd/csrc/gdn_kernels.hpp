@@ -57,6 +57,7 @@ struct BwdArgs {
 // launch errors are left for hipGetLastError.
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream);
+
 void launch_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta,
                       bool beta_bf16, bool fp16, float* state, void* out, int N, int E, int H, float scale,
                       hipStream_t stream);

@@ -13,9 +13,9 @@ stores the last step, waits for everything and announces the steps the loop did 
 The model replays the kernel's loop and its wait counts against a queue in which exactly the last N
 operations are still in flight, and asserts: every wait covers the part it waits for; every
 announcement comes after all six stores of its step have retired; every step is announced exactly
-once (so bwd_dkw, which waits for the count of its chunk to reach 8, one per value slice, reads a
-chunk only after every slice's stores of it are visible).  A count that assumes an announcement
-that was not issued, or forgets the copy-out, must fail.
+once, in the order the scan finishes them (so bwd_dkw, which waits for the count of its chunk to
+reach 8, one per value slice, reads a chunk only after every slice's stores of it are visible).  A
+count that assumes an announcement that was not issued, or forgets the copy-out, must fail.
 """
 
 import pytest
@@ -131,3 +131,4 @@ def test_chunk_counts_reach_eight_only_after_every_slice():
         for step in per_slice[s]:
             counts[n - 1 - step] += 1
     assert counts == [8] * n
+

@@ -499,29 +499,38 @@ def _bwd_direct(gdn, xs, bounds, do, beside, monkeypatch):
     return [x.cpu() for x in (dq, dk, dv, dg, db)], sync[:-1].view(nc, H), int(sync[-1])
 
 
-@pytest.mark.parametrize("kind", ["config2", "two_docs", "three_docs"])
+def _beside(H, n_docs, nc):
+    """Whether the library runs the kernel after a state scan beside it: every scan workgroup (one per
+    head, 16-wide value slice and document, a whole CU each) is resident at once, and documents average
+    at least 64 chunks."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    return H * 8 * n_docs <= cus and nc >= 64 * n_docs
+
+
+@pytest.mark.parametrize("kind", ["config2", "two_long_docs_h4", "three_docs"])
 def test_bwd_dkw_beside_scan_matches_after_scan(gdn, kind, monkeypatch):
-    """cqgdn_bwd runs bwd_dkw on a second stream beside the reverse scan when every scan workgroup (one
-    per head, 16-wide value slice and document) is resident at once: each chunk-head waits, bounded,
-    until all eight value slices have announced its dS and dVn (device-scope stores, then an atomic
-    count).  Otherwise, and with CQGDN_DKW_BESIDE_SCAN=0, bwd_dkw runs after the scan.  Both orders give
-    bit-identical gradients.  The workspace's counts show which path ran: beside the scan every
-    chunk-head's count ends at 8 and the resident count at the scan's workgroup count; after it both
-    stay at bwd_local's zeros."""
+    """cqgdn_bwd runs bwd_dkw on a second stream beside the reverse scan, taking chunks in the order
+    the scan finishes them, when every scan workgroup is resident at once and the documents are long:
+    each chunk-head waits, bounded, until all eight value slices have announced its dS and dVn
+    (device-scope stores, then an atomic count).  Otherwise, and
+    with CQGDN_DKW_BESIDE_SCAN=0, bwd_dkw runs after the scan.  Both orders give bit-identical
+    gradients.  The workspace's counts show which path ran: beside the scan every chunk-head's count
+    ends at 8 and the resident count at the scan's workgroup count; after it both stay at bwd_local's
+    zeros."""
     from cqgdn import synthetic
 
-    H = 16
+    H = 4 if kind.endswith("h4") else 16
     if kind == "config2":
         T, mask, bounds = synthetic.config_events(2, seed=0)
         xs = inputs(T, H, seed=21, readonly=mask)
-    elif kind == "two_docs":
-        T, bounds = 1500, (0, 700, 1500)
+    elif kind == "two_long_docs_h4":
+        T, bounds = 8400, (0, 4200, 8400)
         xs = inputs(T, H, seed=22)
     else:
         T, bounds = 1200, (0, 300, 777, 1200)
         xs = inputs(T, H, seed=23)
     n_docs = len(bounds) - 1
-    fits = H * 8 * n_docs <= torch.cuda.get_device_properties(0).multi_processor_count
+    fits = _beside(H, n_docs, gdn.device_metadata(bounds, DEV)[1].shape[0])
     print(f"case bwd_dkw beside the reverse scan ({kind}): T={T} docs={n_docs} fits={fits}", flush=True)
     do = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(24)).bfloat16()
     after, ready_a, resident_a = _bwd_direct(gdn, xs, bounds, do, False, monkeypatch)
@@ -530,17 +539,22 @@ def test_bwd_dkw_beside_scan_matches_after_scan(gdn, kind, monkeypatch):
         assert not torch.isnan(a.float()).any(), name
         assert torch.equal(a, b), name
     assert not ready_a.any() and resident_a == 0
+    assert (kind != "three_docs") == fits
     if fits:
         assert bool((ready_b == 8).all()) and resident_b == H * 8 * n_docs, (ready_b.unique(), resident_b)
     else:
         assert not ready_b.any() and resident_b == 0
+    if kind == "two_long_docs_h4":  # two documents, four heads
+        ref = O.chunk_delta_backward(*(x.double() for x in xs), do.double(), bounds)
+        for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta"), beside, ref):
+            assert_close_bf16(name, x, r)
 
 
 def test_bwd_beside_scan_graph_replay(gdn):
     """The cached backward with bwd_dkw beside the reverse scan (second stream, fork and join events,
     the counts zeroed by bwd_local inside the call) captured in a HIP graph: each replay, with eager
     work between, equals the eager call bitwise."""
-    T, bounds, H = 900, (0, 900), 16
+    T, bounds, H = 4200, (0, 4200), 16
     print(f"case cached bwd beside the scan, graph replay T={T} H={H}", flush=True)
     q, k, v, g, b = (x.to(DEV).contiguous() for x in inputs(T, H, seed=4343))
     dy = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(4344)).bfloat16().to(DEV)
