@@ -357,6 +357,10 @@ int bwd_impl(const void* q, const void* k, const void* v, const float* g, const 
   a.side = side;
   a.side_fork = side_fork;
   a.side_join = side_join;
+  if (side) {
+    const char* t = getenv("CQGDN_TEST_DKW_GIVE_UP");  // failure-handling tests only
+    a.dkw_never_ready = t && t[0] == '1';
+  }
   if (const hipError_t e = launch_bwd(a, (hipStream_t)stream))
     return fail(CQGDN_EHIP, "cqgdn_bwd: waiting for the forward scan's stream: %s", hipGetErrorString(e));
   return check_launch("cqgdn_bwd");

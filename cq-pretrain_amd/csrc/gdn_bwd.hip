@@ -535,7 +535,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     const bf16* __restrict__ dVn, const bf16* __restrict__ vin, const float* __restrict__ beta,
     const bf16* __restrict__ Tm, const int32_t* __restrict__ chunks, int H, float scale, int normalize,
     bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv, float* __restrict__ dg,
-    float* __restrict__ dbeta, const int* __restrict__ ready) {
+    float* __restrict__ dbeta, const int* __restrict__ ready, int ready_target, int ready_polls) {
   // grid (H, NC).  After the reverse scan: chunks first to last (the scan wrote the
   // first chunks last, so they are the likeliest still in the memory-side cache).
   // Beside the scan (ready != null): chunks last to first, the order the scan
@@ -558,7 +558,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ float dgw[4][64];
   __shared__ __attribute__((aligned(16))) float Rs[64];  // rsqrt norms of q (1 without normalize)
-  __shared__ float pzs;  // 1, or NaN when the wait for the reverse scan gave up (every output is poisoned)
+  __shared__ int stale_s;  // nonzero when the wait for the reverse scan gave up
   bf16* Qs = reinterpret_cast<bf16*>(r1);
   bf16* Ks = reinterpret_cast<bf16*>(r2);
   bf16* dPm = reinterpret_cast<bf16*>(r3);
@@ -678,14 +678,16 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     }
   }
   // dS_{c+1} and dVn are the reverse scan's: beside it, wait until all eight value
-  // slices of this chunk are stored (wave 1 has the fewest phase-1 pairs)
+  // slices of this chunk are stored (wave 1 has the fewest phase-1 pairs).  If the
+  // wait gives up, dS_{c+1} and dVn are taken as NaN, which turns every output that
+  // depends on them (dk, dv, dg, dbeta) to NaN; dq does not depend on them.
   if (wave == 1) {
     bool ok = true;
-    if (ready && lane == 0) ok = count_wait_ge(ready + cb, D / 16);
-    if (lane == 0) pzs = ok ? 1.f : __builtin_nanf("");
+    if (ready && lane == 0) ok = count_wait_ge(ready + cb, ready_target, ready_polls);
+    if (lane == 0) stale_s = ok ? 0 : 1;
   }
   lds_barrier();
-  const float pz = pzs;
+  const bool stale = stale_s != 0;
   const __amdgpu_buffer_rsrc_t dh_rs = buf_rsrc(dh + cb * (D * D), D * D * 2);
 
   // (device-scope loads beside the scan, which may still be running)
@@ -696,6 +698,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       const int i = (2 * kb + (q4 >> 1)) * (D * 16) + (16 * (2 * wave + mm) + r) * 16 + 8 * (q4 & 1);
       bd[mm][kb] = ready ? buf_ld16_sc1<bf16x8>(dh_rs, i * 2) : ld8(dh + cb * (D * D) + i);
     }
+  if (stale) {
+    asm volatile("");  // a branch, not selects
+#pragma unroll
+    for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) bd[mm][kb] = cvt8(f32x8{NAN, NAN, NAN, NAN, NAN, NAN, NAN, NAN});
+  }
 
   // ---- phase 2: dQ^T (k-tiles 2w, 2w+1 as rows, t columns); dG_t from the output term ----
   // Each MFMA takes the operands of dQ = dO h^T + (dP Gam) K swapped, so a lane holds 4
@@ -787,7 +796,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       const int k0 = 16 * (2 * wave + mm) + 4 * q4;
       const f32x4 qr = cvtf4(ld4(Qs + t * LDK + k0));
       const f32x4 x = normalize ? (dQ[mm][n] - qr * dot) * rs : dQ[mm][n];
-      buf_st4(dq_rs, r * rowb + k0 * 2, 16 * n * rowb, x * pz);  // row t, columns k0 .. k0 + 3
+      buf_st4(dq_rs, r * rowb + k0 * 2, 16 * n * rowb, x);  // row t, columns k0 .. k0 + 3
     }
   }
   }
@@ -796,7 +805,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     const bf16* dvs = dVn + cb * (CH * D);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if (ready)
+      if (stale)
+        st8(dVs + 512 * (4 * i + wave) + 8 * lane, cvt8(f32x8{NAN, NAN, NAN, NAN, NAN, NAN, NAN, NAN}));
+      else if (ready)
         dma16_sc1(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
       else
         dma16(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
@@ -1076,7 +1087,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         const int s = 16 * n + r;
         const f32x4 vv = cvtf4(ld4(Vs + s * LDK + 16 * m + 4 * q4));
         colB[n] += acc[n][0] * vv[0] + acc[n][1] * vv[1] + acc[n][2] * vv[2] + acc[n][3] * vv[3];
-        buf_st4(dv_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, acc[n] * (Bs[s] * pz));  // row s
+        buf_st4(dv_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, acc[n] * Bs[s]);  // row s
       }
     }
 #pragma unroll
@@ -1159,7 +1170,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       const int m = 2 * wave + mm;
       const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
       const f32x4 out = normalize ? (dkr[mm][n] - kk * dot) * rsn[n] : dkr[mm][n];
-      buf_st4(dk_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, out * pz);  // row t
+      buf_st4(dk_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, out);  // row t
     }
   }
   if (tid < 64) {
@@ -1172,8 +1183,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       if (t + off < 64) x += o;
     }
     if (in) {
-      dg[(size_t)(ci.start + t) * H + h] = x * pz;
-      dbeta[(size_t)(ci.start + t) * H + h] = (dbw[t] + dbw[64 + t] + dbw[128 + t] + dbw[192 + t]) * pz;
+      dg[(size_t)(ci.start + t) * H + h] = x;
+      dbeta[(size_t)(ci.start + t) * H + h] = dbw[t] + dbw[64 + t] + dbw[128 + t] + dbw[192 + t];
     }
   }
 }
@@ -1223,7 +1234,8 @@ hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
       TimedLaunch tl(K_BWD_DKW, a.side);
       hipLaunchKernelGGL(bwd_dkw_kernel, grid_p, dim3(256), 0, a.side, a.q, a.k, Ff(F_RQ), Ff(F_RK), Ff(F_GC),
                          F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.v, a.beta, F(F_TM), a.chunks, a.H, a.scale,
-                         (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta, (const int*)ready);
+                         (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta, (const int*)ready,
+                         a.dkw_never_ready ? D / 16 + 1 : D / 16, a.dkw_never_ready ? 4 : COUNT_SPIN_LIMIT);
     }
     if (const hipError_t e = hipEventRecord(a.side_join, a.side)) return e;
     return hipStreamWaitEvent(stream, a.side_join, 0);
@@ -1233,7 +1245,7 @@ hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
   TimedLaunch tl(K_BWD_DKW, stream);
   hipLaunchKernelGGL(bwd_dkw_kernel, grid_p, dim3(256), 0, stream, a.q, a.k, Ff(F_RQ), Ff(F_RK), Ff(F_GC),
                      F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.v, a.beta, F(F_TM), a.chunks, a.H, a.scale,
-                     (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta, (const int*)nullptr);
+                     (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta, (const int*)nullptr, 0, 0);
   return hipSuccess;
 }
 

@@ -549,8 +549,8 @@ __device__ __forceinline__ int count_read(const int* p) {
 // COUNT_SPIN_LIMIT polls (about a second), so a hand-off that never comes ends
 // the waiting kernel with poisoned results instead of hanging it.
 constexpr int COUNT_SPIN_LIMIT = 1 << 18;
-__device__ __forceinline__ bool count_wait_ge(const int* p, int target) {
-  for (int i = 0; i < COUNT_SPIN_LIMIT; ++i) {
+__device__ __forceinline__ bool count_wait_ge(const int* p, int target, int limit = COUNT_SPIN_LIMIT) {
+  for (int i = 0; i < limit; ++i) {
     if (count_read(p) >= target) return true;
     __builtin_amdgcn_s_sleep(127);
   }

@@ -51,6 +51,9 @@ struct BwdArgs {
   // on the caller's stream behind bwd_local; side_join is recorded behind it)
   hipStream_t side;
   hipEvent_t side_fork, side_join;
+  // failure-handling tests only: bwd_dkw beside the scan waits for a count the scan
+  // never reaches, with a short poll limit, so every chunk's wait gives up
+  bool dkw_never_ready;
 };
 
 // Both return the first error of their stream-ordering calls (hipSuccess without them);

@@ -550,6 +550,27 @@ def test_bwd_dkw_beside_scan_matches_after_scan(gdn, kind, monkeypatch):
             assert_close_bf16(name, x, r)
 
 
+def test_bwd_dkw_wait_gives_up_with_nan_not_a_hang(gdn, monkeypatch):
+    """bwd_dkw's wait for a chunk of the reverse scan is bounded.  CQGDN_TEST_DKW_GIVE_UP=1 (failure
+    tests only) makes every chunk wait for a count the scan never reaches, four polls long: the call
+    still ends, the gradients that depend on the scan's dS and dV_new (dk, dv, dg, dbeta) are NaN in
+    every element, and dq, which does not, equals the normal call's bitwise."""
+    from cqgdn import synthetic
+
+    H = 16
+    T, mask, bounds = synthetic.config_events(2, seed=0)
+    print(f"case bwd_dkw wait give-up, config 2 T={T}", flush=True)
+    xs = inputs(T, H, seed=25, readonly=mask)
+    do = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(26)).bfloat16()
+    good, _, _ = _bwd_direct(gdn, xs, bounds, do, True, monkeypatch)
+    monkeypatch.setenv("CQGDN_TEST_DKW_GIVE_UP", "1")
+    bad, ready, resident = _bwd_direct(gdn, xs, bounds, do, True, monkeypatch)
+    assert bool((ready == 8).all()) and resident == H * 8  # the scan itself ran and announced every chunk
+    assert torch.equal(bad[0], good[0]), "dq"
+    for name, x in zip(("dk", "dv", "dg", "dbeta"), bad[1:]):
+        assert bool(torch.isnan(x.float()).all()), name
+
+
 def test_bwd_beside_scan_graph_replay(gdn):
     """The cached backward with bwd_dkw beside the reverse scan (second stream, fork and join events,
     the counts zeroed by bwd_local inside the call) captured in a HIP graph: each replay, with eager
