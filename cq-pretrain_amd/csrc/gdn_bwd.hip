@@ -1196,7 +1196,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 // still waits for.  Bounded: after COUNT_SPIN_LIMIT polls it ends anyway, and
 // bwd_dkw's own bounded waits then decide.
 __global__ __launch_bounds__(64) void scan_resident_gate_kernel(const int* __restrict__ resident, int expected) {
-  if (threadIdx.x == 0) count_wait_ge(resident, expected);
+  if (threadIdx.x == 0) count_wait_ge<4>(resident, expected, COUNT_SPIN_LIMIT * 4);  // one wave: polls fast
 }
 
 static void launch_resident_gate(const int* resident, int expected, hipStream_t stream) {

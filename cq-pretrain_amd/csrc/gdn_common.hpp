@@ -545,14 +545,16 @@ __device__ __forceinline__ int count_read(const int* p) {
 }
 // Poll *p until it reaches target, sleeping about 8,000 cycles (a few
 // microseconds) between polls: hundreds of waiting workgroups polling a few
-// lines faster than that slow the scan they wait for.  Bounded: false after
-// COUNT_SPIN_LIMIT polls (about a second), so a hand-off that never comes ends
-// the waiting kernel with poisoned results instead of hanging it.
+// lines faster than that slow the scan they wait for (a lone waiter may poll
+// faster: SLEEP is s_sleep's argument, in units of 64 cycles).  Bounded: false
+// after `limit` polls (COUNT_SPIN_LIMIT: about a second), so a hand-off that
+// never comes ends the waiting kernel with poisoned results instead of hanging it.
 constexpr int COUNT_SPIN_LIMIT = 1 << 18;
+template <int SLEEP = 127>
 __device__ __forceinline__ bool count_wait_ge(const int* p, int target, int limit = COUNT_SPIN_LIMIT) {
   for (int i = 0; i < limit; ++i) {
     if (count_read(p) >= target) return true;
-    __builtin_amdgcn_s_sleep(127);
+    __builtin_amdgcn_s_sleep(SLEEP);
   }
   return false;
 }
