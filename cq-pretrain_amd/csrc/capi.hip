@@ -115,8 +115,9 @@ constexpr int kBesideMinChunks = 64;
 // The side stream for a kernel beside a state scan, or null (*out) when that kernel
 // runs after the scan: each scan workgroup (one per head, 16-wide value slice and
 // document) holds a whole CU, and the kernel beside waits for the scan's chunks,
-// so every scan workgroup must be resident at once; `env` = "0" in the
-// environment keeps the kernel after the scan.
+// so every scan workgroup must be resident at once, leaving at least half of the
+// CUs to the kernel beside; `env` = "0" in the environment keeps the kernel after
+// the scan.
 int side_beside_scan(const char* env, int64_t T, int H, int64_t n_chunks, int n_docs, ScanSide** out) {
   *out = nullptr;
   const char* e = getenv(env);
@@ -126,7 +127,7 @@ int side_beside_scan(const char* env, int64_t T, int H, int64_t n_chunks, int n_
   if (n_chunks < (int64_t)kBesideMinChunks * n_docs) return CQGDN_OK;
   ScanSide* side = nullptr;
   if (const int err = scan_side(&side)) return err;
-  if ((int64_t)H * 8 * n_docs <= side->cus) *out = side;
+  if ((int64_t)H * 8 * n_docs * 2 <= side->cus) *out = side;
   return CQGDN_OK;
 }
 

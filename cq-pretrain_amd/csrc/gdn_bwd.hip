@@ -630,9 +630,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 
   // ---- phase 1: P, dP over the ten causal (t-tile, s-tile) pairs: wave w takes t-tile w with
   //      s-tiles 0 .. min(w, 2) and wave 0 also the (3, 3) diagonal, at most three pairs a wave ----
+  // The gates Gam[t][s] of this wave's pairs stay in registers for the wy phase 3, which
+  // takes the same pairs in the same fragment layout: gk[n] for s-tile n of t-tile wave,
+  // gk[3] for wave 0's (3, 3) tile.
+  f32x4 gk[4];
   {
     // dPm of t-tile tt, s-tile n; its row sums are added to rowE, its column sums to dgl
-    auto pair = [&](int tt, int n, float(&rowE)[4]) -> f32x4 {
+    auto pair = [&](int tt, int n, float(&rowE)[4], f32x4& gout) -> f32x4 {
       f32x4 p = zero4(), dp = zero4();
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
@@ -648,6 +652,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       for (int i = 0; i < 4; ++i) {
         const int t = 16 * tt + 4 * q4 + i;
         const float gam = (s <= t) ? __expf(g4[i] - gs) : 0.f;
+        gout[i] = gam;
         dpm[i] = scale * dp[i] * gam;
         const float e = dpm[i] * p[i];
         rowE[i] += e;
@@ -661,7 +666,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       if (n == 3 && wave == 3) continue;  // the (3, 3) tile is wave 0's
-      const f32x4 dpm = (n <= wave) ? pair(wave, n, rowE) : zero4();
+      const f32x4 dpm = (n <= wave) ? pair(wave, n, rowE, gk[n]) : zero4();
       st4(dPm + (16 * n + r) * LDT + 16 * wave + 4 * q4, dpm);  // transposed: dPm^T[s][t], 4 rows t in 8 bytes
     }
     sum16x4(rowE);
@@ -670,7 +675,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       if (r == 0) dgl[16 * wave + 4 * q4 + i] += rowE[i];
     if (wave == 0) {
       float rowE3[4] = {0.f, 0.f, 0.f, 0.f};
-      st4(dPm + (48 + r) * LDT + 48 + 4 * q4, pair(3, 3, rowE3));
+      st4(dPm + (48 + r) * LDT + 48 + 4 * q4, pair(3, 3, rowE3, gk[3]));
       sum16x4(rowE3);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -989,9 +994,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   // ---- wy phase 3: dA = -T^T Y, dM, dbeta and dG from A, over the causal (i-tile, j-tile) pairs
   //      shared out as in phase 1 ----
   {
-    // (beta dM)^T of i-tile it, j-tile n (at, ak: T^T and K fragments of i-tile it)
-    auto pair = [&](int it, int n, const bf16x8(&at)[2], const bf16x8(&ak)[4], float(&rowB)[4],
-                    float(&rowE)[4]) -> f32x4 {
+    // (beta dM)^T of i-tile it, j-tile n (at, ak: T^T and K fragments of i-tile it; gam: the
+    // tile's gates from phase 1, whose diagonal 1 is masked here by dA's strict mask)
+    auto pair = [&](int it, int n, const bf16x8(&at)[2], const bf16x8(&ak)[4], const f32x4& gam,
+                    float(&rowB)[4], float(&rowE)[4]) -> f32x4 {
       f32x4 da = zero4(), kk = zero4();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -999,19 +1005,16 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) kk = mfma(ak[kb], ld8(Ks + (16 * n + r) * LDK + 32 * kb + 8 * q4), kk);
       const int j = 16 * n + r;
-      const f32x4 g4 = *reinterpret_cast<const f32x4*>(&Gs[16 * it + 4 * q4]);
       const f32x4 b4 = *reinterpret_cast<const f32x4*>(&Bs[16 * it + 4 * q4]);
-      const float gj = Gs[j];
       float colE = 0.f;
       f32x4 dmp;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int i = 16 * it + 4 * q4 + e;
         const bool strict = j < i;
-        const float gam = strict ? __expf(g4[e] - gj) : 0.f;
         const float dA = strict ? -da[e] : 0.f;
-        const float dM = dA * gam;
-        const float Aij = b4[e] * kk[e] * gam;
+        const float dM = dA * gam[e];
+        const float Aij = b4[e] * kk[e] * gam[e];
         dmp[e] = b4[e] * dM;
         rowB[e] += dM * kk[e];
         const float e2 = dA * Aij;
@@ -1044,7 +1047,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         if (n == 3 && wave == 3) continue;  // the (3, 3) tile is wave 0's
-        const f32x4 dmp = (n <= wave) ? pair(wave, n, at, ak, rowB, rowE) : zero4();
+        const f32x4 dmp = (n <= wave) ? pair(wave, n, at, ak, gk[n], rowB, rowE) : zero4();
         st4(S1 + (16 * n + r) * LDT + 16 * wave + 4 * q4, dmp);
       }
       rows(wave, rowB, rowE);
@@ -1056,7 +1059,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) ak[kb] = ld8(Ks + (48 + r) * LDK + 32 * kb + 8 * q4);
       float rowB[4] = {0.f, 0.f, 0.f, 0.f}, rowE[4] = {0.f, 0.f, 0.f, 0.f};
-      st4(S1 + (48 + r) * LDT + 48 + 4 * q4, pair(3, 3, at, ak, rowB, rowE));
+      st4(S1 + (48 + r) * LDT + 48 + 4 * q4, pair(3, 3, at, ak, gk[3], rowB, rowE));
       rows(3, rowB, rowE);
     }
   }
