@@ -444,11 +444,11 @@ def test_fused_mode_matches_cached_mode_at_config2_size(gdn, monkeypatch):
         assert torch.equal(a, b), name
 
 
-def test_bwd_recompute_graph_replay(gdn):
+@pytest.mark.parametrize("T,bounds,H", [(700, (0, 300, 700), 8), (4200, (0, 4200), 16)])
+def test_bwd_recompute_graph_replay(gdn, T, bounds, H):
     """cqgdn_bwd_recompute (the fused-mode backward: forward rebuilt in the call, its state scan on a
-    second stream joined back by events) captured in a HIP graph: each replay, with eager work
-    between, equals the eager call bitwise."""
-    T, bounds, H = 700, (0, 300, 700), 8
+    second stream joined back by events) captured in a HIP graph, at two sizes: each replay, with eager
+    work between, equals the eager call bitwise."""
     print(f"case bwd_recompute graph replay T={T} bounds={bounds} H={H}", flush=True)
     q, k, v, g, b = (x.to(DEV).contiguous() for x in inputs(T, H, seed=4242))
     dy = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(4243)).bfloat16().to(DEV)
