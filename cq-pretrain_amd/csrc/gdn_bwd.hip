@@ -20,6 +20,13 @@
 // prepare_wy_repr_bwd_da/_full, reverse_cumsum, l2_bwd) regrouped into three
 // kernels.  All reductions run in a fixed order (no atomics), so results are
 // bitwise reproducible from run to run.
+//
+// bwd_dkw may run on a second stream beside the reverse scan (launch_bwd): the
+// scan then stores each chunk's dS / dVn at device scope and announces the chunk
+// with an atomic count, and bwd_dkw takes the chunks in the order the scan
+// finishes them, each waiting (bounded) for its count.  The atomics only order
+// the hand-off; every value is computed as in the sequential order, so the
+// results are the same bits either way.
 #include "gdn_common.hpp"
 #include "gdn_layout.hpp"
 #include "gdn_kernels.hpp"
