@@ -82,11 +82,14 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def training_case(gdn, synthetic, torch, config, device):
+def training_case(gdn, synthetic, torch, config, device, fp16=False):
     T, mask, bounds = synthetic.config_events(config, seed=0)
     xs = [x.to(device) for x in synthetic.make_inputs(T, H, D, seed=config, readonly=mask)]
     gen = torch.Generator().manual_seed(100 + config)
     do = torch.randn(1, T, H, D, generator=gen).bfloat16().to(device)
+    if fp16:  # the reference's fp16 training inputs, on the fp16 kernels
+        xs = [x.half() if x.dim() == 4 else x for x in xs]
+        do = do.half()
     leaves = [x.requires_grad_() for x in xs]
     # packed documents (config 3) go in as cu_seqlens, one state reset per document
     packed = {}
@@ -551,6 +554,12 @@ def main():
         finally:
             gdn.MODE = "cached"
         del stepf
+        log("config 2 fwd+bwd, fp16 inputs (fp16 kernels)")
+        _, _, steph, _ = training_case(gdn, synthetic, torch, 2, device, fp16=True)
+        for _ in range(args.warmup):
+            steph()
+        extra["config2_fwd_bwd_ms_fp16"] = round(time_steps(torch, steph, args.steps) * 1e3, 4)
+        del steph
         log("whole GatedDelta layer, width 2048 (content 2048 and 8192, image-CQ plans)")
         log("layer decode step, width 2048 (N = 1 and 64 sequences)")
         extra["layer_decode_w2048"] = [layer_decode_case(torch, device, n) for n in (1, 64)]

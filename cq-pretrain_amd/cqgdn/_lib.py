@@ -21,11 +21,11 @@ LIB_PATH = Path(__file__).resolve().with_name("libcqgdn.so")
 OPS_PATH = LIB_PATH.with_name("libcqgdn_torch.so")
 
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
-NORMALIZE, TRAINING, PRECISE, NO_OUTPUT = 1, 2, 4, 8
+NORMALIZE, TRAINING, PRECISE, NO_OUTPUT, FP16 = 1, 2, 4, 8, 16
 STATIC_WORKSPACE_BYTES = 64 << 20  # CQGDN_STATIC_WORKSPACE_BYTES
-FWD_BUFFERS, BWD_BUFFERS = 10, 7
+FWD_BUFFERS, BWD_BUFFERS = 10, 8
 FWD_NAMES = ("rq", "rk", "gcum", "T", "W", "UT", "KgT", "hT", "vnT", "vscale")
-BWD_NAMES = ("dvlT", "XT", "dh", "dVn", "knP", "WT", "sync")
+BWD_NAMES = ("dvlT", "XT", "dh", "dVn", "knP", "WT", "sync", "dscale")
 
 # every symbol include/cqgdn.h declares, with (restype, argtypes)
 _P, _I, _I64, _U, _F, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_uint, ctypes.c_float, ctypes.c_size_t

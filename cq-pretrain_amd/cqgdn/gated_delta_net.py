@@ -235,14 +235,15 @@ def _as(x, dtype):
 
 
 def _flatten(q, k, v, g, beta, bounds):
-    """Packed [1,T,...] views; unpacked batches become one document per row.  q, k, v in bf16, the
-    kernels' operand type (fp16 inputs are rounded to it: bf16 keeps every fp16 magnitude in range)."""
+    """Packed [1,T,...] views; unpacked batches become one document per row.  q, k, v keep their
+    dtype, bf16 or fp16 (one for all three): the kernels compute with operands of that type."""
     b, t = q.shape[0], q.shape[1]
     if bounds is None:
         bounds = tuple(range(0, b * t + 1, t)) if t > 0 else (0,) * (b + 1)
     if b != 1:
         q, k, v, g, beta = (x.reshape(1, b * t, *x.shape[2:]) for x in (q, k, v, g, beta))
-    q, k, v = (_as(x, torch.bfloat16) for x in (q, k, v))
+    dt = q.dtype if q.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
+    q, k, v = (_as(x, dt) for x in (q, k, v))
     g, beta = (_as(x, torch.float32) for x in (g, beta))
     return q, k, v, g, beta, bounds
 
@@ -327,8 +328,9 @@ def delta(
     q, k, v: [B,T,H,128] bf16 or fp16 time-first; g, beta: [B,T,H] (computed in fp32).
     Packed documents: B == 1 with ``cu_seqlens`` (device) and ``cu_seqlens_cpu``
     (host) bounds; the state resets at each document.  Returns ``(o, None)``, o and the
-    gradients in the input dtypes.  The kernels' MFMA operands are bf16 either way (fp16
-    inputs are rounded to bf16 once, which keeps every value's range).
+    gradients in the input dtypes.  The kernels' MFMA operands take the inputs' type: fp16
+    inputs run the fp16 kernels (CQGDN_FP16), with V and dO scaled by powers of two inside the
+    calls so that every fp16 operand stays in range.
     """
     if initial_state is not None or output_final_state:
         raise NotImplementedError("This training adapter requires zero initial state and no state output")
@@ -361,7 +363,7 @@ def prefill(q, k, v, g, beta, bounds, initial_state=None):
     Runs the precise forward (fp16 MFMA operands, CQGDN_PRECISE), whose final states
     stay within 1e-3 relative of an fp32 computation.
     q, k, v: [1,T,H,128] bf16 or fp16 (l2norm applied inside, scale 128^-0.5); g, beta [1,T,H].
-    fp16 values are rounded to bf16 once at the boundary, as in ``delta``.
+    fp16 inputs are read as fp16 (CQGDN_FP16), bf16 inputs are rounded to fp16 operands.
     Returns ``(o [1,T,H,128] time-first in the dtype of q, state [n_docs,H,K,V] fp32)``.
     """
     bounds = tuple(int(b) for b in bounds)

@@ -253,7 +253,7 @@ int fwd_impl(const void* q, const void* k, const void* v, const float* g, const 
              size_t workspace_bytes, void* stream, hipStream_t scan_stream, hipEvent_t scan_fork,
              hipEvent_t scan_join) {
   if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
-  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING | CQGDN_PRECISE | CQGDN_NO_OUTPUT))
+  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING | CQGDN_PRECISE | CQGDN_NO_OUTPUT | CQGDN_FP16))
     return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
   if ((flags & CQGDN_NO_OUTPUT) && !(flags & CQGDN_TRAINING))
     return fail(CQGDN_EINVAL, "CQGDN_NO_OUTPUT rebuilds a training workspace: it needs CQGDN_TRAINING");
@@ -279,9 +279,9 @@ int fwd_impl(const void* q, const void* k, const void* v, const float* g, const 
   for (const void* p : {q, k, v, (const void*)o})
     if (p && !aligned(p, 16)) return fail(CQGDN_EINVAL, "q/k/v/o must be 16-byte aligned");
   FwdArgs a{};
-  a.q = static_cast<const bf16*>(q);
-  a.k = static_cast<const bf16*>(k);
-  a.v = static_cast<const bf16*>(v);
+  a.q = q;
+  a.k = k;
+  a.v = v;
   a.g = g;
   a.beta = beta;
   a.chunks = chunk_table;
@@ -293,10 +293,12 @@ int fwd_impl(const void* q, const void* k, const void* v, const float* g, const 
   a.scale = scale;
   a.normalize = (flags & CQGDN_NORMALIZE) != 0;
   a.precise = (flags & CQGDN_PRECISE) != 0;
+  a.fp16 = (flags & CQGDN_FP16) != 0;
+  a.training = (flags & CQGDN_TRAINING) != 0;
   a.no_output = (flags & CQGDN_NO_OUTPUT) != 0;
   a.initial_state = initial_state;
   a.final_state = final_state;
-  a.o = static_cast<bf16*>(o);
+  a.o = o;
   a.ws = static_cast<uint8_t*>(workspace);
   cqgdn_fwd_buffer_offsets(T, H, n_chunks, a.off, F_COUNT);
   a.scan_stream = scan_stream;
@@ -317,7 +319,7 @@ int bwd_impl(const void* q, const void* k, const void* v, const float* g, const 
              bool launch, hipEvent_t dkw_after, hipStream_t side = nullptr, hipEvent_t side_fork = nullptr,
              hipEvent_t side_join = nullptr) {
   if (const int e = check_common(T, H, n_chunks, n_docs, chunk_table, doc_chunk)) return e;
-  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING)) return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
+  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING | CQGDN_FP16)) return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
   if (T == 0) return ok();
   if (!q || !k || !v || !g || !beta || !dout || !fwd_workspace || !bwd_workspace || !dq || !dk || !dv || !dg ||
       !dbeta)
@@ -331,10 +333,10 @@ int bwd_impl(const void* q, const void* k, const void* v, const float* g, const 
     if (!aligned(p, 16)) return fail(CQGDN_EINVAL, "q/k/v/do/dq/dk/dv must be 16-byte aligned");
   if (!launch) return ok();
   BwdArgs a{};
-  a.q = static_cast<const bf16*>(q);
-  a.k = static_cast<const bf16*>(k);
-  a.v = static_cast<const bf16*>(v);
-  a.dout = static_cast<const bf16*>(dout);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dout = dout;
   a.g = g;
   a.beta = beta;
   a.chunks = chunk_table;
@@ -345,13 +347,14 @@ int bwd_impl(const void* q, const void* k, const void* v, const float* g, const 
   a.n_docs = n_docs;
   a.scale = scale;
   a.normalize = (flags & CQGDN_NORMALIZE) != 0;
+  a.fp16 = (flags & CQGDN_FP16) != 0;
   a.fws = static_cast<const uint8_t*>(fwd_workspace);
   a.bws = static_cast<uint8_t*>(bwd_workspace);
   cqgdn_fwd_buffer_offsets(T, H, n_chunks, a.foff, F_COUNT);
   cqgdn_bwd_buffer_offsets(T, H, n_chunks, a.boff, B_COUNT);
-  a.dq = static_cast<bf16*>(dq);
-  a.dk = static_cast<bf16*>(dk);
-  a.dv = static_cast<bf16*>(dv);
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
   a.dg = dg;
   a.dbeta = dbeta;
   a.dkw_after = dkw_after;
@@ -395,7 +398,8 @@ int cqgdn_bwd_recompute(const void* q, const void* k, const void* v, const float
                         const int32_t* doc_chunk, int n_docs, float scale, unsigned flags, void* fwd_workspace,
                         size_t fwd_workspace_bytes, void* bwd_workspace, size_t bwd_workspace_bytes, void* dq,
                         void* dk, void* dv, float* dg, float* dbeta, void* stream) {
-  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING)) return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
+  if (flags & ~(CQGDN_NORMALIZE | CQGDN_TRAINING | CQGDN_FP16))
+    return fail(CQGDN_EINVAL, "unknown flags 0x%x", flags);
   // every argument is checked before anything is launched
   if (const int e = bwd_impl(q, k, v, g, beta, dout, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, flags,
                              fwd_workspace, fwd_workspace_bytes, bwd_workspace, bwd_workspace_bytes, dq, dk, dv, dg,
@@ -404,7 +408,7 @@ int cqgdn_bwd_recompute(const void* q, const void* k, const void* v, const float
   if (T == 0) return ok();
   ScanSide* side = nullptr;
   if (const int e = scan_side(&side)) return e;
-  const unsigned fflags = (flags & CQGDN_NORMALIZE) | CQGDN_TRAINING | CQGDN_NO_OUTPUT;
+  const unsigned fflags = (flags & (CQGDN_NORMALIZE | CQGDN_FP16)) | CQGDN_TRAINING | CQGDN_NO_OUTPUT;
   if (const int e = fwd_impl(q, k, v, g, beta, T, H, chunk_table, n_chunks, doc_chunk, n_docs, scale, fflags, nullptr,
                              nullptr, nullptr, fwd_workspace, fwd_workspace_bytes, stream, side->stream, side->fork,
                              side->join))

@@ -21,6 +21,15 @@
 // kernels.  All reductions run in a fixed order (no atomics), so results are
 // bitwise reproducible from run to run.
 //
+// E is the operand type: bf16, or fp16 for fp16 inputs.  In fp16 every quantity is
+// carried in exact power-of-two scales that keep it inside fp16's range: the
+// forward's scale s_v of V (h and v_new carry it; the V rows read here are scaled
+// by it too) and the scale s_d of dO.  s_d brings max|dO| below 2^e with
+// T 2^e <= 2^15: with unit-norm q rows a state gradient satisfies |dS| <= T max|dO|,
+// so dS and dVn stay below about 2^15.  dv_local, X, dS, dVn and dv carry s_d; dP,
+// dW, dT, dA, dq, dk, dg and dbeta carry s_d s_v.  Each output is divided by its
+// scale in fp32 before it is stored.
+//
 // bwd_dkw may run on a second stream beside the reverse scan (launch_bwd): the
 // scan then stores each chunk's dS / dVn at device scope and announces the chunk
 // with an atomic count, and bwd_dkw takes the chunks in the order the scan
@@ -39,12 +48,15 @@ constexpr int LDT = 72;   // bf16 row stride, 128 x 64 and 64 x 64 tiles
 // ---------------------------------------------------------------------------
 // bwd_local
 // ---------------------------------------------------------------------------
+template <class E>  // dscale: null in bf16; in fp16 the device scalar s_d
 __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ rq,
-    const float* __restrict__ rk, const bf16* __restrict__ dout, const float* __restrict__ gc,
-    const float* __restrict__ beta, const bf16* __restrict__ Tm,
-    const int32_t* __restrict__ chunks, int H, float scale, bf16* __restrict__ dvlT, bf16* __restrict__ XT,
-    bf16* __restrict__ knP, bf16* __restrict__ WT, int* __restrict__ sync) {
+    const E* __restrict__ q, const E* __restrict__ k, const float* __restrict__ rq,
+    const float* __restrict__ rk, const E* __restrict__ dout, const float* __restrict__ gc,
+    const float* __restrict__ beta, const E* __restrict__ Tm,
+    const int32_t* __restrict__ chunks, int H, float scale, const float* __restrict__ dscale,
+    E* __restrict__ dvlT, E* __restrict__ XT, E* __restrict__ knP, E* __restrict__ WT, int* __restrict__ sync) {
+  typedef typename Vec<E>::x8 X8;
+  constexpr bool F16 = __is_same(E, f16);
   // grid (H, NC), chunks dispatched first to last: the reverse state scan that
   // follows reads the last chunks first, and they are then the most recently
   // written (still in the memory-side cache).  The scan's other two operands,
@@ -65,16 +77,16 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
   // 52 KB, so three workgroups share a CU.  The outputs are staged over them
   // once they are read and stored as whole rows: X^T over Qs | Ks, dv_local^T
   // (64-element rows, 16-byte columns XOR-swizzled by row) over dOs.
-  __shared__ __attribute__((aligned(16))) bf16 QK[2 * 64 * LDK];  // Qs | Ks, then X^T [v][k]
-  __shared__ __attribute__((aligned(16))) bf16 dOs[64 * LDK];     // dO rows, then dv_local^T [v][s]
+  __shared__ __attribute__((aligned(16))) E QK[2 * 64 * LDK];  // Qs | Ks, then X^T [v][k]
+  __shared__ __attribute__((aligned(16))) E dOs[64 * LDK];     // dO rows, then dv_local^T [v][s]
   __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ __attribute__((aligned(16))) float Bs[64];
-  bf16* Qs = QK;
-  bf16* Ks = QK + 64 * LDK;
+  E* Qs = QK;
+  E* Ks = QK + 64 * LDK;
   static_assert(64 * LDK >= 128 * 64, "dv_local^T fits the dO tile");
 
   // T rows t = 16 wave + r, for -W^T below (requested with the inputs)
-  bf16x8 at[2];
+  X8 at[2];
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) at[kb] = ld8(Tm + cb * (CH * CH) + (16 * wave + r) * CH + 32 * kb + 8 * q4);
   {
@@ -86,7 +98,7 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
     // q and k non-temporally: what this kernel writes (the reverse scan's operands,
     // 188 MB at T = 9216, H = 16) and what the scan writes do not both fit the
     // 256 MB memory-side cache, and q, k are read next only by bwd_dkw, after the scan
-    bf16x8 xq[4], xk[4], xd[4];
+    X8 xq[4], xk[4], xd[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
@@ -98,11 +110,16 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
       Gs[t] = gc[ev];
       Bs[t] = keep_if(in, beta[ev]);
     }
+    if constexpr (F16) {  // dO s_d (exact: a power of two, in range)
+      const float ds = *dscale;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xd[j] = to8<E>(cvtf8(xd[j]) * ds);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      st8(Qs + t * LDK + col, keep_if(in, scaled8<bf16>(xq[j], rqt)));
-      st8(Ks + t * LDK + col, keep_if(in, scaled8<bf16>(xk[j], rkt)));
+      st8(Qs + t * LDK + col, keep_if(in, scaled8<E>(xq[j], rqt)));
+      st8(Ks + t * LDK + col, keep_if(in, scaled8<E>(xk[j], rkt)));
       st8(dOs + t * LDK + col, keep_if(in, xd[j]));
     }
   }
@@ -115,11 +132,11 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
     const int t = tid >> 2, p = tid & 3;
     if (t < ci.len) {
       const float kd = __expf(Gs[ci.len - 1] - Gs[t]);
-      bf16* kp = knP + ((size_t)(ci.start + t) * H + h) * D + 8 * p;
+      E* kp = knP + ((size_t)(ci.start + t) * H + h) * D + 8 * p;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        st8(kp + 32 * j, cat(cvt4(cvtf4(ld4(Ks + t * LDK + 32 * j + 4 * p)) * kd),
-                             cvt4(cvtf4(ld4(Ks + t * LDK + 32 * j + 16 + 4 * p)) * kd)));
+        st8(kp + 32 * j, cat(to4<E>(cvtf4(ld4(Ks + t * LDK + 32 * j + 4 * p)) * kd),
+                             to4<E>(cvtf4(ld4(Ks + t * LDK + 32 * j + 16 + 4 * p)) * kd)));
     }
   }
 
@@ -137,14 +154,14 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
   // -W^T [k][perm32(t)] with W = T (beta gam K): t-tile = wave, k-tiles n; beta gam K
   // is read transposed from the K rows and scaled per event s on the way
   {
-    bf16* wt = WT + cb * (D * CH);
+    E* wt = WT + cb * (D * CH);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       f32x4 aw = zero4();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
         if (kb == 0 || wave >= 2)  // T[t][s] = 0 for s > t
-          aw = mfma(at[kb], cvt8(cvtf8(ld8_tr(Ks, LDK, 32 * kb, 16 * n)) * fbg[kb]), aw);
+          aw = mfma(at[kb], to8<E>(cvtf8(ld8_tr(Ks, LDK, 32 * kb, 16 * n)) * fbg[kb]), aw);
       st4(wt + (16 * n + r) * CH + perm32(16 * wave + 4 * q4), -aw);
     }
   }
@@ -175,9 +192,9 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
   f32x4 dvl[8];
   {
     const int kb0 = wave >= 2 ? 1 : 0;
-    bf16x8 a[2];
+    X8 a[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) a[kb] = pack_perm(pp[2 * kb], pp[2 * kb + 1]);
+    for (int kb = 0; kb < 2; ++kb) a[kb] = pack_permv<E>(pp[2 * kb], pp[2 * kb + 1]);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       dvl[n] = zero4();
@@ -191,9 +208,9 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm) {
     const int m = 2 * wave + mm;
-    bf16x8 a[2];
+    X8 a[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) a[kb] = cvt8(cvtf8(ld8_tr(Qs, LDK, 32 * kb, 16 * m)) * fg[kb]);
+    for (int kb = 0; kb < 2; ++kb) a[kb] = to8<E>(cvtf8(ld8_tr(Qs, LDK, 32 * kb, 16 * m)) * fg[kb]);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       xt[mm][n] = zero4();
@@ -202,8 +219,8 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
     }
   }
   __syncthreads();  // the input tiles are read: they take the output tiles
-  bf16* xts = QK;   // X^T [v][k], row stride LDK
-  bf16* dvs = dOs;  // dv_local^T [v][s], 64-element rows, 16-byte column c at c ^ (v & 7)
+  E* xts = QK;      // X^T [v][k], row stride LDK
+  E* dvs = dOs;     // dv_local^T [v][s], 64-element rows, 16-byte column c at c ^ (v & 7)
 #pragma unroll
   for (int n = 0; n < 8; ++n) {
     const int v = 16 * n + r, sc = 2 * wave + (q4 >> 1);
@@ -213,7 +230,7 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
   }
   __syncthreads();
   {
-    bf16* out = dvlT + cb * (D * CH);
+    E* out = dvlT + cb * (D * CH);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int seg = 256 * i + tid, v = seg >> 3, part = seg & 7;
@@ -221,7 +238,7 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
     }
   }
   {
-    bf16* out = XT + cb * (D * D);
+    E* out = XT + cb * (D * D);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int seg = 256 * i + tid, v = seg >> 4, part = seg & 15;
@@ -249,31 +266,37 @@ constexpr int BS_STAGES = 4;
 constexpr int BS_SROW = 136;
 constexpr int BS_VROW = 72;
 
+template <class E>
 struct __attribute__((aligned(16))) BwdStage {
-  bf16 kn[64 * 128];   // Kn rows t
-  bf16 wt[128 * 64];   // -W^T rows k
-  bf16 dvl[16 * 64];   // dv_local^T rows of the slice
-  bf16 xt[16 * 128];   // X^T rows of the slice
-  float glast;         // G of the chunk's last event
+  E kn[64 * 128];   // Kn rows t
+  E wt[128 * 64];   // -W^T rows k
+  E dvl[16 * 64];   // dv_local^T rows of the slice
+  E xt[16 * 128];   // X^T rows of the slice
+  float glast;      // G of the chunk's last event
   float pad[3];
 };
 
+template <class E>
 struct __attribute__((aligned(16))) BwdScratch {
-  bf16 s[16 * BS_SROW];  // dS_{c+1}, [v][k]
-  bf16 v[16 * BS_VROW];  // dVn, [v][t]
+  E s[16 * BS_SROW];  // dS_{c+1}, [v][k]
+  E v[16 * BS_VROW];  // dVn, [v][t]
 };
-static_assert(sizeof(BwdScratch) <= 128 * 64 * sizeof(bf16), "scratch must fit the -W^T region");
-__device__ __forceinline__ BwdScratch& bwd_scratch(BwdStage& st) { return *reinterpret_cast<BwdScratch*>(st.wt); }
+static_assert(sizeof(BwdScratch<bf16>) <= 128 * 64 * sizeof(bf16), "scratch must fit the -W^T region");
+template <class E>
+__device__ __forceinline__ BwdScratch<E>& bwd_scratch(BwdStage<E>& st) {
+  return *reinterpret_cast<BwdScratch<E>*>(st.wt);
+}
 
 // Issue part `part` of the asynchronous copies of chunk c into stage S (no
 // wait on memory here): part 0 kdec Kn, G_last and the X^T slice (21 copies),
 // part 1 (loader 1, which also stores the outputs) -W^T and the dv_local^T
 // slice (18 copies).
 constexpr int BWD_PART_COPIES[2] = {21, 18};
-__device__ __forceinline__ void bwd_issue(BwdStage& S, const int32_t* __restrict__ chunks, int c, int H, int h,
-                                          int v0, int lane, int part, const bf16* __restrict__ knP,
-                                          const float* __restrict__ gc, const bf16* __restrict__ dvlT,
-                                          const bf16* __restrict__ XT, const bf16* __restrict__ WT) {
+template <class E>
+__device__ __forceinline__ void bwd_issue(BwdStage<E>& S, const int32_t* __restrict__ chunks, int c, int H, int h,
+                                          int v0, int lane, int part, const E* __restrict__ knP,
+                                          const float* __restrict__ gc, const E* __restrict__ dvlT,
+                                          const E* __restrict__ XT, const E* __restrict__ WT) {
   const ChunkInfo ci = chunk_info(chunks, c);
   const size_t cb = (size_t)c * H + h;
   if (part == 0) {
@@ -286,20 +309,20 @@ __device__ __forceinline__ void bwd_issue(BwdStage& S, const int32_t* __restrict
     if (lane == 0)  // one lane: a dword copy writes 4 bytes per active lane
       __builtin_amdgcn_global_load_lds(gc + (size_t)(ci.start + ci.len - 1) * H + h, (lds_void_ptr)&S.glast, 4, 0,
                                        0);
-    const bf16* xt = XT + cb * (D * D) + v0 * D;
+    const E* xt = XT + cb * (D * D) + v0 * D;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int v = 4 * i + (lane >> 4), col = (lane & 15) ^ (v & 15);
       dma16(xt + v * D + 8 * col, S.xt + 512 * i);
     }
   } else {
-    const bf16* wt = WT + cb * (D * CH);
+    const E* wt = WT + cb * (D * CH);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int k = 8 * i + (lane >> 3), col = (lane & 7) ^ ((k >> 1) & 7);
       dma16(wt + k * CH + 8 * col, S.wt + 512 * i);
     }
-    const bf16* dvl = dvlT + cb * (D * CH) + v0 * CH;
+    const E* dvl = dvlT + cb * (D * CH) + v0 * CH;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int v = 8 * i + (lane >> 3), col = (lane & 7) ^ ((v >> 1) & 7);
@@ -308,13 +331,14 @@ __device__ __forceinline__ void bwd_issue(BwdStage& S, const int32_t* __restrict
   }
 }
 
-__device__ __forceinline__ void bwd_fix_tail(BwdStage& S, const int32_t* __restrict__ chunks, int c, int lane) {
+template <class E>
+__device__ __forceinline__ void bwd_fix_tail(BwdStage<E>& S, const int32_t* __restrict__ chunks, int c, int lane) {
   const int len = chunk_info(chunks, c).len;
   if (len < CH) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int t = 4 * i + (lane >> 4);
-      if (t >= len) st8(S.kn + t * 128 + 8 * (lane & 15), zero8());
+      if (t >= len) st8(S.kn + t * 128 + 8 * (lane & 15), zero8v<E>());
     }
   }
 }
@@ -329,13 +353,13 @@ constexpr int BWD_OUT_STORES = 6;
 // them first to last, so they are the oldest in the memory-side cache).  With
 // bwd_dkw beside the scan (SC1) the stores are device-scope: bwd_dkw reads them
 // while the scan runs.
-template <bool SC1>
-__device__ __forceinline__ void bwd_copy_out(const BwdScratch& sc, int c, int H, int h, int slice, int lane,
-                                             bf16* __restrict__ dhS, bf16* __restrict__ dVnS) {
+template <bool SC1, class E>
+__device__ __forceinline__ void bwd_copy_out(const BwdScratch<E>& sc, int c, int H, int h, int slice, int lane,
+                                             E* __restrict__ dhS, E* __restrict__ dVnS) {
   const size_t cb = (size_t)c * H + h;
   const int r = lane & 15, q4 = lane >> 4, half = 8 * (q4 & 1), row = 16 * (q4 >> 1) + r;
-  bf16* ds = dhS + cb * (D * D) + slice * (D * 16);
-  bf16* vs = dVnS + cb * (CH * D) + slice * (CH * 16);
+  E* ds = dhS + cb * (D * D) + slice * (D * 16);
+  E* vs = dVnS + cb * (CH * D) + slice * (CH * 16);
   if constexpr (SC1) {
     const __amdgpu_buffer_rsrc_t dr = buf_rsrc(ds, D * 16 * 2), vr = buf_rsrc(vs, CH * 16 * 2);
 #pragma unroll
@@ -358,20 +382,23 @@ __device__ __forceinline__ void bwd_publish(int* __restrict__ ready, int c, int 
   asm volatile("" ::: "memory");
 }
 
+template <class E>
 __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
-    const bf16* __restrict__ knP, const float* __restrict__ gc, const bf16* __restrict__ dvlT,
-    const bf16* __restrict__ XT, const bf16* __restrict__ WT, const int32_t* __restrict__ chunks,
-    const int32_t* __restrict__ doc_chunk, int H, bf16* __restrict__ dhS, bf16* __restrict__ dVnS,
+    const E* __restrict__ knP, const float* __restrict__ gc, const E* __restrict__ dvlT,
+    const E* __restrict__ XT, const E* __restrict__ WT, const int32_t* __restrict__ chunks,
+    const int32_t* __restrict__ doc_chunk, int H, E* __restrict__ dhS, E* __restrict__ dVnS,
     int* __restrict__ ready, int* __restrict__ resident) {
   // ready / resident: null, or the hand-off counts of a bwd_dkw running beside this
   // scan (each workgroup adds one to resident when it starts, and one to a chunk's
   // ready count once its outputs of that chunk are stored)
+  typedef typename Vec<E>::x8 X8;
+  typedef typename Vec<E>::x4 X4;
   const int h = blockIdx.x % H, slice = blockIdx.x / H, d = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const int v0 = 16 * slice;
 
-  __shared__ BwdStage stage[BS_STAGES];
+  __shared__ BwdStage<E> stage[BS_STAGES];
 
   const int c_end = doc_chunk[d + 1], n = c_end - doc_chunk[d];
   // step tau handles chunk c_end - 1 - tau (chunks in reverse)
@@ -393,39 +420,39 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
     for (int tau = -BS_DEPTH; tau < n; ++tau) {
       if (tau >= 0) {
         char* base = reinterpret_cast<char*>(&stage[tau & (BS_STAGES - 1)]);
-        const char* knb = base + offsetof(BwdStage, kn);
-        const char* wtb = base + offsetof(BwdStage, wt);
-        const char* dvb = base + offsetof(BwdStage, dvl);
-        const char* xtb = base + offsetof(BwdStage, xt);
+        const char* knb = base + offsetof(BwdStage<E>, kn);
+        const char* wtb = base + offsetof(BwdStage<E>, wt);
+        const char* dvb = base + offsetof(BwdStage<E>, dvl);
+        const char* xtb = base + offsetof(BwdStage<E>, xt);
         // every operand read is issued ahead of the MFMAs that use them (the
         // kdec Kn fragments first); the scheduling barriers keep the compiler
         // from interleaving them one by one
-        bf16x8 fk[4][4], fw[8][2];
+        X8 fk[4][4], fw[8][2];
         f32x4 xv[8];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int i4 = 0; i4 < 4; ++i4) fk[i4][j] = *reinterpret_cast<const bf16x8*>(knb + kofs[j] + 4096 * i4);
+          for (int i4 = 0; i4 < 4; ++i4) fk[i4][j] = *reinterpret_cast<const X8*>(knb + kofs[j] + 4096 * i4);
         // dVn = dv_local + (kdec Kn) dS_{c+1}, accumulated onto dv_local
         f32x4 dv[4];
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) dv[i4] = cvtf4(*reinterpret_cast<const bf16x4*>(dvb + dofs[i4]));
-        const float glast = reinterpret_cast<const BwdStage*>(base)->glast;
+        for (int i4 = 0; i4 < 4; ++i4) dv[i4] = cvtf4(*reinterpret_cast<const X4*>(dvb + dofs[i4]));
+        const float glast = reinterpret_cast<const BwdStage<E>*>(base)->glast;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int m = 0; m < 8; ++m) fw[m][j] = *reinterpret_cast<const bf16x8*>(wtb + wofs[j] + 2048 * m);
+          for (int m = 0; m < 8; ++m) fw[m][j] = *reinterpret_cast<const X8*>(wtb + wofs[j] + 2048 * m);
 #pragma unroll
-        for (int m = 0; m < 8; ++m) xv[m] = cvtf4(*reinterpret_cast<const bf16x4*>(xtb + xofs[m]));
+        for (int m = 0; m < 8; ++m) xv[m] = cvtf4(*reinterpret_cast<const X4*>(xtb + xofs[m]));
         __builtin_amdgcn_sched_barrier(0);
-        bf16x4 sh[8];
+        X4 sh[8];
 #pragma unroll
-        for (int m = 0; m < 8; ++m) sh[m] = cvt4(dS[m]);
+        for (int m = 0; m < 8; ++m) sh[m] = to4<E>(dS[m]);
         // beside it, the first two terms of dS_c = exp(G_last) dS_{c+1} + X + (-W^T) dVn
         const float gC = __expf(glast);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const bf16x8 sb = cat(sh[2 * j], sh[2 * j + 1]);
+          const X8 sb = cat(sh[2 * j], sh[2 * j + 1]);
 #pragma unroll
           for (int i4 = 0; i4 < 4; ++i4) dv[i4] = mfma(fk[i4][j], sb, dv[i4]);
 #pragma unroll
@@ -434,18 +461,18 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
         __builtin_amdgcn_sched_barrier(0);
         // the -W^T fragments have been read (a wave's LDS operations complete in
         // order): the -W^T region now takes this step's outputs
-        char* sb = base + offsetof(BwdStage, wt);
+        char* sb = base + offsetof(BwdStage<E>, wt);
 #pragma unroll
-        for (int m = 0; m < 8; ++m) *reinterpret_cast<bf16x4*>(sb + sofs + 32 * m) = sh[m];
+        for (int m = 0; m < 8; ++m) *reinterpret_cast<X4*>(sb + sofs + 32 * m) = sh[m];
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const bf16x8 nb = pack_perm(dv[2 * j], dv[2 * j + 1]);
+          const X8 nb = pack_permv<E>(dv[2 * j], dv[2 * j + 1]);
 #pragma unroll
           for (int m = 0; m < 8; ++m) dS[m] = mfma(fw[m][j], nb, dS[m]);
         }
-        char* vbp = sb + sizeof(BwdScratch::s);
+        char* vbp = sb + sizeof(BwdScratch<E>::s);
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) *reinterpret_cast<bf16x4*>(vbp + vofs + 32 * i4) = cvt4(dv[i4]);
+        for (int i4 = 0; i4 < 4; ++i4) *reinterpret_cast<X4*>(vbp + vofs + 32 * i4) = to4<E>(dv[i4]);
       }
       lds_barrier();
     }
@@ -535,18 +562,29 @@ __global__ __launch_bounds__(BS_THREADS) void bwd_scan_kernel(
 constexpr int DKW_R1 = 0, DKW_R2 = 64 * LDK * 2, DKW_R3 = DKW_R2 + 64 * LDK * 2, DKW_R4A = DKW_R3 + 64 * LDT * 2,
               DKW_R4B = DKW_R4A + 64 * LDK * 2, DKW_BYTES = DKW_R4B + 128 * LDT * 2;
 
+template <class E>  // dscale, vscale: null in bf16; in fp16 the device scalars s_d and s_v
 __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ rq,
-    const float* __restrict__ rk, const float* __restrict__ gc, const bf16* __restrict__ hT,
-    const bf16* __restrict__ vnT, const bf16* __restrict__ dout, const bf16* __restrict__ dh,
-    const bf16* __restrict__ dVn, const bf16* __restrict__ vin, const float* __restrict__ beta,
-    const bf16* __restrict__ Tm, const int32_t* __restrict__ chunks, int H, float scale, int normalize,
-    bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv, float* __restrict__ dg,
+    const E* __restrict__ q, const E* __restrict__ k, const float* __restrict__ rq,
+    const float* __restrict__ rk, const float* __restrict__ gc, const E* __restrict__ hT,
+    const E* __restrict__ vnT, const E* __restrict__ dout, const E* __restrict__ dh,
+    const E* __restrict__ dVn, const E* __restrict__ vin, const float* __restrict__ beta,
+    const E* __restrict__ Tm, const int32_t* __restrict__ chunks, int H, float scale, int normalize,
+    const float* __restrict__ dscale, const float* __restrict__ vscale,
+    E* __restrict__ dq, E* __restrict__ dk, E* __restrict__ dv, float* __restrict__ dg,
     float* __restrict__ dbeta, const int* __restrict__ ready, int ready_target, int ready_polls) {
   // grid (H, NC).  After the reverse scan: chunks first to last (the scan wrote the
   // first chunks last, so they are the likeliest still in the memory-side cache).
   // Beside the scan (ready != null): chunks last to first, the order the scan
   // finishes them, each workgroup waiting for its chunk's count after phase 1.
+  typedef typename Vec<E>::x8 X8;
+  constexpr bool F16 = __is_same(E, f16);
+  // fp16: dq, dk, dg and dbeta leave divided by s_d s_v, dv by s_d (powers of two: exact)
+  float inv_dv = 1.f, inv_d = 1.f, vs = 1.f;
+  if constexpr (F16) {
+    vs = *vscale;
+    inv_d = 1.f / *dscale;
+    inv_dv = inv_d / vs;
+  }
   const int h = blockIdx.x, c = ready ? gridDim.y - 1 - blockIdx.y : blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
@@ -566,19 +604,19 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   __shared__ float dgw[4][64];
   __shared__ __attribute__((aligned(16))) float Rs[64];  // rsqrt norms of q (1 without normalize)
   __shared__ int stale_s;  // nonzero when the wait for the reverse scan gave up
-  bf16* Qs = reinterpret_cast<bf16*>(r1);
-  bf16* Ks = reinterpret_cast<bf16*>(r2);
-  bf16* dPm = reinterpret_cast<bf16*>(r3);
-  bf16* dOs = reinterpret_cast<bf16*>(r4a);
-  bf16* VnT = reinterpret_cast<bf16*>(r4b);  // v_new^T [v][t], read transposed as v_new rows
-  bf16* dVs = dOs;                                    // dVn tile, from phase 3 on
+  E* Qs = reinterpret_cast<E*>(r1);
+  E* Ks = reinterpret_cast<E*>(r2);
+  E* dPm = reinterpret_cast<E*>(r3);
+  E* dOs = reinterpret_cast<E*>(r4a);
+  E* VnT = reinterpret_cast<E*>(r4b);  // v_new^T [v][t], read transposed as v_new rows
+  E* dVs = dOs;                        // dVn tile, from phase 3 on
   float* dqdot = reinterpret_cast<float*>(r4a + CH * D * 2);  // [64][4 waves] after the dVn tile
-  bf16* dWs = VnT;                                    // dW rows [t][k], from phase 4 on
+  E* dWs = VnT;                        // dW rows [t][k], from phase 4 on
 
   // This wave's state fragments: rows k = 16 (2 wave + mm) + r of h
   // (column gathers of h^T) and of dS_{c+1}, value block kb.
-  const bf16* ht = hT + cb * (D * D);
-  bf16x8 bh[2][4], bd[2][4];
+  const E* ht = hT + cb * (D * D);
+  X8 bh[2][4], bd[2][4];
   // Every prologue load is issued before the first wait: the column gathers'
   // loads, the gate and norm values (unconditional: rq is allocated either
   // way), the v_new^T rows and the Q, K, dO rows; the gathers' lane exchange
@@ -595,8 +633,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     const size_t ev = (size_t)(ci.start + tc) * H + h, row = ev * D;
     const float gv = gc[ev];
     const float rv = rq[ev], rkv = rk[ev];
-    const bf16* vt = vnT + cb * (D * CH);
-    bf16x8 xv[4], xq[4], xk[4], xo[4];
+    const E* vt = vnT + cb * (D * CH);
+    X8 xv[4], xq[4], xk[4], xo[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int seg = 256 * i + tid, v = seg >> 3, part = seg & 7;
@@ -619,17 +657,22 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       const int seg = 256 * i + tid, v = seg >> 3, part = seg & 7;
       st8(VnT + v * LDT + 8 * part, xv[i]);
     }
+    if constexpr (F16) {  // dO s_d (exact: a power of two, in range)
+      const float ds = *dscale;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xo[j] = to8<E>(cvtf8(xo[j]) * ds);
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
-      st8(Qs + t * LDK + col, keep_if(in, scaled8<bf16>(xq[j], rv)));
-      st8(Ks + t * LDK + col, keep_if(in, scaled8<bf16>(xk[j], rkv)));
+      st8(Qs + t * LDK + col, keep_if(in, scaled8<E>(xq[j], rv)));
+      st8(Ks + t * LDK + col, keep_if(in, scaled8<E>(xk[j], rkv)));
       st8(dOs + t * LDK + col, keep_if(in, xo[j]));
     }
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) bh[mm][kb] = col8_combine(gh[mm][kb]);
+      for (int kb = 0; kb < 4; ++kb) bh[mm][kb] = col8_combine_v<E>(gh[mm][kb]);
   }
   lds_barrier();
   const float glast = Gs[ci.len - 1];
@@ -708,14 +751,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const int i = (2 * kb + (q4 >> 1)) * (D * 16) + (16 * (2 * wave + mm) + r) * 16 + 8 * (q4 & 1);
-      bd[mm][kb] = ready ? buf_ld16_sc1<bf16x8>(dh_rs, i * 2) : ld8(dh + cb * (D * D) + i);
+      bd[mm][kb] = ready ? buf_ld16_sc1<X8>(dh_rs, i * 2) : ld8(dh + cb * (D * D) + i);
     }
   if (stale) {
     asm volatile("");  // a branch, not selects
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) bd[mm][kb] = cvt8(f32x8{NAN, NAN, NAN, NAN, NAN, NAN, NAN, NAN});
+      for (int kb = 0; kb < 4; ++kb) bd[mm][kb] = to8<E>(f32x8{NAN, NAN, NAN, NAN, NAN, NAN, NAN, NAN});
   }
 
   // ---- phase 2: dQ^T (k-tiles 2w, 2w+1 as rows, t columns); dG_t from the output term ----
@@ -734,7 +777,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
-        const bf16x8 a = ld8(dOs + (16 * n + r) * LDK + 32 * kb + 8 * q4);
+        const X8 a = ld8(dOs + (16 * n + r) * LDK + 32 * kb + 8 * q4);
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm) a1[mm][n] = mfma(bh[mm][kb], a, a1[mm][n]);
       }
@@ -743,7 +786,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
       for (int n = 0; n < 4; ++n) {
         if (n < 2 * kb) continue;
-        const bf16x8 a = ld8_tr(dPm, LDT, 32 * kb, 16 * n);  // dPm rows t = 16 n + r
+        const X8 a = ld8_tr(dPm, LDT, 32 * kb, 16 * n);  // dPm rows t = 16 n + r
 #pragma unroll
         for (int mm = 0; mm < 2; ++mm)
           dQ[mm][n] = mfma(ld8_tr(Ks, LDK, 32 * kb, 16 * (2 * wave + mm)), a, dQ[mm][n]);
@@ -808,17 +851,17 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       const int k0 = 16 * (2 * wave + mm) + 4 * q4;
       const f32x4 qr = cvtf4(ld4(Qs + t * LDK + k0));
       const f32x4 x = normalize ? (dQ[mm][n] - qr * dot) * rs : dQ[mm][n];
-      buf_st4(dq_rs, r * rowb + k0 * 2, 16 * n * rowb, x);  // row t, columns k0 .. k0 + 3
+      buf_st4<E>(dq_rs, r * rowb + k0 * 2, 16 * n * rowb, F16 ? x * inv_dv : x);  // row t, columns k0 .. k0 + 3
     }
   }
   }
   // the dVn tile, copied global -> LDS while phase 3 runs (after the dq stores, which retire first)
   {
-    const bf16* dvs = dVn + cb * (CH * D);
+    const E* dvs = dVn + cb * (CH * D);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (stale)
-        st8(dVs + 512 * (4 * i + wave) + 8 * lane, cvt8(f32x8{NAN, NAN, NAN, NAN, NAN, NAN, NAN, NAN}));
+        st8(dVs + 512 * (4 * i + wave) + 8 * lane, to8<E>(f32x8{NAN, NAN, NAN, NAN, NAN, NAN, NAN, NAN}));
       else if (ready)
         dma16_sc1(dvs + 512 * (4 * i + wave) + 8 * lane, dVs + 512 * (4 * i + wave));
       else
@@ -838,7 +881,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       for (int n = 0; n < 4; ++n) a3[n] = a4[n] = zero4();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = ld8_tr(Qs, LDK, 32 * kb, 16 * m);
+        const X8 a = ld8_tr(Qs, LDK, 32 * kb, 16 * m);
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
           if (n > 2 * kb + 1) continue;
@@ -878,7 +921,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   lds_barrier();    // every read of Q, dPm and v_new^T is done
 
   // the wy part's V rows, T rows and beta, requested now and stored over Q and dPm after phase 4
-  bf16x8 pv[4], pt[2];
+  X8 pv[4], pt[2];
   float pb;
   {
     const int t = tid >> 2, p = tid & 3;
@@ -888,18 +931,18 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     pb = keep_if(in, beta[(size_t)(ci.start + tc) * H + h]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) pv[j] = keep_if(in, ld8(vin + row + 32 * j + 8 * p));
-    const bf16* tm = Tm + cb * (CH * CH);
+    const E* tm = Tm + cb * (CH * CH);
 #pragma unroll
     for (int j = 0; j < 2; ++j) pt[j] = ld8(tm + t * CH + 32 * j + 8 * p);
   }
 
   // ---- phase 4: dW = -dVn S^T into LDS rows [t][k]; the wy part's dVn fragments ----
-  bf16x8 fdv[4], fvt[2][2];
+  X8 fdv[4], fvt[2][2];
   {
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       const int t = 16 * n + r;
-      bf16x8 av[4];  // dVn row t, value block kb
+      X8 av[4];  // dVn row t, value block kb
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) av[kb] = ld8(dVs + (2 * kb + (q4 >> 1)) * (CH * 16) + t * 16 + 8 * (q4 & 1));
 #pragma unroll
@@ -924,10 +967,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 
   // ---- the WY part, on the chip-resident operands ----
   const float dgp_t = (tid < 64) ? dgw[0][tid] + dgw[1][tid] + dgw[2][tid] + dgw[3][tid] : 0.f;
-  bf16* Vs = Qs;
-  bf16* Ts = dPm;
-  bf16* S1 = dOs;  // transposed: dT^T[s][t], then (beta dM)^T [j][i]
-  bf16* S2 = VnT;                                                              // Y^T[j][t], over dW rows
+  E* Vs = Qs;
+  E* Ts = dPm;
+  E* S1 = dOs;  // transposed: dT^T[s][t], then (beta dM)^T [j][i]
+  E* S2 = VnT;                                                              // Y^T[j][t], over dW rows
   float* Bs = reinterpret_cast<float*>(r4a + 64 * LDT * 2);                   // after S1
   float* dbw = Bs + 64;                                                        // [4][64]
   float* dkdot = dbw + 256;                                                    // [64][4 waves]
@@ -935,7 +978,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     const int t = tid >> 2, p = tid & 3;
     if (p == 0) Bs[t] = pb;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) st8(Vs + t * LDK + 32 * j + 8 * p, pv[j]);
+    for (int j = 0; j < 4; ++j)  // fp16: V s_v, in the scale of the forward's v_new and U
+      st8(Vs + t * LDK + 32 * j + 8 * p, F16 ? to8<E>(cvtf8(pv[j]) * vs) : pv[j]);
 #pragma unroll
     for (int j = 0; j < 2; ++j) st8(Ts + t * LDT + 32 * j + 8 * p, pt[j]);
   }
@@ -946,13 +990,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   float* dbl = dbw + wave * 64;
 
   // ---- wy phase 1: dT = dW (beta gam K)^T + dVn (beta V)^T -> S1 = dT[t][s]; dW fragments ----
-  bf16x8 fwt[2][2];
+  X8 fwt[2][2];
 #pragma unroll
   for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) fwt[mm][kb] = ld8_tr(dWs, LDK, 32 * kb, 16 * (2 * wave + mm));
   {
-    bf16x8 fdw[4];
+    X8 fdw[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) fdw[kb] = ld8(dWs + (16 * wave + r) * LDK + 32 * kb + 8 * q4);
     f32x4 ak[4], av[4];
@@ -982,7 +1026,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 
   // ---- wy phase 2: Y = dT T^T -> S2 = Y^T[j][t] ----
   {
-    bf16x8 a[2];
+    X8 a[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) a[kb] = ld8_tr(S1, LDT, 32 * kb, 16 * wave);  // dT rows t = 16 wave + r
 #pragma unroll
@@ -1003,7 +1047,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   {
     // (beta dM)^T of i-tile it, j-tile n (at, ak: T^T and K fragments of i-tile it; gam: the
     // tile's gates from phase 1, whose diagonal 1 is masked here by dA's strict mask)
-    auto pair = [&](int it, int n, const bf16x8(&at)[2], const bf16x8(&ak)[4], const f32x4& gam,
+    auto pair = [&](int it, int n, const X8(&at)[2], const X8(&ak)[4], const f32x4& gam,
                     float(&rowB)[4], float(&rowE)[4]) -> f32x4 {
       f32x4 da = zero4(), kk = zero4();
 #pragma unroll
@@ -1045,7 +1089,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       }
     };
     {
-      bf16x8 at[2], ak[4];
+      X8 at[2], ak[4];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) at[kb] = ld8_tr(Ts, LDT, 32 * kb, 16 * wave);
 #pragma unroll
@@ -1060,7 +1104,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       rows(wave, rowB, rowE);
     }
     if (wave == 0) {
-      bf16x8 at[2], ak[4];
+      X8 at[2], ak[4];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) at[kb] = ld8_tr(Ts, LDT, 32 * kb, 48);
 #pragma unroll
@@ -1087,7 +1131,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       for (int n = 0; n < 4; ++n) acc[n] = zero4();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = fvt[mm][kb];
+        const X8 a = fvt[mm][kb];
 #pragma unroll
         for (int n = 0; n < 4; ++n)
           if (kb >= 1 || n < 2) acc[n] = mfma(a, ld8_tr(Ts, LDT, 32 * kb, 16 * n), acc[n]);
@@ -1097,7 +1141,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
         const int s = 16 * n + r;
         const f32x4 vv = cvtf4(ld4(Vs + s * LDK + 16 * m + 4 * q4));
         colB[n] += acc[n][0] * vv[0] + acc[n][1] * vv[1] + acc[n][2] * vv[2] + acc[n][3] * vv[3];
-        buf_st4(dv_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, acc[n] * Bs[s]);  // row s
+        buf_st4<E>(dv_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb,
+                   acc[n] * (F16 ? Bs[s] * inv_d : Bs[s]));  // row s
       }
     }
 #pragma unroll
@@ -1120,8 +1165,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       for (int n = 0; n < 4; ++n) ak[n] = aw[n] = zero4();
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 a = ld8_tr(Ks, LDK, 32 * kb, 16 * m);
-        const bf16x8 w = fwt[mm][kb];
+        const X8 a = ld8_tr(Ks, LDK, 32 * kb, 16 * m);
+        const X8 w = fwt[mm][kb];
 #pragma unroll
         for (int n = 0; n < 4; ++n) {
           if (n >= 2 * kb) ak[n] = mfma(a, ld8_tr(S1, LDT, 32 * kb, 16 * n), ak[n]);
@@ -1180,7 +1225,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       const int m = 2 * wave + mm;
       const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
       const f32x4 out = normalize ? (dkr[mm][n] - kk * dot) * rsn[n] : dkr[mm][n];
-      buf_st4(dk_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, out);  // row t
+      buf_st4<E>(dk_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, F16 ? out * inv_dv : out);  // row t
     }
   }
   if (tid < 64) {
@@ -1193,8 +1238,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       if (t + off < 64) x += o;
     }
     if (in) {
-      dg[(size_t)(ci.start + t) * H + h] = x;
-      dbeta[(size_t)(ci.start + t) * H + h] = dbw[t] + dbw[64 + t] + dbw[128 + t] + dbw[192 + t];
+      const float db = dbw[t] + dbw[64 + t] + dbw[128 + t] + dbw[192 + t];
+      dg[(size_t)(ci.start + t) * H + h] = F16 ? x * inv_dv : x;
+      dbeta[(size_t)(ci.start + t) * H + h] = F16 ? db * inv_dv : db;
     }
   }
 }
@@ -1213,20 +1259,43 @@ static void launch_resident_gate(const int* resident, int expected, hipStream_t 
   hipLaunchKernelGGL(scan_resident_gate_kernel, dim3(1), dim3(64), 0, stream, resident, expected);
 }
 
-hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
-  auto F = [&](int i) { return reinterpret_cast<const bf16*>(a.fws + a.foff[i]); };
+// The scale target of dO: max|dO s_d| < 2^e with T 2^e <= 2^15, at most 2^1.
+static int dout_scale_target(int T) {
+  int lg = 0;
+  while (lg < 31 && (1LL << lg) < (long long)T) ++lg;  // 2^lg >= T
+  return 15 - lg < 1 ? 15 - lg : 1;
+}
+
+template <class E>
+static hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t stream) {
+  auto F = [&](int i) { return reinterpret_cast<const E*>(a.fws + a.foff[i]); };
   auto Ff = [&](int i) { return reinterpret_cast<const float*>(a.fws + a.foff[i]); };
-  auto B = [&](int i) { return reinterpret_cast<bf16*>(a.bws + a.boff[i]); };
+  auto B = [&](int i) { return reinterpret_cast<E*>(a.bws + a.boff[i]); };
+  const E* q = static_cast<const E*>(a.q);
+  const E* k = static_cast<const E*>(a.k);
+  const E* v = static_cast<const E*>(a.v);
+  const E* dout = static_cast<const E*>(a.dout);
+  E* dq = static_cast<E*>(a.dq);
+  E* dk = static_cast<E*>(a.dk);
+  E* dv = static_cast<E*>(a.dv);
   const dim3 grid_p(a.H, a.n_chunks);  // chunk-major dispatch (the kernels pick the chunk order)
   int* sync = reinterpret_cast<int*>(a.bws + a.boff[B_SYNC]);
   int* ready = sync;                                 // [NC][H]
   int* resident = sync + (size_t)a.n_chunks * a.H;  // one count
   const bool beside = a.side != nullptr;
+  // fp16: the scales s_d (computed here) and s_v (the forward's)
+  float* dsc = nullptr;
+  const float* vsc = nullptr;
+  if (__is_same(E, f16)) {
+    dsc = reinterpret_cast<float*>(a.bws + a.boff[B_DSC]);
+    vsc = Ff(F_VSC);
+    launch_range_scale(a.dout, true, (size_t)a.T * a.H * (D / 8), nullptr, 0, dout_scale_target(a.T), dsc, stream);
+  }
   {
     TimedLaunch tl(K_BWD_LOCAL, stream);
-    hipLaunchKernelGGL(bwd_local_kernel, dim3(a.H, a.n_chunks), dim3(256), 0, stream, a.q, a.k, Ff(F_RQ),
-                       Ff(F_RK), a.dout, Ff(F_GC), a.beta, F(F_TM), a.chunks, a.H, a.scale, B(B_DVLT), B(B_XT),
-                       B(B_KNP), B(B_WT), sync);
+    hipLaunchKernelGGL(bwd_local_kernel<E>, dim3(a.H, a.n_chunks), dim3(256), 0, stream, q, k, Ff(F_RQ), Ff(F_RK),
+                       dout, Ff(F_GC), a.beta, F(F_TM), a.chunks, a.H, a.scale, (const float*)dsc, B(B_DVLT),
+                       B(B_XT), B(B_KNP), B(B_WT), sync);
   }
   if (beside) {
     if (const hipError_t e = hipEventRecord(a.side_fork, stream)) return e;
@@ -1234,7 +1303,7 @@ hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
   }
   {
     TimedLaunch tl(K_BWD_SCAN, stream);
-    hipLaunchKernelGGL(bwd_scan_kernel, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, B(B_KNP),
+    hipLaunchKernelGGL(bwd_scan_kernel<E>, dim3(a.H * (D / 16), a.n_docs), dim3(BS_THREADS), 0, stream, B(B_KNP),
                        Ff(F_GC), B(B_DVLT), B(B_XT), B(B_WT), a.chunks, a.doc_chunk, a.H, B(B_DH), B(B_DVN),
                        beside ? ready : nullptr, beside ? resident : nullptr);
   }
@@ -1242,9 +1311,9 @@ hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
     launch_resident_gate(resident, a.H * (D / 16) * a.n_docs, a.side);
     {
       TimedLaunch tl(K_BWD_DKW, a.side);
-      hipLaunchKernelGGL(bwd_dkw_kernel, grid_p, dim3(256), 0, a.side, a.q, a.k, Ff(F_RQ), Ff(F_RK), Ff(F_GC),
-                         F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.v, a.beta, F(F_TM), a.chunks, a.H, a.scale,
-                         (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta, (const int*)ready,
+      hipLaunchKernelGGL(bwd_dkw_kernel<E>, grid_p, dim3(256), 0, a.side, q, k, Ff(F_RQ), Ff(F_RK), Ff(F_GC),
+                         F(F_HT), F(F_VNT), dout, B(B_DH), B(B_DVN), v, a.beta, F(F_TM), a.chunks, a.H, a.scale,
+                         (int)a.normalize, (const float*)dsc, vsc, dq, dk, dv, a.dg, a.dbeta, (const int*)ready,
                          a.dkw_never_ready ? D / 16 + 1 : D / 16, a.dkw_never_ready ? 4 : COUNT_SPIN_LIMIT);
     }
     if (const hipError_t e = hipEventRecord(a.side_join, a.side)) return e;
@@ -1253,10 +1322,14 @@ hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
   if (a.dkw_after)
     if (const hipError_t e = hipStreamWaitEvent(stream, a.dkw_after, 0)) return e;
   TimedLaunch tl(K_BWD_DKW, stream);
-  hipLaunchKernelGGL(bwd_dkw_kernel, grid_p, dim3(256), 0, stream, a.q, a.k, Ff(F_RQ), Ff(F_RK), Ff(F_GC),
-                     F(F_HT), F(F_VNT), a.dout, B(B_DH), B(B_DVN), a.v, a.beta, F(F_TM), a.chunks, a.H, a.scale,
-                     (int)a.normalize, a.dq, a.dk, a.dv, a.dg, a.dbeta, (const int*)nullptr, 0, 0);
+  hipLaunchKernelGGL(bwd_dkw_kernel<E>, grid_p, dim3(256), 0, stream, q, k, Ff(F_RQ), Ff(F_RK), Ff(F_GC), F(F_HT),
+                     F(F_VNT), dout, B(B_DH), B(B_DVN), v, a.beta, F(F_TM), a.chunks, a.H, a.scale, (int)a.normalize,
+                     (const float*)dsc, vsc, dq, dk, dv, a.dg, a.dbeta, (const int*)nullptr, 0, 0);
   return hipSuccess;
+}
+
+hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream) {
+  return a.fp16 ? launch_bwd_t<f16>(a, stream) : launch_bwd_t<bf16>(a, stream);
 }
 
 }  // namespace cqgdn

@@ -144,10 +144,11 @@ __device__ __forceinline__ bf16x4 ld4_c(const bf16* tile, int ld, int row0, int 
 }
 
 // ---- fp16 operands ----------------------------------------------------------
-// The precise (inference) forward keeps its MFMA operands in fp16: 11 mantissa
-// bits instead of bf16's 8, at the same MFMA rate (v_mfma_f32_16x16x32_f16).
-// The kernels are templates over the operand element type E (bf16 or f16);
-// Vec<E> names its vector types and the helpers below are overloaded on them.
+// The precise (inference) forward, and the forward and backward of fp16 inputs,
+// keep their MFMA operands in fp16: 11 mantissa bits instead of bf16's 8, at the
+// same MFMA rate (v_mfma_f32_16x16x32_f16).  The kernels are templates over the
+// operand element type E (bf16 or f16); Vec<E> names its vector types and the
+// helpers below are overloaded on them.
 typedef _Float16 f16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -219,13 +220,37 @@ __device__ __forceinline__ typename Vec<E>::x8 ld8_trv(const E* tile, int ld, in
 // tile[k0 + 4 q4 + e][n0 + r] for e = 0..3 and tile[k0 + 16 + 4 q4 + e - 4][n0 + r]
 // for e = 4..7, the K order of a B (or A) operand built by pack_perm from
 // accumulator fragments.
-__device__ __forceinline__ bf16x8 ld8_trp(const bf16* tile, int ld, int k0, int n0) {
+template <class E>
+__device__ __forceinline__ typename Vec<E>::x8 ld8_trpv(const E* tile, int ld, int k0, int n0) {
   typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
   const int lane = threadIdx.x & 63, r = lane & 15, q4 = lane >> 4;
-  const bf16* p = tile + (k0 + 4 * q4 + (r >> 2)) * ld + n0 + 4 * (r & 3);
+  const E* p = tile + (k0 + 4 * q4 + (r >> 2)) * ld + n0 + 4 * (r & 3);
   const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
   const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 16 * ld));
-  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  return __builtin_bit_cast(typename Vec<E>::x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+__device__ __forceinline__ bf16x8 ld8_trp(const bf16* tile, int ld, int k0, int n0) {
+  return ld8_trpv<bf16>(tile, ld, k0, n0);
+}
+
+// The fp16 forms of the bf16 helpers above, so that a kernel templated on its operand
+// type calls them by one name: transposed fragments, non-temporal rows, and the
+// operand rows of q and k formed from fp16 inputs.
+__device__ __forceinline__ f16x8 ld8_tr(const f16* tile, int ld, int k0, int n0) {
+  return ld8_trv<f16>(tile, ld, k0, n0);
+}
+__device__ __forceinline__ f16x8 ld8_trp(const f16* tile, int ld, int k0, int n0) {
+  return ld8_trpv<f16>(tile, ld, k0, n0);
+}
+__device__ __forceinline__ f16x8 ld8_nt(const f16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p));
+}
+__device__ __forceinline__ void st8_nt(f16* p, f16x8 x) {
+  __builtin_nontemporal_store(x, reinterpret_cast<f16x8*>(p));
+}
+template <class E>
+__device__ __forceinline__ typename Vec<E>::x8 scaled8(f16x8 x, float r) {
+  return to8<E>(cvtf8(x) * r);
 }
 
 // Transposed read of a 16-row LDS tile [v][k] (row stride ld): lane (q4, r)
@@ -293,6 +318,17 @@ __device__ __forceinline__ bf16x8 col8_combine(const Col8& g) {
 }
 __device__ __forceinline__ bf16x8 gather8_col_rows(const bf16* M, int ld, int row0, int col0, int nrows) {
   return col8_combine(col8_load_rows(M, ld, row0, col0, nrows));
+}
+// The same gathers over an fp16 matrix (they move 16-bit values without looking at them)
+__device__ __forceinline__ Col8 col8_load(const f16* M, int ld, int row0, int col0) {
+  return col8_load(reinterpret_cast<const bf16*>(M), ld, row0, col0);
+}
+__device__ __forceinline__ Col8 col8_load_rows(const f16* M, int ld, int row0, int col0, int nrows) {
+  return col8_load_rows(reinterpret_cast<const bf16*>(M), ld, row0, col0, nrows);
+}
+template <class E>
+__device__ __forceinline__ typename Vec<E>::x8 col8_combine_v(const Col8& g) {
+  return __builtin_bit_cast(typename Vec<E>::x8, col8_combine(g));
 }
 
 // ---- workgroup synchronization for loader/consumer kernels ----------------
@@ -453,6 +489,13 @@ __device__ __forceinline__ float dot8(bf16x8 a, bf16x8 b, float c) {
     c = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{a[e], a[e + 1]}, bf16x2{b[e], b[e + 1]}, c, false);
   return c;
 }
+// the same over 8 fp16 pairs (v_dot2_f32_f16)
+__device__ __forceinline__ float dot8(f16x8 a, f16x8 b, float c) {
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) c = __builtin_amdgcn_fdot2(f16x2{a[e], a[e + 1]}, f16x2{b[e], b[e + 1]}, c, false);
+  return c;
+}
 
 // sum16 of four independent values, level by level (each value gets the same operations in
 // the same order as sum16): a DPP move then reads a register written three instructions
@@ -494,7 +537,8 @@ __device__ __forceinline__ V keep_if(bool in, V x) {
 // wave-uniform SGPR offset (the row), instead of a 64-bit address per lane.
 // 0x00020000 is the resource's fourth dword for a raw buffer on gfx9-family parts.
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rows_rsrc(bf16* base, int start, int len, int H, int h) {
+template <class E>  // bf16 or fp16 rows
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rows_rsrc(E* base, int start, int len, int H, int h) {
   return __builtin_amdgcn_make_buffer_rsrc(base + ((size_t)start * H + h) * D, (short)0, (len - 1) * H * D * 2 + D * 2,
                                            0x00020000);
 }
@@ -512,8 +556,10 @@ __device__ __forceinline__ void buf_st16(__amdgpu_buffer_rsrc_t rs, int voff, in
 __device__ __forceinline__ void buf_st1(__amdgpu_buffer_rsrc_t rs, int voff, int soff, float x) {
   __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, (bf16)x), rs, voff, soff, 0);
 }
+// four values rounded to E (bf16 or fp16), 8 bytes
+template <class E = bf16>
 __device__ __forceinline__ void buf_st4(__amdgpu_buffer_rsrc_t rs, int voff, int soff, f32x4 x) {
-  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, cvt4(x)), rs, voff, soff, 0);
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, to4<E>(x)), rs, voff, soff, 0);
 }
 
 // ---- hand-off between two kernels running at the same time ----------------

@@ -28,11 +28,12 @@ constexpr int LDA = 65;   // row stride (fp32) of the 64 x 64 solve matrix
 // ---------------------------------------------------------------------------
 // fwd_prep
 // ---------------------------------------------------------------------------
-// E: operand element type (bf16, or f16 for the precise forward).  vscale: null,
-// or the power-of-two factor applied to V (fp16 range, see vscale_final_kernel).
-template <class E, bool NORMALIZE>
+// I: input element type of q, k, v (bf16 or f16).  E: operand element type (bf16,
+// or f16 for the precise forward and for fp16 inputs).  vscale: null, or the
+// power-of-two factor applied to V (fp16 range, see vscale_final_kernel).
+template <class I, class E, bool NORMALIZE>
 __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const I* __restrict__ q, const I* __restrict__ k, const I* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const int32_t* __restrict__ chunks,
     int H, const float* __restrict__ vscale, float* __restrict__ rq,
     float* __restrict__ rk, float* __restrict__ gc, E* __restrict__ Tm, E* __restrict__ W,
@@ -75,7 +76,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     gv = g[ev];
     bv = beta[ev];
   }
-  bf16x8 lq[4], lk[4];
+  typename Vec<I>::x8 lq[4], lk[4];
   Col8 vg[2][2];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -83,7 +84,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     lk[j] = ld8_nt(k + row_r + 32 * j + 8 * p_r);
   }
   {
-    const bf16* vb = v + ((size_t)ci.start * H + h) * D;
+    const I* vb = v + ((size_t)ci.start * H + h) * D;
 #pragma unroll
     for (int nn = 0; nn < 2; ++nn)
 #pragma unroll
@@ -305,7 +306,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
       const f32x4 b1 = *reinterpret_cast<const f32x4*>(Bs + 32 * kb + 8 * q4 + 4);
       const f32x8 bb = f32x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]} * vs;
 #pragma unroll
-      for (int nn = 0; nn < 2; ++nn) bvf[nn][kb] = to8<E>(cvtf8(col8_combine(vg[nn][kb])) * bb);
+      for (int nn = 0; nn < 2; ++nn) bvf[nn][kb] = to8<E>(cvtf8(col8_combine_v<I>(vg[nn][kb])) * bb);
     }
     E* ut = UT + cb * (D * CH);
 #pragma unroll
@@ -699,12 +700,12 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
 // ---------------------------------------------------------------------------
 // fwd_out: O^T (v rows, t columns) per chunk and head.
 // ---------------------------------------------------------------------------
-template <class E>
+template <class I, class E>  // I: element type of q, k and o; E: operand type (as fwd_prep)
 __global__ __launch_bounds__(256) void fwd_out_kernel(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const float* __restrict__ rq,
+    const I* __restrict__ q, const I* __restrict__ k, const float* __restrict__ rq,
     const float* __restrict__ rk, const float* __restrict__ gc, const E* __restrict__ hT,
     const E* __restrict__ vnT, const int32_t* __restrict__ chunks, int H,
-    float scale, const float* __restrict__ vscale, bf16* __restrict__ o) {
+    float scale, const float* __restrict__ vscale, I* __restrict__ o) {
   typedef typename Vec<E>::x8 X8;
   // grid (H, NC), chunks last to first: the state scan wrote the last chunks
   // last, so they are the likeliest still in the memory-side cache
@@ -736,7 +737,7 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
     const bool in = t < ci.len;
     const size_t ev = (size_t)(ci.start + clamp_row(t, ci.len)) * H + h, row = ev * D;
     const float rqt = rq[ev], rkt = rk[ev];
-    bf16x8 xq[4], xk[4];
+    typename Vec<I>::x8 xq[4], xk[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
@@ -813,18 +814,21 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
   for (int n = 0; n < 4; ++n) {
     const int t = 16 * n + r;
     if (t >= ci.len) continue;
-    bf16* orow = o + ((size_t)(ci.start + t) * H + h) * D;
+    I* orow = o + ((size_t)(ci.start + t) * H + h) * D;
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) st4(orow + 16 * (2 * wave + mm) + 4 * q4, acc[mm][n] * osc);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Power-of-two scale of V for the fp16 (precise) forward.  The recurrence is
-// linear in (V, initial state): scaling both by vs scales W-free quantities
-// (U, v_new, every state, O) by vs exactly, so the kernels carry them scaled
-// and divide O and the final state by vs.  vs brings max(|V|, |S0|) into
-// [32, 64), far inside fp16's range (65504) for U, v_new and the state.
+// Power-of-two scale of V for the fp16 forwards.  The recurrence is linear in
+// (V, initial state): scaling both by vs scales W-free quantities (U, v_new,
+// every state, O) by vs exactly, so the kernels carry them scaled and divide O
+// and the final state by vs.  vs brings max(|V|, |S0|) into [2^(t-1), 2^t):
+// t = 6 for inference, far inside fp16's range (65504) for U, v_new and the
+// state; t = 3 for training, where the backward multiplies V-scaled by
+// dO-scaled quantities (dP, dW) and keeps their products in fp16 too.  The same
+// kernels give the backward's scale of dO (launch_range_scale).
 // ---------------------------------------------------------------------------
 constexpr int VS_BLOCKS = kVscaleBlocks;
 
@@ -836,7 +840,8 @@ __device__ __forceinline__ float block_max(float m, float* red) {
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
-__global__ __launch_bounds__(256) void vscale_partial_kernel(const bf16* __restrict__ v, size_t nv8,
+template <class I>
+__global__ __launch_bounds__(256) void vscale_partial_kernel(const I* __restrict__ v, size_t nv8,
                                                              const float* __restrict__ s0, size_t ns,
                                                              float* __restrict__ part) {
   __shared__ float red[4];
@@ -852,7 +857,7 @@ __global__ __launch_bounds__(256) void vscale_partial_kernel(const bf16* __restr
   if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
-__global__ __launch_bounds__(256) void vscale_final_kernel(const float* __restrict__ part, int n,
+__global__ __launch_bounds__(256) void vscale_final_kernel(const float* __restrict__ part, int n, int target,
                                                            float* __restrict__ vscale) {
   __shared__ float red[4];
   float m = 0.f;
@@ -863,7 +868,7 @@ __global__ __launch_bounds__(256) void vscale_final_kernel(const float* __restri
     if (m > 0.f && isfinite(m)) {
       int e;
       frexpf(m, &e);  // m < 2^e
-      sc = ldexpf(1.f, min(max(6 - e, -60), 60));
+      sc = ldexpf(1.f, min(max(target - e, -60), 60));
     }
     vscale[0] = sc;
   }
@@ -872,22 +877,25 @@ __global__ __launch_bounds__(256) void vscale_final_kernel(const float* __restri
 // ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
-template <class E>
+template <class I, class E>
 static hipError_t launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stream) {
   E* ws[F_COUNT];
   for (int i = 0; i < F_COUNT; ++i) ws[i] = reinterpret_cast<E*>(a.ws + a.off[i]);
   float* rq = reinterpret_cast<float*>(ws[F_RQ]);
   float* rk = reinterpret_cast<float*>(ws[F_RK]);
   float* gcum = reinterpret_cast<float*>(ws[F_GC]);
+  const I* q = static_cast<const I*>(a.q);
+  const I* k = static_cast<const I*>(a.k);
+  const I* v = static_cast<const I*>(a.v);
   {
     TimedLaunch tl(K_FWD_PREP, stream);
     const dim3 grid_p(a.H, a.n_chunks);
     if (a.normalize)
-      hipLaunchKernelGGL((fwd_prep_kernel<E, true>), grid_p, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
+      hipLaunchKernelGGL((fwd_prep_kernel<I, E, true>), grid_p, dim3(256), 0, stream, q, k, v, a.g, a.beta,
                          a.chunks, a.H, vscale, rq, rk, gcum, ws[F_TM], ws[F_W],
                          ws[F_UT], ws[F_KGT]);
     else
-      hipLaunchKernelGGL((fwd_prep_kernel<E, false>), grid_p, dim3(256), 0, stream, a.q, a.k, a.v, a.g, a.beta,
+      hipLaunchKernelGGL((fwd_prep_kernel<I, E, false>), grid_p, dim3(256), 0, stream, q, k, v, a.g, a.beta,
                          a.chunks, a.H, vscale, rq, rk, gcum, ws[F_TM], ws[F_W],
                          ws[F_UT], ws[F_KGT]);
   }
@@ -907,20 +915,30 @@ static hipError_t launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_
     if (const hipError_t e = hipEventRecord(a.scan_join, a.scan_stream)) return e;
   if (a.no_output) return hipSuccess;
   TimedLaunch tl(K_FWD_OUT, stream);
-  hipLaunchKernelGGL(fwd_out_kernel<E>, dim3(a.H, a.n_chunks), dim3(256), 0, stream, a.q, a.k, rq, rk, gcum,
-                     ws[F_HT], ws[F_VNT], a.chunks, a.H, a.scale, vscale, a.o);
+  hipLaunchKernelGGL((fwd_out_kernel<I, E>), dim3(a.H, a.n_chunks), dim3(256), 0, stream, q, k, rq, rk, gcum,
+                     ws[F_HT], ws[F_VNT], a.chunks, a.H, a.scale, vscale, static_cast<I*>(a.o));
   return hipSuccess;
 }
 
+void launch_range_scale(const void* x, bool fp16, size_t n8, const float* s0, size_t ns, int target, float* out,
+                        hipStream_t stream) {
+  if (fp16)
+    hipLaunchKernelGGL(vscale_partial_kernel<f16>, dim3(VS_BLOCKS), dim3(256), 0, stream,
+                       static_cast<const f16*>(x), n8, s0, ns, out + 1);
+  else
+    hipLaunchKernelGGL(vscale_partial_kernel<bf16>, dim3(VS_BLOCKS), dim3(256), 0, stream,
+                       static_cast<const bf16*>(x), n8, s0, ns, out + 1);
+  hipLaunchKernelGGL(vscale_final_kernel, dim3(1), dim3(256), 0, stream, out + 1, VS_BLOCKS, target, out);
+}
+
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
-  if (!a.precise) return launch_fwd_t<bf16>(a, nullptr, stream);
+  if (!a.precise && !a.fp16) return launch_fwd_t<bf16, bf16>(a, nullptr, stream);
   float* vsc = reinterpret_cast<float*>(a.ws + a.off[F_VSC]);
   const size_t nv8 = (size_t)a.T * a.H * (D / 8);
   const size_t ns = a.initial_state ? (size_t)a.n_docs * a.H * D * D : 0;
-  hipLaunchKernelGGL(vscale_partial_kernel, dim3(VS_BLOCKS), dim3(256), 0, stream, a.v, nv8, a.initial_state, ns,
-                     vsc + 1);
-  hipLaunchKernelGGL(vscale_final_kernel, dim3(1), dim3(256), 0, stream, vsc + 1, VS_BLOCKS, vsc);
-  return launch_fwd_t<f16>(a, vsc, stream);
+  launch_range_scale(a.v, a.fp16, nv8, a.initial_state, ns, a.training ? kVscaleTargetTraining : kVscaleTarget,
+                     vsc, stream);
+  return a.fp16 ? launch_fwd_t<f16, f16>(a, vsc, stream) : launch_fwd_t<bf16, f16>(a, vsc, stream);
 }
 
 }  // namespace cqgdn

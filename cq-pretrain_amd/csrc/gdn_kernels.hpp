@@ -12,18 +12,20 @@ namespace cqgdn {
 typedef __bf16 bf16;
 
 struct FwdArgs {
-  const bf16 *q, *k, *v;
+  const void *q, *k, *v;     // bf16, or fp16 with fp16 (both [T][H][D])
   const float *g, *beta;
   const int32_t* chunks;     // [n_chunks][2] (start, len)
   const int32_t* doc_chunk;  // [n_docs + 1]
   int T, H, n_chunks, n_docs;
   float scale;
   bool normalize;
-  bool precise;                // fp16 operands (inference only); operands in the workspace are then fp16
+  bool precise;                // fp16 operands from bf16 inputs (inference); the workspace then holds fp16
+  bool fp16;                   // fp16 inputs and output, fp16 operands (inference or training)
+  bool training;               // the workspace feeds the backward (V's scale target, with fp16 operands)
   bool no_output;              // rebuild the workspace only (the backward's recompute): no output kernel
   const float* initial_state;  // [n_docs][H][K][V] or null
   float* final_state;          // [n_docs][H][K][V] or null
-  bf16* o;                     // [T][H][D]
+  void* o;                     // [T][H][D], in the inputs' type
   uint8_t* ws;
   size_t off[F_COUNT];
   // optional: the state scan runs on scan_stream, after scan_fork (recorded on the
@@ -33,18 +35,19 @@ struct FwdArgs {
 };
 
 struct BwdArgs {
-  const bf16 *q, *k, *v, *dout;
+  const void *q, *k, *v, *dout;  // bf16, or fp16 with fp16 (as dq, dk, dv)
   const float *g, *beta;
   const int32_t* chunks;
   const int32_t* doc_chunk;
   int T, H, n_chunks, n_docs;
   float scale;
   bool normalize;
+  bool fp16;           // fp16 inputs and gradients, fp16 operands (the forward workspace's too)
   const uint8_t* fws;  // forward workspace
   size_t foff[F_COUNT];
   uint8_t* bws;        // backward workspace
   size_t boff[B_COUNT];
-  bf16 *dq, *dk, *dv;
+  void *dq, *dk, *dv;
   float *dg, *dbeta;
   hipEvent_t dkw_after;  // optional: bwd_dkw waits for this event (the forward scan's join)
   // optional: bwd_dkw runs on `side` beside the reverse scan (after side_fork, recorded
@@ -60,6 +63,11 @@ struct BwdArgs {
 // launch errors are left for hipGetLastError.
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream);
+// out[0] = 2^(target - e) for the e with max|x| in [2^(e-1), 2^e) over n8 groups of 8
+// values of x (bf16, or fp16) and ns fp32 values of s0 (1 if all are zero or one is not
+// finite); out[1 .. kVscaleBlocks] take the partial maxima (gdn_fwd.hip)
+void launch_range_scale(const void* x, bool fp16, size_t n8, const float* s0, size_t ns, int target, float* out,
+                        hipStream_t stream);
 
 void launch_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta,
                       bool beta_bf16, bool fp16, float* state, void* out, int N, int E, int H, float scale,

@@ -1,6 +1,8 @@
 // Workspace layout of the GDN forward/backward passes (host and device).
 //
-// In the precise forward (CQGDN_PRECISE) every buffer listed as bf16 holds fp16.
+// In the precise forward (CQGDN_PRECISE) and with fp16 inputs (CQGDN_FP16) every
+// buffer listed as bf16 holds fp16, in the scales the kernels state (V's s_v for
+// U, h and v_new; dO's s_d for the backward's buffers).
 //
 // The forward workspace holds everything the backward re-reads apart from the
 // inputs (the reference saves q,k,v,gcum,beta,A in fused mode and also
@@ -31,7 +33,7 @@ enum FwdBuf {
   F_KGT,     // bf16 [NC][H][D][64]   (K * exp(G_last - G)) transposed (k, t), perm32 columns
   F_HT,      // bf16 [NC][H][D][D]    state entering the chunk, (v, k)
   F_VNT,     // bf16 [NC][H][D][64]   v_new transposed (v, t)
-  F_VSC,     // f32  [1 + 256]        power-of-two scale of V and block partials (precise forward)
+  F_VSC,     // f32  [1 + 256]        power-of-two scale s_v of V and block partials (fp16 operands)
   F_COUNT
 };
 
@@ -45,11 +47,15 @@ enum BwdBuf {
   B_SYNC,      // i32  [NC][H] + 64     per (chunk, head): reverse-scan value slices whose dS / dVn are stored,
                //                       then at [NC][H] the count of resident reverse-scan workgroups
                //                       (bwd_dkw beside the scan; zeroed by bwd_local)
+  B_DSC,       // f32  [1 + 256]        power-of-two scale s_d of dO and block partials (fp16 operands)
   B_COUNT
 };
 
 constexpr size_t kAlign = 256;
-constexpr int kVscaleBlocks = 256;  // partial maxima behind the precise forward's V scale
+constexpr int kVscaleBlocks = 256;  // partial maxima behind the fp16 paths' scales of V and dO
+// the scales bring max|V| (and the initial state) into [2^(t-1), 2^t): t for inference, and
+// for training, where the backward also keeps products of V- and dO-scaled values in fp16
+constexpr int kVscaleTarget = 6, kVscaleTargetTraining = 3;
 
 inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
@@ -76,6 +82,7 @@ inline void bwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   s[B_KNP] = ev * 128 * 2;
   s[B_WT] = chunk * 128 * 64 * 2;
   s[B_SYNC] = (chunk + 64) * 4;
+  s[B_DSC] = (1 + kVscaleBlocks) * 4;
 }
 
 // Offsets of every buffer; returns the total size in bytes.

@@ -11,7 +11,8 @@
 // registered for the CUDA dispatch key, which is what PyTorch-ROCm tensors on an AMD GPU carry;
 // nothing computes on the CPU (no fallback).
 //
-// Schemas (T events, H heads, time-first [1,T,H,128] bf16 q/k/v, fp32 [1,T,H] g/beta):
+// Schemas (T events, H heads, time-first [1,T,H,128] q/k/v of one dtype, bf16 or fp16 (which
+// sets CQGDN_FP16; outputs and gradients take that dtype), fp32 [1,T,H] g/beta):
 //   fwd(q, k, v, g, beta, table, doc, scale, flags, initial_state?, want_state) -> (o, state, ws)
 //       cqgdn_fwd; o is empty with CQGDN_NO_OUTPUT, state empty unless want_state
 //   bwd(q, k, v, g, beta, dy, table, doc, scale, flags, ws?) -> (dq, dk, dv, dg, dbeta)
@@ -48,12 +49,21 @@ at::Tensor bytes(size_t n, const at::Tensor& like) {
   return at::empty({(int64_t)(n ? n : 1)}, like.options().dtype(at::kByte));
 }
 
+// CQGDN_FP16 follows the tensors' dtype: q, k, v (and dy) share one, bf16 or fp16
+unsigned dtype_flag(const at::Tensor& q, std::initializer_list<const at::Tensor*> same) {
+  const auto dt = q.scalar_type();
+  TORCH_CHECK_VALUE(dt == at::kBFloat16 || dt == at::kHalf, "QKV must share BF16/FP16 dtype");
+  for (const at::Tensor* x : same) TORCH_CHECK_VALUE(x->scalar_type() == dt, "QKV must share BF16/FP16 dtype");
+  return dt == at::kHalf ? CQGDN_FP16 : 0u;
+}
+
 std::tuple<at::Tensor, at::Tensor, at::Tensor> fwd(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
                                                    const at::Tensor& g, const at::Tensor& beta,
                                                    const at::Tensor& table, const at::Tensor& doc, double scale,
                                                    int64_t flags, const std::optional<at::Tensor>& initial_state,
                                                    bool want_state) {
   TORCH_CHECK_VALUE(q.dim() == 4 && q.size(0) == 1 && q.size(3) == CQGDN_HEAD_DIM, "q must be [1,T,H,128]");
+  flags = (flags & ~(int64_t)CQGDN_FP16) | dtype_flag(q, {&k, &v});
   const int64_t T = q.size(1), H = q.size(2), n_chunks = table.size(0), n_docs = doc.numel() - 1;
   at::Tensor ws = bytes(cqgdn_fwd_workspace_size(T, (int)H, n_chunks), q);
   at::Tensor o = (flags & CQGDN_NO_OUTPUT) ? at::empty({0}, v.options()) : at::empty_like(v);
@@ -74,6 +84,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> bwd(
     const at::Tensor& dy, const at::Tensor& table, const at::Tensor& doc, double scale, int64_t flags,
     const std::optional<at::Tensor>& fwd_ws) {
   TORCH_CHECK_VALUE(v.dim() == 4 && v.size(0) == 1 && v.size(3) == CQGDN_HEAD_DIM, "v must be [1,T,H,128]");
+  flags = (flags & ~(int64_t)CQGDN_FP16) | dtype_flag(q, {&k, &v, &dy});
   const int64_t T = v.size(1), H = v.size(2), n_chunks = table.size(0), n_docs = doc.numel() - 1;
   at::Tensor bws = bytes(cqgdn_bwd_workspace_size(T, (int)H, n_chunks), v);
   at::Tensor dq = at::empty_like(v), dk = at::empty_like(v), dv = at::empty_like(v);

@@ -11,7 +11,8 @@
  * message of the last failure on the calling thread.
  *
  * Layouts (T = events, H = heads, D = 128 head dimension):
- *   q, k, v, o, dq, dk, dv, do : bf16 [T][H][D]   (the reference's TND order, B = 1)
+ *   q, k, v, o, dq, dk, dv, do : bf16 [T][H][D]   (the reference's TND order, B = 1);
+ *                                fp16 with CQGDN_FP16
  *   g, beta, dg, dbeta         : fp32 [T][H]
  *   chunk_table                : int32 [n_chunks][2] = (first event, length <= 64);
  *                                chunks never cross a document boundary
@@ -40,7 +41,7 @@ extern "C" {
 
 /* flags of cqgdn_fwd / cqgdn_bwd */
 #define CQGDN_NORMALIZE 1u /* l2-normalize q and k in the kernels (use_qk_l2norm_in_kernel=True) */
-#define CQGDN_TRAINING 2u  /* the workspace will feed cqgdn_bwd (bf16 operands; excludes CQGDN_PRECISE) */
+#define CQGDN_TRAINING 2u  /* the workspace will feed cqgdn_bwd (excludes CQGDN_PRECISE) */
 /* Inference forward with fp16 MFMA operands (11-bit mantissa instead of bf16's 8) for final
  * states within 1e-3 of an fp32 computation; V and the initial state are scaled by a power of
  * two inside the call so every fp16 operand stays in range.  Not combinable with CQGDN_TRAINING. */
@@ -49,6 +50,13 @@ extern "C" {
  * not written and may be NULL).  The backward's recompute of the reference's `fused` mode, which
  * keeps no w / h / v_new between the forward and the backward (ops/gated_delta_net.py:143-156,192-194). */
 #define CQGDN_NO_OUTPUT 8u
+/* q, k, v and o (cqgdn_fwd), and dout, dq, dk, dv (cqgdn_bwd, cqgdn_bwd_recompute) are fp16
+ * [T][H][D] instead of bf16, and every kernel computes with fp16 MFMA operands (as CQGDN_PRECISE
+ * does for bf16 inputs): the reference's fp16 training and prefill (ops/gated_delta_net.py:233-234).
+ * V, the initial state and (in the backward) dout are scaled by powers of two inside the calls so
+ * that the fp16 operands stay in range.  Combinable with CQGDN_TRAINING; a cqgdn_bwd call passes it
+ * exactly when the cqgdn_fwd call that made its workspace did. */
+#define CQGDN_FP16 16u
 
 /* Library version string, e.g. "cqgdn 0.1.0 gfx950". */
 const char* cqgdn_version(void);
@@ -73,7 +81,7 @@ int64_t cqgdn_chunk_table(const int64_t* bounds, int n_bounds, int32_t* table, i
  * per-row l2 scales, not normalized copies).
  */
 #define CQGDN_FWD_BUFFERS 10
-#define CQGDN_BWD_BUFFERS 7
+#define CQGDN_BWD_BUFFERS 8
 size_t cqgdn_fwd_workspace_size(int64_t T, int H, int64_t n_chunks);
 int cqgdn_fwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets, int count);
 size_t cqgdn_bwd_workspace_size(int64_t T, int H, int64_t n_chunks);
@@ -89,10 +97,11 @@ int cqgdn_bwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets
  *   scale          : output scale (the reference uses D^-0.5, ops/gated_delta_net.py:248)
  *   initial_state  : NULL or [n_docs][H][K][V] fp32 starting state per document
  *   final_state    : NULL or [n_docs][H][K][V] fp32, written with each document's last state
- *   o              : [T][H][D] bf16 output (time-first)
+ *   o              : [T][H][D] output (time-first), bf16 (fp16 with CQGDN_FP16)
  *   workspace      : >= cqgdn_fwd_workspace_size() bytes, 256-byte aligned
- *   flags          : CQGDN_NORMALIZE | (CQGDN_TRAINING or CQGDN_PRECISE); the reference's
- *                    prefill (ops/gated_delta_net.py:292-311) maps to NORMALIZE | PRECISE.
+ *   flags          : CQGDN_NORMALIZE | (CQGDN_TRAINING or CQGDN_PRECISE) | CQGDN_FP16 with fp16
+ *                    q/k/v/o; the reference's prefill (ops/gated_delta_net.py:292-311) maps to
+ *                    NORMALIZE | PRECISE (| FP16 for fp16 inputs).
  *                    A CQGDN_TRAINING forward takes no initial_state and no final_state.
  */
 int cqgdn_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta, int64_t T, int H,
@@ -139,7 +148,8 @@ int cqgdn_fwd_static_init(void);
  * The reference keeps the normalized q, k and their rstd (ctx.save_for_backward,
  * :184); this call takes the inputs q, k and forms the normalized rows from the
  * rstd kept in the workspace, rounded as the forward rounded them.  Gradients are
- * written in the input layouts: dq, dk, dv bf16 [T][H][D]; dg, dbeta fp32 [T][H].
+ * written in the input layouts: dq, dk, dv bf16 [T][H][D] (fp16 with CQGDN_FP16, which
+ * must match the forward's flags); dg, dbeta fp32 [T][H].
  */
 int cqgdn_bwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const void* dout,
               int64_t T, int H, const int32_t* chunk_table, int64_t n_chunks, const int32_t* doc_chunk, int n_docs,

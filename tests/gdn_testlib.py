@@ -12,6 +12,10 @@ import torch
 TOL_BF16 = 2e-2
 TOL_STATE = 1e-3
 TOL_INTER = 1e-2  # bf16-rounded intermediates (T, W, U, h, v_new, ...)
+# fp16 inputs on the fp16 kernels (CQGDN_FP16): operands with 11-bit mantissas instead of 8.  On
+# MI355X the outputs and gradients measured rel_l2 4e-4 .. 9e-4 (max_rel up to 9e-4) against the
+# float64 oracle of the fp16 values, ten times below the bf16 route's 5e-3.
+TOL_FP16 = 2e-3
 #  * A_log and dt_bias gradients: the reference's conditioned control error
 #    (scripts/validation/validate_qwen35_cq.py:84-101), ||a - b|| / ||sum_t |dg_t * dg_t/dp| || <= 0.025,
 #    where the denominator is the float64 sum of the absolute per-event contributions.  These two

@@ -43,7 +43,7 @@ def test_header_constants_match_binding():
     for name, value in (("CQGDN_FWD_BUFFERS", _lib.FWD_BUFFERS), ("CQGDN_BWD_BUFFERS", _lib.BWD_BUFFERS),
                         ("CQGDN_NORMALIZE", _lib.NORMALIZE), ("CQGDN_TRAINING", _lib.TRAINING),
                         ("CQGDN_PRECISE", _lib.PRECISE), ("CQGDN_NO_OUTPUT", _lib.NO_OUTPUT),
-                        ("CQGDN_EINVAL", _lib.EINVAL), ("CQGDN_EUNSUPPORTED", _lib.EUNSUPPORTED),
+                        ("CQGDN_FP16", _lib.FP16), ("CQGDN_EINVAL", _lib.EINVAL), ("CQGDN_EUNSUPPORTED", _lib.EUNSUPPORTED),
                         ("CQGDN_EHIP", _lib.EHIP)):
         m = re.search(rf"#define {name} (\d+)", text)
         assert m and int(m.group(1)) == value, name
@@ -98,6 +98,11 @@ def test_fwd_rejects_invalid_arguments_before_launch(lib):
     assert _fwd(lib, flags=_lib.PRECISE | _lib.TRAINING) == _lib.EINVAL
     assert b"PRECISE" in lib.cqgdn_last_error()
     assert _fwd(lib, flags=8) == _lib.EINVAL
+    assert _fwd(lib, flags=32) == _lib.EINVAL and b"unknown flags" in lib.cqgdn_last_error()
+    # fp16 inputs with either forward are valid requests: an invalid size still fails first
+    for flags in (_lib.FP16 | _lib.TRAINING, _lib.FP16 | _lib.PRECISE, _lib.FP16):
+        assert _fwd(lib, flags=flags | _lib.NORMALIZE, ws_bytes=100) == _lib.EINVAL
+        assert b"workspace" in lib.cqgdn_last_error()
 
 
 def test_bwd_checks_its_inputs_before_launch(lib):
@@ -119,6 +124,9 @@ def test_bwd_checks_its_inputs_before_launch(lib):
     assert bwd(k=ctypes.c_void_p(258)) == _lib.EINVAL and b"aligned" in lib.cqgdn_last_error()
     assert bwd(fws_bytes=100) == _lib.EINVAL and b"forward workspace" in lib.cqgdn_last_error()
     assert bwd(T=0, n_chunks=0) == _lib.OK  # nothing to do
+    assert bwd(T=0, n_chunks=0, flags=_lib.NORMALIZE | _lib.TRAINING | _lib.FP16) == _lib.OK
+    assert bwd(flags=_lib.NORMALIZE | _lib.TRAINING | _lib.FP16, q=None) == _lib.EINVAL
+    assert bwd(flags=_lib.PRECISE) == _lib.EINVAL and b"unknown flags" in lib.cqgdn_last_error()
 
 
 def _bwd_recompute(lib, **kw):
