@@ -48,12 +48,15 @@ constexpr int LDT = 72;   // bf16 row stride, 128 x 64 and 64 x 64 tiles
 // ---------------------------------------------------------------------------
 // bwd_local
 // ---------------------------------------------------------------------------
-template <class E>  // dscale: null in bf16; in fp16 the device scalar s_d
+// dscale: null in bf16; in fp16 the scale s_d of dO, which this kernel forms from the
+// partial maxima after dscale[0] (range_scale, target ds_target) and stores in
+// dscale[0] for bwd_dkw
+template <class E>
 __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
     const E* __restrict__ q, const E* __restrict__ k, const float* __restrict__ rq,
     const float* __restrict__ rk, const E* __restrict__ dout, const float* __restrict__ gc,
     const float* __restrict__ beta, const E* __restrict__ Tm,
-    const int32_t* __restrict__ chunks, int H, float scale, const float* __restrict__ dscale,
+    const int32_t* __restrict__ chunks, int H, float scale, float* __restrict__ dscale, int ds_target,
     E* __restrict__ dvlT, E* __restrict__ XT, E* __restrict__ knP, E* __restrict__ WT, int* __restrict__ sync) {
   typedef typename Vec<E>::x8 X8;
   constexpr bool F16 = __is_same(E, f16);
@@ -81,9 +84,13 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
   __shared__ __attribute__((aligned(16))) E dOs[64 * LDK];     // dO rows, then dv_local^T [v][s]
   __shared__ __attribute__((aligned(16))) float Gs[64];
   __shared__ __attribute__((aligned(16))) float Bs[64];
+  __shared__ float red[4];
   E* Qs = QK;
   E* Ks = QK + 64 * LDK;
   static_assert(64 * LDK >= 128 * 64, "dv_local^T fits the dO tile");
+  // fp16: this thread's partial maximum of |dO|, requested before the other loads
+  const float dpart = F16 ? range_partial4(dscale + 1) : 0.f;
+  float ds = 1.f;  // s_d (fp16), formed once the input loads are in flight
 
   // T rows t = 16 wave + r, for -W^T below (requested with the inputs)
   X8 at[2];
@@ -111,7 +118,7 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
       Bs[t] = keep_if(in, beta[ev]);
     }
     if constexpr (F16) {  // dO s_d (exact: a power of two, in range)
-      const float ds = *dscale;
+      ds = range_scale(dpart, ds_target, red);
 #pragma unroll
       for (int j = 0; j < 4; ++j) xd[j] = to8<E>(cvtf8(xd[j]) * ds);
     }
@@ -245,6 +252,7 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
       st8(out + v * D + 8 * part, ld8(xts + v * LDK + 8 * part));
     }
   }
+  if (F16 && blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) dscale[0] = ds;  // for bwd_dkw
 }
 
 // ---------------------------------------------------------------------------
@@ -1283,18 +1291,18 @@ static hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t stream) {
   int* ready = sync;                                 // [NC][H]
   int* resident = sync + (size_t)a.n_chunks * a.H;  // one count
   const bool beside = a.side != nullptr;
-  // fp16: the scales s_d (computed here) and s_v (the forward's)
+  // fp16: the scales s_d (partial maxima here, the scale itself in bwd_local) and s_v (the forward's)
   float* dsc = nullptr;
   const float* vsc = nullptr;
   if (__is_same(E, f16)) {
     dsc = reinterpret_cast<float*>(a.bws + a.boff[B_DSC]);
     vsc = Ff(F_VSC);
-    launch_range_scale(a.dout, true, (size_t)a.T * a.H * (D / 8), nullptr, 0, dout_scale_target(a.T), dsc, stream);
+    launch_range_partials(a.dout, true, (size_t)a.T * a.H * (D / 8), nullptr, 0, dsc, stream);
   }
   {
     TimedLaunch tl(K_BWD_LOCAL, stream);
     hipLaunchKernelGGL(bwd_local_kernel<E>, dim3(a.H, a.n_chunks), dim3(256), 0, stream, q, k, Ff(F_RQ), Ff(F_RK),
-                       dout, Ff(F_GC), a.beta, F(F_TM), a.chunks, a.H, a.scale, (const float*)dsc, B(B_DVLT),
+                       dout, Ff(F_GC), a.beta, F(F_TM), a.chunks, a.H, a.scale, dsc, dout_scale_target(a.T), B(B_DVLT),
                        B(B_XT), B(B_KNP), B(B_WT), sync);
   }
   if (beside) {

@@ -431,6 +431,33 @@ __device__ __forceinline__ void dma16(const void* src, void* lds) {
   __builtin_amdgcn_global_load_lds(src, (lds_void_ptr)lds, 16, 0, 0);
 }
 
+// ---- power-of-two range scales of the fp16 paths ---------------------------
+// The scale of V (or dO) is 2^(target - e) for the e with max|x| in [2^(e-1), 2^e),
+// and 1 when every value is zero or one is not finite.  A pass over x leaves 1024
+// partial maxima in scale[1 .. 1024]; the first kernel that needs the scale forms it
+// in each of its 256-thread workgroups, thread i contributing the largest of partials
+// i, i + 256, i + 512, i + 768 (range_partial4), and one workgroup stores it in
+// scale[0] for the kernels after it.  Every thread of the workgroup calls
+// range_scale (it holds a barrier); red: 4 floats of LDS.
+__device__ __forceinline__ float range_partial4(const float* part) {
+  const int i = threadIdx.x;
+  return fmaxf(fmaxf(part[i], part[i + 256]), fmaxf(part[i + 512], part[i + 768]));
+}
+__device__ __forceinline__ float range_scale(float m, int target, float* red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  lds_barrier();  // orders LDS only: the caller's global loads stay in flight
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float sc = 1.f;
+  if (m > 0.f && isfinite(m)) {
+    int e;
+    frexpf(m, &e);  // m < 2^e
+    sc = ldexpf(1.f, min(max(target - e, -60), 60));
+  }
+  return sc;
+}
+
 // ---- wave reductions -------------------------------------------------------
 // x of another lane of the same 16-lane row, by a DPP control (VALU only, no LDS)
 template <int CTRL>

@@ -29,13 +29,15 @@ constexpr int LDA = 65;   // row stride (fp32) of the 64 x 64 solve matrix
 // fwd_prep
 // ---------------------------------------------------------------------------
 // I: input element type of q, k, v (bf16 or f16).  E: operand element type (bf16,
-// or f16 for the precise forward and for fp16 inputs).  vscale: null, or the
-// power-of-two factor applied to V (fp16 range, see vscale_final_kernel).
+// or f16 for the precise forward and for fp16 inputs).  vscale: with f16 operands,
+// the power-of-two factor applied to V (fp16 range), which this kernel forms from
+// the partial maxima after vscale[0] (range_scale, target vs_target) and stores in
+// vscale[0] for the scan and the output kernel; null with bf16 operands.
 template <class I, class E, bool NORMALIZE>
 __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     const I* __restrict__ q, const I* __restrict__ k, const I* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const int32_t* __restrict__ chunks,
-    int H, const float* __restrict__ vscale, float* __restrict__ rq,
+    int H, float* __restrict__ vscale, int vs_target, float* __restrict__ rq,
     float* __restrict__ rk, float* __restrict__ gc, E* __restrict__ Tm, E* __restrict__ W,
     E* __restrict__ UT, E* __restrict__ KgT) {
   typedef typename Vec<E>::x8 X8;
@@ -54,7 +56,11 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
   __shared__ __attribute__((aligned(16))) E Ks[64 * LDK];      // K rows, then (beta gam K) rows
   __shared__ __attribute__((aligned(16))) float Af[64 * LDA];  // the solve's matrix, then the KgT tile
   __shared__ __attribute__((aligned(16))) E Ts[64 * LDT];
-  const float vs = vscale ? *vscale : 1.f;
+  __shared__ float red[4];
+  // fp16 operands (the only ones with a scale): this thread's partial maximum of
+  // |V|, requested before the other loads
+  constexpr bool SCALED = __is_same(E, f16);
+  const float vpart = SCALED ? range_partial4(vscale + 1) : 0.f;
 
   // Every global load is issued first, before any store (a wait for a load
   // also waits for every store issued before it), so the kernel pays one memory
@@ -90,6 +96,10 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) vg[nn][kb] = col8_load_rows(vb, H * D, 32 * kb, 16 * (2 * wave + nn), ci.len);
   }
+  // the scale of V, while the loads above are in flight (stored for the kernels
+  // after this one at the end, where the store holds up no wait for a load)
+  float vs = 1.f;
+  if constexpr (SCALED) vs = range_scale(vpart, vs_target, red);
   const int rowe = H * D * (int)sizeof(E);  // bytes per event row of W
   const int rows_bytes = ((ci.len - 1) * H + 1) * D * (int)sizeof(E);
   const int gate_bytes = ((ci.len - 1) * H + 1) * (int)sizeof(float);
@@ -350,6 +360,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
       st8(kgt + kr * CH + 8 * part, ld8(kgs + kr * CH + 8 * (part ^ (2 * ((kr >> 3) & 3)))));
     }
   }
+  if (SCALED && blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) vscale[0] = vs;
 }
 
 // ---------------------------------------------------------------------------
@@ -828,7 +839,7 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
 // t = 6 for inference, far inside fp16's range (65504) for U, v_new and the
 // state; t = 3 for training, where the backward multiplies V-scaled by
 // dO-scaled quantities (dP, dW) and keeps their products in fp16 too.  The same
-// kernels give the backward's scale of dO (launch_range_scale).
+// kernels give the backward's scale of dO (launch_range_partials, then bwd_local).
 // ---------------------------------------------------------------------------
 constexpr int VS_BLOCKS = kVscaleBlocks;
 
@@ -847,38 +858,32 @@ __global__ __launch_bounds__(256) void vscale_partial_kernel(const I* __restrict
   __shared__ float red[4];
   float m = 0.f;
   const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv8; i += stride) {
-    const f32x8 x = cvtf8(ld8(v + 8 * i));
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // eight 16-byte loads in flight per thread: one at a time, the loop waits out a
+  // memory round trip per load and reads at about a quarter of HBM's rate
+  // (the last round's loads past the end are skipped lane by lane, all in one round trip)
+  constexpr int U = 8;
+  for (; i < nv8; i += U * stride) {
+    typename Vec<I>::x8 x[U];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) m = fmaxf(m, fabsf(x[s]));
+    for (int u = 0; u < U; ++u) x[u] = i + u * stride < nv8 ? ld8(v + 8 * (i + u * stride)) : zero8v<I>();
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const f32x8 f = cvtf8(x[u]);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) m = fmaxf(m, fabsf(f[s]));
+    }
   }
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < ns; i += stride) m = fmaxf(m, fabsf(s0[i]));
   m = block_max(m, red);
   if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
-__global__ __launch_bounds__(256) void vscale_final_kernel(const float* __restrict__ part, int n, int target,
-                                                           float* __restrict__ vscale) {
-  __shared__ float red[4];
-  float m = 0.f;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) m = fmaxf(m, part[i]);
-  m = block_max(m, red);
-  if (threadIdx.x == 0) {
-    float sc = 1.f;
-    if (m > 0.f && isfinite(m)) {
-      int e;
-      frexpf(m, &e);  // m < 2^e
-      sc = ldexpf(1.f, min(max(target - e, -60), 60));
-    }
-    vscale[0] = sc;
-  }
-}
-
 // ---------------------------------------------------------------------------
 // host launchers
 // ---------------------------------------------------------------------------
 template <class I, class E>
-static hipError_t launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_t stream) {
+static hipError_t launch_fwd_t(const FwdArgs& a, float* vscale, int vs_target, hipStream_t stream) {
   E* ws[F_COUNT];
   for (int i = 0; i < F_COUNT; ++i) ws[i] = reinterpret_cast<E*>(a.ws + a.off[i]);
   float* rq = reinterpret_cast<float*>(ws[F_RQ]);
@@ -892,11 +897,11 @@ static hipError_t launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_
     const dim3 grid_p(a.H, a.n_chunks);
     if (a.normalize)
       hipLaunchKernelGGL((fwd_prep_kernel<I, E, true>), grid_p, dim3(256), 0, stream, q, k, v, a.g, a.beta,
-                         a.chunks, a.H, vscale, rq, rk, gcum, ws[F_TM], ws[F_W],
+                         a.chunks, a.H, vscale, vs_target, rq, rk, gcum, ws[F_TM], ws[F_W],
                          ws[F_UT], ws[F_KGT]);
     else
       hipLaunchKernelGGL((fwd_prep_kernel<I, E, false>), grid_p, dim3(256), 0, stream, q, k, v, a.g, a.beta,
-                         a.chunks, a.H, vscale, rq, rk, gcum, ws[F_TM], ws[F_W],
+                         a.chunks, a.H, vscale, vs_target, rq, rk, gcum, ws[F_TM], ws[F_W],
                          ws[F_UT], ws[F_KGT]);
   }
   const dim3 grid_s(a.H * (D / 16), a.n_docs);
@@ -920,25 +925,25 @@ static hipError_t launch_fwd_t(const FwdArgs& a, const float* vscale, hipStream_
   return hipSuccess;
 }
 
-void launch_range_scale(const void* x, bool fp16, size_t n8, const float* s0, size_t ns, int target, float* out,
-                        hipStream_t stream) {
+void launch_range_partials(const void* x, bool fp16, size_t n8, const float* s0, size_t ns, float* out,
+                           hipStream_t stream) {
+  static_assert(VS_BLOCKS == 4 * 256, "range_partial4 takes four partials per thread of a 256-thread workgroup");
   if (fp16)
     hipLaunchKernelGGL(vscale_partial_kernel<f16>, dim3(VS_BLOCKS), dim3(256), 0, stream,
                        static_cast<const f16*>(x), n8, s0, ns, out + 1);
   else
     hipLaunchKernelGGL(vscale_partial_kernel<bf16>, dim3(VS_BLOCKS), dim3(256), 0, stream,
                        static_cast<const bf16*>(x), n8, s0, ns, out + 1);
-  hipLaunchKernelGGL(vscale_final_kernel, dim3(1), dim3(256), 0, stream, out + 1, VS_BLOCKS, target, out);
 }
 
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream) {
-  if (!a.precise && !a.fp16) return launch_fwd_t<bf16, bf16>(a, nullptr, stream);
+  if (!a.precise && !a.fp16) return launch_fwd_t<bf16, bf16>(a, nullptr, 0, stream);
   float* vsc = reinterpret_cast<float*>(a.ws + a.off[F_VSC]);
   const size_t nv8 = (size_t)a.T * a.H * (D / 8);
   const size_t ns = a.initial_state ? (size_t)a.n_docs * a.H * D * D : 0;
-  launch_range_scale(a.v, a.fp16, nv8, a.initial_state, ns, a.training ? kVscaleTargetTraining : kVscaleTarget,
-                     vsc, stream);
-  return a.fp16 ? launch_fwd_t<f16, f16>(a, vsc, stream) : launch_fwd_t<bf16, f16>(a, vsc, stream);
+  launch_range_partials(a.v, a.fp16, nv8, a.initial_state, ns, vsc, stream);
+  const int target = a.training ? kVscaleTargetTraining : kVscaleTarget;
+  return a.fp16 ? launch_fwd_t<f16, f16>(a, vsc, target, stream) : launch_fwd_t<bf16, f16>(a, vsc, target, stream);
 }
 
 }  // namespace cqgdn

@@ -63,11 +63,11 @@ struct BwdArgs {
 // launch errors are left for hipGetLastError.
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t stream);
 hipError_t launch_bwd(const BwdArgs& a, hipStream_t stream);
-// out[0] = 2^(target - e) for the e with max|x| in [2^(e-1), 2^e) over n8 groups of 8
-// values of x (bf16, or fp16) and ns fp32 values of s0 (1 if all are zero or one is not
-// finite); out[1 .. kVscaleBlocks] take the partial maxima (gdn_fwd.hip)
-void launch_range_scale(const void* x, bool fp16, size_t n8, const float* s0, size_t ns, int target, float* out,
-                        hipStream_t stream);
+// out[1 .. kVscaleBlocks] = partial maxima of |x| over n8 groups of 8 values of x (bf16,
+// or fp16) and ns fp32 values of s0; the first kernel that needs the power-of-two scale
+// forms it from them (range_scale in gdn_common.hpp) and stores it in out[0] (gdn_fwd.hip)
+void launch_range_partials(const void* x, bool fp16, size_t n8, const float* s0, size_t ns, float* out,
+                           hipStream_t stream);
 
 void launch_recurrent(const void* q, const void* k, const void* v, const float* g, const void* beta,
                       bool beta_bf16, bool fp16, float* state, void* out, int N, int E, int H, float scale,

@@ -33,7 +33,7 @@ enum FwdBuf {
   F_KGT,     // bf16 [NC][H][D][64]   (K * exp(G_last - G)) transposed (k, t), perm32 columns
   F_HT,      // bf16 [NC][H][D][D]    state entering the chunk, (v, k)
   F_VNT,     // bf16 [NC][H][D][64]   v_new transposed (v, t)
-  F_VSC,     // f32  [1 + 256]        power-of-two scale s_v of V and block partials (fp16 operands)
+  F_VSC,     // f32  [1 + 1024]       power-of-two scale s_v of V and block partials (fp16 operands)
   F_COUNT
 };
 
@@ -47,12 +47,12 @@ enum BwdBuf {
   B_SYNC,      // i32  [NC][H] + 64     per (chunk, head): reverse-scan value slices whose dS / dVn are stored,
                //                       then at [NC][H] the count of resident reverse-scan workgroups
                //                       (bwd_dkw beside the scan; zeroed by bwd_local)
-  B_DSC,       // f32  [1 + 256]        power-of-two scale s_d of dO and block partials (fp16 operands)
+  B_DSC,       // f32  [1 + 1024]       power-of-two scale s_d of dO and block partials (fp16 operands)
   B_COUNT
 };
 
 constexpr size_t kAlign = 256;
-constexpr int kVscaleBlocks = 256;  // partial maxima behind the fp16 paths' scales of V and dO
+constexpr int kVscaleBlocks = 1024;  // partial maxima behind the fp16 paths' scales of V and dO
 // the scales bring max|V| (and the initial state) into [2^(t-1), 2^t): t for inference, and
 // for training, where the backward also keeps products of V- and dO-scaled values in fp16
 constexpr int kVscaleTarget = 6, kVscaleTargetTraining = 3;
