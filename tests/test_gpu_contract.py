@@ -444,14 +444,18 @@ def test_fused_mode_matches_cached_mode_at_config2_size(gdn, monkeypatch):
         assert torch.equal(a, b), name
 
 
-@pytest.mark.parametrize("T,bounds,H", [(700, (0, 300, 700), 8), (4200, (0, 4200), 16)])
-def test_bwd_recompute_graph_replay(gdn, T, bounds, H):
+@pytest.mark.parametrize("T,bounds,H,dtype", [(700, (0, 300, 700), 8, torch.bfloat16),
+                                               (4200, (0, 4200), 16, torch.bfloat16),
+                                               (4200, (0, 4200), 16, torch.float16)])
+def test_bwd_recompute_graph_replay(gdn, T, bounds, H, dtype):
     """cqgdn_bwd_recompute (the fused-mode backward: forward rebuilt in the call, its state scan on a
-    second stream joined back by events) captured in a HIP graph, at two sizes: each replay, with eager
-    work between, equals the eager call bitwise."""
-    print(f"case bwd_recompute graph replay T={T} bounds={bounds} H={H}", flush=True)
+    second stream joined back by events) captured in a HIP graph, at two sizes and with fp16 inputs
+    (whose range scales are formed inside the call): each replay, with eager work between, equals the
+    eager call bitwise."""
+    print(f"case bwd_recompute graph replay T={T} bounds={bounds} H={H} {dtype}", flush=True)
     q, k, v, g, b = (x.to(DEV).contiguous() for x in inputs(T, H, seed=4242))
-    dy = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(4243)).bfloat16().to(DEV)
+    q, k, v = (x.to(dtype) for x in (q, k, v))
+    dy = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(4243)).to(dtype).to(DEV)
 
     def run():
         return gdn._backward(q, k, v, g, b, None, dy, bounds, True, 128 ** -0.5)
@@ -576,14 +580,16 @@ def test_bwd_dkw_wait_gives_up_with_nan_not_a_hang(gdn, monkeypatch):
         assert bool(torch.isnan(x.float()).all()), name
 
 
-def test_bwd_beside_scan_graph_replay(gdn):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_bwd_beside_scan_graph_replay(gdn, dtype):
     """The cached backward with bwd_dkw beside the reverse scan (second stream, fork and join events,
-    the counts zeroed by bwd_local inside the call) captured in a HIP graph: each replay, with eager
-    work between, equals the eager call bitwise."""
+    the counts zeroed by bwd_local inside the call; with fp16 inputs also the scale of dO) captured in a
+    HIP graph: each replay, with eager work between, equals the eager call bitwise."""
     T, bounds, H = 4200, (0, 4200), 16
-    print(f"case cached bwd beside the scan, graph replay T={T} H={H}", flush=True)
+    print(f"case cached bwd beside the scan, graph replay T={T} H={H} {dtype}", flush=True)
     q, k, v, g, b = (x.to(DEV).contiguous() for x in inputs(T, H, seed=4343))
-    dy = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(4344)).bfloat16().to(DEV)
+    q, k, v = (x.to(dtype) for x in (q, k, v))
+    dy = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(4344)).to(dtype).to(DEV)
     _, _, ws = gdn._forward(q, k, v, g, b, bounds, True, 128 ** -0.5, training=True)
 
     def run():

@@ -1,7 +1,7 @@
 """cqgdn_fwd_static, the forward that allocates nothing (include/cqgdn.h), through the C ABI.
 
-It must give exactly what cqgdn_fwd gives with a caller workspace (same kernels, same inputs),
-on two calls in a row -- the second smaller, so it runs over what the first left in the shared
+It must give exactly what cqgdn_fwd gives with a caller workspace (same kernels, same inputs; bf16
+and fp16 q/k/v), on two calls in a row -- the second smaller, so it runs over what the first left in the shared
 static workspace -- leave the device's free memory unchanged once cqgdn_fwd_static_init has reserved
 the static array on the device (a second set-up reserves nothing more), replay from a HIP graph it was captured into with the results of
 the eager call, and reject what it cannot serve: a workspace larger than its static one, and a
@@ -27,7 +27,7 @@ def _run(gdn, lib, xs, bounds, static, initial_state=None, free_bytes=None):
     o = torch.empty_like(v)
     state = torch.empty(nd, H, 128, 128, dtype=torch.float32, device=DEV)
     init = None if initial_state is None else initial_state.to(DEV).contiguous()
-    flags = _lib.NORMALIZE | _lib.PRECISE
+    flags = _lib.NORMALIZE | _lib.PRECISE | (_lib.FP16 if q.dtype == torch.float16 else 0)
     P = gdn._ptr
     common = (P(q), P(k), P(v), P(g), P(b), T, H, P(table), nc, P(doc), nd, 128 ** -0.5, flags, P(init), P(state),
               P(o))
@@ -60,10 +60,12 @@ def test_static_forward_matches_workspace_forward(gdn):
     assert lib.cqgdn_fwd_static_init() == 0, lib.cqgdn_last_error().decode()
     torch.cuda.synchronize()
     assert torch.cuda.mem_get_info()[0] == middle, "a second set-up reserved memory again"
-    cases = [(1900, (0, 700, 1900), 16, None), (300, (0, 129, 300), 16, 0.05)]  # the second one smaller
-    for T, bounds, H, s0 in cases:
-        print(f"case static forward T={T} bounds={bounds} H={H}", flush=True)
-        xs = synthetic.make_inputs(T, H, 128, seed=T)
+    # each second call smaller than the one before it; then the same with fp16 q/k/v (CQGDN_FP16)
+    cases = [(1900, (0, 700, 1900), 16, None, torch.bfloat16), (300, (0, 129, 300), 16, 0.05, torch.bfloat16),
+             (1200, (0, 500, 1200), 16, 0.05, torch.float16), (257, (0, 257), 16, None, torch.float16)]
+    for T, bounds, H, s0, dtype in cases:
+        print(f"case static forward T={T} bounds={bounds} H={H} {dtype}", flush=True)
+        xs = [x.to(dtype) if x.dim() == 4 else x for x in synthetic.make_inputs(T, H, 128, seed=T)]
         init = None if s0 is None else torch.randn(len(bounds) - 1, H, 128, 128,
                                                    generator=torch.Generator().manual_seed(5)) * s0
         o_ws, st_ws = _run(gdn, lib, xs, bounds, False, init)
