@@ -23,7 +23,8 @@ Printed: one JSON line with the contract keys, plus
   cpu_baseline  the fp32 chunked torch oracle on this host's cores (a bounded
                 sample: one config-2 fwd+bwd; rows: one config-0 forward and the
                 config-4 decode step)
-  extra         config-1 and config-3 fwd+bwd, per-kernel table (MFMA / HBM
+  extra         config-1 and config-3 fwd+bwd, config-2 fwd+bwd in the fused mode and
+                with fp16 inputs, per-kernel table (MFMA / HBM
                 fractions), the whole GatedDelta layer at width 2048 (content 2048 and
                 8192 on image-CQ plans, beside the reference's published Ascend 910B
                 medians), prefill, and the decode step (B=64, 256 steps, GB/s)
@@ -66,6 +67,8 @@ def parse_args():
                          "known size (the scale of the HBM byte counters); prints no JSON")
     ap.add_argument("--config", type=int, default=2, choices=(1, 2, 3),
                     help="with --profile: the benchmark configuration whose fwd+bwd steps are profiled")
+    ap.add_argument("--fp16", action="store_true",
+                    help="with --profile: fp16 q/k/v and dO (the fp16 kernels, CQGDN_FP16)")
     ap.add_argument("--dkw-after-scan", action="store_true",
                     help="with --profile: bwd_dkw after the reverse scan (CQGDN_DKW_BESIDE_SCAN=0), the "
                          "pass the per-kernel table and the roofline are measured in")
@@ -450,8 +453,9 @@ def main():
     if args.profile:
         if args.dkw_after_scan:
             os.environ[DKW_ENV] = "0"
-        log(f"config {args.config} fwd+bwd (profile{', bwd_dkw after the scan' if args.dkw_after_scan else ''})")
-        _, _, step, _ = training_case(gdn, synthetic, torch, args.config, device)
+        log(f"config {args.config} fwd+bwd (profile{', bwd_dkw after the scan' if args.dkw_after_scan else ''}"
+            f"{', fp16 inputs' if args.fp16 else ''})")
+        _, _, step, _ = training_case(gdn, synthetic, torch, args.config, device, fp16=args.fp16)
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
