@@ -621,8 +621,8 @@ def test_delta_fp16_inputs_match_oracle(gdn, monkeypatch, mode):
     kernels (CQGDN_FP16) forward and backward: output and gradients come back in the input dtypes and
     match the float64 oracle of the same fp16 values to TOL_FP16.  The values are drawn in fp32 and
     rounded to fp16, so most of them are not bf16 values.  Beside it, the same values rounded to bf16
-    run through the bf16 kernels (the route fp16 inputs took before the fp16 kernels), measured
-    against the same oracle: every output of the fp16 route is at least four times closer."""
+    run through the bf16 kernels (8-bit mantissas in place of fp16's 11), measured against the same
+    oracle: every output of the fp16 route is at least four times closer."""
     monkeypatch.setattr(gdn, "MODE", mode)
     T, bounds, H = 257, (0, 100, 257), 8
     print(f"case fp16 inputs T={T} bounds={bounds} mode={mode}", flush=True)
