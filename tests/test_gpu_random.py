@@ -5,8 +5,9 @@ documents with empty, one-event, partial-chunk, whole-chunk and multi-chunk leng
 (host_bounds allows empty documents, ops/gated_delta_net.py:102-114), a share of read-only
 CQ events (k = v = g = beta = 0, tests/test_qwen35_cq.py), the in-kernel l2norm on or off and
 both backward modes, then compares the output and all five gradients with the oracle
-(the reference's NPU gate: relative L2 within 2e-2).  The prefill cases add random initial
-states and compare the per-document final states to 1e-3.
+(the reference's NPU gate: relative L2 within 2e-2).  The fp16 cases draw the same kinds of
+batches with fp16 q/k/v and dO (the fp16 kernels, CQGDN_FP16) and hold them to TOL_FP16.  The
+prefill cases add random initial states and compare the per-document final states to 1e-3.
 """
 
 import random
@@ -14,7 +15,7 @@ import random
 import pytest
 import torch
 
-from gdn_testlib import TOL_STATE, assert_close_bf16, rel_l2
+from gdn_testlib import TOL_BF16, TOL_FP16, TOL_STATE, assert_close_bf16, rel_l2
 from oracle import gdn_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -35,36 +36,46 @@ def draw_case(seed):
     return H, tuple(bounds), rnd.choice([0.0, 0.0, 0.25]), rnd.random() < 0.75, rnd.choice(["cached", "fused"])
 
 
-def make(T, H, seed, readonly_share, normalize):
+def make(T, H, seed, readonly_share, normalize, dtype=torch.bfloat16):
     from cqgdn import synthetic
 
     gen = torch.Generator().manual_seed(7000 + seed)
     readonly = (torch.rand(T, generator=gen) < readonly_share) if readonly_share else None
-    q, k, v, g, b = synthetic.make_inputs(T, H, 128, seed=8000 + seed, readonly=readonly)
+    q, k, v, g, b = synthetic.make_inputs(T, H, 128, seed=8000 + seed, readonly=readonly, dtype=dtype)
     if not normalize:  # callers that normalize themselves pass unit rows (zero rows stay zero)
-        q, k = (O.l2norm(x.double()).bfloat16() for x in (q, k))
+        q, k = (O.l2norm(x.double()).to(dtype) for x in (q, k))
     return [q, k, v, g, b]
 
 
-@pytest.mark.parametrize("seed", range(12))
-def test_random_training_case_matches_oracle(gdn, monkeypatch, seed):
+def _training_case(gdn, monkeypatch, seed, dtype, tol):
     H, bounds, ro, normalize, mode = draw_case(seed)
     T = bounds[-1]
-    print(f"case seed={seed} T={T} bounds={bounds} H={H} readonly={ro} normalize={normalize} mode={mode}",
-          flush=True)
+    print(f"case seed={seed} T={T} bounds={bounds} H={H} readonly={ro} normalize={normalize} mode={mode} "
+          f"{dtype}", flush=True)
     monkeypatch.setattr(gdn, "MODE", mode)
-    xs = make(T, H, seed, ro, normalize)
-    do = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(9000 + seed)).bfloat16()
+    xs = make(T, H, seed, ro, normalize, dtype)
+    do = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(9000 + seed)).to(dtype)
     xd = [x.to(DEV).requires_grad_() for x in xs]
     cu = torch.tensor(bounds, device=DEV)
     y, _ = gdn.delta(*xd, use_qk_l2norm_in_kernel=normalize, cu_seqlens=cu, cu_seqlens_cpu=list(bounds))
     y.backward(do.to(DEV))
     torch.cuda.synchronize()
+    assert y.dtype == dtype and all(x.grad.dtype == x.dtype for x in xd)
     q, k, v, g, b = (x.double() for x in xs)
-    assert_close_bf16("o", y.detach().cpu(), O.chunk_delta(q, k, v, g, b, bounds, normalize=normalize))
+    assert_close_bf16("o", y.detach().cpu(), O.chunk_delta(q, k, v, g, b, bounds, normalize=normalize), tol=tol)
     ref = O.chunk_delta_backward(q, k, v, g, b, do.double(), bounds, normalize=normalize)
     for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta"), xd, ref):
-        assert_close_bf16(name, x.grad.cpu(), r)
+        assert_close_bf16(name, x.grad.cpu(), r, tol=tol)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_training_case_matches_oracle(gdn, monkeypatch, seed):
+    _training_case(gdn, monkeypatch, seed, torch.bfloat16, TOL_BF16)
+
+
+@pytest.mark.parametrize("seed", range(200, 208))
+def test_random_fp16_training_case_matches_oracle(gdn, monkeypatch, seed):
+    _training_case(gdn, monkeypatch, seed, torch.float16, TOL_FP16)
 
 
 @pytest.mark.parametrize("seed", range(100, 106))
