@@ -14,6 +14,7 @@
   of ops/gated_delta_layout.py:66-83), and on a projection that is a column slice of a wider tensor.
 """
 
+import numpy as np
 import pytest
 import torch
 
@@ -557,6 +558,39 @@ def test_bwd_dkw_beside_scan_matches_after_scan(gdn, kind, monkeypatch):
         ref = O.chunk_delta_backward(*(x.double() for x in xs), do.double(), bounds)
         for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta"), beside, ref):
             assert_close_bf16(name, x, r, tol=TOL_FP16 if kind.endswith("fp16") else TOL_BF16)
+
+
+# seeds chosen to cover 4 heads x 3 and 4 documents, 8 x 1 and 2, 16 x 1, in both types
+@pytest.mark.parametrize("seed", [300, 302, 306, 308, 310, 314, 316, 318])
+def test_bwd_dkw_beside_scan_random_cases_bit_identical(gdn, seed, monkeypatch):
+    """Random cases that run bwd_dkw beside the reverse scan: 4, 8 or 16 heads, as many documents
+    (at most four) as leave half of the CUs free, each of 64 to 93 chunks with a ragged end, a fifth
+    of the rows read-only at random, bf16 or fp16.  The gradients equal those of the after-the-scan
+    path bitwise, none is NaN, and every chunk-head's count reaches the scan's eight value slices."""
+    rng = np.random.default_rng(seed)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    H = int(rng.choice([4, 8, 16]))
+    n_docs = int(rng.integers(1, max(1, min(4, cus // (16 * H))) + 1))
+    lens = [int(rng.integers(64 * 64, 64 * 94)) for _ in range(n_docs)]
+    bounds = tuple(int(x) for x in np.concatenate([[0], np.cumsum(lens)]))
+    T = bounds[-1]
+    fp16 = bool(rng.integers(0, 2))
+    mask = torch.from_numpy(rng.random(T) < 0.2)
+    nc = gdn.device_metadata(bounds, DEV)[1].shape[0]
+    print(f"case random beside seed={seed}: H={H} docs={n_docs} T={T} chunks={nc} fp16={fp16}", flush=True)
+    assert _beside(H, n_docs, nc)
+    xs = inputs(T, H, seed=seed, readonly=mask)
+    do = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(seed + 1)).bfloat16()
+    if fp16:
+        xs = [x.half() if x.dim() == 4 else x for x in xs]
+        do = do.half()
+    after, ready_a, resident_a = _bwd_direct(gdn, xs, bounds, do, False, monkeypatch)
+    beside, ready_b, resident_b = _bwd_direct(gdn, xs, bounds, do, True, monkeypatch)
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dbeta"), after, beside):
+        assert not torch.isnan(a.float()).any(), name
+        assert torch.equal(a, b), name
+    assert not ready_a.any() and resident_a == 0
+    assert bool((ready_b == 8).all()) and resident_b == H * 8 * n_docs, (ready_b.unique(), resident_b)
 
 
 def test_bwd_dkw_wait_gives_up_with_nan_not_a_hang(gdn, monkeypatch):
