@@ -64,7 +64,8 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
   // follows reads the last chunks first, and they are then the most recently
   // written (still in the memory-side cache).  The scan's other two operands,
   // the perm32 copy of Kn and -W^T, are made here for the same reason.
-  const int h = blockIdx.x, c = blockIdx.y;
+  const HeadChunk hc = xcd_head_chunk(gridDim.x, gridDim.y);  // all heads of a chunk on one XCD
+  const int h = hc.h, c = hc.p;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);
@@ -593,7 +594,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     inv_d = 1.f / *dscale;
     inv_dv = inv_d / vs;
   }
-  const int h = blockIdx.x, c = ready ? gridDim.y - 1 - blockIdx.y : blockIdx.y;
+  const HeadChunk hc = xcd_head_chunk(gridDim.x, gridDim.y);  // all heads of a chunk on one XCD
+  const int h = hc.h, c = ready ? gridDim.y - 1 - hc.p : hc.p;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);

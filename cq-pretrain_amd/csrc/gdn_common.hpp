@@ -642,4 +642,27 @@ __device__ __forceinline__ ChunkInfo chunk_info(const int32_t* table, int c) {
   return ChunkInfo{table[2 * c], table[2 * c + 1]};
 }
 
+// The (head, chunk position) of this workgroup in a grid of (H, NC) chunk-heads.
+// The dispatcher deals consecutive workgroups out to the XCDs in turn, so with the
+// plain mapping (head = blockIdx.x) each XCD holds H / 8 heads of every chunk, and
+// each line of an fp32 [T][H] array (g, beta, the norms, dg: 128 bytes = two events of
+// all 16 heads) is fetched into all eight L2s.  Here the j-th workgroup an XCD receives
+// takes head j % H of chunk position 8 (j / H) + xcd: all heads of a chunk run on one
+// XCD, at about the same time, and share those lines in its L2.  Positions still come
+// in blocks of eight chunks in dispatch order; the last NC % 8 positions keep the plain
+// mapping.  A bijection of [0, H NC) for any H, NC.
+constexpr int kXcds = 8;
+struct HeadChunk {
+  int h, p;
+};
+__device__ __forceinline__ HeadChunk xcd_head_chunk(int H, int NC) {
+  const int i = blockIdx.y * gridDim.x + blockIdx.x;  // dispatch order
+  const int full = NC / kXcds * kXcds;
+  if (i < full * H) {
+    const int xcd = i % kXcds, j = i / kXcds;
+    return HeadChunk{j % H, j / H * kXcds + xcd};
+  }
+  return HeadChunk{i % H, i / H};
+}
+
 }  // namespace cqgdn

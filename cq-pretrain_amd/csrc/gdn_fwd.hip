@@ -45,7 +45,8 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
   // grid (H, NC), chunks dispatched last to first: the state scan reads the
   // first chunks first, and they are then the most recently written (still in
   // the memory-side cache)
-  const int h = blockIdx.x, c = gridDim.y - 1 - blockIdx.y;
+  const HeadChunk hc = xcd_head_chunk(gridDim.x, gridDim.y);  // all heads of a chunk on one XCD
+  const int h = hc.h, c = gridDim.y - 1 - hc.p;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);
@@ -720,7 +721,8 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
   typedef typename Vec<E>::x8 X8;
   // grid (H, NC), chunks last to first: the state scan wrote the last chunks
   // last, so they are the likeliest still in the memory-side cache
-  const int h = blockIdx.x, c = gridDim.y - 1 - blockIdx.y;
+  const HeadChunk hc = xcd_head_chunk(gridDim.x, gridDim.y);  // all heads of a chunk on one XCD
+  const int h = hc.h, c = gridDim.y - 1 - hc.p;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, q4 = lane >> 4;
   const ChunkInfo ci = chunk_info(chunks, c);
