@@ -650,15 +650,17 @@ __device__ __forceinline__ ChunkInfo chunk_info(const int32_t* table, int c) {
 // takes head j % H of chunk position 8 (j / H) + xcd: all heads of a chunk run on one
 // XCD, at about the same time, and share those lines in its L2.  Positions still come
 // in blocks of eight chunks in dispatch order; the last NC % 8 positions keep the plain
-// mapping.  A bijection of [0, H NC) for any H, NC.
-constexpr int kXcds = 8;
+// mapping.  A bijection of [0, H NC) for any H, NC.  Below kXcdMapMinChunks chunks the
+// plain mapping is kept: those arrays are then small, and at 36 chunks (config 1) the
+// mapping made the step 1% slower where at 144 it made it 1% faster.
+constexpr int kXcds = 8, kXcdMapMinChunks = 64;
 struct HeadChunk {
   int h, p;
 };
 __device__ __forceinline__ HeadChunk xcd_head_chunk(int H, int NC) {
   const int i = blockIdx.y * gridDim.x + blockIdx.x;  // dispatch order
   const int full = NC / kXcds * kXcds;
-  if (i < full * H) {
+  if (NC >= kXcdMapMinChunks && i < full * H) {
     const int xcd = i % kXcds, j = i / kXcds;
     return HeadChunk{j % H, j / H * kXcds + xcd};
   }
