@@ -57,11 +57,11 @@ def test_forward_intermediates_and_output(gdn, T, bounds, H):
     check_forward(gdn, T, bounds, H, seed=900 + T)
 
 
-# fwd_prep gives each workgroup up to three chunks (as many as full rounds of three
-# workgroups per CU the chunk-heads make); on a 256-CU device these take two and
-# three chunks per workgroup, and the last workgroup of each head has one chunk fewer
+# 102 and 146 chunks: from 64 chunks on the chunk kernels map all heads of a chunk to one
+# XCD in blocks of eight chunk positions, and the last 6 (resp. 2) positions keep the
+# plain mapping; every chunk-head's intermediates are checked
 @pytest.mark.parametrize("T,bounds,H", [(6454, (0, 3000, 6454), 16), (9300, (0, 9300), 16)])
-def test_forward_chunks_shared_by_workgroups(gdn, T, bounds, H):
+def test_forward_xcd_mapped_chunks(gdn, T, bounds, H):
     print(f"case T={T} bounds={bounds} H={H}", flush=True)
     check_forward(gdn, T, bounds, H, seed=T)
 
