@@ -8,6 +8,8 @@ both backward modes, then compares the output and all five gradients with the or
 (the reference's NPU gate: relative L2 within 2e-2).  The fp16 cases draw the same kinds of
 batches with fp16 q/k/v and dO (the fp16 kernels, CQGDN_FP16) and hold them to TOL_FP16.  The
 prefill cases add random initial states and compare the per-document final states to 1e-3.
+The long cases (at least 64 chunks, up to about 11,000 events in one to three documents) run
+the chunk kernels' XCD-aware mapping and, in the cached mode, bwd_dkw beside the reverse scan.
 """
 
 import random
@@ -93,3 +95,38 @@ def test_random_prefill_case_matches_oracle(gdn, seed):
     for d in range(n_docs):
         r = rel_l2(states[d].cpu(), ref_states[d])
         assert r <= TOL_STATE, f"document {d} (length {bounds[d + 1] - bounds[d]}): final state rel_l2 {r:.3e}"
+
+
+def draw_long_case(seed):
+    """4, 8 or 16 heads; one to three documents of 2,000 to 11,000 events, so that every batch has
+    at least 64 chunks (the chunk kernels then put all heads of a chunk on one XCD, and bwd_dkw runs
+    beside the reverse scan where it fits); cached or fused mode; bf16 or fp16."""
+    rnd = random.Random(seed)
+    H = rnd.choice([4, 8, 16])
+    n_docs = rnd.randint(1, 3)
+    lens = [rnd.randint(2000, 9000 // n_docs + 2000) for _ in range(n_docs)]
+    bounds = [0]
+    for n in lens:
+        bounds.append(bounds[-1] + n)
+    return H, tuple(bounds), rnd.choice(["cached", "fused"]), rnd.choice([torch.bfloat16, torch.float16])
+
+
+@pytest.mark.parametrize("seed", range(3000, 3008))
+def test_random_long_case_matches_oracle(gdn, monkeypatch, seed):
+    H, bounds, mode, dtype = draw_long_case(seed)
+    T = bounds[-1]
+    print(f"case long seed={seed} T={T} bounds={bounds} H={H} mode={mode} {dtype}", flush=True)
+    monkeypatch.setattr(gdn, "MODE", mode)
+    tol = TOL_FP16 if dtype == torch.float16 else TOL_BF16
+    xs = make(T, H, seed, 0.2, True, dtype)
+    do = torch.randn(1, T, H, 128, generator=torch.Generator().manual_seed(9000 + seed)).to(dtype)
+    xd = [x.to(DEV).requires_grad_() for x in xs]
+    y, _ = gdn.delta(*xd, use_qk_l2norm_in_kernel=True, cu_seqlens=torch.tensor(bounds, device=DEV),
+                     cu_seqlens_cpu=list(bounds))
+    y.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    q, k, v, g, b = (x.double() for x in xs)
+    assert_close_bf16("o", y.detach().cpu(), O.chunk_delta(q, k, v, g, b, bounds), tol=tol)
+    ref = O.chunk_delta_backward(q, k, v, g, b, do.double(), bounds)
+    for name, x, r in zip(("dq", "dk", "dv", "dg", "dbeta"), xd, ref):
+        assert_close_bf16(name, x.grad.cpu(), r, tol=tol)
