@@ -777,6 +777,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   // The row's gate and norm are then one value per lane, its sums over k run over the
   // 4 lanes of a column (permlane swaps), and dq leaves as 8-byte pieces of rows.
   f32x4 dQ[2][4];
+  f32x4 qrow[4][2];  // q[t = 16 n + r][k = 16 (2w + mm) + 4 q4 + i], kept for the dq stores
+  float pdot[4];     // this wave's parts of the row dots q_t . dQ_t (l2norm backward of dq)
   {
     f32x4 a1[2][4];
 #pragma unroll
@@ -804,36 +806,22 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       const float f = scale * __expf(Gs[16 * n + r]);
-      f32x4 qr[2];  // q[t][k] at this lane's k
 #pragma unroll
-      for (int mm = 0; mm < 2; ++mm) qr[mm] = cvtf4(ld4(Qs + (16 * n + r) * LDK + 16 * (2 * wave + mm) + 4 * q4));
-      float x = 0.f;
+      for (int mm = 0; mm < 2; ++mm) qrow[n][mm] = cvtf4(ld4(Qs + (16 * n + r) * LDK + 16 * (2 * wave + mm) + 4 * q4));
+      float x = 0.f, y = 0.f;  // x: the output term's dG_t part; y: q_t . dQ_t (dQ complete here)
 #pragma unroll
       for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float inter = a1[mm][n][i] * f;
           dQ[mm][n][i] += inter;
-          x += qr[mm][i] * inter;
+          x += qrow[n][mm][i] * inter;
+          y += qrow[n][mm][i] * dQ[mm][n][i];
         }
       x = sum_rows4(x);
       if (q4 == 0) dgl[16 * n + r] += x;
+      pdot[n] = sum_rows4(y);
     }
-  }
-
-  // ---- l2norm backward of dq on the phase-2 registers: this wave's parts of the row dots q_t . dq_t ----
-  float pdot[4];
-#pragma unroll
-  for (int n = 0; n < 4; ++n) {
-    f32x4 qr[2];
-#pragma unroll
-    for (int mm = 0; mm < 2; ++mm) qr[mm] = cvtf4(ld4(Qs + (16 * n + r) * LDK + 16 * (2 * wave + mm) + 4 * q4));
-    float x = 0.f;
-#pragma unroll
-    for (int mm = 0; mm < 2; ++mm)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x += qr[mm][i] * dQ[mm][n][i];
-    pdot[n] = sum_rows4(x);
   }
   lds_barrier();  // every read of the dO rows is done: the row dots and then the dVn tile may replace them
   if (q4 == 0) {
@@ -859,8 +847,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const int k0 = 16 * (2 * wave + mm) + 4 * q4;
-      const f32x4 qr = cvtf4(ld4(Qs + t * LDK + k0));
-      const f32x4 x = normalize ? (dQ[mm][n] - qr * dot) * rs : dQ[mm][n];
+      const f32x4 x = normalize ? (dQ[mm][n] - qrow[n][mm] * dot) * rs : dQ[mm][n];
       buf_st4<E>(dq_rs, r * rowb + k0 * 2, 16 * n * rowb, F16 ? x * inv_dv : x);  // row t, columns k0 .. k0 + 3
     }
   }
@@ -1165,6 +1152,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 
   // ---- wy phase 4a: dK in registers ----
   f32x4 dkr[2][4];
+  f32x4 krow[4][2];  // k[t = 16 n + r][16 (2w + mm) + 4 q4 + i], kept for the dk stores
+  float pdk[4] = {0.f, 0.f, 0.f, 0.f};  // this wave's parts of the row dots k_t . dK_t
   {
     float colB[4] = {0.f, 0.f, 0.f, 0.f}, colG[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1190,12 +1179,13 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       for (int n = 0; n < 4; ++n) {
         const int t = 16 * n + r;
         const float bg = Bs[t] * __expf(Gs[t]);
-        const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
+        const f32x4 kk = krow[n][mm] = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
         // aw holds -(T^T dW): every use takes its sign back
         const float x = aw[n][0] * kk[0] + aw[n][1] * kk[1] + aw[n][2] * kk[2] + aw[n][3] * kk[3];
         colB[n] -= __expf(Gs[t]) * x;
         colG[n] -= bg * x;
         dkr[mm][n] = ak[n] + aw[n] * -bg + fkp[mm][n];
+        pdk[n] += kk[0] * dkr[mm][n][0] + kk[1] * dkr[mm][n][1] + kk[2] * dkr[mm][n][2] + kk[3] * dkr[mm][n][3];
       }
     }
 #pragma unroll
@@ -1210,15 +1200,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     }
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      const int t = 16 * n + r;
-      float pd = 0.f;
-#pragma unroll
-      for (int mm = 0; mm < 2; ++mm) {
-        const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * (2 * wave + mm) + 4 * q4));
-        pd += kk[0] * dkr[mm][n][0] + kk[1] * dkr[mm][n][1] + kk[2] * dkr[mm][n][2] + kk[3] * dkr[mm][n][3];
-      }
-      pd = sum_rows4(pd);
-      if (q4 == 0) dkdot[4 * t + wave] = pd;
+      const float pd = sum_rows4(pdk[n]);
+      if (q4 == 0) dkdot[4 * (16 * n + r) + wave] = pd;
     }
   }
   lds_barrier();
@@ -1233,8 +1216,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
 #pragma unroll
     for (int mm = 0; mm < 2; ++mm) {
       const int m = 2 * wave + mm;
-      const f32x4 kk = cvtf4(ld4(Ks + t * LDK + 16 * m + 4 * q4));
-      const f32x4 out = normalize ? (dkr[mm][n] - kk * dot) * rsn[n] : dkr[mm][n];
+      const f32x4 out = normalize ? (dkr[mm][n] - krow[n][mm] * dot) * rsn[n] : dkr[mm][n];
       buf_st4<E>(dk_rs, r * rowb + (16 * m + 4 * q4) * 2, 16 * n * rowb, F16 ? out * inv_dv : out);  // row t
     }
   }
