@@ -23,8 +23,8 @@ OPS_PATH = LIB_PATH.with_name("libcqgdn_torch.so")
 OK, EINVAL, EUNSUPPORTED, EHIP = 0, 1, 2, 3
 NORMALIZE, TRAINING, PRECISE, NO_OUTPUT, FP16 = 1, 2, 4, 8, 16
 STATIC_WORKSPACE_BYTES = 64 << 20  # CQGDN_STATIC_WORKSPACE_BYTES
-FWD_BUFFERS, BWD_BUFFERS = 10, 8
-FWD_NAMES = ("rq", "rk", "gcum", "T", "W", "UT", "KgT", "hT", "vnT", "vscale")
+FWD_BUFFERS, BWD_BUFFERS = 9, 8
+FWD_NAMES = ("rk", "gcum", "T", "W", "UT", "KgT", "hT", "vnT", "vscale")
 BWD_NAMES = ("dvlT", "XT", "dh", "dVn", "knP", "WT", "sync", "dscale")
 
 # every symbol include/cqgdn.h declares, with (restype, argtypes)

@@ -69,18 +69,18 @@ def bytes_per_chunk(kernel, c, d=D):
     sq = d * d * 2  # bf16 [D][D] chunk state
     tm = CHUNK * CHUNK * 2  # bf16 [64][64] T matrix
     return {
-        # q,k,v,g,beta -> rq,rk,gcum,T,-W rows,U^T,KgT
-        "fwd_prep": 3 * e + 2 * s + 3 * s + tm + e + 2 * tile,
+        # k,v,g,beta -> rk,gcum,T,-W rows,U^T,KgT (q's l2 scale is formed by its readers)
+        "fwd_prep": 2 * e + 2 * s + 2 * s + tm + e + 2 * tile,
         # -W rows, U^T, KgT, gcum -> h^T, v_new^T
         "fwd_scan": e + 2 * tile + s + sq + tile,
-        # q, k, rq, rk, gcum, h^T, v_new^T -> o
-        "fwd_out": 2 * e + 3 * s + sq + tile + e,
-        # q, k, rq, rk, dO, gcum, beta, T -> dv_local^T, X^T, kdec Kn perm32, -W^T
-        "bwd_local": 3 * e + 4 * s + tm + tile + sq + e + tile,
+        # q, k, rk, gcum, h^T, v_new^T -> o
+        "fwd_out": 2 * e + 2 * s + sq + tile + e,
+        # q, k, rk, dO, gcum, beta, T -> dv_local^T, X^T, kdec Kn perm32, -W^T
+        "bwd_local": 3 * e + 3 * s + tm + tile + sq + e + tile,
         # kdec Kn perm32, gcum, dv_local^T, X^T, -W^T -> dh, dv_new (both value-slice-major)
         "bwd_scan": e + s + tile + sq + tile + sq + tile,
-        # q, k, rq, rk, gcum, h^T, v_new^T, dO, dh, dv_new, v, beta, T -> dq, dk, dv, dg, dbeta
-        "bwd_dkw": 2 * e + 3 * s + sq + tile + e + sq + tile + e + s + tm + 3 * e + 2 * s,
+        # q, k, rk, gcum, h^T, v_new^T, dO, dh, dv_new, v, beta, T -> dq, dk, dv, dg, dbeta
+        "bwd_dkw": 2 * e + 2 * s + sq + tile + e + sq + tile + e + s + tm + 3 * e + 2 * s,
     }[kernel]
 
 

@@ -53,7 +53,7 @@ constexpr int LDT = 72;   // bf16 row stride, 128 x 64 and 64 x 64 tiles
 // dscale[0] for bwd_dkw
 template <class E>
 __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
-    const E* __restrict__ q, const E* __restrict__ k, const float* __restrict__ rq,
+    const E* __restrict__ q, const E* __restrict__ k, int normalize,
     const float* __restrict__ rk, const E* __restrict__ dout, const float* __restrict__ gc,
     const float* __restrict__ beta, const E* __restrict__ Tm,
     const int32_t* __restrict__ chunks, int H, float scale, float* __restrict__ dscale, int ds_target,
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
     const bool in = t < ci.len;
     const int tc = clamp_row(t, ci.len);
     const size_t ev = (size_t)(ci.start + tc) * H + h, row = ev * D;
-    const float rqt = rq[ev], rkt = rk[ev];
+    const float rkt = rk[ev];
     // q and k non-temporally: what this kernel writes (the reverse scan's operands,
     // 188 MB at T = 9216, H = 16) and what the scan writes do not both fit the
     // 256 MB memory-side cache, and q, k are read next only by bwd_dkw, after the scan
@@ -118,6 +118,7 @@ __global__ __launch_bounds__(256, 3) void bwd_local_kernel(
       Gs[t] = gc[ev];
       Bs[t] = keep_if(in, beta[ev]);
     }
+    const float rqt = normalize ? row_rnorm(xq) : 1.f;
     if constexpr (F16) {  // dO s_d (exact: a power of two, in range)
       ds = range_scale(dpart, ds_target, red);
 #pragma unroll
@@ -573,7 +574,7 @@ constexpr int DKW_R1 = 0, DKW_R2 = 64 * LDK * 2, DKW_R3 = DKW_R2 + 64 * LDK * 2,
 
 template <class E>  // dscale, vscale: null in bf16; in fp16 the device scalars s_d and s_v
 __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
-    const E* __restrict__ q, const E* __restrict__ k, const float* __restrict__ rq,
+    const E* __restrict__ q, const E* __restrict__ k,
     const float* __restrict__ rk, const float* __restrict__ gc, const E* __restrict__ hT,
     const E* __restrict__ vnT, const E* __restrict__ dout, const E* __restrict__ dh,
     const E* __restrict__ dVn, const E* __restrict__ vin, const float* __restrict__ beta,
@@ -628,9 +629,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
   const E* ht = hT + cb * (D * D);
   X8 bh[2][4], bd[2][4];
   // Every prologue load is issued before the first wait: the column gathers'
-  // loads, the gate and norm values (unconditional: rq is allocated either
+  // loads, the gate and k-norm values (unconditional: rk is allocated either
   // way), the v_new^T rows and the Q, K, dO rows; the gathers' lane exchange
-  // comes last.
+  // comes last.  The q norm is formed from the Q rows (row_rnorm).
   {
     Col8 gh[2][4];
 #pragma unroll
@@ -642,7 +643,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
     const int tc = clamp_row(t, ci.len);
     const size_t ev = (size_t)(ci.start + tc) * H + h, row = ev * D;
     const float gv = gc[ev];
-    const float rv = rq[ev], rkv = rk[ev];
+    const float rkv = rk[ev];
     const E* vt = vnT + cb * (D * CH);
     X8 xv[4], xq[4], xk[4], xo[4];
 #pragma unroll
@@ -658,9 +659,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkw_kernel(
       xo[j] = ld8(dout + row + col);
     }
     dgw[wave][lane] = 0.f;
+    const float rv = normalize ? row_rnorm(xq) : 1.f;
     if (p == 0) {
       Gs[t] = gv;
-      Rs[t] = normalize ? rv : 1.f;
+      Rs[t] = rv;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -1285,7 +1287,7 @@ static hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t stream) {
   }
   {
     TimedLaunch tl(K_BWD_LOCAL, stream);
-    hipLaunchKernelGGL(bwd_local_kernel<E>, dim3(a.H, a.n_chunks), dim3(256), 0, stream, q, k, Ff(F_RQ), Ff(F_RK),
+    hipLaunchKernelGGL(bwd_local_kernel<E>, dim3(a.H, a.n_chunks), dim3(256), 0, stream, q, k, (int)a.normalize, Ff(F_RK),
                        dout, Ff(F_GC), a.beta, F(F_TM), a.chunks, a.H, a.scale, dsc, dout_scale_target(a.T), B(B_DVLT),
                        B(B_XT), B(B_KNP), B(B_WT), sync);
   }
@@ -1303,7 +1305,7 @@ static hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t stream) {
     launch_resident_gate(resident, a.H * (D / 16) * a.n_docs, a.side);
     {
       TimedLaunch tl(K_BWD_DKW, a.side);
-      hipLaunchKernelGGL(bwd_dkw_kernel<E>, grid_p, dim3(256), 0, a.side, q, k, Ff(F_RQ), Ff(F_RK), Ff(F_GC),
+      hipLaunchKernelGGL(bwd_dkw_kernel<E>, grid_p, dim3(256), 0, a.side, q, k, Ff(F_RK), Ff(F_GC),
                          F(F_HT), F(F_VNT), dout, B(B_DH), B(B_DVN), v, a.beta, F(F_TM), a.chunks, a.H, a.scale,
                          (int)a.normalize, (const float*)dsc, vsc, dq, dk, dv, a.dg, a.dbeta, (const int*)ready,
                          a.dkw_never_ready ? D / 16 + 1 : D / 16, a.dkw_never_ready ? 4 : COUNT_SPIN_LIMIT);
@@ -1314,7 +1316,7 @@ static hipError_t launch_bwd_t(const BwdArgs& a, hipStream_t stream) {
   if (a.dkw_after)
     if (const hipError_t e = hipStreamWaitEvent(stream, a.dkw_after, 0)) return e;
   TimedLaunch tl(K_BWD_DKW, stream);
-  hipLaunchKernelGGL(bwd_dkw_kernel<E>, grid_p, dim3(256), 0, stream, q, k, Ff(F_RQ), Ff(F_RK), Ff(F_GC), F(F_HT),
+  hipLaunchKernelGGL(bwd_dkw_kernel<E>, grid_p, dim3(256), 0, stream, q, k, Ff(F_RK), Ff(F_GC), F(F_HT),
                      F(F_VNT), dout, B(B_DH), B(B_DVN), v, a.beta, F(F_TM), a.chunks, a.H, a.scale, (int)a.normalize,
                      (const float*)dsc, vsc, dq, dk, dv, a.dg, a.dbeta, (const int*)nullptr, 0, 0);
   return hipSuccess;

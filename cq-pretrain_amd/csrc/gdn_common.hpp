@@ -546,6 +546,23 @@ __device__ __forceinline__ float sum4(float x) {
   return x;
 }
 
+// The l2 scale rsqrt(sum x^2 + 1e-6) of an event row of q or k, whose 128 values
+// four adjacent threads hold as 8-value pieces (columns 32 j + 8 p of row t for
+// thread 4 t + p).  Every kernel that reads q or k rows in this layout forms the
+// scale itself, with the same sums in the same order, so all of them apply the
+// same bits and no kernel stores it.
+template <class X8>
+__device__ __forceinline__ float row_rnorm(const X8 (&x)[4]) {
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const f32x8 y = cvtf8(x[j]);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) ss += y[s] * y[s];
+  }
+  return rsqrtf(sum4(ss) + 1e-6f);
+}
+
 // Rows past a tail chunk's length re-read the chunk's last row (always in bounds)
 // and are zeroed after the load.  A load issued under a condition is waited for
 // on its own (the compiler branches around it); unconditional loads of a phase

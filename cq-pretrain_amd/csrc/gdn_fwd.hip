@@ -35,9 +35,9 @@ constexpr int LDA = 65;   // row stride (fp32) of the 64 x 64 solve matrix
 // vscale[0] for the scan and the output kernel; null with bf16 operands.
 template <class I, class E, bool NORMALIZE>
 __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
-    const I* __restrict__ q, const I* __restrict__ k, const I* __restrict__ v,
+    const I* __restrict__ k, const I* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta, const int32_t* __restrict__ chunks,
-    int H, float* __restrict__ vscale, int vs_target, float* __restrict__ rq,
+    int H, float* __restrict__ vscale, int vs_target,
     float* __restrict__ rk, float* __restrict__ gc, E* __restrict__ Tm, E* __restrict__ W,
     E* __restrict__ UT, E* __restrict__ KgT) {
   typedef typename Vec<E>::x8 X8;
@@ -65,15 +65,16 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
 
   // Every global load is issued first, before any store (a wait for a load
   // also waits for every store issued before it), so the kernel pays one memory
-  // round trip: the gates (wave 0), this thread's pieces of its q and k rows,
+  // round trip: the gates (wave 0), this thread's pieces of its k row,
   // and this wave's operand fragments of V for U = T (beta V), column gathers
   // for value tiles 2 wave, 2 wave + 1 (rows past the chunk re-read its last
   // row; their beta is zero).  Each phase waits only for what it reads: the
   // gathers' lane exchange runs where U is formed, and the stores of the row
   // phase go through buffer resources (rows past the chunk dropped by the range
   // check), so no store is conditional and the compiler can count what is in flight.
-  // q and k are loaded non-temporally: nothing reads them again before the state
-  // scan, whose operands (written here) then keep more of the memory-side cache.
+  // k is loaded non-temporally: nothing reads it again before the state scan,
+  // whose operands (written here) then keep more of the memory-side cache.  q is
+  // not read here: its l2 scale is formed by each kernel that reads q (row_rnorm).
   // (V's column gathers share lines between lanes and stay ordinary loads.)
   const int t_r = tid >> 2, p_r = tid & 3;  // row phase: thread (t, p) owns columns 8p + 32j, j = 0..3
   const size_t row_r = ((size_t)(ci.start + clamp_row(t_r, ci.len)) * H + h) * D;
@@ -83,13 +84,10 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     gv = g[ev];
     bv = beta[ev];
   }
-  typename Vec<I>::x8 lq[4], lk[4];
+  typename Vec<I>::x8 lk[4];
   Col8 vg[2][2];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    lq[j] = ld8_nt(q + row_r + 32 * j + 8 * p_r);
-    lk[j] = ld8_nt(k + row_r + 32 * j + 8 * p_r);
-  }
+  for (int j = 0; j < 4; ++j) lk[j] = ld8_nt(k + row_r + 32 * j + 8 * p_r);
   {
     const I* vb = v + ((size_t)ci.start * H + h) * D;
 #pragma unroll
@@ -133,25 +131,7 @@ __global__ __launch_bounds__(256, 3) void fwd_prep_kernel(
     const float gam_t = __expf(Gs[t]);
     const float kdec_t = __expf(glast - Gs[t]);
     const float b_t = Bs[t];
-    const __amdgpu_buffer_rsrc_t rq_rs = buf_rsrc(rq + (size_t)ci.start * H + h, gate_bytes);
     const __amdgpu_buffer_rsrc_t rk_rs = buf_rsrc(rk + (size_t)ci.start * H + h, gate_bytes);
-    // q: only its scale is stored; each reader forms its own operand rows (scaled8)
-    {
-      f32x8 x[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = keep_if(in, cvtf8(lq[j]));
-      float rs = 1.f;
-      if (NORMALIZE) {
-        float ss = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int s = 0; s < 8; ++s) ss += x[j][s] * x[j][s];
-        ss = sum4(ss);
-        rs = rsqrtf(ss + 1e-6f);
-      }
-      buf_stf(rq_rs, t * H * 4, 0, rs);  // the four threads of row t store the same value
-    }
     // k
     {
       f32x8 x[4];
@@ -714,7 +694,7 @@ __global__ __launch_bounds__(SC_THREADS) void fwd_scan_kernel(
 // ---------------------------------------------------------------------------
 template <class I, class E>  // I: element type of q, k and o; E: operand type (as fwd_prep)
 __global__ __launch_bounds__(256) void fwd_out_kernel(
-    const I* __restrict__ q, const I* __restrict__ k, const float* __restrict__ rq,
+    const I* __restrict__ q, const I* __restrict__ k, int normalize,
     const float* __restrict__ rk, const float* __restrict__ gc, const E* __restrict__ hT,
     const E* __restrict__ vnT, const int32_t* __restrict__ chunks, int H,
     float scale, const float* __restrict__ vscale, I* __restrict__ o) {
@@ -749,7 +729,7 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
     const int t = tid >> 2, p = tid & 3;
     const bool in = t < ci.len;
     const size_t ev = (size_t)(ci.start + clamp_row(t, ci.len)) * H + h, row = ev * D;
-    const float rqt = rq[ev], rkt = rk[ev];
+    const float rkt = rk[ev];
     typename Vec<I>::x8 xq[4], xk[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -758,6 +738,7 @@ __global__ __launch_bounds__(256) void fwd_out_kernel(
       xk[j] = ld8(k + row + col);
     }
     if (p == 0) Gs[t] = gc[ev];
+    const float rqt = normalize ? row_rnorm(xq) : 1.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = 32 * j + 8 * p;
@@ -888,7 +869,6 @@ template <class I, class E>
 static hipError_t launch_fwd_t(const FwdArgs& a, float* vscale, int vs_target, hipStream_t stream) {
   E* ws[F_COUNT];
   for (int i = 0; i < F_COUNT; ++i) ws[i] = reinterpret_cast<E*>(a.ws + a.off[i]);
-  float* rq = reinterpret_cast<float*>(ws[F_RQ]);
   float* rk = reinterpret_cast<float*>(ws[F_RK]);
   float* gcum = reinterpret_cast<float*>(ws[F_GC]);
   const I* q = static_cast<const I*>(a.q);
@@ -898,12 +878,12 @@ static hipError_t launch_fwd_t(const FwdArgs& a, float* vscale, int vs_target, h
     TimedLaunch tl(K_FWD_PREP, stream);
     const dim3 grid_p(a.H, a.n_chunks);
     if (a.normalize)
-      hipLaunchKernelGGL((fwd_prep_kernel<I, E, true>), grid_p, dim3(256), 0, stream, q, k, v, a.g, a.beta,
-                         a.chunks, a.H, vscale, vs_target, rq, rk, gcum, ws[F_TM], ws[F_W],
+      hipLaunchKernelGGL((fwd_prep_kernel<I, E, true>), grid_p, dim3(256), 0, stream, k, v, a.g, a.beta,
+                         a.chunks, a.H, vscale, vs_target, rk, gcum, ws[F_TM], ws[F_W],
                          ws[F_UT], ws[F_KGT]);
     else
-      hipLaunchKernelGGL((fwd_prep_kernel<I, E, false>), grid_p, dim3(256), 0, stream, q, k, v, a.g, a.beta,
-                         a.chunks, a.H, vscale, vs_target, rq, rk, gcum, ws[F_TM], ws[F_W],
+      hipLaunchKernelGGL((fwd_prep_kernel<I, E, false>), grid_p, dim3(256), 0, stream, k, v, a.g, a.beta,
+                         a.chunks, a.H, vscale, vs_target, rk, gcum, ws[F_TM], ws[F_W],
                          ws[F_UT], ws[F_KGT]);
   }
   const dim3 grid_s(a.H * (D / 16), a.n_docs);
@@ -922,7 +902,7 @@ static hipError_t launch_fwd_t(const FwdArgs& a, float* vscale, int vs_target, h
     if (const hipError_t e = hipEventRecord(a.scan_join, a.scan_stream)) return e;
   if (a.no_output) return hipSuccess;
   TimedLaunch tl(K_FWD_OUT, stream);
-  hipLaunchKernelGGL((fwd_out_kernel<I, E>), dim3(a.H, a.n_chunks), dim3(256), 0, stream, q, k, rq, rk, gcum,
+  hipLaunchKernelGGL((fwd_out_kernel<I, E>), dim3(a.H, a.n_chunks), dim3(256), 0, stream, q, k, (int)a.normalize, rk, gcum,
                      ws[F_HT], ws[F_VNT], a.chunks, a.H, a.scale, vscale, static_cast<I*>(a.o));
   return hipSuccess;
 }

@@ -8,8 +8,10 @@
 // inputs (the reference saves q,k,v,gcum,beta,A in fused mode and also
 // w,h,v_new in cached mode, ops/gated_delta_net.py:184); keeping h and v_new
 // avoids re-running the serial state scan in the backward.  No normalized copy
-// of q and k is kept: every reader scales its q and k rows by rq / rk on the way
-// into LDS, with the rounding fwd_prep applies (bf16 or fp16 of float(x) * r).
+// of q and k is kept: every reader scales its q and k rows by their l2 scales on
+// the way into LDS, with the rounding fwd_prep applies (bf16 or fp16 of
+// float(x) * r).  The k scales rk are kept; the q scales are formed by each
+// kernel that reads q rows (row_rnorm), so no kernel before them reads q.
 // Buffers are addressed by event (time-first [T][H][D], the caller's TND
 // order) or by chunk ([NC][H][...], one 64-event block per chunk, rows past a
 // tail chunk's length are zero).  Value-slice-major
@@ -24,8 +26,7 @@
 namespace cqgdn {
 
 enum FwdBuf {
-  F_RQ = 0,  // f32  [T][H]      rsqrt(sum q^2 + eps) (1 without the in-kernel l2norm)
-  F_RK,      // f32  [T][H]      rsqrt(sum k^2 + eps) (1 without the in-kernel l2norm)
+  F_RK = 0,  // f32  [T][H]      rsqrt(sum k^2 + eps) (1 without the in-kernel l2norm)
   F_GC,      // f32  [T][H]      chunk-local cumsum of g
   F_TM,      // bf16 [NC][H][64][64]  T = (I + A)^-1, row-major (t, s)
   F_W,       // bf16 [T][H][D]   -W, W = T (beta*exp(G)*K), rows (t, k), perm32 column order
@@ -61,7 +62,6 @@ inline size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 inline void fwd_sizes(int64_t T, int64_t H, int64_t NC, size_t* s) {
   const size_t ev = (size_t)T * H, chunk = (size_t)NC * H;
-  s[F_RQ] = ev * 4;
   s[F_RK] = ev * 4;
   s[F_GC] = ev * 4;
   s[F_TM] = chunk * 64 * 64 * 2;

@@ -77,10 +77,11 @@ int64_t cqgdn_chunk_table(const int64_t* bounds, int n_bounds, int32_t* table, i
  * Forward workspace: size in bytes, and the byte offset of each of its
  * CQGDN_FWD_BUFFERS internal buffers (order documented in gdn_layout.hpp) so
  * that tests can inspect intermediates.  The same workspace must be passed,
- * unmodified, to cqgdn_bwd, with the same q and k (the workspace keeps their
- * per-row l2 scales, not normalized copies).
+ * unmodified, to cqgdn_bwd, with the same q and k (the workspace keeps the
+ * per-row l2 scales of k, not normalized copies; the kernels that read q form
+ * its scales themselves).
  */
-#define CQGDN_FWD_BUFFERS 10
+#define CQGDN_FWD_BUFFERS 9
 #define CQGDN_BWD_BUFFERS 8
 size_t cqgdn_fwd_workspace_size(int64_t T, int H, int64_t n_chunks);
 int cqgdn_fwd_buffer_offsets(int64_t T, int H, int64_t n_chunks, size_t* offsets, int count);
