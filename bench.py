@@ -470,16 +470,23 @@ def main():
         kernels = {} if args.no_extra else kernel_table(torch, _lib, workmodel, step, bounds)
     dominant = max(kernels, key=lambda k: kernels[k]["us"]) if kernels else "bwd_dkw"
 
-    # timed region (the product path, bwd_dkw beside the reverse scan): K steps, the dominant
-    # kernel's launches bracketed by HIP events on its stream
+    # timed region (the product path, bwd_dkw beside the reverse scan): K steps with no
+    # instrumentation armed, after two untimed steps in this mode
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms = elapsed / args.steps * 1e3
+    # the same K steps again with the dominant kernel's launches bracketed by HIP events on
+    # its stream: its launch span beside the scan
     with _lib.KernelTimer(dominant, args.steps) as timer_beside:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
         torch.cuda.synchronize()
-        elapsed = time.perf_counter() - t0
-    ms = elapsed / args.steps * 1e3
     # the same K steps with bwd_dkw after the scan: the dominant kernel's own launch time
     with dkw_after_scan():
         for _ in range(2):

@@ -79,10 +79,13 @@ int cqgdn_timer_arm(const char* kernel, int max_launches) {
     return fail(CQGDN_EINVAL, "cqgdn_timer_arm: max_launches %d not in 1..65536", max_launches);
   t.events.resize(2 * (size_t)max_launches);
   for (size_t i = 0; i < t.events.size(); ++i) {
-    if (hipEventCreate(&t.events[i]) != hipSuccess) {
+    // timing events without the system-scope fence: they bracket one kernel on
+    // one device, and the fence's cache write-back would lengthen the gap they
+    // measure across (on a side stream, right at the kernel's launch)
+    if (hipEventCreateWithFlags(&t.events[i], hipEventDisableSystemFence) != hipSuccess) {
       t.events.resize(i);
       release(t);
-      return fail(CQGDN_EHIP, "cqgdn_timer_arm: hipEventCreate failed");
+      return fail(CQGDN_EHIP, "cqgdn_timer_arm: hipEventCreateWithFlags failed");
     }
   }
   t.capacity = max_launches;
