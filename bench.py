@@ -108,13 +108,19 @@ def training_case(gdn, synthetic, torch, config, device, fp16=False):
     return T, bounds, step, xs
 
 
-def time_steps(torch, step, steps):
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) / steps
+def time_steps(torch, step, steps, windows=5):
+    """Seconds per step of the secondary configurations: the median over `windows` windows of
+    `steps` steps each, each window bracketed by synchronizations (the headline value times
+    exactly K steps in one window instead)."""
+    per = []
+    for _ in range(windows):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        per.append((time.perf_counter() - t0) / steps)
+    return statistics.median(per)
 
 
 def kernel_table(torch, _lib, workmodel, step, bounds, reps=5):
